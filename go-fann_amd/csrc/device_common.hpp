@@ -1,0 +1,455 @@
+// device_common.hpp -- device-side building blocks of the gfx950 search
+// path: visited hash, symmetric min-max frontier heap, bounded binary heaps,
+// CSR/DNF predicates, range atoms, early stop and wave64 reductions.
+//
+// Every routine keeps the observable semantics of the GO-FANN routine it
+// cites (paths relative to the GO-FANN source tree); the layout and
+// parallelisation are this file's own (wave64, LDS-resident state).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "gofann_hip.h"
+
+namespace gofann {
+
+constexpr uint32_t kHashCapacity = 4096;  // backend_pq.cu:194
+constexpr int kMaxDegree = 64;            // include/config1B.h:29 FIXED_DEGREE
+constexpr uint32_t kPoolUsed = 0x80000000u;  // backend_pq.cu:713
+constexpr int kMaxStopWidth = 10;         // backend_pq.cu:72 kTopk
+constexpr int kWave = 64;
+
+// Frontier entry: priority `first`, label-local row | used bit, unbiased
+// score `base` (gpu_predicate::BiasedPair, gpu_predicate_index.cuh:137-144).
+struct Entry {
+    float first;
+    uint32_t second;
+    float base;
+};
+
+struct ResultEntry {  // KernelPair<dist_t, uint32_t>
+    float first;
+    uint32_t second;
+};
+
+struct StopEntry {  // KernelPair<dist_t, idx_t>
+    float first;
+    uint32_t pad;
+    uint64_t second;
+};
+
+__device__ __forceinline__ uint32_t fbits(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float bitsf(uint32_t u) { return __uint_as_float(u); }
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// Wave-uniform broadcast of lane 0's value.
+__device__ __forceinline__ int bcast0(int v) { return __builtin_amdgcn_readlane(v, 0); }
+__device__ __forceinline__ uint32_t bcast0u(uint32_t v)
+{
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0));
+}
+__device__ __forceinline__ float bcast0f(float v)
+{
+    return bitsf(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(fbits(v)), 0)));
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// Number of set bits of `mask` below this lane (exclusive prefix).
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask)
+{
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// ---------------------------------------------------------------------------
+// Visited hash: native_visited_hash.cuh:10-60 (linear probing, 4096 slots,
+// empty = UINT32_MAX, add drops silently when full).  Two storages share the
+// probe sequence: LDS (when the workgroup budget allows) or a per-route
+// global slab accessed with agent-scope atomics so lanes of one wave observe
+// each other's inserts without L1 staleness.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t hash_code(uint32_t value)
+{
+    const uint64_t mixed = static_cast<uint64_t>(value) ^
+                           (static_cast<uint64_t>(value >> 16) * 0x4bcb391f924ed183ULL) ^
+                           0xa0ab69ccd854fc0aULL;
+    return static_cast<uint32_t>(mixed % kHashCapacity);
+}
+
+template <bool kLds>
+struct VisitedHash {
+    uint32_t* slots;
+
+    __device__ __forceinline__ uint32_t load(uint32_t i) const
+    {
+        if constexpr (kLds) return slots[i];
+        return __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __device__ __forceinline__ void store(uint32_t i, uint32_t v) const
+    {
+        if constexpr (kLds) {
+            slots[i] = v;
+        } else {
+            __hip_atomic_store(slots + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // All lanes: fill every slot with UINT32_MAX.
+    __device__ void clear(int lane) const
+    {
+        uint4* p = reinterpret_cast<uint4*>(slots);
+        const uint4 empty = make_uint4(UINT32_MAX, UINT32_MAX, UINT32_MAX, UINT32_MAX);
+        for (uint32_t i = lane; i < kHashCapacity / 4; i += kWave) p[i] = empty;
+    }
+    __device__ bool test(uint32_t value) const
+    {
+        uint32_t slot = hash_code(value);
+        for (uint32_t probes = 0; probes < kHashCapacity; ++probes) {
+            const uint32_t v = load(slot);
+            if (v == UINT32_MAX) return false;
+            if (v == value) return true;
+            slot = (slot + 1) % kHashCapacity;
+        }
+        return false;
+    }
+    __device__ void add(uint32_t value) const
+    {
+        uint32_t slot = hash_code(value);
+        for (uint32_t probes = 0; probes < kHashCapacity; ++probes) {
+            const uint32_t v = load(slot);
+            if (v == value) return;
+            if (v == UINT32_MAX) {
+                store(slot, value);
+                return;
+            }
+            slot = (slot + 1) % kHashCapacity;
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Symmetric min-max heap (include/smmh2.h:1-147): slot 0 empty, slot 1 =
+// minimum, slot 2 = maximum; comparisons on `first` only.  Executed by one
+// lane; the array lives in LDS.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void entry_swap(Entry* a, Entry* b)
+{
+    const Entry t = *a;
+    *a = *b;
+    *b = t;
+}
+
+__device__ __forceinline__ int smmh_adjust_sibling(Entry* h, int y, int size)
+{
+    if (y & 1) {
+        const int s = y + 1;
+        if (s >= size) return y;
+        if (h[y].first > h[s].first) {
+            entry_swap(&h[y], &h[s]);
+            return s;
+        }
+    } else {
+        const int s = y - 1;
+        if (h[y].first < h[s].first) {
+            entry_swap(&h[y], &h[s]);
+            return s;
+        }
+    }
+    return y;
+}
+
+__device__ __forceinline__ int smmh_adjust_grandparent(Entry* h, int y)
+{
+    if (y <= 2) return y;
+    const int g = (y - 3) >> 2;
+    const int gl = (g << 1) + 1;
+    const int gr = (g << 1) + 2;
+    if (h[gl].first > h[y].first) {
+        entry_swap(&h[gl], &h[y]);
+        return gl;
+    } else if (h[gr].first < h[y].first) {
+        entry_swap(&h[gr], &h[y]);
+        return gr;
+    }
+    return y;
+}
+
+__device__ void smmh_insert(Entry* h, int& size, const Entry& e)
+{
+    int y = size;
+    h[size++] = e;
+    for (;;) {
+        y = smmh_adjust_sibling(h, y, size);
+        const int x = smmh_adjust_grandparent(h, y);
+        if (x == y) break;
+        y = x;
+    }
+}
+
+__device__ __forceinline__ int smmh_adjust_grandchild(Entry* h, int y, int size)
+{
+    if (y & 1) {
+        const int cl = (y << 1) + 1;
+        if (cl >= size) return y;
+        const int cr = ((y + 1) << 1) + 1;
+        int c = cl;
+        if (cr < size && h[cr].first < h[cl].first) c = cr;
+        if (h[c].first < h[y].first) {
+            entry_swap(&h[c], &h[y]);
+            return c;
+        }
+    } else {
+        const int cl = ((y - 1) << 1) + 2;
+        const int cr = (y << 1) + 2;
+        if (cl >= size) return y;
+        int c = cl;
+        if (cr < size && h[cr].first > h[cl].first) c = cr;
+        if (h[c].first > h[y].first) {
+            entry_swap(&h[c], &h[y]);
+            return c;
+        }
+    }
+    return y;
+}
+
+__device__ void smmh_pop_max(Entry* h, int& size)
+{
+    h[2] = h[--size];
+    int y = 2;
+    for (;;) {
+        (void)smmh_adjust_sibling(h, y, size);
+        const int x = smmh_adjust_grandchild(h, y, size);
+        if (x == y) break;
+        y = x;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Bounded max-heaps of include/bin_heap.h:4-64 (push sifts the appended
+// element up; pop returns the root and sifts the former tail down without
+// storing the root at the tail).
+// ---------------------------------------------------------------------------
+template <class T>
+__device__ void bin_push(T* h, int size)
+{
+    int now = size - 1;
+    int parent = (now - 1) / 2;
+    while (now > 0 && h[parent].first < h[now].first) {
+        const T t = h[now];
+        h[now] = h[parent];
+        h[parent] = t;
+        now = parent;
+        parent = (now - 1) / 2;
+    }
+}
+
+template <class T>
+__device__ T bin_pop(T* h, int size)
+{
+    const T ret = h[0];
+    const int len = size - 1;
+    if (len <= 0) return ret;
+    h[0] = h[size - 1];
+    int now = 0;
+    while (now * 2 + 1 < len) {
+        const int left = now * 2 + 1;
+        const int right = now * 2 + 2;
+        int next = left;
+        if (right < len && h[left].first < h[right].first) next = right;
+        if (!(h[now].first < h[next].first)) break;
+        const T t = h[now];
+        h[now] = h[next];
+        h[next] = t;
+        now = next;
+    }
+    return ret;
+}
+
+// ---------------------------------------------------------------------------
+// Posting shortlist order (posting_shortlist_heap.cuh:15-21): a pair is worse
+// when its distance is larger, ties broken by the larger id.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool pair_worse(float ld, uint32_t lid, float rd, uint32_t rid)
+{
+    return ld > rd || (ld == rd && lid > rid);
+}
+
+// ---------------------------------------------------------------------------
+// Early stop: backend_pq.cu:2822-2873.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int adaptive_limit(int queue_limit, int expanded, int passed,
+                                              int stop_width)
+{
+    const int queue_base = queue_limit > 1 ? queue_limit : 1;
+    int base_limit = (queue_base + 1) / 2;
+    const int min_base = stop_width > 0 ? stop_width * 2 : 1;
+    base_limit = base_limit > min_base ? base_limit : min_base;
+    const int denom = (expanded + 16) > 1 ? (expanded + 16) : 1;
+    const int pass_with_prior = passed + 8;
+    const int pass_estimate = pass_with_prior < denom ? pass_with_prior : denom;
+    const int reject_estimate = (denom - pass_estimate) > 0 ? (denom - pass_estimate) : 0;
+    const int64_t numerator = static_cast<int64_t>(queue_limit) * reject_estimate;
+    int extra = static_cast<int>((numerator + (2 * denom - 1)) / (2 * denom));
+    extra = extra > 0 ? extra : 0;
+    extra = extra < 32 ? extra : 32;
+    return base_limit + extra;
+}
+
+__device__ __forceinline__ bool early_stop_reached(int mode, int bad, int fixed_limit,
+                                                   int queue_limit, int expanded, int passed,
+                                                   int stop_width)
+{
+    if (mode == GOFANN_EARLY_STOP_OFF) return false;
+    if (mode == GOFANN_EARLY_STOP_ADAPTIVE)
+        return bad >= adaptive_limit(queue_limit, expanded, passed, stop_width);
+    return bad >= fixed_limit;
+}
+
+// ---------------------------------------------------------------------------
+// Predicates: gpu_predicate_index.cuh:52-166 (CSR storage, threshold 0) and
+// range_filter.cuh:23-124.
+// ---------------------------------------------------------------------------
+struct PredCounters {
+    uint32_t rows;
+    uint32_t labels;
+};
+
+__device__ __forceinline__ bool range_matches(uint32_t mode, float lower, float upper, float v)
+{
+    switch (mode) {
+    case 0: return true;
+    case 1: return v > lower;
+    case 2: return v < upper;
+    case 3: return v >= lower && v < upper;
+    default: return false;
+    }
+}
+
+__device__ __forceinline__ bool pred_enabled(const gofann_predicate_view& v, uint32_t route)
+{
+    return v.route_enabled ? v.route_enabled[route] != 0 : (v.csr_offsets != nullptr);
+}
+
+__device__ __forceinline__ bool pred_contains(const gofann_predicate_view& v, uint32_t handle,
+                                              uint32_t sample, PredCounters& c)
+{
+    if (sample >= v.rows || v.csr_offsets == nullptr) return false;
+    const uint32_t begin = v.csr_offsets[sample];
+    const uint32_t end = v.csr_offsets[sample + 1];
+    ++c.rows;
+    for (uint32_t i = begin; i < end; ++i) {
+        const uint32_t label = v.csr_labels[i];
+        ++c.labels;
+        if (label >= handle) return label == handle;
+    }
+    return false;
+}
+
+__device__ bool pred_matches(const gofann_predicate_view& v, uint32_t route, uint32_t sample,
+                             PredCounters& c)
+{
+    if (sample >= v.rows) return false;
+    if (v.clauses) {
+        for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i) {
+            const gofann_clause cl = v.clauses[i];
+            bool pass = true;
+            for (uint32_t j = cl.label_begin; pass && j < cl.label_end; ++j)
+                pass = pred_contains(v, v.route_handles[j], sample, c);
+            for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
+                const gofann_range_atom a = v.ranges[j];
+                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                       range_matches(a.mode, a.lower, a.upper,
+                                     v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
+                                                   a.dimension]);
+            }
+            if (pass) return true;
+        }
+        return false;
+    }
+    for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i)
+        if (!pred_contains(v, v.route_handles[i], sample, c)) return false;
+    return true;
+}
+
+__device__ __forceinline__ float priority(float base, float penalty, bool pass)
+{
+    if (pass || penalty == 0.0f || !isfinite(base) || base == FLT_MAX) return base;
+    if (base > FLT_MAX - penalty) return FLT_MAX;
+    return base + penalty;
+}
+
+__device__ __forceinline__ float bias_penalty(float alpha, float start)
+{
+    const double wide = static_cast<double>(alpha) * fmax(static_cast<double>(fabsf(start)), 1e-6);
+    return isfinite(wide) ? static_cast<float>(fmin(wide, static_cast<double>(FLT_MAX))) : 0.0f;
+}
+
+__device__ __forceinline__ uint32_t count_active_ranges(const uint8_t* modes, uint32_t route,
+                                                        uint32_t count)
+{
+    if (modes == nullptr) return 0;
+    uint32_t active = 0;
+    for (uint32_t r = 0; r < count; ++r)
+        if (modes[static_cast<size_t>(route) * count + r] != 0) ++active;
+    return active;
+}
+
+__device__ __forceinline__ uint32_t count_matching_ranges(const gofann_routes& rt, uint32_t route,
+                                                          uint32_t sample)
+{
+    if (rt.range_modes == nullptr || rt.range_lower == nullptr || rt.range_upper == nullptr)
+        return 0;
+    uint32_t matched = 0;
+    for (uint32_t r = 0; r < rt.range_count; ++r) {
+        const size_t qf = static_cast<size_t>(route) * rt.range_count + r;
+        const uint8_t mode = rt.range_modes[qf];
+        if (mode == 0) continue;
+        if (rt.base_range_values == nullptr) return 0;
+        if (range_matches(mode, rt.range_lower[qf], rt.range_upper[qf],
+                          rt.base_range_values[static_cast<size_t>(sample) * rt.range_count + r]))
+            ++matched;
+    }
+    return matched;
+}
+
+__device__ __forceinline__ float apply_filter_bonuses(float dist, bool bit_match, uint32_t matched,
+                                                      float bit_bonus, float range_bonus)
+{
+    if (bit_match) dist *= bit_bonus;
+    for (uint32_t i = 0; i < matched; ++i) dist *= range_bonus;
+    return dist;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_min(float v)
+{
+    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v)
+{
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// XCD-aware block -> slot mapping: the dispatcher deals consecutive
+// workgroups round-robin over the 8 XCDs, so block b runs on XCD b % 8.
+// Slot ranges are handed out in contiguous runs per XCD, so routes sorted by
+// graph group share one XCD's L2.  A bijection on [0, nblocks).
+__device__ __forceinline__ uint32_t xcd_slot(uint32_t b, uint32_t nblocks)
+{
+    const uint32_t xcd = b & 7u;
+    const uint32_t k = b >> 3;
+    const uint32_t q = nblocks >> 3;
+    const uint32_t r = nblocks & 7u;
+    return xcd * q + (xcd < r ? xcd : r) + k;
+}
+
+}  // namespace gofann

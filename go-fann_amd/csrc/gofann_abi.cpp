@@ -1,0 +1,239 @@
+// gofann_abi.cpp -- extern "C" entry points of gofann_hip.h.  Validates
+// arguments, maps them to the kernel launchers and converts every failure
+// into a status code plus a message (no exception crosses the ABI).
+#include <hip/hip_runtime.h>
+
+#include <new>
+#include <string>
+
+#include "gofann_hip.h"
+#include "gofann_internal.hpp"
+
+namespace gofann {
+
+void* Context::scratch(int slot, size_t bytes)
+{
+    if (slot < 0 || slot >= kScratchCount) return nullptr;
+    if (scratch_bytes[slot] >= bytes && scratch_ptr[slot] != nullptr) return scratch_ptr[slot];
+    if (scratch_ptr[slot] != nullptr) {
+        // The stream may still read the old buffer.
+        if (hipStreamSynchronize(stream) != hipSuccess) return nullptr;
+        (void)hipFree(scratch_ptr[slot]);
+        scratch_ptr[slot] = nullptr;
+        scratch_bytes[slot] = 0;
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    scratch_ptr[slot] = p;
+    scratch_bytes[slot] = bytes;
+    return p;
+}
+
+}  // namespace gofann
+
+using gofann::Context;
+
+namespace {
+Context* as_ctx(gofann_ctx* c) { return reinterpret_cast<Context*>(c); }
+
+template <class F>
+int guarded(gofann_ctx* c, F&& f)
+{
+    if (c == nullptr) return GOFANN_ERR_INVALID;
+    try {
+        return f(as_ctx(c));
+    } catch (const std::bad_alloc&) {
+        return as_ctx(c)->fail(GOFANN_ERR_NOMEM, "host allocation failed");
+    } catch (const std::exception& e) {
+        return as_ctx(c)->fail(GOFANN_ERR_INVALID, e.what());
+    }
+}
+}  // namespace
+
+extern "C" {
+
+int gofann_create(int device, gofann_ctx** out)
+{
+    if (out == nullptr) return GOFANN_ERR_INVALID;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return GOFANN_ERR_HIP;
+    if (hipSetDevice(device) != hipSuccess) return GOFANN_ERR_HIP;
+    Context* ctx = new (std::nothrow) Context();
+    if (ctx == nullptr) return GOFANN_ERR_NOMEM;
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        delete ctx;
+        return GOFANN_ERR_HIP;
+    }
+    ctx->compute_units = prop.multiProcessorCount;
+    ctx->lds_per_block = static_cast<int>(prop.sharedMemPerBlock);
+    int per_cu = 0;
+    if (hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, device) !=
+            hipSuccess ||
+        per_cu <= 0)
+        per_cu = ctx->lds_per_block;
+    ctx->lds_per_cu = per_cu;
+    *out = reinterpret_cast<gofann_ctx*>(ctx);
+    return GOFANN_OK;
+}
+
+void gofann_destroy(gofann_ctx* c)
+{
+    if (c == nullptr) return;
+    Context* ctx = as_ctx(c);
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (int i = 0; i < Context::kScratchCount; ++i)
+        if (ctx->scratch_ptr[i]) (void)hipFree(ctx->scratch_ptr[i]);
+    delete ctx;
+}
+
+const char* gofann_last_error(const gofann_ctx* c)
+{
+    if (c == nullptr) return "null context";
+    return reinterpret_cast<const Context*>(c)->error.c_str();
+}
+
+int gofann_set_stream(gofann_ctx* c, void* stream)
+{
+    return guarded(c, [&](Context* ctx) {
+        ctx->stream = static_cast<hipStream_t>(stream);
+        return GOFANN_OK;
+    });
+}
+
+int gofann_synchronize(gofann_ctx* c)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (hipStreamSynchronize(ctx->stream) != hipSuccess) return ctx->fail_hip("synchronize");
+        return GOFANN_OK;
+    });
+}
+
+int gofann_device_info(gofann_ctx* c, int* compute_units, int* lds_bytes)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (compute_units) *compute_units = ctx->compute_units;
+        if (lds_bytes) *lds_bytes = ctx->lds_per_cu;
+        return GOFANN_OK;
+    });
+}
+
+int gofann_pq_search(gofann_ctx* c, const gofann_pq_view* pq, const void* queries, int query_elem,
+                     const gofann_graph_view* graph, const gofann_predicate_view* predicate,
+                     const gofann_routes* routes, const gofann_search_params* params,
+                     uint32_t* out_ids, float* out_dists, gofann_route_stats* stats)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (!out_ids || !out_dists) return ctx->fail(GOFANN_ERR_INVALID, "null outputs");
+        return gofann::pq_search(ctx, pq, queries, query_elem, graph, predicate, routes, params,
+                                 out_ids, out_dists, stats);
+    });
+}
+
+int gofann_rabitq_prepare_queries(gofann_ctx* c, const gofann_rabitq_view* rq,
+                                  const float* queries, uint32_t count, const float* rotation,
+                                  gofann_rabitq_queries* out)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::rabitq_prepare(ctx, rq, queries, count, rotation, out);
+    });
+}
+
+int gofann_rabitq_search(gofann_ctx* c, const gofann_rabitq_view* rq,
+                         const gofann_rabitq_queries* prepared, const gofann_graph_view* graph,
+                         const gofann_predicate_view* predicate, const gofann_routes* routes,
+                         const gofann_search_params* params, uint32_t* out_ids, float* out_dists,
+                         gofann_route_stats* stats)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (!out_ids || !out_dists) return ctx->fail(GOFANN_ERR_INVALID, "null outputs");
+        return gofann::rabitq_search(ctx, rq, prepared, graph, predicate, routes, params, out_ids,
+                                     out_dists, stats);
+    });
+}
+
+int gofann_pq_posting_scan(gofann_ctx* c, const gofann_pq_view* pq, const void* queries,
+                           int query_elem, const gofann_predicate_view* predicate,
+                           const uint32_t* route_query, const uint32_t* cand_ids,
+                           const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                           uint32_t routes, int shortlist_k, uint32_t* out_ids, float* out_dists,
+                           uint32_t* pass_counts)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (routes > 0 && (!route_query || !cand_ids || !cand_offsets || !cand_sizes || !out_ids ||
+                           !out_dists))
+            return ctx->fail(GOFANN_ERR_INVALID, "posting scan arrays missing");
+        return gofann::pq_posting_scan(ctx, pq, queries, query_elem, predicate, route_query,
+                                       cand_ids, cand_offsets, cand_sizes, routes, shortlist_k,
+                                       out_ids, out_dists, pass_counts);
+    });
+}
+
+int gofann_rabitq_posting_scan(gofann_ctx* c, const gofann_rabitq_view* rq,
+                               const gofann_rabitq_queries* prepared,
+                               const gofann_predicate_view* predicate,
+                               const uint32_t* route_query, const uint32_t* cand_ids,
+                               const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                               uint32_t routes, int shortlist_k, uint32_t* out_ids,
+                               float* out_dists, uint32_t* pass_counts)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (routes > 0 && (!route_query || !cand_ids || !cand_offsets || !cand_sizes || !out_ids ||
+                           !out_dists))
+            return ctx->fail(GOFANN_ERR_INVALID, "posting scan arrays missing");
+        return gofann::rabitq_posting_scan(ctx, rq, prepared, predicate, route_query, cand_ids,
+                                           cand_offsets, cand_sizes, routes, shortlist_k, out_ids,
+                                           out_dists, pass_counts);
+    });
+}
+
+int gofann_exact_rerank(gofann_ctx* c, const void* base, int base_elem, uint32_t dim,
+                        uint32_t samples, const void* queries, const uint32_t* route_query,
+                        const uint32_t* shortlist, uint32_t width, uint32_t routes, uint32_t topk,
+                        uint32_t* out_ids, float* out_dists)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (routes > 0 && (!out_ids || !out_dists))
+            return ctx->fail(GOFANN_ERR_INVALID, "null outputs");
+        return gofann::exact_rerank(ctx, base, base_elem, dim, samples, queries, route_query,
+                                    shortlist, width, routes, topk, out_ids, out_dists);
+    });
+}
+
+int gofann_predicate_masks(gofann_ctx* c, const gofann_predicate_view* predicate,
+                           const uint32_t* route_ids, const uint32_t* sample_ids, uint32_t n,
+                           uint32_t* masks)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::predicate_masks(ctx, predicate, route_ids, sample_ids, n, masks);
+    });
+}
+
+int gofann_pq_score(gofann_ctx* c, const gofann_pq_view* pq, const void* queries, int query_elem,
+                    const uint32_t* q_idx, const uint32_t* s_idx, uint32_t n, float* out)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (n > 0 && (!q_idx || !s_idx || !out))
+            return ctx->fail(GOFANN_ERR_INVALID, "score arrays missing");
+        return gofann::pq_score(ctx, pq, queries, query_elem, q_idx, s_idx, n, out);
+    });
+}
+
+int gofann_rabitq_score(gofann_ctx* c, const gofann_rabitq_view* rq,
+                        const gofann_rabitq_queries* prepared, const uint32_t* q_idx,
+                        const uint32_t* s_idx, uint32_t n, float* out, int32_t* ip_int)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (n > 0 && (!q_idx || !s_idx || !out))
+            return ctx->fail(GOFANN_ERR_INVALID, "score arrays missing");
+        return gofann::rabitq_score(ctx, rq, prepared, q_idx, s_idx, n, out, ip_int);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// gofann_internal.hpp -- context object behind the C ABI (gofann_hip.h) and
+// the internal entry points each kernel file implements.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "gofann_hip.h"
+
+namespace gofann {
+
+// Owns the stream binding, device properties, the last error message and
+// the grow-only device scratch buffers of one host thread's search state
+// (the reference's per-context buffers, backend_pq.cu:6753-6990).
+struct Context {
+    enum ScratchSlot { kScratchHash = 0, kScratchSegments = 1, kScratchMisc = 2, kScratchCount = 3 };
+
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int compute_units = 0;
+    int lds_per_block = 0;
+    int lds_per_cu = 0;
+    std::string error;
+    void* scratch_ptr[kScratchCount] = {nullptr, nullptr, nullptr};
+    size_t scratch_bytes[kScratchCount] = {0, 0, 0};
+    int last_hash_in_lds = 0;
+    int last_lds_bytes = 0;
+
+    int fail(int code, const std::string& msg)
+    {
+        error = msg;
+        return code;
+    }
+    int fail_hip(const std::string& what)
+    {
+        const hipError_t e = hipGetLastError();
+        error = what + ": " + hipGetErrorString(e);
+        return GOFANN_ERR_HIP;
+    }
+    // Returns a device buffer of at least `bytes` for `slot` (grows, never
+    // shrinks; freed by gofann_destroy).  nullptr on allocation failure.
+    void* scratch(int slot, size_t bytes);
+};
+
+int pq_search(Context* ctx, const gofann_pq_view* pq, const void* queries, int query_elem,
+              const gofann_graph_view* g, const gofann_predicate_view* pred,
+              const gofann_routes* r, const gofann_search_params* p, uint32_t* out_ids,
+              float* out_dists, gofann_route_stats* stats);
+int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre,
+                  const gofann_graph_view* g, const gofann_predicate_view* pred,
+                  const gofann_routes* r, const gofann_search_params* p, uint32_t* out_ids,
+                  float* out_dists, gofann_route_stats* stats);
+int pq_score(Context* ctx, const gofann_pq_view* pq, const void* queries, int query_elem,
+             const uint32_t* q_idx, const uint32_t* s_idx, uint32_t n, float* out);
+int rabitq_score(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre,
+                 const uint32_t* q_idx, const uint32_t* s_idx, uint32_t n, float* out,
+                 int32_t* ip_int);
+int pq_posting_scan(Context* ctx, const gofann_pq_view* pq, const void* queries, int query_elem,
+                    const gofann_predicate_view* pred, const uint32_t* route_query,
+                    const uint32_t* cand_ids, const uint32_t* cand_offsets,
+                    const uint32_t* cand_sizes, uint32_t routes, int shortlist_k,
+                    uint32_t* out_ids, float* out_dists, uint32_t* pass_counts);
+int rabitq_posting_scan(Context* ctx, const gofann_rabitq_view* rq,
+                        const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
+                        const uint32_t* route_query, const uint32_t* cand_ids,
+                        const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                        uint32_t routes, int shortlist_k, uint32_t* out_ids, float* out_dists,
+                        uint32_t* pass_counts);
+int exact_rerank(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
+                 const void* queries, const uint32_t* route_query, const uint32_t* shortlist,
+                 uint32_t width, uint32_t routes, uint32_t topk, uint32_t* out_ids,
+                 float* out_dists);
+int predicate_masks(Context* ctx, const gofann_predicate_view* pred, const uint32_t* route_ids,
+                    const uint32_t* sample_ids, uint32_t n, uint32_t* masks);
+int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
+                   uint32_t count, const float* rotation, gofann_rabitq_queries* out);
+
+}  // namespace gofann

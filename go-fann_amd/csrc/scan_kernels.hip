@@ -1,0 +1,520 @@
+// scan_kernels.hip -- posting-list scans and exact rerank on gfx950.
+//
+// Posting scans (lowfreq_pq_scan_kernel, src/search/pq/backend_pq.cu:
+// 2046-2185; lowfreq_rabitq_resident_posting_kernel, src/search/rabitq/
+// backend_rabitq.cu:5494-5682) keep the `shortlist_k` best predicate-valid
+// candidates by (distance, id) through posting_shortlist_heap
+// (src/search/common/posting_shortlist_heap.cuh).  That heap keeps exactly
+// the k least admissible pairs of the scanned multiset (admissible: id !=
+// UINT32_MAX and distance <= FLT_MAX, so NaN and +inf never enter) and
+// emits them sorted, padded with (FLT_MAX, UINT32_MAX).  Here a 256-thread
+// workgroup scores a chunk of candidates in parallel into LDS and a bitonic
+// sort on the (distance, id) order merges the chunk with the running top-k,
+// which yields the same sorted multiset.
+//
+// Exact rerank: one wave per candidate (lane j accumulates dimensions
+// j mod 64 with fma, xor butterfly 32..1), unique valid candidates, top-k
+// by (distance, id) -- the host reranker's order (backend_pq.cu:2479-2592)
+// and resident_pq_batch_exact_rerank_kernel (backend_pq.cu:5201-5310).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "device_common.hpp"
+#include "gofann_internal.hpp"
+
+namespace gofann {
+
+constexpr int kScanThreads = 256;
+constexpr int kScanSlots = 2048;       // LDS pairs: running top-k + chunk
+constexpr int kMaxShortlist = 512;
+
+__device__ __forceinline__ bool admissible(float d, uint32_t id)
+{
+    return id != UINT32_MAX && d <= FLT_MAX;
+}
+
+// (distance, id) ascending; (FLT_MAX, UINT32_MAX) pads sort last.
+__device__ __forceinline__ bool pair_less(float ad, uint32_t aid, float bd, uint32_t bid)
+{
+    return ad < bd || (ad == bd && aid < bid);
+}
+
+__device__ void bitonic_sort(float* d, uint32_t* id, int n, int tid, int nthreads)
+{
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < n / 2; i += nthreads) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool ascending = (lo & size) == 0;
+                const bool swap = ascending ? pair_less(d[hi], id[hi], d[lo], id[lo])
+                                            : pair_less(d[lo], id[lo], d[hi], id[hi]);
+                if (swap) {
+                    const float td = d[lo];
+                    d[lo] = d[hi];
+                    d[hi] = td;
+                    const uint32_t ti = id[lo];
+                    id[lo] = id[hi];
+                    id[hi] = ti;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Serial-order ADC of the posting scan (backend_pq.cu:2102-2106).
+__device__ __forceinline__ float adc_serial(const float* lut, const uint8_t* row, int M)
+{
+    float dist = 0.0f;
+    if (M % 16 == 0) {
+        for (int m0 = 0; m0 < M; m0 += 16) {
+            const uint4 w = *reinterpret_cast<const uint4*>(row + m0);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+                dist += lut[(m0 + t) * 256 + ((ws[t >> 2] >> (8 * (t & 3))) & 0xffu)];
+        }
+    } else {
+        for (int m = 0; m < M; ++m) dist += lut[m * 256 + row[m]];
+    }
+    return dist;
+}
+
+struct ScanArgs {
+    gofann_predicate_view pred;
+    const uint32_t* route_query;
+    const uint32_t* cand_ids;
+    const uint32_t* cand_offsets;
+    const uint32_t* cand_sizes;
+    uint32_t routes;
+    int k;
+    int k_pow2;  // running-top-k region (power of two >= k)
+    uint32_t* out_ids;
+    float* out_dists;
+    uint32_t* pass_counts;
+    uint32_t table_bytes;
+    uint32_t samples;  // ids >= samples are skipped (RaBitQ scan)
+};
+
+struct PqScanScorer {
+    const uint8_t* codes;
+    const float* centroids;
+    const void* queries;
+    int query_f32;
+    uint32_t dim;
+    uint32_t pq_dim;
+    float* lut;
+
+    __device__ void setup(uint32_t q, int tid, unsigned char* lds)
+    {
+        lut = reinterpret_cast<float*>(lds);
+        const int M = static_cast<int>(pq_dim);
+        const int sub = static_cast<int>(dim) / M;
+        const float* qf = static_cast<const float*>(queries) + static_cast<size_t>(q) * dim;
+        const uint8_t* qu = static_cast<const uint8_t*>(queries) + static_cast<size_t>(q) * dim;
+        for (int e = tid; e < M * 256; e += kScanThreads) {
+            const int mm = e >> 8, k = e & 255;
+            const float* crow = centroids + static_cast<size_t>(k) * dim;
+            float acc = 0.0f;
+            for (int t = 0; t < sub; ++t) {
+                const int d = mm * sub + t;
+                const float qv = query_f32 ? qf[d] : static_cast<float>(qu[d]);
+                const float diff = qv - crow[d];
+                acc = fmaf(diff, diff, acc);
+            }
+            lut[e] = acc;
+        }
+    }
+    __device__ float score(uint32_t sample) const
+    {
+        return adc_serial(lut, codes + static_cast<size_t>(sample) * pq_dim, static_cast<int>(pq_dim));
+    }
+};
+
+struct RabitqScanScorer {
+    const uint8_t* codes;
+    const float* factors;
+    const uint32_t* anchor_ids;
+    const int8_t* q8;
+    const float* q_scale;
+    const float* q_k1;
+    const float* centroid_dists;
+    uint32_t num_anchors;
+    uint32_t padded_dim;
+    uint32_t* planes;
+    float scale, k1;
+    const float* g_row;
+
+    __device__ void setup(uint32_t q, int tid, unsigned char* lds)
+    {
+        planes = reinterpret_cast<uint32_t*>(lds);
+        const uint32_t words = padded_dim / 32;
+        const int8_t* qrow = q8 + static_cast<size_t>(q) * padded_dim;
+        for (uint32_t w = tid; w < words; w += kScanThreads) {
+            uint32_t pl[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (uint32_t b = 0; b < 32; ++b) {
+                const uint32_t v = static_cast<uint8_t>(qrow[w * 32 + b]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pl[j] |= ((v >> j) & 1u) << (31u - b);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) planes[w * 8 + j] = pl[j];
+        }
+        scale = q_scale[q];
+        k1 = q_k1[q];
+        g_row = centroid_dists + static_cast<size_t>(q) * num_anchors;
+    }
+    __device__ float score(uint32_t sample) const
+    {
+        const uint32_t words = padded_dim / 32;
+        const uint4* row =
+            reinterpret_cast<const uint4*>(codes + static_cast<size_t>(sample) * (padded_dim / 8));
+        uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t w4 = 0; w4 < words / 4; ++w4) {
+            const uint4 c = row[w4];
+            const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint4 p0 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2];
+                const uint4 p1 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2 + 1];
+                cnt[0] += __popc(p0.x & cw[t]);
+                cnt[1] += __popc(p0.y & cw[t]);
+                cnt[2] += __popc(p0.z & cw[t]);
+                cnt[3] += __popc(p0.w & cw[t]);
+                cnt[4] += __popc(p1.x & cw[t]);
+                cnt[5] += __popc(p1.y & cw[t]);
+                cnt[6] += __popc(p1.z & cw[t]);
+                cnt[7] += __popc(p1.w & cw[t]);
+            }
+        }
+        int32_t ip = 0;
+#pragma unroll
+        for (int j = 0; j < 7; ++j) ip += static_cast<int32_t>(cnt[j]) << j;
+        ip -= 128 * static_cast<int32_t>(cnt[7]);
+        const uint32_t anchor = anchor_ids[sample];
+        const float short_ip = static_cast<float>(ip) * scale;
+        const float t = short_ip + k1;
+        return fmaf(factors[static_cast<size_t>(sample) * 3 + 1], t,
+                    factors[static_cast<size_t>(sample) * 3] + g_row[anchor]);
+    }
+};
+
+template <class Scorer>
+__global__ __launch_bounds__(kScanThreads) void posting_scan_kernel(ScanArgs a, Scorer sc)
+{
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ float s_d[kScanSlots];
+    __shared__ uint32_t s_id[kScanSlots];
+    __shared__ uint32_t s_pass;
+    const int tid = static_cast<int>(threadIdx.x);
+    const uint32_t route = blockIdx.x;
+    if (route >= a.routes) return;
+
+    sc.setup(a.route_query[route], tid, lds);
+    for (int i = tid; i < kScanSlots; i += kScanThreads) {
+        s_d[i] = FLT_MAX;
+        s_id[i] = UINT32_MAX;
+    }
+    if (tid == 0) s_pass = 0;
+    __syncthreads();
+
+    const bool enabled = pred_enabled(a.pred, route);
+    const uint32_t begin = a.cand_offsets[route];
+    const uint32_t count = a.cand_sizes[route];
+    const int chunk = kScanSlots - a.k_pow2;
+    uint32_t passes = 0;
+    for (uint32_t base = 0; base < count; base += static_cast<uint32_t>(chunk)) {
+        for (int i = tid; i < chunk; i += kScanThreads) {
+            const uint32_t j = base + static_cast<uint32_t>(i);
+            float d = FLT_MAX;
+            uint32_t id = UINT32_MAX;
+            if (j < count) {
+                const uint32_t s = a.cand_ids[begin + j];
+                bool ok = s != UINT32_MAX && s < a.samples;
+                if (ok && enabled) {
+                    PredCounters c{0, 0};
+                    ok = pred_matches(a.pred, route, s, c);
+                    passes += ok ? 1u : 0u;
+                }
+                if (ok) {
+                    const float v = sc.score(s);
+                    if (admissible(v, s)) {
+                        d = v;
+                        id = s;
+                    }
+                }
+            }
+            s_d[a.k_pow2 + i] = d;
+            s_id[a.k_pow2 + i] = id;
+        }
+        __syncthreads();
+        bitonic_sort(s_d, s_id, kScanSlots, tid, kScanThreads);
+    }
+    atomicAdd(&s_pass, passes);
+    __syncthreads();
+    for (int i = tid; i < a.k; i += kScanThreads) {
+        a.out_ids[static_cast<size_t>(route) * a.k + i] = s_id[i];
+        a.out_dists[static_cast<size_t>(route) * a.k + i] = s_d[i];
+    }
+    if (tid == 0 && a.pass_counts) a.pass_counts[route] = s_pass;
+}
+
+// Exact rerank: one workgroup of 4 waves per route.
+struct RerankArgs {
+    const void* base;
+    int base_elem;
+    uint32_t dim;
+    uint32_t samples;
+    const void* queries;
+    const uint32_t* route_query;
+    const uint32_t* shortlist;
+    uint32_t width;
+    uint32_t width_pow2;
+    uint32_t routes;
+    uint32_t topk;
+    uint32_t* out_ids;
+    float* out_dists;
+};
+
+constexpr int kRerankThreads = 256;
+
+__global__ __launch_bounds__(kRerankThreads) void exact_rerank_kernel(RerankArgs a)
+{
+    __shared__ float s_d[kMaxShortlist];
+    __shared__ uint32_t s_id[kMaxShortlist];
+    __shared__ uint32_t s_keep[kMaxShortlist];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const uint32_t route = blockIdx.x;
+    if (route >= a.routes) return;
+    const uint32_t q = a.route_query[route];
+
+    for (uint32_t i = tid; i < a.width_pow2; i += kRerankThreads) {
+        s_d[i] = FLT_MAX;
+        s_id[i] = UINT32_MAX;
+    }
+    __syncthreads();
+    for (uint32_t c = wave; c < a.width; c += kRerankThreads / kWave) {
+        const uint32_t s = a.shortlist[static_cast<size_t>(route) * a.width + c];
+        if (s == UINT32_MAX || s >= a.samples) continue;  // uniform per wave
+        float acc = 0.0f;
+        if (a.base_elem == GOFANN_ELEM_U8) {
+            const uint8_t* b = static_cast<const uint8_t*>(a.base) + static_cast<size_t>(s) * a.dim;
+            const uint8_t* qq = static_cast<const uint8_t*>(a.queries) + static_cast<size_t>(q) * a.dim;
+            for (uint32_t d = lane; d < a.dim; d += kWave) {
+                const float diff = static_cast<float>(qq[d]) - static_cast<float>(b[d]);
+                acc = fmaf(diff, diff, acc);
+            }
+        } else if (a.base_elem == GOFANN_ELEM_F32) {
+            const float* b = static_cast<const float*>(a.base) + static_cast<size_t>(s) * a.dim;
+            const float* qq = static_cast<const float*>(a.queries) + static_cast<size_t>(q) * a.dim;
+            for (uint32_t d = lane; d < a.dim; d += kWave) {
+                const float diff = qq[d] - b[d];
+                acc = fmaf(diff, diff, acc);
+            }
+        } else {
+            const __half* b = static_cast<const __half*>(a.base) + static_cast<size_t>(s) * a.dim;
+            const float* qq = static_cast<const float*>(a.queries) + static_cast<size_t>(q) * a.dim;
+            for (uint32_t d = lane; d < a.dim; d += kWave) {
+                const float diff = qq[d] - __half2float(b[d]);
+                acc = fmaf(diff, diff, acc);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, kWave);
+        if (lane == 0) {
+            s_d[c] = acc;
+            s_id[c] = s;
+        }
+    }
+    __syncthreads();
+    bitonic_sort(s_d, s_id, static_cast<int>(a.width_pow2), tid, kRerankThreads);
+    // Unique valid ids (a duplicate has the same distance, so it is adjacent).
+    for (uint32_t i = tid; i < a.width_pow2; i += kRerankThreads)
+        s_keep[i] = (s_id[i] != UINT32_MAX && (i == 0 || s_id[i - 1] != s_id[i])) ? 1u : 0u;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t o = 0;
+        for (uint32_t i = 0; i < a.width_pow2 && o < a.topk; ++i) {
+            if (!s_keep[i]) continue;
+            a.out_ids[static_cast<size_t>(route) * a.topk + o] = s_id[i];
+            a.out_dists[static_cast<size_t>(route) * a.topk + o] = s_d[i];
+            ++o;
+        }
+        for (; o < a.topk; ++o) {
+            a.out_ids[static_cast<size_t>(route) * a.topk + o] = UINT32_MAX;
+            a.out_dists[static_cast<size_t>(route) * a.topk + o] = FLT_MAX;
+        }
+    }
+}
+
+// Candidate pass bitsets: each lane evaluates one (route, sample) pair; the
+// wave ballot is split into the reference's 32-bit words.
+__global__ __launch_bounds__(64) void predicate_masks_kernel(gofann_predicate_view pred,
+                                                            const uint32_t* route_ids,
+                                                            const uint32_t* sample_ids, uint32_t n,
+                                                            uint32_t* masks)
+{
+    const uint32_t i = blockIdx.x * kWave + threadIdx.x;
+    bool pass = false;
+    if (i < n) {
+        PredCounters c{0, 0};
+        pass = pred_enabled(pred, route_ids[i]) &&
+               pred_matches(pred, route_ids[i], sample_ids[i], c);
+    }
+    const uint64_t b = ballot(pass);
+    const uint32_t w0 = blockIdx.x * 2;
+    const uint32_t words = (n + 31) / 32;
+    if (threadIdx.x == 0 && w0 < words) masks[w0] = static_cast<uint32_t>(b);
+    if (threadIdx.x == 0 && w0 + 1 < words) masks[w0 + 1] = static_cast<uint32_t>(b >> 32);
+}
+
+int predicate_masks(Context* ctx, const gofann_predicate_view* pred, const uint32_t* route_ids,
+                    const uint32_t* sample_ids, uint32_t n, uint32_t* masks)
+{
+    if (!pred || !route_ids || !sample_ids || !masks)
+        return ctx->fail(GOFANN_ERR_INVALID, "predicate mask inputs incomplete");
+    if (n == 0) return GOFANN_OK;
+    hipLaunchKernelGGL(predicate_masks_kernel, dim3((n + kWave - 1) / kWave), dim3(kWave), 0,
+                       ctx->stream, *pred, route_ids, sample_ids, n, masks);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("predicate masks launch");
+    return GOFANN_OK;
+}
+
+namespace {
+uint32_t pow2_at_least(uint32_t x)
+{
+    uint32_t p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+}  // namespace
+
+int pq_posting_scan(Context* ctx, const gofann_pq_view* pq, const void* queries, int query_elem,
+                    const gofann_predicate_view* pred, const uint32_t* route_query,
+                    const uint32_t* cand_ids, const uint32_t* cand_offsets,
+                    const uint32_t* cand_sizes, uint32_t routes, int shortlist_k,
+                    uint32_t* out_ids, float* out_dists, uint32_t* pass_counts)
+{
+    if (!pq || !pq->codes || !pq->centroids || !queries || pq->pq_dim == 0 ||
+        pq->dim % pq->pq_dim != 0 || pq->pq_dim > 64)
+        return ctx->fail(GOFANN_ERR_INVALID, "PQ view invalid for posting scan (pq_dim <= 64)");
+    if (shortlist_k < 1 || shortlist_k > kMaxShortlist)
+        return ctx->fail(GOFANN_ERR_INVALID, "shortlist_k must be in [1, 512]");
+    if (routes == 0) return GOFANN_OK;
+    ScanArgs a;
+    a.pred = pred ? *pred : gofann_predicate_view{};
+    a.route_query = route_query;
+    a.cand_ids = cand_ids;
+    a.cand_offsets = cand_offsets;
+    a.cand_sizes = cand_sizes;
+    a.routes = routes;
+    a.k = shortlist_k;
+    a.k_pow2 = static_cast<int>(pow2_at_least(static_cast<uint32_t>(shortlist_k)));
+    a.out_ids = out_ids;
+    a.out_dists = out_dists;
+    a.pass_counts = pass_counts;
+    a.samples = pq->samples ? pq->samples : UINT32_MAX;
+    PqScanScorer sc;
+    sc.codes = pq->codes;
+    sc.centroids = pq->centroids;
+    sc.queries = queries;
+    sc.query_f32 = query_elem == GOFANN_ELEM_F32 ? 1 : 0;
+    sc.dim = pq->dim;
+    sc.pq_dim = pq->pq_dim;
+    sc.lut = nullptr;
+    const uint32_t lds = pq->pq_dim * 256u * 4u;
+    a.table_bytes = lds;
+    auto kern = posting_scan_kernel<PqScanScorer>;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
+        hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute posting scan");
+    hipLaunchKernelGGL(kern, dim3(routes), dim3(kScanThreads), lds, ctx->stream, a, sc);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("pq posting scan launch");
+    return GOFANN_OK;
+}
+
+int rabitq_posting_scan(Context* ctx, const gofann_rabitq_view* rq,
+                        const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
+                        const uint32_t* route_query, const uint32_t* cand_ids,
+                        const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                        uint32_t routes, int shortlist_k, uint32_t* out_ids, float* out_dists,
+                        uint32_t* pass_counts)
+{
+    if (!rq || !pre || !rq->codes || rq->padded_dim == 0 || rq->padded_dim % 128 != 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view invalid for posting scan");
+    if (shortlist_k < 1 || shortlist_k > kMaxShortlist)
+        return ctx->fail(GOFANN_ERR_INVALID, "shortlist_k must be in [1, 512]");
+    if (routes == 0) return GOFANN_OK;
+    ScanArgs a;
+    a.pred = pred ? *pred : gofann_predicate_view{};
+    a.route_query = route_query;
+    a.cand_ids = cand_ids;
+    a.cand_offsets = cand_offsets;
+    a.cand_sizes = cand_sizes;
+    a.routes = routes;
+    a.k = shortlist_k;
+    a.k_pow2 = static_cast<int>(pow2_at_least(static_cast<uint32_t>(shortlist_k)));
+    a.out_ids = out_ids;
+    a.out_dists = out_dists;
+    a.pass_counts = pass_counts;
+    a.samples = rq->samples ? rq->samples : UINT32_MAX;
+    RabitqScanScorer sc;
+    sc.codes = rq->codes;
+    sc.factors = rq->factors;
+    sc.anchor_ids = rq->anchor_ids;
+    sc.q8 = pre->q8;
+    sc.q_scale = pre->scale;
+    sc.q_k1 = pre->k1;
+    sc.centroid_dists = pre->centroid_dists;
+    sc.num_anchors = rq->num_anchors;
+    sc.padded_dim = rq->padded_dim;
+    sc.planes = nullptr;
+    sc.scale = sc.k1 = 0.0f;
+    sc.g_row = nullptr;
+    const uint32_t lds = rq->padded_dim;
+    a.table_bytes = lds;
+    hipLaunchKernelGGL(posting_scan_kernel<RabitqScanScorer>, dim3(routes), dim3(kScanThreads), lds,
+                       ctx->stream, a, sc);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("rabitq posting scan launch");
+    return GOFANN_OK;
+}
+
+int exact_rerank(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
+                 const void* queries, const uint32_t* route_query, const uint32_t* shortlist,
+                 uint32_t width, uint32_t routes, uint32_t topk, uint32_t* out_ids,
+                 float* out_dists)
+{
+    if (!base || !queries || !route_query || !shortlist || dim == 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "rerank inputs incomplete");
+    if (base_elem < GOFANN_ELEM_U8 || base_elem > GOFANN_ELEM_F16)
+        return ctx->fail(GOFANN_ERR_INVALID, "unknown base element type");
+    if (width == 0 || width > static_cast<uint32_t>(kMaxShortlist) || topk == 0 || topk > width)
+        return ctx->fail(GOFANN_ERR_INVALID, "rerank width must be in [1, 512], topk in [1, width]");
+    if (routes == 0) return GOFANN_OK;
+    RerankArgs a;
+    a.base = base;
+    a.base_elem = base_elem;
+    a.dim = dim;
+    a.samples = samples;
+    a.queries = queries;
+    a.route_query = route_query;
+    a.shortlist = shortlist;
+    a.width = width;
+    a.width_pow2 = pow2_at_least(width);
+    a.routes = routes;
+    a.topk = topk;
+    a.out_ids = out_ids;
+    a.out_dists = out_dists;
+    hipLaunchKernelGGL(exact_rerank_kernel, dim3(routes), dim3(kRerankThreads), 0, ctx->stream, a);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("exact rerank launch");
+    return GOFANN_OK;
+}
+
+}  // namespace gofann

@@ -1,0 +1,188 @@
+"""ctypes binding of libgofann_hip.so (C ABI declared in include/gofann_hip.h).
+
+The structures mirror the header field by field.  Device arrays are passed as
+raw pointers taken from torch tensors on the GPU; torch is used only for
+device memory and streams.  The library must exist (built by
+go-fann_amd/build.py): there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE.parent / "libgofann_hip.so"
+
+GOFANN_OK = 0
+EARLY_STOP_FIXED, EARLY_STOP_OFF, EARLY_STOP_ADAPTIVE = 0, 1, 2
+ELEM_U8, ELEM_F32, ELEM_F16 = 0, 1, 2
+
+P = C.c_void_p
+U32 = C.c_uint32
+
+
+class GraphView(C.Structure):
+    _fields_ = [("graph", P), ("row_to_sample", P), ("label_offset", P),
+                ("rows", U32), ("degree", U32), ("groups", U32), ("samples", U32)]
+
+
+class Clause(C.Structure):
+    _fields_ = [("label_begin", U32), ("label_end", U32), ("range_begin", U32),
+                ("range_end", U32)]
+
+
+class RangeAtom(C.Structure):
+    _fields_ = [("dimension", U32), ("mode", U32), ("lower", C.c_float),
+                ("upper", C.c_float)]
+
+
+class PredicateView(C.Structure):
+    _fields_ = [("route_offsets", P), ("route_handles", P), ("clauses", P),
+                ("ranges", P), ("route_enabled", P), ("route_compiled", P),
+                ("base_ranges", P), ("csr_offsets", P), ("csr_labels", P),
+                ("rows", U32), ("range_stride", U32), ("alpha", C.c_float),
+                ("pending_base_stop", C.c_int)]
+
+
+class Routes(C.Structure):
+    _fields_ = [("route_query", P), ("route_group", P), ("route_start", P),
+                ("row_filter_mask", P), ("query_filter_bits", P), ("range_modes", P),
+                ("range_lower", P), ("range_upper", P), ("base_range_values", P),
+                ("range_count", U32), ("count", U32), ("launch_order", P)]
+
+
+class SearchParams(C.Structure):
+    _fields_ = [("queue_limit", C.c_int), ("finish_limit", C.c_int),
+                ("early_stop_mode", C.c_int), ("max_steps", C.c_int),
+                ("stop_width", C.c_int), ("result_width", C.c_int),
+                ("bit_filter_bonus", C.c_float), ("range_filter_bonus", C.c_float),
+                ("predicate_bias", C.c_int)]
+
+
+class RouteStats(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("steps", "expanded", "passed", "scored",
+                                          "pred_rows", "pred_labels", "admitted",
+                                          "exhausted")]
+
+
+STATS_FIELDS = [f[0] for f in RouteStats._fields_]
+
+
+class PqView(C.Structure):
+    _fields_ = [("codes", P), ("centroids", P), ("dim", U32), ("pq_dim", U32),
+                ("samples", U32)]
+
+
+class RabitqView(C.Structure):
+    _fields_ = [("codes", P), ("factors", P), ("anchor_ids", P), ("anchors", P),
+                ("dim", U32), ("padded_dim", U32), ("num_anchors", U32),
+                ("samples", U32)]
+
+
+class RabitqQueries(C.Structure):
+    _fields_ = [("rotated", P), ("q8", P), ("scale", P), ("k1", P),
+                ("centroid_dists", P), ("count", U32)]
+
+
+# Every symbol include/gofann_hip.h declares, with its ctypes signature.
+SIGNATURES = {
+    "gofann_create": (C.c_int, [C.c_int, C.POINTER(P)]),
+    "gofann_destroy": (None, [P]),
+    "gofann_last_error": (C.c_char_p, [P]),
+    "gofann_set_stream": (C.c_int, [P, P]),
+    "gofann_synchronize": (C.c_int, [P]),
+    "gofann_device_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "gofann_pq_search": (C.c_int, [P, C.POINTER(PqView), P, C.c_int, C.POINTER(GraphView),
+                                   C.POINTER(PredicateView), C.POINTER(Routes),
+                                   C.POINTER(SearchParams), P, P, P]),
+    "gofann_rabitq_prepare_queries": (C.c_int, [P, C.POINTER(RabitqView), P, U32, P,
+                                                C.POINTER(RabitqQueries)]),
+    "gofann_rabitq_search": (C.c_int, [P, C.POINTER(RabitqView), C.POINTER(RabitqQueries),
+                                       C.POINTER(GraphView), C.POINTER(PredicateView),
+                                       C.POINTER(Routes), C.POINTER(SearchParams), P, P, P]),
+    "gofann_pq_posting_scan": (C.c_int, [P, C.POINTER(PqView), P, C.c_int,
+                                         C.POINTER(PredicateView), P, P, P, P, U32, C.c_int,
+                                         P, P, P]),
+    "gofann_rabitq_posting_scan": (C.c_int, [P, C.POINTER(RabitqView),
+                                             C.POINTER(RabitqQueries),
+                                             C.POINTER(PredicateView), P, P, P, P, U32,
+                                             C.c_int, P, P, P]),
+    "gofann_exact_rerank": (C.c_int, [P, P, C.c_int, U32, U32, P, P, P, U32, U32, U32, P, P]),
+    "gofann_predicate_masks": (C.c_int, [P, C.POINTER(PredicateView), P, P, U32, P]),
+    "gofann_pq_score": (C.c_int, [P, C.POINTER(PqView), P, C.c_int, P, P, U32, P]),
+    "gofann_rabitq_score": (C.c_int, [P, C.POINTER(RabitqView), C.POINTER(RabitqQueries),
+                                      P, P, U32, P, P]),
+}
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load the HIP library; raises if it was not built (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: run go-fann_amd/build.py "
+                           "(the GPU path has no CPU fallback)")
+    lib = C.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_GLOBAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a torch tensor, None for None."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+class GofannError(RuntimeError):
+    pass
+
+
+class Context:
+    """Owns one gofann_ctx bound to torch's current stream on `device`."""
+
+    def __init__(self, device: int = 0):
+        import torch
+        self.lib = load()
+        self.device = device
+        h = P()
+        rc = self.lib.gofann_create(device, C.byref(h))
+        if rc != GOFANN_OK:
+            raise GofannError(f"gofann_create failed ({rc})")
+        self.handle = h
+        self.bind_stream(torch.cuda.current_stream(device))
+
+    def bind_stream(self, stream) -> None:
+        self.check(self.lib.gofann_set_stream(self.handle, P(stream.cuda_stream)))
+
+    def check(self, rc: int) -> None:
+        if rc != GOFANN_OK:
+            msg = self.lib.gofann_last_error(self.handle)
+            raise GofannError(f"gofann call failed ({rc}): {msg.decode() if msg else ''}")
+
+    def synchronize(self) -> None:
+        self.check(self.lib.gofann_synchronize(self.handle))
+
+    def device_info(self) -> tuple[int, int]:
+        cu, lds = C.c_int(), C.c_int()
+        self.check(self.lib.gofann_device_info(self.handle, C.byref(cu), C.byref(lds)))
+        return cu.value, lds.value
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.gofann_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,226 @@
+"""Host driver of the GPU stage (mirrors backend_pq / backend_rabitq's
+init_benchmark_contexts -> execute_single_iteration shape,
+src/search/pq/backend_pq.cu:11088-11439): device-resident index arrays,
+route batches through the C ABI, rerank, route merge.
+
+All compute runs in libgofann_hip.so kernels; torch supplies device memory
+and the stream.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import (ELEM_F16, ELEM_F32, ELEM_U8, GraphView, PqView, PredicateView,
+                   RabitqQueries, RabitqView, Routes, SearchParams)
+
+DEV = "cuda"
+
+
+def to_dev(a, dtype=None):
+    if a is None:
+        return None
+    if isinstance(a, torch.Tensor):
+        return a.to(DEV).contiguous()
+    arr = np.ascontiguousarray(a)
+    if arr.dtype.fields is not None:  # structured -> raw bytes
+        arr = arr.view(np.uint8).reshape(-1)
+    t = torch.from_numpy(arr.copy())
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.to(DEV)
+
+
+def u32(a):
+    """uint32 numpy -> int32 torch bit pattern on the device."""
+    return to_dev(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32))
+
+
+def u64(a):
+    return to_dev(np.ascontiguousarray(a, dtype=np.uint64).view(np.int64))
+
+
+@dataclass
+class DeviceGraph:
+    graph: torch.Tensor
+    row_to_sample: torch.Tensor
+    label_offset: torch.Tensor
+    csr_offsets: torch.Tensor
+    csr_labels: torch.Tensor
+    posting_ids: torch.Tensor
+    rows: int
+    degree: int
+    groups: int
+    samples: int
+
+    @classmethod
+    def upload(cls, index) -> "DeviceGraph":
+        g = index.graph if index.rows > 0 else np.full((1, index.degree), 0xFFFFFFFF, np.uint32)
+        r2s = index.row_to_sample if index.rows > 0 else np.zeros(1, np.uint32)
+        return cls(u32(g.reshape(-1)), u32(r2s), u32(index.label_offset), u32(index.csr_offsets),
+                   u32(index.csr_labels), u32(index.posting_ids), index.rows, index.degree,
+                   index.num_labels, int(index.csr_offsets.shape[0] - 1))
+
+    def view(self) -> GraphView:
+        return GraphView(_lib.ptr(self.graph), _lib.ptr(self.row_to_sample),
+                         _lib.ptr(self.label_offset), self.rows, self.degree, self.groups,
+                         self.samples)
+
+
+@dataclass
+class DeviceRoutes:
+    route_query: torch.Tensor
+    route_group: torch.Tensor
+    route_start: torch.Tensor
+    launch_order: torch.Tensor
+    pred_offsets: torch.Tensor
+    pred_handles: torch.Tensor
+    pred_clauses: torch.Tensor
+    pred_ranges: torch.Tensor
+    pred_enabled: torch.Tensor
+    pred_compiled: torch.Tensor
+    base_ranges: torch.Tensor | None
+    range_stride: int
+    count: int
+
+    @classmethod
+    def upload(cls, rs, base_ranges=None) -> "DeviceRoutes":
+        p = rs.predicate
+        br = None
+        stride = 0
+        if base_ranges is not None:
+            br = to_dev(np.ascontiguousarray(base_ranges, dtype=np.float32))
+            stride = int(base_ranges.shape[1])
+        n = max(rs.count, 1)
+        return cls(u32(rs.route_query if rs.count else np.zeros(1, np.uint32)),
+                   u32(rs.route_group if rs.count else np.zeros(1, np.uint32)),
+                   u32(rs.route_start if rs.count else np.zeros(1, np.uint32)),
+                   u32(np.arange(n, dtype=np.uint32)),
+                   u32(p.route_offsets), u32(p.handles), to_dev(p.clauses), to_dev(p.ranges),
+                   to_dev(p.enabled if rs.count else np.zeros(1, np.uint8)),
+                   to_dev(p.compiled if rs.count else np.zeros(1, np.uint8)),
+                   br, stride, rs.count)
+
+    def routes_view(self, begin: int = 0, end: int | None = None) -> Routes:
+        end = self.count if end is None else end
+        order = self.launch_order[begin:end]
+        return Routes(_lib.ptr(self.route_query), _lib.ptr(self.route_group),
+                      _lib.ptr(self.route_start), None, None, None, None, None, None, 0,
+                      end - begin, _lib.ptr(order))
+
+    def predicate_view(self, dg: DeviceGraph, alpha: float, pending_base_stop: bool,
+                       enabled: bool = True) -> PredicateView:
+        return PredicateView(_lib.ptr(self.pred_offsets), _lib.ptr(self.pred_handles),
+                             _lib.ptr(self.pred_clauses), _lib.ptr(self.pred_ranges),
+                             _lib.ptr(self.pred_enabled) if enabled else None,
+                             _lib.ptr(self.pred_compiled), _lib.ptr(self.base_ranges),
+                             _lib.ptr(dg.csr_offsets), _lib.ptr(dg.csr_labels),
+                             dg.samples, self.range_stride, float(alpha),
+                             1 if pending_base_stop else 0)
+
+
+def search_params(queue_limit=64, result_width=100, early_stop_mode=_lib.EARLY_STOP_ADAPTIVE,
+                  finish_limit=1, max_steps=0, stop_width=10, bias=True,
+                  bit_bonus=1.0, range_bonus=1.0) -> SearchParams:
+    return SearchParams(queue_limit, finish_limit, early_stop_mode, max_steps, stop_width,
+                        result_width, bit_bonus, range_bonus, 1 if bias else 0)
+
+
+def pq_view(codes: torch.Tensor, table: torch.Tensor) -> PqView:
+    return PqView(_lib.ptr(codes), _lib.ptr(table), int(table.shape[1]), int(codes.shape[1]),
+                  int(codes.shape[0]))
+
+
+def query_elem(q: torch.Tensor) -> int:
+    if q.dtype == torch.uint8:
+        return ELEM_U8
+    if q.dtype == torch.float32:
+        return ELEM_F32
+    raise ValueError("queries must be uint8 or float32")
+
+
+def run_pq_routes(ctx: _lib.Context, pqv: PqView, queries: torch.Tensor, dg: DeviceGraph,
+                  dr: DeviceRoutes, params: SearchParams, alpha: float = 0.15,
+                  pending_base_stop: bool = True, begin: int = 0, end: int | None = None,
+                  out=None):
+    end = dr.count if end is None else end
+    n = dr.count
+    W = params.result_width
+    if out is None:
+        ids = torch.empty(n * W, dtype=torch.int32, device=DEV)
+        dists = torch.empty(n * W, dtype=torch.float32, device=DEV)
+        stats = torch.zeros(n * 8, dtype=torch.int32, device=DEV)
+    else:
+        ids, dists, stats = out
+    gv = dg.view()
+    pv = dr.predicate_view(dg, alpha, pending_base_stop)
+    rv = dr.routes_view(begin, end)
+    ctx.check(ctx.lib.gofann_pq_search(ctx.handle, pqv, _lib.ptr(queries), query_elem(queries),
+                                       gv, pv, rv, params, _lib.ptr(ids), _lib.ptr(dists),
+                                       _lib.ptr(stats)))
+    return ids, dists, stats
+
+
+def run_pq_posting(ctx, pqv: PqView, queries: torch.Tensor, dg: DeviceGraph, dr: DeviceRoutes,
+                   cand_offsets, cand_sizes, shortlist_k: int):
+    n = dr.count
+    ids = torch.empty(max(n, 1) * shortlist_k, dtype=torch.int32, device=DEV)
+    dists = torch.empty(max(n, 1) * shortlist_k, dtype=torch.float32, device=DEV)
+    passes = torch.empty(max(n, 1), dtype=torch.int32, device=DEV)
+    if n == 0:
+        return ids[:0], dists[:0], passes[:0]
+    co = u32(cand_offsets)
+    cs = u32(cand_sizes)
+    pv = dr.predicate_view(dg, 0.0, False)
+    ctx.check(ctx.lib.gofann_pq_posting_scan(ctx.handle, pqv, _lib.ptr(queries),
+                                             query_elem(queries), pv, _lib.ptr(dr.route_query),
+                                             _lib.ptr(dg.posting_ids), _lib.ptr(co),
+                                             _lib.ptr(cs), n, shortlist_k, _lib.ptr(ids),
+                                             _lib.ptr(dists), _lib.ptr(passes)))
+    return ids, dists, passes
+
+
+def exact_rerank(ctx, base: torch.Tensor, queries: torch.Tensor, route_query: torch.Tensor,
+                 shortlist: torch.Tensor, width: int, routes: int, topk: int):
+    elem = {torch.uint8: ELEM_U8, torch.float32: ELEM_F32, torch.float16: ELEM_F16}[base.dtype]
+    ids = torch.empty(max(routes, 1) * topk, dtype=torch.int32, device=DEV)
+    dists = torch.empty(max(routes, 1) * topk, dtype=torch.float32, device=DEV)
+    if routes == 0:
+        return ids[:0], dists[:0]
+    ctx.check(ctx.lib.gofann_exact_rerank(ctx.handle, _lib.ptr(base), elem, int(base.shape[1]),
+                                          int(base.shape[0]), _lib.ptr(queries),
+                                          _lib.ptr(route_query), _lib.ptr(shortlist), width,
+                                          routes, topk, _lib.ptr(ids), _lib.ptr(dists)))
+    return ids, dists
+
+
+def merge_routes(route_to_query: np.ndarray, ids: np.ndarray, dists: np.ndarray, queries: int,
+                 topk: int):
+    """Route -> original query merge (rabitq_lowfreq_merge.h:709-815):
+    minimum distance per sample, (distance, id) order, top-k."""
+    width = ids.shape[1] if ids.ndim == 2 else topk
+    ids = ids.reshape(-1, width)
+    dists = dists.reshape(-1, width)
+    out_i = np.full((queries, topk), 0xFFFFFFFF, dtype=np.uint32)
+    out_d = np.full((queries, topk), np.finfo(np.float32).max, dtype=np.float32)
+    q_of = np.repeat(route_to_query.astype(np.int64), width)
+    fi = ids.reshape(-1).astype(np.uint32)
+    fd = dists.reshape(-1)
+    ok = fi != 0xFFFFFFFF
+    q_of, fi, fd = q_of[ok], fi[ok], fd[ok]
+    order = np.lexsort((fd, fi, q_of))  # per query, per sample, min distance first
+    q_of, fi, fd = q_of[order], fi[order], fd[order]
+    first = np.ones(len(fi), dtype=bool)
+    first[1:] = (q_of[1:] != q_of[:-1]) | (fi[1:] != fi[:-1])
+    q_of, fi, fd = q_of[first], fi[first], fd[first]
+    order = np.lexsort((fi, fd, q_of))
+    q_of, fi, fd = q_of[order], fi[order], fd[order]
+    start = np.searchsorted(q_of, np.arange(queries))
+    rank = np.arange(len(q_of)) - start[q_of]
+    keep = rank < topk
+    out_i[q_of[keep], rank[keep]] = fi[keep]
+    out_d[q_of[keep], rank[keep]] = fd[keep]
+    return out_i, out_d

@@ -1,0 +1,194 @@
+"""Seeded synthetic workloads of the BASELINE configurations.
+
+Seeds follow the convention seed = 1000 * cfg + role (1 centroids, 2 points,
+3 attributes, 4 queries, 5 quantizer / rotation, 6 graph).  Generation runs
+in torch on the requested device (the GPU for full-size configs, the CPU for
+test-size ones); the returned arrays live on that device.
+
+Attribute models:
+  * labels:  one categorical label per vector (uniform or Zipf)
+  * tags:    1..5 distinct tags per vector drawn Zipf(s) from a vocabulary
+  * ranges:  numeric attribute(s) per vector
+Query filters are conjunctions of labels/tags plus optional half-open ranges.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(int(seed))
+    return g
+
+
+@dataclass
+class Workload:
+    name: str
+    base: torch.Tensor            # [N, D] uint8 / float32 / float16
+    queries: torch.Tensor         # [Q, D] same element type (f32 queries for f16 base)
+    cluster_of: torch.Tensor      # [N] int64 generating mixture component
+    centroids: torch.Tensor       # [K, D] float32 mixture centres
+    label_offsets: np.ndarray     # CSR over samples, uint32 [N+1]
+    label_values: np.ndarray      # uint32, strictly increasing per row
+    num_labels: int
+    query_labels: list            # per query: list of required labels (AND)
+    base_ranges: np.ndarray | None = None      # [N, range_count] float32
+    query_ranges: list | None = None           # per query: list of (dim, mode, lo, hi)
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def n(self) -> int:
+        return int(self.base.shape[0])
+
+    @property
+    def dim(self) -> int:
+        return int(self.base.shape[1])
+
+
+def gaussian_mixture(n: int, dim: int, k: int, sigma: float, seed_base: int, device,
+                     centre_scale: float = 1.0, centre_offset: float = 0.0,
+                     chunk: int = 1 << 20):
+    """Points = centre[c] + N(0, sigma^2), c uniform over k centres."""
+    gc = _gen(seed_base + 1, device)
+    centres = torch.randn(k, dim, generator=gc, device=device) * centre_scale + centre_offset
+    gp = _gen(seed_base + 2, device)
+    cluster = torch.randint(0, k, (n,), generator=gp, device=device)
+    out = torch.empty(n, dim, dtype=torch.float32, device=device)
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        out[s:e] = centres[cluster[s:e]] + sigma * torch.randn(e - s, dim, generator=gp, device=device)
+    return out, cluster, centres
+
+
+def _zipf_probs(vocab: int, s: float) -> np.ndarray:
+    w = 1.0 / np.arange(1, vocab + 1, dtype=np.float64) ** s
+    return w / w.sum()
+
+
+def zipf_tags(n: int, vocab: int, s: float, min_tags: int, max_tags: int, seed: int):
+    """1..k distinct tags per row, Zipf-distributed; CSR (offsets, values)."""
+    rng = np.random.default_rng(seed)
+    probs = _zipf_probs(vocab, s)
+    counts = rng.integers(min_tags, max_tags + 1, size=n)
+    draws = rng.choice(vocab, size=(n, max_tags), p=probs)
+    # distinct tags: drop repeats inside a row, keep the first `count` distinct
+    rows = np.sort(draws, axis=1)
+    dup = np.zeros_like(rows, dtype=bool)
+    dup[:, 1:] = rows[:, 1:] == rows[:, :-1]
+    rows = np.where(dup, vocab, rows)                      # vocab = hole
+    rows = np.sort(rows, axis=1)
+    valid = rows < vocab
+    # keep at most counts[i] smallest-index distinct draws (order-free subset)
+    keep = np.arange(max_tags)[None, :] < counts[:, None]
+    keep &= valid
+    nnz = keep.sum(axis=1)
+    offsets = np.zeros(n + 1, dtype=np.uint64)
+    np.cumsum(nnz, out=offsets[1:])
+    values = rows[keep].astype(np.uint32)
+    return offsets.astype(np.uint32), values
+
+
+def categorical_labels(n: int, vocab: int, seed: int, zipf_s: float | None = None):
+    rng = np.random.default_rng(seed)
+    if zipf_s is None:
+        lab = rng.integers(0, vocab, size=n)
+    else:
+        lab = rng.choice(vocab, size=n, p=_zipf_probs(vocab, zipf_s))
+    offsets = np.arange(n + 1, dtype=np.uint32)
+    return offsets, lab.astype(np.uint32)
+
+
+def label_frequencies(offsets: np.ndarray, values: np.ndarray, vocab: int) -> np.ndarray:
+    return np.bincount(values.astype(np.int64), minlength=vocab)
+
+
+def config1(n=1_000_000, nq=10_000, device="cpu", dim=128, k=256, sigma=0.3, labels=10):
+    """C1: fp32 mixture, one uniform label of 10, single-label equality queries."""
+    cfg = 1000
+    x, cl, cen = gaussian_mixture(n, dim, k, sigma, cfg, device)
+    gq = _gen(cfg + 4, device)
+    qc = torch.randint(0, k, (nq,), generator=gq, device=device)
+    q = cen[qc] + sigma * torch.randn(nq, dim, generator=gq, device=device)
+    lo, lv = categorical_labels(n, labels, cfg + 3)
+    rng = np.random.default_rng(cfg + 4)
+    ql = [[int(v)] for v in rng.integers(0, labels, size=nq)]
+    return Workload("C1", x, q, cl, cen, lo, lv, labels, ql,
+                    meta=dict(config=1, sigma=sigma, clusters=k))
+
+
+def config2(n=10_000_000, nq=100_000, device="cpu", dim=192, k=1024, sigma=16.0,
+            vocab=2000, zipf_s=1.1, sel_lo=0.001, sel_hi=0.20):
+    """C2: uint8 mixture (clipped), 1-5 Zipf tags, AND of 1-2 tags per query
+    with estimated selectivity in [sel_lo, sel_hi]."""
+    cfg = 2000
+    # centres uniform in [32, 224] per dimension, points clipped to 0..255
+    gc = _gen(cfg + 1, device)
+    cen = 32.0 + 192.0 * torch.rand(k, dim, generator=gc, device=device)
+    gp = _gen(cfg + 2, device)
+    cl = torch.randint(0, k, (n,), generator=gp, device=device)
+    chunk = 1 << 20
+    base = torch.empty(n, dim, dtype=torch.uint8, device=device)
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        v = cen[cl[s:e]] + sigma * torch.randn(e - s, dim, generator=gp, device=device)
+        base[s:e] = v.round_().clamp_(0, 255).to(torch.uint8)
+    gq = _gen(cfg + 4, device)
+    qc = torch.randint(0, k, (nq,), generator=gq, device=device)
+    q = (cen[qc] + sigma * torch.randn(nq, dim, generator=gq, device=device)).round_().clamp_(0, 255)
+    q = q.to(torch.uint8)
+    lo, lv = zipf_tags(n, vocab, zipf_s, 1, 5, cfg + 3)
+    freq = label_frequencies(lo, lv, vocab) / float(n)
+    rng = np.random.default_rng(cfg + 4)
+    probs = _zipf_probs(vocab, zipf_s)
+    ql = []
+    while len(ql) < nq:
+        m = int(rng.integers(1, 3))
+        tags = rng.choice(vocab, size=m, p=probs)
+        if m == 2 and tags[0] == tags[1]:
+            continue
+        sel = float(np.prod(freq[tags]))
+        if sel_lo <= sel <= sel_hi:
+            ql.append(sorted(int(t) for t in tags))
+    return Workload("C2", base, q, cl, cen, lo, lv, vocab, ql,
+                    meta=dict(config=2, sigma=sigma, clusters=k))
+
+
+def small_labelled(n=4096, nq=64, dim=32, k=16, sigma=0.6, labels=6, seed=77, device="cpu",
+                   dtype="f32", tags=False, ranges=False):
+    """Test-size workload: overlapping mixture so per-label kNN graphs are
+    navigable; optional tags (AND of 1-2) and one numeric range attribute."""
+    cfg = seed * 1000
+    x, cl, cen = gaussian_mixture(n, dim, k, sigma, cfg, device)
+    gq = _gen(cfg + 4, device)
+    qc = torch.randint(0, k, (nq,), generator=gq, device=device)
+    q = cen[qc] + sigma * torch.randn(nq, dim, generator=gq, device=device)
+    if dtype == "u8":
+        lo_, hi_ = float(x.min()), float(x.max())
+        sc = 255.0 / (hi_ - lo_)
+        x = ((x - lo_) * sc).round().clamp(0, 255).to(torch.uint8)
+        q = ((q - lo_) * sc).round().clamp(0, 255).to(torch.uint8)
+        cen = (cen - lo_) * sc
+    rng = np.random.default_rng(cfg + 3)
+    if tags:
+        lo, lv = zipf_tags(n, labels, 0.7, 1, 3, cfg + 3)
+        ql = []
+        for _ in range(nq):
+            m = int(rng.integers(1, 3))
+            ql.append(sorted(set(int(t) for t in rng.integers(0, labels, size=m))))
+    else:
+        lo, lv = categorical_labels(n, labels, cfg + 3)
+        ql = [[int(v)] for v in rng.integers(0, labels, size=nq)]
+    base_ranges = None
+    query_ranges = None
+    if ranges:
+        base_ranges = rng.integers(0, 1000, size=(n, 1)).astype(np.float32)
+        query_ranges = []
+        for _ in range(nq):
+            lo_v = float(rng.integers(0, 800))
+            query_ranges.append([(0, 3, lo_v, lo_v + float(rng.integers(100, 400)))])
+    return Workload("small", x, q, cl, cen, lo, lv, labels, ql, base_ranges, query_ranges,
+                    meta=dict(sigma=sigma, clusters=k))

@@ -1,0 +1,263 @@
+/*
+ * gofann_hip.h -- C ABI of the MI355X (gfx950) GPU stage of GO-FANN's
+ * filtered graph search.  Plain C: opaque context, POD views of
+ * caller-owned device arrays, int status codes, no exceptions and no
+ * framework types cross this boundary.
+ *
+ * Reference interfaces replaced (paths relative to the GO-FANN tree):
+ *   - kernel launch of native_warp_independent_search_kernel_impl
+ *     (src/search/pq/backend_pq.cu:5015-5199, launched :9863-9960)
+ *       -> gofann_pq_search
+ *   - native_rabitq_search_kernel (src/search/rabitq/backend_rabitq.cu:
+ *     4293-4470, launched :10874-10988)              -> gofann_rabitq_search
+ *   - lowfreq_pq_scan_kernel (backend_pq.cu:2136-2185) -> gofann_pq_posting_scan
+ *   - lowfreq_rabitq_resident_posting_kernel (backend_rabitq.cu:5751)
+ *                                                     -> gofann_rabitq_posting_scan
+ *   - init_prepared_query_state query preparation (backend_rabitq.cu:
+ *     7800-8084; RabitqQueryRotation src/search/rabitq/
+ *     rabitq_query_rotation.cuh:51-113)             -> gofann_rabitq_prepare_queries
+ *   - resident_pq_batch_exact_rerank_kernel (backend_pq.cu:5201-5310) and
+ *     highfreq_float_gpu_l2_kernel/_topk_kernel (backend_rabitq.cu:
+ *     6173-6270)                                     -> gofann_exact_rerank
+ *
+ * Conventions (mirroring check_cuda/fail_pq, backend_pq.cu:1015, 1338-1343):
+ * every call returns GOFANN_OK or a negative status and records a message
+ * retrievable with gofann_last_error(ctx).  All array pointers are device
+ * pointers unless a field says otherwise; the library never frees them.
+ * Calls are asynchronous on the context's stream; outputs are valid after
+ * gofann_synchronize (or an event recorded on that stream).  One context
+ * per host thread; contexts never share scratch memory.
+ */
+#ifndef GOFANN_HIP_H
+#define GOFANN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GOFANN_OK 0
+#define GOFANN_ERR_INVALID -1
+#define GOFANN_ERR_HIP -2
+#define GOFANN_ERR_UNSUPPORTED -3
+#define GOFANN_ERR_NOMEM -4
+
+#define GOFANN_EARLY_STOP_FIXED 0 /* backend_pq.cu:1615-1617 */
+#define GOFANN_EARLY_STOP_OFF 1
+#define GOFANN_EARLY_STOP_ADAPTIVE 2
+
+#define GOFANN_ELEM_U8 0
+#define GOFANN_ELEM_F32 1
+#define GOFANN_ELEM_F16 2
+
+typedef struct gofann_ctx gofann_ctx;
+
+/* ---- context (replaces init_graph_context / cleanup, backend_pq.cu:6753) */
+int gofann_create(int device, gofann_ctx** out);
+void gofann_destroy(gofann_ctx* ctx);
+const char* gofann_last_error(const gofann_ctx* ctx);
+/* Use a caller-created hipStream_t (passed as void*); NULL = default. */
+int gofann_set_stream(gofann_ctx* ctx, void* hip_stream);
+int gofann_synchronize(gofann_ctx* ctx);
+/* Number of the device's compute units and its LDS per workgroup. */
+int gofann_device_info(gofann_ctx* ctx, int* compute_units, int* lds_bytes);
+
+/* ---- device arrays -------------------------------------------------------
+ * Label-partitioned graph (GraphMetadata + resident graph, src/data/
+ * dataloader.h:583-602, backend_pq.cu:1516-1523).  Group g owns global rows
+ * [label_offset[g], label_offset[g] + label_size[g]); adjacency entries are
+ * label-local rows, UINT32_MAX = empty slot. */
+typedef struct {
+    const uint32_t* graph;          /* [rows][degree] */
+    const uint32_t* row_to_sample;  /* [rows] */
+    const uint32_t* label_offset;   /* [groups] */
+    uint32_t rows;
+    uint32_t degree;                /* row stride; at most 64 are read */
+    uint32_t groups;
+    uint32_t samples;
+} gofann_graph_view;
+
+/* Device predicate (gpu_predicate::View, src/predicates/
+ * gpu_predicate_index.cuh:25-48), CSR storage, DNF clauses per route. */
+typedef struct {
+    uint32_t label_begin, label_end, range_begin, range_end;
+} gofann_clause;
+typedef struct {
+    uint32_t dimension, mode; /* mode 0 any, 1 (>lo), 2 (<hi), 3 [lo,hi) */
+    float lower, upper;
+} gofann_range_atom;
+typedef struct {
+    const uint32_t* route_offsets;     /* [routes+1] -> clauses */
+    const uint32_t* route_handles;     /* clause labels */
+    const gofann_clause* clauses;      /* NULL: conjunction of handles */
+    const gofann_range_atom* ranges;
+    const uint8_t* route_enabled;      /* NULL: enabled iff csr_offsets */
+    const uint8_t* route_compiled;     /* NULL: none compiled */
+    const float* base_ranges;          /* [samples][range_stride] */
+    const uint32_t* csr_offsets;       /* [samples+1] sample-major labels */
+    const uint32_t* csr_labels;        /* strictly increasing per row */
+    uint32_t rows;                     /* samples */
+    uint32_t range_stride;
+    float alpha;                       /* bias penalty factor */
+    int pending_base_stop;
+} gofann_predicate_view;
+
+/* Routes of one batch.  Route r searches group route_group[r] from the
+ * label-local seed route_start[r] with query vector route_query[r].  The
+ * legacy filter arrays (uncompiled routes) may be NULL = pass. */
+typedef struct {
+    const uint32_t* route_query;
+    const uint32_t* route_group;
+    const uint32_t* route_start;
+    const uint64_t* row_filter_mask;   /* [rows] */
+    const uint64_t* query_filter_bits; /* [routes] */
+    const uint8_t* range_modes;        /* [routes][range_count] */
+    const float* range_lower;
+    const float* range_upper;
+    const float* base_range_values;    /* [samples][range_count] */
+    uint32_t range_count;
+    uint32_t count;
+    /* Optional host-side hint: launch order (device array of route ids);
+     * NULL = identity.  Results stay indexed by route id. */
+    const uint32_t* launch_order;
+} gofann_routes;
+
+typedef struct {
+    int queue_limit;    /* beam Q */
+    int finish_limit;   /* fixed early stop limit */
+    int early_stop_mode;
+    int max_steps;      /* 0 = unlimited */
+    int stop_width;     /* <= 10 */
+    int result_width;   /* W, shortlist handed to rerank, <= 512 */
+    float bit_filter_bonus;
+    float range_filter_bonus;
+    int predicate_bias; /* kPredicateBias */
+} gofann_search_params;
+
+/* Per-route counters emitted by the traversal kernels (bytes model). */
+typedef struct {
+    int32_t steps;
+    int32_t expanded;
+    int32_t passed;
+    int32_t scored;
+    int32_t pred_rows;
+    int32_t pred_labels;
+    int32_t admitted;
+    int32_t exhausted;
+} gofann_route_stats;
+
+typedef struct {
+    const uint8_t* codes;     /* [samples][pq_dim] */
+    const float* centroids;   /* [256][dim] */
+    uint32_t dim;
+    uint32_t pq_dim;
+    uint32_t samples;
+} gofann_pq_view;
+
+typedef struct {
+    const uint8_t* codes;          /* [samples][padded_dim/8], MSB-first u32 words */
+    const float* factors;          /* [samples][3] f_add, f_rescale, f_err */
+    const uint32_t* anchor_ids;    /* [samples] */
+    const float* anchors;          /* [anchors][padded_dim], rotated centroids */
+    uint32_t dim;
+    uint32_t padded_dim;
+    uint32_t num_anchors;
+    uint32_t samples;
+} gofann_rabitq_view;
+
+/* Prepared RaBitQ queries (init_prepared_query_state outputs). */
+typedef struct {
+    float* rotated;          /* [queries][padded_dim] */
+    int8_t* q8;              /* [queries][padded_dim] */
+    float* scale;            /* [queries] */
+    float* k1;               /* [queries] */
+    float* centroid_dists;   /* [queries][num_anchors] */
+    uint32_t count;
+} gofann_rabitq_queries;
+
+/* ---- PQ traversal (backend_pq.cu:3980-5199, device-resident transport).
+ * queries: [n][dim] u8 (query_elem GOFANN_ELEM_U8) or f32.  Outputs per
+ * route: out_ids/out_dists [routes][result_width] ascending, sample ids,
+ * UINT32_MAX / FLT_MAX padding; stats may be NULL. */
+int gofann_pq_search(gofann_ctx* ctx, const gofann_pq_view* pq,
+                     const void* queries, int query_elem,
+                     const gofann_graph_view* graph,
+                     const gofann_predicate_view* predicate,
+                     const gofann_routes* routes,
+                     const gofann_search_params* params,
+                     uint32_t* out_ids, float* out_dists,
+                     gofann_route_stats* stats);
+
+/* ---- RaBitQ query preparation: rotation GEMM on MFMA (FP32 operands),
+ * int8 quantization, query factors, centroid distances.  queries [n][dim]
+ * f32; rotation [dim][padded_dim] row-major (y = q R). */
+int gofann_rabitq_prepare_queries(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                                  const float* queries, uint32_t count,
+                                  const float* rotation,
+                                  gofann_rabitq_queries* out);
+
+/* ---- RaBitQ traversal (backend_rabitq.cu:3487-4470). */
+int gofann_rabitq_search(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                         const gofann_rabitq_queries* prepared,
+                         const gofann_graph_view* graph,
+                         const gofann_predicate_view* predicate,
+                         const gofann_routes* routes,
+                         const gofann_search_params* params,
+                         uint32_t* out_ids, float* out_dists,
+                         gofann_route_stats* stats);
+
+/* ---- posting scans (backend_pq.cu:2046-2185; backend_rabitq.cu:5494-5682).
+ * Route r scans sample ids cand_ids[cand_offsets[r] .. + cand_sizes[r]).
+ * Outputs [routes][shortlist_k] ascending by (distance, id); pass_counts
+ * (may be NULL) receives the predicate passes per route. */
+int gofann_pq_posting_scan(gofann_ctx* ctx, const gofann_pq_view* pq,
+                           const void* queries, int query_elem,
+                           const gofann_predicate_view* predicate,
+                           const uint32_t* route_query, const uint32_t* cand_ids,
+                           const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                           uint32_t routes, int shortlist_k,
+                           uint32_t* out_ids, float* out_dists,
+                           uint32_t* pass_counts);
+
+int gofann_rabitq_posting_scan(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                               const gofann_rabitq_queries* prepared,
+                               const gofann_predicate_view* predicate,
+                               const uint32_t* route_query, const uint32_t* cand_ids,
+                               const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                               uint32_t routes, int shortlist_k,
+                               uint32_t* out_ids, float* out_dists,
+                               uint32_t* pass_counts);
+
+/* ---- exact rerank on the GPU: per route, unique valid candidates of the
+ * shortlist, exact L2 against base[samples][dim] (u8 / f32 / f16 with f32
+ * queries for f32 and f16, u8 queries for u8), top-k by (distance, id). */
+int gofann_exact_rerank(gofann_ctx* ctx, const void* base, int base_elem,
+                        uint32_t dim, uint32_t samples, const void* queries,
+                        const uint32_t* route_query, const uint32_t* shortlist,
+                        uint32_t width, uint32_t routes, uint32_t topk,
+                        uint32_t* out_ids, float* out_dists);
+
+/* ---- device predicate bitsets (prepare_candidate_pass_masks,
+ * src/predicates/gpu_predicate_parallel.cuh:21-42): bit i % 32 of
+ * masks[i / 32] = matches(route_ids[i], sample_ids[i]); ceil(n/32) words. */
+int gofann_predicate_masks(gofann_ctx* ctx, const gofann_predicate_view* predicate,
+                           const uint32_t* route_ids, const uint32_t* sample_ids,
+                           uint32_t n, uint32_t* masks);
+
+/* ---- batched scoring of explicit candidate lists (minimum-slice entry
+ * points): out[i] = ADC / RaBitQ estimate of (query q_idx[i], sample s[i]).
+ * PQ uses the traversal's summation order; RaBitQ also returns the exact
+ * integer dot product ip_int[i] (may be NULL). */
+int gofann_pq_score(gofann_ctx* ctx, const gofann_pq_view* pq, const void* queries,
+                    int query_elem, const uint32_t* q_idx, const uint32_t* s_idx,
+                    uint32_t n, float* out);
+int gofann_rabitq_score(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                        const gofann_rabitq_queries* prepared, const uint32_t* q_idx,
+                        const uint32_t* s_idx, uint32_t n, float* out, int32_t* ip_int);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,314 @@
+"""ctypes front-end of the CPU oracle (oracle/libgofann_oracle.so) and of the
+reference-header checker (oracle/_ref/libgofann_ref.so).
+
+TEST INFRASTRUCTURE ONLY.  Importable from tests/, __graft_entry__.smoke()
+and bench.py's cpu_baseline leg; the product path never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libgofann_oracle.so"
+REF_LIB = HERE / "_ref" / "libgofann_ref.so"
+
+P = C.c_void_p
+U32 = C.c_uint32
+
+
+class Pair(C.Structure):
+    _fields_ = [("first", C.c_float), ("second", C.c_uint32), ("base", C.c_float)]
+
+
+class Predicate(C.Structure):
+    _fields_ = [("route_offsets", P), ("route_handles", P), ("clauses", P), ("ranges", P),
+                ("route_enabled", P), ("route_compiled", P), ("base_ranges", P),
+                ("csr_offsets", P), ("csr_labels", P), ("rows", U32), ("range_stride", U32),
+                ("alpha", C.c_float), ("pending_base_stop", C.c_int)]
+
+
+class PredCounters(C.Structure):
+    _fields_ = [("rows_checked", C.c_uint64), ("label_words", C.c_uint64),
+                ("range_values", C.c_uint64)]
+
+
+class Graph(C.Structure):
+    _fields_ = [("graph", P), ("degree", U32), ("row_to_sample", P), ("label_offset", P),
+                ("route_group", P), ("route_start", P), ("row_filter_mask", P),
+                ("query_filter_bits", P), ("range_modes", P), ("range_lower", P),
+                ("range_upper", P), ("base_range_values", P), ("range_count", U32)]
+
+
+class Params(C.Structure):
+    _fields_ = [("queue_limit", C.c_int), ("finish_limit", C.c_int),
+                ("early_stop_mode", C.c_int), ("max_steps", C.c_int), ("stop_width", C.c_int),
+                ("result_width", C.c_int), ("bit_filter_bonus", C.c_float),
+                ("range_filter_bonus", C.c_float), ("bias", C.c_int),
+                ("rabitq_verdict", C.c_int)]
+
+
+class Stats(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("steps", "expanded", "passed", "scored", "pred_rows",
+                                          "pred_labels", "admitted", "exhausted")]
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            raise RuntimeError(f"{LIB} missing: run make -C oracle")
+        _lib = C.CDLL(str(LIB))
+        _lib.orc_hash_code.restype = U32
+        _lib.orc_hash_test.restype = C.c_int
+        _lib.orc_smmh2_pop_max.restype = Pair
+        _lib.orc_smmh2_pop_min.restype = Pair
+        _lib.orc_smmh2_insert.argtypes = [P, C.POINTER(C.c_int), Pair]
+        _lib.orc_smmh2_pop_max.argtypes = [P, C.POINTER(C.c_int)]
+        _lib.orc_smmh2_pop_min.argtypes = [P, C.POINTER(C.c_int)]
+        for name in ("orc_pq_adc", "orc_priority", "orc_bias_penalty", "orc_rabitq_score_b1",
+                     "orc_l2_u8", "orc_l2_f32", "orc_l2_f16", "orc_half_to_float",
+                     "orc_minimum_pending_base", "orc_apply_filter_bonuses"):
+            getattr(_lib, name).restype = C.c_float
+        _lib.orc_priority.argtypes = [C.c_float, C.c_float, C.c_int, P]
+        _lib.orc_bias_penalty.argtypes = [C.c_float, C.c_float]
+        _lib.orc_rabitq_score_b1.argtypes = [C.c_int32, C.c_float, C.c_float, C.c_float,
+                                             C.c_float, C.c_float]
+        _lib.orc_half_to_float.argtypes = [C.c_uint16]
+        _lib.orc_minimum_pending_base.argtypes = [P, C.c_int, Pair, Pair, C.c_int, C.c_int]
+        _lib.orc_apply_filter_bonuses.argtypes = [C.c_float, C.c_int, U32, C.c_float, C.c_float]
+        _lib.orc_rabitq_ip_int.restype = C.c_int32
+        _lib.orc_rabitq_ip_popcount.restype = C.c_int32
+        _lib.orc_rabitq_ip_dp4a.restype = C.c_int32
+        _lib.orc_range_matches.argtypes = [U32, C.c_float, C.c_float, C.c_float]
+        _lib.orc_csr_contains.argtypes = [P, U32, U32, U32, P]
+        _lib.orc_pred_matches.argtypes = [C.POINTER(Predicate), U32, U32, P]
+        _lib.orc_pred_enabled.argtypes = [C.POINTER(Predicate), U32]
+    return _lib
+
+
+def ref():
+    """Reference-header checker, or None when oracle/_ref was not built."""
+    global _ref
+    if _ref is None:
+        if not REF_LIB.exists():
+            return None
+        _ref = C.CDLL(str(REF_LIB))
+        _ref.ref_priority.restype = C.c_float
+        _ref.ref_priority.argtypes = [C.c_float, C.c_float, C.c_int, P]
+        _ref.ref_minimum_pending_base.restype = C.c_float
+        _ref.ref_apply_filter_bonuses.restype = C.c_float
+        _ref.ref_apply_filter_bonuses.argtypes = [C.c_float, C.c_int, U32, C.c_float, C.c_float]
+        _ref.ref_fp16_decode.restype = C.c_float
+        _ref.ref_fp16_decode.argtypes = [C.c_uint16]
+        _ref.ref_fp16_l2_scalar.restype = C.c_float
+        _ref.ref_pred_matches.argtypes = [P, P, P, P, P, P, U32, P, P, U32, U32, U32]
+        _ref.ref_pred_enabled.argtypes = [P, P, P, U32]
+        _ref.ref_csr_contains.argtypes = [P, P, U32, U32, U32]
+        _ref.ref_minimum_pending_base.argtypes = [P, C.c_int, P, P, C.c_int, C.c_int]
+        _ref.ref_merge_routes.argtypes = [P, U32, U32, P, P, U32, U32, P, P]
+        _ref.ref_fp16_l2_scalar.argtypes = [P, P, U32]
+        _ref.ref_shortlist_sort.argtypes = [P, P, C.c_int]
+        _ref.ref_shortlist_insert.argtypes = [C.c_float, U32, P, P, C.c_int]
+        _ref.ref_shortlist_can_enter.argtypes = [C.c_float, U32, P, P, C.c_int]
+    return _ref
+
+
+def p(a):
+    """Address of a numpy array (None passes through)."""
+    if a is None:
+        return None
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def c_arr(a, dtype):
+    if a is None:
+        return None
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+class PredicateArrays:
+    """Keeps numpy buffers alive behind a Predicate struct."""
+
+    def __init__(self, route_offsets, handles, clauses, ranges, enabled, compiled,
+                 csr_offsets, csr_labels, rows, base_ranges=None, alpha=0.0,
+                 pending_base_stop=False):
+        self.arrs = dict(
+            route_offsets=c_arr(route_offsets, np.uint32), handles=c_arr(handles, np.uint32),
+            clauses=None if clauses is None else np.ascontiguousarray(clauses),
+            ranges=None if ranges is None else np.ascontiguousarray(ranges),
+            enabled=c_arr(enabled, np.uint8), compiled=c_arr(compiled, np.uint8),
+            csr_offsets=c_arr(csr_offsets, np.uint32), csr_labels=c_arr(csr_labels, np.uint32),
+            base_ranges=c_arr(base_ranges, np.float32))
+        a = self.arrs
+        stride = 0 if base_ranges is None else int(np.asarray(base_ranges).shape[1])
+        self.struct = Predicate(p(a["route_offsets"]), p(a["handles"]), p(a["clauses"]),
+                                p(a["ranges"]), p(a["enabled"]), p(a["compiled"]),
+                                p(a["base_ranges"]), p(a["csr_offsets"]), p(a["csr_labels"]),
+                                rows, stride, alpha, 1 if pending_base_stop else 0)
+
+    @classmethod
+    def from_plan(cls, compiled, index, base_ranges=None, alpha=0.0, pending_base_stop=False):
+        return cls(compiled.route_offsets, compiled.handles, compiled.clauses, compiled.ranges,
+                   compiled.enabled, compiled.compiled, index.csr_offsets, index.csr_labels,
+                   int(index.csr_offsets.shape[0] - 1), base_ranges, alpha, pending_base_stop)
+
+
+def params(queue_limit=64, result_width=100, early_stop_mode=2, finish_limit=1, max_steps=0,
+           stop_width=10, bias=True, bit_bonus=1.0, range_bonus=1.0, rabitq_verdict=0) -> Params:
+    return Params(queue_limit, finish_limit, early_stop_mode, max_steps, stop_width,
+                  result_width, bit_bonus, range_bonus, 1 if bias else 0, rabitq_verdict)
+
+
+def graph_struct(index, route_group, route_start):
+    keep = dict(graph=c_arr(index.graph.reshape(-1), np.uint32),
+                r2s=c_arr(index.row_to_sample, np.uint32),
+                lo=c_arr(index.label_offset, np.uint32),
+                rg=c_arr(route_group, np.uint32), rs=c_arr(route_start, np.uint32))
+    g = Graph(p(keep["graph"]), index.degree, p(keep["r2s"]), p(keep["lo"]), p(keep["rg"]),
+              p(keep["rs"]), None, None, None, None, None, None, 0)
+    return g, keep
+
+
+def pq_search(index, routes, pred: PredicateArrays, prm: Params, codes, table, queries):
+    """Oracle beam search of every route.  Returns ids [R][W] u32,
+    dists [R][W] f32, stats structured array."""
+    L = lib()
+    g, keep = graph_struct(index, routes.route_group, routes.route_start)
+    n = routes.count
+    W = prm.result_width
+    ids = np.empty((n, W), np.uint32)
+    dists = np.empty((n, W), np.float32)
+    stats = (Stats * max(n, 1))()
+    codes = c_arr(codes, np.uint8)
+    table = c_arr(table, np.float32)
+    qf = queries.dtype == np.float32
+    q = np.ascontiguousarray(queries)
+    rq = c_arr(routes.route_query, np.uint32)
+    rc = L.orc_pq_search_batch(C.byref(g), C.byref(pred.struct), C.byref(prm), p(codes),
+                               p(table), p(q), 1 if qf else 0, p(rq), int(table.shape[1]),
+                               int(codes.shape[1]), n, p(ids), p(dists), stats)
+    assert rc == 0
+    return ids, dists, stats_array(stats, n)
+
+
+def rabitq_search(index, routes, pred: PredicateArrays, prm: Params, codes, factors,
+                  anchor_ids, q8, scale, k1, cdist, num_anchors, padded_dim):
+    L = lib()
+    g, keep = graph_struct(index, routes.route_group, routes.route_start)
+    n = routes.count
+    W = prm.result_width
+    ids = np.empty((n, W), np.uint32)
+    dists = np.empty((n, W), np.float32)
+    stats = (Stats * max(n, 1))()
+    arrs = [c_arr(codes, np.uint8), c_arr(factors, np.float32), c_arr(anchor_ids, np.uint32),
+            c_arr(q8, np.int8), c_arr(scale, np.float32), c_arr(k1, np.float32),
+            c_arr(cdist, np.float32), c_arr(routes.route_query, np.uint32)]
+    rc = L.orc_rabitq_search_batch(C.byref(g), C.byref(pred.struct), C.byref(prm), p(arrs[0]),
+                                   U32(padded_dim // 8), p(arrs[1]), p(arrs[2]), p(arrs[3]),
+                                   p(arrs[4]), p(arrs[5]), p(arrs[6]), U32(num_anchors),
+                                   U32(padded_dim), p(arrs[7]), U32(n), p(ids), p(dists), stats)
+    assert rc == 0
+    return ids, dists, stats_array(stats, n)
+
+
+STATS_FIELDS = [f[0] for f in Stats._fields_]
+
+
+def stats_array(stats, n):
+    out = np.zeros((n, len(STATS_FIELDS)), np.int32)
+    for i in range(n):
+        out[i] = [getattr(stats[i], f) for f in STATS_FIELDS]
+    return out
+
+
+def pq_lut(table, query, pq_dim):
+    L = lib()
+    table = c_arr(table, np.float32)
+    lut = np.empty(pq_dim * 256, np.float32)
+    if query.dtype == np.uint8:
+        L.orc_pq_lut_u8(p(table), p(np.ascontiguousarray(query)), int(table.shape[1]), pq_dim,
+                        p(lut))
+    else:
+        L.orc_pq_lut_f32(p(table), p(c_arr(query, np.float32)), int(table.shape[1]), pq_dim,
+                         p(lut))
+    return lut
+
+
+def pq_adc(lut, code):
+    code = c_arr(code, np.uint8)
+    return lib().orc_pq_adc(p(lut), p(code), int(code.shape[0]))
+
+
+def rabitq_quantize(rotated_row):
+    r = c_arr(rotated_row, np.float32)
+    q8 = np.empty(r.shape[0], np.int8)
+    s = C.c_float()
+    lib().orc_rabitq_quantize(p(r), U32(r.shape[0]), p(q8), C.byref(s))
+    k1 = C.c_float()
+    lib().orc_rabitq_query_factors(p(r), U32(r.shape[0]), C.byref(k1), None)
+    return q8, s.value, k1.value
+
+
+def rabitq_ip(q8, code, which="int"):
+    q8 = c_arr(q8, np.int8)
+    code = c_arr(code, np.uint8)
+    fn = {"int": lib().orc_rabitq_ip_int, "popcount": lib().orc_rabitq_ip_popcount,
+          "dp4a": lib().orc_rabitq_ip_dp4a}[which]
+    return fn(p(q8), p(code), U32(q8.shape[0]))
+
+
+def posting_scan_pq(pred, codes, table, queries, route_query, cand_ids, cand_offsets,
+                    cand_sizes, k, score_first=False):
+    L = lib()
+    n = len(route_query)
+    ids = np.empty((max(n, 1), k), np.uint32)
+    dists = np.empty((max(n, 1), k), np.float32)
+    passes = np.empty(max(n, 1), np.uint32)
+    arrs = [c_arr(codes, np.uint8), c_arr(table, np.float32), np.ascontiguousarray(queries),
+            c_arr(route_query, np.uint32), c_arr(cand_ids, np.uint32),
+            c_arr(cand_offsets, np.uint32), c_arr(cand_sizes, np.uint32)]
+    rc = L.orc_pq_posting_scan(C.byref(pred.struct) if pred else None, p(arrs[0]), p(arrs[1]),
+                               p(arrs[2]), 1 if queries.dtype == np.float32 else 0, p(arrs[3]),
+                               p(arrs[4]), p(arrs[5]), p(arrs[6]), U32(n),
+                               int(arrs[1].shape[1]), int(arrs[0].shape[1]), k,
+                               1 if score_first else 0, p(ids), p(dists), p(passes))
+    assert rc == 0
+    return ids[:n], dists[:n], passes[:n]
+
+
+def rerank(base, queries, route_query, shortlist, topk):
+    L = lib()
+    elem = {np.dtype(np.uint8): 0, np.dtype(np.float32): 1, np.dtype(np.float16): 2}[base.dtype]
+    base_c = np.ascontiguousarray(base)
+    if elem == 2:
+        base_c = base_c.view(np.uint16)
+    q = np.ascontiguousarray(queries)
+    sl = c_arr(shortlist, np.uint32)
+    n, width = sl.shape
+    ids = np.empty((n, topk), np.uint32)
+    dists = np.empty((n, topk), np.float32)
+    rq = c_arr(route_query, np.uint32)
+    rc = L.orc_rerank(p(base_c), elem, U32(base.shape[1]), U32(base.shape[0]), p(q), p(rq),
+                      p(sl), U32(width), U32(n), U32(topk), p(ids), p(dists))
+    assert rc == 0
+    return ids, dists
+
+
+def merge(route_to_query, ids, dists, queries, topk):
+    L = lib()
+    ids = c_arr(ids, np.uint32)
+    dists = c_arr(dists, np.float32)
+    r2q = c_arr(route_to_query, np.uint32)
+    n, width = ids.shape
+    oi = np.empty((queries, topk), np.uint32)
+    od = np.empty((queries, topk), np.float32)
+    assert L.orc_merge_routes(p(r2q), U32(n), U32(queries), p(ids), p(dists), U32(width),
+                              U32(topk), p(oi), p(od)) == 0
+    return oi, od

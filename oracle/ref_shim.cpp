@@ -1,0 +1,190 @@
+// ref_shim.cpp -- C entry points over the reference's own host-compilable
+// headers, compiled where they lie under the GO-FANN source tree (never
+// copied).  TEST INFRASTRUCTURE ONLY: the resulting oracle/_ref library is a
+// second checker for the oracle restatement; the product never loads it.
+//
+// Headers used (all plain C++ when not compiled by nvcc):
+//   src/predicates/gpu_predicate_index.cuh   (View, contains, matches, priority)
+//   src/predicates/range_filter.cuh          (range counting, filter bonuses)
+//   src/search/common/posting_shortlist_heap.cuh
+//   src/search/pq/pq_resident_posting.cuh    (bounds, candidate)
+//   src/search/rabitq/rabitq_lowfreq_merge.h (merge_route_results_to_original)
+//   src/data/fp16_l2.h                       (decode, scalar L2)
+#include "predicates/gpu_predicate_index.cuh"
+#include "predicates/range_filter.cuh"
+#include "search/common/posting_shortlist_heap.cuh"
+#include "search/pq/pq_resident_posting.cuh"
+#include "search/rabitq/rabitq_lowfreq_merge.h"
+#include "data/fp16_l2.h"
+
+#include <cstdint>
+#include <vector>
+
+namespace gp = go_fann::gpu_predicate;
+
+namespace {
+gp::View make_view(const uint32_t* route_offsets, const uint32_t* route_handles,
+                   const void* clauses, const void* ranges, const uint8_t* route_enabled,
+                   const float* base_ranges, uint32_t range_stride,
+                   const uint32_t* csr_offsets, const uint32_t* csr_labels, uint32_t rows)
+{
+    gp::View v;
+    v.route_offsets = route_offsets;
+    v.route_handles = route_handles;
+    v.clauses = static_cast<const gp::Clause*>(clauses);
+    v.ranges = static_cast<const gp::RangeAtom*>(ranges);
+    v.route_enabled = route_enabled;
+    v.base_ranges = base_ranges;
+    v.range_stride = range_stride;
+    v.csr_offsets = csr_offsets;
+    v.csr_labels = csr_labels;
+    v.rows = rows;
+    return v;
+}
+}  // namespace
+
+extern "C" {
+
+int ref_pred_matches(const uint32_t* route_offsets, const uint32_t* route_handles,
+                     const void* clauses, const void* ranges, const uint8_t* route_enabled,
+                     const float* base_ranges, uint32_t range_stride,
+                     const uint32_t* csr_offsets, const uint32_t* csr_labels, uint32_t rows,
+                     uint32_t route, uint32_t sample)
+{
+    const gp::View v = make_view(route_offsets, route_handles, clauses, ranges, route_enabled,
+                                 base_ranges, range_stride, csr_offsets, csr_labels, rows);
+    return gp::matches(v, route, sample) ? 1 : 0;
+}
+
+int ref_pred_enabled(const uint32_t* route_offsets, const uint8_t* route_enabled,
+                     const uint32_t* csr_offsets, uint32_t route)
+{
+    gp::View v;
+    v.route_offsets = route_offsets;
+    v.route_enabled = route_enabled;
+    v.csr_offsets = csr_offsets;
+    return gp::enabled(v, route) ? 1 : 0;
+}
+
+int ref_csr_contains(const uint32_t* csr_offsets, const uint32_t* csr_labels, uint32_t rows,
+                     uint32_t handle, uint32_t sample)
+{
+    gp::View v;
+    v.csr_offsets = csr_offsets;
+    v.csr_labels = csr_labels;
+    v.rows = rows;
+    return gp::contains(v, handle, sample) ? 1 : 0;
+}
+
+float ref_priority(float base, float penalty, int pass, int* saturated)
+{
+    bool s = false;
+    const float r = gp::priority(base, penalty, pass != 0, s);
+    if (saturated) *saturated = s ? 1 : 0;
+    return r;
+}
+
+// Pool entries are {first, second, base} triples (gp::BiasedPair layout).
+float ref_minimum_pending_base(const void* pool, int size, const void* current,
+                               const void* next, int current_valid, int next_valid)
+{
+    const auto* p = static_cast<const gp::BiasedPair*>(pool);
+    return gp::minimum_pending_base(p, size, *static_cast<const gp::BiasedPair*>(current),
+                                    *static_cast<const gp::BiasedPair*>(next),
+                                    current_valid != 0, next_valid != 0,
+                                    [](uint32_t payload) { return (payload & 0x80000000u) == 0; });
+}
+
+uint32_t ref_count_matching_ranges(const uint8_t* modes, const float* lower, const float* upper,
+                                   const float* base_values, uint32_t route, uint32_t sample,
+                                   uint32_t count)
+{
+    return go_fann::range_filter::count_matching_active_ranges(modes, lower, upper, base_values,
+                                                               route, sample, count);
+}
+
+uint32_t ref_count_active_ranges(const uint8_t* modes, uint32_t route, uint32_t count)
+{
+    return go_fann::range_filter::count_active_ranges(modes, route, count);
+}
+
+float ref_apply_filter_bonuses(float dist, int bit_match, uint32_t matched, float bit_bonus,
+                               float range_bonus)
+{
+    return go_fann::range_filter::apply_filter_bonuses(dist, bit_match != 0, matched, bit_bonus,
+                                                       range_bonus);
+}
+
+int ref_shortlist_can_enter(float dist, uint32_t id, const float* d, const uint32_t* ids, int k)
+{
+    return go_fann::posting_shortlist_heap::can_enter<uint32_t>(dist, id, d, ids, k) ? 1 : 0;
+}
+
+void ref_shortlist_insert(float dist, uint32_t id, float* d, uint32_t* ids, int k)
+{
+    go_fann::posting_shortlist_heap::insert<uint32_t>(dist, id, d, ids, k);
+}
+
+void ref_shortlist_sort(float* d, uint32_t* ids, int k)
+{
+    go_fann::posting_shortlist_heap::sort<uint32_t>(d, ids, k);
+}
+
+// pq_resident_posting::View fields in declaration order.
+int ref_pq_resident_probe(const uint32_t* group_offsets, const uint32_t* group_sizes,
+                          const uint32_t* sample_ids, const uint64_t* row_masks,
+                          const uint32_t* query_groups, const uint64_t* query_masks,
+                          const uint8_t* range_modes, const float* range_lower,
+                          const float* range_upper, const float* base_ranges, uint32_t groups,
+                          uint32_t rows, uint32_t samples, uint32_t routes,
+                          uint32_t range_count, uint32_t route, uint32_t index,
+                          uint32_t* out_begin, uint32_t* out_count)
+{
+    go_fann::pq_resident_posting::View v{group_offsets, group_sizes, sample_ids, row_masks,
+                                         query_groups, query_masks, range_modes, range_lower,
+                                         range_upper, base_ranges, groups, rows, samples,
+                                         routes, range_count, true};
+    uint32_t begin = 0, count = 0;
+    go_fann::pq_resident_posting::bounds(v, route, begin, count);
+    *out_begin = begin;
+    *out_count = count;
+    return index < count ? static_cast<int>(go_fann::pq_resident_posting::candidate(
+                               v, route, begin + index))
+                         : -1;
+}
+
+float ref_fp16_decode(uint16_t h) { return go_fann::fp16_l2::decode(h); }
+
+float ref_fp16_l2_scalar(const uint16_t* base, const float* query, uint32_t cols)
+{
+    return go_fann::fp16_l2::scalar(base, query, cols);
+}
+
+// Route merge over dense [routes][width] results; outputs [queries][topk].
+int ref_merge_routes(const uint32_t* route_to_query, uint32_t routes, uint32_t queries,
+                     const uint32_t* route_ids, const float* route_dists, uint32_t width,
+                     uint32_t topk, uint32_t* out_ids, float* out_dists)
+{
+    std::vector<uint32_t> r2q(route_to_query, route_to_query + routes);
+    std::vector<std::vector<uint32_t>> ids(routes);
+    std::vector<std::vector<float>> dists(routes);
+    std::vector<int> steps(routes, 1);
+    for (uint32_t r = 0; r < routes; ++r) {
+        ids[r].assign(route_ids + size_t(r) * width, route_ids + size_t(r + 1) * width);
+        dists[r].assign(route_dists + size_t(r) * width, route_dists + size_t(r + 1) * width);
+    }
+    std::vector<std::vector<uint32_t>> merged;
+    std::vector<int> merged_steps;
+    std::vector<std::vector<float>> merged_d;
+    const auto strategy = go_fann::backend_rabitq::lowfreq_merge::merge_route_results_to_original(
+        r2q, queries, ids, dists, steps, topk, merged, merged_steps, &merged_d);
+    for (uint32_t q = 0; q < queries; ++q) {
+        for (uint32_t i = 0; i < topk; ++i) {
+            out_ids[size_t(q) * topk + i] = i < merged[q].size() ? merged[q][i] : UINT32_MAX;
+            out_dists[size_t(q) * topk + i] = i < merged_d[q].size() ? merged_d[q][i] : 3.402823466e+38f;
+        }
+    }
+    return static_cast<int>(strategy);
+}
+
+}  // extern "C"
