@@ -287,8 +287,9 @@ __global__ __launch_bounds__(64) void traversal_kernel(TraversalArgs a, Scorer s
     Entry* frontier = reinterpret_cast<Entry*>(lds + a.off_frontier);
     ResultEntry* topk = reinterpret_cast<ResultEntry*>(lds + a.off_topk);
     StopEntry* stop = reinterpret_cast<StopEntry*>(lds + a.off_stop);
+    // The global slab holds one table per launch slot (slot < routes.count).
     VisitedHash<kHashLds> hash{kHashLds ? reinterpret_cast<uint32_t*>(lds + a.off_hash)
-                                        : a.hash_global + static_cast<size_t>(route) * kHashCapacity};
+                                        : a.hash_global + static_cast<size_t>(slot) * kHashCapacity};
 
     const int Q = a.params.queue_limit;
     const int W = a.params.result_width;

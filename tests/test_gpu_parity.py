@@ -1,0 +1,242 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the CPU
+oracle on the same seeded inputs.  Integer, index and ordering outputs must
+be identical; floats are compared bit for bit where the kernel reproduces
+the oracle's operation order (traversal, posting scans, rerank) and with the
+reference's own tolerances where a GEMM order differs (RaBitQ rotation and
+centroid distances: rabitq_query_rotation_test.cu:31, 47-49)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from conftest import load_golden
+from gofann_amd import _lib
+from gofann_amd import index as gi
+from gofann_amd import plan as gp
+from gofann_amd import search as gs
+from gofann_amd import synth
+
+pytestmark = pytest.mark.gpu
+U32MAX = 0xFFFFFFFF
+
+
+def say(*a):
+    print("[gpu-test]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def as_u32(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.fixture(scope="module", params=["u8-tags", "f32-labels", "f32-ranges"])
+def world(request):
+    kind = request.param
+    if kind == "u8-tags":
+        wl = synth.small_labelled(n=6000, nq=48, dim=48, k=12, sigma=0.7, labels=7, seed=21,
+                                  dtype="u8", tags=True)
+    elif kind == "f32-labels":
+        wl = synth.small_labelled(n=6000, nq=48, dim=64, k=12, sigma=0.7, labels=5, seed=22)
+    else:
+        wl = synth.small_labelled(n=6000, nq=48, dim=32, k=12, sigma=0.7, labels=4, seed=23,
+                                  tags=True, ranges=True)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=32, threshold=300)
+    pl = gp.plan_queries(li, wl.query_labels, wl.query_ranges)
+    return kind, wl, li, pl
+
+
+def _pq(wl, M):
+    table = gi.train_pq(wl.base, M, iters=6)
+    codes = gi.pq_encode(wl.base, table, M)
+    return table, codes
+
+
+@pytest.mark.parametrize("M", [16, 48])
+@pytest.mark.parametrize("mode", ["adaptive-bias", "off", "fixed-nobias"])
+def test_pq_search_matches_oracle(gpu_ctx, world, M, mode):
+    kind, wl, li, pl = world
+    if wl.dim % M:
+        pytest.skip("pq_dim must divide dim")
+    say("pq_search", kind, M, mode)
+    table, codes = _pq(wl, M)
+    rs = pl.graph
+    bias = mode == "adaptive-bias"
+    es = {"adaptive-bias": 2, "off": 1, "fixed-nobias": 0}[mode]
+    Q, W = (48, 40) if mode != "off" else (24, 16)
+    maxs = 60 if mode == "off" else 0
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, wl.base_ranges, alpha=0.15 if bias else 0.0,
+                                          pending_base_stop=bias)
+    prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=es, finish_limit=3,
+                      max_steps=maxs, bias=bias)
+    q = wl.queries.numpy()
+    oi, od, ost = po.pq_search(li, rs, pred_o, prm_o, codes.numpy(), table.numpy(), q)
+
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+    pqv = gs.pq_view(codes.cuda(), table.cuda())
+    keep = (codes.cuda(), table.cuda())
+    pqv = gs.pq_view(*keep)
+    qd = wl.queries.cuda()
+    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=es, finish_limit=3,
+                           max_steps=maxs, bias=bias)
+    ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, qd, dg, dr, prm,
+                                      alpha=0.15 if bias else 0.0, pending_base_stop=bias)
+    torch.cuda.synchronize()
+    gi_ = as_u32(ids).reshape(rs.count, W)
+    gd = dists.cpu().numpy().reshape(rs.count, W)
+    gst = st.cpu().numpy().reshape(rs.count, 8)
+    say("routes", rs.count, "hash_in_lds", gpu_ctx.lib and "n/a")
+    assert np.array_equal(gi_, oi), "route ids differ"
+    assert np.array_equal(gd.view(np.uint32), od.view(np.uint32)), "distances differ in bits"
+    assert np.array_equal(gst, ost), "per-route counters differ"
+
+
+def test_pq_search_batched_launch_order(gpu_ctx, world):
+    """Route sub-ranges and the XCD slot mapping give the same answers."""
+    kind, wl, li, pl = world
+    say("pq_search batches", kind)
+    table, codes = _pq(wl, 16)
+    rs = pl.graph
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+    keep = (codes.cuda(), table.cuda())
+    pqv = gs.pq_view(*keep)
+    qd = wl.queries.cuda()
+    prm = gs.search_params(queue_limit=32, result_width=20)
+    a = gs.run_pq_routes(gpu_ctx, pqv, qd, dg, dr, prm)
+    n = rs.count
+    out = (torch.empty_like(a[0]), torch.empty_like(a[1]), torch.zeros_like(a[2]))
+    for b0 in range(0, n, 7):
+        gs.run_pq_routes(gpu_ctx, pqv, qd, dg, dr, prm, begin=b0, end=min(n, b0 + 7), out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], out[0]) and torch.equal(a[1], out[1]) and torch.equal(a[2], out[2])
+
+
+def test_pq_score_matches_oracle_adc(gpu_ctx, world):
+    kind, wl, li, pl = world
+    say("pq_score", kind)
+    M = 16
+    table, codes = _pq(wl, M)
+    rng = np.random.default_rng(1)
+    n = 500
+    qi = np.sort(rng.integers(0, wl.queries.shape[0], n)).astype(np.uint32)
+    si = rng.integers(0, wl.n, n).astype(np.uint32)
+    keep = (codes.cuda(), table.cuda())
+    pqv = gs.pq_view(*keep)
+    qd = wl.queries.cuda()
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    qt, st = gs.u32(qi), gs.u32(si)
+    gpu_ctx.check(gpu_ctx.lib.gofann_pq_score(gpu_ctx.handle, pqv, _lib.ptr(qd), gs.query_elem(qd),
+                                              _lib.ptr(qt), _lib.ptr(st), n, _lib.ptr(out)))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    q = wl.queries.numpy()
+    want = np.array([po.pq_adc(po.pq_lut(table.numpy(), q[a], M), codes.numpy()[b])
+                     for a, b in zip(qi, si)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_predicate_masks_fixture(gpu_ctx):
+    """gpu_predicate_parallel_test.cu: ballot masks equal scalar matches for
+    counts {0, 1, 17, 31, 32, 33, 63, 64, 65, 97}, partial words zero."""
+    say("predicate masks")
+    fx = load_golden("predicate_parallel.json")
+    from gofann_amd.plan import CLAUSE_DTYPE, RANGE_DTYPE
+    clauses = np.array([tuple(c) for c in fx["clauses"]], dtype=CLAUSE_DTYPE)
+    ranges = np.array([tuple(r) for r in fx["ranges"]], dtype=RANGE_DTYPE)
+    pa = po.PredicateArrays(fx["route_offsets"], fx["handles"], clauses, ranges,
+                            fx["route_enabled"], None, fx["csr_offsets"], fx["csr_labels"],
+                            fx["rows"], np.array(fx["base_ranges"], np.float32))
+    import ctypes as C
+    L = po.lib()
+    dev = {k: gs.to_dev(v) for k, v in [("off", np.array(fx["route_offsets"], np.uint32)),
+                                         ("h", np.array(fx["handles"], np.uint32)),
+                                         ("cl", clauses), ("rg", ranges),
+                                         ("en", np.array(fx["route_enabled"], np.uint8)),
+                                         ("br", np.array(fx["base_ranges"], np.float32)),
+                                         ("co", np.array(fx["csr_offsets"], np.uint32)),
+                                         ("cv", np.array(fx["csr_labels"], np.uint32))]}
+    pv = _lib.PredicateView(*[_lib.ptr(dev[k]) for k in ("off", "h", "cl", "rg", "en")], None,
+                            _lib.ptr(dev["br"]), _lib.ptr(dev["co"]), _lib.ptr(dev["cv"]),
+                            fx["rows"], 2, 0.0, 0)
+    mapping = np.array(fx["mapping"], np.uint32)
+    for route in range(len(fx["route_enabled"])):
+        for count in fx["counts"]:
+            samples = np.array([mapping[fx["offset"] + (i * 37) % 97] for i in range(count)],
+                               np.uint32)
+            routes = np.full(count, route, np.uint32)
+            words = (count + 31) // 32
+            masks = torch.full((max(words, 1),), -559038737, dtype=torch.int32, device="cuda")
+            rt, stt = gs.u32(routes if count else np.zeros(1, np.uint32)), \
+                gs.u32(samples if count else np.zeros(1, np.uint32))
+            gpu_ctx.check(gpu_ctx.lib.gofann_predicate_masks(gpu_ctx.handle, pv, _lib.ptr(rt),
+                                                             _lib.ptr(stt), count, _lib.ptr(masks)))
+            torch.cuda.synchronize()
+            m = as_u32(masks)
+            for i in range(count):
+                want = L.orc_pred_enabled(C.byref(pa.struct), route) and \
+                    L.orc_pred_matches(C.byref(pa.struct), route, int(samples[i]), None)
+                assert bool((m[i // 32] >> (i % 32)) & 1) == bool(want), (route, count, i)
+            if count % 32:
+                assert (m[count // 32] >> (count % 32)) == 0
+            if count == 0:
+                assert m[0] == np.uint32(0xDEADBEEF)
+
+
+def test_pq_posting_scan_matches_oracle(gpu_ctx, world):
+    kind, wl, li, pl = world
+    say("pq posting scan", kind)
+    M = 16
+    table, codes = _pq(wl, M)
+    # scan every label's posting as a route (routes of all queries x labels)
+    labels = wl.query_labels
+    rows = []
+    for qi, ls in enumerate(labels):
+        anchor = ls[0]
+        rows.append((qi, anchor, [l for l in ls if l != anchor],
+                     [tuple(a) for a in (wl.query_ranges[qi] if wl.query_ranges else [])]))
+    rs = gp._routeset(rows, li)
+    off = np.array([li.posting_offset[r[1]] for r in rows], np.uint32)
+    size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]] for r in rows], np.uint32)
+    for k in (10, 100, 257):
+        pred = po.PredicateArrays.from_plan(rs.predicate, li, wl.base_ranges)
+        oi, od, opass = po.posting_scan_pq(pred, codes.numpy(), table.numpy(), wl.queries.numpy(),
+                                           rs.route_query, li.posting_ids, off, size, k)
+        dg = gs.DeviceGraph.upload(li)
+        dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+        keep = (codes.cuda(), table.cuda())
+        pqv = gs.pq_view(*keep)
+        ids, dists, passes = gs.run_pq_posting(gpu_ctx, pqv, wl.queries.cuda(), dg, dr, off, size, k)
+        torch.cuda.synchronize()
+        assert np.array_equal(as_u32(ids).reshape(-1, k), oi)
+        assert np.array_equal(dists.cpu().numpy().reshape(-1, k).view(np.uint32), od.view(np.uint32))
+        assert np.array_equal(as_u32(passes), opass)
+
+
+@pytest.mark.parametrize("elem", ["u8", "f32", "f16"])
+def test_exact_rerank_matches_oracle(gpu_ctx, elem):
+    say("rerank", elem)
+    rng = np.random.default_rng(5)
+    n, d, routes, width, topk = 2000, 72, 40, 100, 10
+    if elem == "u8":
+        base = rng.integers(0, 256, (n, d)).astype(np.uint8)
+        q = rng.integers(0, 256, (routes, d)).astype(np.uint8)
+    else:
+        base = rng.normal(size=(n, d)).astype(np.float32 if elem == "f32" else np.float16)
+        q = rng.normal(size=(routes, d)).astype(np.float32)
+    sl = rng.integers(0, n + 10, (routes, width)).astype(np.uint32)
+    sl[:, ::11] = U32MAX
+    sl[:, 3] = sl[:, 4]
+    rq = np.arange(routes, dtype=np.uint32)
+    oi, od = po.rerank(base, q, rq, sl, topk)
+    bt = torch.from_numpy(base).cuda()
+    ids, dists = gs.exact_rerank(gpu_ctx, bt, torch.from_numpy(q).cuda(), gs.u32(rq), gs.u32(sl),
+                                 width, routes, topk)
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids).reshape(routes, topk), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(routes, topk).view(np.uint32), od.view(np.uint32))

@@ -1,0 +1,199 @@
+"""GPU parity of the RaBitQ path: query preparation against FP64 with the
+reference's tolerances, the integer quantization / popcount path bit-exact
+against the oracle on the same rotated input, traversal and posting scan
+identical to the oracle."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from conftest import load_golden
+from gofann_amd import _lib
+from gofann_amd import index as gi
+from gofann_amd import plan as gp
+from gofann_amd import search as gs
+from gofann_amd import synth
+
+pytestmark = pytest.mark.gpu
+U32MAX = 0xFFFFFFFF
+
+
+def say(*a):
+    print("[gpu-test]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def as_u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def prepare(ctx, queries: torch.Tensor, rotation: torch.Tensor, anchors: torch.Tensor, dim, P):
+    n = queries.shape[0]
+    A = anchors.shape[0]
+    out = dict(rotated=torch.empty(n, P, device="cuda"), q8=torch.empty(n, P, dtype=torch.int8, device="cuda"),
+               scale=torch.empty(n, device="cuda"), k1=torch.empty(n, device="cuda"),
+               cd=torch.empty(n, max(A, 1), device="cuda"))
+    rv = _lib.RabitqView(None, None, None, _lib.ptr(anchors), dim, P, A, 0)
+    rq = _lib.RabitqQueries(_lib.ptr(out["rotated"]), _lib.ptr(out["q8"]), _lib.ptr(out["scale"]),
+                            _lib.ptr(out["k1"]), _lib.ptr(out["cd"]), n)
+    ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, rv, _lib.ptr(queries), n,
+                                                    _lib.ptr(rotation), rq))
+    torch.cuda.synchronize()
+    return out, rq
+
+
+@pytest.mark.parametrize("shape", load_golden("rotation.json")["shapes"])
+def test_rotation_and_centroids_vs_fp64(gpu_ctx, shape):
+    """rabitq_query_rotation_test.cu:11-61 shapes and tolerances."""
+    fx = load_golden("rotation.json")
+    n, d, p = shape
+    say("prepare", n, d, p)
+    P = ((p + 63) // 64) * 64
+    rng = np.random.default_rng(20260927)
+    q = rng.uniform(-1, 1, (n, d)).astype(np.float32)
+    r = (rng.uniform(-1, 1, (d, P)) / np.sqrt(d)).astype(np.float32)
+    anchors = np.concatenate([q @ r, rng.normal(size=(5, P)).astype(np.float32)])  # rows of Y are anchors
+    out, _ = prepare(gpu_ctx, torch.from_numpy(q).cuda(), torch.from_numpy(r).cuda(),
+                     torch.from_numpy(anchors).cuda(), d, P)
+    y = out["rotated"].cpu().numpy()
+    want = q.astype(np.float64) @ r.astype(np.float64)
+    a_tol, r_tol = fx["rotation_tol"]
+    assert np.all(np.isfinite(y))
+    assert np.all(np.abs(y - want) <= a_tol + r_tol * np.abs(want))
+    cd = out["cd"].cpu().numpy()
+    y64 = y.astype(np.float64)
+    cw = ((y64[:, None, :] - anchors.astype(np.float64)[None]) ** 2).sum(-1)
+    ca, cr = fx["centroid_tol"]
+    assert np.all(cd >= 0)
+    assert np.all(np.abs(cd - cw) <= ca + cr * cw)
+    # integer path exact against the oracle on the GPU's rotated rows
+    q8 = out["q8"].cpu().numpy()
+    sc = out["scale"].cpu().numpy()
+    k1 = out["k1"].cpu().numpy()
+    for i in range(n):
+        oq, osc, ok1 = po.rabitq_quantize(y[i])
+        assert np.array_equal(q8[i], oq) and sc[i] == np.float32(osc) and k1[i] == np.float32(ok1)
+
+
+@pytest.fixture(scope="module")
+def rworld():
+    wl = synth.small_labelled(n=6000, nq=40, dim=60, k=10, sigma=0.7, labels=5, seed=31, tags=True)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=32, threshold=300)
+    P = 128
+    rot = gi.random_rotation(wl.dim, P, 31005, "cpu")
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
+    pl = gp.plan_queries(li, wl.query_labels)
+    return wl, li, pl, rot, codes, fac, aid, anchors, P
+
+
+def _rviews(rw):
+    wl, li, pl, rot, codes, fac, aid, anchors, P = rw
+    dev = dict(codes=codes.cuda(), fac=fac.cuda(), aid=aid.cuda(), anchors=anchors.cuda(),
+               rot=rot.cuda(), q=wl.queries.float().cuda())
+    rv = _lib.RabitqView(_lib.ptr(dev["codes"]), _lib.ptr(dev["fac"]), _lib.ptr(dev["aid"]),
+                         _lib.ptr(dev["anchors"]), wl.dim, P, anchors.shape[0], wl.n)
+    return dev, rv
+
+
+def test_rabitq_score_ip_exact(gpu_ctx, rworld):
+    wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
+    say("rabitq score")
+    dev, rv = _rviews(rworld)
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rng = np.random.default_rng(3)
+    n = 600
+    qi = np.sort(rng.integers(0, wl.queries.shape[0], n)).astype(np.uint32)
+    si = rng.integers(0, wl.n, n).astype(np.uint32)
+    d = torch.empty(n, device="cuda")
+    ip = torch.empty(n, dtype=torch.int32, device="cuda")
+    qt, st = gs.u32(qi), gs.u32(si)
+    gpu_ctx.check(gpu_ctx.lib.gofann_rabitq_score(gpu_ctx.handle, rv, rq, _lib.ptr(qt), _lib.ptr(st),
+                                                  n, _lib.ptr(d), _lib.ptr(ip)))
+    torch.cuda.synchronize()
+    q8 = out["q8"].cpu().numpy()
+    sc, k1, cd = out["scale"].cpu().numpy(), out["k1"].cpu().numpy(), out["cd"].cpu().numpy()
+    cn, fn, an = codes.numpy(), fac.numpy(), aid.numpy()
+    L = po.lib()
+    for i in range(n):
+        a, b = int(qi[i]), int(si[i])
+        oip = po.rabitq_ip(q8[a], cn[b], "int")
+        assert int(ip[i]) == oip
+        want = L.orc_rabitq_score_b1(oip, sc[a], k1[a], fn[b, 0].item(), fn[b, 1].item(), cd[a, an[b]])
+        assert np.float32(d[i].item()) == np.float32(want)
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias):
+    wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
+    say("rabitq search bias", bias)
+    dev, rv = _rviews(rworld)
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rs = pl.graph
+    Q, W = 40, 30
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15 if bias else 0.0,
+                                          pending_base_stop=bias)
+    prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias, rabitq_verdict=1)
+    oi, od, ost = po.rabitq_search(li, rs, pred_o, prm_o, codes.numpy(), fac.numpy(),
+                                   aid.numpy().astype(np.uint32), out["q8"].cpu().numpy(),
+                                   out["scale"].cpu().numpy(), out["k1"].cpu().numpy(),
+                                   out["cd"].cpu().numpy(), anchors.shape[0], P)
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs)
+    n = rs.count
+    ids = torch.empty(n * W, dtype=torch.int32, device="cuda")
+    dists = torch.empty(n * W, device="cuda")
+    st = torch.zeros(n * 8, dtype=torch.int32, device="cuda")
+    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias)
+    gpu_ctx.check(gpu_ctx.lib.gofann_rabitq_search(
+        gpu_ctx.handle, rv, rq, dg.view(), dr.predicate_view(dg, 0.15 if bias else 0.0, bias),
+        dr.routes_view(), prm, _lib.ptr(ids), _lib.ptr(dists), _lib.ptr(st)))
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids).reshape(n, W), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(n, W).view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(st.cpu().numpy().reshape(n, 8), ost)
+
+
+def test_rabitq_posting_scan_matches_oracle(gpu_ctx, rworld):
+    wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
+    say("rabitq posting scan")
+    dev, rv = _rviews(rworld)
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rows = [(qi, ls[0], [l for l in ls if l != ls[0]], []) for qi, ls in enumerate(wl.query_labels)]
+    rs = gp._routeset(rows, li)
+    off = np.array([li.posting_offset[r[1]] for r in rows], np.uint32)
+    size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]] for r in rows], np.uint32)
+    k = 100
+    pred = po.PredicateArrays.from_plan(rs.predicate, li)
+    L = po.lib()
+    n = rs.count
+    oi = np.empty((n, k), np.uint32)
+    od = np.empty((n, k), np.float32)
+    opass = np.empty(n, np.uint32)
+    arrs = [np.ascontiguousarray(a) for a in (codes.numpy(), fac.numpy(), aid.numpy().astype(np.uint32),
+                                               out["q8"].cpu().numpy(), out["scale"].cpu().numpy(),
+                                               out["k1"].cpu().numpy(), out["cd"].cpu().numpy(),
+                                               rs.route_query, li.posting_ids, off, size)]
+    import ctypes as C
+    assert L.orc_rabitq_posting_scan(C.byref(pred.struct), *[po.p(a) for a in arrs[:1]], C.c_uint32(P // 8),
+                                     *[po.p(a) for a in arrs[1:7]], C.c_uint32(anchors.shape[0]),
+                                     C.c_uint32(P), *[po.p(a) for a in arrs[7:]], C.c_uint32(n), k,
+                                     po.p(oi), po.p(od), po.p(opass)) == 0
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs)
+    ids = torch.empty(n * k, dtype=torch.int32, device="cuda")
+    dists = torch.empty(n * k, device="cuda")
+    passes = torch.empty(n, dtype=torch.int32, device="cuda")
+    co, cs = gs.u32(off), gs.u32(size)
+    gpu_ctx.check(gpu_ctx.lib.gofann_rabitq_posting_scan(
+        gpu_ctx.handle, rv, rq, dr.predicate_view(dg, 0.0, False), _lib.ptr(dr.route_query),
+        _lib.ptr(dg.posting_ids), _lib.ptr(co), _lib.ptr(cs), n, k, _lib.ptr(ids), _lib.ptr(dists),
+        _lib.ptr(passes)))
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids).reshape(n, k), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(n, k).view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(as_u32(passes), opass)

@@ -112,8 +112,9 @@ def test_max_steps_and_stats_consistency(tiny):
 
 
 def test_oracle_rabitq_full_beam(tiny):
-    wl, li, table, codes, pl = tiny
-    rs = pl.graph
+    wl = tiny[0]
+    li = complete_graph_index(wl)
+    rs = gp.plan_queries(li, wl.query_labels).graph
     x = wl.base
     P = 64
     rot = gi.random_rotation(x.shape[1], P, 5, "cpu")
@@ -127,7 +128,7 @@ def test_oracle_rabitq_full_beam(tiny):
         q8[i], sc[i], k1[i] = po.rabitq_quantize(qr[i])
     an = anchors.numpy().astype(np.float64)
     cd = ((qr.astype(np.float64)[:, None, :] - an[None]) ** 2).sum(-1).astype(np.float32)
-    W = 30
+    W = 8
     pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15, pending_base_stop=True)
     prm = po.params(queue_limit=1000, result_width=W, early_stop_mode=1, rabitq_verdict=1)
     ids, dists, st = po.rabitq_search(li, rs, pred, prm, rcodes.numpy(), fac.numpy(),
