@@ -6,9 +6,9 @@
 //                                  backend_rabitq.cu:2898-2929)
 //   q8, scale                     (quantize_rabitq_queries_int8_kernel,
 //                                  backend_rabitq.cu:2931-2964)
-//   g[q][a] = max(0, -2<q,c_a> + |q|^2 + |c_a|^2)
-//                                 (centroid_distances, rabitq_query_rotation.
-//                                  cuh:12-39, 89-113)
+//   g[q][a] = |q - c_a|^2         (centroid_distances, rabitq_query_rotation.
+//                                  cuh:12-39, 89-113; computed directly, not
+//                                  through the cancelling norm expansion)
 // The reductions that feed the integer path (scale, k1) use the reference's
 // 256-thread order exactly: strided partial sums, then a shared tree.
 #include <hip/hip_runtime.h>
@@ -104,34 +104,51 @@ __global__ __launch_bounds__(256) void quantize_queries_kernel(const float* rota
     }
 }
 
-// rabitq_row_norms_kernel order: 256 strided fma partials, shared tree.
-__global__ __launch_bounds__(256) void row_norms_kernel(const float* m, uint32_t rows, uint32_t dim,
-                                                        float* norms)
+// g[q][a] = sum_p (y[q][p] - c[a][p])^2, accumulated directly (fma, p
+// ascending) rather than as |y|^2 + |c|^2 - 2<y,c>: the expansion cancels
+// catastrophically when a query sits on an anchor.  A 256-thread block owns
+// a 32 x 32 (query, anchor) tile; both operand tiles stream through LDS in
+// 64-wide slices of the padded dimension.
+constexpr int kCdTile = 32;
+constexpr int kCdSlice = 64;
+
+__global__ __launch_bounds__(256) void centroid_dist_kernel(const float* y, const float* c,
+                                                            uint32_t queries, uint32_t anchors,
+                                                            uint32_t P, float* out)
 {
-    __shared__ float part[256];
-    const uint32_t r = blockIdx.x;
-    const uint32_t t = threadIdx.x;
-    if (r >= rows) return;
-    float sum = 0.0f;
-    for (uint32_t d = t; d < dim; d += 256) {
-        const float v = m[static_cast<size_t>(r) * dim + d];
-        sum = fmaf(v, v, sum);
-    }
-    part[t] = sum;
-    __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
-        if (t < s) part[t] += part[t + s];
+    __shared__ float ys[kCdTile][kCdSlice + 1];
+    __shared__ float cs[kCdTile][kCdSlice + 1];
+    const int t = static_cast<int>(threadIdx.x);
+    const uint32_t q0 = blockIdx.y * kCdTile;
+    const uint32_t a0 = blockIdx.x * kCdTile;
+    // thread t owns pairs (qi, ai) with qi = t / 8, ai = (t % 8) * 4 + j
+    const int qi = t >> 3;
+    const int ai = (t & 7) * 4;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t p0 = 0; p0 < P; p0 += kCdSlice) {
+        for (int e = t; e < kCdTile * kCdSlice; e += 256) {
+            const int r = e / kCdSlice, k = e % kCdSlice;
+            const uint32_t pk = p0 + k;
+            ys[r][k] = (q0 + r < queries && pk < P) ? y[static_cast<size_t>(q0 + r) * P + pk] : 0.0f;
+            cs[r][k] = (a0 + r < anchors && pk < P) ? c[static_cast<size_t>(a0 + r) * P + pk] : 0.0f;
+        }
+        __syncthreads();
+        const int kmax = (P - p0) < static_cast<uint32_t>(kCdSlice) ? static_cast<int>(P - p0) : kCdSlice;
+        for (int k = 0; k < kmax; ++k) {
+            const float yv = ys[qi][k];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float d = yv - cs[ai + j][k];
+                acc[j] = fmaf(d, d, acc[j]);
+            }
+        }
         __syncthreads();
     }
-    if (t == 0) norms[r] = part[0];
-}
-
-__global__ void finish_centroid_kernel(float* dists, const float* qn, const float* an,
-                                       uint32_t queries, uint32_t anchors)
-{
-    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= static_cast<size_t>(queries) * anchors) return;
-    dists[i] = fmaxf(0.0f, dists[i] + qn[i / anchors] + an[i % anchors]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t qq = q0 + qi, aa = a0 + ai + j;
+        if (qq < queries && aa < anchors) out[static_cast<size_t>(qq) * anchors + aa] = acc[j];
+    }
 }
 
 namespace {
@@ -158,20 +175,9 @@ int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* quer
     hipLaunchKernelGGL(quantize_queries_kernel, dim3(count), dim3(256), 0, ctx->stream, out->rotated,
                        P, count, out->q8, out->scale, out->k1);
     if (A > 0 && rq->anchors) {
-        const size_t need = (static_cast<size_t>(count) + A) * sizeof(float);
-        float* norms = static_cast<float*>(ctx->scratch(Context::kScratchMisc, need));
-        if (!norms) return ctx->fail(GOFANN_ERR_NOMEM, "norm scratch");
-        hipLaunchKernelGGL(row_norms_kernel, dim3(count), dim3(256), 0, ctx->stream, out->rotated,
-                           count, P, norms);
-        hipLaunchKernelGGL(row_norms_kernel, dim3(A), dim3(256), 0, ctx->stream, rq->anchors, A, P,
-                           norms + count);
-        // dots[N][A] = -2 * rotated[N][P] anchors[A][P]^T
-        GemmArgs h{out->rotated, rq->anchors, out->centroid_dists, count, A, P, P, 1, 1, P, A, -2.0f};
-        launch_gemm(ctx, h);
-        const size_t pairs = static_cast<size_t>(count) * A;
-        hipLaunchKernelGGL(finish_centroid_kernel, dim3(static_cast<uint32_t>((pairs + 255) / 256)),
-                           dim3(256), 0, ctx->stream, out->centroid_dists, norms, norms + count,
-                           count, A);
+        const dim3 grid((A + kCdTile - 1) / kCdTile, (count + kCdTile - 1) / kCdTile);
+        hipLaunchKernelGGL(centroid_dist_kernel, grid, dim3(256), 0, ctx->stream, out->rotated,
+                           rq->anchors, count, A, P, out->centroid_dists);
     }
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("RaBitQ preparation launch");
     return GOFANN_OK;

@@ -56,7 +56,7 @@ def _pq(wl, M):
     return table, codes
 
 
-@pytest.mark.parametrize("M", [16, 48])
+@pytest.mark.parametrize("M", [16, 32, 48])
 @pytest.mark.parametrize("mode", ["adaptive-bias", "off", "fixed-nobias"])
 def test_pq_search_matches_oracle(gpu_ctx, world, M, mode):
     kind, wl, li, pl = world
