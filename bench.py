@@ -1,0 +1,328 @@
+#!/usr/bin/env python3
+"""Filtered QPS at recall@10 >= 0.90 on one MI355X (BASELINE.json metric).
+
+Workload: BASELINE config C2 -- 10M x 192 uint8 vectors from a 1024-centre
+Gaussian mixture (clipped to 0..255), PQ M=48 x 8 bit (fp32 ADC table),
+label-partitioned graphs of out-degree 64, 1-5 Zipf(1.1) tags per vector
+from a 2000-tag vocabulary, 100k queries that AND 1-2 tags (selectivity
+0.1%-20%), top-10.  Synthetic, seeded data; the index is built on the GPU
+before the timed region (build is not measured).
+
+One step = the whole GPU stage for all 100k queries with inputs resident in
+HBM: graph traversal of every graph route (shortlist W=100), posting scans of
+rare-tag routes, exact uint8 rerank of every shortlist on the GPU, and the
+route -> query merge.  QPS = queries / step wall time.  The beam width is the
+smallest of a short ladder that reaches recall@10 >= 0.90 (macro recall over
+a sample of queries with exact ground truth).
+
+Prints one JSON line (rank 0).  `--gpus N` with N > 1 exits: this build
+measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "go-fann_amd"))
+
+PEAK_HBM_GBPS = 8000.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--n", type=int, default=10_000_000, help="base vectors (C2: 10M)")
+    ap.add_argument("--queries", type=int, default=100_000)
+    ap.add_argument("--gt-queries", type=int, default=2000)
+    ap.add_argument("--queue", type=int, default=0, help="beam width; 0 = ladder search")
+    ap.add_argument("--ladder", default="64,96,128,192,256")
+    ap.add_argument("--target-recall", type=float, default=0.90)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def build_world(args, torch):
+    from gofann_amd import index as gi
+    from gofann_amd import plan as gp
+    from gofann_amd import synth
+    t0 = time.time()
+    wl = synth.config2(n=args.n, nq=args.queries, device="cuda")
+    torch.cuda.synchronize()
+    log(f"data {wl.n}x{wl.dim} u8, {len(wl.query_labels)} queries in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    table = gi.train_pq(wl.base, 48, iters=25, sample=65536, seed=2005)
+    codes = gi.pq_encode(wl.base, table, 48)
+    torch.cuda.synchronize()
+    log(f"PQ M=48 trained+encoded in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=64, threshold=2000)
+    log(f"label graphs: {int((li.label_size > 0).sum())} labels, {li.rows} rows, "
+        f"degree 64 in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    pl = gp.plan_queries(li, wl.query_labels)
+    log(f"plan: {pl.graph.count} graph routes, {pl.posting.count} posting routes "
+        f"in {time.time() - t0:.1f}s")
+    return wl, li, table, codes, pl
+
+
+def ground_truth(wl, li, torch, nq, seed=7):
+    """Exact filtered top-10 by squared L2 (integer, exact) for a sample of
+    queries; ties broken by sample id."""
+    rng = np.random.default_rng(seed)
+    qids = np.sort(rng.choice(len(wl.query_labels), size=min(nq, len(wl.query_labels)),
+                              replace=False))
+    n = wl.n
+    # padded sample-major tag table on the device for membership tests
+    counts = np.diff(li.csr_offsets.astype(np.int64))
+    width = int(counts.max()) if n else 1
+    tags = np.full((n, width), -1, dtype=np.int32)
+    rows = np.repeat(np.arange(n), counts)
+    cols = np.arange(len(li.csr_labels)) - np.repeat(li.csr_offsets[:-1].astype(np.int64), counts)
+    tags[rows, cols] = li.csr_labels.astype(np.int32)
+    tags_d = torch.from_numpy(tags).cuda()
+    post_d = torch.from_numpy(li.posting_ids.astype(np.int64)).cuda()
+    gt = {}
+    base = wl.base
+    for q in qids:
+        labels = sorted(wl.query_labels[q], key=lambda l: int(li.cat_freq[l]))
+        l0 = labels[0]
+        cand = post_d[int(li.posting_offset[l0]):int(li.posting_offset[l0 + 1])]
+        for l in labels[1:]:
+            cand = cand[(tags_d[cand] == int(l)).any(1)]
+        if cand.numel() == 0:
+            continue
+        d = ((base[cand].int() - wl.queries[q].int()) ** 2).sum(1).long()
+        key = d * (1 << 32) + cand
+        k = min(10, int(cand.numel()))
+        top = torch.topk(key, k, largest=False).values
+        gt[int(q)] = (top & 0xFFFFFFFF).cpu().numpy().astype(np.uint32)
+    return gt
+
+
+def recall_at_10(result: np.ndarray, gt: dict) -> float:
+    vals = []
+    for q, g in gt.items():
+        if len(g) == 0:
+            continue
+        vals.append(len(set(result[q].tolist()) & set(g.tolist())) / len(g))
+    return float(np.mean(vals)) if vals else 0.0
+
+
+class Pipeline:
+    """Device-resident index + one full GPU step."""
+
+    def __init__(self, ctx, wl, li, table, codes, pl, torch):
+        from gofann_amd import search as gs
+        self.gs, self.torch, self.ctx = gs, torch, ctx
+        self.wl, self.pl = wl, pl
+        self.dg = gs.DeviceGraph.upload(li)
+        self.keep = (codes, table)
+        self.pqv = gs.pq_view(codes, table)
+        self.q = wl.queries
+        self.dr_graph = gs.DeviceRoutes.upload(pl.graph)
+        self.dr_post = gs.DeviceRoutes.upload(pl.posting)
+        allr = np.concatenate([pl.graph.route_to_query, pl.posting.route_to_query])
+        self.n_graph = pl.graph.count
+        self.n_post = pl.posting.count
+        off, order = gs.query_route_csr(allr, pl.queries)
+        self.q_off, self.q_routes = gs.u32(off), gs.u32(order)
+        self.route_query_all = gs.u32(np.concatenate([pl.graph.route_query,
+                                                      pl.posting.route_query]))
+        self.W = 100
+        n = self.n_graph + self.n_post
+        self.sl_ids = torch.empty(max(n, 1) * self.W, dtype=torch.int32, device="cuda")
+        self.sl_d = torch.empty(max(n, 1) * self.W, dtype=torch.float32, device="cuda")
+        self.stats = torch.zeros(max(self.n_graph, 1) * 8, dtype=torch.int32, device="cuda")
+        self.co = gs.u32(pl.cand_offsets if self.n_post else np.zeros(1, np.uint32))
+        self.cs = gs.u32(pl.cand_sizes if self.n_post else np.zeros(1, np.uint32))
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+
+    def step(self, Q: int, timed_kernel=False):
+        gs, torch = self.gs, self.torch
+        W, ng, npost = self.W, self.n_graph, self.n_post
+        prm = gs.search_params(queue_limit=Q, result_width=W)
+        if timed_kernel:
+            self.ev[0].record()
+        if ng:
+            gs.run_pq_routes(self.ctx, self.pqv, self.q, self.dg, self.dr_graph, prm,
+                             out=(self.sl_ids, self.sl_d, self.stats))
+        if timed_kernel:
+            self.ev[1].record()
+        if npost:
+            ids_p = self.sl_ids[ng * W:]
+            d_p = self.sl_d[ng * W:]
+            pv = self.dr_post.predicate_view(self.dg, 0.0, False)
+            self.ctx.check(self.ctx.lib.gofann_pq_posting_scan(
+                self.ctx.handle, self.pqv, gs._lib.ptr(self.q), gs.query_elem(self.q), pv,
+                gs._lib.ptr(self.dr_post.route_query), gs._lib.ptr(self.dg.posting_ids),
+                gs._lib.ptr(self.co), gs._lib.ptr(self.cs), npost, W, gs._lib.ptr(ids_p),
+                gs._lib.ptr(d_p), None))
+        n = ng + npost
+        rr_i, rr_d = gs.exact_rerank(self.ctx, self.wl.base, self.q, self.route_query_all,
+                                     self.sl_ids, W, n, 10)
+        out_i, out_d = gs.merge_routes_gpu(self.ctx, self.q_off, self.q_routes, rr_i, rr_d, 10,
+                                           self.pl.queries, 10)
+        return out_i
+
+    def kernel_ms(self) -> float:
+        return self.ev[0].elapsed_time(self.ev[1])
+
+    def route_stats(self) -> np.ndarray:
+        return self.stats[: self.n_graph * 8].cpu().numpy().reshape(-1, 8)
+
+
+def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int) -> float:
+    """Bytes the traversal must move per launch: adjacency row + row_to_sample
+    of each expanded node, code row + row_to_sample of each scored candidate,
+    CSR offsets of each predicate row opened and each label word read."""
+    E = st[:, 1].astype(np.float64).sum()
+    V = st[:, 3].astype(np.float64).sum()
+    rows = st[:, 4].astype(np.float64).sum()
+    labels = st[:, 5].astype(np.float64).sum()
+    return E * (4 * degree + 4) + V * (code_bytes + 4) + rows * 8 + labels * 4
+
+
+def cpu_baseline(wl, li, table, codes, pl, Q, seconds, torch):
+    """The oracle (a single-threaded C restatement of the reference path) on
+    a bounded sample of the same workload: graph search, posting scan, exact
+    rerank and merge for the first queries until `seconds` elapse."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle as po
+    from gofann_amd import plan as gp
+    base = wl.base.cpu().numpy()
+    qs = wl.queries.cpu().numpy()
+    codes_h = codes.cpu().numpy()
+    table_h = table.cpu().numpy()
+    done = 0
+    t0 = time.perf_counter()
+    qlist = list(range(len(wl.query_labels)))
+    chunk = 64
+    while done < len(qlist) and time.perf_counter() - t0 < seconds:
+        sel = qlist[done: done + chunk]
+        sub = gp.plan_queries(li, [wl.query_labels[i] for i in sel])
+        rs = sub.graph
+        res_i, res_d, r2q = [], [], []
+        if rs.count:
+            pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
+                                                pending_base_stop=True)
+            ids, _, _ = po.pq_search(li, rs, pred, po.params(queue_limit=Q, result_width=100),
+                                     codes_h, table_h, qs[sel])
+            ri, rd = po.rerank(base, qs[sel], rs.route_query, ids, 10)
+            res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
+        if sub.posting.count:
+            pr = po.PredicateArrays.from_plan(sub.posting.predicate, li)
+            pi, _, _ = po.posting_scan_pq(pr, codes_h, table_h, qs[sel], sub.posting.route_query,
+                                          li.posting_ids, sub.cand_offsets, sub.cand_sizes, 100)
+            ri, rd = po.rerank(base, qs[sel], sub.posting.route_query, pi, 10)
+            res_i.append(ri), res_d.append(rd), r2q.append(sub.posting.route_to_query)
+        if res_i:
+            po.merge(np.concatenate(r2q), np.concatenate(res_i), np.concatenate(res_d),
+                     len(sel), 10)
+        done += len(sel)
+    el = time.perf_counter() - t0
+    return done / el, done, el
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build's "
+              "search path runs on a single MI355X and has no multi-GPU mode.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from gofann_amd import _lib
+    torch.cuda.init()
+    wl, li, table, codes, pl = build_world(args, torch)
+    t0 = time.time()
+    gt = ground_truth(wl, li, torch, args.gt_queries)
+    log(f"ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
+    ctx = _lib.Context(0)
+    pipe = Pipeline(ctx, wl, li, table, codes, pl, torch)
+
+    ladder = [args.queue] if args.queue else [int(x) for x in args.ladder.split(",")]
+    chosen, rec = ladder[-1], 0.0
+    for Q in ladder:
+        out = pipe.step(Q)
+        torch.cuda.synchronize()
+        res = out.cpu().numpy().view(np.uint32).reshape(pl.queries, 10)
+        rec = recall_at_10(res, gt)
+        log(f"Q={Q}: recall@10={rec:.4f}")
+        chosen = Q
+        if rec >= args.target_recall:
+            break
+
+    for _ in range(args.warmup):
+        pipe.step(chosen)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    kernel_ms = []
+    for _ in range(args.steps):
+        out = pipe.step(chosen, timed_kernel=True)
+        torch.cuda.synchronize()
+        kernel_ms.append(pipe.kernel_ms())
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1000.0 / args.steps
+    qps = pl.queries / (ms_per_step / 1000.0)
+    res = out.cpu().numpy().view(np.uint32).reshape(pl.queries, 10)
+    rec = recall_at_10(res, gt)
+    st = pipe.route_stats()
+    kms = float(np.mean(kernel_ms))
+    abytes = algorithmic_bytes(st, li.degree, 48)
+    achieved = abytes / (kms / 1000.0) / 1e9
+    log(f"step {ms_per_step:.1f} ms, traversal kernel {kms:.1f} ms, recall {rec:.4f}, "
+        f"steps/route {st[:, 0].mean():.1f}, scored/route {st[:, 3].mean():.1f}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cq, cn, cel = cpu_baseline(wl, li, table, codes, pl, chosen, args.cpu_seconds, torch)
+        cpu = {"value": round(cq, 2), "unit": "queries/s", "cores": 1, "kind": "port",
+               "sample": f"first {cn} of the {pl.queries} C2 queries (graph search Q={chosen}, "
+                         f"posting scan, exact rerank, merge) in {cel:.1f}s on one host core"}
+        log(f"cpu baseline {cq:.1f} qps over {cn} queries")
+
+    line = {
+        "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
+        "value": round(qps, 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {"workload": "C2: 10Mx192 u8 mixture, PQ M=48 fp32 ADC, graph R=64, "
+                               "Zipf(1.1) tags/2000, AND of 1-2 tags, top-10",
+                   "n": wl.n, "queries": pl.queries, "graph_routes": pl.graph.count,
+                   "posting_routes": pl.posting.count, "queue": chosen, "shortlist": 100,
+                   "rerank": "exact u8 on GPU", "recall_at_10": round(rec, 4),
+                   "gt_queries": len(gt)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 5),
+                     "traffic": None, "kernel": "traversal_kernel<PqScorer<48>>",
+                     "kernel_ms": round(kms, 3), "algorithmic_bytes": abytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -215,6 +215,17 @@ int gofann_predicate_masks(gofann_ctx* c, const gofann_predicate_view* predicate
     });
 }
 
+int gofann_merge_routes(gofann_ctx* c, const uint32_t* query_route_offsets,
+                        const uint32_t* query_routes, const uint32_t* route_ids,
+                        const float* route_dists, uint32_t width, uint32_t queries, uint32_t topk,
+                        uint32_t* out_ids, float* out_dists)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::merge_routes(ctx, query_route_offsets, query_routes, route_ids,
+                                    route_dists, width, queries, topk, out_ids, out_dists);
+    });
+}
+
 int gofann_pq_score(gofann_ctx* c, const gofann_pq_view* pq, const void* queries, int query_elem,
                     const uint32_t* q_idx, const uint32_t* s_idx, uint32_t n, float* out)
 {

@@ -75,6 +75,9 @@ int exact_rerank(Context* ctx, const void* base, int base_elem, uint32_t dim, ui
                  float* out_dists);
 int predicate_masks(Context* ctx, const gofann_predicate_view* pred, const uint32_t* route_ids,
                     const uint32_t* sample_ids, uint32_t n, uint32_t* masks);
+int merge_routes(Context* ctx, const uint32_t* q_route_offsets, const uint32_t* q_routes,
+                 const uint32_t* route_ids, const float* route_dists, uint32_t width,
+                 uint32_t queries, uint32_t topk, uint32_t* out_ids, float* out_dists);
 int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
                    uint32_t count, const float* rotation, gofann_rabitq_queries* out);
 

@@ -386,6 +386,79 @@ int predicate_masks(Context* ctx, const gofann_predicate_view* pred, const uint3
     return GOFANN_OK;
 }
 
+// Route -> original query merge (merge_route_results_to_original,
+// src/search/rabitq/rabitq_lowfreq_merge.h:709-815): for each query the
+// minimum distance per sample over its routes, ordered by (distance, id),
+// first topk.  One thread per query keeps a sorted top-k with dedup: a
+// sample already held is replaced only by a smaller distance, and a sample
+// evicted earlier can never re-enter with a larger one (the k-th distance
+// only falls), so the streamed result equals the hash/dedup/sort of the
+// reference.
+constexpr int kMaxMergeTopk = 64;
+
+__global__ __launch_bounds__(256) void merge_routes_kernel(const uint32_t* q_route_offsets,
+                                                          const uint32_t* q_routes,
+                                                          const uint32_t* route_ids,
+                                                          const float* route_dists, uint32_t width,
+                                                          uint32_t queries, uint32_t topk,
+                                                          uint32_t* out_ids, float* out_dists)
+{
+    const uint32_t q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= queries) return;
+    float bd[kMaxMergeTopk];
+    uint32_t bi[kMaxMergeTopk];
+    uint32_t n = 0;
+    for (uint32_t k = q_route_offsets[q]; k < q_route_offsets[q + 1]; ++k) {
+        const uint32_t r = q_routes[k];
+        for (uint32_t i = 0; i < width; ++i) {
+            const uint32_t id = route_ids[static_cast<size_t>(r) * width + i];
+            if (id == UINT32_MAX) continue;
+            const float d = route_dists[static_cast<size_t>(r) * width + i];
+            uint32_t have = n;
+            for (uint32_t j = 0; j < n; ++j)
+                if (bi[j] == id) have = j;
+            if (have < n) {
+                if (!(d < bd[have])) continue;
+                for (uint32_t j = have; j + 1 < n; ++j) {  // drop the old entry
+                    bd[j] = bd[j + 1];
+                    bi[j] = bi[j + 1];
+                }
+                --n;
+            }
+            if (n == topk && !pair_less(d, id, bd[n - 1], bi[n - 1])) continue;
+            uint32_t pos = n < topk ? n : topk - 1;
+            while (pos > 0 && pair_less(d, id, bd[pos - 1], bi[pos - 1])) {
+                bd[pos] = bd[pos - 1];
+                bi[pos] = bi[pos - 1];
+                --pos;
+            }
+            bd[pos] = d;
+            bi[pos] = id;
+            if (n < topk) ++n;
+        }
+    }
+    for (uint32_t j = 0; j < topk; ++j) {
+        out_ids[static_cast<size_t>(q) * topk + j] = j < n ? bi[j] : UINT32_MAX;
+        out_dists[static_cast<size_t>(q) * topk + j] = j < n ? bd[j] : FLT_MAX;
+    }
+}
+
+int merge_routes(Context* ctx, const uint32_t* q_route_offsets, const uint32_t* q_routes,
+                 const uint32_t* route_ids, const float* route_dists, uint32_t width,
+                 uint32_t queries, uint32_t topk, uint32_t* out_ids, float* out_dists)
+{
+    if (!q_route_offsets || !q_routes || !route_ids || !route_dists || !out_ids || !out_dists)
+        return ctx->fail(GOFANN_ERR_INVALID, "merge inputs incomplete");
+    if (topk == 0 || topk > static_cast<uint32_t>(kMaxMergeTopk))
+        return ctx->fail(GOFANN_ERR_INVALID, "merge topk must be in [1, 64]");
+    if (queries == 0) return GOFANN_OK;
+    hipLaunchKernelGGL(merge_routes_kernel, dim3((queries + 255) / 256), dim3(256), 0, ctx->stream,
+                       q_route_offsets, q_routes, route_ids, route_dists, width, queries, topk,
+                       out_ids, out_dists);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("merge launch");
+    return GOFANN_OK;
+}
+
 namespace {
 uint32_t pow2_at_least(uint32_t x)
 {

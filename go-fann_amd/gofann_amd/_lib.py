@@ -109,6 +109,7 @@ SIGNATURES = {
                                              C.POINTER(PredicateView), P, P, P, P, U32,
                                              C.c_int, P, P, P]),
     "gofann_exact_rerank": (C.c_int, [P, P, C.c_int, U32, U32, P, P, P, U32, U32, U32, P, P]),
+    "gofann_merge_routes": (C.c_int, [P, P, P, P, P, U32, U32, U32, P, P]),
     "gofann_predicate_masks": (C.c_int, [P, C.POINTER(PredicateView), P, P, U32, P]),
     "gofann_pq_score": (C.c_int, [P, C.POINTER(PqView), P, C.c_int, P, P, U32, P]),
     "gofann_rabitq_score": (C.c_int, [P, C.POINTER(RabitqView), C.POINTER(RabitqQueries),

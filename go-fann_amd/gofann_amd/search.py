@@ -224,3 +224,25 @@ def merge_routes(route_to_query: np.ndarray, ids: np.ndarray, dists: np.ndarray,
     out_i[q_of[keep], rank[keep]] = fi[keep]
     out_d[q_of[keep], rank[keep]] = fd[keep]
     return out_i, out_d
+
+
+def query_route_csr(route_to_query: np.ndarray, queries: int):
+    """CSR of routes per original query (route ids grouped by query)."""
+    r2q = np.asarray(route_to_query, dtype=np.int64)
+    order = np.argsort(r2q, kind="stable").astype(np.uint32)
+    counts = np.bincount(r2q, minlength=queries)
+    offsets = np.zeros(queries + 1, dtype=np.uint32)
+    np.cumsum(counts, out=offsets[1:])
+    return offsets, order
+
+
+def merge_routes_gpu(ctx, q_offsets: torch.Tensor, q_routes: torch.Tensor, ids: torch.Tensor,
+                     dists: torch.Tensor, width: int, queries: int, topk: int):
+    out_i = torch.empty(max(queries, 1) * topk, dtype=torch.int32, device=DEV)
+    out_d = torch.empty(max(queries, 1) * topk, dtype=torch.float32, device=DEV)
+    if queries == 0:
+        return out_i[:0], out_d[:0]
+    ctx.check(ctx.lib.gofann_merge_routes(ctx.handle, _lib.ptr(q_offsets), _lib.ptr(q_routes),
+                                          _lib.ptr(ids), _lib.ptr(dists), width, queries, topk,
+                                          _lib.ptr(out_i), _lib.ptr(out_d)))
+    return out_i, out_d

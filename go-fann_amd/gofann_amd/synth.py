@@ -74,21 +74,22 @@ def zipf_tags(n: int, vocab: int, s: float, min_tags: int, max_tags: int, seed: 
     rng = np.random.default_rng(seed)
     probs = _zipf_probs(vocab, s)
     counts = rng.integers(min_tags, max_tags + 1, size=n)
-    draws = rng.choice(vocab, size=(n, max_tags), p=probs)
-    # distinct tags: drop repeats inside a row, keep the first `count` distinct
-    rows = np.sort(draws, axis=1)
-    dup = np.zeros_like(rows, dtype=bool)
-    dup[:, 1:] = rows[:, 1:] == rows[:, :-1]
-    rows = np.where(dup, vocab, rows)                      # vocab = hole
-    rows = np.sort(rows, axis=1)
+    # draw extra candidates so rows keep `count` distinct tags in draw order
+    extra = 2 * max_tags
+    draws = rng.choice(vocab, size=(n, extra), p=probs)
+    seen_before = np.zeros_like(draws, dtype=bool)
+    for j in range(1, extra):
+        seen_before[:, j] = (draws[:, :j] == draws[:, j:j + 1]).any(axis=1)
+    fresh = ~seen_before
+    rank = np.cumsum(fresh, axis=1)
+    keep = fresh & (rank <= counts[:, None])
+    rows = np.where(keep, draws, vocab)
+    rows = np.sort(rows, axis=1)                           # CSR rows are sorted
     valid = rows < vocab
-    # keep at most counts[i] smallest-index distinct draws (order-free subset)
-    keep = np.arange(max_tags)[None, :] < counts[:, None]
-    keep &= valid
-    nnz = keep.sum(axis=1)
+    nnz = valid.sum(axis=1)
     offsets = np.zeros(n + 1, dtype=np.uint64)
     np.cumsum(nnz, out=offsets[1:])
-    values = rows[keep].astype(np.uint32)
+    values = rows[valid].astype(np.uint32)
     return offsets.astype(np.uint32), values
 
 

@@ -239,6 +239,15 @@ int gofann_exact_rerank(gofann_ctx* ctx, const void* base, int base_elem,
                         uint32_t width, uint32_t routes, uint32_t topk,
                         uint32_t* out_ids, float* out_dists);
 
+/* ---- route -> original query merge (merge_route_results_to_original,
+ * src/search/rabitq/rabitq_lowfreq_merge.h:709-815): query q owns routes
+ * query_routes[query_route_offsets[q] .. [q+1]); per query, minimum
+ * distance per sample, (distance, id) order, first topk (<= 64). */
+int gofann_merge_routes(gofann_ctx* ctx, const uint32_t* query_route_offsets,
+                        const uint32_t* query_routes, const uint32_t* route_ids,
+                        const float* route_dists, uint32_t width, uint32_t queries,
+                        uint32_t topk, uint32_t* out_ids, float* out_dists);
+
 /* ---- device predicate bitsets (prepare_candidate_pass_masks,
  * src/predicates/gpu_predicate_parallel.cuh:21-42): bit i % 32 of
  * masks[i / 32] = matches(route_ids[i], sample_ids[i]); ceil(n/32) words. */

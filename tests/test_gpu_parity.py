@@ -240,3 +240,29 @@ def test_exact_rerank_matches_oracle(gpu_ctx, elem):
     torch.cuda.synchronize()
     assert np.array_equal(as_u32(ids).reshape(routes, topk), oi)
     assert np.array_equal(dists.cpu().numpy().reshape(routes, topk).view(np.uint32), od.view(np.uint32))
+
+
+def test_merge_routes_matches_oracle(gpu_ctx):
+    say("merge routes")
+    fx = load_golden("route_merge.json")
+    rng = np.random.default_rng(9)
+    cases = [(np.array(c["route_to_query"], np.uint32), np.array(c["ids"], np.uint32),
+              np.array(c["dists"], np.float32), c["queries"], c["topk"], c["expected"])
+             for c in fx["cases"]]
+    for _ in range(6):
+        routes, width, queries, topk = int(rng.integers(1, 300)), int(rng.integers(1, 20)), \
+            int(rng.integers(1, 60)), int(rng.integers(1, 12))
+        ids = rng.integers(0, 50, (routes, width)).astype(np.uint32)
+        ids[rng.random((routes, width)) < 0.2] = U32MAX
+        d = (rng.integers(0, 40, (routes, width)) / 4).astype(np.float32)
+        cases.append((rng.integers(0, queries, routes).astype(np.uint32), ids, d, queries, topk, None))
+    for r2q, ids, d, queries, topk, expected in cases:
+        oi, od = po.merge(r2q, ids, d, queries, topk)
+        if expected is not None:
+            assert oi.tolist() == expected
+        off, order = gs.query_route_csr(r2q, queries)
+        gi_, gd = gs.merge_routes_gpu(gpu_ctx, gs.u32(off), gs.u32(order), gs.u32(ids.reshape(-1)),
+                                      gs.to_dev(d.reshape(-1)), ids.shape[1], queries, topk)
+        torch.cuda.synchronize()
+        assert np.array_equal(as_u32(gi_).reshape(queries, topk), oi)
+        assert np.array_equal(gd.cpu().numpy().reshape(queries, topk).view(np.uint32), od.view(np.uint32))
