@@ -240,8 +240,6 @@ def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch
     rep_bridges = rep_bridges if rep_bridges is not None else R // 2
     xg = xg.float()
     order = torch.argsort(cluster_of, stable=True)
-    inv = torch.empty_like(order)
-    inv[order] = torch.arange(n, device=dev)
     xs = xg[order]
     bs = cluster_of[order]
     k_local = R - bridges
@@ -290,9 +288,10 @@ def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch
         cand = torch.cat([cand, torch.full((n, R - cand.shape[1]), -1, device=dev,
                                            dtype=cand.dtype)], 1)
     # back to the caller's row order
+    # sorted position i is the caller's row order[i]; so are its edge targets
     mapped = torch.where(cand >= 0, order[cand.clamp(min=0)], torch.full_like(cand, -1))
     res = torch.empty_like(mapped)
-    res[inv] = mapped
+    res[order] = mapped
     res_np = res.cpu().numpy()
     return np.where(res_np >= 0, res_np, 0xFFFFFFFF).astype(np.uint32)
 
