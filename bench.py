@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--queries", type=int, default=100_000)
     ap.add_argument("--gt-queries", type=int, default=2000)
     ap.add_argument("--queue", type=int, default=0, help="beam width; 0 = ladder search")
-    ap.add_argument("--ladder", default="64,96,128,192,256")
+    ap.add_argument("--ladder", default="32,48,64,96,128,192,256,384")
     ap.add_argument("--target-recall", type=float, default=0.90)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -74,7 +74,7 @@ def build_world(args, torch):
     log(f"label graphs: {int((li.label_size > 0).sum())} labels, {li.rows} rows, "
         f"degree 64 in {time.time() - t0:.1f}s")
     t0 = time.time()
-    pl = gp.plan_queries(li, wl.query_labels)
+    pl = gp.plan_queries(li, wl.query_labels, seeds="nearest_bucket", queries=wl.queries)
     log(f"plan: {pl.graph.count} graph routes, {pl.posting.count} posting routes "
         f"in {time.time() - t0:.1f}s")
     return wl, li, table, codes, pl
@@ -214,7 +214,8 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, torch):
     chunk = 64
     while done < len(qlist) and time.perf_counter() - t0 < seconds:
         sel = qlist[done: done + chunk]
-        sub = gp.plan_queries(li, [wl.query_labels[i] for i in sel])
+        sub = gp.plan_queries(li, [wl.query_labels[i] for i in sel], seeds="nearest_bucket",
+                              queries=qs[sel])
         rs = sub.graph
         res_i, res_d, r2q = [], [], []
         if rs.count:
@@ -312,7 +313,8 @@ def main():
                                "Zipf(1.1) tags/2000, AND of 1-2 tags, top-10",
                    "n": wl.n, "queries": pl.queries, "graph_routes": pl.graph.count,
                    "posting_routes": pl.posting.count, "queue": chosen, "shortlist": 100,
-                   "rerank": "exact u8 on GPU", "recall_at_10": round(rec, 4),
+                   "rerank": "exact u8 on GPU", "seeds": "nearest bucket representative",
+                   "recall_at_10": round(rec, 4),
                    "gt_queries": len(gt)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 5),

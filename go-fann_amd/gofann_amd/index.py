@@ -156,6 +156,12 @@ class LabelIndex:
     csr_offsets: np.ndarray     # [N+1] u32 sample-major labels
     csr_labels: np.ndarray      # u32
     degree: int
+    # bucket representatives per graph label (entry points of the
+    # nearest-bucket seed mode): CSR over labels of (cluster, local row)
+    rep_offset: np.ndarray | None = None
+    rep_cluster: np.ndarray | None = None
+    rep_row: np.ndarray | None = None
+    centres: np.ndarray | None = None
 
     @property
     def rows(self) -> int:
@@ -228,7 +234,7 @@ def _bucket_knn(xg: torch.Tensor, bucket_of: torch.Tensor, k: int, max_batch_ele
 
 def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch.Tensor,
                       degree: int, bridges: int = 4, rep_bridges: int | None = None,
-                      max_batch_elems: int = 1 << 27) -> np.ndarray:
+                      max_batch_elems: int = 1 << 27, return_reps: bool = False):
     """Graph over the rows of one label group (rows in the given order).
 
     Edges of a row: exact kNN inside its (label, cluster) bucket, then the
@@ -293,7 +299,12 @@ def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch
     res = torch.empty_like(mapped)
     res[order] = mapped
     res_np = res.cpu().numpy()
-    return np.where(res_np >= 0, res_np, 0xFFFFFFFF).astype(np.uint32)
+    graph_np = np.where(res_np >= 0, res_np, 0xFFFFFFFF).astype(np.uint32)
+    if return_reps:
+        # (cluster id, representative row in the caller's order) per bucket
+        return graph_np, uniq.cpu().numpy().astype(np.int32), \
+            order[rep].cpu().numpy().astype(np.uint32)
+    return graph_np
 
 
 def nearest_centre(x: torch.Tensor, centres: torch.Tensor, chunk: int = 1 << 18) -> torch.Tensor:
@@ -324,6 +335,8 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
     graph = np.full((total, degree), UINT32_MAX, dtype=np.uint32)
     seed_local = np.full(num_labels, UINT32_MAX, dtype=np.uint32)
     cluster = nearest_centre(base, centres)
+    rep_cluster = [np.zeros(0, np.int32)] * num_labels
+    rep_row = [np.zeros(0, np.uint32)] * num_labels
     for l in graph_labels:
         s0, s1 = int(post_off[l]), int(post_off[l + 1])
         samples = post_ids[s0:s1]
@@ -331,11 +344,16 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
         row_to_sample[o:o + len(samples)] = samples
         sidx = torch.as_tensor(samples.astype(np.int64), device=base.device)
         xg = base[sidx].float()
-        graph[o:o + len(samples)] = build_group_graph(xg, cluster[sidx], centres, degree, bridges)
+        graph[o:o + len(samples)], rep_cluster[l], rep_row[l] = build_group_graph(
+            xg, cluster[sidx], centres, degree, bridges, return_reps=True)
         # seed: row nearest the group mean (fp64), dataloader.cpp:7361-7406
         xd = xg.double()
         mu = xd.mean(0, keepdim=True)
         seed_local[l] = int(((xd - mu) ** 2).sum(1).argmin())
+    rep_off = np.zeros(num_labels + 1, dtype=np.int64)
+    np.cumsum([len(r) for r in rep_row], out=rep_off[1:])
     return LabelIndex(num_labels, threshold, cat_freq, label_offset, label_size, row_to_sample,
                       graph, seed_local, post_off, post_ids,
-                      label_offsets.astype(np.uint32), label_values.astype(np.uint32), degree)
+                      label_offsets.astype(np.uint32), label_values.astype(np.uint32), degree,
+                      rep_off, np.concatenate(rep_cluster), np.concatenate(rep_row),
+                      centres.detach().float().cpu().numpy())

@@ -87,9 +87,33 @@ def _routeset(rows: list, index) -> RouteSet:
     return RouteSet(rq, rg, rs, rq.copy(), pred)
 
 
+def nearest_bucket_seeds(index, rs: RouteSet, queries) -> np.ndarray:
+    """Per-route seed: the representative row of the route label's bucket
+    whose mixture centre is nearest the query (an IVF-style entry point).
+    The reference seeds every route of a label at the label's medoid
+    (dataloader.cpp:7361-7406); this mode only changes `route_start`."""
+    import torch
+    q = torch.as_tensor(queries).float()
+    cen = torch.as_tensor(index.centres, device=q.device)
+    out = rs.route_start.copy()
+    groups = rs.route_group
+    for g in np.unique(groups):
+        lo, hi = int(index.rep_offset[g]), int(index.rep_offset[g + 1])
+        if hi == lo:
+            continue
+        sel = np.nonzero(groups == g)[0]
+        c = cen[torch.as_tensor(index.rep_cluster[lo:hi].astype(np.int64), device=q.device)]
+        qq = q[torch.as_tensor(rs.route_query[sel].astype(np.int64), device=q.device)]
+        d = (c * c).sum(1)[None, :] - 2 * qq @ c.t()
+        best = d.argmin(1).cpu().numpy()
+        out[sel] = index.rep_row[lo + best]
+    return out
+
+
 def plan_queries(index, query_labels: list, query_ranges: list | None = None,
-                 sort_by_group: bool = True) -> Plan:
-    """Routes for every query (see module docstring)."""
+                 sort_by_group: bool = True, seeds: str = "medoid", queries=None) -> Plan:
+    """Routes for every query (see module docstring).  seeds="medoid" keeps
+    the reference's one seed per label; "nearest_bucket" needs `queries`."""
     graph_rows, post_rows = [], []
     for q, labels in enumerate(query_labels):
         rng = [tuple(a) for a in (query_ranges[q] if query_ranges is not None else [])]
@@ -106,6 +130,10 @@ def plan_queries(index, query_labels: list, query_ranges: list | None = None,
     if sort_by_group:
         graph_rows.sort(key=lambda r: (r[1], r[0]))
     g = _routeset(graph_rows, index)
+    if seeds == "nearest_bucket" and g.count:
+        g.route_start = nearest_bucket_seeds(index, g, queries)
+    elif seeds != "medoid":
+        raise ValueError(f"unknown seed mode {seeds}")
     p = _routeset(post_rows, index)
     off = np.array([index.posting_offset[r[1]] for r in post_rows], dtype=np.uint64)
     size = np.array([index.posting_offset[r[1] + 1] - index.posting_offset[r[1]]
