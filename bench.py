@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--target-recall", type=float, default=0.90)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-inline-exact", action="store_true",
+                    help="rank graph routes by ADC and rerank a 100-wide shortlist instead")
     return ap.parse_args()
 
 
@@ -124,15 +126,22 @@ def recall_at_10(result: np.ndarray, gt: dict) -> float:
 
 
 class Pipeline:
-    """Device-resident index + one full GPU step."""
+    """Device-resident index + one full GPU step.
 
-    def __init__(self, ctx, wl, li, table, codes, pl, torch):
+    inline=True: graph routes rank their result heap by exact distance on
+    the resident base vectors (inline exact rerank), so each graph route
+    emits its exact top-10 directly; posting routes keep a 100-wide ADC
+    shortlist that the exact rerank kernel reduces to 10.  inline=False:
+    every route emits a 100-wide ADC shortlist, all reranked exactly."""
+
+    def __init__(self, ctx, wl, li, table, codes, pl, torch, inline=True, width=100):
         from gofann_amd import search as gs
         self.gs, self.torch, self.ctx = gs, torch, ctx
         self.wl, self.pl = wl, pl
+        self.inline = inline
         self.dg = gs.DeviceGraph.upload(li)
         self.keep = (codes, table)
-        self.pqv = gs.pq_view(codes, table)
+        self.pqv = gs.pq_view(codes, table, wl.base if inline else None)
         self.q = wl.queries
         self.dr_graph = gs.DeviceRoutes.upload(pl.graph)
         self.dr_post = gs.DeviceRoutes.upload(pl.posting)
@@ -143,38 +152,64 @@ class Pipeline:
         self.q_off, self.q_routes = gs.u32(off), gs.u32(order)
         self.route_query_all = gs.u32(np.concatenate([pl.graph.route_query,
                                                       pl.posting.route_query]))
-        self.W = 100
+        self.route_query_post = gs.u32(pl.posting.route_query if self.n_post
+                                       else np.zeros(1, np.uint32))
+        self.W = width
+        self.GW = 10 if inline else width  # graph route output width
         n = self.n_graph + self.n_post
-        self.sl_ids = torch.empty(max(n, 1) * self.W, dtype=torch.int32, device="cuda")
-        self.sl_d = torch.empty(max(n, 1) * self.W, dtype=torch.float32, device="cuda")
-        self.stats = torch.zeros(max(self.n_graph, 1) * 8, dtype=torch.int32, device="cuda")
+        dev = dict(device="cuda")
+        if inline:
+            # final per-route top-10: graph routes write theirs directly
+            self.fin_i = torch.empty(max(n, 1) * 10, dtype=torch.int32, **dev)
+            self.fin_d = torch.empty(max(n, 1) * 10, dtype=torch.float32, **dev)
+            self.sl_ids = torch.empty(max(self.n_post, 1) * self.W, dtype=torch.int32, **dev)
+            self.sl_d = torch.empty(max(self.n_post, 1) * self.W, dtype=torch.float32, **dev)
+        else:
+            self.sl_ids = torch.empty(max(n, 1) * self.W, dtype=torch.int32, **dev)
+            self.sl_d = torch.empty(max(n, 1) * self.W, dtype=torch.float32, **dev)
+        self.stats = torch.zeros(max(self.n_graph, 1) * 8, dtype=torch.int32, **dev)
         self.co = gs.u32(pl.cand_offsets if self.n_post else np.zeros(1, np.uint32))
         self.cs = gs.u32(pl.cand_sizes if self.n_post else np.zeros(1, np.uint32))
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
 
+    def _posting_scan(self, ids, dists):
+        gs = self.gs
+        pv = self.dr_post.predicate_view(self.dg, 0.0, False)
+        self.ctx.check(self.ctx.lib.gofann_pq_posting_scan(
+            self.ctx.handle, self.pqv, gs._lib.ptr(self.q), gs.query_elem(self.q), pv,
+            gs._lib.ptr(self.dr_post.route_query), gs._lib.ptr(self.dg.posting_ids),
+            gs._lib.ptr(self.co), gs._lib.ptr(self.cs), self.n_post, self.W, gs._lib.ptr(ids),
+            gs._lib.ptr(dists), None))
+
     def step(self, Q: int, timed_kernel=False):
-        gs, torch = self.gs, self.torch
-        W, ng, npost = self.W, self.n_graph, self.n_post
-        prm = gs.search_params(queue_limit=Q, result_width=W)
+        gs = self.gs
+        W, GW, ng, npost = self.W, self.GW, self.n_graph, self.n_post
+        prm = gs.search_params(queue_limit=Q, result_width=GW, inline_exact=self.inline)
+        if self.inline:
+            g_out = (self.fin_i[: max(ng, 1) * 10], self.fin_d[: max(ng, 1) * 10], self.stats)
+        else:
+            g_out = (self.sl_ids, self.sl_d, self.stats)
         if timed_kernel:
             self.ev[0].record()
         if ng:
-            gs.run_pq_routes(self.ctx, self.pqv, self.q, self.dg, self.dr_graph, prm,
-                             out=(self.sl_ids, self.sl_d, self.stats))
+            gs.run_pq_routes(self.ctx, self.pqv, self.q, self.dg, self.dr_graph, prm, out=g_out)
         if timed_kernel:
             self.ev[1].record()
-        if npost:
-            ids_p = self.sl_ids[ng * W:]
-            d_p = self.sl_d[ng * W:]
-            pv = self.dr_post.predicate_view(self.dg, 0.0, False)
-            self.ctx.check(self.ctx.lib.gofann_pq_posting_scan(
-                self.ctx.handle, self.pqv, gs._lib.ptr(self.q), gs.query_elem(self.q), pv,
-                gs._lib.ptr(self.dr_post.route_query), gs._lib.ptr(self.dg.posting_ids),
-                gs._lib.ptr(self.co), gs._lib.ptr(self.cs), npost, W, gs._lib.ptr(ids_p),
-                gs._lib.ptr(d_p), None))
-        n = ng + npost
-        rr_i, rr_d = gs.exact_rerank(self.ctx, self.wl.base, self.q, self.route_query_all,
-                                     self.sl_ids, W, n, 10)
+        if self.inline:
+            if npost:
+                self._posting_scan(self.sl_ids, self.sl_d)
+                self.ctx.check(self.ctx.lib.gofann_exact_rerank(
+                    self.ctx.handle, gs._lib.ptr(self.wl.base), gs.ELEM_U8,
+                    int(self.wl.base.shape[1]), int(self.wl.base.shape[0]),
+                    gs._lib.ptr(self.q), gs._lib.ptr(self.route_query_post),
+                    gs._lib.ptr(self.sl_ids), W, npost, 10,
+                    gs._lib.ptr(self.fin_i[ng * 10:]), gs._lib.ptr(self.fin_d[ng * 10:])))
+            rr_i, rr_d = self.fin_i, self.fin_d
+        else:
+            if npost:
+                self._posting_scan(self.sl_ids[ng * W:], self.sl_d[ng * W:])
+            rr_i, rr_d = gs.exact_rerank(self.ctx, self.wl.base, self.q, self.route_query_all,
+                                         self.sl_ids, W, ng + npost, 10)
         out_i, out_d = gs.merge_routes_gpu(self.ctx, self.q_off, self.q_routes, rr_i, rr_d, 10,
                                            self.pl.queries, 10)
         return out_i
@@ -186,21 +221,25 @@ class Pipeline:
         return self.stats[: self.n_graph * 8].cpu().numpy().reshape(-1, 8)
 
 
-def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int) -> float:
+def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes: int) -> float:
     """Bytes the traversal must move per launch: adjacency row + row_to_sample
     of each expanded node, code row + row_to_sample of each scored candidate,
-    CSR offsets of each predicate row opened and each label word read."""
+    CSR offsets of each predicate row opened and each label word read, and
+    (inline exact ranking) the base vector of each expanded node that passes."""
     E = st[:, 1].astype(np.float64).sum()
+    Pn = st[:, 2].astype(np.float64).sum()
     V = st[:, 3].astype(np.float64).sum()
     rows = st[:, 4].astype(np.float64).sum()
     labels = st[:, 5].astype(np.float64).sum()
-    return E * (4 * degree + 4) + V * (code_bytes + 4) + rows * 8 + labels * 4
+    return (E * (4 * degree + 4) + V * (code_bytes + 4) + rows * 8 + labels * 4
+            + Pn * exact_bytes)
 
 
-def cpu_baseline(wl, li, table, codes, pl, Q, seconds, torch):
+def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline):
     """The oracle (a single-threaded C restatement of the reference path) on
-    a bounded sample of the same workload: graph search, posting scan, exact
-    rerank and merge for the first queries until `seconds` elapse."""
+    a bounded sample of the same workload: graph search (with the same
+    inline exact ranking as the GPU step), posting scan, exact rerank and
+    merge for the first queries until `seconds` elapse."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import pyoracle as po
     from gofann_amd import plan as gp
@@ -221,9 +260,16 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, torch):
         if rs.count:
             pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
                                                 pending_base_stop=True)
-            ids, _, _ = po.pq_search(li, rs, pred, po.params(queue_limit=Q, result_width=100),
-                                     codes_h, table_h, qs[sel])
-            ri, rd = po.rerank(base, qs[sel], rs.route_query, ids, 10)
+            if inline:
+                ri, rd, _ = po.pq_search(li, rs, pred,
+                                         po.params(queue_limit=Q, result_width=10,
+                                                   inline_exact=True),
+                                         codes_h, table_h, qs[sel], base=base)
+            else:
+                ids, _, _ = po.pq_search(li, rs, pred,
+                                         po.params(queue_limit=Q, result_width=100),
+                                         codes_h, table_h, qs[sel])
+                ri, rd = po.rerank(base, qs[sel], rs.route_query, ids, 10)
             res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
         if sub.posting.count:
             pr = po.PredicateArrays.from_plan(sub.posting.predicate, li)
@@ -253,7 +299,8 @@ def main():
     gt = ground_truth(wl, li, torch, args.gt_queries)
     log(f"ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     ctx = _lib.Context(0)
-    pipe = Pipeline(ctx, wl, li, table, codes, pl, torch)
+    inline = not args.no_inline_exact
+    pipe = Pipeline(ctx, wl, li, table, codes, pl, torch, inline=inline)
 
     ladder = [args.queue] if args.queue else [int(x) for x in args.ladder.split(",")]
     chosen, rec = ladder[-1], 0.0
@@ -283,14 +330,14 @@ def main():
     rec = recall_at_10(res, gt)
     st = pipe.route_stats()
     kms = float(np.mean(kernel_ms))
-    abytes = algorithmic_bytes(st, li.degree, 48)
+    abytes = algorithmic_bytes(st, li.degree, 48, wl.dim if inline else 0)
     achieved = abytes / (kms / 1000.0) / 1e9
     log(f"step {ms_per_step:.1f} ms, traversal kernel {kms:.1f} ms, recall {rec:.4f}, "
         f"steps/route {st[:, 0].mean():.1f}, scored/route {st[:, 3].mean():.1f}")
 
     cpu = None
     if not args.no_cpu_baseline:
-        cq, cn, cel = cpu_baseline(wl, li, table, codes, pl, chosen, args.cpu_seconds, torch)
+        cq, cn, cel = cpu_baseline(wl, li, table, codes, pl, chosen, args.cpu_seconds, inline)
         cpu = {"value": round(cq, 2), "unit": "queries/s", "cores": 1, "kind": "port",
                "sample": f"first {cn} of the {pl.queries} C2 queries (graph search Q={chosen}, "
                          f"posting scan, exact rerank, merge) in {cel:.1f}s on one host core"}
@@ -312,7 +359,8 @@ def main():
         "config": {"workload": "C2: 10Mx192 u8 mixture, PQ M=48 fp32 ADC, graph R=64, "
                                "Zipf(1.1) tags/2000, AND of 1-2 tags, top-10",
                    "n": wl.n, "queries": pl.queries, "graph_routes": pl.graph.count,
-                   "posting_routes": pl.posting.count, "queue": chosen, "shortlist": 100,
+                   "posting_routes": pl.posting.count, "queue": chosen,
+                   "graph_ranking": "inline exact u8" if inline else "ADC, shortlist 100",
                    "rerank": "exact u8 on GPU", "seeds": "nearest bucket representative",
                    "recall_at_10": round(rec, 4),
                    "gt_queries": len(gt)},

@@ -39,6 +39,7 @@ namespace gofann {
 // lane evaluates that fixed tree for its own candidate in registers.
 template <int kM>
 struct PqScorer {
+    static constexpr bool kHasExact = true;
     const uint8_t* codes;
     const float* centroids;
     const void* queries;
@@ -46,12 +47,60 @@ struct PqScorer {
     uint32_t dim;
     uint32_t pq_dim;
     float* lut;
+    const void* exact_base;  // resident vectors for the inline exact distance
+    uint32_t query;
 
     __device__ int m() const { return kM > 0 ? kM : static_cast<int>(pq_dim); }
+
+    // Exact distance of the expanded node in the reference's 32-lane order
+    // (backend_pq.cu:4507-4540): lane j < 32 sums the 4-element words j,
+    // j+32, ... (elements in order), then the xor butterfly 16..1.  u8 uses
+    // integer squares added as float; f32 uses fma.  Wave-uniform result.
+    __device__ float exact(uint32_t sample, int lane) const
+    {
+        float acc = 0.0f;
+        const uint32_t words = dim / 4;
+        if (lane < 32) {
+            if (query_f32) {
+                const float* b = static_cast<const float*>(exact_base) + static_cast<size_t>(sample) * dim;
+                const float* q = static_cast<const float*>(queries) + static_cast<size_t>(query) * dim;
+                for (uint32_t w = lane; w < words; w += 32) {
+                    const float4 bv = reinterpret_cast<const float4*>(b)[w];
+                    const float4 qv = reinterpret_cast<const float4*>(q)[w];
+                    float d = bv.x - qv.x;
+                    acc = fmaf(d, d, acc);
+                    d = bv.y - qv.y;
+                    acc = fmaf(d, d, acc);
+                    d = bv.z - qv.z;
+                    acc = fmaf(d, d, acc);
+                    d = bv.w - qv.w;
+                    acc = fmaf(d, d, acc);
+                }
+            } else {
+                const uint32_t* b = reinterpret_cast<const uint32_t*>(
+                    static_cast<const uint8_t*>(exact_base) + static_cast<size_t>(sample) * dim);
+                const uint32_t* q = reinterpret_cast<const uint32_t*>(
+                    static_cast<const uint8_t*>(queries) + static_cast<size_t>(query) * dim);
+                for (uint32_t w = lane; w < words; w += 32) {
+                    const uint32_t bw = b[w], qw = q[w];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int diff = static_cast<int>((bw >> (8 * t)) & 0xffu) -
+                                         static_cast<int>((qw >> (8 * t)) & 0xffu);
+                        acc += static_cast<float>(diff * diff);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, 32);
+        return bcast0f(acc);
+    }
 
     __device__ void setup(uint32_t q, int lane, unsigned char* lds)
     {
         lut = reinterpret_cast<float*>(lds);
+        query = q;
         const int M = m();
         const int sub = static_cast<int>(dim) / M;
         const float* qf = static_cast<const float*>(queries) + static_cast<size_t>(q) * dim;
@@ -117,6 +166,7 @@ struct PqScorer {
 // bit 31-b <-> dimension 32w+b.  Estimate: fma(f_rescale, ip*scale + k1,
 // f_add + g[anchor]).
 struct RabitqScorer {
+    static constexpr bool kHasExact = false;
     const uint8_t* codes;
     const float* factors;
     const uint32_t* anchor_ids;
@@ -371,6 +421,7 @@ __global__ __launch_bounds__(64) void traversal_kernel(TraversalArgs a, Scorer s
         // Verdict of the expanded node (backend_pq.cu:4393-4441).  Skipped
         // when the pool ran dry: the loop leaves below before reading it.
         int filt = 1;
+        float rank = now.base;
         if (!exhausted) {
             const uint32_t global_row = label_offset + now_local;
             const uint32_t sample = a.graph.row_to_sample[global_row];
@@ -389,6 +440,11 @@ __global__ __launch_bounds__(64) void traversal_kernel(TraversalArgs a, Scorer s
                 pc.rows += c.rows;
                 pc.labels += c.labels;
             }
+            // Inline exact distance of a passing node ranks the heaps
+            // (backend_pq.cu:4507-4546, 4566-4572).
+            if constexpr (Scorer::kHasExact) {
+                if (filt == 1 && a.params.inline_exact_rerank) rank = sc.exact(sample, lane);
+            }
         }
         const float current = now.base;
 
@@ -403,9 +459,9 @@ __global__ __launch_bounds__(64) void traversal_kernel(TraversalArgs a, Scorer s
             ++passed;
             int improved = 0;
             if (lane == 0) {
-                const ResultEntry te = {current, now_local};
+                const ResultEntry te = {rank, now_local};
                 StopEntry se;
-                se.first = current;
+                se.first = rank;
                 se.pad = 0;
                 se.second = (static_cast<uint64_t>(fbits(current)) << 32) | now_local;
                 if (stop_size < SW) {
@@ -725,6 +781,8 @@ PqScorer<kM> make_pq_scorer(const gofann_pq_view* pq, const void* queries, int q
     sc.dim = pq->dim;
     sc.pq_dim = pq->pq_dim;
     sc.lut = nullptr;
+    sc.exact_base = pq->exact_base;
+    sc.query = 0;
     return sc;
 }
 
@@ -736,6 +794,8 @@ int check_pq(Context* ctx, const gofann_pq_view* pq, const void* queries, int qu
         return ctx->fail(GOFANN_ERR_INVALID, "pq_dim must divide dim and be in [1, 256]");
     if (query_elem != GOFANN_ELEM_U8 && query_elem != GOFANN_ELEM_F32)
         return ctx->fail(GOFANN_ERR_INVALID, "PQ queries must be u8 or f32");
+    if (pq->exact_base != nullptr && pq->dim % 4 != 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "inline exact distances need dim % 4 == 0");
     return GOFANN_OK;
 }
 
@@ -779,6 +839,8 @@ int pq_search(Context* ctx, const gofann_pq_view* pq, const void* queries, int q
     if (rc) return rc;
     rc = check_params(ctx, g, r, p);
     if (rc) return rc;
+    if (p->inline_exact_rerank && pq->exact_base == nullptr)
+        return ctx->fail(GOFANN_ERR_INVALID, "inline exact rerank needs gofann_pq_view.exact_base");
     const uint32_t lut_bytes = pq->pq_dim * 256u * 4u;
     switch (pq->pq_dim) {
     case 16:
@@ -808,6 +870,8 @@ int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabit
     if (rc) return rc;
     rc = check_params(ctx, g, r, p);
     if (rc) return rc;
+    if (p->inline_exact_rerank)
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "RaBitQ traversal has no inline exact rerank");
     const uint32_t plane_bytes = rq->padded_dim;  // 8 planes x padded_dim bits
     return launch_traversal(ctx, make_rabitq_scorer(rq, pre), plane_bytes, g, pred, r, p, out_ids,
                             out_dists, stats, 1);

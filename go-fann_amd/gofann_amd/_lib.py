@@ -57,7 +57,7 @@ class SearchParams(C.Structure):
                 ("early_stop_mode", C.c_int), ("max_steps", C.c_int),
                 ("stop_width", C.c_int), ("result_width", C.c_int),
                 ("bit_filter_bonus", C.c_float), ("range_filter_bonus", C.c_float),
-                ("predicate_bias", C.c_int)]
+                ("predicate_bias", C.c_int), ("inline_exact_rerank", C.c_int)]
 
 
 class RouteStats(C.Structure):
@@ -71,7 +71,7 @@ STATS_FIELDS = [f[0] for f in RouteStats._fields_]
 
 class PqView(C.Structure):
     _fields_ = [("codes", P), ("centroids", P), ("dim", U32), ("pq_dim", U32),
-                ("samples", U32)]
+                ("samples", U32), ("exact_base", P)]
 
 
 class RabitqView(C.Structure):

@@ -124,14 +124,16 @@ class DeviceRoutes:
 
 def search_params(queue_limit=64, result_width=100, early_stop_mode=_lib.EARLY_STOP_ADAPTIVE,
                   finish_limit=1, max_steps=0, stop_width=10, bias=True,
-                  bit_bonus=1.0, range_bonus=1.0) -> SearchParams:
+                  bit_bonus=1.0, range_bonus=1.0, inline_exact=False) -> SearchParams:
     return SearchParams(queue_limit, finish_limit, early_stop_mode, max_steps, stop_width,
-                        result_width, bit_bonus, range_bonus, 1 if bias else 0)
+                        result_width, bit_bonus, range_bonus, 1 if bias else 0,
+                        1 if inline_exact else 0)
 
 
-def pq_view(codes: torch.Tensor, table: torch.Tensor) -> PqView:
+def pq_view(codes: torch.Tensor, table: torch.Tensor, exact_base: torch.Tensor | None = None
+            ) -> PqView:
     return PqView(_lib.ptr(codes), _lib.ptr(table), int(table.shape[1]), int(codes.shape[1]),
-                  int(codes.shape[0]))
+                  int(codes.shape[0]), _lib.ptr(exact_base))
 
 
 def query_elem(q: torch.Tensor) -> int:

@@ -134,6 +134,10 @@ typedef struct {
     float bit_filter_bonus;
     float range_filter_bonus;
     int predicate_bias; /* kPredicateBias */
+    /* Exact distance of every expanded predicate-passing node ranks the
+     * result/stop heaps (enable_true_distance_rerank, backend_pq.cu:
+     * 4507-4546, 4566-4572); needs gofann_pq_view.exact_base. */
+    int inline_exact_rerank;
 } gofann_search_params;
 
 /* Per-route counters emitted by the traversal kernels (bytes model). */
@@ -154,6 +158,7 @@ typedef struct {
     uint32_t dim;
     uint32_t pq_dim;
     uint32_t samples;
+    const void* exact_base;   /* [samples][dim] u8 or f32 (matches the queries); may be NULL */
 } gofann_pq_view;
 
 typedef struct {

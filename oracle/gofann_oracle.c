@@ -672,7 +672,7 @@ static float bits_float(uint32_t u)
 
 int orc_beam_search_route(const orc_graph* g, const orc_predicate* pred,
                           const orc_search_params* p, uint32_t route,
-                          orc_scorer scorer, void* sctx, uint32_t* out_ids,
+                          orc_scorer scorer, orc_exact exact, void* sctx, uint32_t* out_ids,
                           float* out_dists, orc_route_stats* st)
 {
     const int Q = p->queue_limit;
@@ -755,6 +755,7 @@ int orc_beam_search_route(const orc_graph* g, const orc_predicate* pred,
          * When the pool is exhausted the loop breaks below before the
          * verdict is read, so it is not evaluated here. */
         int filt = 1;
+        float rank = now.base;
         if (!exhausted) {
             const uint32_t global_row = label_offset + now_local;
             const uint32_t sample = g->row_to_sample[global_row];
@@ -770,6 +771,8 @@ int orc_beam_search_route(const orc_graph* g, const orc_predicate* pred,
             } else if (!enabled && !compiled) {
                 filt = (filt == 1 && bit_match && exact_range) ? 1 : 2;
             }
+            /* Inline exact distance of a passing node (:4507-4546). */
+            if (filt == 1 && p->inline_exact && exact) rank = exact(sctx, route, sample);
         }
         const float current_dist = now.base;
 
@@ -783,8 +786,10 @@ int orc_beam_search_route(const orc_graph* g, const orc_predicate* pred,
         ++expanded;
         if (filt == 1) {
             ++passed;
-            orc_result_pair te = {current_dist, now_local};
-            orc_stop_pair se = {current_dist,
+            /* ranked by the exact distance when inline rerank is on; the
+             * stop payload keeps the approximate distance (:4566-4579) */
+            orc_result_pair te = {rank, now_local};
+            orc_stop_pair se = {rank,
                                 ((uint64_t)float_bits(current_dist) << 32) | (uint64_t)now_local};
             int improved = 0;
             if (stop_size < stop_width) {
@@ -905,10 +910,53 @@ int orc_beam_search_route(const orc_graph* g, const orc_predicate* pred,
 }
 
 /* ---------------------------------------------------------------------- */
+float orc_exact_inline_u8(const uint8_t* q, const uint8_t* b, uint32_t dim)
+{
+    /* backend_pq.cu:4507-4536: integer squares of (u8 - u8), added as float */
+    float s[32];
+    const uint32_t words = dim / 4;
+    for (uint32_t j = 0; j < 32; ++j) {
+        float acc = 0.0f;
+        for (uint32_t w = j; w < words; w += 32)
+            for (uint32_t t = 0; t < 4; ++t) {
+                const int diff = (int)b[4 * w + t] - (int)q[4 * w + t];
+                acc += (float)(diff * diff);
+            }
+        s[j] = acc;
+    }
+    for (int off = 16; off > 0; off >>= 1)
+        for (int j = 0; j < off; ++j) s[j] = s[j] + s[j + off];
+    return s[0];
+}
+
+float orc_exact_inline_f32(const float* q, const float* b, uint32_t dim)
+{
+    /* fp32 payload variant (backend_rabitq.cu:3936-3944 per element, fma) in
+     * the same 32-lane word order */
+    float s[32];
+    const uint32_t words = dim / 4;
+    for (uint32_t j = 0; j < 32; ++j) {
+        float acc = 0.0f;
+        for (uint32_t w = j; w < words; w += 32)
+            for (uint32_t t = 0; t < 4; ++t) {
+                const float diff = b[4 * w + t] - q[4 * w + t];
+                acc = fmaf(diff, diff, acc);
+            }
+        s[j] = acc;
+    }
+    for (int off = 16; off > 0; off >>= 1)
+        for (int j = 0; j < off; ++j) s[j] = s[j] + s[j + off];
+    return s[0];
+}
+
 typedef struct {
     const uint8_t* codes;
     int pq_dim;
     const float* lut; /* current route's table */
+    const void* base; /* exact vectors (inline rerank) */
+    const void* query;
+    int is_float;
+    int dim;
 } pq_ctx;
 
 static float pq_score(void* ctx, uint32_t route, uint32_t sample)
@@ -918,22 +966,37 @@ static float pq_score(void* ctx, uint32_t route, uint32_t sample)
     return orc_pq_adc(c->lut, c->codes + (size_t)sample * c->pq_dim, c->pq_dim);
 }
 
+static float pq_exact(void* ctx, uint32_t route, uint32_t sample)
+{
+    (void)route;
+    const pq_ctx* c = (const pq_ctx*)ctx;
+    if (c->is_float)
+        return orc_exact_inline_f32((const float*)c->query,
+                                    (const float*)c->base + (size_t)sample * c->dim, c->dim);
+    return orc_exact_inline_u8((const uint8_t*)c->query,
+                               (const uint8_t*)c->base + (size_t)sample * c->dim, c->dim);
+}
+
 int orc_pq_search_batch(const orc_graph* g, const orc_predicate* pred,
                         const orc_search_params* p, const uint8_t* codes,
                         const float* centroids, const void* queries, int query_is_float,
-                        const uint32_t* route_query, int dim, int pq_dim, uint32_t routes,
-                        uint32_t* out_ids, float* out_dists, orc_route_stats* stats)
+                        const void* exact_base, const uint32_t* route_query, int dim,
+                        int pq_dim, uint32_t routes, uint32_t* out_ids, float* out_dists,
+                        orc_route_stats* stats)
 {
     float* lut = (float*)malloc((size_t)pq_dim * 256 * sizeof(float));
     if (!lut) return -1;
-    pq_ctx ctx = {codes, pq_dim, lut};
+    pq_ctx ctx = {codes, pq_dim, lut, exact_base, NULL, query_is_float, dim};
     for (uint32_t r = 0; r < routes; ++r) {
         const uint32_t q = route_query[r];
-        if (query_is_float)
+        if (query_is_float) {
+            ctx.query = (const float*)queries + (size_t)q * dim;
             orc_pq_lut_f32(centroids, (const float*)queries + (size_t)q * dim, dim, pq_dim, lut);
-        else
+        } else {
+            ctx.query = (const uint8_t*)queries + (size_t)q * dim;
             orc_pq_lut_u8(centroids, (const uint8_t*)queries + (size_t)q * dim, dim, pq_dim, lut);
-        if (orc_beam_search_route(g, pred, p, r, pq_score, &ctx,
+        }
+        if (orc_beam_search_route(g, pred, p, r, pq_score, exact_base ? pq_exact : NULL, &ctx,
                                   out_ids + (size_t)r * p->result_width,
                                   out_dists + (size_t)r * p->result_width,
                                   stats ? stats + r : NULL) != 0) {
@@ -983,7 +1046,7 @@ int orc_rabitq_search_batch(const orc_graph* g, const orc_predicate* pred,
                   centroid_dists, num_anchors, padded_dim, 0};
     for (uint32_t r = 0; r < routes; ++r) {
         ctx.query = route_query[r];
-        if (orc_beam_search_route(g, pred, p, r, rabitq_score, &ctx,
+        if (orc_beam_search_route(g, pred, p, r, rabitq_score, NULL, &ctx,
                                   out_ids + (size_t)r * p->result_width,
                                   out_dists + (size_t)r * p->result_width,
                                   stats ? stats + r : NULL) != 0)

@@ -114,6 +114,7 @@ typedef struct {
     float range_filter_bonus;
     int bias;          /* kPredicateBias: frontier orders by biased priority */
     int rabitq_verdict; /* 1: backend_rabitq.cu:3873-3894 verdict chain */
+    int inline_exact;   /* enable_true_distance_rerank (backend_pq.cu:4507-4546) */
 } orc_search_params;
 
 typedef struct {
@@ -191,19 +192,26 @@ float orc_rabitq_score_b1(int32_t ip_int, float scale, float k1, float f_add,
 
 /* ---------------- traversal (backend_pq.cu:3980-5013) --------------------- */
 typedef float (*orc_scorer)(void* ctx, uint32_t route, uint32_t sample);
+/* Exact distance of the expanded node (may be NULL when inline_exact = 0). */
+typedef float (*orc_exact)(void* ctx, uint32_t route, uint32_t sample);
 
 int orc_beam_search_route(const orc_graph* g, const orc_predicate* pred,
                           const orc_search_params* p, uint32_t route,
-                          orc_scorer scorer, void* scorer_ctx,
+                          orc_scorer scorer, orc_exact exact, void* scorer_ctx,
                           uint32_t* out_ids, float* out_dists,
                           orc_route_stats* stats);
+/* Inline exact distance in the reference's 32-lane order: partial j sums
+ * 4-element words j, j+32, ... (elements in order), xor butterfly 16..1. */
+float orc_exact_inline_u8(const uint8_t* q, const uint8_t* b, uint32_t dim);
+float orc_exact_inline_f32(const float* q, const float* b, uint32_t dim);
 
 /* Batch drivers: one call runs every route.  Queries are per route
  * (route_query[route] selects the query vector row). */
 int orc_pq_search_batch(const orc_graph* g, const orc_predicate* pred,
                         const orc_search_params* p, const uint8_t* codes,
                         const float* centroids, const void* queries,
-                        int query_is_float, const uint32_t* route_query,
+                        int query_is_float, const void* exact_base,
+                        const uint32_t* route_query,
                         int dim, int pq_dim, uint32_t routes, uint32_t* out_ids,
                         float* out_dists, orc_route_stats* stats);
 

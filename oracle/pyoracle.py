@@ -47,7 +47,7 @@ class Params(C.Structure):
                 ("early_stop_mode", C.c_int), ("max_steps", C.c_int), ("stop_width", C.c_int),
                 ("result_width", C.c_int), ("bit_filter_bonus", C.c_float),
                 ("range_filter_bonus", C.c_float), ("bias", C.c_int),
-                ("rabitq_verdict", C.c_int)]
+                ("rabitq_verdict", C.c_int), ("inline_exact", C.c_int)]
 
 
 class Stats(C.Structure):
@@ -161,9 +161,11 @@ class PredicateArrays:
 
 
 def params(queue_limit=64, result_width=100, early_stop_mode=2, finish_limit=1, max_steps=0,
-           stop_width=10, bias=True, bit_bonus=1.0, range_bonus=1.0, rabitq_verdict=0) -> Params:
+           stop_width=10, bias=True, bit_bonus=1.0, range_bonus=1.0, rabitq_verdict=0,
+           inline_exact=False) -> Params:
     return Params(queue_limit, finish_limit, early_stop_mode, max_steps, stop_width,
-                  result_width, bit_bonus, range_bonus, 1 if bias else 0, rabitq_verdict)
+                  result_width, bit_bonus, range_bonus, 1 if bias else 0, rabitq_verdict,
+                  1 if inline_exact else 0)
 
 
 def graph_struct(index, route_group, route_start):
@@ -176,7 +178,8 @@ def graph_struct(index, route_group, route_start):
     return g, keep
 
 
-def pq_search(index, routes, pred: PredicateArrays, prm: Params, codes, table, queries):
+def pq_search(index, routes, pred: PredicateArrays, prm: Params, codes, table, queries,
+              base=None):
     """Oracle beam search of every route.  Returns ids [R][W] u32,
     dists [R][W] f32, stats structured array."""
     L = lib()
@@ -191,8 +194,9 @@ def pq_search(index, routes, pred: PredicateArrays, prm: Params, codes, table, q
     qf = queries.dtype == np.float32
     q = np.ascontiguousarray(queries)
     rq = c_arr(routes.route_query, np.uint32)
+    b = None if base is None else np.ascontiguousarray(base)
     rc = L.orc_pq_search_batch(C.byref(g), C.byref(pred.struct), C.byref(prm), p(codes),
-                               p(table), p(q), 1 if qf else 0, p(rq), int(table.shape[1]),
+                               p(table), p(q), 1 if qf else 0, p(b), p(rq), int(table.shape[1]),
                                int(codes.shape[1]), n, p(ids), p(dists), stats)
     assert rc == 0
     return ids, dists, stats_array(stats, n)

@@ -96,6 +96,39 @@ def test_pq_search_matches_oracle(gpu_ctx, world, M, mode):
     assert np.array_equal(gst, ost), "per-route counters differ"
 
 
+@pytest.mark.parametrize("W", [10, 40])
+def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W):
+    """Inline exact distances (enable_true_distance_rerank) on resident
+    vectors: identical ids, distance bits and counters."""
+    kind, wl, li, pl = world
+    say("pq_search inline exact", kind, W)
+    table, codes = _pq(wl, 16)
+    rs = pl.graph
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, wl.base_ranges, alpha=0.15,
+                                          pending_base_stop=True)
+    prm_o = po.params(queue_limit=48, result_width=W, inline_exact=True)
+    base = wl.base.numpy()
+    oi, od, ost = po.pq_search(li, rs, pred_o, prm_o, codes.numpy(), table.numpy(),
+                               wl.queries.numpy(), base=base)
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+    keep = (codes.cuda(), table.cuda(), wl.base.cuda())
+    pqv = gs.pq_view(*keep)
+    prm = gs.search_params(queue_limit=48, result_width=W, inline_exact=True)
+    ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, wl.queries.cuda(), dg, dr, prm)
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids).reshape(rs.count, W), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(rs.count, W).view(np.uint32),
+                          od.view(np.uint32))
+    assert np.array_equal(st.cpu().numpy().reshape(rs.count, 8), ost)
+    # results are exact squared distances
+    for r in range(min(rs.count, 8)):
+        q = wl.queries.numpy()[rs.route_query[r]].astype(np.float64)
+        for i, d in zip(oi[r], od[r]):
+            if i != U32MAX:
+                assert abs(((base[i].astype(np.float64) - q) ** 2).sum() - d) <= 1e-5 * max(1.0, d)
+
+
 def test_pq_search_batched_launch_order(gpu_ctx, world):
     """Route sub-ranges and the XCD slot mapping give the same answers."""
     kind, wl, li, pl = world

@@ -149,3 +149,67 @@ def test_oracle_rabitq_full_beam(tiny):
         want = sorted(zip(np.array(est, np.float32).tolist(), cand))[:W]
         got = [(float(a), int(b)) for a, b in zip(dists[r], ids[r]) if b != U32MAX]
         assert sorted(got) == sorted(want)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_inline_exact_full_beam_equals_exact_brute_force(tiny, bias):
+    """Inline exact ranking (backend_pq.cu:4507-4546): the result heap is
+    ordered by the true L2 distance of each expanded passing row.  With the
+    complete-graph group every row but one is expanded, so the W results
+    are the W exactly-nearest passing rows of the group with at most one
+    row left out, and every returned distance is that row's exact L2."""
+    wl, _, table, codes, _ = tiny
+    li = complete_graph_index(wl)
+    rs = gp.plan_queries(li, wl.query_labels).graph
+    W = 8
+    pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15 if bias else 0.0,
+                                        pending_base_stop=bias)
+    prm = po.params(queue_limit=1000, result_width=W, early_stop_mode=1, bias=bias,
+                    inline_exact=True)
+    q = wl.queries.numpy()
+    base = wl.base.numpy()
+    ids, dists, st = po.pq_search(li, rs, pred, prm, codes, table, q, base=base)
+    for r in range(rs.count):
+        label = int(rs.route_group[r])
+        qi = int(rs.route_query[r])
+        rows = li.row_to_sample[li.label_offset[label]:li.label_offset[label] + li.label_size[label]]
+        allowed = gp.filter_mask(li, wl.query_labels[qi], [], None)
+        cand = [int(s) for s in rows if allowed[s]]
+        exact = {s: float(((base[s].astype(np.float64) - q[qi]) ** 2).sum()) for s in cand}
+        got = [(float(d), int(i)) for d, i in zip(dists[r], ids[r]) if i != U32MAX]
+        for d, i in got:
+            assert d == pytest.approx(exact[i], rel=1e-5, abs=1e-4)
+        assert all(got[k][0] <= got[k + 1][0] for k in range(len(got) - 1))
+        ranked = sorted(cand, key=lambda s: (exact[s], s))
+        got_ids = [i for _, i in got]
+        options = [ranked[:W]] + [[s for s in ranked if s != x][:W] for x in ranked[:W]]
+        assert any(sorted(got_ids) == sorted(o) for o in options), r
+        assert st[r, 2] >= len(cand) - 1
+
+
+def test_inline_exact_u8_distances_are_integer_exact():
+    """uint8 inline exact: each lane's squared differences are integers and
+    their float sums stay below 2^24, so every distance is the exact integer
+    squared L2."""
+    wl = synth.small_labelled(n=700, nq=8, dim=48, k=5, sigma=0.8, labels=2, seed=9, tags=True,
+                              dtype="u8")
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=16, threshold=40)
+    table = gi.train_pq(wl.base, 8, iters=6)
+    codes = gi.pq_encode(wl.base, table, 8)
+    rs = gp.plan_queries(li, wl.query_labels).graph
+    pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15, pending_base_stop=True)
+    prm = po.params(queue_limit=64, result_width=10, inline_exact=True)
+    q = wl.queries.numpy()
+    base = wl.base.numpy()
+    ids, dists, _ = po.pq_search(li, rs, pred, prm, codes.numpy(), table.numpy(), q, base=base)
+    n_checked = 0
+    for r in range(rs.count):
+        for d, i in zip(dists[r], ids[r]):
+            if i == U32MAX:
+                continue
+            want = int(((base[i].astype(np.int64) - q[rs.route_query[r]].astype(np.int64)) ** 2)
+                       .sum())
+            assert float(d) == float(want)
+            n_checked += 1
+    assert n_checked > 0
