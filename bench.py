@@ -72,7 +72,7 @@ def build_world(args, torch):
     log(f"PQ M=48 trained+encoded in {time.time() - t0:.1f}s")
     t0 = time.time()
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=64, threshold=2000)
+                              wl.centroids, degree=64, threshold=2000, progress=log)
     log(f"label graphs: {int((li.label_size > 0).sum())} labels, {li.rows} rows, "
         f"degree 64 in {time.time() - t0:.1f}s")
     t0 = time.time()

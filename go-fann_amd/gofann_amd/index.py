@@ -320,8 +320,10 @@ def nearest_centre(x: torch.Tensor, centres: torch.Tensor, chunk: int = 1 << 18)
 
 def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_values: np.ndarray,
                       num_labels: int, centres: torch.Tensor, degree: int,
-                      threshold: int = 2000, bridges: int = 4) -> LabelIndex:
-    """Label-partitioned graphs for labels with more than `threshold` rows."""
+                      threshold: int = 2000, bridges: int = 4, progress=None) -> LabelIndex:
+    """Label-partitioned graphs for labels with more than `threshold` rows.
+    `progress(msg)` (optional) is called about every 30 s of building."""
+    import time
     cat_freq, post_off, post_ids = postings_from_csr(label_offsets, label_values, num_labels)
     graph_labels = np.nonzero(cat_freq > threshold)[0]
     label_size = np.zeros(num_labels, dtype=np.uint32)
@@ -337,7 +339,11 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
     cluster = nearest_centre(base, centres)
     rep_cluster = [np.zeros(0, np.int32)] * num_labels
     rep_row = [np.zeros(0, np.uint32)] * num_labels
-    for l in graph_labels:
+    t_last = time.time()
+    for done, l in enumerate(graph_labels):
+        if progress is not None and time.time() - t_last > 30.0:
+            progress(f"label graphs: {done}/{len(graph_labels)} labels built")
+            t_last = time.time()
         s0, s1 = int(post_off[l]), int(post_off[l + 1])
         samples = post_ids[s0:s1]
         o = int(label_offset[l])
