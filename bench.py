@@ -54,6 +54,12 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-inline-exact", action="store_true",
                     help="rank graph routes by ADC and rerank a 100-wide shortlist instead")
+    ap.add_argument("--table-mode", type=int, default=0,
+                    help="PQ table placement: 0 auto, 1 LDS table, 2 on-demand entries")
+    ap.add_argument("--hash-mode", type=int, default=0,
+                    help="visited hash placement: 0 auto, 1 LDS, 2 global")
+    ap.add_argument("--no-neighbor-samples", action="store_true",
+                    help="gather neighbour sample ids through row_to_sample")
     return ap.parse_args()
 
 
@@ -134,12 +140,15 @@ class Pipeline:
     shortlist that the exact rerank kernel reduces to 10.  inline=False:
     every route emits a 100-wide ADC shortlist, all reranked exactly."""
 
-    def __init__(self, ctx, wl, li, table, codes, pl, torch, inline=True, width=100):
+    def __init__(self, ctx, wl, li, table, codes, pl, torch, inline=True, width=100,
+                 table_mode=0, hash_mode=0, neighbor_samples=True, dg=None):
         from gofann_amd import search as gs
         self.gs, self.torch, self.ctx = gs, torch, ctx
         self.wl, self.pl = wl, pl
         self.inline = inline
-        self.dg = gs.DeviceGraph.upload(li)
+        self.table_mode, self.hash_mode = table_mode, hash_mode
+        self.dg = dg if dg is not None else gs.DeviceGraph.upload(
+            li, neighbor_samples=neighbor_samples)
         self.keep = (codes, table)
         self.pqv = gs.pq_view(codes, table, wl.base if inline else None)
         self.q = wl.queries
@@ -184,7 +193,8 @@ class Pipeline:
     def step(self, Q: int, timed_kernel=False):
         gs = self.gs
         W, GW, ng, npost = self.W, self.GW, self.n_graph, self.n_post
-        prm = gs.search_params(queue_limit=Q, result_width=GW, inline_exact=self.inline)
+        prm = gs.search_params(queue_limit=Q, result_width=GW, inline_exact=self.inline,
+                               table_mode=self.table_mode, hash_mode=self.hash_mode)
         if self.inline:
             g_out = (self.fin_i[: max(ng, 1) * 10], self.fin_d[: max(ng, 1) * 10], self.stats)
         else:
@@ -221,18 +231,23 @@ class Pipeline:
         return self.stats[: self.n_graph * 8].cpu().numpy().reshape(-1, 8)
 
 
-def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes: int) -> float:
-    """Bytes the traversal must move per launch: adjacency row + row_to_sample
-    of each expanded node, code row + row_to_sample of each scored candidate,
-    CSR offsets of each predicate row opened and each label word read, and
-    (inline exact ranking) the base vector of each expanded node that passes."""
+def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes: int,
+                      neighbor_samples: bool) -> float:
+    """Bytes the traversal must move per launch: the adjacency row of each
+    expanded node (plus its neighbour-sample row when the graph carries
+    one), the code row of each scored candidate (plus its row_to_sample
+    word when it does not), CSR offsets of each predicate row opened and
+    each label word read, and (inline exact ranking) the base vector of each
+    expanded node that passes.  Frontier entries carry sample ids, so an
+    expanded node's own row_to_sample word is not read."""
     E = st[:, 1].astype(np.float64).sum()
     Pn = st[:, 2].astype(np.float64).sum()
     V = st[:, 3].astype(np.float64).sum()
     rows = st[:, 4].astype(np.float64).sum()
     labels = st[:, 5].astype(np.float64).sum()
-    return (E * (4 * degree + 4) + V * (code_bytes + 4) + rows * 8 + labels * 4
-            + Pn * exact_bytes)
+    adj = 8 * degree if neighbor_samples else 4 * degree
+    code = code_bytes if neighbor_samples else code_bytes + 4
+    return E * adj + V * code + rows * 8 + labels * 4 + Pn * exact_bytes
 
 
 def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline):
@@ -300,7 +315,9 @@ def main():
     log(f"ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     ctx = _lib.Context(0)
     inline = not args.no_inline_exact
-    pipe = Pipeline(ctx, wl, li, table, codes, pl, torch, inline=inline)
+    pipe = Pipeline(ctx, wl, li, table, codes, pl, torch, inline=inline,
+                    table_mode=args.table_mode, hash_mode=args.hash_mode,
+                    neighbor_samples=not args.no_neighbor_samples)
 
     ladder = [args.queue] if args.queue else [int(x) for x in args.ladder.split(",")]
     chosen, rec = ladder[-1], 0.0
@@ -330,10 +347,13 @@ def main():
     rec = recall_at_10(res, gt)
     st = pipe.route_stats()
     kms = float(np.mean(kernel_ms))
-    abytes = algorithmic_bytes(st, li.degree, 48, wl.dim if inline else 0)
+    abytes = algorithmic_bytes(st, li.degree, 48, wl.dim if inline else 0,
+                               not args.no_neighbor_samples)
     achieved = abytes / (kms / 1000.0) / 1e9
+    placed = ctx.last_placement()
     log(f"step {ms_per_step:.1f} ms, traversal kernel {kms:.1f} ms, recall {rec:.4f}, "
-        f"steps/route {st[:, 0].mean():.1f}, scored/route {st[:, 3].mean():.1f}")
+        f"steps/route {st[:, 0].mean():.1f}, scored/route {st[:, 3].mean():.1f}, "
+        f"admitted/route {st[:, 6].mean():.1f}, placement {placed}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -363,7 +383,8 @@ def main():
                    "graph_ranking": "inline exact u8" if inline else "ADC, shortlist 100",
                    "rerank": "exact u8 on GPU", "seeds": "nearest bucket representative",
                    "recall_at_10": round(rec, 4),
-                   "gt_queries": len(gt)},
+                   "gt_queries": len(gt), "placement": placed,
+                   "neighbor_samples": not args.no_neighbor_samples},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 5),
                      "traffic": None, "kernel": "traversal_kernel<PqScorer<48>>",

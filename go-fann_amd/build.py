@@ -32,9 +32,9 @@ DEVICE = [
 ]
 
 
-def _compile(src: Path) -> Path:
-    obj = OUT_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON]
+def _compile(src: Path, out_dir: Path = OUT_DIR, defines: tuple = ()) -> Path:
+    obj = out_dir / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON, *[f"-D{d}" for d in defines]]
     if src.suffix == ".hip":
         cmd += ["-x", "hip", *DEVICE]
     else:
@@ -54,22 +54,25 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    OUT_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = True, lib: Path = LIB, defines: tuple = ()) -> Path:
+    """Compile every source and link `lib`; `defines` are extra -D macros
+    (e.g. GOFANN_TRAVERSAL_MIN_WAVES=5) for alternative builds."""
+    out_dir = OUT_DIR if not defines else OUT_DIR / "_".join(defines).replace("=", "")
+    out_dir.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     with ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, out_dir, defines), sources))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
            "-o", str(tmp), "-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("link failed")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":

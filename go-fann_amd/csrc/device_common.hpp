@@ -23,11 +23,14 @@ constexpr int kMaxStopWidth = 10;         // backend_pq.cu:72 kTopk
 constexpr int kWave = 64;
 
 // Frontier entry: priority `first`, label-local row | used bit, unbiased
-// score `base` (gpu_predicate::BiasedPair, gpu_predicate_index.cuh:137-144).
+// score `base` (gpu_predicate::BiasedPair, gpu_predicate_index.cuh:137-144)
+// and the row's sample id, carried so that expanding the entry needs no
+// row -> sample lookup (16 B, one ds_read_b128).
 struct Entry {
     float first;
     uint32_t second;
     float base;
+    uint32_t sample;
 };
 
 struct ResultEntry {  // KernelPair<dist_t, uint32_t>
@@ -67,11 +70,19 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask)
 }
 
 // ---------------------------------------------------------------------------
-// Visited hash: native_visited_hash.cuh:10-60 (linear probing, 4096 slots,
-// empty = UINT32_MAX, add drops silently when full).  Two storages share the
-// probe sequence: LDS (when the workgroup budget allows) or a per-route
-// global slab accessed with agent-scope atomics so lanes of one wave observe
-// each other's inserts without L1 staleness.
+// Visited set: native_visited_hash.cuh:10-60.  Observable semantics: an exact
+// set of label-local rows that stops accepting values once it holds 4096 of
+// them (add drops silently when the 4096-slot table is full; test answers
+// membership).  Any exact set with that capacity rule is indistinguishable,
+// so the storage is chosen for residency:
+//   kVisitedLds    the 4096-slot linear-probing table in LDS (16 KiB);
+//   kVisitedGlobal the same table in a per-route global slab (agent-scope
+//                  atomics, so lanes see each other's inserts past L1);
+//   kVisitedSpill  a 1024-slot LDS table (4 KiB) that moves into the global
+//                  table before its load passes 3/4 -- long routes only.
+// Inserts of one step run lane-parallel (compare-and-swap) while the set
+// cannot fill; otherwise lane 0 adds in admission order, reproducing which
+// values the reference drops.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t hash_code(uint32_t value)
 {
@@ -81,52 +92,140 @@ __device__ __forceinline__ uint32_t hash_code(uint32_t value)
     return static_cast<uint32_t>(mixed % kHashCapacity);
 }
 
-template <bool kLds>
-struct VisitedHash {
+constexpr int kVisitedGlobal = 0;
+constexpr int kVisitedLds = 1;
+constexpr int kVisitedSpill = 2;
+constexpr uint32_t kSpillSlots = 1024;
+constexpr uint32_t kSpillLimit = kSpillSlots * 3 / 4;
+
+// Linear-probing table over `cap` slots (a power of two dividing 4096).
+template <bool kShared>
+struct ProbeTable {
     uint32_t* slots;
+    uint32_t cap;
 
     __device__ __forceinline__ uint32_t load(uint32_t i) const
     {
-        if constexpr (kLds) return slots[i];
+        if constexpr (kShared) return slots[i];
         return __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __device__ __forceinline__ void store(uint32_t i, uint32_t v) const
     {
-        if constexpr (kLds) {
+        if constexpr (kShared) {
             slots[i] = v;
         } else {
             __hip_atomic_store(slots + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    // All lanes: fill every slot with UINT32_MAX.
     __device__ void clear(int lane) const
     {
         uint4* p = reinterpret_cast<uint4*>(slots);
         const uint4 empty = make_uint4(UINT32_MAX, UINT32_MAX, UINT32_MAX, UINT32_MAX);
-        for (uint32_t i = lane; i < kHashCapacity / 4; i += kWave) p[i] = empty;
+        for (uint32_t i = lane; i < cap / 4; i += kWave) p[i] = empty;
     }
     __device__ bool test(uint32_t value) const
     {
-        uint32_t slot = hash_code(value);
-        for (uint32_t probes = 0; probes < kHashCapacity; ++probes) {
+        uint32_t slot = hash_code(value) & (cap - 1);
+        for (uint32_t probes = 0; probes < cap; ++probes) {
             const uint32_t v = load(slot);
             if (v == UINT32_MAX) return false;
             if (v == value) return true;
-            slot = (slot + 1) % kHashCapacity;
+            slot = (slot + 1) & (cap - 1);
         }
         return false;
     }
-    __device__ void add(uint32_t value) const
+    // Serial insert: 1 when stored, 0 when present or the table is full.
+    __device__ int add(uint32_t value) const
     {
-        uint32_t slot = hash_code(value);
-        for (uint32_t probes = 0; probes < kHashCapacity; ++probes) {
+        uint32_t slot = hash_code(value) & (cap - 1);
+        for (uint32_t probes = 0; probes < cap; ++probes) {
             const uint32_t v = load(slot);
-            if (v == value) return;
+            if (v == value) return 0;
             if (v == UINT32_MAX) {
                 store(slot, value);
-                return;
+                return 1;
             }
-            slot = (slot + 1) % kHashCapacity;
+            slot = (slot + 1) & (cap - 1);
+        }
+        return 0;
+    }
+    // Lane-parallel insert; the caller guarantees a free slot for every
+    // inserting lane.  1 when this lane stored the value.
+    __device__ int add_parallel(uint32_t value) const
+    {
+        uint32_t slot = hash_code(value) & (cap - 1);
+        for (uint32_t probes = 0; probes < cap; ++probes) {
+            uint32_t expected = UINT32_MAX;
+            if constexpr (kShared) {
+                expected = atomicCAS(slots + slot, UINT32_MAX, value);
+            } else {
+                __hip_atomic_compare_exchange_strong(slots + slot, &expected, value,
+                                                     __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (expected == UINT32_MAX) return 1;
+            if (expected == value) return 0;
+            slot = (slot + 1) & (cap - 1);
+        }
+        return 0;
+    }
+};
+
+template <int kMode>
+struct VisitedSet {
+    ProbeTable<true> shared;    // LDS table (kVisitedLds, kVisitedSpill)
+    ProbeTable<false> global;   // global slab of 4096 slots
+    uint32_t count;             // values held (wave-uniform)
+    bool spilled;               // kVisitedSpill: moved to the global slab
+
+    __device__ void init(uint32_t* lds_slots, uint32_t* global_slots, int lane)
+    {
+        shared = {lds_slots, kMode == kVisitedSpill ? kSpillSlots : kHashCapacity};
+        global = {global_slots, kHashCapacity};
+        count = 0;
+        spilled = false;
+        if constexpr (kMode == kVisitedGlobal) {
+            global.clear(lane);
+        } else {
+            shared.clear(lane);
+        }
+    }
+    __device__ __forceinline__ bool in_global() const
+    {
+        return kMode == kVisitedGlobal || (kMode == kVisitedSpill && spilled);
+    }
+    __device__ bool test(uint32_t value) const
+    {
+        return in_global() ? global.test(value) : shared.test(value);
+    }
+    // Lane 0 only; the caller broadcasts the result into `count`.  A full
+    // set ignores adds (the probe would find neither the value's slot nor
+    // an empty one), so `added` tracks the values stored by this batch.
+    __device__ int add_serial(uint32_t value, uint32_t added) const
+    {
+        if (count + added >= kHashCapacity) return 0;
+        return in_global() ? global.add(value) : shared.add(value);
+    }
+    __device__ int add_parallel(uint32_t value) const
+    {
+        return in_global() ? global.add_parallel(value) : shared.add_parallel(value);
+    }
+    // All lanes, before inserting `incoming` more values: move the small LDS
+    // table into the global slab when it would pass its load limit.
+    __device__ void reserve(uint32_t incoming, int lane)
+    {
+        if constexpr (kMode == kVisitedSpill) {
+            if (spilled || count + incoming <= kSpillLimit) return;
+            global.clear(lane);
+            __threadfence();
+            __syncthreads();
+            for (uint32_t i = lane; i < kSpillSlots; i += kWave) {
+                const uint32_t v = shared.slots[i];
+                if (v != UINT32_MAX) (void)global.add_parallel(v);
+            }
+            __threadfence();
+            __syncthreads();
+            spilled = true;
         }
     }
 };
@@ -178,7 +277,7 @@ __device__ __forceinline__ int smmh_adjust_grandparent(Entry* h, int y)
     return y;
 }
 
-__device__ void smmh_insert(Entry* h, int& size, const Entry& e)
+__device__ __forceinline__ void smmh_insert(Entry* h, int& size, const Entry& e)
 {
     int y = size;
     h[size++] = e;
@@ -216,7 +315,7 @@ __device__ __forceinline__ int smmh_adjust_grandchild(Entry* h, int y, int size)
     return y;
 }
 
-__device__ void smmh_pop_max(Entry* h, int& size)
+__device__ __forceinline__ void smmh_pop_max(Entry* h, int& size)
 {
     h[2] = h[--size];
     int y = 2;
@@ -234,7 +333,7 @@ __device__ void smmh_pop_max(Entry* h, int& size)
 // storing the root at the tail).
 // ---------------------------------------------------------------------------
 template <class T>
-__device__ void bin_push(T* h, int size)
+__device__ __forceinline__ void bin_push(T* h, int size)
 {
     int now = size - 1;
     int parent = (now - 1) / 2;
@@ -248,7 +347,7 @@ __device__ void bin_push(T* h, int size)
 }
 
 template <class T>
-__device__ T bin_pop(T* h, int size)
+__device__ __forceinline__ T bin_pop(T* h, int size)
 {
     const T ret = h[0];
     const int len = size - 1;
@@ -349,7 +448,7 @@ __device__ __forceinline__ bool pred_contains(const gofann_predicate_view& v, ui
     return false;
 }
 
-__device__ bool pred_matches(const gofann_predicate_view& v, uint32_t route, uint32_t sample,
+__device__ __forceinline__ bool pred_matches(const gofann_predicate_view& v, uint32_t route, uint32_t sample,
                              PredCounters& c)
 {
     if (sample >= v.rows) return false;
@@ -372,6 +471,160 @@ __device__ bool pred_matches(const gofann_predicate_view& v, uint32_t route, uin
     }
     for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i)
         if (!pred_contains(v, v.route_handles[i], sample, c)) return false;
+    return true;
+}
+
+// One sample's CSR label row held across the wave: lane k holds label
+// begin+k of the first 64 (UINT32_MAX past the end).  Loaded once per
+// expanded node; every handle test of the route's clauses reads it.
+struct WaveRow {
+    uint32_t begin, end;  // wave-uniform bounds
+    uint32_t lab;         // this lane's label of the first chunk
+    bool valid;           // sample < rows and CSR present
+};
+
+__device__ __forceinline__ WaveRow wave_row_load(const gofann_predicate_view& v, uint32_t sample,
+                                                 uint32_t begin, uint32_t end, int lane)
+{
+    WaveRow r;
+    r.valid = sample < v.rows && v.csr_offsets != nullptr;
+    r.begin = begin;
+    r.end = r.valid ? end : begin;
+    const uint32_t len = r.end - r.begin;
+    r.lab = static_cast<uint32_t>(lane) < len ? v.csr_labels[r.begin + lane] : UINT32_MAX;
+    return r;
+}
+
+// Wave-uniform csr_contains_sorted (gpu_predicate_index.cuh:58-78) over a
+// WaveRow: the first label >= handle decides, and the number of labels the
+// serial scan would have read is counted exactly.
+__device__ __forceinline__ bool wave_row_contains(const gofann_predicate_view& v, const WaveRow& r,
+                                  uint32_t handle, int lane, PredCounters& c)
+{
+    if (!r.valid) return false;
+    ++c.rows;
+    const uint32_t len = r.end - r.begin;
+    for (uint32_t base = 0; base < len; base += kWave) {
+        const uint32_t k = base + static_cast<uint32_t>(lane);
+        const uint32_t lab = base == 0 ? r.lab : (k < len ? v.csr_labels[r.begin + k] : UINT32_MAX);
+        const uint64_t ge = ballot(k < len && lab >= handle);
+        if (ge) {
+            const int f = __builtin_ctzll(ge);
+            c.labels += base + static_cast<uint32_t>(f) + 1u;
+            return static_cast<uint32_t>(__shfl(static_cast<int>(lab), f, kWave)) == handle;
+        }
+    }
+    c.labels += len;
+    return false;
+}
+
+// pred_matches for a wave-uniform sample whose row is held in a WaveRow.
+__device__ __forceinline__ bool wave_pred_matches(const gofann_predicate_view& v, uint32_t route, uint32_t sample,
+                                  const WaveRow& row, int lane, PredCounters& c)
+{
+    if (sample >= v.rows) return false;
+    if (v.clauses) {
+        for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i) {
+            const gofann_clause cl = v.clauses[i];
+            bool pass = true;
+            for (uint32_t j = cl.label_begin; pass && j < cl.label_end; ++j)
+                pass = wave_row_contains(v, row, v.route_handles[j], lane, c);
+            for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
+                const gofann_range_atom a = v.ranges[j];
+                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                       range_matches(a.mode, a.lower, a.upper,
+                                     v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
+                                                   a.dimension]);
+            }
+            if (pass) return true;
+        }
+        return false;
+    }
+    for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i)
+        if (!wave_row_contains(v, row, v.route_handles[i], lane, c)) return false;
+    return true;
+}
+
+// Per-lane pred_matches with the row's first labels loaded up front (one
+// round of independent loads instead of a dependent chain); the serial
+// decision order and the counters are those of pred_contains.
+constexpr int kLaneRowBatch = 8;
+
+struct LaneRow {
+    uint32_t begin, end;
+    uint32_t lab[kLaneRowBatch];  // UINT32_MAX past the end; constant-indexed only
+};
+
+__device__ __forceinline__ bool lane_row_contains(const gofann_predicate_view& v, const LaneRow& r,
+                                                  uint32_t handle, PredCounters& c)
+{
+    ++c.rows;
+    const uint32_t len = r.end - r.begin;
+    // First batch position whose label is >= handle (the serial scan stops
+    // there), found with constant indices so the batch stays in registers.
+    uint32_t hit = static_cast<uint32_t>(kLaneRowBatch);
+    bool eq = false;
+#pragma unroll
+    for (int k = 0; k < kLaneRowBatch; ++k) {
+        const bool stop = hit == static_cast<uint32_t>(kLaneRowBatch) &&
+                          static_cast<uint32_t>(k) < len && r.lab[k] >= handle;
+        if (stop) {
+            hit = static_cast<uint32_t>(k);
+            eq = r.lab[k] == handle;
+        }
+    }
+    if (hit < static_cast<uint32_t>(kLaneRowBatch)) {
+        c.labels += hit + 1u;
+        return eq;
+    }
+    if (len <= static_cast<uint32_t>(kLaneRowBatch)) {
+        c.labels += len;
+        return false;
+    }
+    c.labels += static_cast<uint32_t>(kLaneRowBatch);
+    for (uint32_t i = r.begin + kLaneRowBatch; i < r.end; ++i) {
+        const uint32_t label = v.csr_labels[i];
+        ++c.labels;
+        if (label >= handle) return label == handle;
+    }
+    return false;
+}
+
+__device__ __forceinline__ bool lane_pred_matches(const gofann_predicate_view& v, uint32_t route,
+                                                  uint32_t sample, PredCounters& c)
+{
+    if (sample >= v.rows || v.csr_offsets == nullptr) return pred_matches(v, route, sample, c);
+    LaneRow r;
+    r.begin = v.csr_offsets[sample];
+    r.end = v.csr_offsets[sample + 1];
+    const uint32_t last = r.end > r.begin ? r.end - 1 : r.begin;
+#pragma unroll
+    for (int k = 0; k < kLaneRowBatch; ++k) {
+        // Clamped address: every load is in bounds, so the batch issues as
+        // independent loads; entries past the end are masked afterwards.
+        const uint32_t i = r.begin + static_cast<uint32_t>(k) < last ? r.begin + k : last;
+        const uint32_t x = r.end > r.begin ? v.csr_labels[i] : UINT32_MAX;
+        r.lab[k] = r.begin + static_cast<uint32_t>(k) < r.end ? x : UINT32_MAX;
+    }
+    if (v.clauses) {
+        for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i) {
+            const gofann_clause cl = v.clauses[i];
+            bool pass = true;
+            for (uint32_t j = cl.label_begin; pass && j < cl.label_end; ++j)
+                pass = lane_row_contains(v, r, v.route_handles[j], c);
+            for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
+                const gofann_range_atom a = v.ranges[j];
+                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                       range_matches(a.mode, a.lower, a.upper,
+                                     v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
+                                                   a.dimension]);
+            }
+            if (pass) return true;
+        }
+        return false;
+    }
+    for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i)
+        if (!lane_row_contains(v, r, v.route_handles[i], c)) return false;
     return true;
 }
 

@@ -124,6 +124,18 @@ int gofann_device_info(gofann_ctx* c, int* compute_units, int* lds_bytes)
     });
 }
 
+int gofann_last_placement(gofann_ctx* c, int* table_in_lds, int* hash_in_lds, int* lds_bytes,
+                          int* resident_per_cu)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (table_in_lds) *table_in_lds = ctx->last_table_in_lds;
+        if (hash_in_lds) *hash_in_lds = ctx->last_hash_in_lds;
+        if (lds_bytes) *lds_bytes = ctx->last_lds_bytes;
+        if (resident_per_cu) *resident_per_cu = ctx->last_resident;
+        return GOFANN_OK;
+    });
+}
+
 int gofann_pq_search(gofann_ctx* c, const gofann_pq_view* pq, const void* queries, int query_elem,
                      const gofann_graph_view* graph, const gofann_predicate_view* predicate,
                      const gofann_routes* routes, const gofann_search_params* params,

@@ -26,8 +26,11 @@ struct Context {
     std::string error;
     void* scratch_ptr[kScratchCount] = {nullptr, nullptr, nullptr};
     size_t scratch_bytes[kScratchCount] = {0, 0, 0};
+    // Placement chosen by the last traversal launch (diagnostics).
     int last_hash_in_lds = 0;
+    int last_table_in_lds = 0;
     int last_lds_bytes = 0;
+    int last_resident = 0;
 
     int fail(int code, const std::string& msg)
     {

@@ -1,0 +1,8 @@
+// pq_search_m32.hip -- PQ traversal kernels for pq_dim = 32 (instantiated here
+// so the kernel variants compile in parallel).
+#include "traversal.hpp"
+
+namespace gofann {
+template int pq_search_m<32>(GOFANN_PQ_SEARCH_M_ARGS);
+
+}  // namespace gofann

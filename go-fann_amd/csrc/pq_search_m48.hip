@@ -1,0 +1,8 @@
+// pq_search_m48.hip -- PQ traversal kernels for pq_dim = 48 (instantiated here
+// so the kernel variants compile in parallel).
+#include "traversal.hpp"
+
+namespace gofann {
+template int pq_search_m<48>(GOFANN_PQ_SEARCH_M_ARGS);
+
+}  // namespace gofann

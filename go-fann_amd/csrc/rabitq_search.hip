@@ -1,0 +1,96 @@
+// rabitq_search.hip -- RaBitQ graph search entry and batched RaBitQ scoring.
+#include "traversal.hpp"
+
+namespace gofann {
+__global__ __launch_bounds__(64) void rabitq_score_kernel(RabitqScorer sc, const uint32_t* q_idx,
+                                                         const uint32_t* s_idx, uint32_t n,
+                                                         float* out, int32_t* ip_out)
+{
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int lane = static_cast<int>(threadIdx.x);
+    const uint32_t i = blockIdx.x * kWave + lane;
+    const uint32_t first = blockIdx.x * kWave;
+    const uint32_t last = first + kWave < n ? first + kWave : n;
+    for (uint32_t j = first; j < last; ++j) {
+        const uint32_t qj = q_idx[j];
+        if (j > first && q_idx[j - 1] == qj) continue;
+        __syncthreads();
+        sc.setup(qj, lane, lds);
+        __syncthreads();
+        const bool mine = i < n && q_idx[i] == qj;
+        if (mine) {
+            out[i] = sc.score(s_idx[i], true);
+            if (ip_out) ip_out[i] = sc.ip_int(s_idx[i]);
+        }
+    }
+}
+
+
+namespace {
+
+RabitqScorer make_rabitq_scorer(const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre)
+{
+    RabitqScorer sc;
+    sc.codes = rq->codes;
+    sc.factors = rq->factors;
+    sc.anchor_ids = rq->anchor_ids;
+    sc.q8 = pre->q8;
+    sc.q_scale = pre->scale;
+    sc.q_k1 = pre->k1;
+    sc.centroid_dists = pre->centroid_dists;
+    sc.num_anchors = rq->num_anchors;
+    sc.padded_dim = rq->padded_dim;
+    sc.planes = nullptr;
+    sc.scale = 0.0f;
+    sc.k1 = 0.0f;
+    sc.g_row = nullptr;
+    return sc;
+}
+
+int check_rabitq(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre)
+{
+    if (!rq || !pre || !rq->codes || !rq->factors || !rq->anchor_ids || !pre->q8 || !pre->scale ||
+        !pre->k1 || !pre->centroid_dists)
+        return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view incomplete");
+    if (rq->padded_dim == 0 || rq->padded_dim % 128 != 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "padded_dim must be a positive multiple of 128");
+    return GOFANN_OK;
+}
+
+}  // namespace
+
+int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre,
+                  const gofann_graph_view* g, const gofann_predicate_view* pred,
+                  const gofann_routes* r, const gofann_search_params* p, uint32_t* out_ids,
+                  float* out_dists, gofann_route_stats* stats)
+{
+    int rc = check_rabitq(ctx, rq, pre);
+    if (rc) return rc;
+    rc = check_params(ctx, g, r, p);
+    if (rc) return rc;
+    if (p->inline_exact_rerank)
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "RaBitQ traversal has no inline exact rerank");
+    if (r->count == 0) return GOFANN_OK;
+    const uint32_t plane_bytes = rq->padded_dim;  // 8 planes x padded_dim bits
+    const Layout l = make_layout(plane_bytes, p->queue_limit, p->result_width);
+    const Placement pl = choose_visited<RabitqScorer>(ctx, l, p->hash_mode);
+    ctx->last_table_in_lds = 1;
+    return launch_traversal(ctx, make_rabitq_scorer(rq, pre), l, pl, g, pred, r, p, out_ids,
+                            out_dists, stats, 1);
+}
+
+int rabitq_score(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre,
+                 const uint32_t* q_idx, const uint32_t* s_idx, uint32_t n, float* out,
+                 int32_t* ip_int)
+{
+    int rc = check_rabitq(ctx, rq, pre);
+    if (rc) return rc;
+    if (n == 0) return GOFANN_OK;
+    const dim3 grid((n + kWave - 1) / kWave), block(kWave);
+    hipLaunchKernelGGL(rabitq_score_kernel, grid, block, rq->padded_dim, ctx->stream,
+                       make_rabitq_scorer(rq, pre), q_idx, s_idx, n, out, ip_int);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("rabitq_score launch");
+    return GOFANN_OK;
+}
+
+}  // namespace gofann

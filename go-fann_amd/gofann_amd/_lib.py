@@ -12,11 +12,13 @@ import os
 from pathlib import Path
 
 _HERE = Path(__file__).resolve().parent
-LIB_PATH = _HERE.parent / "libgofann_hip.so"
+# GOFANN_HIP_LIB may name an alternative build of the same library.
+LIB_PATH = Path(os.environ.get("GOFANN_HIP_LIB", str(_HERE.parent / "libgofann_hip.so")))
 
 GOFANN_OK = 0
 EARLY_STOP_FIXED, EARLY_STOP_OFF, EARLY_STOP_ADAPTIVE = 0, 1, 2
 ELEM_U8, ELEM_F32, ELEM_F16 = 0, 1, 2
+PLACE_AUTO, PLACE_LDS, PLACE_GLOBAL, PLACE_SPILL = 0, 1, 2, 3
 
 P = C.c_void_p
 U32 = C.c_uint32
@@ -24,7 +26,8 @@ U32 = C.c_uint32
 
 class GraphView(C.Structure):
     _fields_ = [("graph", P), ("row_to_sample", P), ("label_offset", P),
-                ("rows", U32), ("degree", U32), ("groups", U32), ("samples", U32)]
+                ("rows", U32), ("degree", U32), ("groups", U32), ("samples", U32),
+                ("neighbor_samples", P)]
 
 
 class Clause(C.Structure):
@@ -57,7 +60,8 @@ class SearchParams(C.Structure):
                 ("early_stop_mode", C.c_int), ("max_steps", C.c_int),
                 ("stop_width", C.c_int), ("result_width", C.c_int),
                 ("bit_filter_bonus", C.c_float), ("range_filter_bonus", C.c_float),
-                ("predicate_bias", C.c_int), ("inline_exact_rerank", C.c_int)]
+                ("predicate_bias", C.c_int), ("inline_exact_rerank", C.c_int),
+                ("table_mode", C.c_int), ("hash_mode", C.c_int)]
 
 
 class RouteStats(C.Structure):
@@ -93,6 +97,8 @@ SIGNATURES = {
     "gofann_set_stream": (C.c_int, [P, P]),
     "gofann_synchronize": (C.c_int, [P]),
     "gofann_device_info": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "gofann_last_placement": (C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                        C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "gofann_pq_search": (C.c_int, [P, C.POINTER(PqView), P, C.c_int, C.POINTER(GraphView),
                                    C.POINTER(PredicateView), C.POINTER(Routes),
                                    C.POINTER(SearchParams), P, P, P]),
@@ -176,6 +182,13 @@ class Context:
         cu, lds = C.c_int(), C.c_int()
         self.check(self.lib.gofann_device_info(self.handle, C.byref(cu), C.byref(lds)))
         return cu.value, lds.value
+
+    def last_placement(self) -> dict:
+        """Placement chosen by the last traversal launch."""
+        v = [C.c_int() for _ in range(4)]
+        self.check(self.lib.gofann_last_placement(self.handle, *[C.byref(x) for x in v]))
+        return dict(table_in_lds=v[0].value, hash_in_lds=v[1].value, lds_bytes=v[2].value,
+                    resident_per_cu=v[3].value)
 
     def close(self) -> None:
         if getattr(self, "handle", None):

@@ -55,19 +55,48 @@ class DeviceGraph:
     degree: int
     groups: int
     samples: int
+    # [rows][degree] sample id of every adjacency entry (optional)
+    neighbor_samples: torch.Tensor | None = None
 
     @classmethod
-    def upload(cls, index) -> "DeviceGraph":
+    def upload(cls, index, neighbor_samples: bool = False) -> "DeviceGraph":
         g = index.graph if index.rows > 0 else np.full((1, index.degree), 0xFFFFFFFF, np.uint32)
         r2s = index.row_to_sample if index.rows > 0 else np.zeros(1, np.uint32)
-        return cls(u32(g.reshape(-1)), u32(r2s), u32(index.label_offset), u32(index.csr_offsets),
-                   u32(index.csr_labels), u32(index.posting_ids), index.rows, index.degree,
-                   index.num_labels, int(index.csr_offsets.shape[0] - 1))
+        dg = cls(u32(g.reshape(-1)), u32(r2s), u32(index.label_offset), u32(index.csr_offsets),
+                 u32(index.csr_labels), u32(index.posting_ids), index.rows, index.degree,
+                 index.num_labels, int(index.csr_offsets.shape[0] - 1))
+        if neighbor_samples:
+            dg.neighbor_samples = neighbor_sample_table(dg, index)
+        return dg
 
     def view(self) -> GraphView:
         return GraphView(_lib.ptr(self.graph), _lib.ptr(self.row_to_sample),
                          _lib.ptr(self.label_offset), self.rows, self.degree, self.groups,
-                         self.samples)
+                         self.samples, _lib.ptr(self.neighbor_samples))
+
+
+def neighbor_sample_table(dg: "DeviceGraph", index) -> torch.Tensor:
+    """row_to_sample[label_offset[g] + graph[r][j]] for every row r of group
+    g (0 where the slot is empty; the kernel never reads those), built on the
+    device one group at a time."""
+    out = torch.zeros_like(dg.graph)
+    if index.rows == 0:
+        return out
+    deg = index.degree
+    g2 = dg.graph.view(-1, deg)
+    o2 = out.view(-1, deg)
+    r2s = dg.row_to_sample.long() & 0xFFFFFFFF
+    for grp in np.nonzero(index.label_size)[0]:
+        lo = int(index.label_offset[grp])
+        hi = lo + int(index.label_size[grp])
+        step = 1 << 20
+        for a in range(lo, hi, step):
+            b = min(hi, a + step)
+            adj = g2[a:b].long() & 0xFFFFFFFF
+            valid = adj != 0xFFFFFFFF
+            idx = torch.where(valid, adj + lo, torch.zeros_like(adj))
+            o2[a:b] = torch.where(valid, r2s[idx], torch.zeros_like(adj)).to(torch.int32)
+    return out
 
 
 @dataclass
@@ -124,10 +153,11 @@ class DeviceRoutes:
 
 def search_params(queue_limit=64, result_width=100, early_stop_mode=_lib.EARLY_STOP_ADAPTIVE,
                   finish_limit=1, max_steps=0, stop_width=10, bias=True,
-                  bit_bonus=1.0, range_bonus=1.0, inline_exact=False) -> SearchParams:
+                  bit_bonus=1.0, range_bonus=1.0, inline_exact=False,
+                  table_mode=_lib.PLACE_AUTO, hash_mode=_lib.PLACE_AUTO) -> SearchParams:
     return SearchParams(queue_limit, finish_limit, early_stop_mode, max_steps, stop_width,
                         result_width, bit_bonus, range_bonus, 1 if bias else 0,
-                        1 if inline_exact else 0)
+                        1 if inline_exact else 0, table_mode, hash_mode)
 
 
 def pq_view(codes: torch.Tensor, table: torch.Tensor, exact_base: torch.Tensor | None = None

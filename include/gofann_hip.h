@@ -52,6 +52,11 @@ extern "C" {
 #define GOFANN_ELEM_F32 1
 #define GOFANN_ELEM_F16 2
 
+#define GOFANN_PLACE_AUTO 0
+#define GOFANN_PLACE_LDS 1
+#define GOFANN_PLACE_GLOBAL 2
+#define GOFANN_PLACE_SPILL 3 /* visited set: 1024-slot LDS table moved to the global slab when 3/4 full */
+
 typedef struct gofann_ctx gofann_ctx;
 
 /* ---- context (replaces init_graph_context / cleanup, backend_pq.cu:6753) */
@@ -63,6 +68,12 @@ int gofann_set_stream(gofann_ctx* ctx, void* hip_stream);
 int gofann_synchronize(gofann_ctx* ctx);
 /* Number of the device's compute units and its LDS per workgroup. */
 int gofann_device_info(gofann_ctx* ctx, int* compute_units, int* lds_bytes);
+/* Placement the last traversal launch chose (no reference counterpart;
+ * diagnostics): ADC table in LDS (1) or on demand (0); visited set global
+ * (0), LDS (1) or spilling LDS (2); dynamic LDS bytes per route; resident
+ * routes per CU.  Any pointer may be NULL. */
+int gofann_last_placement(gofann_ctx* ctx, int* table_in_lds, int* hash_in_lds, int* lds_bytes,
+                          int* resident_per_cu);
 
 /* ---- device arrays -------------------------------------------------------
  * Label-partitioned graph (GraphMetadata + resident graph, src/data/
@@ -77,6 +88,12 @@ typedef struct {
     uint32_t degree;                /* row stride; at most 64 are read */
     uint32_t groups;
     uint32_t samples;
+    /* Optional [rows][degree] sample id of each adjacency entry
+     * (row_to_sample[label_offset + graph[r][j]]; the reference ships the
+     * same "neighbor samples" words in its graph-row payload,
+     * src/execution/async_io.cpp:1025-1047).  NULL: gathered through
+     * row_to_sample.  Results are identical either way. */
+    const uint32_t* neighbor_samples;
 } gofann_graph_view;
 
 /* Device predicate (gpu_predicate::View, src/predicates/
@@ -138,6 +155,16 @@ typedef struct {
      * result/stop heaps (enable_true_distance_rerank, backend_pq.cu:
      * 4507-4546, 4566-4572); needs gofann_pq_view.exact_base. */
     int inline_exact_rerank;
+    /* Placement of per-route state; results are identical in every mode.
+     * table_mode (PQ): 0 auto, 1 ADC table in LDS (computePQTable layout,
+     * M x 256 fp32), 2 table entries computed on demand from the
+     * L2-resident centroid table (same fma chain, so the same bits).
+     * hash_mode (visited set): 0 auto, 1 the 4096-slot table in LDS, 2 the
+     * same table in a per-route global slab, 3 a 1024-slot LDS table moved
+     * into the global slab before it passes 3/4 load.
+     * Auto picks the placement with the most resident routes per CU. */
+    int table_mode;
+    int hash_mode;
 } gofann_search_params;
 
 /* Per-route counters emitted by the traversal kernels (bytes model). */

@@ -56,13 +56,28 @@ def _pq(wl, M):
     return table, codes
 
 
+# Placements of the per-route state: (ADC table, visited hash, neighbour
+# sample table).  Every placement must give the oracle's bits.
+PLACEMENTS = {
+    "auto": (_lib.PLACE_AUTO, _lib.PLACE_AUTO, False),
+    "lds-lds-nsamp": (_lib.PLACE_LDS, _lib.PLACE_LDS, True),
+    "direct-global-nsamp": (_lib.PLACE_GLOBAL, _lib.PLACE_GLOBAL, True),
+    "direct-lds": (_lib.PLACE_GLOBAL, _lib.PLACE_LDS, False),
+    "direct-spill-nsamp": (_lib.PLACE_GLOBAL, _lib.PLACE_SPILL, True),
+    "lds-spill": (_lib.PLACE_LDS, _lib.PLACE_SPILL, False),
+}
+HASH_CODE = {_lib.PLACE_GLOBAL: 0, _lib.PLACE_LDS: 1, _lib.PLACE_SPILL: 2}
+
+
+@pytest.mark.parametrize("place", list(PLACEMENTS))
 @pytest.mark.parametrize("M", [16, 32, 48])
 @pytest.mark.parametrize("mode", ["adaptive-bias", "off", "fixed-nobias"])
-def test_pq_search_matches_oracle(gpu_ctx, world, M, mode):
+def test_pq_search_matches_oracle(gpu_ctx, world, M, mode, place):
     kind, wl, li, pl = world
     if wl.dim % M:
         pytest.skip("pq_dim must divide dim")
-    say("pq_search", kind, M, mode)
+    table_mode, hash_mode, nsamp = PLACEMENTS[place]
+    say("pq_search", kind, M, mode, place)
     table, codes = _pq(wl, M)
     rs = pl.graph
     bias = mode == "adaptive-bias"
@@ -76,32 +91,37 @@ def test_pq_search_matches_oracle(gpu_ctx, world, M, mode):
     q = wl.queries.numpy()
     oi, od, ost = po.pq_search(li, rs, pred_o, prm_o, codes.numpy(), table.numpy(), q)
 
-    dg = gs.DeviceGraph.upload(li)
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
     dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
-    pqv = gs.pq_view(codes.cuda(), table.cuda())
     keep = (codes.cuda(), table.cuda())
     pqv = gs.pq_view(*keep)
     qd = wl.queries.cuda()
     prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=es, finish_limit=3,
-                           max_steps=maxs, bias=bias)
+                           max_steps=maxs, bias=bias, table_mode=table_mode, hash_mode=hash_mode)
     ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, qd, dg, dr, prm,
                                       alpha=0.15 if bias else 0.0, pending_base_stop=bias)
     torch.cuda.synchronize()
     gi_ = as_u32(ids).reshape(rs.count, W)
     gd = dists.cpu().numpy().reshape(rs.count, W)
     gst = st.cpu().numpy().reshape(rs.count, 8)
-    say("routes", rs.count, "hash_in_lds", gpu_ctx.lib and "n/a")
+    placed = gpu_ctx.last_placement()
+    say("routes", rs.count, placed)
+    if table_mode != _lib.PLACE_AUTO:
+        assert placed["table_in_lds"] == (1 if table_mode == _lib.PLACE_LDS else 0)
+        assert placed["hash_in_lds"] == HASH_CODE[hash_mode]
     assert np.array_equal(gi_, oi), "route ids differ"
     assert np.array_equal(gd.view(np.uint32), od.view(np.uint32)), "distances differ in bits"
     assert np.array_equal(gst, ost), "per-route counters differ"
 
 
+@pytest.mark.parametrize("place", list(PLACEMENTS))
 @pytest.mark.parametrize("W", [10, 40])
-def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W):
+def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W, place):
     """Inline exact distances (enable_true_distance_rerank) on resident
     vectors: identical ids, distance bits and counters."""
     kind, wl, li, pl = world
-    say("pq_search inline exact", kind, W)
+    table_mode, hash_mode, nsamp = PLACEMENTS[place]
+    say("pq_search inline exact", kind, W, place)
     table, codes = _pq(wl, 16)
     rs = pl.graph
     pred_o = po.PredicateArrays.from_plan(rs.predicate, li, wl.base_ranges, alpha=0.15,
@@ -110,11 +130,12 @@ def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W):
     base = wl.base.numpy()
     oi, od, ost = po.pq_search(li, rs, pred_o, prm_o, codes.numpy(), table.numpy(),
                                wl.queries.numpy(), base=base)
-    dg = gs.DeviceGraph.upload(li)
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
     dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
     keep = (codes.cuda(), table.cuda(), wl.base.cuda())
     pqv = gs.pq_view(*keep)
-    prm = gs.search_params(queue_limit=48, result_width=W, inline_exact=True)
+    prm = gs.search_params(queue_limit=48, result_width=W, inline_exact=True,
+                           table_mode=table_mode, hash_mode=hash_mode)
     ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, wl.queries.cuda(), dg, dr, prm)
     torch.cuda.synchronize()
     assert np.array_equal(as_u32(ids).reshape(rs.count, W), oi)
@@ -127,6 +148,48 @@ def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W):
         for i, d in zip(oi[r], od[r]):
             if i != U32MAX:
                 assert abs(((base[i].astype(np.float64) - q) ** 2).sum() - d) <= 1e-5 * max(1.0, d)
+
+
+@pytest.fixture(scope="module")
+def long_world():
+    """One 12k-row label graph, degree 64, and PQ codes that are all zero:
+    every candidate ties, so a beam without early stop admits far more than
+    the visited set's 4096 values (it fills and drops), and the spilling
+    LDS table moves to its global slab early."""
+    wl = synth.small_labelled(n=12000, nq=6, dim=32, k=8, sigma=1.0, labels=1, seed=32)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=64, threshold=300)
+    pl = gp.plan_queries(li, wl.query_labels)
+    table = gi.train_pq(wl.base, 8, iters=3)
+    codes = torch.zeros(wl.n, 8, dtype=torch.uint8)
+    return wl, li, pl, table, codes
+
+
+@pytest.mark.parametrize("place", list(PLACEMENTS))
+def test_pq_search_visited_fill_matches_oracle(gpu_ctx, long_world, place):
+    wl, li, pl, table, codes = long_world
+    table_mode, hash_mode, nsamp = PLACEMENTS[place]
+    say("pq_search visited fill", place)
+    rs = pl.graph
+    Q, W, steps = 256, 40, 450
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.0, pending_base_stop=False)
+    prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=1, max_steps=steps,
+                      bias=False)
+    oi, od, ost = po.pq_search(li, rs, pred_o, prm_o, codes.numpy(), table.numpy(),
+                               wl.queries.numpy())
+    assert ost[:, 6].max() > 4096, "the beam must overfill the visited set"
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
+    dr = gs.DeviceRoutes.upload(rs)
+    keep = (codes.cuda(), table.cuda())
+    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=1, max_steps=steps,
+                           bias=False, table_mode=table_mode, hash_mode=hash_mode)
+    ids, dists, st = gs.run_pq_routes(gpu_ctx, gs.pq_view(*keep), wl.queries.cuda(), dg, dr, prm,
+                                      alpha=0.0, pending_base_stop=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids).reshape(rs.count, W), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(rs.count, W).view(np.uint32),
+                          od.view(np.uint32))
+    assert np.array_equal(st.cpu().numpy().reshape(rs.count, 8), ost)
 
 
 def test_pq_search_batched_launch_order(gpu_ctx, world):

@@ -128,9 +128,11 @@ def test_rabitq_score_ip_exact(gpu_ctx, rworld):
 
 
 @pytest.mark.parametrize("bias", [True, False])
-def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias):
+@pytest.mark.parametrize("hash_mode,nsamp", [(_lib.PLACE_AUTO, False), (_lib.PLACE_LDS, True),
+                                             (_lib.PLACE_GLOBAL, True), (_lib.PLACE_SPILL, False)])
+def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp):
     wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
-    say("rabitq search bias", bias)
+    say("rabitq search bias", bias, "hash", hash_mode, "nsamp", nsamp)
     dev, rv = _rviews(rworld)
     out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
     rs = pl.graph
@@ -142,13 +144,14 @@ def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias):
                                    aid.numpy().astype(np.uint32), out["q8"].cpu().numpy(),
                                    out["scale"].cpu().numpy(), out["k1"].cpu().numpy(),
                                    out["cd"].cpu().numpy(), anchors.shape[0], P)
-    dg = gs.DeviceGraph.upload(li)
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
     dr = gs.DeviceRoutes.upload(rs)
     n = rs.count
     ids = torch.empty(n * W, dtype=torch.int32, device="cuda")
     dists = torch.empty(n * W, device="cuda")
     st = torch.zeros(n * 8, dtype=torch.int32, device="cuda")
-    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias)
+    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias,
+                           hash_mode=hash_mode)
     gpu_ctx.check(gpu_ctx.lib.gofann_rabitq_search(
         gpu_ctx.handle, rv, rq, dg.view(), dr.predicate_view(dg, 0.15 if bias else 0.0, bias),
         dr.routes_view(), prm, _lib.ptr(ids), _lib.ptr(dists), _lib.ptr(st)))
