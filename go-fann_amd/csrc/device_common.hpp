@@ -590,13 +590,21 @@ __device__ __forceinline__ bool lane_row_contains(const gofann_predicate_view& v
     return false;
 }
 
-__device__ __forceinline__ bool lane_pred_matches(const gofann_predicate_view& v, uint32_t route,
-                                                  uint32_t sample, PredCounters& c)
+// Three phases so a caller can overlap the row loads with other memory
+// rounds: bounds (CSR offsets), fill (the first labels), eval (clauses).
+__device__ __forceinline__ void lane_row_bounds(const gofann_predicate_view& v, uint32_t sample,
+                                                bool active, LaneRow& r)
 {
-    if (sample >= v.rows || v.csr_offsets == nullptr) return pred_matches(v, route, sample, c);
-    LaneRow r;
-    r.begin = v.csr_offsets[sample];
-    r.end = v.csr_offsets[sample + 1];
+    r.begin = 0;
+    r.end = 0;
+    if (active && sample < v.rows && v.csr_offsets != nullptr) {
+        r.begin = v.csr_offsets[sample];
+        r.end = v.csr_offsets[sample + 1];
+    }
+}
+
+__device__ __forceinline__ void lane_row_fill(const gofann_predicate_view& v, LaneRow& r)
+{
     const uint32_t last = r.end > r.begin ? r.end - 1 : r.begin;
 #pragma unroll
     for (int k = 0; k < kLaneRowBatch; ++k) {
@@ -606,6 +614,12 @@ __device__ __forceinline__ bool lane_pred_matches(const gofann_predicate_view& v
         const uint32_t x = r.end > r.begin ? v.csr_labels[i] : UINT32_MAX;
         r.lab[k] = r.begin + static_cast<uint32_t>(k) < r.end ? x : UINT32_MAX;
     }
+}
+
+__device__ __forceinline__ bool lane_pred_eval(const gofann_predicate_view& v, uint32_t route,
+                                               uint32_t sample, const LaneRow& r, PredCounters& c)
+{
+    if (sample >= v.rows || v.csr_offsets == nullptr) return pred_matches(v, route, sample, c);
     if (v.clauses) {
         for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i) {
             const gofann_clause cl = v.clauses[i];

@@ -588,6 +588,26 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
             }
         }
 
+        // First memory round of the step: the expanded node's label row and,
+        // for every unvisited neighbour (adjacency order, lane i takes
+        // neighbour i of the prefetched row, backend_pq.cu:4636-4684), its
+        // CSR bounds.  Loads without side effects; the serial order of the
+        // decisions below is the reference's.
+        WaveRow vrow{0, 0, UINT32_MAX, false};
+        if (!exhausted && enabled)
+            vrow = wave_row_load(a.pred, now.sample, cur.csr_begin, cur.csr_end, lane);
+        const uint32_t idx = cur.adj;
+        const bool keep = idx != UINT32_MAX && !visited.test(idx);
+        const uint64_t keep_mask = ballot(keep);
+        const int list_len = __popcll(keep_mask);
+        uint32_t my_sample = 0;
+        if (keep)
+            my_sample = a.graph.neighbor_samples ? cur.nsamp
+                                                 : a.graph.row_to_sample[label_offset + idx];
+        const bool need_pass = keep && bias && enabled;
+        LaneRow lrow;
+        lane_row_bounds(a.pred, my_sample, need_pass, lrow);
+
         // Verdict of the expanded node (backend_pq.cu:4393-4441).  Skipped
         // when the pool ran dry: the loop leaves below before reading it.
         int filt = 1;
@@ -595,10 +615,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
         if (!exhausted) {
             const uint32_t sample = now.sample;
             PredCounters c{0, 0};
-            if (enabled) {
-                const WaveRow row = wave_row_load(a.pred, sample, cur.csr_begin, cur.csr_end, lane);
-                filt = wave_pred_matches(a.pred, route, sample, row, lane, c) ? 1 : 2;
-            }
+            if (enabled) filt = wave_pred_matches(a.pred, route, sample, vrow, lane, c) ? 1 : 2;
             if (fallback) {
                 const uint32_t global_row = label_offset + now_local;
                 const uint64_t rmask =
@@ -675,23 +692,14 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
             if (mode == GOFANN_EARLY_STOP_ADAPTIVE && improved) finished = 0;
         }
 
-        // Unvisited neighbours in adjacency order (backend_pq.cu:4636-4684):
-        // lane i tests neighbour i of the prefetched row.
-        const uint32_t idx = cur.adj;
-        const bool keep = idx != UINT32_MAX && !visited.test(idx);
-        const uint64_t keep_mask = ballot(keep);
-        const int list_len = __popcll(keep_mask);
-
         if (early_stop_reached(mode, finished, a.params.finish_limit, Q, expanded, passed, SW) ||
             (a.params.max_steps > 0 && step >= a.params.max_steps))
             break;
 
-        // Lane-parallel scoring, predicate pass bits and priorities
+        // Second round: candidate label rows, then code rows and table
+        // entries; predicate pass bits and priorities
         // (backend_pq.cu:4704-4747, 4826-4864).
-        uint32_t my_sample = 0;
-        if (keep)
-            my_sample = a.graph.neighbor_samples ? cur.nsamp
-                                                 : a.graph.row_to_sample[label_offset + idx];
+        if (need_pass) lane_row_fill(a.pred, lrow);
         const float dist = sc.score(my_sample, keep);
         scored += list_len;
         float first = dist;
@@ -704,8 +712,8 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
                                          a.params.bit_filter_bonus, a.params.range_filter_bonus);
         }
         const float base = first;
-        if (keep && bias && enabled) {
-            const bool pass = lane_pred_matches(a.pred, route, my_sample, pc);
+        if (need_pass) {
+            const bool pass = lane_pred_eval(a.pred, route, my_sample, lrow, pc);
             first = priority(base, penalty, pass);
         }
 
