@@ -60,6 +60,8 @@ def parse():
                     help="visited hash placement: 0 auto, 1 LDS, 2 global")
     ap.add_argument("--no-neighbor-samples", action="store_true",
                     help="gather neighbour sample ids through row_to_sample")
+    ap.add_argument("--no-records", action="store_true",
+                    help="separate code rows and CSR labels instead of 64-byte sample records")
     return ap.parse_args()
 
 
@@ -141,7 +143,7 @@ class Pipeline:
     every route emits a 100-wide ADC shortlist, all reranked exactly."""
 
     def __init__(self, ctx, wl, li, table, codes, pl, torch, inline=True, width=100,
-                 table_mode=0, hash_mode=0, neighbor_samples=True, dg=None):
+                 table_mode=0, hash_mode=0, neighbor_samples=True, dg=None, records=True):
         from gofann_amd import search as gs
         self.gs, self.torch, self.ctx = gs, torch, ctx
         self.wl, self.pl = wl, pl
@@ -149,8 +151,12 @@ class Pipeline:
         self.table_mode, self.hash_mode = table_mode, hash_mode
         self.dg = dg if dg is not None else gs.DeviceGraph.upload(
             li, neighbor_samples=neighbor_samples)
+        # per-sample records: PQ codes + inline label slab in one 64-byte line
+        self.records = gs.SampleRecords.build(codes, li.csr_offsets, li.csr_labels) \
+            if records else None
         self.keep = (codes, table)
-        self.pqv = gs.pq_view(codes, table, wl.base if inline else None)
+        self.pqv = gs.pq_view(self.records if records else codes, table,
+                              wl.base if inline else None)
         self.q = wl.queries
         self.dr_graph = gs.DeviceRoutes.upload(pl.graph)
         self.dr_post = gs.DeviceRoutes.upload(pl.posting)
@@ -202,7 +208,8 @@ class Pipeline:
         if timed_kernel:
             self.ev[0].record()
         if ng:
-            gs.run_pq_routes(self.ctx, self.pqv, self.q, self.dg, self.dr_graph, prm, out=g_out)
+            gs.run_pq_routes(self.ctx, self.pqv, self.q, self.dg, self.dr_graph, prm, out=g_out,
+                             records=self.records)
         if timed_kernel:
             self.ev[1].record()
         if self.inline:
@@ -232,20 +239,24 @@ class Pipeline:
 
 
 def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes: int,
-                      neighbor_samples: bool) -> float:
+                      neighbor_samples: bool, record_bytes: int = 0) -> float:
     """Bytes the traversal must move per launch: the adjacency row of each
     expanded node (plus its neighbour-sample row when the graph carries
-    one), the code row of each scored candidate (plus its row_to_sample
-    word when it does not), CSR offsets of each predicate row opened and
-    each label word read, and (inline exact ranking) the base vector of each
+    one), what each scored candidate reads (its sample record -- codes and
+    inline labels -- or its code row, row_to_sample word, and the CSR offsets
+    and label words its predicate test reads), the expanded node's own label
+    slab or CSR words, and (inline exact ranking) the base vector of each
     expanded node that passes.  Frontier entries carry sample ids, so an
-    expanded node's own row_to_sample word is not read."""
+    expanded node's row_to_sample word is not read."""
     E = st[:, 1].astype(np.float64).sum()
     Pn = st[:, 2].astype(np.float64).sum()
     V = st[:, 3].astype(np.float64).sum()
     rows = st[:, 4].astype(np.float64).sum()
     labels = st[:, 5].astype(np.float64).sum()
     adj = 8 * degree if neighbor_samples else 4 * degree
+    if record_bytes:
+        return E * (adj + 16) + V * (record_bytes + (0 if neighbor_samples else 4)) \
+            + Pn * exact_bytes
     code = code_bytes if neighbor_samples else code_bytes + 4
     return E * adj + V * code + rows * 8 + labels * 4 + Pn * exact_bytes
 
@@ -317,7 +328,8 @@ def main():
     inline = not args.no_inline_exact
     pipe = Pipeline(ctx, wl, li, table, codes, pl, torch, inline=inline,
                     table_mode=args.table_mode, hash_mode=args.hash_mode,
-                    neighbor_samples=not args.no_neighbor_samples)
+                    neighbor_samples=not args.no_neighbor_samples,
+                    records=not args.no_records)
 
     ladder = [args.queue] if args.queue else [int(x) for x in args.ladder.split(",")]
     chosen, rec = ladder[-1], 0.0
@@ -348,7 +360,8 @@ def main():
     st = pipe.route_stats()
     kms = float(np.mean(kernel_ms))
     abytes = algorithmic_bytes(st, li.degree, 48, wl.dim if inline else 0,
-                               not args.no_neighbor_samples)
+                               not args.no_neighbor_samples,
+                               pipe.records.stride if pipe.records is not None else 0)
     achieved = abytes / (kms / 1000.0) / 1e9
     placed = ctx.last_placement()
     log(f"step {ms_per_step:.1f} ms, traversal kernel {kms:.1f} ms, recall {rec:.4f}, "
@@ -384,7 +397,8 @@ def main():
                    "rerank": "exact u8 on GPU", "seeds": "nearest bucket representative",
                    "recall_at_10": round(rec, 4),
                    "gt_queries": len(gt), "placement": placed,
-                   "neighbor_samples": not args.no_neighbor_samples},
+                   "neighbor_samples": not args.no_neighbor_samples,
+                   "sample_records": not args.no_records},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 5),
                      "traffic": None, "kernel": "traversal_kernel<PqScorer<48>>",

@@ -474,6 +474,31 @@ __device__ __forceinline__ bool pred_matches(const gofann_predicate_view& v, uin
     return true;
 }
 
+// Inline label slab (gofann_predicate_view.label_slab): 16 bytes per sample,
+// u16 count then up to 7 u16 labels; count 0xFFFF = read the CSR row.
+constexpr uint32_t kSlabCapacity = 7;
+constexpr uint32_t kSlabOverflow = 0xFFFFu;
+
+__device__ __forceinline__ bool slab_usable(const gofann_predicate_view& v, uint32_t sample)
+{
+    return v.label_slab != nullptr && v.csr_offsets != nullptr && sample < v.rows;
+}
+
+__device__ __forceinline__ uint4 slab_load(const gofann_predicate_view& v, uint32_t sample)
+{
+    return *reinterpret_cast<const uint4*>(v.label_slab + static_cast<size_t>(sample) * v.slab_stride);
+}
+
+__device__ __forceinline__ uint32_t slab_count(const uint4& w) { return w.x & 0xFFFFu; }
+
+// Label k (0-based) of a slab; k may be a runtime value.
+__device__ __forceinline__ uint32_t slab_label(const uint4& w, uint32_t k)
+{
+    const uint32_t h = k + 1;  // u16 index
+    const uint32_t word = (h >> 1) == 0 ? w.x : (h >> 1) == 1 ? w.y : (h >> 1) == 2 ? w.z : w.w;
+    return (word >> (16 * (h & 1))) & 0xFFFFu;
+}
+
 // One sample's CSR label row held across the wave: lane k holds label
 // begin+k of the first 64 (UINT32_MAX past the end).  Loaded once per
 // expanded node; every handle test of the route's clauses reads it.
@@ -516,6 +541,18 @@ __device__ __forceinline__ bool wave_row_contains(const gofann_predicate_view& v
     }
     c.labels += len;
     return false;
+}
+
+// WaveRow of a sample whose inline slab (count != overflow) is at hand.
+__device__ __forceinline__ WaveRow wave_row_from_slab(const uint4& slab, int lane)
+{
+    WaveRow r;
+    r.valid = true;
+    r.begin = 0;
+    r.end = slab_count(slab);
+    const uint32_t l = static_cast<uint32_t>(lane);
+    r.lab = l < r.end && l < kSlabCapacity ? slab_label(slab, l) : UINT32_MAX;
+    return r;
 }
 
 // pred_matches for a wave-uniform sample whose row is held in a WaveRow.
@@ -591,20 +628,42 @@ __device__ __forceinline__ bool lane_row_contains(const gofann_predicate_view& v
 }
 
 // Three phases so a caller can overlap the row loads with other memory
-// rounds: bounds (CSR offsets), fill (the first labels), eval (clauses).
+// rounds: bounds (the slab, or CSR offsets), fill (the first labels), eval
+// (clauses).  `slab` carries the slab words from bounds to fill.
 __device__ __forceinline__ void lane_row_bounds(const gofann_predicate_view& v, uint32_t sample,
-                                                bool active, LaneRow& r)
+                                                bool active, LaneRow& r, uint4& slab)
 {
     r.begin = 0;
     r.end = 0;
-    if (active && sample < v.rows && v.csr_offsets != nullptr) {
+    slab = make_uint4(kSlabOverflow, 0, 0, 0);
+    if (!active) return;
+    if (slab_usable(v, sample)) {
+        slab = slab_load(v, sample);
+    } else if (sample < v.rows && v.csr_offsets != nullptr) {
         r.begin = v.csr_offsets[sample];
         r.end = v.csr_offsets[sample + 1];
     }
 }
 
-__device__ __forceinline__ void lane_row_fill(const gofann_predicate_view& v, LaneRow& r)
+__device__ __forceinline__ void lane_row_fill(const gofann_predicate_view& v, LaneRow& r,
+                                              uint32_t sample, const uint4& slab)
 {
+    if (slab_usable(v, sample)) {
+        const uint32_t n = slab_count(slab);
+        if (n != kSlabOverflow) {
+            // The inline row: same labels, same scan, no memory access.
+            r.begin = 0;
+            r.end = n;
+#pragma unroll
+            for (int k = 0; k < kLaneRowBatch; ++k)
+                r.lab[k] = static_cast<uint32_t>(k) < n && k < static_cast<int>(kSlabCapacity)
+                               ? slab_label(slab, static_cast<uint32_t>(k))
+                               : UINT32_MAX;
+            return;
+        }
+        r.begin = v.csr_offsets[sample];
+        r.end = v.csr_offsets[sample + 1];
+    }
     const uint32_t last = r.end > r.begin ? r.end - 1 : r.begin;
 #pragma unroll
     for (int k = 0; k < kLaneRowBatch; ++k) {

@@ -42,6 +42,10 @@ int check_pq(Context* ctx, const gofann_pq_view* pq, const void* queries, int qu
         return ctx->fail(GOFANN_ERR_INVALID, "PQ queries must be u8 or f32");
     if (pq->exact_base != nullptr && pq->dim % 4 != 0)
         return ctx->fail(GOFANN_ERR_INVALID, "inline exact distances need dim % 4 == 0");
+    if (pq->code_stride != 0 &&
+        (pq->code_stride < pq->pq_dim || (pq->pq_dim % 16 == 0 && pq->code_stride % 16 != 0)))
+        return ctx->fail(GOFANN_ERR_INVALID,
+                         "code_stride must be >= pq_dim (and a multiple of 16 when pq_dim is)");
     return GOFANN_OK;
 }
 

@@ -107,6 +107,7 @@ struct PqScanScorer {
     int query_f32;
     uint32_t dim;
     uint32_t pq_dim;
+    uint32_t stride;  // bytes between code rows
     float* lut;
 
     __device__ void setup(uint32_t q, int tid, unsigned char* lds)
@@ -131,7 +132,7 @@ struct PqScanScorer {
     }
     __device__ float score(uint32_t sample) const
     {
-        return adc_serial(lut, codes + static_cast<size_t>(sample) * pq_dim, static_cast<int>(pq_dim));
+        return adc_serial(lut, codes + static_cast<size_t>(sample) * stride, static_cast<int>(pq_dim));
     }
 };
 
@@ -500,6 +501,7 @@ int pq_posting_scan(Context* ctx, const gofann_pq_view* pq, const void* queries,
     sc.query_f32 = query_elem == GOFANN_ELEM_F32 ? 1 : 0;
     sc.dim = pq->dim;
     sc.pq_dim = pq->pq_dim;
+    sc.stride = pq->code_stride ? pq->code_stride : pq->pq_dim;
     sc.lut = nullptr;
     const uint32_t lds = pq->pq_dim * 256u * 4u;
     a.table_bytes = lds;

@@ -84,6 +84,7 @@ struct PqScorer {
     uint32_t dim;
     uint32_t pq_dim;
     uint32_t sub;            // dim / pq_dim
+    uint32_t stride;         // bytes between code rows
     float* table;            // LDS: ADC table [M][256], or the fp32 query [dim]
     const void* exact_base;  // resident vectors for the inline exact distance
     uint32_t query;
@@ -166,7 +167,7 @@ struct PqScorer {
     __device__ float score(uint32_t sample, bool active) const
     {
         if (!active) return 0.0f;
-        const uint8_t* row = codes + static_cast<size_t>(sample) * m();
+        const uint8_t* row = codes + static_cast<size_t>(sample) * stride;
         if constexpr (kM > 0 && kM % 16 == 0) {
             uint4 w[kM / 16];
 #pragma unroll
@@ -453,8 +454,7 @@ struct TraversalArgs {
 struct NodeLoads {
     uint32_t adj;        // lane j: adjacency entry j (UINT32_MAX past the degree)
     uint32_t nsamp;      // lane j: its sample id (graph.neighbor_samples)
-    uint32_t csr_begin;  // the node's CSR label row (wave-uniform values)
-    uint32_t csr_end;
+    uint4 row;           // the node's label slab, or its CSR bounds in .x/.y
     ExactWords ex;       // exact-distance words (inline exact)
 };
 
@@ -468,11 +468,14 @@ __device__ __forceinline__ void load_node(const TraversalArgs& a, const Scorer& 
     const bool in_row = static_cast<uint32_t>(lane) < degree;
     n.adj = in_row ? a.graph.graph[row + lane] : UINT32_MAX;
     n.nsamp = (in_row && a.graph.neighbor_samples) ? a.graph.neighbor_samples[row + lane] : 0u;
-    n.csr_begin = 0;
-    n.csr_end = 0;
+    n.row = make_uint4(0, 0, 0, 0);
     if (verdict_rows && e.sample < a.pred.rows && a.pred.csr_offsets != nullptr) {
-        n.csr_begin = a.pred.csr_offsets[e.sample];
-        n.csr_end = a.pred.csr_offsets[e.sample + 1];
+        if (slab_usable(a.pred, e.sample)) {
+            n.row = slab_load(a.pred, e.sample);
+        } else {
+            n.row.x = a.pred.csr_offsets[e.sample];
+            n.row.y = a.pred.csr_offsets[e.sample + 1];
+        }
     }
     if constexpr (Scorer::kHasExact) {
         if (exact) sc.exact_load(e.sample, lane, n.ex);
@@ -594,8 +597,17 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
         // CSR bounds.  Loads without side effects; the serial order of the
         // decisions below is the reference's.
         WaveRow vrow{0, 0, UINT32_MAX, false};
-        if (!exhausted && enabled)
-            vrow = wave_row_load(a.pred, now.sample, cur.csr_begin, cur.csr_end, lane);
+        if (!exhausted && enabled) {
+            const uint32_t s0 = now.sample;
+            if (!slab_usable(a.pred, s0)) {
+                vrow = wave_row_load(a.pred, s0, cur.row.x, cur.row.y, lane);
+            } else if (slab_count(cur.row) != kSlabOverflow) {
+                vrow = wave_row_from_slab(cur.row, lane);
+            } else {
+                vrow = wave_row_load(a.pred, s0, a.pred.csr_offsets[s0], a.pred.csr_offsets[s0 + 1],
+                                     lane);
+            }
+        }
         const uint32_t idx = cur.adj;
         const bool keep = idx != UINT32_MAX && !visited.test(idx);
         const uint64_t keep_mask = ballot(keep);
@@ -606,7 +618,8 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
                                                  : a.graph.row_to_sample[label_offset + idx];
         const bool need_pass = keep && bias && enabled;
         LaneRow lrow;
-        lane_row_bounds(a.pred, my_sample, need_pass, lrow);
+        uint4 lslab;
+        lane_row_bounds(a.pred, my_sample, need_pass, lrow, lslab);
 
         // Verdict of the expanded node (backend_pq.cu:4393-4441).  Skipped
         // when the pool ran dry: the loop leaves below before reading it.
@@ -699,7 +712,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
         // Second round: candidate label rows, then code rows and table
         // entries; predicate pass bits and priorities
         // (backend_pq.cu:4704-4747, 4826-4864).
-        if (need_pass) lane_row_fill(a.pred, lrow);
+        if (need_pass) lane_row_fill(a.pred, lrow, my_sample, lslab);
         const float dist = sc.score(my_sample, keep);
         scored += list_len;
         float first = dist;
@@ -972,6 +985,7 @@ PqScorer<kM, kSub> make_pq_scorer(const gofann_pq_view* pq, const void* queries,
     sc.dim = pq->dim;
     sc.pq_dim = pq->pq_dim;
     sc.sub = pq->dim / pq->pq_dim;
+    sc.stride = pq->code_stride ? pq->code_stride : pq->pq_dim;
     sc.table = nullptr;
     sc.exact_base = pq->exact_base;
     sc.query = 0;

@@ -45,7 +45,7 @@ class PredicateView(C.Structure):
                 ("ranges", P), ("route_enabled", P), ("route_compiled", P),
                 ("base_ranges", P), ("csr_offsets", P), ("csr_labels", P),
                 ("rows", U32), ("range_stride", U32), ("alpha", C.c_float),
-                ("pending_base_stop", C.c_int)]
+                ("pending_base_stop", C.c_int), ("label_slab", P), ("slab_stride", U32)]
 
 
 class Routes(C.Structure):
@@ -75,7 +75,7 @@ STATS_FIELDS = [f[0] for f in RouteStats._fields_]
 
 class PqView(C.Structure):
     _fields_ = [("codes", P), ("centroids", P), ("dim", U32), ("pq_dim", U32),
-                ("samples", U32), ("exact_base", P)]
+                ("samples", U32), ("exact_base", P), ("code_stride", U32)]
 
 
 class RabitqView(C.Structure):

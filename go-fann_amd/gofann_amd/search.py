@@ -99,6 +99,62 @@ def neighbor_sample_table(dg: "DeviceGraph", index) -> torch.Tensor:
     return out
 
 
+SLAB_BYTES = 16
+SLAB_CAPACITY = 7
+SLAB_OVERFLOW = 0xFFFF
+
+
+@dataclass
+class SampleRecords:
+    """Per-sample fixed-width device records: the PQ code row, then a
+    16-byte label slab (u16 count, up to 7 u16 labels ascending: the sample's
+    CSR row inline).  One cache line per scored candidate serves the code
+    gather and its predicate test.  Rows with more than 7 labels (or labels
+    >= 0xFFFF) get count 0xFFFF and are read from the CSR."""
+    data: torch.Tensor   # u8 [samples][stride]
+    pq_dim: int
+    stride: int
+    slab_offset: int
+
+    @classmethod
+    def build(cls, codes: torch.Tensor, csr_offsets: np.ndarray, csr_labels: np.ndarray,
+              overflow_every: int = 0) -> "SampleRecords":
+        n, M = int(codes.shape[0]), int(codes.shape[1])
+        slab_off = (M + 15) // 16 * 16
+        stride = slab_off + SLAB_BYTES
+        rec = torch.zeros(n, stride, dtype=torch.uint8, device=DEV)
+        rec[:, :M] = codes.to(DEV)
+        off = torch.from_numpy(csr_offsets.astype(np.int64)).to(DEV)
+        lab = torch.from_numpy(csr_labels.astype(np.int64)).to(DEV)
+        cnt = off[1:] - off[:-1]
+        slab = torch.zeros(n, 8, dtype=torch.int64, device=DEV)
+        ok = cnt <= SLAB_CAPACITY
+        for k in range(SLAB_CAPACITY):
+            has = cnt > k
+            idx = torch.where(has, off[:-1] + k, torch.zeros_like(cnt))
+            v = torch.where(has, lab[idx] if lab.numel() else torch.zeros_like(cnt),
+                            torch.zeros_like(cnt))
+            ok &= v < SLAB_OVERFLOW
+            slab[:, k + 1] = v
+        if overflow_every > 0:  # test hook: force the CSR path on some rows
+            ok &= (torch.arange(n, device=DEV) % overflow_every) != 0
+        slab[:, 0] = torch.where(ok, cnt, torch.full_like(cnt, SLAB_OVERFLOW))
+        slab = torch.where(ok[:, None] | (torch.arange(8, device=DEV) == 0)[None, :], slab,
+                           torch.zeros_like(slab))
+        rec[:, slab_off:] = _u16_bytes(slab)
+        return cls(rec, M, stride, slab_off)
+
+    def slab(self):
+        return self.data.data_ptr() + self.slab_offset, self.stride
+
+
+def _u16_bytes(x: torch.Tensor) -> torch.Tensor:
+    """int64 [n][8] values < 2^16 -> little-endian u8 [n][16]."""
+    lo = (x & 0xFF).to(torch.uint8)
+    hi = ((x >> 8) & 0xFF).to(torch.uint8)
+    return torch.stack([lo, hi], dim=-1).reshape(x.shape[0], 16)
+
+
 @dataclass
 class DeviceRoutes:
     route_query: torch.Tensor
@@ -141,14 +197,16 @@ class DeviceRoutes:
                       end - begin, _lib.ptr(order))
 
     def predicate_view(self, dg: DeviceGraph, alpha: float, pending_base_stop: bool,
-                       enabled: bool = True) -> PredicateView:
+                       enabled: bool = True, records: "SampleRecords | None" = None
+                       ) -> PredicateView:
+        slab, slab_stride = records.slab() if records is not None else (None, 0)
         return PredicateView(_lib.ptr(self.pred_offsets), _lib.ptr(self.pred_handles),
                              _lib.ptr(self.pred_clauses), _lib.ptr(self.pred_ranges),
                              _lib.ptr(self.pred_enabled) if enabled else None,
                              _lib.ptr(self.pred_compiled), _lib.ptr(self.base_ranges),
                              _lib.ptr(dg.csr_offsets), _lib.ptr(dg.csr_labels),
                              dg.samples, self.range_stride, float(alpha),
-                             1 if pending_base_stop else 0)
+                             1 if pending_base_stop else 0, slab, slab_stride)
 
 
 def search_params(queue_limit=64, result_width=100, early_stop_mode=_lib.EARLY_STOP_ADAPTIVE,
@@ -160,10 +218,13 @@ def search_params(queue_limit=64, result_width=100, early_stop_mode=_lib.EARLY_S
                         1 if inline_exact else 0, table_mode, hash_mode)
 
 
-def pq_view(codes: torch.Tensor, table: torch.Tensor, exact_base: torch.Tensor | None = None
-            ) -> PqView:
+def pq_view(codes, table: torch.Tensor, exact_base: torch.Tensor | None = None) -> PqView:
+    """codes: u8 [samples][M] tensor, or SampleRecords (codes inside records)."""
+    if isinstance(codes, SampleRecords):
+        return PqView(codes.data.data_ptr(), _lib.ptr(table), int(table.shape[1]), codes.pq_dim,
+                      int(codes.data.shape[0]), _lib.ptr(exact_base), codes.stride)
     return PqView(_lib.ptr(codes), _lib.ptr(table), int(table.shape[1]), int(codes.shape[1]),
-                  int(codes.shape[0]), _lib.ptr(exact_base))
+                  int(codes.shape[0]), _lib.ptr(exact_base), 0)
 
 
 def query_elem(q: torch.Tensor) -> int:
@@ -177,7 +238,7 @@ def query_elem(q: torch.Tensor) -> int:
 def run_pq_routes(ctx: _lib.Context, pqv: PqView, queries: torch.Tensor, dg: DeviceGraph,
                   dr: DeviceRoutes, params: SearchParams, alpha: float = 0.15,
                   pending_base_stop: bool = True, begin: int = 0, end: int | None = None,
-                  out=None):
+                  out=None, records: SampleRecords | None = None):
     end = dr.count if end is None else end
     n = dr.count
     W = params.result_width
@@ -188,7 +249,7 @@ def run_pq_routes(ctx: _lib.Context, pqv: PqView, queries: torch.Tensor, dg: Dev
     else:
         ids, dists, stats = out
     gv = dg.view()
-    pv = dr.predicate_view(dg, alpha, pending_base_stop)
+    pv = dr.predicate_view(dg, alpha, pending_base_stop, records=records)
     rv = dr.routes_view(begin, end)
     ctx.check(ctx.lib.gofann_pq_search(ctx.handle, pqv, _lib.ptr(queries), query_elem(queries),
                                        gv, pv, rv, params, _lib.ptr(ids), _lib.ptr(dists),

@@ -119,6 +119,13 @@ typedef struct {
     uint32_t range_stride;
     float alpha;                       /* bias penalty factor */
     int pending_base_stop;
+    /* Optional 16-byte label slab per sample at label_slab + s*slab_stride
+     * (16-byte aligned): u16 count, then up to 7 u16 labels, ascending --
+     * the sample's CSR row inline, typically beside its PQ codes so one
+     * cache line serves both.  count 0xFFFF: row too long, read the CSR.
+     * Labels must be < 0xFFFF.  NULL: CSR only.  Results are identical. */
+    const uint8_t* label_slab;
+    uint32_t slab_stride;
 } gofann_predicate_view;
 
 /* Routes of one batch.  Route r searches group route_group[r] from the
@@ -186,6 +193,8 @@ typedef struct {
     uint32_t pq_dim;
     uint32_t samples;
     const void* exact_base;   /* [samples][dim] u8 or f32 (matches the queries); may be NULL */
+    uint32_t code_stride;     /* bytes between code rows; 0 = pq_dim (codes inside wider
+                                 per-sample records); multiple of 16 when pq_dim % 16 == 0 */
 } gofann_pq_view;
 
 typedef struct {

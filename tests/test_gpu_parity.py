@@ -56,16 +56,26 @@ def _pq(wl, M):
     return table, codes
 
 
-# Placements of the per-route state: (ADC table, visited hash, neighbour
-# sample table).  Every placement must give the oracle's bits.
+# Placements of the per-route state: (ADC table, visited set, neighbour
+# sample table, sample records: codes + inline label slab, "overflow" forcing
+# every third row onto the CSR).  Every placement must give the oracle's bits.
 PLACEMENTS = {
-    "auto": (_lib.PLACE_AUTO, _lib.PLACE_AUTO, False),
-    "lds-lds-nsamp": (_lib.PLACE_LDS, _lib.PLACE_LDS, True),
-    "direct-global-nsamp": (_lib.PLACE_GLOBAL, _lib.PLACE_GLOBAL, True),
-    "direct-lds": (_lib.PLACE_GLOBAL, _lib.PLACE_LDS, False),
-    "direct-spill-nsamp": (_lib.PLACE_GLOBAL, _lib.PLACE_SPILL, True),
-    "lds-spill": (_lib.PLACE_LDS, _lib.PLACE_SPILL, False),
+    "auto": (_lib.PLACE_AUTO, _lib.PLACE_AUTO, False, None),
+    "lds-lds-nsamp": (_lib.PLACE_LDS, _lib.PLACE_LDS, True, None),
+    "direct-global-nsamp": (_lib.PLACE_GLOBAL, _lib.PLACE_GLOBAL, True, None),
+    "direct-lds": (_lib.PLACE_GLOBAL, _lib.PLACE_LDS, False, None),
+    "direct-spill-nsamp": (_lib.PLACE_GLOBAL, _lib.PLACE_SPILL, True, None),
+    "lds-spill": (_lib.PLACE_LDS, _lib.PLACE_SPILL, False, None),
+    "auto-records": (_lib.PLACE_AUTO, _lib.PLACE_AUTO, True, "slab"),
+    "lds-records-overflow": (_lib.PLACE_LDS, _lib.PLACE_GLOBAL, False, "overflow"),
 }
+
+
+def records_for(codes, li, kind):
+    if kind is None:
+        return None
+    return gs.SampleRecords.build(codes, li.csr_offsets, li.csr_labels,
+                                  overflow_every=3 if kind == "overflow" else 0)
 HASH_CODE = {_lib.PLACE_GLOBAL: 0, _lib.PLACE_LDS: 1, _lib.PLACE_SPILL: 2}
 
 
@@ -76,7 +86,7 @@ def test_pq_search_matches_oracle(gpu_ctx, world, M, mode, place):
     kind, wl, li, pl = world
     if wl.dim % M:
         pytest.skip("pq_dim must divide dim")
-    table_mode, hash_mode, nsamp = PLACEMENTS[place]
+    table_mode, hash_mode, nsamp, rec = PLACEMENTS[place]
     say("pq_search", kind, M, mode, place)
     table, codes = _pq(wl, M)
     rs = pl.graph
@@ -93,13 +103,15 @@ def test_pq_search_matches_oracle(gpu_ctx, world, M, mode, place):
 
     dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
     dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
-    keep = (codes.cuda(), table.cuda())
+    records = records_for(codes, li, rec)
+    keep = (records if records is not None else codes.cuda(), table.cuda())
     pqv = gs.pq_view(*keep)
     qd = wl.queries.cuda()
     prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=es, finish_limit=3,
                            max_steps=maxs, bias=bias, table_mode=table_mode, hash_mode=hash_mode)
     ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, qd, dg, dr, prm,
-                                      alpha=0.15 if bias else 0.0, pending_base_stop=bias)
+                                      alpha=0.15 if bias else 0.0, pending_base_stop=bias,
+                                      records=records)
     torch.cuda.synchronize()
     gi_ = as_u32(ids).reshape(rs.count, W)
     gd = dists.cpu().numpy().reshape(rs.count, W)
@@ -120,7 +132,7 @@ def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W, place):
     """Inline exact distances (enable_true_distance_rerank) on resident
     vectors: identical ids, distance bits and counters."""
     kind, wl, li, pl = world
-    table_mode, hash_mode, nsamp = PLACEMENTS[place]
+    table_mode, hash_mode, nsamp, rec = PLACEMENTS[place]
     say("pq_search inline exact", kind, W, place)
     table, codes = _pq(wl, 16)
     rs = pl.graph
@@ -132,11 +144,13 @@ def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W, place):
                                wl.queries.numpy(), base=base)
     dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
     dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
-    keep = (codes.cuda(), table.cuda(), wl.base.cuda())
+    records = records_for(codes, li, rec)
+    keep = (records if records is not None else codes.cuda(), table.cuda(), wl.base.cuda())
     pqv = gs.pq_view(*keep)
     prm = gs.search_params(queue_limit=48, result_width=W, inline_exact=True,
                            table_mode=table_mode, hash_mode=hash_mode)
-    ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, wl.queries.cuda(), dg, dr, prm)
+    ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, wl.queries.cuda(), dg, dr, prm,
+                                      records=records)
     torch.cuda.synchronize()
     assert np.array_equal(as_u32(ids).reshape(rs.count, W), oi)
     assert np.array_equal(dists.cpu().numpy().reshape(rs.count, W).view(np.uint32),
@@ -168,7 +182,7 @@ def long_world():
 @pytest.mark.parametrize("place", list(PLACEMENTS))
 def test_pq_search_visited_fill_matches_oracle(gpu_ctx, long_world, place):
     wl, li, pl, table, codes = long_world
-    table_mode, hash_mode, nsamp = PLACEMENTS[place]
+    table_mode, hash_mode, nsamp, rec = PLACEMENTS[place]
     say("pq_search visited fill", place)
     rs = pl.graph
     Q, W, steps = 256, 40, 450
@@ -180,11 +194,12 @@ def test_pq_search_visited_fill_matches_oracle(gpu_ctx, long_world, place):
     assert ost[:, 6].max() > 4096, "the beam must overfill the visited set"
     dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
     dr = gs.DeviceRoutes.upload(rs)
-    keep = (codes.cuda(), table.cuda())
+    records = records_for(codes, li, rec)
+    keep = (records if records is not None else codes.cuda(), table.cuda())
     prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=1, max_steps=steps,
                            bias=False, table_mode=table_mode, hash_mode=hash_mode)
     ids, dists, st = gs.run_pq_routes(gpu_ctx, gs.pq_view(*keep), wl.queries.cuda(), dg, dr, prm,
-                                      alpha=0.0, pending_base_stop=False)
+                                      alpha=0.0, pending_base_stop=False, records=records)
     torch.cuda.synchronize()
     assert np.array_equal(as_u32(ids).reshape(rs.count, W), oi)
     assert np.array_equal(dists.cpu().numpy().reshape(rs.count, W).view(np.uint32),
