@@ -261,6 +261,20 @@ def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes:
     return E * adj + V * code + rows * 8 + labels * 4 + Pn * exact_bytes
 
 
+def measured_traffic(Q: int, placement: dict, records: bool):
+    """HBM bytes per traversal launch from the committed rocprofv3 FETCH_SIZE
+    / WRITE_SIZE summary (profiles/traversal_pq48_c2_traffic.md), when this
+    run's configuration is the one that summary measured; else None."""
+    path = ROOT / "profiles" / "traversal_pq48_c2_traffic.md"
+    if not path.exists() or Q != 128 or not records or placement.get("table_in_lds") != 0 \
+            or placement.get("hash_in_lds") != 2:
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("bytes_per_launch:"):
+            return float(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline):
     """The oracle (a single-threaded C restatement of the reference path) on
     a bounded sample of the same workload: graph search (with the same
@@ -401,7 +415,8 @@ def main():
                    "sample_records": not args.no_records},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 5),
-                     "traffic": None, "kernel": "traversal_kernel<PqScorer<48>>",
+                     "traffic": measured_traffic(chosen, placed, not args.no_records),
+                     "kernel": "traversal_kernel<PqScorer<48>>",
                      "kernel_ms": round(kms, 3), "algorithmic_bytes": abytes},
         "cpu_baseline": cpu,
     }
