@@ -120,6 +120,15 @@ SIGNATURES = {
     "gofann_pq_score": (C.c_int, [P, C.POINTER(PqView), P, C.c_int, P, P, U32, P]),
     "gofann_rabitq_score": (C.c_int, [P, C.POINTER(RabitqView), C.POINTER(RabitqQueries),
                                       P, P, U32, P, P]),
+    "gofann_host_rerank_create": (C.c_int, [P, C.c_int, U32, U32, P, U32, C.POINTER(P)]),
+    "gofann_host_rerank_destroy": (None, [P]),
+    "gofann_host_rerank_last_error": (C.c_char_p, [P]),
+    "gofann_host_rerank_routes": (C.c_int, [P, P, U32, P, U32, U32, P, P]),
+    "gofann_pq_search_host_rerank": (C.c_int, [P, P, C.POINTER(PqView), P, C.c_int,
+                                               C.POINTER(GraphView), C.POINTER(PredicateView),
+                                               C.POINTER(Routes), C.POINTER(SearchParams), P,
+                                               U32, U32, P, P, P]),
+    "gofann_host_merge_routes": (C.c_int, [P, P, P, P, U32, U32, U32, P, P]),
 }
 
 _lib = None

@@ -339,3 +339,98 @@ def merge_routes_gpu(ctx, q_offsets: torch.Tensor, q_routes: torch.Tensor, ids: 
                                           _lib.ptr(ids), _lib.ptr(dists), width, queries, topk,
                                           _lib.ptr(out_i), _lib.ptr(out_d)))
     return out_i, out_d
+
+
+# ---------------------------------------------------------------------------
+# Host side: streamed CPU exact rerank (libgofann_hip.so host pool).
+# ---------------------------------------------------------------------------
+def _np_ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+class HostRerank:
+    """CPU exact rerank over host copies of the base vectors and queries
+    (gofann_host_rerank_*): a worker pool that reranks GPU shortlists, alone
+    or streamed behind the GPU search in route chunks."""
+
+    def __init__(self, base: np.ndarray, queries: np.ndarray, threads: int = 16):
+        import ctypes as C
+        self.lib = _lib.load()
+        elem = {np.dtype(np.uint8): ELEM_U8, np.dtype(np.float32): ELEM_F32,
+                np.dtype(np.float16): ELEM_F16}[base.dtype]
+        self.base = np.ascontiguousarray(base)
+        self.queries = np.ascontiguousarray(queries, dtype=np.uint8 if elem == ELEM_U8
+                                            else np.float32)
+        h = C.c_void_p()
+        rc = self.lib.gofann_host_rerank_create(_np_ptr(self.base), elem, self.base.shape[1],
+                                                self.base.shape[0], _np_ptr(self.queries),
+                                                threads, C.byref(h))
+        if rc != 0:
+            raise _lib.GofannError(f"gofann_host_rerank_create failed ({rc})")
+        self.handle = h
+
+    def _check(self, rc):
+        if rc != 0:
+            msg = self.lib.gofann_host_rerank_last_error(self.handle)
+            raise _lib.GofannError(f"host rerank failed ({rc}): {msg.decode() if msg else ''}")
+
+    def rerank(self, shortlist: np.ndarray, route_query: np.ndarray, topk: int):
+        sl = np.ascontiguousarray(shortlist, dtype=np.uint32)
+        rq = np.ascontiguousarray(route_query, dtype=np.uint32)
+        n, width = sl.shape
+        ids = np.empty((n, topk), np.uint32)
+        dists = np.empty((n, topk), np.float32)
+        self._check(self.lib.gofann_host_rerank_routes(self.handle, _np_ptr(sl), width,
+                                                       _np_ptr(rq), n, topk, _np_ptr(ids),
+                                                       _np_ptr(dists)))
+        return ids, dists
+
+    def search(self, ctx, pqv: PqView, queries: torch.Tensor, dg: DeviceGraph,
+               dr: "DeviceRoutes", params: SearchParams, route_query: np.ndarray,
+               chunk_routes: int, topk: int, alpha: float = 0.15,
+               pending_base_stop: bool = True, records: "SampleRecords | None" = None,
+               stats: torch.Tensor | None = None, out=None):
+        """GPU traversal in chunks with the shortlist handed to the host pool
+        chunk by chunk (gofann_pq_search_host_rerank); host outputs."""
+        n = dr.count
+        rq = np.ascontiguousarray(route_query, dtype=np.uint32)
+        if out is None:
+            out = (np.empty((n, topk), np.uint32), np.empty((n, topk), np.float32))
+        ids, dists = out
+        gv = dg.view()
+        pv = dr.predicate_view(dg, alpha, pending_base_stop, records=records)
+        rv = Routes(_lib.ptr(dr.route_query), _lib.ptr(dr.route_group), _lib.ptr(dr.route_start),
+                    None, None, None, None, None, None, 0, n, None)
+        ctx.check(self.lib.gofann_pq_search_host_rerank(
+            ctx.handle, self.handle, pqv, _lib.ptr(queries), query_elem(queries), gv, pv, rv,
+            params, _np_ptr(rq), chunk_routes, topk, _np_ptr(ids), _np_ptr(dists),
+            _lib.ptr(stats)))
+        return ids, dists
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.gofann_host_rerank_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def host_merge_routes(route_to_query: np.ndarray, ids: np.ndarray, dists: np.ndarray,
+                      queries: int, topk: int):
+    """Route -> query merge on the host (gofann_host_merge_routes)."""
+    lib = _lib.load()
+    off, order = query_route_csr(route_to_query, queries)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    dists = np.ascontiguousarray(dists, dtype=np.float32)
+    width = ids.shape[1] if ids.ndim == 2 else topk
+    out_i = np.empty((queries, topk), np.uint32)
+    out_d = np.empty((queries, topk), np.float32)
+    rc = lib.gofann_host_merge_routes(_np_ptr(off), _np_ptr(order), _np_ptr(ids), _np_ptr(dists),
+                                      width, queries, topk, _np_ptr(out_i), _np_ptr(out_d))
+    if rc != 0:
+        raise _lib.GofannError(f"gofann_host_merge_routes failed ({rc})")
+    return out_i, out_d

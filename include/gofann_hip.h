@@ -307,6 +307,45 @@ int gofann_rabitq_score(gofann_ctx* ctx, const gofann_rabitq_view* rq,
                         const gofann_rabitq_queries* prepared, const uint32_t* q_idx,
                         const uint32_t* s_idx, uint32_t n, float* out, int32_t* ip_int);
 
+/* ---- streamed CPU exact rerank (run_highfreq_streaming_rerank and
+ * highfreq_host_batch_rerank_range, backend_pq.cu:9646-9738, 2479-2592;
+ * exact_l2_u8 :2187-2195).  A host worker pool over caller-owned host
+ * arrays: base [samples][dim] (u8 / f32 / f16) and queries [n][dim] (u8 for
+ * a u8 base, else f32).  Per route: valid unique shortlist ids, exact fp32
+ * L2 with dimensions in order, top-k by (distance, id), ascending, padded
+ * with UINT32_MAX / FLT_MAX.  The shortlist is taken as predicate-verified
+ * (device predicates admit only passing nodes to the result heap). */
+typedef struct gofann_host_rerank gofann_host_rerank;
+int gofann_host_rerank_create(const void* base, int base_elem, uint32_t dim, uint32_t samples,
+                              const void* queries, uint32_t threads, gofann_host_rerank** out);
+void gofann_host_rerank_destroy(gofann_host_rerank* hr);
+const char* gofann_host_rerank_last_error(const gofann_host_rerank* hr);
+/* Host arrays only: shortlist [routes][width], route_query [routes],
+ * outputs [routes][topk]. */
+int gofann_host_rerank_routes(gofann_host_rerank* hr, const uint32_t* shortlist, uint32_t width,
+                              const uint32_t* route_query, uint32_t routes, uint32_t topk,
+                              uint32_t* out_ids, float* out_dists);
+/* PQ traversal (as gofann_pq_search, routes in id order, launch_order
+ * NULL) in chunks of chunk_routes on the context's stream; each chunk's
+ * shortlist (params->result_width ids) is copied to pinned host memory on a
+ * copy stream after the chunk's event and reranked on the host while later
+ * chunks search.  route_query_host: host copy of routes->route_query;
+ * out_ids / out_dists: host [routes][topk].  Returns when every route is
+ * reranked. */
+int gofann_pq_search_host_rerank(gofann_ctx* ctx, gofann_host_rerank* hr, const gofann_pq_view* pq,
+                                 const void* queries, int query_elem,
+                                 const gofann_graph_view* graph,
+                                 const gofann_predicate_view* predicate,
+                                 const gofann_routes* routes, const gofann_search_params* params,
+                                 const uint32_t* route_query_host, uint32_t chunk_routes,
+                                 uint32_t topk, uint32_t* out_ids, float* out_dists,
+                                 gofann_route_stats* stats);
+/* Host route -> query merge (merge_route_results_to_original,
+ * rabitq_lowfreq_merge.h:709-815); host arrays, as gofann_merge_routes. */
+int gofann_host_merge_routes(const uint32_t* query_route_offsets, const uint32_t* query_routes,
+                             const uint32_t* route_ids, const float* route_dists, uint32_t width,
+                             uint32_t queries, uint32_t topk, uint32_t* out_ids, float* out_dists);
+
 #ifdef __cplusplus
 }
 #endif

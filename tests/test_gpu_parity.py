@@ -377,3 +377,38 @@ def test_merge_routes_matches_oracle(gpu_ctx):
         torch.cuda.synchronize()
         assert np.array_equal(as_u32(gi_).reshape(queries, topk), oi)
         assert np.array_equal(gd.cpu().numpy().reshape(queries, topk).view(np.uint32), od.view(np.uint32))
+
+
+@pytest.mark.parametrize("chunk", [7, 1000])
+def test_pq_search_streamed_host_rerank(gpu_ctx, world, chunk):
+    """Chunked GPU traversal with the shortlist streamed through pinned host
+    memory to the CPU rerank pool equals one traversal launch followed by
+    the same rerank, and its shortlists equal the oracle's."""
+    kind, wl, li, pl = world
+    say("streamed host rerank", kind, chunk)
+    table, codes = _pq(wl, 16)
+    rs = pl.graph
+    W, topk = 40, 10
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+    keep = (codes.cuda(), table.cuda())
+    pqv = gs.pq_view(*keep)
+    prm = gs.search_params(queue_limit=48, result_width=W)
+    ids, dists, st = gs.run_pq_routes(gpu_ctx, pqv, wl.queries.cuda(), dg, dr, prm)
+    torch.cuda.synchronize()
+    shortlist = as_u32(ids).reshape(rs.count, W)
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, wl.base_ranges, alpha=0.15,
+                                          pending_base_stop=True)
+    oi, _, _ = po.pq_search(li, rs, pred_o, po.params(queue_limit=48, result_width=W),
+                            codes.numpy(), table.numpy(), wl.queries.numpy())
+    assert np.array_equal(shortlist, oi)
+    base = wl.base.numpy()
+    hr = gs.HostRerank(base, wl.queries.numpy(), threads=4)
+    ri, rd = hr.rerank(shortlist, rs.route_query, topk)
+    st2 = torch.zeros_like(st)
+    si, sd = hr.search(gpu_ctx, pqv, wl.queries.cuda(), dg, dr, prm, rs.route_query, chunk, topk,
+                       stats=st2)
+    hr.close()
+    assert np.array_equal(si, ri)
+    assert np.array_equal(sd.view(np.uint32), rd.view(np.uint32))
+    assert torch.equal(st, st2)

@@ -1,0 +1,83 @@
+"""Host-side (CPU) parts of the C-ABI library: the exact rerank worker pool
+and the route -> query merge, against the oracle on seeded inputs.  These
+entry points touch no GPU, so they run in the CPU suite."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+from gofann_amd import search as gs
+
+U32MAX = 0xFFFFFFFF
+
+
+def _shortlists(rng, routes, width, samples, dup=True):
+    sl = rng.integers(0, samples, size=(routes, width)).astype(np.uint32)
+    sl[rng.random((routes, width)) < 0.1] = U32MAX           # empty slots
+    sl[rng.random((routes, width)) < 0.05] = samples + 7     # ids past the base
+    if dup:
+        sl[:, -3:] = sl[:, :3]                               # duplicates
+    return sl
+
+
+@pytest.mark.parametrize("elem", ["u8", "f32", "f16"])
+@pytest.mark.parametrize("threads", [1, 4])
+def test_host_rerank_matches_oracle(elem, threads):
+    rng = np.random.default_rng(11)
+    n, dim, nq, routes, width, topk = 3000, 40, 30, 200, 60, 10
+    if elem == "u8":
+        base = rng.integers(0, 256, size=(n, dim)).astype(np.uint8)
+        queries = rng.integers(0, 256, size=(nq, dim)).astype(np.uint8)
+    else:
+        base = rng.standard_normal((n, dim)).astype(np.float32 if elem == "f32" else np.float16)
+        queries = rng.standard_normal((nq, dim)).astype(np.float32)
+    rq = rng.integers(0, nq, size=routes).astype(np.uint32)
+    sl = _shortlists(rng, routes, width, n)
+    oi, od = po.rerank(base, queries, rq, sl, topk)
+    hr = gs.HostRerank(base, queries, threads=threads)
+    hi, hd = hr.rerank(sl, rq, topk)
+    hr.close()
+    if elem == "u8":
+        # both sums of squared u8 differences are exact integers: same bits
+        assert np.array_equal(hi, oi)
+        assert np.array_equal(hd.view(np.uint32), od.view(np.uint32))
+    else:
+        # fp32 sequential order (host) vs the 64-lane order (oracle/GPU):
+        # 1e-5 relative, the north star's rerank tolerance
+        assert np.allclose(hd, od, rtol=1e-5, atol=0)
+        assert (hi == oi).mean() > 0.99
+    # ascending by (distance, id), padding last
+    for r in range(routes):
+        valid = hi[r] != U32MAX
+        d = hd[r][valid]
+        assert np.all(d[:-1] <= d[1:])
+        assert np.all(hd[r][~valid] == np.finfo(np.float32).max)
+
+
+def test_host_rerank_matches_brute_force_u8():
+    rng = np.random.default_rng(5)
+    base = rng.integers(0, 256, size=(500, 192)).astype(np.uint8)
+    queries = rng.integers(0, 256, size=(4, 192)).astype(np.uint8)
+    sl = np.tile(np.arange(500, dtype=np.uint32)[None, :], (4, 1))
+    hr = gs.HostRerank(base, queries, threads=2)
+    ids, dists = hr.rerank(sl, np.arange(4, dtype=np.uint32), 10)
+    hr.close()
+    for q in range(4):
+        d = ((base.astype(np.int64) - queries[q].astype(np.int64)) ** 2).sum(1)
+        order = np.lexsort((np.arange(500), d))[:10]
+        assert np.array_equal(ids[q], order.astype(np.uint32))
+        assert np.array_equal(dists[q], d[order].astype(np.float32))
+
+
+def test_host_merge_matches_oracle():
+    rng = np.random.default_rng(3)
+    routes, width, queries, topk = 300, 10, 120, 10
+    r2q = rng.integers(0, queries, size=routes).astype(np.uint32)
+    ids = rng.integers(0, 400, size=(routes, width)).astype(np.uint32)
+    ids[rng.random((routes, width)) < 0.1] = U32MAX
+    d = rng.integers(0, 50, size=(routes, width)).astype(np.float32)  # ties on purpose
+    oi, od = po.merge(r2q, ids, d, queries, topk)
+    hi, hd = gs.host_merge_routes(r2q, ids, d, queries, topk)
+    assert np.array_equal(hi, oi)
+    assert np.array_equal(hd.view(np.uint32), od.view(np.uint32))
