@@ -62,6 +62,13 @@ def parse():
                     help="gather neighbour sample ids through row_to_sample")
     ap.add_argument("--no-records", action="store_true",
                     help="separate code rows and CSR labels instead of 64-byte sample records")
+    ap.add_argument("--no-cpu-rerank-route", action="store_true",
+                    help="skip the GPU+CPU-rerank route measurement")
+    ap.add_argument("--rerank-threads", type=int, default=16,
+                    help="host rerank workers (the GPU box's CPU share is 16 threads)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="end with a 1 GiB fp32 negation (reads and writes 1 GiB) as the "
+                         "copy kernel that calibrates FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -157,6 +164,7 @@ class Pipeline:
         self.keep = (codes, table)
         self.pqv = gs.pq_view(self.records if records else codes, table,
                               wl.base if inline else None)
+        self.pqv_adc = gs.pq_view(self.records if records else codes, table, None)
         self.q = wl.queries
         self.dr_graph = gs.DeviceRoutes.upload(pl.graph)
         self.dr_post = gs.DeviceRoutes.upload(pl.posting)
@@ -236,6 +244,48 @@ class Pipeline:
 
     def route_stats(self) -> np.ndarray:
         return self.stats[: self.n_graph * 8].cpu().numpy().reshape(-1, 8)
+
+
+class CpuRerankRoute:
+    """The GPU+CPU-rerank route (the reference's default schedule): graph
+    routes ranked by ADC emit a 100-wide shortlist; the traversal runs in
+    route chunks and each chunk's shortlist streams through pinned host
+    memory to a host worker pool for exact u8 rerank while later chunks
+    search (gofann_pq_search_host_rerank); posting routes are scanned on the
+    GPU and reranked on the host; routes merge per query on the host."""
+
+    def __init__(self, pipe, threads=16, chunks=16, width=100):
+        gs = pipe.gs
+        self.pipe, self.gs, self.width = pipe, gs, width
+        self.hr = gs.HostRerank(pipe.wl.base.cpu().numpy(), pipe.wl.queries.cpu().numpy(),
+                                threads=threads)
+        self.threads = threads
+        self.chunk = max(1, (pipe.n_graph + chunks - 1) // chunks)
+        self.r2q = np.concatenate([pipe.pl.graph.route_to_query, pipe.pl.posting.route_to_query])
+        self.ids = np.empty((pipe.n_graph + pipe.n_post, 10), np.uint32)
+        self.dists = np.empty((pipe.n_graph + pipe.n_post, 10), np.float32)
+
+    def step(self, Q: int, width: int | None = None) -> np.ndarray:
+        p, gs = self.pipe, self.gs
+        ng, npost = p.n_graph, p.n_post
+        prm = gs.search_params(queue_limit=Q, result_width=width or self.width,
+                               inline_exact=False, table_mode=p.table_mode,
+                               hash_mode=p.hash_mode)
+        if ng:
+            self.hr.search(p.ctx, p.pqv_adc, p.q, p.dg, p.dr_graph, prm, p.pl.graph.route_query,
+                           self.chunk, 10, records=p.records,
+                           out=(self.ids[:ng], self.dists[:ng]))
+        if npost:
+            p._posting_scan(p.sl_ids, p.sl_d)
+            p.torch.cuda.synchronize()
+            sl = p.sl_ids[: npost * p.W].cpu().numpy().view(np.uint32).reshape(npost, p.W)
+            pi, pd = self.hr.rerank(sl, p.pl.posting.route_query, 10)
+            self.ids[ng:], self.dists[ng:] = pi, pd
+        out_i, _ = gs.host_merge_routes(self.r2q, self.ids, self.dists, p.pl.queries, 10)
+        return out_i
+
+    def close(self):
+        self.hr.close()
 
 
 def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes: int,
@@ -382,6 +432,32 @@ def main():
         f"steps/route {st[:, 0].mean():.1f}, scored/route {st[:, 3].mean():.1f}, "
         f"admitted/route {st[:, 6].mean():.1f}, placement {placed}")
 
+    route2 = None
+    if not args.no_cpu_rerank_route:
+        r2 = CpuRerankRoute(pipe, threads=args.rerank_threads)
+        # (beam, shortlist width): the ADC-ranked shortlist limits recall at
+        # wide beams, so the ladder widens it with the beam
+        rung = [(64, 100), (96, 100), (128, 100), (192, 200), (256, 200), (384, 200)]
+        (q2, w2), rec2 = rung[-1], 0.0
+        for Q2, W2 in rung:
+            rec2 = recall_at_10(r2.step(Q2, W2), gt)
+            log(f"GPU+CPU-rerank route Q={Q2} W={W2}: recall@10={rec2:.4f}")
+            q2, w2 = Q2, W2
+            if rec2 >= args.target_recall:
+                break
+        r2.step(q2, w2)
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            res2 = r2.step(q2, w2)
+        ms2 = (time.perf_counter() - t0) * 1000.0 / args.steps
+        rec2 = recall_at_10(res2, gt)
+        route2 = {"qps": round(pl.queries / (ms2 / 1000.0), 1), "ms_per_step": round(ms2, 3),
+                  "queue": q2, "recall_at_10": round(rec2, 4), "shortlist": w2,
+                  "host_threads": args.rerank_threads, "chunks": 16,
+                  "rerank": "exact u8 on the host, streamed behind the GPU search"}
+        log(f"GPU+CPU-rerank route: {route2}")
+        r2.close()
+
     cpu = None
     if not args.no_cpu_baseline:
         cq, cn, cel = cpu_baseline(wl, li, table, codes, pl, chosen, args.cpu_seconds, inline)
@@ -412,7 +488,8 @@ def main():
                    "recall_at_10": round(rec, 4),
                    "gt_queries": len(gt), "placement": placed,
                    "neighbor_samples": not args.no_neighbor_samples,
-                   "sample_records": not args.no_records},
+                   "sample_records": not args.no_records,
+                   "gpu_cpu_rerank_route": route2},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 5),
                      "traffic": measured_traffic(chosen, placed, not args.no_records),
@@ -421,6 +498,13 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    if args.calibrate_copy:
+        x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        torch.neg(x, out=y)
+        torch.cuda.synchronize()
+        log("copy calibration: torch.neg over 1 GiB fp32 (1 GiB read, 1 GiB written)")
     ctx.close()
 
 
