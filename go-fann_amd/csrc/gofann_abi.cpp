@@ -205,6 +205,21 @@ int gofann_rabitq_posting_scan(gofann_ctx* c, const gofann_rabitq_view* rq,
     });
 }
 
+int gofann_rabitq_range_scan(gofann_ctx* c, const gofann_rabitq_view* rq,
+                             const gofann_rabitq_queries* prepared,
+                             const gofann_predicate_view* predicate, const gofann_routes* routes,
+                             const uint32_t* posting_sample_ids, uint64_t resident_rows,
+                             const gofann_posting_segments* segments, int shortlist_k,
+                             int score_first, uint32_t* out_ids, float* out_dists,
+                             uint32_t* pass_counts)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::rabitq_range_scan(ctx, rq, prepared, predicate, routes, posting_sample_ids,
+                                         resident_rows, segments, shortlist_k, score_first,
+                                         out_ids, out_dists, pass_counts);
+    });
+}
+
 int gofann_exact_rerank(gofann_ctx* c, const void* base, int base_elem, uint32_t dim,
                         uint32_t samples, const void* queries, const uint32_t* route_query,
                         const uint32_t* shortlist, uint32_t width, uint32_t routes, uint32_t topk,

@@ -16,7 +16,13 @@ namespace gofann {
 // the grow-only device scratch buffers of one host thread's search state
 // (the reference's per-context buffers, backend_pq.cu:6753-6990).
 struct Context {
-    enum ScratchSlot { kScratchHash = 0, kScratchSegments = 1, kScratchMisc = 2, kScratchCount = 3 };
+    enum ScratchSlot {
+        kScratchHash = 0,
+        kScratchSegments = 1,
+        kScratchMisc = 2,
+        kScratchRange = 3,  // per-segment range-scan shortlists before the merge
+        kScratchCount = 4
+    };
 
     int device = 0;
     hipStream_t stream = nullptr;
@@ -24,8 +30,8 @@ struct Context {
     int lds_per_block = 0;
     int lds_per_cu = 0;
     std::string error;
-    void* scratch_ptr[kScratchCount] = {nullptr, nullptr, nullptr};
-    size_t scratch_bytes[kScratchCount] = {0, 0, 0};
+    void* scratch_ptr[kScratchCount] = {};
+    size_t scratch_bytes[kScratchCount] = {};
     // Placement chosen by the last traversal launch (diagnostics).
     int last_hash_in_lds = 0;
     int last_table_in_lds = 0;
@@ -81,6 +87,12 @@ int predicate_masks(Context* ctx, const gofann_predicate_view* pred, const uint3
 int merge_routes(Context* ctx, const uint32_t* q_route_offsets, const uint32_t* q_routes,
                  const uint32_t* route_ids, const float* route_dists, uint32_t width,
                  uint32_t queries, uint32_t topk, uint32_t* out_ids, float* out_dists);
+int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
+                      const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
+                      const gofann_routes* routes, const uint32_t* posting,
+                      uint64_t resident_rows, const gofann_posting_segments* seg,
+                      int shortlist_k, int score_first, uint32_t* out_ids, float* out_dists,
+                      uint32_t* pass_counts);
 int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
                    uint32_t count, const float* rotation, gofann_rabitq_queries* out);
 

@@ -1,0 +1,462 @@
+// range_scan.hip -- RaBitQ range-posting scan over posting segments and the
+// per-query segment merge on gfx950.
+//
+// Reference: range_posting_rabitq_scan_kernel (src/search/rabitq/
+// backend_rabitq.cu:5846-6015), posting_segments::merge_one_query /
+// merge_shortlists (src/search/common/posting_segment_merge.cuh:12-61) and
+// the host segment plan posting_segments::make_plan (src/execution/
+// posting_segment_plan.h:20-51, implemented in range_posting.cpp).
+//
+// Segment s scans the sample ids posting[offsets[s] .. + sizes[s]) (clipped
+// to resident_rows) for route route_ids[s].  A row is skipped when its
+// sample is >= base_rows or the route has no active range.  Filter-first: an
+// enabled predicate decides; otherwise, with more than one active range,
+// every active range must match (the posting slice already satisfies one);
+// a single active range passes by construction.  Score-first (requested and
+// the predicate enabled): the predicate is consulted only for rows that can
+// enter the shortlist.  Pass counts: filter-first counts every row that
+// passes the filter; score-first counts the rows that could enter the heap
+// at their scan position and matched.
+//
+// One 256-thread workgroup per segment.  A chunk of rows is scored in
+// parallel into LDS at its scan positions; rows whose (distance, id) is not
+// below the running k-th pair are dropped at once (they could not enter the
+// heap).  The survivors are merged into the running top-k: with none the
+// chunk costs nothing more, with at most k_pow2 they are sorted on their
+// own and bitonic-merged with the running list, otherwise the whole LDS
+// region is sorted.  The running list is the k least admissible pairs of
+// the rows scanned so far -- the multiset the reference heap holds -- so the
+// ascending output equals the reference heap sorted.
+//
+// Score-first pass counts: a row enters the reference heap iff fewer than k
+// admitted rows before it are <= it in (distance, id) order.  Rows of
+// earlier chunks are counted by binary search in the running list (only its
+// first k matter), rows earlier in the same chunk by a scan of the
+// survivors before it (a dropped row is larger than every survivor).
+//
+// Merge: output row p takes the segments [query_indptr[p], [p+1]); each
+// segment's sorted list is bitonic-merged into the running top-k (skipped
+// when its best pair cannot enter) and the pass counts are summed, as
+// merge_one_query's heap inserts do.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+#include "device_common.hpp"
+#include "gofann_internal.hpp"
+#include "scan_common.hpp"
+
+namespace gofann {
+
+constexpr int kRangeMaxShortlist = 4096;  // max_range_posting_postfilter_shortlist
+
+struct RangeScanArgs {
+    gofann_predicate_view pred;
+    gofann_routes routes;  // route_query + the query range table
+    const uint32_t* posting;
+    uint64_t resident_rows;
+    const uint32_t* seg_route;
+    const uint64_t* seg_offset;
+    const uint64_t* seg_size;
+    uint32_t segments;
+    uint32_t base_rows;
+    int k;
+    int k_pow2;
+    int slots;        // LDS pairs, a power of two >= k_pow2 + chunk and >= 2 k_pow2
+    int chunk;        // rows scored per pass: 1024 or 2048 (4 or 8 per thread)
+    uint32_t planes_bytes;
+    int score_first;
+    uint32_t* out_ids;
+    float* out_dists;
+    uint32_t* pass_counts;
+};
+
+__device__ __forceinline__ bool pair_le(float ad, uint32_t aid, float bd, uint32_t bid)
+{
+    return !pair_less(bd, bid, ad, aid);
+}
+
+// Entries of the ascending list (d, id)[0, n) that are <= (x, xid).
+__device__ __forceinline__ int count_le(const float* d, const uint32_t* id, int n, float x,
+                                        uint32_t xid)
+{
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (pair_le(d[mid], id[mid], x, xid))
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+// Bitonic merge of [0, n): the first half ascending, the second half
+// non-increasing; result ascending.
+__device__ inline void bitonic_merge(float* d, uint32_t* id, int n, int tid, int nthreads)
+{
+    for (int stride = n >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < n / 2; i += nthreads) {
+            const int lo = 2 * i - (i & (stride - 1));
+            const int hi = lo + stride;
+            if (pair_less(d[hi], id[hi], d[lo], id[lo])) {
+                const float td = d[lo];
+                d[lo] = d[hi];
+                d[hi] = td;
+                const uint32_t ti = id[lo];
+                id[lo] = id[hi];
+                id[hi] = ti;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Sort [base, base + n) descending (n a power of two).
+__device__ inline void bitonic_sort_desc(float* d, uint32_t* id, int base, int n, int tid,
+                                         int nthreads)
+{
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < n / 2; i += nthreads) {
+                const int lo = base + 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool descending = ((lo - base) & size) == 0;
+                const bool swap = descending ? pair_less(d[lo], id[lo], d[hi], id[hi])
+                                             : pair_less(d[hi], id[hi], d[lo], id[lo]);
+                if (swap) {
+                    const float td = d[lo];
+                    d[lo] = d[hi];
+                    d[hi] = td;
+                    const uint32_t ti = id[lo];
+                    id[lo] = id[hi];
+                    id[hi] = ti;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ int pow2_ceil(int x)
+{
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+
+__global__ __launch_bounds__(kScanThreads) void range_scan_kernel(RangeScanArgs a,
+                                                                  RabitqScanScorer sc)
+{
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ uint32_t s_surv;
+    __shared__ uint32_t s_pass;
+    __shared__ uint32_t s_slot;
+    const int tid = static_cast<int>(threadIdx.x);
+    const uint32_t seg = blockIdx.x;
+    if (seg >= a.segments) return;
+    float* s_d = reinterpret_cast<float*>(lds + a.planes_bytes);
+    uint32_t* s_id = reinterpret_cast<uint32_t*>(s_d + a.slots);
+
+    const uint32_t route = a.seg_route[seg];
+    sc.setup(a.routes.route_query[route], tid, lds);
+    for (int i = tid; i < a.slots; i += kScanThreads) {
+        s_d[i] = FLT_MAX;
+        s_id[i] = UINT32_MAX;
+    }
+    if (tid == 0) s_pass = 0;
+
+    // :5895-5902
+    const uint64_t begin = a.seg_offset[seg];
+    uint64_t count = a.seg_size[seg];
+    if (begin > a.resident_rows)
+        count = 0;
+    else if (count > a.resident_rows - begin)
+        count = a.resident_rows - begin;
+    const uint32_t active = count_active_ranges(a.routes.range_modes, route, a.routes.range_count);
+    if (active == 0) count = 0;  // :5917
+    const bool enabled = pred_enabled(a.pred, route);
+    const bool score_first = a.score_first != 0 && enabled;
+    const int k = a.k, kp = a.k_pow2;
+    const int chunk = a.chunk;
+    uint32_t passes = 0;
+    uint32_t surv_total = 0;  // s_surv only grows: a chunk's survivors are its increment
+    if (tid == 0) s_surv = 0;
+    __syncthreads();
+
+    for (uint64_t base = 0; base < count; base += static_cast<uint64_t>(chunk)) {
+        const float kth_d = s_d[k - 1];
+        const uint32_t kth_id = s_id[k - 1];
+        uint32_t surv = 0;
+        for (int i = tid; i < chunk; i += kScanThreads) {
+            const uint64_t j = base + static_cast<uint64_t>(i);
+            float d = FLT_MAX;
+            uint32_t id = UINT32_MAX;
+            if (j < count) {
+                const uint32_t s = a.posting[begin + j];
+                bool ok = s < a.base_rows;
+                if (ok) {
+                    if (enabled) {
+                        PredCounters c{0, 0};
+                        ok = pred_matches(a.pred, route, s, c);
+                    } else if (active > 1) {
+                        ok = count_matching_ranges(a.routes, route, s) == active;
+                    }
+                }
+                if (ok) {
+                    if (!score_first) ++passes;
+                    const float v = sc.score(s);
+                    if (admissible(v, s) && pair_less(v, s, kth_d, kth_id)) {
+                        d = v;
+                        id = s;
+                        ++surv;
+                    }
+                }
+            }
+            s_d[kp + i] = d;
+            s_id[kp + i] = id;
+        }
+        if (surv) atomicAdd(&s_surv, surv);
+        __syncthreads();
+        const uint32_t now = s_surv;
+        const int m = static_cast<int>(now - surv_total);
+        surv_total = now;
+        if (m == 0) continue;  // uniform: nothing can enter
+        if (score_first) {
+            for (int i = tid; i < chunk; i += kScanThreads) {
+                const uint32_t xid = s_id[kp + i];
+                if (xid == UINT32_MAX) continue;
+                const float x = s_d[kp + i];
+                int c = count_le(s_d, s_id, k, x, xid);
+                for (int j = 0; j < i && c < k; ++j)
+                    if (s_id[kp + j] != UINT32_MAX && pair_le(s_d[kp + j], s_id[kp + j], x, xid)) ++c;
+                if (c < k) ++passes;
+            }
+        }
+        const int mp = pow2_ceil(m);
+        if (mp <= kp) {
+            // Gather the survivors at the tail of [kp, 2kp), sort them
+            // descending, then merge with the ascending running list.
+            float keep_d[8];
+            uint32_t keep_id[8];
+            int nk = 0;
+            const int per = chunk / kScanThreads;  // 4 or 8 (see the launcher)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = tid + t * kScanThreads;
+                keep_d[t] = t < per ? s_d[kp + i] : FLT_MAX;
+                keep_id[t] = t < per ? s_id[kp + i] : UINT32_MAX;
+                nk += keep_id[t] != UINT32_MAX ? 1 : 0;
+            }
+            if (tid == 0) s_slot = 0;
+            __syncthreads();
+            for (int i = tid; i < kp; i += kScanThreads) {
+                s_d[kp + i] = FLT_MAX;
+                s_id[kp + i] = UINT32_MAX;
+            }
+            __syncthreads();
+            if (nk) {
+                uint32_t at = atomicAdd(&s_slot, static_cast<uint32_t>(nk));
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    if (keep_id[t] == UINT32_MAX) continue;
+                    const int pos = 2 * kp - mp + static_cast<int>(at++);
+                    s_d[pos] = keep_d[t];
+                    s_id[pos] = keep_id[t];
+                }
+            }
+            __syncthreads();
+            bitonic_sort_desc(s_d, s_id, 2 * kp - mp, mp, tid, kScanThreads);
+            bitonic_merge(s_d, s_id, 2 * kp, tid, kScanThreads);
+        } else {
+            bitonic_sort(s_d, s_id, a.slots, tid, kScanThreads);
+        }
+    }
+    if (passes) atomicAdd(&s_pass, passes);
+    __syncthreads();
+    for (int i = tid; i < k; i += kScanThreads) {
+        a.out_ids[static_cast<size_t>(seg) * k + i] = s_id[i];
+        a.out_dists[static_cast<size_t>(seg) * k + i] = s_d[i];
+    }
+    if (tid == 0 && a.pass_counts) a.pass_counts[seg] = s_pass;
+}
+
+struct SegmentMergeArgs {
+    const uint32_t* query_indptr;
+    uint32_t positions;
+    const uint32_t* seg_ids;
+    const float* seg_dists;
+    const uint32_t* seg_pass;
+    int k;
+    int k_pow2;
+    uint32_t* out_ids;
+    float* out_dists;
+    uint32_t* out_pass;
+};
+
+__global__ __launch_bounds__(kScanThreads) void segment_merge_kernel(SegmentMergeArgs a)
+{
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = static_cast<int>(threadIdx.x);
+    const uint32_t p = blockIdx.x;
+    if (p >= a.positions) return;
+    const int k = a.k, kp = a.k_pow2;
+    float* s_d = reinterpret_cast<float*>(lds);
+    uint32_t* s_id = reinterpret_cast<uint32_t*>(s_d + 2 * kp);
+    for (int i = tid; i < kp; i += kScanThreads) {
+        s_d[i] = FLT_MAX;
+        s_id[i] = UINT32_MAX;
+    }
+    __syncthreads();
+    uint32_t passes = 0;
+    const uint32_t first = a.query_indptr[p], last = a.query_indptr[p + 1];
+    for (uint32_t part = first; part < last; ++part) {
+        passes += a.seg_pass[part];
+        const size_t o = static_cast<size_t>(part) * k;
+        // A segment's list is ascending: when its best pair cannot enter,
+        // none of it can.
+        const bool skip = !pair_less(a.seg_dists[o], a.seg_ids[o], s_d[k - 1], s_id[k - 1]);
+        if (skip) continue;  // uniform
+        for (int i = tid; i < kp; i += kScanThreads) {
+            // reversed into [kp, 2kp): non-increasing, padding first
+            const int src = kp - 1 - i;
+            const bool in = src < k && admissible(a.seg_dists[o + src], a.seg_ids[o + src]);
+            s_d[kp + i] = in ? a.seg_dists[o + src] : FLT_MAX;
+            s_id[kp + i] = in ? a.seg_ids[o + src] : UINT32_MAX;
+        }
+        __syncthreads();
+        bitonic_merge(s_d, s_id, 2 * kp, tid, kScanThreads);
+    }
+    for (int i = tid; i < k; i += kScanThreads) {
+        a.out_ids[static_cast<size_t>(p) * k + i] = s_id[i];
+        a.out_dists[static_cast<size_t>(p) * k + i] = s_d[i];
+    }
+    if (tid == 0 && a.out_pass) a.out_pass[p] = passes;
+}
+
+namespace {
+int pow2_at_least(int x)
+{
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+}  // namespace
+
+int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
+                      const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
+                      const gofann_routes* routes, const uint32_t* posting,
+                      uint64_t resident_rows, const gofann_posting_segments* seg,
+                      int shortlist_k, int score_first, uint32_t* out_ids, float* out_dists,
+                      uint32_t* pass_counts)
+{
+    if (!rq || !pre || !rq->codes || !rq->factors || !rq->anchor_ids || rq->padded_dim == 0 ||
+        rq->padded_dim % 128 != 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view invalid for range scan");
+    if (!pre->q8 || !pre->scale || !pre->k1 || !pre->centroid_dists)
+        return ctx->fail(GOFANN_ERR_INVALID, "prepared RaBitQ queries incomplete");
+    if (!routes || !routes->route_query || !seg)
+        return ctx->fail(GOFANN_ERR_INVALID, "range scan routes or segments missing");
+    if (shortlist_k < 1 || shortlist_k > kRangeMaxShortlist)
+        return ctx->fail(GOFANN_ERR_INVALID, "shortlist_k must be in [1, 4096]");
+    if (!out_ids || !out_dists)
+        return ctx->fail(GOFANN_ERR_INVALID, "range scan outputs missing");
+    if (seg->count == 0) {
+        if (seg->query_indptr && seg->positions)
+            return ctx->fail(GOFANN_ERR_INVALID, "segment plan has positions but no segments");
+        return GOFANN_OK;
+    }
+    if (!seg->route_ids || !seg->offsets || !seg->sizes || (seg->count && !posting))
+        return ctx->fail(GOFANN_ERR_INVALID, "segment plan arrays missing");
+
+    const bool merged = seg->query_indptr != nullptr;
+    uint32_t* scan_ids = out_ids;
+    float* scan_dists = out_dists;
+    uint32_t* scan_pass = pass_counts;
+    const size_t slots_out = static_cast<size_t>(seg->count) * static_cast<size_t>(shortlist_k);
+    if (merged) {
+        const size_t bytes = slots_out * 8 + static_cast<size_t>(seg->count) * 4 + 64;
+        unsigned char* buf = static_cast<unsigned char*>(ctx->scratch(Context::kScratchRange, bytes));
+        if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "range segment scratch allocation failed");
+        scan_ids = reinterpret_cast<uint32_t*>(buf);
+        scan_dists = reinterpret_cast<float*>(buf + slots_out * 4);
+        scan_pass = reinterpret_cast<uint32_t*>(buf + slots_out * 8);
+    }
+
+    RangeScanArgs a;
+    a.pred = pred ? *pred : gofann_predicate_view{};
+    a.routes = *routes;
+    a.posting = posting;
+    a.resident_rows = resident_rows;
+    a.seg_route = seg->route_ids;
+    a.seg_offset = seg->offsets;
+    a.seg_size = seg->sizes;
+    a.segments = seg->count;
+    a.base_rows = rq->samples;
+    a.k = shortlist_k;
+    a.k_pow2 = pow2_at_least(shortlist_k);
+    // LDS pairs [0, k_pow2) hold the running list, [k_pow2, k_pow2 + chunk)
+    // the chunk being scored; the rest stays padding.  At most 8 rows per
+    // thread (the survivor gather keeps them in registers).
+    a.chunk = a.k_pow2 <= 1024 ? 1024 : 2048;
+    a.slots = pow2_at_least(a.k_pow2 + a.chunk);
+    a.planes_bytes = rq->padded_dim;  // 8 bit planes of padded_dim bits
+    a.score_first = score_first ? 1 : 0;
+    a.out_ids = scan_ids;
+    a.out_dists = scan_dists;
+    a.pass_counts = scan_pass;
+    if (a.chunk % kScanThreads != 0 || a.chunk / kScanThreads > 8 || a.slots < 2 * a.k_pow2 ||
+        a.slots < a.k_pow2 + a.chunk)
+        return ctx->fail(GOFANN_ERR_INVALID, "range scan chunk layout invalid");
+
+    RabitqScanScorer sc;
+    sc.codes = rq->codes;
+    sc.factors = rq->factors;
+    sc.anchor_ids = rq->anchor_ids;
+    sc.q8 = pre->q8;
+    sc.q_scale = pre->scale;
+    sc.q_k1 = pre->k1;
+    sc.centroid_dists = pre->centroid_dists;
+    sc.num_anchors = rq->num_anchors;
+    sc.padded_dim = rq->padded_dim;
+    sc.planes = nullptr;
+    sc.scale = sc.k1 = 0.0f;
+    sc.g_row = nullptr;
+
+    const size_t lds = a.planes_bytes + static_cast<size_t>(a.slots) * 8;
+    if (lds > static_cast<size_t>(ctx->lds_per_block))
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "range scan LDS exceeds the workgroup limit");
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(range_scan_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
+        hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute range scan");
+    hipLaunchKernelGGL(range_scan_kernel, dim3(seg->count), dim3(kScanThreads), lds, ctx->stream,
+                       a, sc);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("range scan launch");
+    if (!merged) return GOFANN_OK;
+
+    SegmentMergeArgs m;
+    m.query_indptr = seg->query_indptr;
+    m.positions = seg->positions;
+    m.seg_ids = scan_ids;
+    m.seg_dists = scan_dists;
+    m.seg_pass = scan_pass;
+    m.k = shortlist_k;
+    m.k_pow2 = a.k_pow2;
+    m.out_ids = out_ids;
+    m.out_dists = out_dists;
+    m.out_pass = pass_counts;
+    if (seg->positions == 0) return GOFANN_OK;
+    const size_t mlds = static_cast<size_t>(2 * a.k_pow2) * 8;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(segment_merge_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mlds)) !=
+        hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute segment merge");
+    hipLaunchKernelGGL(segment_merge_kernel, dim3(seg->positions), dim3(kScanThreads), mlds,
+                       ctx->stream, m);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("segment merge launch");
+    return GOFANN_OK;
+}
+
+}  // namespace gofann

@@ -16,6 +16,7 @@ _HERE = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("GOFANN_HIP_LIB", str(_HERE.parent / "libgofann_hip.so")))
 
 GOFANN_OK = 0
+OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM = 0, -1, -2, -3, -4
 EARLY_STOP_FIXED, EARLY_STOP_OFF, EARLY_STOP_ADAPTIVE = 0, 1, 2
 ELEM_U8, ELEM_F32, ELEM_F16 = 0, 1, 2
 PLACE_AUTO, PLACE_LDS, PLACE_GLOBAL, PLACE_SPILL = 0, 1, 2, 3
@@ -89,6 +90,11 @@ class RabitqQueries(C.Structure):
                 ("centroid_dists", P), ("count", U32)]
 
 
+class PostingSegments(C.Structure):
+    _fields_ = [("route_ids", P), ("offsets", P), ("sizes", P), ("count", U32),
+                ("query_indptr", P), ("positions", U32)]
+
+
 # Every symbol include/gofann_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "gofann_create": (C.c_int, [C.c_int, C.POINTER(P)]),
@@ -114,6 +120,13 @@ SIGNATURES = {
                                              C.POINTER(RabitqQueries),
                                              C.POINTER(PredicateView), P, P, P, P, U32,
                                              C.c_int, P, P, P]),
+    "gofann_posting_segment_plan": (C.c_int, [P, P, P, U32, U32, U32, P, P, P, P, P,
+                                              C.POINTER(U32)]),
+    "gofann_range_slices": (C.c_int, [P, P, P, U32, P, P, P, U32, P]),
+    "gofann_rabitq_range_scan": (C.c_int, [P, C.POINTER(RabitqView), C.POINTER(RabitqQueries),
+                                           C.POINTER(PredicateView), C.POINTER(Routes), P,
+                                           C.c_uint64, C.POINTER(PostingSegments), C.c_int,
+                                           C.c_int, P, P, P]),
     "gofann_exact_rerank": (C.c_int, [P, P, C.c_int, U32, U32, P, P, P, U32, U32, U32, P, P]),
     "gofann_merge_routes": (C.c_int, [P, P, P, P, P, U32, U32, U32, P, P]),
     "gofann_predicate_masks": (C.c_int, [P, C.POINTER(PredicateView), P, P, U32, P]),

@@ -271,6 +271,65 @@ int gofann_rabitq_posting_scan(gofann_ctx* ctx, const gofann_rabitq_view* rq,
                                uint32_t* out_ids, float* out_dists,
                                uint32_t* pass_counts);
 
+/* ---- range postings ------------------------------------------------------
+ * Posting segments (posting_segments::Plan, src/execution/
+ * posting_segment_plan.h:12-18).  Segment s scans posting rows
+ * [offsets[s], offsets[s] + sizes[s]) for route route_ids[s].  With
+ * query_indptr, output row p merges segments [query_indptr[p],
+ * query_indptr[p+1]); without it (NULL) segment s is output row s. */
+typedef struct {
+    const uint32_t* route_ids;     /* [count] */
+    const uint64_t* offsets;       /* [count] */
+    const uint64_t* sizes;         /* [count] */
+    uint32_t count;
+    const uint32_t* query_indptr;  /* [positions + 1] or NULL */
+    uint32_t positions;
+} gofann_posting_segments;
+
+/* Host: posting_segments::make_plan (posting_segment_plan.h:20-51) over
+ * host arrays -- each posting of n split into ceil(size / target_rows)
+ * near-equal segments (one empty segment for an empty posting).  Fills the
+ * outputs when capacity covers the plan; *out_count always receives the
+ * segment count.  Returns GOFANN_OK, or GOFANN_ERR_INVALID (target_rows 0,
+ * missing arrays, capacity short) / GOFANN_ERR_UNSUPPORTED (overflow). */
+int gofann_posting_segment_plan(const uint32_t* route_ids, const uint64_t* offsets,
+                                const uint64_t* sizes, uint32_t n, uint32_t target_rows,
+                                uint32_t capacity, uint32_t* seg_route_ids,
+                                uint32_t* seg_positions, uint64_t* seg_offsets,
+                                uint64_t* seg_sizes, uint32_t* query_indptr,
+                                uint32_t* out_count);
+
+/* Host: range_posting::choose_smallest_slice (src/index/
+ * range_posting_index.cpp:277-312) for rows [0, n) of a query range table
+ * (modes/lower/upper [n][range_count], host).  Dimension r of the ordered
+ * range posting index has unique_counts[r] strictly increasing values
+ * unique_values[r] and offsets[r] ([unique_counts[r] + 1] row offsets).
+ * out[q] = {has_active_range, active_dimension_count, range_index, begin,
+ * count} (begin dimension-local; range_index UINT32_MAX when none). */
+int gofann_range_slices(const float* const* unique_values, const uint64_t* const* offsets,
+                        const uint64_t* unique_counts, uint32_t range_count,
+                        const uint8_t* modes, const float* lower, const float* upper,
+                        uint32_t n, uint64_t* out);
+
+/* ---- RaBitQ range-posting scan (range_posting_rabitq_scan_kernel,
+ * backend_rabitq.cu:5846-6015) with the segment merge (merge_one_query,
+ * posting_segment_merge.cuh:12-46).  posting: [resident_rows] sample ids
+ * (device).  routes: route_query and the query range table (range_modes,
+ * range_lower, range_upper, base_range_values, range_count).  Rows with a
+ * sample >= rq->samples are skipped.  score_first: consult an enabled
+ * predicate only for rows that can enter the shortlist (results are the
+ * same; pass counts follow that order).  Outputs [rows][shortlist_k]
+ * ascending by (distance, id), padding UINT32_MAX / FLT_MAX; pass_counts
+ * [rows] (may be NULL); rows = positions with query_indptr, else
+ * segments.  shortlist_k <= 4096. */
+int gofann_rabitq_range_scan(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                             const gofann_rabitq_queries* prepared,
+                             const gofann_predicate_view* predicate,
+                             const gofann_routes* routes, const uint32_t* posting_sample_ids,
+                             uint64_t resident_rows, const gofann_posting_segments* segments,
+                             int shortlist_k, int score_first, uint32_t* out_ids,
+                             float* out_dists, uint32_t* pass_counts);
+
 /* ---- exact rerank on the GPU: per route, unique valid candidates of the
  * shortlist, exact L2 against base[samples][dim] (u8 / f32 / f16 with f32
  * queries for f32 and f16, u8 queries for u8), top-k by (distance, id). */

@@ -1144,6 +1144,131 @@ int orc_rabitq_posting_scan(const orc_predicate* pred, const uint8_t* codes,
 }
 
 /* ======================================================================
+ * Range postings -- segment plan (posting_segment_plan.h:20-51), range
+ * scan (backend_rabitq.cu:5846-6015) and segment merge
+ * (posting_segment_merge.cuh:12-46).
+ * ====================================================================== */
+int orc_segment_plan(const uint32_t* route_ids, const uint64_t* offsets, const uint64_t* sizes,
+                     uint32_t n, uint32_t target_rows, uint32_t capacity, uint32_t* seg_routes,
+                     uint32_t* seg_positions, uint64_t* seg_offsets, uint64_t* seg_sizes,
+                     uint32_t* query_indptr, uint32_t* out_count)
+{
+    if (target_rows == 0 || (n > 0 && (!route_ids || !offsets || !sizes))) return -1;
+    /* :30-38: an empty posting still yields one (empty) segment */
+    uint64_t total = 0;
+    for (uint32_t q = 0; q < n; ++q) {
+        if (offsets[q] > UINT64_MAX - sizes[q]) return -2;
+        const uint64_t count = sizes[q] == 0 ? 1 : 1 + (sizes[q] - 1) / target_rows;
+        if (count > (uint64_t)UINT32_MAX - total) return -2;
+        total += count;
+    }
+    if (out_count) *out_count = (uint32_t)total;
+    if (capacity < total || !seg_routes || !seg_positions || !seg_offsets || !seg_sizes ||
+        !query_indptr)
+        return 1;
+    uint32_t s = 0;
+    query_indptr[0] = 0;
+    for (uint32_t q = 0; q < n; ++q) {
+        const uint64_t rows = sizes[q];
+        const uint64_t count = rows == 0 ? 1 : 1 + (rows - 1) / target_rows;
+        /* :39-49: near-equal parts, the first `rows % count` one row longer */
+        const uint64_t width = rows / count, extra = rows % count;
+        for (uint64_t part = 0; part < count; ++part, ++s) {
+            seg_routes[s] = route_ids[q];
+            seg_positions[s] = q;
+            seg_offsets[s] = offsets[q] + part * width + (part < extra ? part : extra);
+            seg_sizes[s] = width + (part < extra ? 1 : 0);
+        }
+        query_indptr[q + 1] = s;
+    }
+    return 0;
+}
+
+int orc_rabitq_range_scan(const orc_predicate* pred, const orc_range_table* rt,
+                          const uint8_t* codes, uint32_t code_bytes, const float* factors,
+                          const uint32_t* anchor_ids, const int8_t* q8, const float* q_scale,
+                          const float* q_k1, const float* centroid_dists, uint32_t num_anchors,
+                          uint32_t padded_dim, const uint32_t* route_query,
+                          const uint32_t* posting, uint64_t resident_rows, uint32_t base_rows,
+                          const uint32_t* seg_routes, const uint64_t* seg_offsets,
+                          const uint64_t* seg_sizes, uint32_t segments, int shortlist_k,
+                          int score_first, uint32_t* out_ids, float* out_dists,
+                          uint32_t* pass_counts)
+{
+    rq_ctx ctx = {codes, code_bytes, factors, anchor_ids, q8, q_scale, q_k1,
+                  centroid_dists, num_anchors, padded_dim, 0};
+    for (uint32_t sg = 0; sg < segments; ++sg) {
+        float* bd = out_dists + (size_t)sg * shortlist_k;
+        uint32_t* bi = out_ids + (size_t)sg * shortlist_k;
+        for (int i = 0; i < shortlist_k; ++i) {
+            bd[i] = FLT_MAX;
+            bi[i] = UINT32_MAX;
+        }
+        const uint32_t route = seg_routes[sg];
+        ctx.query = route_query[route];
+        /* :5895-5902 clip to the resident rows */
+        const uint64_t begin = seg_offsets[sg];
+        uint64_t count = seg_sizes[sg];
+        if (begin > resident_rows)
+            count = 0;
+        else if (count > resident_rows - begin)
+            count = resident_rows - begin;
+        /* :5903-5913 */
+        const uint32_t active =
+            rt ? orc_count_active_ranges(rt->modes, route, rt->count) : 0;
+        const int enabled = orc_pred_enabled(pred, route);
+        const int sf = score_first && enabled;
+        uint32_t passes = 0;
+        for (uint64_t i = 0; i < count; ++i) {
+            const uint32_t s = posting[begin + i];
+            if (s >= base_rows || active == 0) continue;                    /* :5917 */
+            if (!sf && enabled) {                                            /* :5921-5923 */
+                if (!orc_pred_matches(pred, route, s, NULL)) continue;
+            } else if (!sf && active > 1) {                                  /* :5924-5934 */
+                if (orc_count_matching_ranges(rt->modes, rt->lower, rt->upper, rt->base_values,
+                                              route, s, rt->count) != active)
+                    continue;
+            }
+            const float d = rabitq_score(&ctx, route, s);
+            if (sf) {                                                        /* :5960-5970 */
+                if (!orc_shortlist_can_enter(d, s, bd, bi, shortlist_k)) continue;
+                if (!orc_pred_matches(pred, route, s, NULL)) continue;
+            }
+            ++passes;                                                        /* :5971-5975 */
+            orc_shortlist_insert(d, s, bd, bi, shortlist_k);
+        }
+        orc_shortlist_sort(bd, bi, shortlist_k);
+        if (pass_counts) pass_counts[sg] = passes;
+    }
+    return 0;
+}
+
+int orc_merge_segments(const uint32_t* query_indptr, uint32_t positions,
+                       const uint32_t* seg_ids, const float* seg_dists,
+                       const uint32_t* seg_pass, int shortlist_k, uint32_t* out_ids,
+                       float* out_dists, uint32_t* out_pass)
+{
+    for (uint32_t p = 0; p < positions; ++p) {
+        float* bd = out_dists + (size_t)p * shortlist_k;
+        uint32_t* bi = out_ids + (size_t)p * shortlist_k;
+        for (int i = 0; i < shortlist_k; ++i) {
+            bd[i] = FLT_MAX;
+            bi[i] = UINT32_MAX;
+        }
+        uint32_t passes = 0;
+        for (uint32_t part = query_indptr[p]; part < query_indptr[p + 1]; ++part) {
+            passes += seg_pass[part];
+            const size_t o = (size_t)part * shortlist_k;
+            for (int i = 0; i < shortlist_k; ++i)
+                orc_shortlist_insert(seg_dists[o + i], seg_ids[o + i], bd, bi, shortlist_k);
+        }
+        orc_shortlist_sort(bd, bi, shortlist_k);
+        if (out_pass) out_pass[p] = passes;
+    }
+    return 0;
+}
+
+/* ======================================================================
  * Resident posting producer -- src/search/pq/pq_resident_posting.cuh:27-58:
  * a route's posting slice is its group's [offset, offset + size) when it
  * fits the table; a row yields its sample only when the row mask shares a

@@ -245,6 +245,49 @@ int orc_rabitq_posting_scan(const orc_predicate* pred, const uint8_t* codes,
                             int shortlist_k, uint32_t* out_ids, float* out_dists,
                             uint32_t* pass_counts);
 
+/* ---------------- range posting segments and scan ----------------------
+ * Segment plan: posting_segments::make_plan (src/execution/
+ * posting_segment_plan.h:20-51).  Returns 0 and fills the arrays when
+ * capacity >= the segment count, 1 when capacity is short (out_count still
+ * receives the count), -1 on invalid input, -2 on overflow. */
+int orc_segment_plan(const uint32_t* route_ids, const uint64_t* offsets, const uint64_t* sizes,
+                     uint32_t n, uint32_t target_rows, uint32_t capacity, uint32_t* seg_routes,
+                     uint32_t* seg_positions, uint64_t* seg_offsets, uint64_t* seg_sizes,
+                     uint32_t* query_indptr, uint32_t* out_count);
+
+/* Per-route range table of the query (QueryRangeTable, dataloader.h:545). */
+typedef struct {
+    const uint8_t* modes;       /* [routes][count] */
+    const float* lower;
+    const float* upper;
+    const float* base_values;   /* [samples][count] */
+    uint32_t count;
+} orc_range_table;
+
+/* range_posting_rabitq_scan_kernel (backend_rabitq.cu:5846-6015): segment
+ * s scans posting[offsets[s] .. + sizes[s]) (clipped to resident_rows) for
+ * route seg_routes[s].  Outputs [segments][shortlist_k] ascending by
+ * (distance, id) (the kernel's heap holds the same multiset) and the
+ * per-segment exact pass count. */
+int orc_rabitq_range_scan(const orc_predicate* pred, const orc_range_table* ranges,
+                          const uint8_t* codes, uint32_t code_bytes, const float* factors,
+                          const uint32_t* anchor_ids, const int8_t* q8, const float* q_scale,
+                          const float* q_k1, const float* centroid_dists, uint32_t num_anchors,
+                          uint32_t padded_dim, const uint32_t* route_query,
+                          const uint32_t* posting, uint64_t resident_rows, uint32_t base_rows,
+                          const uint32_t* seg_routes, const uint64_t* seg_offsets,
+                          const uint64_t* seg_sizes, uint32_t segments, int shortlist_k,
+                          int score_first, uint32_t* out_ids, float* out_dists,
+                          uint32_t* pass_counts);
+
+/* merge_one_query (src/search/common/posting_segment_merge.cuh:12-46):
+ * position p merges segments [query_indptr[p], query_indptr[p+1]) through
+ * the shortlist heap and sums their pass counts; output ascending. */
+int orc_merge_segments(const uint32_t* query_indptr, uint32_t positions,
+                       const uint32_t* seg_ids, const float* seg_dists,
+                       const uint32_t* seg_pass, int shortlist_k, uint32_t* out_ids,
+                       float* out_dists, uint32_t* out_pass);
+
 /* ---------------- resident posting view (pq_resident_posting.cuh:27-58) */
 int orc_resident_bounds(const uint32_t* group_offsets, const uint32_t* group_sizes,
                         const uint32_t* query_groups, uint32_t groups, uint32_t rows,

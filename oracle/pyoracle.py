@@ -316,3 +316,111 @@ def merge(route_to_query, ids, dists, queries, topk):
     assert L.orc_merge_routes(p(r2q), U32(n), U32(queries), p(ids), p(dists), U32(width),
                               U32(topk), p(oi), p(od)) == 0
     return oi, od
+
+
+class RangeTable(C.Structure):
+    _fields_ = [("modes", P), ("lower", P), ("upper", P), ("base_values", P), ("count", U32)]
+
+
+def segment_plan(route_ids, offsets, sizes, target_rows):
+    """orc_segment_plan -> (routes, positions, offsets, sizes, indptr)."""
+    L = lib()
+    r = c_arr(route_ids, np.uint32)
+    o = c_arr(offsets, np.uint64)
+    s = c_arr(sizes, np.uint64)
+    n = r.size
+    cnt = U32(0)
+    rc = L.orc_segment_plan(p(r), p(o), p(s), U32(n), U32(target_rows), U32(0), None, None,
+                            None, None, None, C.byref(cnt))
+    if rc < 0:
+        return rc
+    m = cnt.value
+    out = (np.empty(m, np.uint32), np.empty(m, np.uint32), np.empty(m, np.uint64),
+           np.empty(m, np.uint64), np.empty(n + 1, np.uint32))
+    assert L.orc_segment_plan(p(r), p(o), p(s), U32(n), U32(target_rows), U32(m),
+                              *[p(a) for a in out], C.byref(cnt)) == 0
+    return out
+
+
+def ref_segment_plan(route_ids, offsets, sizes, target_rows):
+    """posting_segments::make_plan through oracle/_ref, or None."""
+    R = ref()
+    if R is None or not hasattr(R, "ref_segment_plan"):
+        return None
+    r = c_arr(route_ids, np.uint32)
+    o = c_arr(offsets, np.uint64)
+    s = c_arr(sizes, np.uint64)
+    n = r.size
+    cap = int(sum(max(1, -(-int(x) // target_rows)) for x in s)) + 1
+    out = (np.empty(cap, np.uint32), np.empty(cap, np.uint32), np.empty(cap, np.uint64),
+           np.empty(cap, np.uint64), np.empty(n + 1, np.uint32))
+    m = R.ref_segment_plan(p(r), p(o), p(s), U32(n), U32(target_rows), U32(cap),
+                           *[p(a) for a in out])
+    if m < 0:
+        return m
+    return tuple(a[:m] for a in out[:4]) + (out[4],)
+
+
+def ref_range_slices(path, modes, lower, upper):
+    """choose_smallest_slice over a FARPIDX1 file loaded by the reference
+    loader: ([n][5] uint64, row_count) or (None, message)."""
+    R = ref()
+    if R is None or not hasattr(R, "ref_range_slices"):
+        return None
+    modes = c_arr(modes, np.uint8)
+    n, rc = modes.shape
+    out = np.zeros((max(n, 1), 5), np.uint64)
+    rows = C.c_uint64(0)
+    err = C.create_string_buffer(512)
+    code = R.ref_range_slices(str(path).encode(), p(modes), p(c_arr(lower, np.float32)),
+                              p(c_arr(upper, np.float32)), U32(n), U32(rc), p(out),
+                              C.byref(rows), err, U32(512))
+    if code != 0:
+        return None, err.value.decode()
+    return out[:n], rows.value
+
+
+def rabitq_range_scan(pred, modes, lower, upper, base_values, codes, factors, anchor_ids, q8,
+                      q_scale, q_k1, centroid_dists, route_query, posting, resident_rows,
+                      base_rows, seg_routes, seg_offsets, seg_sizes, k, score_first=False):
+    """orc_rabitq_range_scan -> per-segment (ids, dists, passes)."""
+    L = lib()
+    modes = c_arr(modes, np.uint8)
+    lower, upper = c_arr(lower, np.float32), c_arr(upper, np.float32)
+    bv = c_arr(base_values, np.float32)
+    rt = RangeTable(p(modes), p(lower), p(upper), p(bv),
+                    U32(modes.shape[1] if modes is not None and modes.ndim == 2 else 0))
+    codes = c_arr(codes, np.uint8)
+    arrs = [c_arr(factors, np.float32), c_arr(anchor_ids, np.uint32), c_arr(q8, np.int8),
+            c_arr(q_scale, np.float32), c_arr(q_k1, np.float32),
+            c_arr(centroid_dists, np.float32)]
+    cd = arrs[5]
+    padded = int(np.asarray(q8).shape[1])
+    rq = c_arr(route_query, np.uint32)
+    post = c_arr(posting, np.uint32)
+    sr, so, ss = c_arr(seg_routes, np.uint32), c_arr(seg_offsets, np.uint64), c_arr(seg_sizes, np.uint64)
+    n = sr.size
+    ids = np.empty((max(n, 1), k), np.uint32)
+    dists = np.empty((max(n, 1), k), np.float32)
+    passes = np.empty(max(n, 1), np.uint32)
+    rc = L.orc_rabitq_range_scan(C.byref(pred.struct) if pred else None, C.byref(rt), p(codes),
+                                 U32(codes.shape[1]), *[p(a) for a in arrs], U32(cd.shape[1]),
+                                 U32(padded), p(rq), p(post), C.c_uint64(resident_rows), U32(base_rows),
+                                 p(sr), p(so), p(ss), U32(n), k, 1 if score_first else 0,
+                                 p(ids), p(dists), p(passes))
+    assert rc == 0
+    return ids[:n], dists[:n], passes[:n]
+
+
+def merge_segments(indptr, seg_ids, seg_dists, seg_pass, k):
+    """orc_merge_segments -> per-position (ids, dists, passes)."""
+    L = lib()
+    ip = c_arr(indptr, np.uint32)
+    n = ip.size - 1
+    ids = np.empty((max(n, 1), k), np.uint32)
+    dists = np.empty((max(n, 1), k), np.float32)
+    passes = np.empty(max(n, 1), np.uint32)
+    assert L.orc_merge_segments(p(ip), U32(n), p(c_arr(seg_ids, np.uint32)),
+                                p(c_arr(seg_dists, np.float32)), p(c_arr(seg_pass, np.uint32)),
+                                k, p(ids), p(dists), p(passes)) == 0
+    return ids[:n], dists[:n], passes[:n]

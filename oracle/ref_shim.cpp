@@ -10,14 +10,21 @@
 //   src/search/pq/pq_resident_posting.cuh    (bounds, candidate)
 //   src/search/rabitq/rabitq_lowfreq_merge.h (merge_route_results_to_original)
 //   src/data/fp16_l2.h                       (decode, scalar L2)
+//   src/execution/posting_segment_plan.h     (posting segment plan)
+//   src/index/range_posting_index.{h,cpp}    (FARPIDX1 loader, smallest slice)
 #include "predicates/gpu_predicate_index.cuh"
 #include "predicates/range_filter.cuh"
 #include "search/common/posting_shortlist_heap.cuh"
 #include "search/pq/pq_resident_posting.cuh"
 #include "search/rabitq/rabitq_lowfreq_merge.h"
 #include "data/fp16_l2.h"
+#include "execution/posting_segment_plan.h"
+#include "index/range_posting_index.h"
 
 #include <cstdint>
+#include <cstring>
+#include <exception>
+#include <string>
 #include <vector>
 
 namespace gp = go_fann::gpu_predicate;
@@ -185,6 +192,67 @@ int ref_merge_routes(const uint32_t* route_to_query, uint32_t routes, uint32_t q
         }
     }
     return static_cast<int>(strategy);
+}
+
+// posting_segments::make_plan; returns the segment count or -1 when it throws.
+int ref_segment_plan(const uint32_t* route_ids, const uint64_t* offsets, const uint64_t* sizes,
+                     uint32_t n, uint32_t target_rows, uint32_t capacity, uint32_t* seg_routes,
+                     uint32_t* seg_positions, uint64_t* seg_offsets, uint64_t* seg_sizes,
+                     uint32_t* query_indptr)
+{
+    try {
+        const auto plan = go_fann::posting_segments::make_plan(
+            std::vector<uint32_t>(route_ids, route_ids + n),
+            std::vector<uint64_t>(offsets, offsets + n), std::vector<uint64_t>(sizes, sizes + n),
+            target_rows);
+        const size_t count = plan.route_ids.size();
+        if (count > capacity) return static_cast<int>(count);
+        std::memcpy(seg_routes, plan.route_ids.data(), count * sizeof(uint32_t));
+        std::memcpy(seg_positions, plan.query_positions.data(), count * sizeof(uint32_t));
+        std::memcpy(seg_offsets, plan.offsets.data(), count * sizeof(uint64_t));
+        std::memcpy(seg_sizes, plan.sizes.data(), count * sizeof(uint64_t));
+        std::memcpy(query_indptr, plan.query_indptr.data(), (n + 1) * sizeof(uint32_t));
+        return static_cast<int>(count);
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// Loads a FARPIDX1 file with the reference loader (all of its validation)
+// and chooses the smallest slice for each query row of the range table.
+// out[q] = {has_active, active_dims, range_index, begin, count}.  Returns 0,
+// or -1 with the loader's message in `error` (NUL-terminated, truncated).
+int ref_range_slices(const char* path, const uint8_t* modes, const float* lower,
+                     const float* upper, uint32_t rows, uint32_t range_count, uint64_t* out,
+                     uint64_t* row_count, char* error, uint32_t error_bytes)
+{
+    namespace rp = go_fann::range_posting;
+    try {
+        const rp::Index index = rp::Index::load(path);
+        *row_count = index.row_count();
+        ::QueryRangeTable table;
+        table.rows = rows;
+        table.range_count = range_count;
+        const size_t n = static_cast<size_t>(rows) * range_count;
+        table.modes.assign(modes, modes + n);
+        table.lower_bounds.assign(lower, lower + n);
+        table.upper_bounds.assign(upper, upper + n);
+        for (uint32_t q = 0; q < rows; ++q) {
+            const rp::Slice s = rp::choose_smallest_slice(index, table, q);
+            out[q * 5 + 0] = s.has_active_range ? 1 : 0;
+            out[q * 5 + 1] = s.active_dimension_count;
+            out[q * 5 + 2] = s.range_index;
+            out[q * 5 + 3] = s.begin;
+            out[q * 5 + 4] = s.count;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        if (error && error_bytes) {
+            std::strncpy(error, e.what(), error_bytes - 1);
+            error[error_bytes - 1] = 0;
+        }
+        return -1;
+    }
 }
 
 }  // extern "C"

@@ -241,6 +241,35 @@ def rotation_fixture():
                 rotation_tol=[2e-5, 2e-5], centroid_tol=[1e-3, 2e-5])
 
 
+def range_posting_fixture():
+    """tests/native/range_posting_index_test.cpp:123-205: a two-dimension
+    FARPIDX1 index, the smallest-slice choices for five query rows and the
+    loader's rejections (mutation -> expected message fragment)."""
+    return dict(
+        source="tests/native/range_posting_index_test.cpp:123-205",
+        dimensions=[
+            dict(values=[1.0, 2.0, 4.0], offsets=[0, 2, 4, 6], ids=[0, 1, 2, 3, 4, 5]),
+            dict(values=[10.0, 20.0, 30.0], offsets=[0, 1, 3, 6], ids=[5, 3, 4, 0, 1, 2]),
+        ],
+        # per query row: active ranges [range_index, mode, lower, upper]
+        queries=[
+            [[0, 1, 2.0, 0.0]],
+            [[1, 2, 0.0, 20.0]],
+            [[0, 3, 2.0, 4.0]],
+            [[0, 3, 1.0, 4.0], [1, 3, 10.0, 20.0]],
+            [],
+        ],
+        # expected [has_active_range, active_dimension_count, range_index, begin, count]
+        expected=[[1, 1, 0, 4, 2], [1, 1, 1, 0, 1], [1, 1, 0, 2, 2], [1, 2, 1, 0, 1],
+                  [0, 0, U32MAX, 0, 0]],
+        # eligible_for_scan(slice of row 0, threshold) cases
+        eligible=[[1, False], [2, True]],
+        rejections=[["bad_magic", "magic mismatch"], ["bad_unique_count", "value-domain size"],
+                    ["bad_id", "sample id"], ["duplicate_id", "permutation"],
+                    ["truncated", "file size"]],
+    )
+
+
 def main():
     fixtures = {
         "predicate.json": predicate_fixtures(),
@@ -251,6 +280,7 @@ def main():
         "route_merge.json": merge_fixtures(),
         "fp16_l2.json": fp16_fixture(),
         "rotation.json": rotation_fixture(),
+        "range_posting.json": range_posting_fixture(),
     }
     for name, data in fixtures.items():
         (HERE / name).write_text(json.dumps(data, separators=(",", ":")))
