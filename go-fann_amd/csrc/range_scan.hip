@@ -186,6 +186,9 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_kernel(RangeScanArgs 
     __syncthreads();
 
     for (uint64_t base = 0; base < count; base += static_cast<uint64_t>(chunk)) {
+        // Every read of the previous chunk (s_surv included) ends here, before
+        // this chunk's survivors are counted into s_surv.
+        __syncthreads();
         const float kth_d = s_d[k - 1];
         const uint32_t kth_id = s_id[k - 1];
         uint32_t surv = 0;
@@ -233,6 +236,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_kernel(RangeScanArgs 
                     if (s_id[kp + j] != UINT32_MAX && pair_le(s_d[kp + j], s_id[kp + j], x, xid)) ++c;
                 if (c < k) ++passes;
             }
+            __syncthreads();  // the counts read LDS that the merge below reorders
         }
         const int mp = pow2_ceil(m);
         if (mp <= kp) {
