@@ -205,6 +205,19 @@ int gofann_rabitq_posting_scan(gofann_ctx* c, const gofann_rabitq_view* rq,
     });
 }
 
+int gofann_exact_search(gofann_ctx* c, const void* base, int base_elem, uint32_t dim,
+                        uint32_t samples, const void* queries, const gofann_graph_view* graph,
+                        const uint32_t* label_size, const gofann_predicate_view* predicate,
+                        const gofann_routes* routes, const gofann_exact_params* params,
+                        uint32_t* out_ids, float* out_dists, gofann_route_stats* stats)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::exact_search(ctx, base, base_elem, dim, samples, queries, graph,
+                                    label_size, predicate, routes, params, out_ids, out_dists,
+                                    stats);
+    });
+}
+
 int gofann_rabitq_range_scan(gofann_ctx* c, const gofann_rabitq_view* rq,
                              const gofann_rabitq_queries* prepared,
                              const gofann_predicate_view* predicate, const gofann_routes* routes,

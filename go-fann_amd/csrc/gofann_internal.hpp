@@ -93,6 +93,11 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
                       uint64_t resident_rows, const gofann_posting_segments* seg,
                       int shortlist_k, int score_first, uint32_t* out_ids, float* out_dists,
                       uint32_t* pass_counts);
+int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
+                 const void* queries, const gofann_graph_view* g, const uint32_t* label_size,
+                 const gofann_predicate_view* pred, const gofann_routes* r,
+                 const gofann_exact_params* p, uint32_t* out_ids, float* out_dists,
+                 gofann_route_stats* stats);
 int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
                    uint32_t count, const float* rotation, gofann_rabitq_queries* out);
 

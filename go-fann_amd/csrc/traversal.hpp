@@ -386,38 +386,6 @@ struct RabitqScorer {
 // Frontier helpers (wave-cooperative).
 // ---------------------------------------------------------------------------
 
-// pickup_next_unused_from_native_frontier (backend_pq.cu:844-892): unused
-// entry of least `first`, lowest index on ties; lane 0 marks it used.
-__device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane)
-{
-    int best = -1;
-    float bv = 0.0f;
-    for (int i = lane + 1; i < size; i += kWave) {
-        const Entry e = f[i];
-        if (e.second & kPoolUsed) continue;
-        if (best < 0 || e.first < bv) {
-            best = i;
-            bv = e.first;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const int ob = __shfl_xor(best, off, kWave);
-        const float ov = __shfl_xor(bv, off, kWave);
-        if (ob >= 0 && (best < 0 || ov < bv || (!(bv < ov) && ob < best))) {
-            best = ob;
-            bv = ov;
-        }
-    }
-    best = bcast0(best);
-    if (best < 0) return false;
-    out = f[best];
-    __syncthreads();
-    if (lane == 0) f[best].second |= kPoolUsed;
-    __syncthreads();
-    return true;
-}
-
 // minimum_pending_base (gpu_predicate_index.cuh:147-160) over the reserved
 // current/next entries and every unused frontier entry.
 __device__ __forceinline__ float min_pending_base(const Entry* f, int size, const Entry& now, const Entry& next,

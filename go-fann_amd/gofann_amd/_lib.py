@@ -90,6 +90,12 @@ class RabitqQueries(C.Structure):
                 ("centroid_dists", P), ("count", U32)]
 
 
+class ExactParams(C.Structure):
+    _fields_ = [("queue_limit", C.c_int), ("finish_limit", C.c_int),
+                ("early_stop_mode", C.c_int), ("max_steps", C.c_int), ("topk", C.c_int),
+                ("hash_mode", C.c_int)]
+
+
 class PostingSegments(C.Structure):
     _fields_ = [("route_ids", P), ("offsets", P), ("sizes", P), ("count", U32),
                 ("query_indptr", P), ("positions", U32)]
@@ -120,6 +126,9 @@ SIGNATURES = {
                                              C.POINTER(RabitqQueries),
                                              C.POINTER(PredicateView), P, P, P, P, U32,
                                              C.c_int, P, P, P]),
+    "gofann_exact_search": (C.c_int, [P, P, C.c_int, U32, U32, P, C.POINTER(GraphView), P,
+                                      C.POINTER(PredicateView), C.POINTER(Routes),
+                                      C.POINTER(ExactParams), P, P, P]),
     "gofann_posting_segment_plan": (C.c_int, [P, P, P, U32, U32, U32, P, P, P, P, P,
                                               C.POINTER(U32)]),
     "gofann_range_slices": (C.c_int, [P, P, P, U32, P, P, P, U32, P]),

@@ -271,6 +271,31 @@ int gofann_rabitq_posting_scan(gofann_ctx* ctx, const gofann_rabitq_view* rq,
                                uint32_t* out_ids, float* out_dists,
                                uint32_t* pass_counts);
 
+/* ---- full-GPU exact route (run_full_gpu_highfreq_route, src/search/
+ * full_gpu/backend_full_gpu.cu:1682-2042, launched by full_gpu_highfreq_kernel
+ * :2045-2122).  Beam search keyed by the exact squared L2 of u8 vectors
+ * (integer, returned as float); every expanded node is filtered (row mask &
+ * route bits, all active legacy ranges of `routes`, the route predicate when
+ * enabled) and a passing node enters a sorted best-topk with sample dedup.
+ * base [samples][dim] u8 (16-byte aligned), queries [n][dim] u8.  label_size
+ * [groups] (device; NULL: adjacency entries are trusted) bounds each group's
+ * local ids.  Outputs [routes][topk] ascending by (distance, id), padded
+ * UINT32_MAX / FLT_MAX; stats (may be NULL) per route. */
+typedef struct {
+    int queue_limit;     /* [2, 1024] */
+    int finish_limit;    /* fixed early stop limit */
+    int early_stop_mode;
+    int max_steps;       /* 0 = unlimited */
+    int topk;            /* [1, 10] */
+    int hash_mode;       /* visited-set placement, as gofann_search_params.hash_mode */
+} gofann_exact_params;
+
+int gofann_exact_search(gofann_ctx* ctx, const void* base, int base_elem, uint32_t dim,
+                        uint32_t samples, const void* queries, const gofann_graph_view* graph,
+                        const uint32_t* label_size, const gofann_predicate_view* predicate,
+                        const gofann_routes* routes, const gofann_exact_params* params,
+                        uint32_t* out_ids, float* out_dists, gofann_route_stats* stats);
+
 /* ---- range postings ------------------------------------------------------
  * Posting segments (posting_segments::Plan, src/execution/
  * posting_segment_plan.h:12-18).  Segment s scans posting rows

@@ -1056,6 +1056,195 @@ int orc_rabitq_search_batch(const orc_graph* g, const orc_predicate* pred,
 }
 
 /* ======================================================================
+ * Full-GPU exact route -- backend_full_gpu.cu:1682-2042.
+ * ====================================================================== */
+uint32_t orc_l2_u8_int(const uint8_t* a, const uint8_t* b, uint32_t dim)
+{
+    /* :1235-1243: integer squared differences (the dp4a form :1209-1232,
+     * |b|^2 + |q|^2 - 2 b.q in u32, is the same integer) */
+    uint32_t acc = 0;
+    for (uint32_t d = 0; d < dim; ++d) {
+        const int diff = (int)a[d] - (int)b[d];
+        acc += (uint32_t)(diff * diff);
+    }
+    return acc;
+}
+
+static int better_result(float ld, uint32_t lid, float rd, uint32_t rid)
+{
+    return ld < rd || (ld == rd && lid < rid); /* :1337-1340 */
+}
+
+int orc_insert_best(float dist, uint32_t id, uint32_t topk, float* bd, uint32_t* bi,
+                    uint32_t* size)
+{
+    /* :1342-1375 */
+    int changed = 0;
+    for (uint32_t i = 0; i < *size; ++i) {
+        if (bi[i] != id) continue;
+        if (dist >= bd[i]) return 0;
+        for (uint32_t j = i; j + 1 < *size; ++j) {
+            bd[j] = bd[j + 1];
+            bi[j] = bi[j + 1];
+        }
+        --*size;
+        changed = 1;
+        break;
+    }
+    if (*size == topk && !better_result(dist, id, bd[topk - 1], bi[topk - 1])) return changed;
+    uint32_t pos = *size;
+    if (*size < topk)
+        ++*size;
+    else
+        pos = topk - 1;
+    while (pos > 0 && better_result(dist, id, bd[pos - 1], bi[pos - 1])) {
+        bd[pos] = bd[pos - 1];
+        bi[pos] = bi[pos - 1];
+        --pos;
+    }
+    bd[pos] = dist;
+    bi[pos] = id;
+    return 1;
+}
+
+int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_predicate* pred,
+                     const orc_exact_params* p, const uint8_t* base, uint32_t dim,
+                     uint32_t samples, const uint8_t* queries, const uint32_t* route_query,
+                     uint32_t routes, uint32_t* out_ids, float* out_dists,
+                     orc_route_stats* stats)
+{
+    const int Q = p->queue_limit;
+    const uint32_t K = (uint32_t)p->topk;
+    if (Q < 2 || K == 0 || K > 10) return -1;
+    uint32_t* hash = (uint32_t*)malloc(ORC_HASH_CAPACITY * sizeof(uint32_t));
+    orc_pair* pool = (orc_pair*)malloc((size_t)(Q + 2) * sizeof(orc_pair));
+    if (!hash || !pool) {
+        free(hash);
+        free(pool);
+        return -1;
+    }
+    const uint32_t degree = g->degree < ORC_FIXED_DEGREE ? g->degree : ORC_FIXED_DEGREE;
+    for (uint32_t r = 0; r < routes; ++r) {
+        orc_route_stats st;
+        memset(&st, 0, sizeof(st));
+        float bd[10];
+        uint32_t bi[10];
+        uint32_t bsize = 0;
+        for (int i = 0; i < 10; ++i) {
+            bd[i] = FLT_MAX;
+            bi[i] = UINT32_MAX;
+        }
+        orc_pred_counters pc = {0, 0, 0};
+        const uint32_t group = g->route_group[r];
+        const uint32_t seed = g->route_start[r];
+        const uint32_t gsize = label_size ? label_size[group] : UINT32_MAX;
+        const uint8_t* q = queries + (size_t)route_query[r] * dim;
+        const uint32_t off = g->label_offset[group];
+        const uint64_t qfbit = g->query_filter_bits ? g->query_filter_bits[r] : ~0ULL;
+        const uint32_t active = orc_count_active_ranges(g->range_modes, r, g->range_count);
+        const int enabled = orc_pred_enabled(pred, r);
+        int heap_size = 1;
+        int done = 0;
+        orc_pair now, next;
+        /* :1793-1850: the seed (visited is empty, so it is always fresh) */
+        if (gsize == 0 || seed == UINT32_MAX || seed >= gsize) {
+            done = 1;
+        } else {
+            orc_hash_clear(hash);
+            const uint32_t s0 = g->row_to_sample[off + seed];
+            if (s0 < samples && !orc_hash_test(hash, seed)) {
+                const float d0 = (float)orc_l2_u8_int(base + (size_t)s0 * dim, q, dim);
+                ++st.scored;
+                orc_pair kp = {d0, seed, d0};
+                orc_smmh2_insert(pool, &heap_size, kp);
+                if (heap_size >= Q + 2) orc_smmh2_pop_max(pool, &heap_size);
+                orc_hash_add(hash, seed);
+            } else {
+                done = 1;
+            }
+        }
+        if (!done && !orc_pickup_unused(pool, heap_size, &now)) done = 1;
+        if (done) st.exhausted = 1;
+        uint32_t steps = 0, finished = 0;
+        int first_step = 1;
+        while (!done) {
+            if (p->max_steps != 0 && steps >= (uint32_t)p->max_steps) break; /* :1878-1883 */
+            /* :1885-1918: the expanded node's filter and best-k */
+            const uint32_t cur = now.second & ~ORC_POOL_USED;
+            const uint32_t grow = off + cur;
+            const uint32_t sample = g->row_to_sample[grow];
+            const uint64_t rmask = g->row_filter_mask ? g->row_filter_mask[grow] : ~0ULL;
+            int pass = (rmask & qfbit) != 0;
+            if (pass && active != 0)
+                pass = orc_count_matching_ranges(g->range_modes, g->range_lower, g->range_upper,
+                                                 g->base_range_values, r, sample,
+                                                 g->range_count) == active;
+            if (pass && enabled) pass = orc_pred_matches(pred, r, sample, &pc);
+            ++st.expanded;
+            int improved = 0;
+            if (pass) {
+                ++st.passed;
+                improved = orc_insert_best(now.first, sample, K, bd, bi, &bsize);
+            }
+            ++steps;
+            /* :1920-1958: neighbours, then ordered admission :1962-1981 */
+            uint32_t cl[ORC_FIXED_DEGREE];
+            float cd[ORC_FIXED_DEGREE];
+            int nc = 0;
+            for (uint32_t e = 0; e < degree; ++e) {
+                const uint32_t local = g->graph[(size_t)grow * g->degree + e];
+                if (local == UINT32_MAX || local >= gsize || orc_hash_test(hash, local)) continue;
+                const uint32_t s = g->row_to_sample[off + local];
+                if (s >= samples) continue;
+                cl[nc] = local;
+                cd[nc] = (float)orc_l2_u8_int(base + (size_t)s * dim, q, dim);
+                ++nc;
+            }
+            st.scored += nc;
+            for (int i = 0; i < nc; ++i) {
+                orc_pair kp = {cd[i], cl[i], cd[i]};
+                if (heap_size > 2 && heap_size >= Q + 1 && pool[2].first < kp.first) continue;
+                orc_smmh2_insert(pool, &heap_size, kp);
+                ++st.admitted;
+                orc_hash_add(hash, cl[i]);
+                if (heap_size >= Q + 2) orc_smmh2_pop_max(pool, &heap_size);
+            }
+            /* :1985-2030: pickup and early stop */
+            if (!orc_pickup_unused(pool, heap_size, &next)) {
+                st.exhausted = 1;
+                break;
+            }
+            if (!first_step) {
+                const uint32_t ns = g->row_to_sample[off + (next.second & ~ORC_POOL_USED)];
+                if (p->early_stop_mode == ORC_EARLY_STOP_ADAPTIVE && improved) {
+                    finished = 0;
+                } else if (bsize == K && !better_result(next.first, ns, bd[K - 1], bi[K - 1])) {
+                    ++finished;
+                    if (orc_early_stop_reached(p->early_stop_mode, (int)finished, p->finish_limit,
+                                               Q, st.expanded, st.passed, (int)K))
+                        break;
+                } else {
+                    finished = 0;
+                }
+            }
+            now = next;
+            first_step = 0;
+        }
+        st.steps = (int32_t)steps;
+        st.pred_rows = (int32_t)pc.rows_checked;
+        st.pred_labels = (int32_t)pc.label_words;
+        for (uint32_t i = 0; i < K; ++i) {
+            out_ids[(size_t)r * K + i] = i < bsize ? bi[i] : UINT32_MAX;
+            out_dists[(size_t)r * K + i] = i < bsize ? bd[i] : FLT_MAX;
+        }
+        if (stats) stats[r] = st;
+    }
+    free(hash);
+    free(pool);
+    return 0;
+}
+
+/* ======================================================================
  * Posting scans -- backend_pq.cu:2046-2133 (PQ, serial ADC order) and
  * backend_rabitq.cu:5494-5682 (RaBitQ).
  * ====================================================================== */

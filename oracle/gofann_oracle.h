@@ -225,6 +225,32 @@ int orc_rabitq_search_batch(const orc_graph* g, const orc_predicate* pred,
                             uint32_t routes, uint32_t* out_ids, float* out_dists,
                             orc_route_stats* stats);
 
+/* ---------------- full-GPU exact route (backend_full_gpu.cu:1682-2042) ----
+ * Exact-distance beam over u8 vectors: frontier keys are the integer squared
+ * L2 (l2_distance_device :1199-1244) as float; each expanded node that passes
+ * the filter enters a sorted best-k with sample dedup (insert_best_result
+ * :1342-1375).  Filter of an expanded node: row mask & route bits non-zero,
+ * every active legacy range matches, and the route predicate when enabled
+ * (candidate_passes_device :1015-1092 over the same label/range sets). */
+typedef struct {
+    int queue_limit;
+    int finish_limit;
+    int early_stop_mode;
+    int max_steps;
+    int topk; /* <= 10 (defaults::max_topk) */
+} orc_exact_params;
+
+uint32_t orc_l2_u8_int(const uint8_t* a, const uint8_t* b, uint32_t dim);
+int orc_insert_best(float dist, uint32_t id, uint32_t topk, float* best_d, uint32_t* best_i,
+                    uint32_t* best_size);
+/* label_size [groups] (NULL: adjacency entries are taken as valid); stats
+ * may be NULL; out [routes][topk] ascending by (distance, id). */
+int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_predicate* pred,
+                     const orc_exact_params* p, const uint8_t* base, uint32_t dim,
+                     uint32_t samples, const uint8_t* queries, const uint32_t* route_query,
+                     uint32_t routes, uint32_t* out_ids, float* out_dists,
+                     orc_route_stats* stats);
+
 /* ---------------- posting scans (backend_pq.cu:2046-2133) ---------------- */
 int orc_pq_posting_scan(const orc_predicate* pred, const uint8_t* codes,
                         const float* centroids, const void* queries,

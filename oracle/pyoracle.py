@@ -424,3 +424,38 @@ def merge_segments(indptr, seg_ids, seg_dists, seg_pass, k):
                                 p(c_arr(seg_dists, np.float32)), p(c_arr(seg_pass, np.uint32)),
                                 k, p(ids), p(dists), p(passes)) == 0
     return ids[:n], dists[:n], passes[:n]
+
+
+class ExactParams(C.Structure):
+    _fields_ = [("queue_limit", C.c_int), ("finish_limit", C.c_int),
+                ("early_stop_mode", C.c_int), ("max_steps", C.c_int), ("topk", C.c_int)]
+
+
+def exact_search(index, routes, pred, base, queries, queue_limit=64, topk=10,
+                 early_stop_mode=2, finish_limit=1, max_steps=0, label_size=None,
+                 row_filter_mask=None, query_filter_bits=None, range_modes=None,
+                 range_lower=None, range_upper=None, base_range_values=None):
+    """orc_exact_search over every route: ids [R][topk] u32, dists f32, stats."""
+    L = lib()
+    g, keep = graph_struct(index, routes.route_group, routes.route_start)
+    extra = dict(rm=c_arr(row_filter_mask, np.uint64), qb=c_arr(query_filter_bits, np.uint64),
+                 modes=c_arr(range_modes, np.uint8), lo=c_arr(range_lower, np.float32),
+                 hi=c_arr(range_upper, np.float32), brv=c_arr(base_range_values, np.float32),
+                 ls=c_arr(label_size, np.uint32))
+    g.row_filter_mask, g.query_filter_bits = p(extra["rm"]), p(extra["qb"])
+    g.range_modes, g.range_lower, g.range_upper = p(extra["modes"]), p(extra["lo"]), p(extra["hi"])
+    g.base_range_values = p(extra["brv"])
+    g.range_count = 0 if range_modes is None else int(np.asarray(range_modes).shape[1])
+    n = routes.count
+    ids = np.empty((max(n, 1), topk), np.uint32)
+    dists = np.empty((max(n, 1), topk), np.float32)
+    stats = (Stats * max(n, 1))()
+    b = np.ascontiguousarray(base, dtype=np.uint8)
+    q = np.ascontiguousarray(queries, dtype=np.uint8)
+    rq = c_arr(routes.route_query, np.uint32)
+    prm = ExactParams(queue_limit, finish_limit, early_stop_mode, max_steps, topk)
+    rc = L.orc_exact_search(C.byref(g), p(extra["ls"]), C.byref(pred.struct) if pred else None,
+                            C.byref(prm), p(b), U32(b.shape[1]), U32(b.shape[0]), p(q), p(rq),
+                            U32(n), p(ids), p(dists), stats)
+    assert rc == 0
+    return ids[:n], dists[:n], stats_array(stats, n)

@@ -1,0 +1,154 @@
+"""GPU parity of the full-GPU exact route (gofann_exact_search): ids,
+distance bits and the eight per-route counters identical to the oracle,
+across visited-set placements, neighbour-sample tables, early-stop modes,
+beam sizes, route predicates and legacy bit/range filters, and the three
+distance paths (dim % 16 == 0, dim % 4 == 0, any dim)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from gofann_amd import _lib
+from gofann_amd import index as gi
+from gofann_amd import plan as gp
+from gofann_amd import search as gs
+from gofann_amd import synth
+
+pytestmark = pytest.mark.gpu
+U32MAX = 0xFFFFFFFF
+
+
+def say(*a):
+    print("[gpu-test]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def _world(dim, seed, n=5000, nq=40):
+    wl = synth.small_labelled(n=n, nq=nq, dim=dim, k=10, sigma=0.7, labels=5, seed=seed, tags=True,
+                              dtype="u8")
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=32, threshold=300)
+    pl = gp.plan_queries(li, wl.query_labels)
+    return wl, li, pl.graph
+
+
+@pytest.fixture(scope="module")
+def eworld(gpu_ctx):
+    return _world(48, 51)
+
+
+def _run(ctx, wl, li, rs, pred_o, pred_g, Q, topk, mode, hash_mode, nsamp, max_steps=0,
+         finish=1, legacy=None):
+    base, q = wl.base.numpy(), wl.queries.numpy()
+    kw = {}
+    if legacy is not None:
+        kw = dict(row_filter_mask=legacy["rmask"], query_filter_bits=legacy["qbits"],
+                  range_modes=legacy["modes"], range_lower=legacy["lo"], range_upper=legacy["hi"],
+                  base_range_values=legacy["brv"])
+    oi, od, ost = po.exact_search(li, rs, pred_o, base, q, queue_limit=Q, topk=topk,
+                                  early_stop_mode=mode, finish_limit=finish, max_steps=max_steps,
+                                  label_size=li.label_size, **kw)
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
+    dr = gs.DeviceRoutes.upload(rs)
+    dev = dict(base=wl.base.cuda(), q=wl.queries.cuda(), ls=gs.u32(li.label_size))
+    rv = dr.routes_view()
+    if legacy is not None:
+        for k in ("rmask", "qbits"):
+            dev[k] = torch.from_numpy(legacy[k].view(np.int64)).cuda()
+        dev["modes"] = torch.from_numpy(legacy["modes"]).cuda()
+        dev["lo"] = torch.from_numpy(legacy["lo"]).cuda()
+        dev["hi"] = torch.from_numpy(legacy["hi"]).cuda()
+        dev["brv"] = torch.from_numpy(legacy["brv"]).cuda()
+        rv.row_filter_mask, rv.query_filter_bits = _lib.ptr(dev["rmask"]), _lib.ptr(dev["qbits"])
+        rv.range_modes, rv.range_lower = _lib.ptr(dev["modes"]), _lib.ptr(dev["lo"])
+        rv.range_upper, rv.base_range_values = _lib.ptr(dev["hi"]), _lib.ptr(dev["brv"])
+        rv.range_count = legacy["modes"].shape[1]
+    n = rs.count
+    ids = torch.empty(n * topk, dtype=torch.int32, device="cuda")
+    dists = torch.empty(n * topk, device="cuda")
+    st = torch.zeros(n * 8, dtype=torch.int32, device="cuda")
+    prm = _lib.ExactParams(Q, finish, mode, max_steps, topk, hash_mode)
+    ctx.check(ctx.lib.gofann_exact_search(ctx.handle, _lib.ptr(dev["base"]), _lib.ELEM_U8, wl.dim,
+                                          wl.n, _lib.ptr(dev["q"]), dg.view(), _lib.ptr(dev["ls"]),
+                                          pred_g(dr, dg), rv, prm, _lib.ptr(ids), _lib.ptr(dists),
+                                          _lib.ptr(st)))
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy().view(np.uint32).reshape(n, topk), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(n, topk).view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(st.cpu().numpy().reshape(n, 8), ost)
+    return oi, ost
+
+
+PLACE = {"auto": (_lib.PLACE_AUTO, False), "lds-nsamp": (_lib.PLACE_LDS, True),
+         "global": (_lib.PLACE_GLOBAL, False), "spill-nsamp": (_lib.PLACE_SPILL, True)}
+
+
+@pytest.mark.parametrize("place", list(PLACE))
+@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 64), (1, 128)])
+@pytest.mark.parametrize("with_pred", [False, True])
+def test_exact_search_matches_oracle(gpu_ctx, eworld, place, mode, Q, with_pred):
+    wl, li, rs = eworld
+    hash_mode, nsamp = PLACE[place]
+    say("exact search", place, "mode", mode, "Q", Q, "pred", with_pred)
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li) if with_pred else None
+
+    def pred_g(dr, dg):
+        return dr.predicate_view(dg, 0.0, False) if with_pred else _lib.PredicateView()
+
+    oi, ost = _run(gpu_ctx, wl, li, rs, pred_o, pred_g, Q, 10, mode, hash_mode, nsamp,
+                   max_steps=300 if mode == 1 else 0, finish=2)
+    assert (oi[:, 0] != U32MAX).sum() > rs.count // 2
+    assert ost[:, 0].max() > 5
+
+
+def test_exact_search_legacy_filters_and_topk1(gpu_ctx, eworld):
+    wl, li, rs = eworld
+    say("exact search legacy filters")
+    rng = np.random.default_rng(9)
+    rc = 2
+    legacy = dict(rmask=rng.integers(1, 4, li.row_to_sample.shape[0]).astype(np.uint64),
+                  qbits=rng.integers(1, 4, rs.count).astype(np.uint64),
+                  modes=rng.integers(0, 4, (rs.count, rc)).astype(np.uint8),
+                  brv=rng.integers(0, 20, (wl.n, rc)).astype(np.float32))
+    legacy["lo"] = rng.integers(0, 8, (rs.count, rc)).astype(np.float32)
+    legacy["hi"] = legacy["lo"] + rng.integers(4, 12, (rs.count, rc)).astype(np.float32)
+    for topk in (1, 10):
+        _run(gpu_ctx, wl, li, rs, None, lambda dr, dg: _lib.PredicateView(), 48, topk, 2,
+             _lib.PLACE_AUTO, True, legacy=legacy)
+
+
+@pytest.mark.parametrize("dim", [44, 45])
+def test_exact_search_distance_paths(gpu_ctx, dim):
+    wl, li, rs = _world(dim, 60 + dim, n=3000, nq=24)
+    say("exact search dim", dim)
+    _run(gpu_ctx, wl, li, rs, None, lambda dr, dg: _lib.PredicateView(), 32, 10, 2,
+         _lib.PLACE_AUTO, False)
+
+
+def test_exact_search_invalid_seeds(gpu_ctx, eworld):
+    wl, li, rs = eworld
+    say("exact search invalid seeds")
+    start = rs.route_start.copy()
+    start[0] = U32MAX
+    start[1] = li.label_size[rs.route_group[1]]
+    rs2 = gp.RouteSet(rs.route_query, rs.route_group, start, rs.route_to_query, rs.predicate)
+    oi, ost = _run(gpu_ctx, wl, li, rs2, None, lambda dr, dg: _lib.PredicateView(), 32, 10, 2,
+                   _lib.PLACE_AUTO, False)
+    assert np.all(oi[:2] == U32MAX) and np.all(ost[:2, 0] == 0)
+
+
+def test_exact_search_rejects_bad_params(gpu_ctx, eworld):
+    wl, li, rs = eworld
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs)
+    base, q = wl.base.cuda(), wl.queries.cuda()
+    for Q, k, elem in ((1, 10, _lib.ELEM_U8), (32, 11, _lib.ELEM_U8), (32, 10, _lib.ELEM_F32)):
+        prm = _lib.ExactParams(Q, 1, 2, 0, k, 0)
+        rc = gpu_ctx.lib.gofann_exact_search(gpu_ctx.handle, _lib.ptr(base), elem, wl.dim, wl.n,
+                                             _lib.ptr(q), dg.view(), None, _lib.PredicateView(),
+                                             dr.routes_view(), prm, None, None, None)
+        assert rc in (_lib.ERR_INVALID, _lib.ERR_UNSUPPORTED)
