@@ -36,6 +36,13 @@ namespace gofann {
 
 constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 
+// 1: rows of 128, 192 or 256 bytes use kernels with the row length fixed
+// at compile time (all of a row's loads in flight at once, at the price of
+// about 40 more VGPRs and so fewer resident routes); 0 keeps the loop.
+#ifndef GOFANN_EXACT_FIXED_ROWS
+#define GOFANN_EXACT_FIXED_ROWS 0
+#endif
+
 struct ExactArgs {
     gofann_graph_view graph;
     const uint32_t* label_size;
@@ -94,6 +101,37 @@ __device__ __forceinline__ uint32_t l2_u8_row(const uint8_t* row, const uint32_t
     return acc;
 }
 
+// Rows of kC 16-byte chunks (dim = 16 kC): every chunk's load is issued
+// before the first dot product, so a row costs one memory round trip.
+template <int kC>
+__device__ __forceinline__ void row_load(const uint8_t* row, bool keep, uint4 (&b)[kC])
+{
+    const uint4* r4 = reinterpret_cast<const uint4*>(row);
+#pragma unroll
+    for (int i = 0; i < kC; ++i) b[i] = keep ? r4[i] : make_uint4(0, 0, 0, 0);
+}
+
+template <int kC>
+__device__ __forceinline__ uint32_t row_dist(const uint4 (&b)[kC], const uint32_t* q,
+                                             uint32_t qnorm)
+{
+    const uint4* q4 = reinterpret_cast<const uint4*>(q);
+    uint32_t nb = 0, dot = 0;
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+        const uint4 w = q4[i];
+        nb = __builtin_amdgcn_udot4(b[i].x, b[i].x, nb, false);
+        nb = __builtin_amdgcn_udot4(b[i].y, b[i].y, nb, false);
+        nb = __builtin_amdgcn_udot4(b[i].z, b[i].z, nb, false);
+        nb = __builtin_amdgcn_udot4(b[i].w, b[i].w, nb, false);
+        dot = __builtin_amdgcn_udot4(b[i].x, w.x, dot, false);
+        dot = __builtin_amdgcn_udot4(b[i].y, w.y, dot, false);
+        dot = __builtin_amdgcn_udot4(b[i].z, w.z, dot, false);
+        dot = __builtin_amdgcn_udot4(b[i].w, w.w, dot, false);
+    }
+    return nb + qnorm - 2u * dot;
+}
+
 __device__ __forceinline__ bool better(float ld, uint32_t lid, float rd, uint32_t rid)
 {
     return ld < rd || (ld == rd && lid < rid);
@@ -131,19 +169,192 @@ __device__ __forceinline__ bool best_insert(float d, uint32_t id, uint32_t K, fl
     return true;
 }
 
-// Lane j: adjacency entry j of the node `e` and, when the graph carries
-// them, its sample id.
-__device__ __forceinline__ void load_adjacency(const gofann_graph_view& g, uint32_t off,
-                                               uint32_t degree, const Entry& e, int lane,
-                                               uint32_t& adj, uint32_t& nsamp)
+// ---------------------------------------------------------------------------
+// Register frontier (capacity Q + 2 <= 64): lane i holds smmh2 entry i.  The
+// heap code is the LDS version's (include/smmh2.h:77-147) with every index
+// wave-uniform: an entry is read with v_readlane and written by the one lane
+// that owns it, so each heap step costs a few VALU/SALU instructions instead
+// of a dependent LDS round trip.  The array layout -- and with it every
+// tie-break of pickup and pop_max -- is the LDS heap's.
+// ---------------------------------------------------------------------------
+struct RegHeap {
+    float first;
+    uint32_t second;
+    uint32_t sample;
+};
+
+__device__ __forceinline__ float rh_first(const RegHeap& h, int i)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first), i));
+}
+
+__device__ __forceinline__ Entry rh_get(const RegHeap& h, int i)
+{
+    Entry e;
+    e.first = rh_first(h, i);
+    e.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.second), i));
+    e.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.sample), i));
+    e.base = e.first;
+    return e;
+}
+
+__device__ __forceinline__ void rh_set(RegHeap& h, int i, const Entry& e, int lane)
+{
+    const bool me = lane == i;
+    h.first = me ? e.first : h.first;
+    h.second = me ? e.second : h.second;
+    h.sample = me ? e.sample : h.sample;
+}
+
+__device__ __forceinline__ void rh_swap(RegHeap& h, int i, int j, int lane)
+{
+    const Entry a = rh_get(h, i);
+    const Entry b = rh_get(h, j);
+    rh_set(h, i, b, lane);
+    rh_set(h, j, a, lane);
+}
+
+__device__ __forceinline__ int rh_adjust_sibling(RegHeap& h, int y, int size, int lane)
+{
+    if (y & 1) {
+        const int s = y + 1;
+        if (s >= size) return y;
+        if (rh_first(h, y) > rh_first(h, s)) {
+            rh_swap(h, y, s, lane);
+            return s;
+        }
+    } else {
+        const int s = y - 1;
+        if (rh_first(h, y) < rh_first(h, s)) {
+            rh_swap(h, y, s, lane);
+            return s;
+        }
+    }
+    return y;
+}
+
+__device__ __forceinline__ int rh_adjust_grandparent(RegHeap& h, int y, int lane)
+{
+    if (y <= 2) return y;
+    const int g = (y - 3) >> 2;
+    const int gl = (g << 1) + 1;
+    const int gr = (g << 1) + 2;
+    const float fy = rh_first(h, y);
+    if (rh_first(h, gl) > fy) {
+        rh_swap(h, gl, y, lane);
+        return gl;
+    } else if (rh_first(h, gr) < fy) {
+        rh_swap(h, gr, y, lane);
+        return gr;
+    }
+    return y;
+}
+
+__device__ __forceinline__ void rh_insert(RegHeap& h, int& size, const Entry& e, int lane)
+{
+    int y = size;
+    rh_set(h, size++, e, lane);
+    for (;;) {
+        y = rh_adjust_sibling(h, y, size, lane);
+        const int x = rh_adjust_grandparent(h, y, lane);
+        if (x == y) break;
+        y = x;
+    }
+}
+
+__device__ __forceinline__ int rh_adjust_grandchild(RegHeap& h, int y, int size, int lane)
+{
+    if (y & 1) {
+        const int cl = (y << 1) + 1;
+        if (cl >= size) return y;
+        const int cr = ((y + 1) << 1) + 1;
+        int c = cl;
+        if (cr < size && rh_first(h, cr) < rh_first(h, cl)) c = cr;
+        if (rh_first(h, c) < rh_first(h, y)) {
+            rh_swap(h, c, y, lane);
+            return c;
+        }
+    } else {
+        const int cl = ((y - 1) << 1) + 2;
+        const int cr = (y << 1) + 2;
+        if (cl >= size) return y;
+        int c = cl;
+        if (cr < size && rh_first(h, cr) > rh_first(h, cl)) c = cr;
+        if (rh_first(h, c) > rh_first(h, y)) {
+            rh_swap(h, c, y, lane);
+            return c;
+        }
+    }
+    return y;
+}
+
+__device__ __forceinline__ void rh_pop_max(RegHeap& h, int& size, int lane)
+{
+    --size;
+    rh_set(h, 2, rh_get(h, size), lane);
+    int y = 2;
+    for (;;) {
+        (void)rh_adjust_sibling(h, y, size, lane);
+        const int x = rh_adjust_grandchild(h, y, size, lane);
+        if (x == y) break;
+        y = x;
+    }
+}
+
+// Unused entry of least `first`, lowest index on ties; marked used.
+__device__ __forceinline__ bool rh_pickup(RegHeap& h, int size, Entry& out, int lane)
+{
+    const bool live = lane >= 1 && lane < size && !(h.second & kPoolUsed);
+    float bv = live ? h.first : 0.0f;
+    int best = live ? lane : -1;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const int ob = __shfl_xor(best, off, kWave);
+        const float ov = __shfl_xor(bv, off, kWave);
+        if (ob >= 0 && (best < 0 || ov < bv || (!(bv < ov) && ob < best))) {
+            best = ob;
+            bv = ov;
+        }
+    }
+    best = bcast0(best);
+    if (best < 0) return false;
+    out = rh_get(h, best);
+    if (lane == best) h.second |= kPoolUsed;
+    return true;
+}
+
+// Loads a picked node needs when it is expanded, issued at pickup: lane j's
+// adjacency entry j (and its sample id when the graph carries them), and the
+// node's label slab or CSR bounds (.x/.y) for the filter.
+struct ExactNode {
+    uint32_t adj;
+    uint32_t nsamp;
+    uint4 row;
+};
+
+__device__ __forceinline__ void load_node(const gofann_graph_view& g,
+                                          const gofann_predicate_view& pv, bool verdict_rows,
+                                          uint32_t off, uint32_t degree, const Entry& e, int lane,
+                                          ExactNode& n)
 {
     const size_t row = static_cast<size_t>(off + (e.second & ~kPoolUsed)) * g.degree;
     const bool in_row = static_cast<uint32_t>(lane) < degree;
-    adj = in_row ? g.graph[row + lane] : UINT32_MAX;
-    nsamp = (in_row && g.neighbor_samples) ? g.neighbor_samples[row + lane] : 0u;
+    n.adj = in_row ? g.graph[row + lane] : UINT32_MAX;
+    n.nsamp = (in_row && g.neighbor_samples) ? g.neighbor_samples[row + lane] : 0u;
+    n.row = make_uint4(0, 0, 0, 0);
+    if (verdict_rows && e.sample < pv.rows && pv.csr_offsets != nullptr) {
+        if (slab_usable(pv, e.sample)) {
+            n.row = slab_load(pv, e.sample);
+        } else {
+            n.row.x = pv.csr_offsets[e.sample];
+            n.row.y = pv.csr_offsets[e.sample + 1];
+        }
+    }
 }
 
-template <int kVisited>
+// kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  kReg: the
+// frontier lives in registers (Q + 2 <= 64), else in LDS.
+template <int kVisited, int kC, bool kReg>
 __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
 {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -208,6 +419,7 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
     bool done = false;
     const Entry sentinel = {FLT_MAX, UINT32_MAX, FLT_MAX, UINT32_MAX};
     Entry now = sentinel, next = sentinel;
+    RegHeap rh{FLT_MAX, UINT32_MAX, UINT32_MAX};
 
     // Seed (:1793-1850).
     if (gsize == 0 || seed == UINT32_MAX || seed >= gsize) {
@@ -215,103 +427,162 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
     } else {
         const uint32_t s0 = a.graph.row_to_sample[off + seed];
         if (s0 < a.samples) {
-            if (lane == 0) {
-                const float d0 = static_cast<float>(
-                    l2_u8_row(a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn));
-                const Entry kp = {d0, seed, d0, s0};
-                smmh_insert(frontier, heap_size, kp);
-                (void)visited.add_serial(seed, 0);
+            const float d0 = bcast0f(
+                lane == 0 ? static_cast<float>(
+                                l2_u8_row(a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn))
+                          : 0.0f);
+            const Entry kp = {d0, seed, d0, s0};
+            if constexpr (kReg) {
+                rh_insert(rh, heap_size, kp, lane);
+            } else {
+                if (lane == 0) smmh_insert(frontier, heap_size, kp);
+                heap_size = bcast0(heap_size);
             }
+            if (lane == 0) (void)visited.add_serial(seed, 0);
             visited.count = 1;
             st.scored = 1;
-            heap_size = bcast0(heap_size);
         } else {
             done = true;
         }
     }
     __threadfence_block();
     __syncthreads();
-    if (!done && !pickup(frontier, heap_size, now, lane)) done = true;
+    if (!done) {
+        bool found;
+        if constexpr (kReg)
+            found = rh_pickup(rh, heap_size, now, lane);
+        else
+            found = pickup(frontier, heap_size, now, lane);
+        if (!found) done = true;
+    }
     if (done) st.exhausted = 1;
 
-    // Adjacency of the node about to be expanded, loaded at pickup time.
-    uint32_t adj = UINT32_MAX, nsamp = 0;
-    if (!done) load_adjacency(a.graph, off, degree, now, lane, adj, nsamp);
+    ExactNode cur{UINT32_MAX, 0, make_uint4(0, 0, 0, 0)};
+    if (!done) load_node(a.graph, a.pred, enabled, off, degree, now, lane, cur);
 
     uint32_t steps = 0, finished = 0;
     bool first_step = true;
     while (!done) {
         if (a.params.max_steps != 0 && steps >= static_cast<uint32_t>(a.params.max_steps)) break;
 
-        // Neighbour tests first (loads only), then the expanded node's filter.
+        // One memory round for the neighbours (visited tests, sample ids) and
+        // the expanded node's label row, then one for the neighbours' rows.
+        const uint32_t adj = cur.adj;
         const bool fresh = adj != UINT32_MAX && adj < gsize && !visited.test(adj);
         uint32_t samp = 0;
-        if (fresh) samp = a.graph.neighbor_samples ? nsamp : a.graph.row_to_sample[off + adj];
+        if (fresh) samp = a.graph.neighbor_samples ? cur.nsamp : a.graph.row_to_sample[off + adj];
         const bool keep = fresh && samp < a.samples;
-
-        int improved = 0;
-        if (lane == 0) {
-            const uint32_t grow = off + (now.second & ~kPoolUsed);
-            const uint32_t sample = now.sample;
-            const uint64_t rmask =
-                a.routes.row_filter_mask ? a.routes.row_filter_mask[grow] : ~0ULL;
-            bool pass = (rmask & qfbit) != 0;
-            if (pass && active != 0) pass = count_matching_ranges(a.routes, route, sample) == active;
-            if (pass && enabled) pass = pred_matches(a.pred, route, sample, pc);
-            ++st.expanded;
-            if (pass) {
-                ++st.passed;
-                improved = best_insert(now.first, sample, K, s_bd, s_bi, bsize) ? 1 : 0;
+        const uint32_t sample = now.sample;
+        WaveRow vrow{0, 0, UINT32_MAX, false};
+        if (enabled) {
+            if (!slab_usable(a.pred, sample)) {
+                vrow = wave_row_load(a.pred, sample, cur.row.x, cur.row.y, lane);
+            } else if (slab_count(cur.row) != kSlabOverflow) {
+                vrow = wave_row_from_slab(cur.row, lane);
+            } else {
+                vrow = wave_row_load(a.pred, sample, a.pred.csr_offsets[sample],
+                                     a.pred.csr_offsets[sample + 1], lane);
             }
         }
+        const uint8_t* brow = a.base + static_cast<size_t>(samp) * a.dim;
+        uint32_t d32;
+        if constexpr (kC > 0) {
+            uint4 rb[kC];
+            row_load<kC>(brow, keep, rb);
+            d32 = row_dist<kC>(rb, qw, qn);
+        } else {
+            d32 = keep ? l2_u8_row(brow, qw, a.dim, qn) : 0u;
+        }
+        // The distance is complete here: the rows and query words are dead
+        // before the filter below.
+        asm volatile("" : "+v"(d32)::"memory");
+
+        // The expanded node's filter (wave-uniform) and best-k (lane 0).
+        const uint32_t grow = off + (now.second & ~kPoolUsed);
+        const uint64_t rmask = a.routes.row_filter_mask ? a.routes.row_filter_mask[grow] : ~0ULL;
+        bool ok = (rmask & qfbit) != 0;
+        if (ok && active != 0) ok = count_matching_ranges(a.routes, route, sample) == active;
+        PredCounters c{0, 0};
+        if (ok && enabled) ok = wave_pred_matches(a.pred, route, sample, vrow, lane, c);
+        int improved = 0;
+        if (lane == 0) {
+            pc.rows += c.rows;
+            pc.labels += c.labels;
+            if (ok) improved = best_insert(now.first, sample, K, s_bd, s_bi, bsize) ? 1 : 0;
+        }
+        ++st.expanded;
+        st.passed += ok ? 1 : 0;
         ++steps;
 
-        const float dist = keep ? static_cast<float>(l2_u8_row(
-                                      a.base + static_cast<size_t>(samp) * a.dim, qw, a.dim, qn))
-                                : FLT_MAX;
+        const float dist = keep ? static_cast<float>(d32) : FLT_MAX;
         st.scored += __popcll(ballot(keep));
 
         // Drop what cannot enter a full frontier (its maximum only falls
-        // during the step), compact the rest in adjacency order.
+        // during the step), then admit the rest in adjacency order.
         const bool full = heap_size > 2 && heap_size >= Q + 1;
-        const float thr = full ? frontier[2].first : 0.0f;
+        float thr = 0.0f;
+        if (full) {
+            if constexpr (kReg)
+                thr = rh_first(rh, 2);
+            else
+                thr = frontier[2].first;
+        }
         const bool cand = keep && !(full && thr < dist);
         const uint64_t cand_mask = ballot(cand);
-        const int n_cand = __popcll(cand_mask);
-        const uint32_t pos = lanes_below(cand_mask);
-        if (cand) {
-            s_row[pos] = adj;
-            s_samp[pos] = samp;
-            s_dist[pos] = dist;
-        }
-        __syncthreads();
-        if (lane == 0) {
-            uint64_t adm = 0;
-            for (int i = 0; i < n_cand; ++i) {
-                const Entry kp = {s_dist[i], s_row[i], s_dist[i], s_samp[i]};
-                if (heap_size > 2 && heap_size >= Q + 1 && frontier[2].first < kp.first) continue;
-                smmh_insert(frontier, heap_size, kp);
-                adm |= 1ull << i;
-                ++st.admitted;
-                if (heap_size >= Q + 2) smmh_pop_max(frontier, heap_size);
+        uint64_t adm = 0;  // admitted lanes
+        if constexpr (kReg) {
+            for (uint64_t m = cand_mask; m; m &= m - 1) {
+                const int j = __builtin_ctzll(m);
+                Entry kp;
+                kp.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dist), j));
+                kp.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(adj), j));
+                kp.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), j));
+                kp.base = kp.first;
+                if (heap_size > 2 && heap_size >= Q + 1 && rh_first(rh, 2) < kp.first) continue;
+                rh_insert(rh, heap_size, kp, lane);
+                adm |= 1ull << j;
+                if (heap_size >= Q + 2) rh_pop_max(rh, heap_size, lane);
             }
-            s_adm = adm;
+        } else {
+            const int n_cand = __popcll(cand_mask);
+            const uint32_t pos = lanes_below(cand_mask);
+            if (cand) {
+                s_row[pos] = adj;
+                s_samp[pos] = samp;
+                s_dist[pos] = dist;
+            }
+            __syncthreads();
+            if (lane == 0) {
+                uint64_t ap = 0;
+                for (int i = 0; i < n_cand; ++i) {
+                    const Entry kp = {s_dist[i], s_row[i], s_dist[i], s_samp[i]};
+                    if (heap_size > 2 && heap_size >= Q + 1 && frontier[2].first < kp.first)
+                        continue;
+                    smmh_insert(frontier, heap_size, kp);
+                    ap |= 1ull << i;
+                    if (heap_size >= Q + 2) smmh_pop_max(frontier, heap_size);
+                }
+                s_adm = ap;
+            }
+            heap_size = bcast0(heap_size);
+            __syncthreads();
+            const uint64_t ap = s_adm;  // by compacted position
+            adm = ballot(cand && ((ap >> pos) & 1ull));
         }
-        heap_size = bcast0(heap_size);
-        __syncthreads();
-        const uint64_t adm = s_adm;
         const uint32_t n_adm = static_cast<uint32_t>(__popcll(adm));
+        st.admitted += static_cast<int32_t>(n_adm);
         visited.reserve(n_adm, lane);
         if (visited.count + n_adm <= kHashCapacity) {
-            const bool mine = cand && ((adm >> pos) & 1ull);
-            const int ins = mine ? visited.add_parallel(adj) : 0;
+            const int ins = ((adm >> lane) & 1ull) ? visited.add_parallel(adj) : 0;
             visited.count += static_cast<uint32_t>(__popcll(ballot(ins != 0)));
         } else {
+            // The set may fill: serial adds in admission (lane) order
+            // reproduce which values the reference drops.
             uint32_t added = 0;
-            if (lane == 0) {
-                for (int i = 0; i < n_cand; ++i)
-                    if ((adm >> i) & 1ull)
-                        added += static_cast<uint32_t>(visited.add_serial(s_row[i], added));
+            for (uint64_t m = adm; m; m &= m - 1) {
+                const int j = __builtin_ctzll(m);
+                const uint32_t v = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(adj), j));
+                if (lane == 0) added += static_cast<uint32_t>(visited.add_serial(v, added));
             }
             visited.count += bcast0u(added);
         }
@@ -319,11 +590,16 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
         __syncthreads();
 
         // Pickup and early stop (:1985-2030).
-        if (!pickup(frontier, heap_size, next, lane)) {
+        bool found;
+        if constexpr (kReg)
+            found = rh_pickup(rh, heap_size, next, lane);
+        else
+            found = pickup(frontier, heap_size, next, lane);
+        if (!found) {
             st.exhausted = 1;
             break;
         }
-        load_adjacency(a.graph, off, degree, next, lane, adj, nsamp);
+        load_node(a.graph, a.pred, enabled, off, degree, next, lane, cur);
         int stop = 0;
         if (lane == 0 && !first_step) {
             if (mode == GOFANN_EARLY_STOP_ADAPTIVE && improved) {
@@ -365,11 +641,11 @@ namespace {
 
 inline uint32_t align16u(uint32_t x) { return (x + 15u) & ~15u; }
 
-template <int kVisited>
+template <int kVisited, int kC, bool kReg>
 int resident(Context* ctx, uint32_t lds)
 {
     if (lds > static_cast<uint32_t>(ctx->lds_per_block)) return 0;
-    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited>);
+    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited, kC, kReg>);
     if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lds)) != hipSuccess) {
         (void)hipGetLastError();
@@ -384,6 +660,59 @@ int resident(Context* ctx, uint32_t lds)
 }
 
 }  // namespace
+
+// Visited-set placement with the most resident routes per CU (ties: the
+// full LDS table, then the spilling table, then the global slab), then the
+// launch.
+template <int kC, bool kReg>
+int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
+                 uint32_t lds_spill, uint32_t lds_glob, uint32_t count)
+{
+    const int rf = resident<kVisitedLds, kC, kReg>(ctx, lds_full);
+    const int rs = resident<kVisitedSpill, kC, kReg>(ctx, lds_spill);
+    const int rg = resident<kVisitedGlobal, kC, kReg>(ctx, lds_glob);
+    int mode = kVisitedLds;
+    int res = rf;
+    if (hash_mode == GOFANN_PLACE_GLOBAL) {
+        mode = kVisitedGlobal;
+        res = rg;
+    } else if (hash_mode == GOFANN_PLACE_SPILL) {
+        mode = kVisitedSpill;
+        res = rs;
+    } else if (hash_mode == GOFANN_PLACE_AUTO) {
+        if (rs > res) {
+            mode = kVisitedSpill;
+            res = rs;
+        }
+        if (rg > res) {
+            mode = kVisitedGlobal;
+            res = rg;
+        }
+    }
+    if (res <= 0)
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "per-route LDS state exceeds the workgroup limit");
+    a.hash_global = nullptr;
+    if (mode != kVisitedLds) {
+        const size_t need = static_cast<size_t>(count) * kHashCapacity * sizeof(uint32_t);
+        a.hash_global = static_cast<uint32_t*>(ctx->scratch(Context::kScratchHash, need));
+        if (!a.hash_global) return ctx->fail(GOFANN_ERR_NOMEM, "visited set scratch");
+    }
+    const uint32_t lds = mode == kVisitedLds ? lds_full : (mode == kVisitedSpill ? lds_spill : lds_glob);
+    const dim3 grid(count), block(kWave);
+    if (mode == kVisitedLds)
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedLds, kC, kReg>), grid, block, lds, ctx->stream, a);
+    else if (mode == kVisitedSpill)
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedSpill, kC, kReg>), grid, block, lds, ctx->stream, a);
+    else
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedGlobal, kC, kReg>), grid, block, lds, ctx->stream, a);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("exact route launch");
+    ctx->last_table_in_lds = 0;
+    ctx->last_hash_in_lds = mode == kVisitedGlobal ? 0 : (mode == kVisitedLds ? 1 : 2);
+    ctx->last_lds_bytes = static_cast<int>(lds);
+    ctx->last_resident = res;
+    return GOFANN_OK;
+}
+
 
 int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
                  const void* queries, const gofann_graph_view* g, const uint32_t* label_size,
@@ -426,54 +755,35 @@ int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, ui
     a.out_ids = out_ids;
     a.out_dists = out_dists;
     a.stats = stats;
+    // LDS: the query row, then (LDS frontier only) Q + 2 entries, then the
+    // visited table of the chosen placement.
+    const bool reg = p->queue_limit + 2 <= kWave;
     a.off_frontier = align16u((dim + 15u) / 16u * 16u);
-    a.off_hash = align16u(a.off_frontier + static_cast<uint32_t>(p->queue_limit + 2) * sizeof(Entry));
+    a.off_hash = reg ? a.off_frontier
+                     : align16u(a.off_frontier + static_cast<uint32_t>(p->queue_limit + 2) *
+                                                     sizeof(Entry));
     const uint32_t lds_full = a.off_hash + kHashCapacity * 4u;
     const uint32_t lds_spill = a.off_hash + kSpillSlots * 4u;
     const uint32_t lds_glob = a.off_hash;
-    const int rf = resident<kVisitedLds>(ctx, lds_full);
-    const int rs = resident<kVisitedSpill>(ctx, lds_spill);
-    const int rg = resident<kVisitedGlobal>(ctx, lds_glob);
-    int mode = kVisitedLds;
-    int res = rf;
-    if (p->hash_mode == GOFANN_PLACE_GLOBAL) {
-        mode = kVisitedGlobal;
-        res = rg;
-    } else if (p->hash_mode == GOFANN_PLACE_SPILL) {
-        mode = kVisitedSpill;
-        res = rs;
-    } else if (p->hash_mode == GOFANN_PLACE_AUTO) {
-        if (rs > res) {
-            mode = kVisitedSpill;
-            res = rs;
-        }
-        if (rg > res) {
-            mode = kVisitedGlobal;
-            res = rg;
+    const int chunks = (GOFANN_EXACT_FIXED_ROWS && (dim == 128 || dim == 192 || dim == 256))
+                           ? static_cast<int>(dim / 16)
+                           : 0;
+    const int h = p->hash_mode;
+    const uint32_t n = r->count;
+    if (reg) {
+        switch (chunks) {
+        case 8: return launch_exact<8, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+        case 12: return launch_exact<12, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+        case 16: return launch_exact<16, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+        default: return launch_exact<0, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
         }
     }
-    if (res <= 0)
-        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "per-route LDS state exceeds the workgroup limit");
-    a.hash_global = nullptr;
-    if (mode != kVisitedLds) {
-        const size_t need = static_cast<size_t>(r->count) * kHashCapacity * sizeof(uint32_t);
-        a.hash_global = static_cast<uint32_t*>(ctx->scratch(Context::kScratchHash, need));
-        if (!a.hash_global) return ctx->fail(GOFANN_ERR_NOMEM, "visited set scratch");
+    switch (chunks) {
+    case 8: return launch_exact<8, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+    case 12: return launch_exact<12, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+    case 16: return launch_exact<16, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+    default: return launch_exact<0, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
     }
-    const uint32_t lds = mode == kVisitedLds ? lds_full : (mode == kVisitedSpill ? lds_spill : lds_glob);
-    const dim3 grid(r->count), block(kWave);
-    if (mode == kVisitedLds)
-        hipLaunchKernelGGL(exact_route_kernel<kVisitedLds>, grid, block, lds, ctx->stream, a);
-    else if (mode == kVisitedSpill)
-        hipLaunchKernelGGL(exact_route_kernel<kVisitedSpill>, grid, block, lds, ctx->stream, a);
-    else
-        hipLaunchKernelGGL(exact_route_kernel<kVisitedGlobal>, grid, block, lds, ctx->stream, a);
-    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("exact route launch");
-    ctx->last_table_in_lds = 0;
-    ctx->last_hash_in_lds = mode == kVisitedGlobal ? 0 : (mode == kVisitedLds ? 1 : 2);
-    ctx->last_lds_bytes = static_cast<int>(lds);
-    ctx->last_resident = res;
-    return GOFANN_OK;
 }
 
 }  // namespace gofann

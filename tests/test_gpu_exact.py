@@ -1,8 +1,9 @@
 """GPU parity of the full-GPU exact route (gofann_exact_search): ids,
 distance bits and the eight per-route counters identical to the oracle,
 across visited-set placements, neighbour-sample tables, early-stop modes,
-beam sizes, route predicates and legacy bit/range filters, and the three
-distance paths (dim % 16 == 0, dim % 4 == 0, any dim)."""
+beam sizes, route predicates and legacy bit/range filters, and every
+distance path (rows of fixed length 128/192/256, dim % 16 == 0, dim % 4 ==
+0, any dim)."""
 from __future__ import annotations
 
 import sys
@@ -38,7 +39,7 @@ def _world(dim, seed, n=5000, nq=40):
 
 @pytest.fixture(scope="module")
 def eworld(gpu_ctx):
-    return _world(48, 51)
+    return _world(128, 51)
 
 
 def _run(ctx, wl, li, rs, pred_o, pred_g, Q, topk, mode, hash_mode, nsamp, max_steps=0,
@@ -88,7 +89,8 @@ PLACE = {"auto": (_lib.PLACE_AUTO, False), "lds-nsamp": (_lib.PLACE_LDS, True),
 
 
 @pytest.mark.parametrize("place", list(PLACE))
-@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 64), (1, 128)])
+# Q + 2 <= 64 keeps the frontier in registers, larger beams in LDS.
+@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (1, 128)])
 @pytest.mark.parametrize("with_pred", [False, True])
 def test_exact_search_matches_oracle(gpu_ctx, eworld, place, mode, Q, with_pred):
     wl, li, rs = eworld
@@ -121,7 +123,7 @@ def test_exact_search_legacy_filters_and_topk1(gpu_ctx, eworld):
              _lib.PLACE_AUTO, True, legacy=legacy)
 
 
-@pytest.mark.parametrize("dim", [44, 45])
+@pytest.mark.parametrize("dim", [44, 45, 48, 192, 256])
 def test_exact_search_distance_paths(gpu_ctx, dim):
     wl, li, rs = _world(dim, 60 + dim, n=3000, nq=24)
     say("exact search dim", dim)
