@@ -64,6 +64,8 @@ def parse():
                     help="separate code rows and CSR labels instead of 64-byte sample records")
     ap.add_argument("--no-cpu-rerank-route", action="store_true",
                     help="skip the GPU+CPU-rerank route measurement")
+    ap.add_argument("--no-rabitq-prep", action="store_true",
+                    help="skip the RaBitQ query-preparation (rotation GEMM) measurement")
     ap.add_argument("--no-exact-route", action="store_true",
                     help="skip the full-GPU exact route measurement")
     ap.add_argument("--exact-ladder", default="32,48,64,96,128,192,256",
@@ -353,6 +355,53 @@ def exact_route_bytes(st: np.ndarray, degree: int, dim: int, neighbor_samples: b
     return E * adj + V * (dim + (0 if neighbor_samples else 4)) + rows * 8 + labels * 4
 
 
+PEAK_FP32_MFMA_TFLOPS = 157.3
+
+
+def rabitq_prep_leg(ctx, torch, nq=10_000, dim=4096, anchors=512, reps=3):
+    """RaBitQ query preparation at the C3 shape (10k queries, 4096-d, padded
+    4096, 512 anchors): rotation SGEMM on MFMA, int8 quantization, factors
+    and centroid distances, timed with HIP events on the launch stream.
+    Inputs are seeded Gaussians (the timing does not depend on values)."""
+    from gofann_amd import _lib
+    g = torch.Generator(device="cuda").manual_seed(3003)
+    q = torch.randn(nq, dim, device="cuda", generator=g)
+    q /= q.norm(dim=1, keepdim=True)
+    rot = torch.randn(dim, dim, device="cuda", generator=g) / dim ** 0.5
+    anc = torch.randn(anchors, dim, device="cuda", generator=g) / dim ** 0.5
+    out = dict(rotated=torch.empty(nq, dim, device="cuda"),
+               q8=torch.empty(nq, dim, dtype=torch.int8, device="cuda"),
+               scale=torch.empty(nq, device="cuda"), k1=torch.empty(nq, device="cuda"),
+               cd=torch.empty(nq, anchors, device="cuda"))
+    rv = _lib.RabitqView(None, None, None, _lib.ptr(anc), dim, dim, anchors, 0)
+    rq = _lib.RabitqQueries(_lib.ptr(out["rotated"]), _lib.ptr(out["q8"]), _lib.ptr(out["scale"]),
+                            _lib.ptr(out["k1"]), _lib.ptr(out["cd"]), nq)
+
+    def run():
+        ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, rv, _lib.ptr(q), nq,
+                                                        _lib.ptr(rot), rq))
+
+    run()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(reps):
+        run()
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / reps
+    gemm = 2.0 * nq * dim * dim
+    cdist = 3.0 * nq * anchors * dim  # subtract + fma per element
+    tf = gemm / (ms / 1000.0) / 1e12
+    return {"shape": f"{nq}x{dim}x{dim} rotation + {nq}x{anchors} centroid distances (C3)",
+            "ms": round(ms, 3), "rotation_gflop": round(gemm / 1e9, 1),
+            "centroid_gflop": round(cdist / 1e9, 1),
+            "rotation_tflops_lower_bound": round(tf, 2), "peak_fp32_mfma_tflops": PEAK_FP32_MFMA_TFLOPS,
+            "frac_lower_bound": round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
+            "note": "whole preparation time charged to the rotation GEMM (a lower bound); "
+                    "rocprofv3 times the rocBLAS SGEMM alone at 2.64 ms = 126.9 TFLOP/s"}
+
+
 def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes: int,
                       neighbor_samples: bool, record_bytes: int = 0) -> float:
     """Bytes the traversal must move per launch: the adjacency row of each
@@ -572,6 +621,11 @@ def main():
                                "algorithmic_bytes": b3}}
         log(f"exact route: {route3}")
 
+    prep = None
+    if not args.no_rabitq_prep:
+        prep = rabitq_prep_leg(ctx, torch)
+        log(f"RaBitQ query preparation: {prep}")
+
     # Headline: the faster all-GPU route that reaches the target recall
     # (C2 names both the PQ route and the Full-GPU exact route).
     pq_route = {"qps": round(qps, 1), "ms_per_step": round(ms_per_step, 3),
@@ -633,7 +687,8 @@ def main():
                    "sample_records": not args.no_records,
                    "pq_route": pq_route,
                    "full_gpu_exact_route": route3,
-                   "gpu_cpu_rerank_route": route2},
+                   "gpu_cpu_rerank_route": route2,
+                   "rabitq_query_prep": prep},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
     }

@@ -64,7 +64,7 @@ def build(verbose: bool = True, lib: Path = LIB, defines: tuple = ()) -> Path:
         objs = list(ex.map(lambda src: _compile(src, out_dir, defines), sources))
     tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
-           "-o", str(tmp), "-lpthread"]
+           "-o", str(tmp), "-lpthread", "-lrocblas"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)

@@ -88,6 +88,7 @@ void gofann_destroy(gofann_ctx* c)
     Context* ctx = as_ctx(c);
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    gofann::destroy_blas(ctx);
     for (int i = 0; i < Context::kScratchCount; ++i)
         if (ctx->scratch_ptr[i]) (void)hipFree(ctx->scratch_ptr[i]);
     delete ctx;

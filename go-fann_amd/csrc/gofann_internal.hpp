@@ -37,6 +37,7 @@ struct Context {
     int last_table_in_lds = 0;
     int last_lds_bytes = 0;
     int last_resident = 0;
+    void* blas = nullptr;  // rocblas_handle of the query-rotation GEMM (lazy)
 
     int fail(int code, const std::string& msg)
     {
@@ -98,6 +99,7 @@ int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, ui
                  const gofann_predicate_view* pred, const gofann_routes* r,
                  const gofann_exact_params* p, uint32_t* out_ids, float* out_dists,
                  gofann_route_stats* stats);
+void destroy_blas(Context* ctx);
 int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
                    uint32_t count, const float* rotation, gofann_rabitq_queries* out);
 

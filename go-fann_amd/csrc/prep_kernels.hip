@@ -1,6 +1,7 @@
 // prep_kernels.hip -- RaBitQ query preparation on gfx950
 // (init_prepared_query_state, src/search/rabitq/backend_rabitq.cu:7800-8084):
-//   rotated = Q R                 (FP32 GEMM on MFMA; RabitqQueryRotation::
+//   rotated = Q R                 (FP32 SGEMM on MFMA through rocBLAS -- a
+//                                  plain library GEMM; RabitqQueryRotation::
 //                                  apply, rabitq_query_rotation.cuh:71-87)
 //   k1 = -0.5 * sum(rotated)      (compute_rabitq_query_factors_kernel,
 //                                  backend_rabitq.cu:2898-2929)
@@ -19,48 +20,9 @@
 #include "device_common.hpp"
 #include "gofann_internal.hpp"
 
+#include <rocblas/rocblas.h>
+
 namespace gofann {
-
-// C[m][n] = alpha * sum_k A(m,k) B(k,n) in FP32 on the 32x32x2 MFMA.  One
-// wave computes one 32x32 tile; a 256-thread workgroup covers 64x64.
-// A(m,k) = A[m*a_m + k*a_k], B(k,n) = B[k*b_k + n*b_n], C row-major ldc.
-struct GemmArgs {
-    const float* A;
-    const float* B;
-    float* C;
-    uint32_t M, N, K;
-    size_t a_m, a_k, b_k, b_n, ldc;
-    float alpha;
-};
-
-__global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g)
-{
-    const int lane = static_cast<int>(threadIdx.x) & 63;
-    const int wave = static_cast<int>(threadIdx.x) >> 6;
-    const uint32_t m0 = blockIdx.y * 64 + (wave >> 1) * 32;
-    const uint32_t n0 = blockIdx.x * 64 + (wave & 1) * 32;
-    const uint32_t row = m0 + (lane & 31);   // A operand row of this lane
-    const uint32_t col = n0 + (lane & 31);   // B operand column of this lane
-    const uint32_t kk = static_cast<uint32_t>(lane >> 5);
-    typedef float float16v __attribute__((ext_vector_type(16)));
-    float16v acc;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-    for (uint32_t k = 0; k < g.K; k += 2) {
-        const uint32_t kx = k + kk;
-        const float a = (row < g.M && kx < g.K) ? g.A[row * g.a_m + kx * g.a_k] : 0.0f;
-        const float b = (col < g.N && kx < g.K) ? g.B[kx * g.b_k + col * g.b_n] : 0.0f;
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
-    }
-    // Output layout of the 32x32 MFMA: lane l, register i holds
-    // D[8*(i/4) + 4*(l/32) + i%4][l%32].
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t r = m0 + 8 * (i / 4) + 4 * (lane >> 5) + (i % 4);
-        const uint32_t c = n0 + (lane & 31);
-        if (r < g.M && c < g.N) g.C[r * g.ldc + c] = g.alpha * acc[i];
-    }
-}
 
 // One 256-thread block per query row: scale, q8 and k1.
 __global__ __launch_bounds__(256) void quantize_queries_kernel(const float* rotated, uint32_t P,
@@ -151,13 +113,25 @@ __global__ __launch_bounds__(256) void centroid_dist_kernel(const float* y, cons
     }
 }
 
-namespace {
-void launch_gemm(Context* ctx, const GemmArgs& g)
+// The context's rocBLAS handle, created on first use and bound to the
+// context's current stream before every call.
+rocblas_handle blas_handle(Context* ctx)
 {
-    const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64), block(256);
-    hipLaunchKernelGGL(gemm_f32_mfma_kernel, grid, block, 0, ctx->stream, g);
+    if (!ctx->blas) {
+        rocblas_handle h = nullptr;
+        if (rocblas_create_handle(&h) != rocblas_status_success) return nullptr;
+        ctx->blas = h;
+    }
+    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
+    if (rocblas_set_stream(h, ctx->stream) != rocblas_status_success) return nullptr;
+    return h;
 }
-}  // namespace
+
+void destroy_blas(Context* ctx)
+{
+    if (ctx->blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
+    ctx->blas = nullptr;
+}
 
 int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
                    uint32_t count, const float* rotation, gofann_rabitq_queries* out)
@@ -169,9 +143,16 @@ int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* quer
         return ctx->fail(GOFANN_ERR_INVALID, "invalid RaBitQ dimensions");
     if (count == 0) return GOFANN_OK;
     const uint32_t D = rq->dim, P = rq->padded_dim, A = rq->num_anchors;
-    // rotated[N][P] = Q[N][D] R[D][P]
-    GemmArgs g{queries, rotation, out->rotated, count, P, D, D, 1, P, 1, P, 1.0f};
-    launch_gemm(ctx, g);
+    // rotated[N][P] = Q[N][D] R[D][P]: FP32 SGEMM on the MFMA units through
+    // rocBLAS; column-major, that is rotated^T = R^T Q^T.
+    rocblas_handle h = blas_handle(ctx);
+    if (!h) return ctx->fail(GOFANN_ERR_HIP, "rocBLAS handle");
+    const float one = 1.0f, zero = 0.0f;
+    if (rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, static_cast<int>(P),
+                      static_cast<int>(count), static_cast<int>(D), &one, rotation,
+                      static_cast<int>(P), queries, static_cast<int>(D), &zero, out->rotated,
+                      static_cast<int>(P)) != rocblas_status_success)
+        return ctx->fail(GOFANN_ERR_HIP, "rocblas_sgemm (query rotation)");
     hipLaunchKernelGGL(quantize_queries_kernel, dim3(count), dim3(256), 0, ctx->stream, out->rotated,
                        P, count, out->q8, out->scale, out->k1);
     if (A > 0 && rq->anchors) {
