@@ -64,6 +64,16 @@ def parse():
                     help="separate code rows and CSR labels instead of 64-byte sample records")
     ap.add_argument("--no-cpu-rerank-route", action="store_true",
                     help="skip the GPU+CPU-rerank route measurement")
+    ap.add_argument("--config", choices=("c2", "c3"), default="c2",
+                    help="c2 (default): 10Mx192 u8 PQ/exact routes; c3: 2.7Mx4096 fp32 RaBitQ "
+                         "with range predicates")
+    ap.add_argument("--n-c3", type=int, default=2_700_000)
+    ap.add_argument("--queries-c3", type=int, default=10_000)
+    ap.add_argument("--gt-queries-c3", type=int, default=999)
+    ap.add_argument("--c3-ladder", default="64,96,128,192,256,384,512")
+    ap.add_argument("--c3-scan-rows", type=int, default=20_000,
+                    help="ranges whose smallest posting slice has at most this many rows are "
+                         "scanned; wider ones search the graph with the range predicate")
     ap.add_argument("--no-rabitq-prep", action="store_true",
                     help="skip the RaBitQ query-preparation (rotation GEMM) measurement")
     ap.add_argument("--no-exact-route", action="store_true",
@@ -494,8 +504,268 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False
     return done / el, done, el
 
 
+# ---------------------------------------------------------------------------
+# C3: 2.7M x 4096 fp32, one-bit RaBitQ, range predicates (--config c3).
+# ---------------------------------------------------------------------------
+def rabitq_traversal_bytes(st: np.ndarray, degree: int, code_bytes: int) -> float:
+    """Bytes the RaBitQ traversal must move: the adjacency row and
+    row_to_sample word of each expanded node, each scored candidate's code
+    row, factors (12 B), anchor id and row_to_sample word, its base range
+    value (the route predicate is a range atom), and the CSR words of label
+    checks."""
+    E = st[:, 1].astype(np.float64).sum()
+    V = st[:, 3].astype(np.float64).sum()
+    rows = st[:, 4].astype(np.float64).sum()
+    labels = st[:, 5].astype(np.float64).sum()
+    return E * (4 * degree + 4) + V * (code_bytes + 12 + 4 + 4 + 4) + rows * 8 + labels * 4
+
+
+def build_world_c3(args, torch):
+    from gofann_amd import index as gi
+    from gofann_amd import range_posting as rp
+    from gofann_amd import synth
+    t0 = time.time()
+    wl = synth.config3(n=args.n_c3, nq=args.queries_c3, device="cuda")
+    torch.cuda.synchronize()
+    log(f"C3 data {wl.n}x{wl.dim} fp32, {wl.queries.shape[0]} queries in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, 1, wl.centroids,
+                              degree=32, threshold=0, progress=log)
+    log(f"C3 graph: {li.rows} rows, degree {li.degree} in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    P = wl.dim
+    rot = gi.random_rotation(wl.dim, P, 3003, "cuda")
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
+    torch.cuda.synchronize()
+    log(f"C3 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
+    rpi = rp.RangePostingIndex.build(wl.base_ranges)
+    return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), rpi
+
+
+def ground_truth_c3(wl, torch, nq):
+    """Exact filtered top-10 (fp32 L2 over the rows whose attribute lies in
+    the query's range) for the first nq queries."""
+    attr = torch.as_tensor(wl.base_ranges[:, 0], device="cuda")
+    bn = (wl.base * wl.base).sum(1)
+    gt = {}
+    for s in range(0, nq, 32):
+        e = min(nq, s + 32)
+        q = wl.queries[s:e]
+        d = bn[None, :] + (q * q).sum(1)[:, None] - 2.0 * (q @ wl.base.t())
+        for j in range(e - s):
+            _, _, lo, hi = wl.query_ranges[s + j][0]
+            m = (attr >= lo) & (attr < hi)
+            dj = torch.where(m, d[j], torch.full_like(d[j], float("inf")))
+            v, i = torch.topk(dj, 10, largest=False)
+            ids = i[torch.isfinite(v)].cpu().numpy()
+            if ids.size:
+                gt[s + j] = ids
+    return gt
+
+
+class RabitqRangePipeline:
+    """One step of the C3 route set on the GPU: query preparation (rotation
+    SGEMM, int8, factors, centroid distances), RaBitQ graph traversal with
+    the range predicate for wide ranges, the RaBitQ range-posting scan over
+    the smallest slice for narrow ones (both shortlist 200), exact fp32
+    rerank of the 200, and the per-query merge."""
+
+    def __init__(self, ctx, wl, li, rq, rpi, torch, scan_rows, width=200, segment_rows=4096):
+        from gofann_amd import _lib
+        from gofann_amd import plan as gp
+        from gofann_amd import range_posting as rp
+        from gofann_amd import search as gs
+        self.ctx, self.wl, self.torch, self.L, self.gs = ctx, wl, torch, _lib, gs
+        nq = wl.queries.shape[0]
+        self.nq, self.W = nq, width
+        P = rq["P"]
+        modes = np.full((nq, 1), 3, np.uint8)
+        lo = np.array([r[0][2] for r in wl.query_ranges], np.float32)[:, None]
+        hi = np.array([r[0][3] for r in wl.query_ranges], np.float32)[:, None]
+        slices = rp.choose_slices(rpi, modes, lo, hi)
+        post = slices[:, 4] <= scan_rows
+        gq = np.nonzero(~post)[0].astype(np.uint32)
+        pq = np.nonzero(post)[0].astype(np.uint32)
+        self.ng, self.np_ = len(gq), len(pq)
+        # graph routes: one per wide-range query, seeded at the nearest bucket
+        rows = [(int(q), 0, [], [tuple(wl.query_ranges[q][0])]) for q in gq]
+        rs = gp._routeset(rows, li)
+        if rs.count:
+            rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
+        self.rs = rs
+        self.dg = gs.DeviceGraph.upload(li)
+        self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+        # posting routes: the smallest slice, in segments
+        self.post_query = gs.u32(pq if len(pq) else np.zeros(1, np.uint32))
+        self.modes_p = torch.from_numpy(modes[pq] if len(pq) else modes[:1]).cuda()
+        self.lo_p = torch.from_numpy(lo[pq] if len(pq) else lo[:1]).cuda()
+        self.hi_p = torch.from_numpy(hi[pq] if len(pq) else hi[:1]).cuda()
+        self.brv = torch.from_numpy(wl.base_ranges).cuda()
+        offs, sizes = rp.route_postings(rpi, slices[pq])
+        self.scan_rows_total = int(sizes.sum())
+        plan = rp.segment_plan(np.arange(len(pq), dtype=np.uint32), offs, sizes, segment_rows)
+        self.segs = rp.DeviceSegments(plan, merged=True)
+        self.postings = rpi.device_postings()
+        self.resident = rpi.resident_rows
+        # RaBitQ index on the device
+        self.dev = dict(codes=rq["codes"], fac=rq["fac"], aid=rq["aid"].view(torch.int32),
+                        anchors=rq["anchors"], rot=rq["rot"])
+        self.rv = _lib.RabitqView(_lib.ptr(self.dev["codes"]), _lib.ptr(self.dev["fac"]),
+                                  _lib.ptr(self.dev["aid"]), _lib.ptr(self.dev["anchors"]),
+                                  wl.dim, P, rq["anchors"].shape[0], wl.n)
+        A = rq["anchors"].shape[0]
+        self.prep = dict(rotated=torch.empty(nq, P, device="cuda"),
+                         q8=torch.empty(nq, P, dtype=torch.int8, device="cuda"),
+                         scale=torch.empty(nq, device="cuda"), k1=torch.empty(nq, device="cuda"),
+                         cd=torch.empty(nq, A, device="cuda"))
+        self.rq = _lib.RabitqQueries(*[_lib.ptr(self.prep[k]) for k in
+                                       ("rotated", "q8", "scale", "k1", "cd")], nq)
+        n = self.ng + self.np_
+        self.sl_i = torch.empty(max(n, 1) * width, dtype=torch.int32, device="cuda")
+        self.sl_d = torch.empty(max(n, 1) * width, dtype=torch.float32, device="cuda")
+        self.passes = torch.empty(max(self.np_, 1), dtype=torch.int32, device="cuda")
+        self.stats = torch.zeros(max(self.ng, 1) * 8, dtype=torch.int32, device="cuda")
+        self.route_query = gs.u32(np.concatenate([gq, pq]))
+        r2q = np.concatenate([gq, pq]).astype(np.uint32)
+        off, order = gs.query_route_csr(r2q, nq)
+        self.q_off, self.q_routes = gs.u32(off), gs.u32(order)
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+
+    def step(self, Q: int, timed=False):
+        L, gs, ctx, W = self.L, self.gs, self.ctx, self.W
+        ev = self.ev
+        if timed:
+            ev[0].record()
+        ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, self.rv,
+                                                        L.ptr(self.wl.queries), self.nq,
+                                                        L.ptr(self.dev["rot"]), self.rq))
+        if timed:
+            ev[1].record()
+        if self.ng:
+            prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=True)
+            ctx.check(ctx.lib.gofann_rabitq_search(
+                ctx.handle, self.rv, self.rq, self.dg.view(),
+                self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(), prm,
+                L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
+        if timed:
+            ev[2].record()
+        if self.np_:
+            routes = L.Routes(L.ptr(self.post_query), None, None, None, None, L.ptr(self.modes_p),
+                              L.ptr(self.lo_p), L.ptr(self.hi_p), L.ptr(self.brv), 1, self.np_,
+                              None)
+            ctx.check(ctx.lib.gofann_rabitq_range_scan(
+                ctx.handle, self.rv, self.rq, L.PredicateView(), routes, L.ptr(self.postings),
+                self.resident, self.segs.view(), W, 0, L.ptr(self.sl_i[self.ng * W:]),
+                L.ptr(self.sl_d[self.ng * W:]), L.ptr(self.passes)))
+        if timed:
+            ev[3].record()
+        n = self.ng + self.np_
+        fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
+                                       self.sl_i, W, n, 10)
+        if timed:
+            ev[4].record()
+        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, fin_i, fin_d, 10,
+                                       self.nq, 10)
+        if timed:
+            ev[5].record()
+        return out_i
+
+    def stage_ms(self):
+        e = self.ev
+        return dict(prep=e[0].elapsed_time(e[1]), traversal=e[1].elapsed_time(e[2]),
+                    range_scan=e[2].elapsed_time(e[3]), rerank=e[3].elapsed_time(e[4]),
+                    merge=e[4].elapsed_time(e[5]))
+
+    def route_stats(self):
+        return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
+
+
+def main_c3(args):
+    import torch
+    from gofann_amd import _lib
+    torch.cuda.init()
+    wl, li, rq, rpi = build_world_c3(args, torch)
+    t0 = time.time()
+    gt = ground_truth_c3(wl, torch, args.gt_queries_c3)
+    log(f"C3 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
+    ctx = _lib.Context(0)
+    pipe = RabitqRangePipeline(ctx, wl, li, rq, rpi, torch, args.c3_scan_rows)
+    log(f"C3 routes: {pipe.ng} graph (wide ranges), {pipe.np_} range-posting scans "
+        f"({pipe.scan_rows_total} rows)")
+    ladder = [args.queue] if args.queue else [int(x) for x in args.c3_ladder.split(",")]
+    chosen, rec = ladder[-1], 0.0
+    nq = wl.queries.shape[0]
+    for Q in ladder:
+        out = pipe.step(Q)
+        torch.cuda.synchronize()
+        rec = recall_at_10(out.cpu().numpy().view(np.uint32).reshape(nq, 10), gt)
+        log(f"C3 Q={Q}: recall@10={rec:.4f}")
+        chosen = Q
+        if rec >= args.target_recall:
+            break
+    for _ in range(args.warmup):
+        pipe.step(chosen)
+    torch.cuda.synchronize()
+    stages = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = pipe.step(chosen, timed=True)
+        torch.cuda.synchronize()
+        stages.append(pipe.stage_ms())
+    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    res = out.cpu().numpy().view(np.uint32).reshape(nq, 10)
+    rec = recall_at_10(res, gt)
+    sel = wl.meta["selectivity"]
+    by_sel = {}
+    for s in sorted(set(sel.tolist())):
+        qs = {q: v for q, v in gt.items() if sel[q] == s}
+        by_sel[f"{100 * s:g}%"] = round(recall_at_10(res, qs), 4) if qs else None
+    st_ms = {k: round(float(np.mean([d[k] for d in stages])), 3) for k in stages[0]}
+    st = pipe.route_stats()
+    P = rq["P"]
+    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
+    sb = pipe.scan_rows_total * (4 + P // 8 + 12 + 4 + 4) + 0.0
+    rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 4 + 4) + 0.0
+    kern = {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
+            "range_scan_kernel+segment_merge_kernel": (st_ms["range_scan"], sb),
+            "exact_rerank_kernel (f32)": (st_ms["rerank"], rb)}
+    per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
+               "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None}
+           for k, v in kern.items()}
+    top = max(kern, key=lambda k: kern[k][0])
+    ach = kern[top][1] / (kern[top][0] / 1000.0) / 1e9
+    log(f"C3 step {ms:.1f} ms, stages {st_ms}, recall {rec:.4f} {by_sel}")
+    line = {
+        "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
+        "value": round(nq / (ms / 1000.0), 1),
+        "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8 codes / f32 rerank", "data": "synthetic",
+        "config": {"workload": "C3: 2.7Mx4096 fp32 unit-norm mixture, RaBitQ 1-bit (512 B "
+                               "codes), graph R=32, int32 attribute U[0,10000), ranges at "
+                               "0.5/5/50%, exact fp32 rerank of 200, top-10",
+                   "n": wl.n, "queries": nq, "graph_routes": pipe.ng,
+                   "range_posting_routes": pipe.np_, "scan_rows": pipe.scan_rows_total,
+                   "queue": chosen, "shortlist": pipe.W, "recall_at_10": round(rec, 4),
+                   "recall_by_selectivity": by_sel, "gt_queries": len(gt),
+                   "stage_ms": st_ms, "kernels": per, "placement": ctx.last_placement(),
+                   "data_model": "centre + rank-64 shared-basis spread 0.7 + N(0, 0.05^2), "
+                                 "normalised"},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5), "traffic": None,
+                     "kernel": top, "kernel_ms": kern[top][0],
+                     "algorithmic_bytes": kern[top][1]},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
 def main():
     args = parse()
+    if args.config == "c3" and args.gpus == 1:
+        main_c3(args)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build's "
               "search path runs on a single MI355X and has no multi-GPU mode.", file=sys.stderr)

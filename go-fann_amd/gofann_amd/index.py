@@ -184,9 +184,25 @@ def postings_from_csr(offsets: np.ndarray, values: np.ndarray, num_labels: int):
     return cat_freq, post_off, post_ids
 
 
-def _bucket_knn(xg: torch.Tensor, bucket_of: torch.Tensor, k: int, max_batch_elems: int):
-    """Exact k nearest rows inside each bucket (self excluded).  xg rows are
-    sorted by bucket.  Returns int64 [n, k] local row ids, -1 where missing."""
+def _row_norms(x: torch.Tensor, chunk: int = 1 << 18) -> torch.Tensor:
+    """Squared row norms of a large matrix, a chunk of rows at a time."""
+    out = torch.empty(x.shape[0], dtype=torch.float32, device=x.device)
+    for s0 in range(0, x.shape[0], chunk):
+        xs = x[s0:s0 + chunk].float()
+        out[s0:s0 + chunk] = (xs * xs).sum(1)
+    return out
+
+
+# Groups above this many bytes of fp32 rows are built without full copies
+# (rows gathered per bucket batch, means and distances a chunk at a time).
+LEAN_GROUP_BYTES = 8 << 30
+
+
+def _bucket_knn(xg: torch.Tensor, bucket_of: torch.Tensor, k: int, max_batch_elems: int,
+                order: torch.Tensor | None = None):
+    """Exact k nearest rows inside each bucket (self excluded).  The rows
+    xg[order[i]] (xg[i] without `order`) are sorted by bucket.  Returns int64
+    [n, k] ids in that sorted row space, -1 where missing."""
     dev = xg.device
     n = xg.shape[0]
     out = torch.full((n, k), -1, dtype=torch.int64, device=dev)
@@ -197,9 +213,13 @@ def _bucket_knn(xg: torch.Tensor, bucket_of: torch.Tensor, k: int, max_batch_ele
     starts[1:] = torch.cumsum(counts, 0)[:-1]
     counts_h = counts.cpu().numpy()
     starts_h = starts.cpu().numpy()
-    order = np.argsort(counts_h, kind="stable")
     i = 0
-    xn = (xg * xg).sum(1)
+    if order is None:
+        xn = (xg * xg).sum(1)
+    else:
+        xn = _row_norms(xg)[order]
+    border = order
+    order = np.argsort(counts_h, kind="stable")
     while i < len(order):
         bm = int(counts_h[order[i]])
         j = i
@@ -217,7 +237,7 @@ def _bucket_knn(xg: torch.Tensor, bucket_of: torch.Tensor, k: int, max_batch_ele
         rows = st[:, None] + ar[None, :]  # [nb, bmax]
         valid = ar[None, :] < ct[:, None]
         rows_c = torch.where(valid, rows, torch.zeros_like(rows))
-        xb = xg[rows_c]  # [nb, bmax, D]
+        xb = xg[rows_c] if border is None else xg[border[rows_c]]  # [nb, bmax, D]
         d2 = xn[rows_c][:, :, None] + xn[rows_c][:, None, :] - 2 * torch.bmm(xb, xb.transpose(1, 2))
         big = torch.finfo(d2.dtype).max
         d2 = d2.masked_fill(~valid[:, None, :], big)
@@ -244,21 +264,37 @@ def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch
     n = xg.shape[0]
     R = degree
     rep_bridges = rep_bridges if rep_bridges is not None else R // 2
+    lean = n * xg.shape[1] * 4 > LEAN_GROUP_BYTES
     xg = xg.float()
     order = torch.argsort(cluster_of, stable=True)
-    xs = xg[order]
     bs = cluster_of[order]
     k_local = R - bridges
-    knn = _bucket_knn(xs, bs, k_local, max_batch_elems)  # in sorted row space
+    xs = None if lean else xg[order]
+    if lean:
+        knn = _bucket_knn(xg, bs, k_local, max_batch_elems, order=order)
+    else:
+        knn = _bucket_knn(xs, bs, k_local, max_batch_elems)  # in sorted row space
     uniq, counts = torch.unique_consecutive(bs, return_counts=True)
     nb = uniq.shape[0]
     starts = torch.zeros_like(counts)
     starts[1:] = torch.cumsum(counts, 0)[:-1]
     bucket_idx = torch.repeat_interleave(torch.arange(nb, device=dev), counts)
     # representative: row nearest its bucket mean
-    sums = torch.zeros(nb, xs.shape[1], device=dev).index_add_(0, bucket_idx, xs)
-    means = sums / counts[:, None].float()
-    dm = ((xs - means[bucket_idx]) ** 2).sum(1)
+    if lean:
+        b_orig = torch.searchsorted(uniq, cluster_of)
+        sums = torch.zeros(nb, xg.shape[1], device=dev)
+        for s0 in range(0, n, 1 << 18):
+            sums.index_add_(0, b_orig[s0:s0 + (1 << 18)], xg[s0:s0 + (1 << 18)])
+        means = sums / counts[:, None].float()
+        dm_o = torch.empty(n, dtype=torch.float32, device=dev)
+        for s0 in range(0, n, 1 << 18):
+            d = xg[s0:s0 + (1 << 18)] - means[b_orig[s0:s0 + (1 << 18)]]
+            dm_o[s0:s0 + (1 << 18)] = (d * d).sum(1)
+        dm = dm_o[order]
+    else:
+        sums = torch.zeros(nb, xs.shape[1], device=dev).index_add_(0, bucket_idx, xs)
+        means = sums / counts[:, None].float()
+        dm = ((xs - means[bucket_idx]) ** 2).sum(1)
     big = torch.finfo(dm.dtype).max
     rep = torch.empty(nb, dtype=torch.int64, device=dev)
     for_min = torch.full((nb,), big, device=dev).scatter_reduce(0, bucket_idx, dm, "amin")
@@ -349,13 +385,25 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
         o = int(label_offset[l])
         row_to_sample[o:o + len(samples)] = samples
         sidx = torch.as_tensor(samples.astype(np.int64), device=base.device)
-        xg = base[sidx].float()
+        whole = len(samples) == base.shape[0] and base.dtype == torch.float32
+        xg = base if whole else base[sidx].float()  # every row, in order: no copy
         graph[o:o + len(samples)], rep_cluster[l], rep_row[l] = build_group_graph(
             xg, cluster[sidx], centres, degree, bridges, return_reps=True)
         # seed: row nearest the group mean (fp64), dataloader.cpp:7361-7406
-        xd = xg.double()
-        mu = xd.mean(0, keepdim=True)
-        seed_local[l] = int(((xd - mu) ** 2).sum(1).argmin())
+        if xg.shape[0] * xg.shape[1] * 4 > LEAN_GROUP_BYTES:
+            step = 1 << 16
+            mu = torch.zeros(1, xg.shape[1], dtype=torch.float64, device=xg.device)
+            for s0 in range(0, xg.shape[0], step):
+                mu += xg[s0:s0 + step].double().sum(0, keepdim=True)
+            mu /= xg.shape[0]
+            dist = torch.empty(xg.shape[0], dtype=torch.float64, device=xg.device)
+            for s0 in range(0, xg.shape[0], step):
+                dist[s0:s0 + step] = ((xg[s0:s0 + step].double() - mu) ** 2).sum(1)
+            seed_local[l] = int(dist.argmin())
+        else:
+            xd = xg.double()
+            mu = xd.mean(0, keepdim=True)
+            seed_local[l] = int(((xd - mu) ** 2).sum(1).argmin())
     rep_off = np.zeros(num_labels + 1, dtype=np.int64)
     np.cumsum([len(r) for r in rep_row], out=rep_off[1:])
     return LabelIndex(num_labels, threshold, cat_freq, label_offset, label_size, row_to_sample,

@@ -193,3 +193,47 @@ def small_labelled(n=4096, nq=64, dim=32, k=16, sigma=0.6, labels=6, seed=77, de
             query_ranges.append([(0, 3, lo_v, lo_v + float(rng.integers(100, 400)))])
     return Workload("small", x, q, cl, cen, lo, lv, labels, ql, base_ranges, query_ranges,
                     meta=dict(sigma=sigma, clusters=k))
+
+
+def config3(n=2_700_000, nq=10_000, device="cuda", dim=4096, k=512, rank=64, spread=0.7,
+            noise=0.05, selectivities=(0.005, 0.05, 0.5), attr_range=10_000, seed=3,
+            chunk=1 << 17):
+    """C3: unit-normalised vectors from a k-centre mixture in `dim`
+    dimensions and one int32 attribute uniform in [0, attr_range).  A point
+    is centre + U z + e, normalised: U a shared random [rank][dim] basis
+    (so the data has low intrinsic dimension and meaningful nearest
+    neighbours), z ~ N(0, spread^2 |c|^2 / rank) per coordinate so that |U z|
+    is about spread |c|, e ~ N(0, noise^2).  Queries come from the same
+    mixture; query i carries the range [lo, lo + w) of the attribute with
+    w = selectivities[i % len] * attr_range and lo uniform (mode 3)."""
+    cfg = seed * 1000
+    gc = _gen(cfg + 1, device)
+    centres = torch.randn(k, dim, generator=gc, device=device)
+    basis = torch.randn(rank, dim, generator=gc, device=device)
+    zscale = spread / rank ** 0.5  # |U z| ~ spread * sqrt(dim) ~ spread * |c|
+
+    def draw(m, g):
+        cl = torch.randint(0, k, (m,), generator=g, device=device)
+        out = torch.empty(m, dim, dtype=torch.float32, device=device)
+        for s in range(0, m, chunk):
+            e = min(m, s + chunk)
+            z = torch.randn(e - s, rank, generator=g, device=device) * zscale
+            x = centres[cl[s:e]] + z @ basis + noise * torch.randn(e - s, dim, generator=g,
+                                                                   device=device)
+            out[s:e] = x / x.norm(dim=1, keepdim=True)
+        return out, cl
+
+    base, cl = draw(n, _gen(cfg + 2, device))
+    queries, _ = draw(nq, _gen(cfg + 4, device))
+    rng = np.random.default_rng(cfg + 3)
+    attr = rng.integers(0, attr_range, size=n).astype(np.float32)
+    sel = np.array([selectivities[i % len(selectivities)] for i in range(nq)], dtype=np.float64)
+    width = np.maximum(1, np.round(sel * attr_range)).astype(np.int64)
+    lo = (rng.random(nq) * (attr_range - width + 1)).astype(np.int64)
+    query_ranges = [[(0, 3, float(lo[i]), float(lo[i] + width[i]))] for i in range(nq)]
+    cn = centres / centres.norm(dim=1, keepdim=True)
+    wl = Workload("config3", base, queries, cl, cn,
+                  np.arange(n + 1, dtype=np.uint32), np.zeros(n, dtype=np.uint32), 1,
+                  [[0] for _ in range(nq)], attr[:, None].copy(), query_ranges,
+                  meta=dict(selectivity=sel, spread=spread, rank=rank, noise=noise))
+    return wl
