@@ -40,6 +40,7 @@
 // merge_one_query's heap inserts do.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <cstdint>
 
@@ -286,6 +287,287 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_kernel(RangeScanArgs 
     if (tid == 0 && a.pass_counts) a.pass_counts[seg] = s_pass;
 }
 
+// ---------------------------------------------------------------------------
+// Group-per-row scan.  A group of G lanes (G a power of two, <= 32) scores
+// one code row: lane l of the group owns the 16-byte code vectors l, l + G,
+// .. of the row (W of them, padded_dim / 128 = G * W), so one wave load
+// reads 64 / G whole rows, and keeps the query bit planes of its words in
+// registers.  The group's partial inner products are summed by a DPP
+// butterfly.  Each chunk is first passed over one row per thread: the
+// posting id, the filter, and the row's distance terms that need no code
+// bits (f_add + g, f_rescale) are gathered into LDS; filter-first packs the
+// passing rows (the shortlist does not depend on scan order), score-first
+// keeps scan positions for its pass counts.
+// ---------------------------------------------------------------------------
+
+// Sum of x over the G-lane group holding this lane (G a power of two <= 32),
+// delivered to every lane of the group; every lane of the group is active.
+template <int G>
+__device__ __forceinline__ int group_sum(int x)
+{
+    if constexpr (G >= 2) x += __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);   // lane ^ 1
+    if constexpr (G >= 4) x += __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);   // lane ^ 2
+    if constexpr (G >= 8) x += __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);  // 7 - lane in 8
+    if constexpr (G >= 16) x += __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false); // 15 - lane in 16
+    if constexpr (G >= 32) x += __shfl_xor(x, 16, 64);
+    return x;
+}
+
+// This lane's share of sum_d q8[d] * bit[d] over its W code vectors:
+// sum_j 2^j popc(plane_j & code) for the seven low planes, minus 128 times
+// the sign plane's count.
+template <int W>
+__device__ __forceinline__ int lane_ip(const uint4 (&c)[W], const uint32_t (&pl)[W * 32])
+{
+    uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        const uint32_t cw[4] = {c[w].x, c[w].y, c[w].z, c[w].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) cnt[j] += __popc(pl[w * 32 + t * 8 + j] & cw[t]);
+    }
+    int ip = 0;
+#pragma unroll
+    for (int j = 0; j < 7; ++j) ip += static_cast<int>(cnt[j]) << j;
+    return ip - 128 * static_cast<int>(cnt[7]);
+}
+
+constexpr int kRowUnroll = 2;  // rows in flight per group
+
+template <int G, int W>
+__global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeScanArgs a,
+                                                                        RabitqScanScorer sc)
+{
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ uint32_t s_surv;
+    __shared__ uint32_t s_rows;
+    __shared__ uint32_t s_pass;
+    __shared__ uint32_t s_slot;
+    const int tid = static_cast<int>(threadIdx.x);
+    const uint32_t seg = blockIdx.x;
+    if (seg >= a.segments) return;
+    float* s_d = reinterpret_cast<float*>(lds + a.planes_bytes);
+    uint32_t* s_id = reinterpret_cast<uint32_t*>(s_d + a.slots);
+    float* s_f1 = reinterpret_cast<float*>(s_id + a.slots);
+
+    const uint32_t route = a.seg_route[seg];
+    const uint32_t query = a.routes.route_query[route];
+    sc.setup(query, tid, lds);
+    for (int i = tid; i < a.slots; i += kScanThreads) {
+        s_d[i] = FLT_MAX;
+        s_id[i] = UINT32_MAX;
+    }
+    if (tid == 0) {
+        s_pass = 0;
+        s_surv = 0;
+        s_rows = 0;
+    }
+    __syncthreads();
+    constexpr int kGroups = kScanThreads / G;
+    const int lg = tid & (G - 1);
+    const int grp = tid / G;
+    uint32_t pl[W * 32];
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint4 v = reinterpret_cast<const uint4*>(sc.planes)[(lg + G * w) * 8 + t];
+            pl[w * 32 + t * 4 + 0] = v.x;
+            pl[w * 32 + t * 4 + 1] = v.y;
+            pl[w * 32 + t * 4 + 2] = v.z;
+            pl[w * 32 + t * 4 + 3] = v.w;
+        }
+    const uint4* codes = reinterpret_cast<const uint4*>(sc.codes);
+    const size_t row_vecs = static_cast<size_t>(G) * W;
+
+    // :5895-5902
+    const uint64_t begin = a.seg_offset[seg];
+    uint64_t count = a.seg_size[seg];
+    if (begin > a.resident_rows)
+        count = 0;
+    else if (count > a.resident_rows - begin)
+        count = a.resident_rows - begin;
+    const uint32_t active = count_active_ranges(a.routes.range_modes, route, a.routes.range_count);
+    if (active == 0) count = 0;  // :5917
+    const bool enabled = pred_enabled(a.pred, route);
+    const bool score_first = a.score_first != 0 && enabled;
+    const int k = a.k, kp = a.k_pow2;
+    const int chunk = a.chunk;
+    const int per = chunk / kScanThreads;
+    uint32_t passes = 0;
+    uint32_t surv_total = 0;  // s_surv and s_rows only grow: a chunk's count is the increment
+    uint32_t rows_total = 0;
+
+    for (uint64_t base = 0; base < count; base += static_cast<uint64_t>(chunk)) {
+        // Every read of the previous chunk ends here.
+        __syncthreads();
+        const float kth_d = s_d[k - 1];
+        const uint32_t kth_id = s_id[k - 1];
+        // Pass 1, one row per thread: posting id, filter, code-free terms.
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            if (t >= per) break;
+            const int i = tid + t * kScanThreads;
+            const uint64_t j = base + static_cast<uint64_t>(i);
+            uint32_t s = UINT32_MAX;
+            bool ok = false;
+            if (j < count) {
+                s = a.posting[begin + j];
+                ok = s < a.base_rows;
+                if (ok) {
+                    if (enabled) {
+                        PredCounters c{0, 0};
+                        ok = pred_matches(a.pred, route, s, c);
+                    } else if (active > 1) {
+                        ok = count_matching_ranges(a.routes, route, s) == active;
+                    }
+                }
+            }
+            float add0 = FLT_MAX, f1 = 0.0f;
+            if (ok) {
+                if (!score_first) ++passes;
+                const uint32_t anchor = sc.anchor_ids[s];
+                add0 = sc.factors[static_cast<size_t>(s) * 3] + sc.g_row[anchor];
+                f1 = sc.factors[static_cast<size_t>(s) * 3 + 1];
+            }
+            int pos = i;
+            if (!score_first) {
+                // pack the passing rows: a wave reserves its slots at once
+                const uint64_t mask = __ballot(ok);
+                uint32_t first = 0;
+                if (__lane_id() == __ffsll(static_cast<unsigned long long>(mask)) - 1)
+                    first = atomicAdd(&s_rows, static_cast<uint32_t>(__popcll(mask)));
+                first = __shfl(first, __ffsll(static_cast<unsigned long long>(mask)) - 1, 64);
+                pos = static_cast<int>(first - rows_total) +
+                      __popcll(mask & ((1ull << __lane_id()) - 1ull));
+            }
+            if (ok || score_first) {
+                s_id[kp + pos] = ok ? s : UINT32_MAX;
+                s_d[kp + pos] = add0;
+                s_f1[pos] = f1;
+            }
+        }
+        __syncthreads();
+        int n_rows;
+        if (score_first) {
+            const uint64_t left = count - base;
+            n_rows = left < static_cast<uint64_t>(chunk) ? static_cast<int>(left) : chunk;
+        } else {
+            const uint32_t now = s_rows;
+            n_rows = static_cast<int>(now - rows_total);
+            rows_total = now;
+        }
+        for (int i = n_rows + tid; i < chunk; i += kScanThreads) {
+            s_d[kp + i] = FLT_MAX;
+            s_id[kp + i] = UINT32_MAX;
+        }
+        // Pass 2, a group per row: code bits, distance, survivor test.
+        uint32_t surv = 0;
+        for (int i0 = grp; i0 < n_rows; i0 += kGroups * kRowUnroll) {
+            uint32_t sid[kRowUnroll];
+            uint4 c[kRowUnroll][W];
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) {
+                const int i = i0 + u * kGroups;
+                sid[u] = i < n_rows ? s_id[kp + i] : UINT32_MAX;
+                if (sid[u] != UINT32_MAX) {
+                    const uint4* row = codes + static_cast<size_t>(sid[u]) * row_vecs;
+#pragma unroll
+                    for (int w = 0; w < W; ++w) c[u][w] = row[lg + G * w];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kRowUnroll; ++u) {
+                if (sid[u] == UINT32_MAX) continue;  // uniform over the group
+                const int ip = group_sum<G>(lane_ip<W>(c[u], pl));
+                if (lg == 0) {
+                    const int i = i0 + u * kGroups;
+                    const float short_ip = static_cast<float>(ip) * sc.scale;
+                    const float tt = short_ip + sc.k1;
+                    const float v = fmaf(s_f1[i], tt, s_d[kp + i]);
+                    const bool in = admissible(v, sid[u]) && pair_less(v, sid[u], kth_d, kth_id);
+                    s_d[kp + i] = in ? v : FLT_MAX;
+                    s_id[kp + i] = in ? sid[u] : UINT32_MAX;
+                    surv += in ? 1u : 0u;
+                }
+            }
+        }
+        if (surv) atomicAdd(&s_surv, surv);
+        __syncthreads();
+        const uint32_t now = s_surv;
+        const int m = static_cast<int>(now - surv_total);
+        surv_total = now;
+        if (m == 0) continue;  // uniform: nothing can enter
+        if (score_first) {
+            for (int i = tid; i < chunk; i += kScanThreads) {
+                const uint32_t xid = s_id[kp + i];
+                if (xid == UINT32_MAX) continue;
+                const float x = s_d[kp + i];
+                int cnt = count_le(s_d, s_id, k, x, xid);
+                for (int j = 0; j < i && cnt < k; ++j)
+                    if (s_id[kp + j] != UINT32_MAX && pair_le(s_d[kp + j], s_id[kp + j], x, xid))
+                        ++cnt;
+                if (cnt < k) ++passes;
+            }
+            __syncthreads();  // the counts read LDS that the merge below reorders
+        }
+        const int mp = pow2_ceil(m);
+        if (mp <= kp) {
+            // Gather the survivors at the tail of [kp, 2kp), sort them
+            // descending, then merge with the ascending running list.
+            float keep_d[8];
+            uint32_t keep_id[8];
+            int nk = 0;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int i = tid + t * kScanThreads;
+                keep_d[t] = t < per ? s_d[kp + i] : FLT_MAX;
+                keep_id[t] = t < per ? s_id[kp + i] : UINT32_MAX;
+                nk += keep_id[t] != UINT32_MAX ? 1 : 0;
+            }
+            if (tid == 0) s_slot = 0;
+            __syncthreads();
+            for (int i = tid; i < kp; i += kScanThreads) {
+                s_d[kp + i] = FLT_MAX;
+                s_id[kp + i] = UINT32_MAX;
+            }
+            __syncthreads();
+            if (nk) {
+                uint32_t at = atomicAdd(&s_slot, static_cast<uint32_t>(nk));
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    if (keep_id[t] == UINT32_MAX) continue;
+                    const int pos = 2 * kp - mp + static_cast<int>(at++);
+                    s_d[pos] = keep_d[t];
+                    s_id[pos] = keep_id[t];
+                }
+            }
+            __syncthreads();
+            bitonic_sort_desc(s_d, s_id, 2 * kp - mp, mp, tid, kScanThreads);
+        } else {
+            // More survivors than the list holds, so 2 kp <= chunk: sort the
+            // chunk descending and move its kp least (its last kp) to
+            // [kp, 2kp), which does not overlap [chunk, chunk + kp).
+            bitonic_sort_desc(s_d, s_id, kp, chunk, tid, kScanThreads);
+            for (int i = tid; i < kp; i += kScanThreads) {
+                s_d[kp + i] = s_d[chunk + i];
+                s_id[kp + i] = s_id[chunk + i];
+            }
+            __syncthreads();
+        }
+        bitonic_merge(s_d, s_id, 2 * kp, tid, kScanThreads);
+    }
+    if (passes) atomicAdd(&s_pass, passes);
+    __syncthreads();
+    for (int i = tid; i < k; i += kScanThreads) {
+        a.out_ids[static_cast<size_t>(seg) * k + i] = s_id[i];
+        a.out_dists[static_cast<size_t>(seg) * k + i] = s_d[i];
+    }
+    if (tid == 0 && a.pass_counts) a.pass_counts[seg] = s_pass;
+}
+
 struct SegmentMergeArgs {
     const uint32_t* query_indptr;
     uint32_t positions;
@@ -428,16 +710,40 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
     sc.scale = sc.k1 = 0.0f;
     sc.g_row = nullptr;
 
-    const size_t lds = a.planes_bytes + static_cast<size_t>(a.slots) * 8;
+    // Group-per-row kernel when the row's 16-byte vectors split evenly over
+    // a power-of-two group of <= 32 lanes, two vectors per lane at most;
+    // thread-per-row kernel otherwise.
+    const uint32_t nvec = rq->padded_dim / 128;
+    const void* kern = nullptr;
+    switch (nvec) {
+        case 1: kern = reinterpret_cast<const void*>(range_scan_group_kernel<1, 1>); break;
+        case 2: kern = reinterpret_cast<const void*>(range_scan_group_kernel<2, 1>); break;
+        case 4: kern = reinterpret_cast<const void*>(range_scan_group_kernel<4, 1>); break;
+        case 8: kern = reinterpret_cast<const void*>(range_scan_group_kernel<8, 1>); break;
+        case 16: kern = reinterpret_cast<const void*>(range_scan_group_kernel<16, 1>); break;
+        case 32: kern = reinterpret_cast<const void*>(range_scan_group_kernel<32, 1>); break;
+        case 64: kern = reinterpret_cast<const void*>(range_scan_group_kernel<32, 2>); break;
+        default: break;
+    }
+    size_t lds;
+    if (kern) {
+        // [0, kp) running list, [kp, kp + chunk) the chunk; the merges use
+        // [0, 2 kp); then chunk floats of f_rescale.
+        a.slots = std::max(2 * a.k_pow2, a.k_pow2 + a.chunk);
+        lds = a.planes_bytes + static_cast<size_t>(a.slots) * 8 + static_cast<size_t>(a.chunk) * 4;
+    } else {
+        kern = reinterpret_cast<const void*>(range_scan_kernel);
+        lds = a.planes_bytes + static_cast<size_t>(a.slots) * 8;
+    }
     if (lds > static_cast<size_t>(ctx->lds_per_block))
         return ctx->fail(GOFANN_ERR_UNSUPPORTED, "range scan LDS exceeds the workgroup limit");
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(range_scan_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
-        hipSuccess)
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
         return ctx->fail_hip("hipFuncSetAttribute range scan");
-    hipLaunchKernelGGL(range_scan_kernel, dim3(seg->count), dim3(kScanThreads), lds, ctx->stream,
-                       a, sc);
-    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("range scan launch");
+    void* kargs[] = {&a, &sc};
+    if (hipLaunchKernel(kern, dim3(seg->count), dim3(kScanThreads), kargs, lds, ctx->stream) !=
+        hipSuccess)
+        return ctx->fail_hip("range scan launch");
     if (!merged) return GOFANN_OK;
 
     SegmentMergeArgs m;

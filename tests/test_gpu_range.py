@@ -32,13 +32,23 @@ def as_u32(t):
     return t.cpu().numpy().view(np.uint32)
 
 
-@pytest.fixture(scope="module")
-def rangeworld(gpu_ctx):
+# Padded dims: 128 .. 4096 take the group-per-row kernel with groups of
+# 1 .. 32 lanes, 8192 its two-vectors-per-lane form, 384 (three 16-byte
+# vectors) the thread-per-row kernel.
+@pytest.fixture(scope="module", params=[128, 384, 1024, 4096, 8192])
+def rangeworld(request, gpu_ctx):
     wl = synth.small_labelled(n=6000, nq=40, dim=60, k=10, sigma=0.7, labels=5, seed=41, tags=True)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
                               wl.centroids, degree=32, threshold=300)
-    P = 128
-    rot = gi.random_rotation(wl.dim, P, 41005, "cpu")
+    P = request.param
+    say("range world, padded dim", P)
+    if P <= 1024:
+        rot = gi.random_rotation(wl.dim, P, 41005, "cpu")
+    else:
+        # any [dim][P] matrix gives codes both sides score alike; a QR this
+        # large would dominate the test
+        g = torch.Generator().manual_seed(41005)
+        rot = torch.randn(wl.dim, P, generator=g) / P ** 0.5
     codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
     n = wl.n
     rng = np.random.default_rng(41)
@@ -81,6 +91,7 @@ def rangeworld(gpu_ctx):
                                                             _lib.ptr(dev["rot"]), rq))
     torch.cuda.synchronize()
     host_q = {k: v.cpu().numpy() for k, v in out.items()}
+    dev["prepared"] = out  # rq holds raw pointers into these tensors
     dg = gs.DeviceGraph.upload(li)
     dr = gs.DeviceRoutes.upload(rs, base_ranges)
     dev.update(postings=index.device_postings(), modes=torch.from_numpy(modes).cuda(),
@@ -110,6 +121,16 @@ def _oracle(w, pred, seg_routes, seg_off, seg_size, k, score_first, resident=Non
                                 w["wl"].n, seg_routes, seg_off, seg_size, k, score_first)
 
 
+def _explain(gi_, gd, oi, od):
+    """Print the first differing (route, position) with its neighbourhood."""
+    bad = np.nonzero((gi_ != oi).any(1) | (gd.view(np.uint32) != od.view(np.uint32)).any(1))[0]
+    for r in bad[:3]:
+        j = int(np.nonzero((gi_[r] != oi[r]) | (gd[r].view(np.uint32) != od[r].view(np.uint32)))[0][0])
+        lo, hi = max(0, j - 2), j + 3
+        say("route", r, "pos", j, "of", gi_.shape[1], "gpu", list(zip(gi_[r, lo:hi].tolist(), gd[r, lo:hi].tolist())),
+            "oracle", list(zip(oi[r, lo:hi].tolist(), od[r, lo:hi].tolist())))
+
+
 @pytest.mark.parametrize("k", [10, 200, 1000, 4096])
 @pytest.mark.parametrize("segment_rows", [0, 700])
 @pytest.mark.parametrize("score_first,with_pred", [(False, False), (False, True), (True, True)])
@@ -135,6 +156,7 @@ def test_range_scan_matches_oracle(gpu_ctx, rangeworld, k, segment_rows, score_f
                                               w["dev"]["postings"], w["index"].resident_rows, segs,
                                               k, score_first)
     torch.cuda.synchronize()
+    _explain(as_u32(ids), dists.cpu().numpy(), oi, od)
     assert np.array_equal(as_u32(ids), oi)
     assert np.array_equal(dists.cpu().numpy().view(np.uint32), od.view(np.uint32))
     assert np.array_equal(as_u32(passes), op)
