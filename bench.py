@@ -64,9 +64,16 @@ def parse():
                     help="separate code rows and CSR labels instead of 64-byte sample records")
     ap.add_argument("--no-cpu-rerank-route", action="store_true",
                     help="skip the GPU+CPU-rerank route measurement")
-    ap.add_argument("--config", choices=("c2", "c3"), default="c2",
+    ap.add_argument("--config", choices=("c2", "c3", "c4"), default="c2",
                     help="c2 (default): 10Mx192 u8 PQ/exact routes; c3: 2.7Mx4096 fp32 RaBitQ "
-                         "with range predicates")
+                         "with range predicates; c4: 100Mx512 fp16 RaBitQ with categorical "
+                         "and range predicates")
+    ap.add_argument("--n-c4", type=int, default=100_000_000)
+    ap.add_argument("--queries-c4", type=int, default=10_000)
+    ap.add_argument("--gt-queries-c4", type=int, default=1000)
+    ap.add_argument("--c4-ladder", default="16,24,32,48,64,96,128,192")
+    ap.add_argument("--c4-threshold", type=int, default=50_000,
+                    help="labels with at most this many rows are posting routes")
     ap.add_argument("--n-c3", type=int, default=2_700_000)
     ap.add_argument("--queries-c3", type=int, default=10_000)
     ap.add_argument("--gt-queries-c3", type=int, default=999)
@@ -509,15 +516,15 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False
 # ---------------------------------------------------------------------------
 def rabitq_traversal_bytes(st: np.ndarray, degree: int, code_bytes: int) -> float:
     """Bytes the RaBitQ traversal must move: the adjacency row and
-    row_to_sample word of each expanded node, each scored candidate's code
-    row, factors (12 B), anchor id and row_to_sample word, its base range
-    value (the route predicate is a range atom), and the CSR words of label
-    checks."""
+    row_to_sample word of each expanded node; per scored candidate its code
+    row, anchor id and f_add/f_rescale (C = P/8 + 4 + 8) and row_to_sample
+    word, plus its base range value (the route predicate is a range atom);
+    and the CSR words of label checks."""
     E = st[:, 1].astype(np.float64).sum()
     V = st[:, 3].astype(np.float64).sum()
     rows = st[:, 4].astype(np.float64).sum()
     labels = st[:, 5].astype(np.float64).sum()
-    return E * (4 * degree + 4) + V * (code_bytes + 12 + 4 + 4 + 4) + rows * 8 + labels * 4
+    return E * (4 * degree + 4) + V * (code_bytes + 4 + 8 + 4 + 4) + rows * 8 + labels * 4
 
 
 def build_world_c3(args, torch):
@@ -724,7 +731,7 @@ def main_c3(args):
     st = pipe.route_stats()
     P = rq["P"]
     tb = rabitq_traversal_bytes(st, li.degree, P // 8)
-    sb = pipe.scan_rows_total * (4 + P // 8 + 12 + 4 + 4) + 0.0
+    sb = pipe.scan_rows_total * (4 + P // 8 + 4 + 8) + 0.0  # posting id + C per row
     rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 4 + 4) + 0.0
     kern = {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
             "range_scan_kernel+segment_merge_kernel": (st_ms["range_scan"], sb),
@@ -761,10 +768,277 @@ def main_c3(args):
     ctx.close()
 
 
+
+# ---------------------------------------------------------------------------
+# C4: 100M x 512 fp16, one-bit RaBitQ (64 B codes), categorical equality or
+# 1-10% range predicates (--config c4).
+# ---------------------------------------------------------------------------
+def build_world_c4(args, torch):
+    from gofann_amd import index as gi
+    from gofann_amd import synth
+    t0 = time.time()
+    wl = synth.config4(n=args.n_c4, nq=args.queries_c4, device="cuda")
+    torch.cuda.synchronize()
+    log(f"C4 data {wl.n}x{wl.dim} fp16, {wl.queries.shape[0]} queries in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=32, threshold=args.c4_threshold, progress=log)
+    torch.cuda.empty_cache()
+    ng = int((li.label_size > 0).sum())
+    log(f"C4 graphs: {ng} label/interval groups, {li.rows} rows, degree {li.degree} in "
+        f"{time.time() - t0:.1f}s")
+    t0 = time.time()
+    P = wl.dim
+    rot = gi.random_rotation(wl.dim, P, 4005, "cuda")
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids, chunk=1 << 18)
+    torch.cuda.synchronize()
+    log(f"C4 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
+    return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P)
+
+
+def ground_truth_c4(wl, torch, nq, chunk=1 << 20):
+    """Exact filtered top-10 (fp32 L2 of the fp16 rows) for the first nq
+    queries: equality on the categorical label, or the attribute range."""
+    n = wl.n
+    q = wl.queries[:nq].float()
+    qn = (q * q).sum(1)
+    cat = torch.as_tensor(wl.label_values[0::2].astype(np.int32), device="cuda")
+    attr = torch.as_tensor(wl.base_ranges[:, 0], device="cuda")
+    qlab = torch.tensor([ql[0] if ql else -1 for ql in wl.query_labels[:nq]], device="cuda",
+                        dtype=torch.int32)
+    lo = torch.tensor([qr[0][2] if qr else 0.0 for qr in wl.query_ranges[:nq]], device="cuda")
+    hi = torch.tensor([qr[0][3] if qr else 0.0 for qr in wl.query_ranges[:nq]], device="cuda")
+    is_rng = qlab < 0
+    best_d = torch.full((10, nq), float("inf"), device="cuda")
+    best_i = torch.full((10, nq), -1, dtype=torch.int64, device="cuda")
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        xf = wl.base[s:e].float()
+        d = (xf * xf).sum(1)[:, None] + qn[None, :] - 2.0 * (xf @ q.t())
+        a = attr[s:e, None]
+        ok = torch.where(is_rng[None, :], (a >= lo[None, :]) & (a < hi[None, :]),
+                         cat[s:e, None] == qlab[None, :])
+        d = torch.where(ok, d, torch.full_like(d, float("inf")))
+        v, i = torch.topk(d, min(10, e - s), dim=0, largest=False)
+        cd = torch.cat([best_d, v], 0)
+        ci = torch.cat([best_i, i + s], 0)
+        v2, j = torch.topk(cd, 10, dim=0, largest=False)
+        best_d, best_i = v2, torch.gather(ci, 0, j)
+    bd, bi = best_d.t().cpu().numpy(), best_i.t().cpu().numpy()
+    gt = {}
+    for r in range(nq):
+        ids = bi[r][np.isfinite(bd[r])]
+        if ids.size:
+            gt[r] = ids
+    return gt
+
+
+class RabitqLabelPipeline:
+    """One step of the C4 route set on the GPU: query preparation, one
+    RaBitQ graph traversal over every graph route (equality queries on a
+    label with a graph; range queries as one route per attribute interval
+    they overlap, with the range as residual predicate only where the
+    interval is not wholly inside it), the RaBitQ label-posting scan for
+    equality queries on rare labels, exact fp16->fp32 rerank of the W-wide
+    shortlists, and the per-query merge."""
+
+    def __init__(self, ctx, wl, li, rq, torch, width=100):
+        from gofann_amd import _lib
+        from gofann_amd import plan as gp
+        from gofann_amd import search as gs
+        self.ctx, self.wl, self.torch, self.L, self.gs = ctx, wl, torch, _lib, gs
+        nq = wl.queries.shape[0]
+        self.nq, self.W = nq, width
+        P = rq["P"]
+        cats, nint, amax = wl.meta["categories"], wl.meta["intervals"], wl.meta["attr_max"]
+        starts = [-(-(i * amax) // nint) for i in range(nint + 1)]  # ceil(i * amax / nint)
+        graph_rows, post_rows = [], []
+        self.interior = 0
+        for q in range(nq):
+            if wl.query_labels[q]:
+                lab = wl.query_labels[q][0]
+                (graph_rows if li.has_graph(lab) else post_rows).append((q, lab, [], []))
+                continue
+            (_, _, lo, hi), = wl.query_ranges[q]
+            i0 = int(lo) * nint // amax
+            i1 = (int(hi) - 1) * nint // amax
+            for i in range(i0, i1 + 1):
+                inside = starts[i] >= lo and starts[i + 1] <= hi
+                self.interior += int(inside)
+                graph_rows.append((q, cats + i, [], [] if inside else [(0, 3, lo, hi)]))
+        graph_rows.sort(key=lambda r: (r[1], r[0]))
+        rs = gp._routeset(graph_rows, li)
+        if rs.count:
+            rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
+        ps = gp._routeset(post_rows, li)
+        self.rs, self.ps = rs, ps
+        self.ng, self.np_ = rs.count, ps.count
+        self.dg = gs.DeviceGraph.upload(li)
+        self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+        self.dp = gs.DeviceRoutes.upload(ps)
+        off = np.array([li.posting_offset[r[1]] for r in post_rows], dtype=np.uint32)
+        size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]]
+                         for r in post_rows], dtype=np.uint32)
+        self.post_rows_total = int(size.sum())
+        self.co, self.cs = gs.u32(off if len(off) else np.zeros(1, np.uint32)), \
+            gs.u32(size if len(size) else np.zeros(1, np.uint32))
+        self.dev = dict(codes=rq["codes"], fac=rq["fac"], aid=rq["aid"].view(torch.int32),
+                        anchors=rq["anchors"], rot=rq["rot"])
+        self.rv = _lib.RabitqView(_lib.ptr(self.dev["codes"]), _lib.ptr(self.dev["fac"]),
+                                  _lib.ptr(self.dev["aid"]), _lib.ptr(self.dev["anchors"]),
+                                  wl.dim, P, rq["anchors"].shape[0], wl.n)
+        A = rq["anchors"].shape[0]
+        self.prep = dict(rotated=torch.empty(nq, P, device="cuda"),
+                         q8=torch.empty(nq, P, dtype=torch.int8, device="cuda"),
+                         scale=torch.empty(nq, device="cuda"), k1=torch.empty(nq, device="cuda"),
+                         cd=torch.empty(nq, A, device="cuda"))
+        self.rq = _lib.RabitqQueries(*[_lib.ptr(self.prep[k]) for k in
+                                       ("rotated", "q8", "scale", "k1", "cd")], nq)
+        n = self.ng + self.np_
+        self.sl_i = torch.empty(max(n, 1) * width, dtype=torch.int32, device="cuda")
+        self.sl_d = torch.empty(max(n, 1) * width, dtype=torch.float32, device="cuda")
+        self.passes = torch.empty(max(self.np_, 1), dtype=torch.int32, device="cuda")
+        self.stats = torch.zeros(max(self.ng, 1) * 8, dtype=torch.int32, device="cuda")
+        r2q = np.concatenate([rs.route_query, ps.route_query]).astype(np.uint32)
+        self.route_query = gs.u32(r2q)
+        off_q, order = gs.query_route_csr(r2q, nq)
+        self.q_off, self.q_routes = gs.u32(off_q), gs.u32(order)
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+
+    def step(self, Q: int, timed=False):
+        L, gs, ctx, W = self.L, self.gs, self.ctx, self.W
+        ev = self.ev
+        if timed:
+            ev[0].record()
+        ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, self.rv,
+                                                        L.ptr(self.wl.queries), self.nq,
+                                                        L.ptr(self.dev["rot"]), self.rq))
+        if timed:
+            ev[1].record()
+        if self.ng:
+            prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=True)
+            ctx.check(ctx.lib.gofann_rabitq_search(
+                ctx.handle, self.rv, self.rq, self.dg.view(),
+                self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(), prm,
+                L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
+        if timed:
+            ev[2].record()
+        if self.np_:
+            ctx.check(ctx.lib.gofann_rabitq_posting_scan(
+                ctx.handle, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
+                L.ptr(self.dp.route_query), L.ptr(self.dg.posting_ids), L.ptr(self.co),
+                L.ptr(self.cs), self.np_, W, L.ptr(self.sl_i[self.ng * W:]),
+                L.ptr(self.sl_d[self.ng * W:]), L.ptr(self.passes)))
+        if timed:
+            ev[3].record()
+        n = self.ng + self.np_
+        fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
+                                       self.sl_i, W, n, 10)
+        if timed:
+            ev[4].record()
+        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, fin_i, fin_d, 10,
+                                       self.nq, 10)
+        if timed:
+            ev[5].record()
+        return out_i
+
+    def stage_ms(self):
+        e = self.ev
+        return dict(prep=e[0].elapsed_time(e[1]), traversal=e[1].elapsed_time(e[2]),
+                    posting_scan=e[2].elapsed_time(e[3]), rerank=e[3].elapsed_time(e[4]),
+                    merge=e[4].elapsed_time(e[5]))
+
+    def route_stats(self):
+        return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
+
+
+def main_c4(args):
+    import torch
+    from gofann_amd import _lib
+    torch.cuda.init()
+    wl, li, rq = build_world_c4(args, torch)
+    t0 = time.time()
+    gt = ground_truth_c4(wl, torch, args.gt_queries_c4)
+    log(f"C4 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
+    ctx = _lib.Context(0)
+    t0 = time.time()
+    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch)
+    log(f"C4 routes: {pipe.ng} graph ({pipe.interior} interior intervals), {pipe.np_} "
+        f"label-posting scans ({pipe.post_rows_total} rows), planned in {time.time() - t0:.1f}s")
+    ladder = [args.queue] if args.queue else [int(x) for x in args.c4_ladder.split(",")]
+    chosen, rec = ladder[-1], 0.0
+    nq = wl.queries.shape[0]
+    for Q in ladder:
+        out = pipe.step(Q)
+        torch.cuda.synchronize()
+        rec = recall_at_10(out.cpu().numpy().view(np.uint32).reshape(nq, 10), gt)
+        log(f"C4 Q={Q}: recall@10={rec:.4f}")
+        chosen = Q
+        if rec >= args.target_recall:
+            break
+    for _ in range(args.warmup):
+        pipe.step(chosen)
+    torch.cuda.synchronize()
+    stages = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = pipe.step(chosen, timed=True)
+        torch.cuda.synchronize()
+        stages.append(pipe.stage_ms())
+    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    res = out.cpu().numpy().view(np.uint32).reshape(nq, 10)
+    rec = recall_at_10(res, gt)
+    rec_eq = recall_at_10(res, {q: v for q, v in gt.items() if wl.query_labels[q]})
+    rec_rg = recall_at_10(res, {q: v for q, v in gt.items() if not wl.query_labels[q]})
+    st_ms = {k: round(float(np.mean([d[k] for d in stages])), 3) for k in stages[0]}
+    st = pipe.route_stats()
+    P = rq["P"]
+    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
+    pb = pipe.post_rows_total * (4 + P // 8 + 4 + 8) + 0.0
+    rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 2 + 4) + 0.0
+    kern = {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
+            "posting_scan_kernel<RabitqScanScorer>": (st_ms["posting_scan"], pb),
+            "exact_rerank_kernel (f16)": (st_ms["rerank"], rb)}
+    per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
+               "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None}
+           for k, v in kern.items()}
+    top = max(kern, key=lambda k: kern[k][0])
+    ach = kern[top][1] / (kern[top][0] / 1000.0) / 1e9
+    log(f"C4 step {ms:.1f} ms, stages {st_ms}, recall {rec:.4f} (equality {rec_eq:.4f}, "
+        f"range {rec_rg:.4f})")
+    line = {
+        "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
+        "value": round(nq / (ms / 1000.0), 1),
+        "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8 codes / f16 rerank", "data": "synthetic",
+        "config": {"workload": "C4: 100Mx512 fp16 unit-norm 4096-centre mixture, RaBitQ 1-bit "
+                               "(64 B codes), graph R=32 per label and per 1% attribute "
+                               "interval, label Zipf(1.1) over 1000, uint32 attribute "
+                               "U[0,2^24), equality or 1-10% range, fp16->fp32 rerank of 100, "
+                               "top-10",
+                   "n": wl.n, "queries": nq, "graph_routes": pipe.ng,
+                   "interior_interval_routes": pipe.interior,
+                   "posting_routes": pipe.np_, "posting_rows": pipe.post_rows_total,
+                   "queue": chosen, "shortlist": pipe.W, "recall_at_10": round(rec, 4),
+                   "recall_equality": round(rec_eq, 4), "recall_range": round(rec_rg, 4),
+                   "gt_queries": len(gt), "stage_ms": st_ms, "kernels": per,
+                   "placement": ctx.last_placement()},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5), "traffic": None,
+                     "kernel": top, "kernel_ms": kern[top][0],
+                     "algorithmic_bytes": kern[top][1]},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
 def main():
     args = parse()
     if args.config == "c3" and args.gpus == 1:
         main_c3(args)
+        return
+    if args.config == "c4" and args.gpus == 1:
+        main_c4(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build's "

@@ -175,7 +175,10 @@ def postings_from_csr(offsets: np.ndarray, values: np.ndarray, num_labels: int):
     n = offsets.shape[0] - 1
     counts = np.diff(offsets.astype(np.int64))
     samples = np.repeat(np.arange(n, dtype=np.uint32), counts)
-    order = np.lexsort((samples, values))  # by label, then sample
+    # by label, then sample: samples are nondecreasing in CSR order, so a
+    # stable sort by label alone keeps them ascending within a label
+    # (torch's multi-threaded sort; int64 keys hold any uint32 label)
+    order = torch.sort(torch.from_numpy(values.astype(np.int64)), stable=True).indices.numpy()
     lab_sorted = values[order]
     post_ids = samples[order].astype(np.uint32)
     cat_freq = np.bincount(lab_sorted.astype(np.int64), minlength=num_labels)

@@ -237,3 +237,75 @@ def config3(n=2_700_000, nq=10_000, device="cuda", dim=4096, k=512, rank=64, spr
                   [[0] for _ in range(nq)], attr[:, None].copy(), query_ranges,
                   meta=dict(selectivity=sel, spread=spread, rank=rank, noise=noise))
     return wl
+
+
+def config4(n=100_000_000, nq=10_000, device="cuda", dim=512, k=4096, rank=64, spread=0.7,
+            noise=0.05, labels=1000, zipf_s=1.1, attr_max=1 << 24, intervals=100,
+            sel_lo=0.01, sel_hi=0.10, seed=4, chunk=1 << 17):
+    """C4: fp16 vectors from a k-centre mixture (the config3 model: centre +
+    shared rank-`rank` spread + noise, normalised), one categorical label
+    Zipf(zipf_s) over `labels` values and one uint32 attribute uniform in
+    [0, attr_max) (attr_max <= 2^24, so float32 holds it exactly).
+
+    Every row also carries an interval label: labels + floor(attr *
+    intervals / attr_max), the attribute's bucket among `intervals` equal
+    ones, so that a range query can run as one graph route per interval it
+    overlaps with the range as residual predicate (the hybrid label +
+    interval graphs of the reference's RaBitQ benchmark).  Row labels are
+    [category, labels + interval].
+
+    Even queries are categorical equality (label drawn from the same Zipf);
+    odd queries are ranges [lo, lo + w) with w = U(sel_lo, sel_hi) *
+    attr_max (mode 3).  query_labels holds [label] for equality queries and
+    [] for range queries."""
+    if attr_max > 1 << 24:
+        raise ValueError("attr_max above 2^24 is not exact in float32")
+    cfg = seed * 1000
+    gc = _gen(cfg + 1, device)
+    centres = torch.randn(k, dim, generator=gc, device=device)
+    basis = torch.randn(rank, dim, generator=gc, device=device)
+    zscale = spread / rank ** 0.5
+
+    def draw(m, g, dtype):
+        cl = torch.randint(0, k, (m,), generator=g, device=device)
+        out = torch.empty(m, dim, dtype=dtype, device=device)
+        for s in range(0, m, chunk):
+            e = min(m, s + chunk)
+            z = torch.randn(e - s, rank, generator=g, device=device) * zscale
+            x = centres[cl[s:e]] + z @ basis + noise * torch.randn(e - s, dim, generator=g,
+                                                                   device=device)
+            out[s:e] = (x / x.norm(dim=1, keepdim=True)).to(dtype)
+        return out, cl
+
+    base, cl = draw(n, _gen(cfg + 2, device), torch.float16)
+    queries, _ = draw(nq, _gen(cfg + 4, device), torch.float32)
+    rng = np.random.default_rng(cfg + 3)
+    probs = _zipf_probs(labels, zipf_s)
+    cat = rng.choice(labels, size=n, p=probs).astype(np.uint32)
+    attr = rng.integers(0, attr_max, size=n, dtype=np.int64)
+    interval = (attr * intervals // attr_max).astype(np.uint32)
+    lv = np.empty(2 * n, dtype=np.uint32)
+    lv[0::2] = cat
+    lv[1::2] = labels + interval
+    lo_off = np.arange(0, 2 * n + 1, 2, dtype=np.uint64)
+    if lo_off[-1] < 1 << 32:
+        lo_off = lo_off.astype(np.uint32)
+    qrng = np.random.default_rng(cfg + 5)
+    qcat = qrng.choice(labels, size=nq, p=probs)
+    sel = qrng.uniform(sel_lo, sel_hi, size=nq)
+    width = np.maximum(1, np.round(sel * attr_max)).astype(np.int64)
+    qlo = (qrng.random(nq) * (attr_max - width + 1)).astype(np.int64)
+    query_labels, query_ranges = [], []
+    for i in range(nq):
+        if i % 2 == 0:
+            query_labels.append([int(qcat[i])])
+            query_ranges.append([])
+        else:
+            query_labels.append([])
+            query_ranges.append([(0, 3, float(qlo[i]), float(qlo[i] + width[i]))])
+    cn = centres / centres.norm(dim=1, keepdim=True)
+    return Workload("config4", base, queries, cl, cn, lo_off, lv, labels + intervals,
+                    query_labels, attr.astype(np.float32)[:, None], query_ranges,
+                    meta=dict(selectivity=np.where(np.arange(nq) % 2 == 1, width / attr_max, 0.0),
+                              categories=labels, intervals=intervals, attr_max=attr_max,
+                              zipf_s=zipf_s, spread=spread, rank=rank, noise=noise))
