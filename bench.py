@@ -992,6 +992,10 @@ def main_c4(args):
     rec_rg = recall_at_10(res, {q: v for q, v in gt.items() if not wl.query_labels[q]})
     st_ms = {k: round(float(np.mean([d[k] for d in stages])), 3) for k in stages[0]}
     st = pipe.route_stats()
+    E = st[:, 1].astype(np.float64)
+    log(f"C4 expansions per graph route: mean {E.mean():.1f}, p50 {np.percentile(E, 50):.0f}, "
+        f"p99 {np.percentile(E, 99):.0f}, max {E.max():.0f}; scored per route "
+        f"{st[:, 3].astype(np.float64).mean():.1f}")
     P = rq["P"]
     tb = rabitq_traversal_bytes(st, li.degree, P // 8)
     pb = pipe.post_rows_total * (4 + P // 8 + 4 + 8) + 0.0

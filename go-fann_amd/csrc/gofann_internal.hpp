@@ -79,6 +79,13 @@ int rabitq_posting_scan(Context* ctx, const gofann_rabitq_view* rq,
                         const uint32_t* cand_offsets, const uint32_t* cand_sizes,
                         uint32_t routes, int shortlist_k, uint32_t* out_ids, float* out_dists,
                         uint32_t* pass_counts);
+bool rabitq_posting_scan_grouped(uint32_t padded_dim);
+int rabitq_posting_scan_group(Context* ctx, const gofann_rabitq_view* rq,
+                              const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
+                              const uint32_t* route_query, const uint32_t* cand_ids,
+                              const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                              uint32_t routes, int shortlist_k, uint32_t* out_ids,
+                              float* out_dists, uint32_t* pass_counts);
 int exact_rerank(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
                  const void* queries, const uint32_t* route_query, const uint32_t* shortlist,
                  uint32_t width, uint32_t routes, uint32_t topk, uint32_t* out_ids,

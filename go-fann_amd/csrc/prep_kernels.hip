@@ -66,51 +66,40 @@ __global__ __launch_bounds__(256) void quantize_queries_kernel(const float* rota
     }
 }
 
-// g[q][a] = sum_p (y[q][p] - c[a][p])^2, accumulated directly (fma, p
-// ascending) rather than as |y|^2 + |c|^2 - 2<y,c>: the expansion cancels
-// catastrophically when a query sits on an anchor.  A 256-thread block owns
-// a 32 x 32 (query, anchor) tile; both operand tiles stream through LDS in
-// 64-wide slices of the padded dimension.
-constexpr int kCdTile = 32;
-constexpr int kCdSlice = 64;
-
-__global__ __launch_bounds__(256) void centroid_dist_kernel(const float* y, const float* c,
-                                                            uint32_t queries, uint32_t anchors,
-                                                            uint32_t P, float* out)
+// Centroid distances as the reference computes them
+// (RabitqQueryRotation::centroid_distances, src/search/rabitq/
+// rabitq_query_rotation.cuh:88-113): row norms, an SGEMM for -2 <y, c>,
+// then g = max(0, -2 <y, c> + |y|^2 + |c|^2) (the clamp absorbs the
+// cancellation when a query sits on an anchor).
+__global__ __launch_bounds__(256) void row_norms_kernel(const float* m, uint32_t rows, uint32_t dim,
+                                                        float* norms)
 {
-    __shared__ float ys[kCdTile][kCdSlice + 1];
-    __shared__ float cs[kCdTile][kCdSlice + 1];
+    __shared__ float part[256];
+    const uint32_t r = blockIdx.x;
+    if (r >= rows) return;
     const int t = static_cast<int>(threadIdx.x);
-    const uint32_t q0 = blockIdx.y * kCdTile;
-    const uint32_t a0 = blockIdx.x * kCdTile;
-    // thread t owns pairs (qi, ai) with qi = t / 8, ai = (t % 8) * 4 + j
-    const int qi = t >> 3;
-    const int ai = (t & 7) * 4;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t p0 = 0; p0 < P; p0 += kCdSlice) {
-        for (int e = t; e < kCdTile * kCdSlice; e += 256) {
-            const int r = e / kCdSlice, k = e % kCdSlice;
-            const uint32_t pk = p0 + k;
-            ys[r][k] = (q0 + r < queries && pk < P) ? y[static_cast<size_t>(q0 + r) * P + pk] : 0.0f;
-            cs[r][k] = (a0 + r < anchors && pk < P) ? c[static_cast<size_t>(a0 + r) * P + pk] : 0.0f;
-        }
-        __syncthreads();
-        const int kmax = (P - p0) < static_cast<uint32_t>(kCdSlice) ? static_cast<int>(P - p0) : kCdSlice;
-        for (int k = 0; k < kmax; ++k) {
-            const float yv = ys[qi][k];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float d = yv - cs[ai + j][k];
-                acc[j] = fmaf(d, d, acc[j]);
-            }
-        }
+    float sum = 0.0f;
+    for (uint32_t d = t; d < dim; d += 256) {
+        const float v = m[static_cast<size_t>(r) * dim + d];
+        sum = fmaf(v, v, sum);
+    }
+    part[t] = sum;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if (t < stride) part[t] += part[t + stride];
         __syncthreads();
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t qq = q0 + qi, aa = a0 + ai + j;
-        if (qq < queries && aa < anchors) out[static_cast<size_t>(qq) * anchors + aa] = acc[j];
-    }
+    if (t == 0) norms[r] = part[0];
+}
+
+__global__ __launch_bounds__(256) void finish_centroid_dist_kernel(float* g, const float* qn,
+                                                                   const float* an,
+                                                                   uint32_t queries,
+                                                                   uint32_t anchors)
+{
+    const size_t pair = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (pair >= static_cast<size_t>(queries) * anchors) return;
+    g[pair] = fmaxf(0.0f, g[pair] + qn[pair / anchors] + an[pair % anchors]);
 }
 
 // The context's rocBLAS handle, created on first use and bound to the
@@ -155,12 +144,30 @@ int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* quer
         return ctx->fail(GOFANN_ERR_HIP, "rocblas_sgemm (query rotation)");
     hipLaunchKernelGGL(quantize_queries_kernel, dim3(count), dim3(256), 0, ctx->stream, out->rotated,
                        P, count, out->q8, out->scale, out->k1);
-    if (A > 0 && rq->anchors) {
-        const dim3 grid((A + kCdTile - 1) / kCdTile, (count + kCdTile - 1) / kCdTile);
-        hipLaunchKernelGGL(centroid_dist_kernel, grid, dim3(256), 0, ctx->stream, out->rotated,
-                           rq->anchors, count, A, P, out->centroid_dists);
-    }
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("RaBitQ preparation launch");
+    if (A > 0 && rq->anchors) {
+        float* norms = static_cast<float*>(
+            ctx->scratch(Context::kScratchMisc, (static_cast<size_t>(count) + A) * sizeof(float)));
+        if (!norms) return ctx->fail(GOFANN_ERR_NOMEM, "centroid norm scratch allocation failed");
+        float* qn = norms;
+        float* an = norms + count;
+        hipLaunchKernelGGL(row_norms_kernel, dim3(count), dim3(256), 0, ctx->stream, out->rotated,
+                           count, P, qn);
+        hipLaunchKernelGGL(row_norms_kernel, dim3(A), dim3(256), 0, ctx->stream, rq->anchors, A, P,
+                           an);
+        // column-major g[A][N] = -2 anchors^T[A][P] rotated[P][N]
+        const float minus2 = -2.0f;
+        if (rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none,
+                          static_cast<int>(A), static_cast<int>(count), static_cast<int>(P),
+                          &minus2, rq->anchors, static_cast<int>(P), out->rotated,
+                          static_cast<int>(P), &zero, out->centroid_dists,
+                          static_cast<int>(A)) != rocblas_status_success)
+            return ctx->fail(GOFANN_ERR_HIP, "rocblas_sgemm (centroid distances)");
+        const size_t pairs = static_cast<size_t>(count) * A;
+        hipLaunchKernelGGL(finish_centroid_dist_kernel, dim3(static_cast<uint32_t>((pairs + 255) / 256)),
+                           dim3(256), 0, ctx->stream, out->centroid_dists, qn, an, count, A);
+        if (hipGetLastError() != hipSuccess) return ctx->fail_hip("centroid distance launch");
+    }
     return GOFANN_OK;
 }
 

@@ -71,6 +71,14 @@ struct RangeScanArgs {
     uint32_t* out_ids;
     float* out_dists;
     uint32_t* pass_counts;
+    // Label-posting mode (group-per-row kernel only): segment s is slice
+    // s % slices of route s / slices over cand_ids[cand_offsets[route] ..
+    // + cand_sizes[route]); the rows are filtered by the route predicate
+    // alone and counted when it is enabled.
+    int label_mode;
+    const uint32_t* cand_offsets;
+    const uint32_t* cand_sizes;
+    uint32_t slices;
 };
 
 __device__ __forceinline__ bool pair_le(float ad, uint32_t aid, float bd, uint32_t bid)
@@ -352,7 +360,8 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     uint32_t* s_id = reinterpret_cast<uint32_t*>(s_d + a.slots);
     float* s_f1 = reinterpret_cast<float*>(s_id + a.slots);
 
-    const uint32_t route = a.seg_route[seg];
+    const bool label_mode = a.label_mode != 0;
+    const uint32_t route = label_mode ? seg / a.slices : a.seg_route[seg];
     const uint32_t query = a.routes.route_query[route];
     sc.setup(query, tid, lds);
     for (int i = tid; i < a.slots; i += kScanThreads) {
@@ -382,17 +391,28 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     const uint4* codes = reinterpret_cast<const uint4*>(sc.codes);
     const size_t row_vecs = static_cast<size_t>(G) * W;
 
-    // :5895-5902
-    const uint64_t begin = a.seg_offset[seg];
-    uint64_t count = a.seg_size[seg];
-    if (begin > a.resident_rows)
-        count = 0;
-    else if (count > a.resident_rows - begin)
-        count = a.resident_rows - begin;
-    const uint32_t active = count_active_ranges(a.routes.range_modes, route, a.routes.range_count);
-    if (active == 0) count = 0;  // :5917
+    uint64_t begin, count;
+    uint32_t active = 0;
+    if (label_mode) {
+        // near-equal slices of the route's posting
+        const uint64_t size = a.cand_sizes[route];
+        const uint64_t part = (size + a.slices - 1) / a.slices;
+        const uint64_t lo = std::min<uint64_t>(size, (seg % a.slices) * part);
+        begin = static_cast<uint64_t>(a.cand_offsets[route]) + lo;
+        count = std::min<uint64_t>(size, lo + part) - lo;
+    } else {
+        // :5895-5902
+        begin = a.seg_offset[seg];
+        count = a.seg_size[seg];
+        if (begin > a.resident_rows)
+            count = 0;
+        else if (count > a.resident_rows - begin)
+            count = a.resident_rows - begin;
+        active = count_active_ranges(a.routes.range_modes, route, a.routes.range_count);
+        if (active == 0) count = 0;  // :5917
+    }
     const bool enabled = pred_enabled(a.pred, route);
-    const bool score_first = a.score_first != 0 && enabled;
+    const bool score_first = !label_mode && a.score_first != 0 && enabled;
     const int k = a.k, kp = a.k_pow2;
     const int chunk = a.chunk;
     const int per = chunk / kScanThreads;
@@ -415,7 +435,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
             bool ok = false;
             if (j < count) {
                 s = a.posting[begin + j];
-                ok = s < a.base_rows;
+                ok = s < a.base_rows;  // UINT32_MAX never is
                 if (ok) {
                     if (enabled) {
                         PredCounters c{0, 0};
@@ -427,7 +447,9 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
             }
             float add0 = FLT_MAX, f1 = 0.0f;
             if (ok) {
-                if (!score_first) ++passes;
+                // filter-first counts every passing row; a label posting
+                // (backend_rabitq.cu:5494-5682) only predicate-checked ones
+                if (label_mode ? enabled : !score_first) ++passes;
                 const uint32_t anchor = sc.anchor_ids[s];
                 add0 = sc.factors[static_cast<size_t>(s) * 3] + sc.g_row[anchor];
                 f1 = sc.factors[static_cast<size_t>(s) * 3 + 1];
@@ -569,7 +591,8 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
 }
 
 struct SegmentMergeArgs {
-    const uint32_t* query_indptr;
+    const uint32_t* query_indptr;  // null: position p takes [p * stride, (p + 1) * stride)
+    uint32_t stride;
     uint32_t positions;
     const uint32_t* seg_ids;
     const float* seg_dists;
@@ -596,7 +619,8 @@ __global__ __launch_bounds__(kScanThreads) void segment_merge_kernel(SegmentMerg
     }
     __syncthreads();
     uint32_t passes = 0;
-    const uint32_t first = a.query_indptr[p], last = a.query_indptr[p + 1];
+    const uint32_t first = a.query_indptr ? a.query_indptr[p] : p * a.stride;
+    const uint32_t last = a.query_indptr ? a.query_indptr[p + 1] : (p + 1) * a.stride;
     for (uint32_t part = first; part < last; ++part) {
         passes += a.seg_pass[part];
         const size_t o = static_cast<size_t>(part) * k;
@@ -628,7 +652,149 @@ int pow2_at_least(int x)
     while (p < x) p <<= 1;
     return p;
 }
+
+// The group-per-row kernel for a padded dimension: the row's 16-byte
+// vectors split evenly over a power-of-two group of <= 32 lanes, two vectors
+// per lane at most; null otherwise (the thread-per-row kernels remain).
+const void* group_scan_kernel(uint32_t padded_dim)
+{
+    if (padded_dim == 0 || padded_dim % 128 != 0) return nullptr;
+    switch (padded_dim / 128) {
+        case 1: return reinterpret_cast<const void*>(range_scan_group_kernel<1, 1>);
+        case 2: return reinterpret_cast<const void*>(range_scan_group_kernel<2, 1>);
+        case 4: return reinterpret_cast<const void*>(range_scan_group_kernel<4, 1>);
+        case 8: return reinterpret_cast<const void*>(range_scan_group_kernel<8, 1>);
+        case 16: return reinterpret_cast<const void*>(range_scan_group_kernel<16, 1>);
+        case 32: return reinterpret_cast<const void*>(range_scan_group_kernel<32, 1>);
+        case 64: return reinterpret_cast<const void*>(range_scan_group_kernel<32, 2>);
+        default: return nullptr;
+    }
+}
+
+RabitqScanScorer scan_scorer(const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre)
+{
+    RabitqScanScorer sc;
+    sc.codes = rq->codes;
+    sc.factors = rq->factors;
+    sc.anchor_ids = rq->anchor_ids;
+    sc.q8 = pre->q8;
+    sc.q_scale = pre->scale;
+    sc.q_k1 = pre->k1;
+    sc.centroid_dists = pre->centroid_dists;
+    sc.num_anchors = rq->num_anchors;
+    sc.padded_dim = rq->padded_dim;
+    sc.planes = nullptr;
+    sc.scale = sc.k1 = 0.0f;
+    sc.g_row = nullptr;
+    return sc;
+}
+
+// Workgroups a label-posting launch aims for: enough to fill every CU
+// several times over.
+constexpr uint32_t kPostingTargetGroups = 4096;
+constexpr uint32_t kPostingMaxSlices = 32;
 }  // namespace
+
+bool rabitq_posting_scan_grouped(uint32_t padded_dim)
+{
+    return group_scan_kernel(padded_dim) != nullptr;
+}
+
+// Label-posting scan (lowfreq_rabitq_resident_posting_kernel,
+// backend_rabitq.cu:5494-5682) on the group-per-row kernel.  A route's
+// posting is cut into `slices` near-equal parts so that few long routes
+// still fill the chip; the parts' shortlists are merged per route (their
+// union's k least pairs are the route's, pass counts add up).
+int rabitq_posting_scan_group(Context* ctx, const gofann_rabitq_view* rq,
+                              const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
+                              const uint32_t* route_query, const uint32_t* cand_ids,
+                              const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                              uint32_t routes, int shortlist_k, uint32_t* out_ids,
+                              float* out_dists, uint32_t* pass_counts)
+{
+    const void* kern = group_scan_kernel(rq->padded_dim);
+    if (!kern) return ctx->fail(GOFANN_ERR_UNSUPPORTED, "padded_dim has no grouped posting scan");
+    if (!pre->q8 || !pre->scale || !pre->k1 || !pre->centroid_dists || !rq->factors ||
+        !rq->anchor_ids)
+        return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view or prepared queries incomplete");
+    if (!route_query || !cand_ids || !cand_offsets || !cand_sizes || !out_ids || !out_dists)
+        return ctx->fail(GOFANN_ERR_INVALID, "posting scan arrays missing");
+    uint32_t slices = (kPostingTargetGroups + routes - 1) / routes;
+    slices = std::max(1u, std::min(slices, kPostingMaxSlices));
+    const uint64_t segments = static_cast<uint64_t>(routes) * slices;
+    if (segments > 0x7fffffffull)
+        return ctx->fail(GOFANN_ERR_INVALID, "too many posting routes");
+
+    uint32_t* scan_ids = out_ids;
+    float* scan_dists = out_dists;
+    uint32_t* scan_pass = pass_counts;
+    if (slices > 1) {
+        const size_t slots_out = static_cast<size_t>(segments) * static_cast<size_t>(shortlist_k);
+        const size_t bytes = slots_out * 8 + static_cast<size_t>(segments) * 4 + 64;
+        unsigned char* buf =
+            static_cast<unsigned char*>(ctx->scratch(Context::kScratchRange, bytes));
+        if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "posting slice scratch allocation failed");
+        scan_ids = reinterpret_cast<uint32_t*>(buf);
+        scan_dists = reinterpret_cast<float*>(buf + slots_out * 4);
+        scan_pass = reinterpret_cast<uint32_t*>(buf + slots_out * 8);
+    }
+
+    RangeScanArgs a{};
+    a.pred = pred ? *pred : gofann_predicate_view{};
+    a.routes.route_query = route_query;
+    a.posting = cand_ids;
+    a.resident_rows = UINT64_MAX;
+    a.segments = static_cast<uint32_t>(segments);
+    a.base_rows = rq->samples ? rq->samples : UINT32_MAX;
+    a.k = shortlist_k;
+    a.k_pow2 = pow2_at_least(shortlist_k);
+    a.chunk = a.k_pow2 <= 1024 ? 1024 : 2048;
+    a.slots = std::max(2 * a.k_pow2, a.k_pow2 + a.chunk);
+    a.planes_bytes = rq->padded_dim;
+    a.score_first = 0;
+    a.out_ids = scan_ids;
+    a.out_dists = scan_dists;
+    a.pass_counts = slices > 1 || pass_counts ? scan_pass : nullptr;
+    a.label_mode = 1;
+    a.cand_offsets = cand_offsets;
+    a.cand_sizes = cand_sizes;
+    a.slices = slices;
+    const size_t lds =
+        a.planes_bytes + static_cast<size_t>(a.slots) * 8 + static_cast<size_t>(a.chunk) * 4;
+    if (lds > static_cast<size_t>(ctx->lds_per_block))
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "posting scan LDS exceeds the workgroup limit");
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute posting scan");
+    RabitqScanScorer sc = scan_scorer(rq, pre);
+    void* kargs[] = {&a, &sc};
+    if (hipLaunchKernel(kern, dim3(a.segments), dim3(kScanThreads), kargs, lds, ctx->stream) !=
+        hipSuccess)
+        return ctx->fail_hip("posting scan launch");
+    if (slices == 1) return GOFANN_OK;
+
+    SegmentMergeArgs m;
+    m.query_indptr = nullptr;
+    m.stride = slices;
+    m.positions = routes;
+    m.seg_ids = scan_ids;
+    m.seg_dists = scan_dists;
+    m.seg_pass = scan_pass;
+    m.k = shortlist_k;
+    m.k_pow2 = a.k_pow2;
+    m.out_ids = out_ids;
+    m.out_dists = out_dists;
+    m.out_pass = pass_counts;
+    const size_t mlds = static_cast<size_t>(2 * a.k_pow2) * 8;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(segment_merge_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mlds)) !=
+        hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute posting merge");
+    hipLaunchKernelGGL(segment_merge_kernel, dim3(routes), dim3(kScanThreads), mlds, ctx->stream,
+                       m);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("posting merge launch");
+    return GOFANN_OK;
+}
 
 int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
                       const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
@@ -692,39 +858,20 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
     a.out_ids = scan_ids;
     a.out_dists = scan_dists;
     a.pass_counts = scan_pass;
+    a.label_mode = 0;
+    a.cand_offsets = nullptr;
+    a.cand_sizes = nullptr;
+    a.slices = 1;
     if (a.chunk % kScanThreads != 0 || a.chunk / kScanThreads > 8 || a.slots < 2 * a.k_pow2 ||
         a.slots < a.k_pow2 + a.chunk)
         return ctx->fail(GOFANN_ERR_INVALID, "range scan chunk layout invalid");
 
-    RabitqScanScorer sc;
-    sc.codes = rq->codes;
-    sc.factors = rq->factors;
-    sc.anchor_ids = rq->anchor_ids;
-    sc.q8 = pre->q8;
-    sc.q_scale = pre->scale;
-    sc.q_k1 = pre->k1;
-    sc.centroid_dists = pre->centroid_dists;
-    sc.num_anchors = rq->num_anchors;
-    sc.padded_dim = rq->padded_dim;
-    sc.planes = nullptr;
-    sc.scale = sc.k1 = 0.0f;
-    sc.g_row = nullptr;
+    RabitqScanScorer sc = scan_scorer(rq, pre);
 
     // Group-per-row kernel when the row's 16-byte vectors split evenly over
     // a power-of-two group of <= 32 lanes, two vectors per lane at most;
     // thread-per-row kernel otherwise.
-    const uint32_t nvec = rq->padded_dim / 128;
-    const void* kern = nullptr;
-    switch (nvec) {
-        case 1: kern = reinterpret_cast<const void*>(range_scan_group_kernel<1, 1>); break;
-        case 2: kern = reinterpret_cast<const void*>(range_scan_group_kernel<2, 1>); break;
-        case 4: kern = reinterpret_cast<const void*>(range_scan_group_kernel<4, 1>); break;
-        case 8: kern = reinterpret_cast<const void*>(range_scan_group_kernel<8, 1>); break;
-        case 16: kern = reinterpret_cast<const void*>(range_scan_group_kernel<16, 1>); break;
-        case 32: kern = reinterpret_cast<const void*>(range_scan_group_kernel<32, 1>); break;
-        case 64: kern = reinterpret_cast<const void*>(range_scan_group_kernel<32, 2>); break;
-        default: break;
-    }
+    const void* kern = group_scan_kernel(rq->padded_dim);
     size_t lds;
     if (kern) {
         // [0, kp) running list, [kp, kp + chunk) the chunk; the merges use
@@ -748,6 +895,7 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
 
     SegmentMergeArgs m;
     m.query_indptr = seg->query_indptr;
+    m.stride = 0;
     m.positions = seg->positions;
     m.seg_ids = scan_ids;
     m.seg_dists = scan_dists;

@@ -367,6 +367,12 @@ int rabitq_posting_scan(Context* ctx, const gofann_rabitq_view* rq,
     if (shortlist_k < 1 || shortlist_k > kMaxShortlist)
         return ctx->fail(GOFANN_ERR_INVALID, "shortlist_k must be in [1, 512]");
     if (routes == 0) return GOFANN_OK;
+    // Code rows that split over a lane group take the group-per-row scan
+    // (range_scan.hip); the thread-per-row kernel below takes the rest.
+    if (rabitq_posting_scan_grouped(rq->padded_dim))
+        return rabitq_posting_scan_group(ctx, rq, pre, pred, route_query, cand_ids, cand_offsets,
+                                         cand_sizes, routes, shortlist_k, out_ids, out_dists,
+                                         pass_counts);
     ScanArgs a;
     a.pred = pred ? *pred : gofann_predicate_view{};
     a.route_query = route_query;

@@ -161,16 +161,24 @@ def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp):
     assert np.array_equal(st.cpu().numpy().reshape(n, 8), ost)
 
 
-def test_rabitq_posting_scan_matches_oracle(gpu_ctx, rworld):
-    wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
-    say("rabitq posting scan")
-    dev, rv = _rviews(rworld)
+# Padded dims 128 / 512 / 1024 take the group-per-row scan (groups of 1, 4
+# and 8 lanes), 384 the thread-per-row kernel.  Forty routes are cut into
+# slices and merged; reps=110 (4400 routes) runs one workgroup per route.
+@pytest.mark.parametrize("P,reps,k", [(128, 1, 100), (384, 1, 100), (512, 1, 100), (1024, 1, 100),
+                                      (512, 1, 10), (512, 1, 512), (512, 110, 100),
+                                      (384, 110, 100)])
+def test_rabitq_posting_scan_matches_oracle(gpu_ctx, rworld, P, reps, k):
+    wl, li, pl, rot, codes, fac, aid, anchors, _ = rworld
+    say("rabitq posting scan P", P, "reps", reps, "k", k)
+    rot = gi.random_rotation(wl.dim, P, 31005 + P, "cpu")
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
+    dev, rv = _rviews((wl, li, pl, rot, codes, fac, aid, anchors, P))
     out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
     rows = [(qi, ls[0], [l for l in ls if l != ls[0]], []) for qi, ls in enumerate(wl.query_labels)]
+    rows = rows * reps
     rs = gp._routeset(rows, li)
     off = np.array([li.posting_offset[r[1]] for r in rows], np.uint32)
     size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]] for r in rows], np.uint32)
-    k = 100
     pred = po.PredicateArrays.from_plan(rs.predicate, li)
     L = po.lib()
     n = rs.count
@@ -200,3 +208,4 @@ def test_rabitq_posting_scan_matches_oracle(gpu_ctx, rworld):
     assert np.array_equal(as_u32(ids).reshape(n, k), oi)
     assert np.array_equal(dists.cpu().numpy().reshape(n, k).view(np.uint32), od.view(np.uint32))
     assert np.array_equal(as_u32(passes), opass)
+    assert (oi[:, 0] != U32MAX).sum() > n // 2 and opass.max() > 0
