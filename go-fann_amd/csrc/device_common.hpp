@@ -16,6 +16,23 @@
 
 namespace gofann {
 
+// popcount(x) + acc as one v_bcnt_u32_b32.  Written out because the
+// compiler otherwise counts each word on its own (bcnt x, 0) and sums the
+// counts with extra adds -- a third more VALU work in the RaBitQ inner loops.
+__device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc)
+{
+    uint32_t r;
+    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
+    return r;
+}
+
+// 16-byte code vectors a per-lane RaBitQ scorer loads before using any.
+#ifndef GOFANN_CODE_BATCH
+#define GOFANN_CODE_BATCH 8
+#endif
+constexpr int kCodeBatch = GOFANN_CODE_BATCH;
+
+
 constexpr uint32_t kHashCapacity = 4096;  // backend_pq.cu:194
 constexpr int kMaxDegree = 64;            // include/config1B.h:29 FIXED_DEGREE
 constexpr uint32_t kPoolUsed = 0x80000000u;  // backend_pq.cu:713

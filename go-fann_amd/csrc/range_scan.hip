@@ -299,13 +299,16 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_kernel(RangeScanArgs 
 // Group-per-row scan.  A group of G lanes (G a power of two, <= 32) scores
 // one code row: lane l of the group owns the 16-byte code vectors l, l + G,
 // .. of the row (W of them, padded_dim / 128 = G * W), so one wave load
-// reads 64 / G whole rows, and keeps the query bit planes of its words in
-// registers.  The group's partial inner products are summed by a DPP
-// butterfly.  Each chunk is first passed over one row per thread: the
+// reads 64 / G whole rows; the query bit planes are read from LDS.  The
+// group's partial inner products are summed by a DPP butterfly.  Each
+// chunk is first passed over one row per thread: the
 // posting id, the filter, and the row's distance terms that need no code
 // bits (f_add + g, f_rescale) are gathered into LDS; filter-first packs the
 // passing rows (the shortlist does not depend on scan order), score-first
-// keeps scan positions for its pass counts.
+// keeps scan positions for its pass counts.  The group pass leaves only
+// the integer inner product in LDS; a third pass, one row per thread again,
+// forms the distance and drops rows that cannot beat the running k-th pair
+// (lane-0 work inside the group pass would cost whole-wave issue per row).
 // ---------------------------------------------------------------------------
 
 // Sum of x over the G-lane group holding this lane (G a power of two <= 32),
@@ -321,28 +324,40 @@ __device__ __forceinline__ int group_sum(int x)
     return x;
 }
 
+// Rows in flight per group in the score pass (a build-time tuning knob).
+#ifndef GOFANN_SCAN_ROW_UNROLL
+#define GOFANN_SCAN_ROW_UNROLL 8
+#endif
+constexpr int kRowUnroll = GOFANN_SCAN_ROW_UNROLL;
+
 // This lane's share of sum_d q8[d] * bit[d] over its W code vectors:
 // sum_j 2^j popc(plane_j & code) for the seven low planes, minus 128 times
-// the sign plane's count.
-template <int W>
-__device__ __forceinline__ int lane_ip(const uint4 (&c)[W], const uint32_t (&pl)[W * 32])
+// the sign plane's count.  The planes sit in LDS plane-major,
+// planes_t[j][word], so the lane's four words of plane j are one 16-byte
+// read and a group's lanes read consecutive 16-byte blocks (no bank
+// conflicts); registers stay free for rows in flight.
+template <int G, int W>
+__device__ __forceinline__ int lane_ip_lds(const uint4 (&c)[W], const uint4* planes_t,
+                                           uint32_t vecs, int lg)
 {
     uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-        const uint32_t cw[4] = {c[w].x, c[w].y, c[w].z, c[w].w};
+        const uint32_t v = static_cast<uint32_t>(lg + G * w);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) cnt[j] += __popc(pl[w * 32 + t * 8 + j] & cw[t]);
+        for (int j = 0; j < 8; ++j) {
+            const uint4 p = planes_t[j * vecs + v];
+            cnt[j] = bcnt_acc(p.x & c[w].x, cnt[j]);
+            cnt[j] = bcnt_acc(p.y & c[w].y, cnt[j]);
+            cnt[j] = bcnt_acc(p.z & c[w].z, cnt[j]);
+            cnt[j] = bcnt_acc(p.w & c[w].w, cnt[j]);
+        }
     }
     int ip = 0;
 #pragma unroll
     for (int j = 0; j < 7; ++j) ip += static_cast<int>(cnt[j]) << j;
     return ip - 128 * static_cast<int>(cnt[7]);
 }
-
-constexpr int kRowUnroll = 2;  // rows in flight per group
 
 template <int G, int W>
 __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeScanArgs a,
@@ -359,6 +374,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     float* s_d = reinterpret_cast<float*>(lds + a.planes_bytes);
     uint32_t* s_id = reinterpret_cast<uint32_t*>(s_d + a.slots);
     float* s_f1 = reinterpret_cast<float*>(s_id + a.slots);
+    int* s_ip = reinterpret_cast<int*>(s_f1 + a.chunk);
 
     const bool label_mode = a.label_mode != 0;
     const uint32_t route = label_mode ? seg / a.slices : a.seg_route[seg];
@@ -377,17 +393,14 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     constexpr int kGroups = kScanThreads / G;
     const int lg = tid & (G - 1);
     const int grp = tid / G;
-    uint32_t pl[W * 32];
-#pragma unroll
-    for (int w = 0; w < W; ++w)
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint4 v = reinterpret_cast<const uint4*>(sc.planes)[(lg + G * w) * 8 + t];
-            pl[w * 32 + t * 4 + 0] = v.x;
-            pl[w * 32 + t * 4 + 1] = v.y;
-            pl[w * 32 + t * 4 + 2] = v.z;
-            pl[w * 32 + t * 4 + 3] = v.w;
-        }
+    // plane-major copy of the word-major planes sc.setup wrote
+    const uint32_t words = sc.padded_dim / 32;
+    uint32_t* planes_t = reinterpret_cast<uint32_t*>(s_ip + a.chunk);
+    for (uint32_t e = tid; e < words * 8; e += kScanThreads)
+        planes_t[(e & 7) * words + (e >> 3)] = sc.planes[e];
+    __syncthreads();
+    const uint4* planes_t4 = reinterpret_cast<const uint4*>(planes_t);
+    const uint32_t vecs = words / 4;
     const uint4* codes = reinterpret_cast<const uint4*>(sc.codes);
     const size_t row_vecs = static_cast<size_t>(G) * W;
 
@@ -485,8 +498,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
             s_d[kp + i] = FLT_MAX;
             s_id[kp + i] = UINT32_MAX;
         }
-        // Pass 2, a group per row: code bits, distance, survivor test.
-        uint32_t surv = 0;
+        // Pass 2, a group per row: the code bits' integer inner product.
         for (int i0 = grp; i0 < n_rows; i0 += kGroups * kRowUnroll) {
             uint32_t sid[kRowUnroll];
             uint4 c[kRowUnroll][W];
@@ -503,18 +515,23 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
 #pragma unroll
             for (int u = 0; u < kRowUnroll; ++u) {
                 if (sid[u] == UINT32_MAX) continue;  // uniform over the group
-                const int ip = group_sum<G>(lane_ip<W>(c[u], pl));
-                if (lg == 0) {
-                    const int i = i0 + u * kGroups;
-                    const float short_ip = static_cast<float>(ip) * sc.scale;
-                    const float tt = short_ip + sc.k1;
-                    const float v = fmaf(s_f1[i], tt, s_d[kp + i]);
-                    const bool in = admissible(v, sid[u]) && pair_less(v, sid[u], kth_d, kth_id);
-                    s_d[kp + i] = in ? v : FLT_MAX;
-                    s_id[kp + i] = in ? sid[u] : UINT32_MAX;
-                    surv += in ? 1u : 0u;
-                }
+                const int ip = group_sum<G>(lane_ip_lds<G, W>(c[u], planes_t4, vecs, lg));
+                if (lg == 0) s_ip[i0 + u * kGroups] = ip;
             }
+        }
+        __syncthreads();
+        // Pass 3, one row per thread: distance and survivor test.
+        uint32_t surv = 0;
+        for (int i = tid; i < n_rows; i += kScanThreads) {
+            const uint32_t sid = s_id[kp + i];
+            if (sid == UINT32_MAX) continue;
+            const float short_ip = static_cast<float>(s_ip[i]) * sc.scale;
+            const float tt = short_ip + sc.k1;
+            const float v = fmaf(s_f1[i], tt, s_d[kp + i]);
+            const bool in = admissible(v, sid) && pair_less(v, sid, kth_d, kth_id);
+            s_d[kp + i] = in ? v : FLT_MAX;
+            s_id[kp + i] = in ? sid : UINT32_MAX;
+            surv += in ? 1u : 0u;
         }
         if (surv) atomicAdd(&s_surv, surv);
         __syncthreads();
@@ -759,8 +776,8 @@ int rabitq_posting_scan_group(Context* ctx, const gofann_rabitq_view* rq,
     a.cand_offsets = cand_offsets;
     a.cand_sizes = cand_sizes;
     a.slices = slices;
-    const size_t lds =
-        a.planes_bytes + static_cast<size_t>(a.slots) * 8 + static_cast<size_t>(a.chunk) * 4;
+    const size_t lds = 2 * static_cast<size_t>(a.planes_bytes) + static_cast<size_t>(a.slots) * 8 +
+                       static_cast<size_t>(a.chunk) * 8;
     if (lds > static_cast<size_t>(ctx->lds_per_block))
         return ctx->fail(GOFANN_ERR_UNSUPPORTED, "posting scan LDS exceeds the workgroup limit");
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -875,9 +892,10 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
     size_t lds;
     if (kern) {
         // [0, kp) running list, [kp, kp + chunk) the chunk; the merges use
-        // [0, 2 kp); then chunk floats of f_rescale.
+        // [0, 2 kp); then per chunk row f_rescale and the inner product.
         a.slots = std::max(2 * a.k_pow2, a.k_pow2 + a.chunk);
-        lds = a.planes_bytes + static_cast<size_t>(a.slots) * 8 + static_cast<size_t>(a.chunk) * 4;
+        lds = 2 * static_cast<size_t>(a.planes_bytes) + static_cast<size_t>(a.slots) * 8 +
+              static_cast<size_t>(a.chunk) * 8;
     } else {
         kern = reinterpret_cast<const void*>(range_scan_kernel);
         lds = a.planes_bytes + static_cast<size_t>(a.slots) * 8;

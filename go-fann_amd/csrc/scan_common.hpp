@@ -145,21 +145,33 @@ struct RabitqScanScorer {
         const uint4* row =
             reinterpret_cast<const uint4*>(codes + static_cast<size_t>(sample) * (padded_dim / 8));
         uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (uint32_t w4 = 0; w4 < words / 4; ++w4) {
-            const uint4 c = row[w4];
-            const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+        // Code loads go out kCodeBatch at a time before any is consumed, so
+        // a row costs ceil(vectors / kCodeBatch) memory round trips, not one
+        // per 16 bytes.
+        const uint32_t vecs = words / 4;
+        for (uint32_t v0 = 0; v0 < vecs; v0 += kCodeBatch) {
+            uint4 cb[kCodeBatch];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint4 p0 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2];
-                const uint4 p1 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2 + 1];
-                cnt[0] += __popc(p0.x & cw[t]);
-                cnt[1] += __popc(p0.y & cw[t]);
-                cnt[2] += __popc(p0.z & cw[t]);
-                cnt[3] += __popc(p0.w & cw[t]);
-                cnt[4] += __popc(p1.x & cw[t]);
-                cnt[5] += __popc(p1.y & cw[t]);
-                cnt[6] += __popc(p1.z & cw[t]);
-                cnt[7] += __popc(p1.w & cw[t]);
+            for (int b = 0; b < kCodeBatch; ++b)
+                cb[b] = v0 + b < vecs ? row[v0 + b] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < kCodeBatch; ++b) {
+                if (v0 + b >= vecs) break;
+                const uint32_t w4 = v0 + b;
+                const uint32_t cw[4] = {cb[b].x, cb[b].y, cb[b].z, cb[b].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint4 p0 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2];
+                    const uint4 p1 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2 + 1];
+                    cnt[0] = bcnt_acc(p0.x & cw[t], cnt[0]);
+                    cnt[1] = bcnt_acc(p0.y & cw[t], cnt[1]);
+                    cnt[2] = bcnt_acc(p0.z & cw[t], cnt[2]);
+                    cnt[3] = bcnt_acc(p0.w & cw[t], cnt[3]);
+                    cnt[4] = bcnt_acc(p1.x & cw[t], cnt[4]);
+                    cnt[5] = bcnt_acc(p1.y & cw[t], cnt[5]);
+                    cnt[6] = bcnt_acc(p1.z & cw[t], cnt[6]);
+                    cnt[7] = bcnt_acc(p1.w & cw[t], cnt[7]);
+                }
             }
         }
         int32_t ip = 0;
