@@ -32,6 +32,20 @@ __device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc)
 #endif
 constexpr int kCodeBatch = GOFANN_CODE_BATCH;
 
+// Sum of x over the G-lane group holding this lane (G a power of two <= 32),
+// delivered to every lane of the group; every lane of the group is active.
+template <int G>
+__device__ __forceinline__ int group_sum(int x)
+{
+    if constexpr (G >= 2) x += __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);   // lane ^ 1
+    if constexpr (G >= 4) x += __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);   // lane ^ 2
+    if constexpr (G >= 8) x += __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);  // 7 - lane in 8
+    if constexpr (G >= 16) x += __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false); // 15 - lane in 16
+    if constexpr (G >= 32) x += __shfl_xor(x, 16, 64);
+    return x;
+}
+
+
 
 constexpr uint32_t kHashCapacity = 4096;  // backend_pq.cu:194
 constexpr int kMaxDegree = 64;            // include/config1B.h:29 FIXED_DEGREE

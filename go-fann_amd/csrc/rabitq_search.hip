@@ -18,8 +18,9 @@ __global__ __launch_bounds__(64) void rabitq_score_kernel(RabitqScorer sc, const
         sc.setup(qj, lane, lds);
         __syncthreads();
         const bool mine = i < n && q_idx[i] == qj;
+        const float v = sc.score(mine ? s_idx[i] : 0u, mine);  // every lane calls score
         if (mine) {
-            out[i] = sc.score(s_idx[i], true);
+            out[i] = v;
             if (ip_out) ip_out[i] = sc.ip_int(s_idx[i]);
         }
     }
@@ -71,7 +72,8 @@ int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabit
     if (p->inline_exact_rerank)
         return ctx->fail(GOFANN_ERR_UNSUPPORTED, "RaBitQ traversal has no inline exact rerank");
     if (r->count == 0) return GOFANN_OK;
-    const uint32_t plane_bytes = rq->padded_dim;  // 8 planes x padded_dim bits
+    // 8 planes x padded_dim bits, then the whole-wave scorer's candidates
+    const uint32_t plane_bytes = rq->padded_dim + kRabitqCoopBytes;
     const Layout l = make_layout(plane_bytes, p->queue_limit, p->result_width);
     const Placement pl = choose_visited<RabitqScorer>(ctx, l, p->hash_mode);
     ctx->last_table_in_lds = 1;
@@ -87,7 +89,7 @@ int rabitq_score(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq
     if (rc) return rc;
     if (n == 0) return GOFANN_OK;
     const dim3 grid((n + kWave - 1) / kWave), block(kWave);
-    hipLaunchKernelGGL(rabitq_score_kernel, grid, block, rq->padded_dim, ctx->stream,
+    hipLaunchKernelGGL(rabitq_score_kernel, grid, block, rq->padded_dim + kRabitqCoopBytes, ctx->stream,
                        make_rabitq_scorer(rq, pre), q_idx, s_idx, n, out, ip_int);
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("rabitq_score launch");
     return GOFANN_OK;

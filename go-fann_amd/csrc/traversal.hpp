@@ -289,9 +289,17 @@ struct PqScorer {
 // 3100-3200, int8 query path).  ip_int = sum_d q8[d] * bit[d] is computed as
 // sum_j w_j * popcount(plane_j & code) over the query's two's-complement bit
 // planes (w_j = 2^j, w_7 = -128), which equals the reference's dp4a dot over
-// nibble masks exactly.  Planes are stored MSB-first like the codes: word w,
-// bit 31-b <-> dimension 32w+b.  Estimate: fma(f_rescale, ip*scale + k1,
-// f_add + g[anchor]).
+// nibble masks exactly.  Planes are stored MSB-first like the codes (word w,
+// bit 31-b <-> dimension 32w+b) and plane-major in LDS: planes[j][word].
+// Estimate: fma(f_rescale, ip*scale + k1, f_add + g[anchor]).
+//
+// Rows of 2048 or 4096 bits are scored by the whole wave: the candidates are
+// packed into LDS and each 16-lane group scores one row per pass (lane l
+// owns the row's 16-byte vectors l and l + 16), so every lane works and the
+// code loads are coalesced; the group's integer partials are summed by DPP.
+// Shorter or longer rows are scored one candidate per lane.
+constexpr uint32_t kRabitqCoopBytes = 512;  // LDS after the planes: [64] ids, [64] ip
+
 struct RabitqScorer {
     static constexpr bool kHasExact = false;
     const uint8_t* codes;
@@ -303,7 +311,7 @@ struct RabitqScorer {
     const float* centroid_dists;
     uint32_t num_anchors;
     uint32_t padded_dim;
-    uint32_t* planes;  // LDS [padded_dim/32][8]
+    uint32_t* planes;  // LDS [8][padded_dim/32], then kRabitqCoopBytes
     float scale;
     float k1;
     const float* g_row;
@@ -321,55 +329,115 @@ struct RabitqScorer {
                 for (int j = 0; j < 8; ++j) pl[j] |= ((v >> j) & 1u) << (31u - b);
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) planes[w * 8 + j] = pl[j];
+            for (int j = 0; j < 8; ++j) planes[j * words + w] = pl[j];
         }
         scale = q_scale[q];
         k1 = q_k1[q];
         g_row = centroid_dists + static_cast<size_t>(q) * num_anchors;
     }
 
-    __device__ float score(uint32_t sample, bool active) const
+    // sum_j w_j popc(plane_j & code) over one 16-byte code vector.
+    __device__ __forceinline__ static void count_vec(const uint4* planes4, uint32_t vecs,
+                                                     uint32_t v, const uint4& c, uint32_t (&cnt)[8])
     {
-        if (!active) return 0.0f;
-        const uint32_t words = padded_dim / 32;
-        const uint4* row = reinterpret_cast<const uint4*>(codes + static_cast<size_t>(sample) * (padded_dim / 8));
-        uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        // Code loads go out kCodeBatch at a time before any is consumed, so
-        // a row costs ceil(vectors / kCodeBatch) memory round trips, not one
-        // per 16 bytes.
-        const uint32_t vecs = words / 4;
-        for (uint32_t v0 = 0; v0 < vecs; v0 += kCodeBatch) {
-            uint4 cb[kCodeBatch];
 #pragma unroll
-            for (int b = 0; b < kCodeBatch; ++b)
-                cb[b] = v0 + b < vecs ? row[v0 + b] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-            for (int b = 0; b < kCodeBatch; ++b) {
-                if (v0 + b >= vecs) break;
-                const uint32_t w4 = v0 + b;
-                const uint32_t cw[4] = {cb[b].x, cb[b].y, cb[b].z, cb[b].w};
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint4 p0 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2];
-                    const uint4 p1 = reinterpret_cast<const uint4*>(planes)[(w4 * 4 + t) * 2 + 1];
-                    cnt[0] = bcnt_acc(p0.x & cw[t], cnt[0]);
-                    cnt[1] = bcnt_acc(p0.y & cw[t], cnt[1]);
-                    cnt[2] = bcnt_acc(p0.z & cw[t], cnt[2]);
-                    cnt[3] = bcnt_acc(p0.w & cw[t], cnt[3]);
-                    cnt[4] = bcnt_acc(p1.x & cw[t], cnt[4]);
-                    cnt[5] = bcnt_acc(p1.y & cw[t], cnt[5]);
-                    cnt[6] = bcnt_acc(p1.z & cw[t], cnt[6]);
-                    cnt[7] = bcnt_acc(p1.w & cw[t], cnt[7]);
-                }
-            }
+        for (int j = 0; j < 8; ++j) {
+            const uint4 p = planes4[j * vecs + v];
+            cnt[j] = bcnt_acc(p.x & c.x, cnt[j]);
+            cnt[j] = bcnt_acc(p.y & c.y, cnt[j]);
+            cnt[j] = bcnt_acc(p.z & c.z, cnt[j]);
+            cnt[j] = bcnt_acc(p.w & c.w, cnt[j]);
         }
+    }
+
+    __device__ __forceinline__ static int32_t combine(const uint32_t (&cnt)[8])
+    {
         int32_t ip = 0;
 #pragma unroll
         for (int j = 0; j < 7; ++j) ip += static_cast<int32_t>(cnt[j]) << j;
-        ip -= 128 * static_cast<int32_t>(cnt[7]);
-        const uint32_t anchor = anchor_ids[sample];
-        const float f_add = factors[static_cast<size_t>(sample) * 3];
-        const float f_rescale = factors[static_cast<size_t>(sample) * 3 + 1];
+        return ip - 128 * static_cast<int32_t>(cnt[7]);
+    }
+
+    // Whole-wave ip of every active lane's candidate, rows of 16 * VPL
+    // vectors.  All 64 lanes call it.
+    template <int VPL>
+    __device__ int32_t ip_coop(uint32_t sample, bool active, int lane) const
+    {
+        uint32_t* s_cand = planes + padded_dim / 4;        // after the 8 planes
+        int32_t* s_ip = reinterpret_cast<int32_t*>(s_cand + kWave);
+        constexpr uint32_t vecs = 16 * VPL;
+        const uint4* planes4 = reinterpret_cast<const uint4*>(planes);
+        const uint64_t m = ballot(active);
+        const int n = __popcll(m);
+        const int rank = __popcll(m & ((1ull << lane) - 1ull));
+        if (active) s_cand[rank] = sample;
+        __syncthreads();
+        const int lg = lane & 15, grp = lane >> 4;
+        for (int b0 = 0; b0 < n; b0 += 16) {
+            // four rows per group in flight, then their counts
+            uint4 cb[4][VPL];
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int r = b0 + it * 4 + grp;
+                const uint32_t sj = r < n ? s_cand[r] : 0u;
+                const uint4* row = reinterpret_cast<const uint4*>(codes + static_cast<size_t>(sj) * (vecs * 16));
+#pragma unroll
+                for (int w = 0; w < VPL; ++w)
+                    cb[it][w] = r < n ? row[lg + 16 * w] : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int r = b0 + it * 4 + grp;
+                uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                for (int w = 0; w < VPL; ++w) count_vec(planes4, vecs, lg + 16 * w, cb[it][w], cnt);
+                const int32_t part = group_sum<16>(combine(cnt));
+                if (lg == 0 && r < n) s_ip[r] = part;
+            }
+        }
+        __syncthreads();
+        return active ? s_ip[rank] : 0;
+    }
+
+    // Every lane of the wave calls score (the whole-wave path needs them all).
+    __device__ float score(uint32_t sample, bool active) const
+    {
+        const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+        const uint32_t vecs = padded_dim / 128;
+        uint32_t anchor = 0;
+        float f_add = 0.0f, f_rescale = 0.0f;
+        if (active) {
+            anchor = anchor_ids[sample];
+            f_add = factors[static_cast<size_t>(sample) * 3];
+            f_rescale = factors[static_cast<size_t>(sample) * 3 + 1];
+        }
+        int32_t ip;
+        if (vecs == 32) {
+            ip = ip_coop<2>(sample, active, lane);
+        } else if (vecs == 16) {
+            ip = ip_coop<1>(sample, active, lane);
+        } else {
+            if (!active) return 0.0f;
+            const uint4* row = reinterpret_cast<const uint4*>(codes + static_cast<size_t>(sample) * (padded_dim / 8));
+            const uint4* planes4 = reinterpret_cast<const uint4*>(planes);
+            uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            // Code loads go out kCodeBatch at a time before any is consumed, so
+            // a row costs ceil(vectors / kCodeBatch) memory round trips, not one
+            // per 16 bytes.
+            for (uint32_t v0 = 0; v0 < vecs; v0 += kCodeBatch) {
+                uint4 cb[kCodeBatch];
+#pragma unroll
+                for (int b = 0; b < kCodeBatch; ++b)
+                    cb[b] = v0 + b < vecs ? row[v0 + b] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int b = 0; b < kCodeBatch; ++b) {
+                    if (v0 + b >= vecs) break;
+                    count_vec(planes4, vecs, v0 + b, cb[b], cnt);
+                }
+            }
+            ip = combine(cnt);
+        }
+        if (!active) return 0.0f;
         const float short_ip = static_cast<float>(ip) * scale;
         const float t = short_ip + k1;
         return fmaf(f_rescale, t, f_add + g_row[anchor]);
@@ -383,7 +451,7 @@ struct RabitqScorer {
         for (uint32_t w = 0; w < words; ++w) {
             const uint32_t cw = row[w];
             for (int j = 0; j < 8; ++j) {
-                const int32_t c = __popc(planes[w * 8 + j] & cw);
+                const int32_t c = __popc(planes[j * words + w] & cw);
                 ip += (j == 7) ? -128 * c : (c << j);
             }
         }

@@ -100,9 +100,27 @@ def _rviews(rw):
     return dev, rv
 
 
-def test_rabitq_score_ip_exact(gpu_ctx, rworld):
+def _at_dim(rw, P):
+    """rworld re-encoded at padded dim P (any [dim][P] matrix gives codes
+    both sides score alike; a QR above 1024 would dominate the test)."""
+    wl, li, pl, rot, codes, fac, aid, anchors, P0 = rw
+    if P == P0:
+        return rw
+    if P <= 1024:
+        rot = gi.random_rotation(wl.dim, P, 31005 + P, "cpu")
+    else:
+        rot = torch.randn(wl.dim, P, generator=torch.Generator().manual_seed(31005 + P)) / P ** 0.5
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
+    return wl, li, pl, rot, codes, fac, aid, anchors, P
+
+
+# 128 and 1024: one candidate per lane; 2048 and 4096: whole-wave scoring
+# (16-lane groups, one and two vectors per lane).
+@pytest.mark.parametrize("P", [128, 1024, 2048, 4096])
+def test_rabitq_score_ip_exact(gpu_ctx, rworld, P):
+    rworld = _at_dim(rworld, P)
     wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
-    say("rabitq score")
+    say("rabitq score P", P)
     dev, rv = _rviews(rworld)
     out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
     rng = np.random.default_rng(3)
@@ -127,12 +145,14 @@ def test_rabitq_score_ip_exact(gpu_ctx, rworld):
         assert np.float32(d[i].item()) == np.float32(want)
 
 
+@pytest.mark.parametrize("P", [128, 2048, 4096])
 @pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("hash_mode,nsamp", [(_lib.PLACE_AUTO, False), (_lib.PLACE_LDS, True),
                                              (_lib.PLACE_GLOBAL, True), (_lib.PLACE_SPILL, False)])
-def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp):
+def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp, P):
+    rworld = _at_dim(rworld, P)
     wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
-    say("rabitq search bias", bias, "hash", hash_mode, "nsamp", nsamp)
+    say("rabitq search P", P, "bias", bias, "hash", hash_mode, "nsamp", nsamp)
     dev, rv = _rviews(rworld)
     out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
     rs = pl.graph
@@ -168,10 +188,8 @@ def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp):
                                       (512, 1, 10), (512, 1, 512), (512, 110, 100),
                                       (384, 110, 100)])
 def test_rabitq_posting_scan_matches_oracle(gpu_ctx, rworld, P, reps, k):
-    wl, li, pl, rot, codes, fac, aid, anchors, _ = rworld
+    wl, li, pl, rot, codes, fac, aid, anchors, _ = _at_dim(rworld, P)
     say("rabitq posting scan P", P, "reps", reps, "k", k)
-    rot = gi.random_rotation(wl.dim, P, 31005 + P, "cpu")
-    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
     dev, rv = _rviews((wl, li, pl, rot, codes, fac, aid, anchors, P))
     out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
     rows = [(qi, ls[0], [l for l in ls if l != ls[0]], []) for qi, ls in enumerate(wl.query_labels)]
