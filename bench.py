@@ -327,11 +327,15 @@ class ExactRoute:
                                       device="cuda")
         self.ev = [pipe.torch.cuda.Event(enable_timing=True) for _ in range(2)]
 
+    # early-stop rule of the beam: (mode, fixed limit); step cap (0: none)
+    stop = (2, 1)  # adaptive (backend_pq.cu:2822-2873)
+    max_steps = 0
+
     def step(self, Q: int, timed_kernel=False):
         p, gs = self.pipe, self.gs
         L = gs._lib
         ng, npost = p.n_graph, p.n_post
-        prm = L.ExactParams(Q, 1, L.EARLY_STOP_ADAPTIVE, 0, 10, p.hash_mode)
+        prm = L.ExactParams(Q, self.stop[1], self.stop[0], self.max_steps, 10, p.hash_mode)
         if timed_kernel:
             self.ev[0].record()
         if ng:

@@ -206,118 +206,141 @@ __device__ __forceinline__ void rh_set(RegHeap& h, int i, const Entry& e, int la
     h.sample = me ? e.sample : h.sample;
 }
 
-__device__ __forceinline__ void rh_swap(RegHeap& h, int i, int j, int lane)
+// Entry i moves to slot y (the hole).
+__device__ __forceinline__ void rh_move(RegHeap& h, int i, int y, int lane)
 {
-    const Entry a = rh_get(h, i);
-    const Entry b = rh_get(h, j);
-    rh_set(h, i, b, lane);
-    rh_set(h, j, a, lane);
+    rh_set(h, y, rh_get(h, i), lane);
 }
 
-__device__ __forceinline__ int rh_adjust_sibling(RegHeap& h, int y, int size, int lane)
-{
-    if (y & 1) {
-        const int s = y + 1;
-        if (s >= size) return y;
-        if (rh_first(h, y) > rh_first(h, s)) {
-            rh_swap(h, y, s, lane);
-            return s;
-        }
-    } else {
-        const int s = y - 1;
-        if (rh_first(h, y) < rh_first(h, s)) {
-            rh_swap(h, y, s, lane);
-            return s;
-        }
-    }
-    return y;
-}
-
-__device__ __forceinline__ int rh_adjust_grandparent(RegHeap& h, int y, int lane)
-{
-    if (y <= 2) return y;
-    const int g = (y - 3) >> 2;
-    const int gl = (g << 1) + 1;
-    const int gr = (g << 1) + 2;
-    const float fy = rh_first(h, y);
-    if (rh_first(h, gl) > fy) {
-        rh_swap(h, gl, y, lane);
-        return gl;
-    } else if (rh_first(h, gr) < fy) {
-        rh_swap(h, gr, y, lane);
-        return gr;
-    }
-    return y;
-}
-
+// The sifts below keep the moving entry in scalar registers and shift each
+// entry it passes into the hole, writing the moving entry once at its final
+// slot.  Every comparison is the swap formulation's (smmh2.h:77-147), so the
+// array -- and with it every later tie-break -- is identical.
 __device__ __forceinline__ void rh_insert(RegHeap& h, int& size, const Entry& e, int lane)
 {
-    int y = size;
-    rh_set(h, size++, e, lane);
+    int y = size++;
     for (;;) {
-        y = rh_adjust_sibling(h, y, size, lane);
-        const int x = rh_adjust_grandparent(h, y, lane);
-        if (x == y) break;
-        y = x;
-    }
-}
-
-__device__ __forceinline__ int rh_adjust_grandchild(RegHeap& h, int y, int size, int lane)
-{
-    if (y & 1) {
-        const int cl = (y << 1) + 1;
-        if (cl >= size) return y;
-        const int cr = ((y + 1) << 1) + 1;
-        int c = cl;
-        if (cr < size && rh_first(h, cr) < rh_first(h, cl)) c = cr;
-        if (rh_first(h, c) < rh_first(h, y)) {
-            rh_swap(h, c, y, lane);
-            return c;
+        // sibling
+        if (y & 1) {
+            const int s = y + 1;
+            if (s < size && e.first > rh_first(h, s)) {
+                rh_move(h, s, y, lane);
+                y = s;
+            }
+        } else {
+            const int s = y - 1;
+            if (e.first < rh_first(h, s)) {
+                rh_move(h, s, y, lane);
+                y = s;
+            }
         }
-    } else {
-        const int cl = ((y - 1) << 1) + 2;
-        const int cr = (y << 1) + 2;
-        if (cl >= size) return y;
-        int c = cl;
-        if (cr < size && rh_first(h, cr) > rh_first(h, cl)) c = cr;
-        if (rh_first(h, c) > rh_first(h, y)) {
-            rh_swap(h, c, y, lane);
-            return c;
+        // grandparent
+        if (y <= 2) break;
+        const int g = (y - 3) >> 2;
+        const int gl = (g << 1) + 1;
+        const int gr = (g << 1) + 2;
+        if (rh_first(h, gl) > e.first) {
+            rh_move(h, gl, y, lane);
+            y = gl;
+        } else if (rh_first(h, gr) < e.first) {
+            rh_move(h, gr, y, lane);
+            y = gr;
+        } else {
+            break;
         }
     }
-    return y;
+    rh_set(h, y, e, lane);
 }
 
 __device__ __forceinline__ void rh_pop_max(RegHeap& h, int& size, int lane)
 {
     --size;
-    rh_set(h, 2, rh_get(h, size), lane);
+    Entry x = rh_get(h, size);  // the last entry refills the max slot
     int y = 2;
     for (;;) {
-        (void)rh_adjust_sibling(h, y, size, lane);
-        const int x = rh_adjust_grandchild(h, y, size, lane);
-        if (x == y) break;
-        y = x;
+        // sibling: a swap leaves x at the sibling for good and continues
+        // with the sibling's entry at y
+        if (y & 1) {
+            const int s = y + 1;
+            if (s < size && x.first > rh_first(h, s)) {
+                const Entry t = rh_get(h, s);
+                rh_set(h, s, x, lane);
+                x = t;
+            }
+        } else {
+            const int s = y - 1;
+            if (x.first < rh_first(h, s)) {
+                const Entry t = rh_get(h, s);
+                rh_set(h, s, x, lane);
+                x = t;
+            }
+        }
+        // grandchild
+        int c;
+        bool down;
+        if (y & 1) {
+            const int cl = (y << 1) + 1;
+            if (cl >= size) break;
+            const int cr = ((y + 1) << 1) + 1;
+            c = cl;
+            float fc = rh_first(h, cl);
+            if (cr < size) {
+                const float fr = rh_first(h, cr);
+                if (fr < fc) {
+                    c = cr;
+                    fc = fr;
+                }
+            }
+            down = fc < x.first;
+        } else {
+            const int cl = ((y - 1) << 1) + 2;
+            const int cr = (y << 1) + 2;
+            if (cl >= size) break;
+            c = cl;
+            float fc = rh_first(h, cl);
+            if (cr < size) {
+                const float fr = rh_first(h, cr);
+                if (fr > fc) {
+                    c = cr;
+                    fc = fr;
+                }
+            }
+            down = fc > x.first;
+        }
+        if (!down) break;
+        rh_move(h, c, y, lane);
+        y = c;
     }
+    rh_set(h, y, x, lane);
 }
 
-// Unused entry of least `first`, lowest index on ties; marked used.
+// Wave-uniform minimum of x: DPP inside each 16-lane row, then the four
+// row minima.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x)
+{
+    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, false)));
+    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xF, 0xF, false)));
+    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x141, 0xF, 0xF, false)));
+    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x140, 0xF, 0xF, false)));
+    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 0));
+    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 16));
+    const uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 32));
+    const uint32_t d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 48));
+    return min(min(a, b), min(c, d));
+}
+
+// Unused entry of least `first`, lowest index on ties; marked used.  The
+// frontier's keys are exact squared distances (>= 0), whose float bits
+// order as unsigned integers: one unsigned minimum, then the lowest lane
+// holding it.
 __device__ __forceinline__ bool rh_pickup(RegHeap& h, int size, Entry& out, int lane)
 {
     const bool live = lane >= 1 && lane < size && !(h.second & kPoolUsed);
-    float bv = live ? h.first : 0.0f;
-    int best = live ? lane : -1;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const int ob = __shfl_xor(best, off, kWave);
-        const float ov = __shfl_xor(bv, off, kWave);
-        if (ob >= 0 && (best < 0 || ov < bv || (!(bv < ov) && ob < best))) {
-            best = ob;
-            bv = ov;
-        }
-    }
-    best = bcast0(best);
-    if (best < 0) return false;
+    const uint32_t key = live ? __float_as_uint(h.first) : UINT32_MAX;
+    const uint32_t mn = wave_min_u32(key);
+    const uint64_t at = ballot(live && key == mn);
+    if (at == 0) return false;
+    const int best = __builtin_ctzll(at);
     out = rh_get(h, best);
     if (lane == best) h.second |= kPoolUsed;
     return true;
