@@ -39,6 +39,11 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 // 1: rows of 128, 192 or 256 bytes use kernels with the row length fixed
 // at compile time (all of a row's loads in flight at once, at the price of
 // about 40 more VGPRs and so fewer resident routes); 0 keeps the loop.
+// 16-byte chunks of a row in flight per round trip on the runtime-length
+// path (a build-time tuning knob: more chunks, more registers).
+#ifndef GOFANN_EXACT_ROW_UNROLL
+#define GOFANN_EXACT_ROW_UNROLL 4
+#endif
 #ifndef GOFANN_EXACT_FIXED_ROWS
 #define GOFANN_EXACT_FIXED_ROWS 0
 #endif
@@ -69,6 +74,7 @@ __device__ __forceinline__ uint32_t l2_u8_row(const uint8_t* row, const uint32_t
     if ((dim & 15u) == 0) {
         const uint4* r4 = reinterpret_cast<const uint4*>(row);
         const uint4* q4 = reinterpret_cast<const uint4*>(q);
+#pragma unroll GOFANN_EXACT_ROW_UNROLL
         for (uint32_t i = 0; i < dim / 16; ++i) {
             const uint4 b = r4[i];
             const uint4 w = q4[i];
@@ -137,35 +143,58 @@ __device__ __forceinline__ bool better(float ld, uint32_t lid, float rd, uint32_
     return ld < rd || (ld == rd && lid < rid);
 }
 
-// insert_best_result on LDS arrays (lane 0).
-__device__ __forceinline__ bool best_insert(float d, uint32_t id, uint32_t K, float* bd,
-                                            uint32_t* bi, uint32_t& size)
+// insert_best_result (backend_full_gpu.cu:1342-1375) on a register array:
+// lane i < K holds entry i, ascending by (distance, id), ids unique.  Every
+// lane calls it with the same (d, id); size is wave-uniform.  The entries
+// live in the first 16-lane row (K <= 10), so shifts are row DPP moves.
+struct BestK {
+    float d;
+    uint32_t id;
+};
+
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, int ctrl)
 {
-    bool changed = false;
-    for (uint32_t i = 0; i < size; ++i) {
-        if (bi[i] != id) continue;
-        if (d >= bd[i]) return false;
-        for (uint32_t j = i; j + 1 < size; ++j) {
-            bd[j] = bd[j + 1];
-            bi[j] = bi[j + 1];
+    switch (ctrl) {
+    case 0x101: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x101, 0xF, 0xF, false));
+    default: return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x111, 0xF, 0xF, false));
+    }
+}
+
+__device__ __forceinline__ bool best_insert(BestK& b, float d, uint32_t id, uint32_t K,
+                                            uint32_t& size, int lane)
+{
+    const bool in = static_cast<uint32_t>(lane) < size;
+    const uint64_t dup = ballot(in && b.id == id);
+    if (dup) {
+        const int i = __builtin_ctzll(dup);
+        if (d >= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.d), i))) return false;
+        // drop entry i: lanes i.. take their right neighbour (row_shl:1)
+        const uint32_t nd = dpp_u32(__float_as_uint(b.d), 0x101);
+        const uint32_t ni = dpp_u32(b.id, 0x101);
+        if (lane >= i) {
+            b.d = __uint_as_float(nd);
+            b.id = ni;
         }
         --size;
-        changed = true;
-        break;
     }
-    if (size == K && !better(d, id, bd[K - 1], bi[K - 1])) return changed;
-    uint32_t pos = size;
-    if (size < K)
-        ++size;
-    else
-        pos = K - 1;
-    while (pos > 0 && better(d, id, bd[pos - 1], bi[pos - 1])) {
-        bd[pos] = bd[pos - 1];
-        bi[pos] = bi[pos - 1];
-        --pos;
+    if (size == K) {
+        const float ld = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.d), static_cast<int>(K) - 1));
+        const uint32_t li = static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(b.id), static_cast<int>(K) - 1));
+        if (!better(d, id, ld, li)) return false;
     }
-    bd[pos] = d;
-    bi[pos] = id;
+    // entries before (d, id) stay; the rest move right (row_shr:1)
+    const int pos = __popcll(ballot(static_cast<uint32_t>(lane) < size && better(b.d, b.id, d, id)));
+    const uint32_t sd = dpp_u32(__float_as_uint(b.d), 0x111);
+    const uint32_t si = dpp_u32(b.id, 0x111);
+    if (lane > pos) {
+        b.d = __uint_as_float(sd);
+        b.id = si;
+    } else if (lane == pos) {
+        b.d = d;
+        b.id = id;
+    }
+    if (size < K) ++size;
     return true;
 }
 
@@ -384,8 +413,6 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
     __shared__ uint32_t s_row[kMaxDegree];
     __shared__ uint32_t s_samp[kMaxDegree];
     __shared__ float s_dist[kMaxDegree];
-    __shared__ float s_bd[kExactMaxTopk];
-    __shared__ uint32_t s_bi[kExactMaxTopk];
     __shared__ uint64_t s_adm;
 
     const int lane = static_cast<int>(threadIdx.x);
@@ -428,16 +455,13 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
     visited.init(reinterpret_cast<uint32_t*>(lds + a.off_hash),
                  a.hash_global ? a.hash_global + static_cast<size_t>(slot) * kHashCapacity : nullptr,
                  lane);
-    if (lane < kExactMaxTopk) {
-        s_bd[lane] = FLT_MAX;
-        s_bi[lane] = UINT32_MAX;
-    }
     __threadfence_block();
     __syncthreads();
 
     gofann_route_stats st{0, 0, 0, 0, 0, 0, 0, 0};
     PredCounters pc{0, 0};
-    uint32_t bsize = 0;
+    uint32_t bsize = 0;  // wave-uniform
+    BestK bk{FLT_MAX, UINT32_MAX};
     int heap_size = 1;
     bool done = false;
     const Entry sentinel = {FLT_MAX, UINT32_MAX, FLT_MAX, UINT32_MAX};
@@ -531,8 +555,8 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
         if (lane == 0) {
             pc.rows += c.rows;
             pc.labels += c.labels;
-            if (ok) improved = best_insert(now.first, sample, K, s_bd, s_bi, bsize) ? 1 : 0;
         }
+        if (ok) improved = best_insert(bk, now.first, sample, K, bsize, lane) ? 1 : 0;
         ++st.expanded;
         st.passed += ok ? 1 : 0;
         ++steps;
@@ -624,10 +648,13 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
         }
         load_node(a.graph, a.pred, enabled, off, degree, next, lane, cur);
         int stop = 0;
+        const float kd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bk.d), static_cast<int>(K) - 1));
+        const uint32_t ki = static_cast<uint32_t>(
+            __builtin_amdgcn_readlane(static_cast<int>(bk.id), static_cast<int>(K) - 1));
         if (lane == 0 && !first_step) {
             if (mode == GOFANN_EARLY_STOP_ADAPTIVE && improved) {
                 finished = 0;
-            } else if (bsize == K && !better(next.first, next.sample, s_bd[K - 1], s_bi[K - 1])) {
+            } else if (bsize == K && !better(next.first, next.sample, kd, ki)) {
                 ++finished;
                 stop = early_stop_reached(mode, static_cast<int>(finished), a.params.finish_limit,
                                           Q, st.expanded, st.passed, static_cast<int>(K))
@@ -645,10 +672,10 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
     __syncthreads();
     uint32_t* oid = a.out_ids + static_cast<size_t>(route) * K;
     float* od = a.out_dists + static_cast<size_t>(route) * K;
-    const uint32_t nb = bcast0u(bsize);
+    const uint32_t nb = bsize;
     if (static_cast<uint32_t>(lane) < K) {
-        oid[lane] = static_cast<uint32_t>(lane) < nb ? s_bi[lane] : UINT32_MAX;
-        od[lane] = static_cast<uint32_t>(lane) < nb ? s_bd[lane] : FLT_MAX;
+        oid[lane] = static_cast<uint32_t>(lane) < nb ? bk.id : UINT32_MAX;
+        od[lane] = static_cast<uint32_t>(lane) < nb ? bk.d : FLT_MAX;
     }
     const int pred_rows = wave_sum(static_cast<int>(pc.rows));
     const int pred_labels = wave_sum(static_cast<int>(pc.labels));
