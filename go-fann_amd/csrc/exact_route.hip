@@ -39,11 +39,6 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 // 1: rows of 128, 192 or 256 bytes use kernels with the row length fixed
 // at compile time (all of a row's loads in flight at once, at the price of
 // about 40 more VGPRs and so fewer resident routes); 0 keeps the loop.
-// 16-byte chunks of a row in flight per round trip on the runtime-length
-// path (a build-time tuning knob: more chunks, more registers).
-#ifndef GOFANN_EXACT_ROW_UNROLL
-#define GOFANN_EXACT_ROW_UNROLL 4
-#endif
 #ifndef GOFANN_EXACT_FIXED_ROWS
 #define GOFANN_EXACT_FIXED_ROWS 0
 #endif
@@ -74,7 +69,9 @@ __device__ __forceinline__ uint32_t l2_u8_row(const uint8_t* row, const uint32_t
     if ((dim & 15u) == 0) {
         const uint4* r4 = reinterpret_cast<const uint4*>(row);
         const uint4* q4 = reinterpret_cast<const uint4*>(q);
-#pragma unroll GOFANN_EXACT_ROW_UNROLL
+        // four 16-byte chunks per round trip: two buy a sixth wave per SIMD
+        // but double the round trips, six cost a wave; both ran slower
+#pragma unroll 4
         for (uint32_t i = 0; i < dim / 16; ++i) {
             const uint4 b = r4[i];
             const uint4 w = q4[i];
@@ -341,21 +338,6 @@ __device__ __forceinline__ void rh_pop_max(RegHeap& h, int& size, int lane)
         y = c;
     }
     rh_set(h, y, x, lane);
-}
-
-// Wave-uniform minimum of x: DPP inside each 16-lane row, then the four
-// row minima.
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x)
-{
-    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, false)));
-    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xF, 0xF, false)));
-    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x141, 0xF, 0xF, false)));
-    x = min(x, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x140, 0xF, 0xF, false)));
-    const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 0));
-    const uint32_t b = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 16));
-    const uint32_t c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 32));
-    const uint32_t d = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 48));
-    return min(min(a, b), min(c, d));
 }
 
 // Unused entry of least `first`, lowest index on ties; marked used.  The

@@ -75,10 +75,17 @@ int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabit
     // 8 planes x padded_dim bits, then the whole-wave scorer's candidates
     const uint32_t plane_bytes = rq->padded_dim + kRabitqCoopBytes;
     const Layout l = make_layout(plane_bytes, p->queue_limit, p->result_width);
-    const Placement pl = choose_visited<RabitqScorer>(ctx, l, p->hash_mode);
     ctx->last_table_in_lds = 1;
-    return launch_traversal(ctx, make_rabitq_scorer(rq, pre), l, pl, g, pred, r, p, out_ids,
-                            out_dists, stats, 1);
+    // Beams with Q + 2 <= 64 keep the frontier in registers (lane i holds
+    // entry i); larger ones in LDS.
+    if (p->queue_limit + 2 <= kWave) {
+        const Placement pl = choose_visited<RabitqScorer, true>(ctx, l, p->hash_mode);
+        return launch_traversal<RabitqScorer, true>(ctx, make_rabitq_scorer(rq, pre), l, pl, g,
+                                                    pred, r, p, out_ids, out_dists, stats, 1);
+    }
+    const Placement pl = choose_visited<RabitqScorer, false>(ctx, l, p->hash_mode);
+    return launch_traversal<RabitqScorer, false>(ctx, make_rabitq_scorer(rq, pre), l, pl, g, pred,
+                                                 r, p, out_ids, out_dists, stats, 1);
 }
 
 int rabitq_score(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre,

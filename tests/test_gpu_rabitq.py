@@ -145,18 +145,20 @@ def test_rabitq_score_ip_exact(gpu_ctx, rworld, P):
         assert np.float32(d[i].item()) == np.float32(want)
 
 
+# Q = 40 keeps the frontier in registers (Q + 2 <= 64), Q = 96 in LDS.
+@pytest.mark.parametrize("Q", [40, 96])
 @pytest.mark.parametrize("P", [128, 2048, 4096])
 @pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("hash_mode,nsamp", [(_lib.PLACE_AUTO, False), (_lib.PLACE_LDS, True),
                                              (_lib.PLACE_GLOBAL, True), (_lib.PLACE_SPILL, False)])
-def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp, P):
+def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp, P, Q):
     rworld = _at_dim(rworld, P)
     wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
-    say("rabitq search P", P, "bias", bias, "hash", hash_mode, "nsamp", nsamp)
+    say("rabitq search P", P, "Q", Q, "bias", bias, "hash", hash_mode, "nsamp", nsamp)
     dev, rv = _rviews(rworld)
     out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
     rs = pl.graph
-    Q, W = 40, 30
+    W = 30
     pred_o = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15 if bias else 0.0,
                                           pending_base_stop=bias)
     prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias, rabitq_verdict=1)
