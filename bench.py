@@ -739,7 +739,7 @@ def main_c3(args):
     sb = pipe.scan_rows_total * (4 + P // 8 + 4 + 8) + 0.0  # posting id + C per row
     rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 4 + 4) + 0.0
     kern = {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
-            "range_scan_kernel+segment_merge_kernel": (st_ms["range_scan"], sb),
+            "range_scan_group_kernel+segment_merge_kernel (range postings)": (st_ms["range_scan"], sb),
             "exact_rerank_kernel (f32)": (st_ms["rerank"], rb)}
     per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
                "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None}
@@ -1006,7 +1006,7 @@ def main_c4(args):
     pb = pipe.post_rows_total * (4 + P // 8 + 4 + 8) + 0.0
     rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 2 + 4) + 0.0
     kern = {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
-            "posting_scan_kernel<RabitqScanScorer>": (st_ms["posting_scan"], pb),
+            "range_scan_group_kernel+segment_merge_kernel (label postings)": (st_ms["posting_scan"], pb),
             "exact_rerank_kernel (f16)": (st_ms["rerank"], rb)}
     per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
                "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None}
