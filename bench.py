@@ -601,6 +601,7 @@ class RabitqRangePipeline:
         self.ng, self.np_ = len(gq), len(pq)
         # graph routes: one per wide-range query, seeded at the nearest bucket
         rows = [(int(q), 0, [], [tuple(wl.query_ranges[q][0])]) for q in gq]
+        self.graph_rows = rows
         rs = gp._routeset(rows, li)
         if rs.count:
             rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
@@ -614,6 +615,8 @@ class RabitqRangePipeline:
         self.hi_p = torch.from_numpy(hi[pq] if len(pq) else hi[:1]).cuda()
         self.brv = torch.from_numpy(wl.base_ranges).cuda()
         offs, sizes = rp.route_postings(rpi, slices[pq])
+        self.scan_query, self.scan_off, self.scan_size = pq, offs, sizes
+        self.rpi, self.modes, self.lo, self.hi = rpi, modes, lo, hi
         self.scan_rows_total = int(sizes.sum())
         plan = rp.segment_plan(np.arange(len(pq), dtype=np.uint32), offs, sizes, segment_rows)
         self.segs = rp.DeviceSegments(plan, merged=True)
@@ -690,6 +693,108 @@ class RabitqRangePipeline:
 
     def route_stats(self):
         return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
+
+
+def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
+    """The oracle (single-threaded C restatement) on a bounded sample of a
+    RaBitQ route set (C3 or C4): for the first queries until `seconds`
+    elapse, their graph routes (RaBitQ beam, shortlist W), their range- or
+    label-posting scans, the exact rerank of the shortlists and the merge.
+    The full base vectors do not fit the host sample, so the rows the
+    shortlists name are gathered (the rerank reads exactly those rows)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import ctypes as C
+    import torch
+    import pyoracle as po
+    from gofann_amd import plan as gp
+    P, W = rq["P"], pipe.W
+    codes = rq["codes"].cpu().numpy()
+    fac = rq["fac"].cpu().numpy()
+    aid = rq["aid"].cpu().numpy().view(np.uint32)
+    A = rq["anchors"].shape[0]
+    pre = {k: pipe.prep[k].cpu().numpy() for k in ("q8", "scale", "k1", "cd")}
+    qs = wl.queries.cpu().numpy()
+    L = po.lib()
+    by_q = {}
+    for r in pipe.graph_rows:
+        by_q.setdefault(r[0], []).append(r)
+    scan_by_q = {}
+    if hasattr(pipe, "scan_query"):
+        for i, q in enumerate(pipe.scan_query):
+            scan_by_q.setdefault(int(q), []).append(i)
+    post_by_q = {}
+    for i, r in enumerate(getattr(pipe, "post_rows", [])):
+        post_by_q.setdefault(r[0], []).append((i, r))
+    done, t0 = 0, time.perf_counter()
+    nq = qs.shape[0]
+    while done < nq and time.perf_counter() - t0 < seconds:
+        sel = list(range(done, min(nq, done + chunk)))
+        lists, r2q = [], []
+        rows = [r for q in sel for r in by_q.get(q, [])]
+        if rows:
+            rs = gp._routeset(rows, li)
+            rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
+            pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
+                                                pending_base_stop=True,
+                                                base_ranges=wl.base_ranges)
+            ids, _, _ = po.rabitq_search(li, rs, pred, po.params(queue_limit=pipe.chosen,
+                                                                 result_width=W,
+                                                                 early_stop_mode=2, bias=True,
+                                                                 rabitq_verdict=1),
+                                         codes, fac, aid, pre["q8"], pre["scale"], pre["k1"],
+                                         pre["cd"], A, P)
+            lists.append(ids), r2q.append(rs.route_query)
+        scans = [i for q in sel for i in scan_by_q.get(q, [])]
+        if scans:  # range-posting scans over the whole smallest slice
+            rq_ = pipe.scan_query[scans].astype(np.uint32)
+            n = len(scans)
+            ids, _, _ = po.rabitq_range_scan(
+                None, pipe.modes[rq_], pipe.lo[rq_], pipe.hi[rq_], wl.base_ranges, codes, fac,
+                aid, pre["q8"], pre["scale"], pre["k1"], pre["cd"], rq_,
+                np.concatenate([d.sample_ids for d in pipe.rpi.dimensions]),
+                pipe.rpi.resident_rows, wl.n, np.arange(n, dtype=np.uint32),
+                pipe.scan_off[scans], pipe.scan_size[scans], W, False)
+            lists.append(ids), r2q.append(rq_)
+        posts = [t for q in sel for t in post_by_q.get(q, [])]
+        if posts:  # label-posting scans
+            prs = gp._routeset([r for _, r in posts], li)
+            pred = po.PredicateArrays.from_plan(prs.predicate, li)
+            off = np.array([li.posting_offset[r[1]] for _, r in posts], np.uint32)
+            size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]]
+                             for _, r in posts], np.uint32)
+            n = prs.count
+            oi = np.empty((n, W), np.uint32)
+            od = np.empty((n, W), np.float32)
+            opass = np.empty(n, np.uint32)
+            arrs = [np.ascontiguousarray(a) for a in (codes, fac, aid, pre["q8"], pre["scale"],
+                                                      pre["k1"], pre["cd"], prs.route_query,
+                                                      li.posting_ids, off, size)]
+            assert L.orc_rabitq_posting_scan(
+                C.byref(pred.struct), po.p(arrs[0]), C.c_uint32(P // 8),
+                *[po.p(a) for a in arrs[1:7]], C.c_uint32(A), C.c_uint32(P),
+                *[po.p(a) for a in arrs[7:]], C.c_uint32(n), W, po.p(oi), po.p(od),
+                po.p(opass)) == 0
+            lists.append(oi), r2q.append(prs.route_query)
+        if lists:
+            sl = np.concatenate(lists)
+            rqy = np.concatenate(r2q).astype(np.uint32)
+            uniq, inv = np.unique(sl[sl != 0xFFFFFFFF], return_inverse=True)
+            local = np.full(sl.shape, 0xFFFFFFFF, np.uint32)
+            local[sl != 0xFFFFFFFF] = inv.astype(np.uint32)
+            rows_h = wl.base[torch.as_tensor(uniq.astype(np.int64), device=wl.base.device)]
+            rows_h = rows_h.cpu().numpy()
+            li_, ld_ = po.rerank(rows_h, qs, rqy, local, 10)
+            li_ = np.where(li_ != 0xFFFFFFFF, uniq[np.minimum(li_, max(len(uniq) - 1, 0))],
+                           0xFFFFFFFF).astype(np.uint32)
+            po.merge(rqy - sel[0], li_, ld_, len(sel), 10)
+        done += len(sel)
+    el = time.perf_counter() - t0
+    return done / el, done, el
+
+
+def cpu_line(rate, done, el, what):
+    return {"value": round(rate, 2), "unit": "queries/s", "cores": 1, "kind": "port",
+            "sample": f"first {done} of the queries ({what}) in {el:.1f}s on one host core"}
 
 
 def main_c3(args):
@@ -769,6 +874,11 @@ def main_c3(args):
                      "algorithmic_bytes": kern[top][1]},
         "cpu_baseline": None,
     }
+    if not args.no_cpu_baseline:
+        pipe.chosen = chosen
+        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph routes at the chosen Q, range-posting scans, exact fp32 rerank, merge")
+        log(f"cpu baseline {cr:.1f} qps over {cn} queries")
     print(json.dumps(line), flush=True)
     ctx.close()
 
@@ -872,6 +982,7 @@ class RabitqLabelPipeline:
                 self.interior += int(inside)
                 graph_rows.append((q, cats + i, [], [] if inside else [(0, 3, lo, hi)]))
         graph_rows.sort(key=lambda r: (r[1], r[0]))
+        self.graph_rows, self.post_rows = graph_rows, post_rows
         rs = gp._routeset(graph_rows, li)
         if rs.count:
             rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
@@ -1039,6 +1150,11 @@ def main_c4(args):
                      "algorithmic_bytes": kern[top][1]},
         "cpu_baseline": None,
     }
+    if not args.no_cpu_baseline:
+        pipe.chosen = chosen
+        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph and interval routes at the chosen Q, label-posting scans, exact fp16 rerank, merge")
+        log(f"cpu baseline {cr:.1f} qps over {cn} queries")
     print(json.dumps(line), flush=True)
 
 def main():
