@@ -81,6 +81,9 @@ def parse():
     ap.add_argument("--c3-scan-rows", type=int, default=20_000,
                     help="ranges whose smallest posting slice has at most this many rows are "
                          "scanned; wider ones search the graph with the range predicate")
+    ap.add_argument("--c3-gather", action="store_true",
+                    help="range scans gather rows by sample id instead of streaming the "
+                         "posting-order copies")
     ap.add_argument("--no-rabitq-prep", action="store_true",
                     help="skip the RaBitQ query-preparation (rotation GEMM) measurement")
     ap.add_argument("--no-exact-route", action="store_true",
@@ -582,7 +585,8 @@ class RabitqRangePipeline:
     the smallest slice for narrow ones (both shortlist 200), exact fp32
     rerank of the 200, and the per-query merge."""
 
-    def __init__(self, ctx, wl, li, rq, rpi, torch, scan_rows, width=200, segment_rows=4096):
+    def __init__(self, ctx, wl, li, rq, rpi, torch, scan_rows, width=200, segment_rows=4096,
+                 resident_copies=True):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
         from gofann_amd import range_posting as rp
@@ -628,6 +632,9 @@ class RabitqRangePipeline:
         self.rv = _lib.RabitqView(_lib.ptr(self.dev["codes"]), _lib.ptr(self.dev["fac"]),
                                   _lib.ptr(self.dev["aid"]), _lib.ptr(self.dev["anchors"]),
                                   wl.dim, P, rq["anchors"].shape[0], wl.n)
+        # posting-order copies of the rows the range scans stream
+        self.prows = (rp.PostingRows(ctx, self.rv, self.postings, self.resident)
+                      if resident_copies else None)
         A = rq["anchors"].shape[0]
         self.prep = dict(rotated=torch.empty(nq, P, device="cuda"),
                          q8=torch.empty(nq, P, dtype=torch.int8, device="cuda"),
@@ -668,10 +675,19 @@ class RabitqRangePipeline:
             routes = L.Routes(L.ptr(self.post_query), None, None, None, None, L.ptr(self.modes_p),
                               L.ptr(self.lo_p), L.ptr(self.hi_p), L.ptr(self.brv), 1, self.np_,
                               None)
-            ctx.check(ctx.lib.gofann_rabitq_range_scan(
-                ctx.handle, self.rv, self.rq, L.PredicateView(), routes, L.ptr(self.postings),
-                self.resident, self.segs.view(), W, 0, L.ptr(self.sl_i[self.ng * W:]),
-                L.ptr(self.sl_d[self.ng * W:]), L.ptr(self.passes)))
+            if self.prows is not None:
+                ctx.check(ctx.lib.gofann_rabitq_range_scan_resident(
+                    ctx.handle, self.rv, self.rq, L.PredicateView(), routes,
+                    L.ptr(self.postings), self.resident, L.ptr(self.prows.codes),
+                    L.ptr(self.prows.aux), self.segs.view(), W, 0,
+                    L.ptr(self.sl_i[self.ng * W:]), L.ptr(self.sl_d[self.ng * W:]),
+                    L.ptr(self.passes)))
+            else:
+                ctx.check(ctx.lib.gofann_rabitq_range_scan(
+                    ctx.handle, self.rv, self.rq, L.PredicateView(), routes,
+                    L.ptr(self.postings), self.resident, self.segs.view(), W, 0,
+                    L.ptr(self.sl_i[self.ng * W:]), L.ptr(self.sl_d[self.ng * W:]),
+                    L.ptr(self.passes)))
         if timed:
             ev[3].record()
         n = self.ng + self.np_
@@ -806,7 +822,8 @@ def main_c3(args):
     gt = ground_truth_c3(wl, torch, args.gt_queries_c3)
     log(f"C3 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     ctx = _lib.Context(0)
-    pipe = RabitqRangePipeline(ctx, wl, li, rq, rpi, torch, args.c3_scan_rows)
+    pipe = RabitqRangePipeline(ctx, wl, li, rq, rpi, torch, args.c3_scan_rows,
+                               resident_copies=not args.c3_gather)
     log(f"C3 routes: {pipe.ng} graph (wide ranges), {pipe.np_} range-posting scans "
         f"({pipe.scan_rows_total} rows)")
     ladder = [args.queue] if args.queue else [int(x) for x in args.c3_ladder.split(",")]

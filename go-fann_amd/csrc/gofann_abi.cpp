@@ -234,6 +234,35 @@ int gofann_rabitq_range_scan(gofann_ctx* c, const gofann_rabitq_view* rq,
     });
 }
 
+int gofann_rabitq_posting_rows(gofann_ctx* c, const gofann_rabitq_view* rq,
+                               const uint32_t* posting_sample_ids, uint64_t rows,
+                               uint8_t* out_codes, uint32_t* out_aux)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::rabitq_posting_rows(ctx, rq, posting_sample_ids, rows, out_codes, out_aux);
+    });
+}
+
+int gofann_rabitq_range_scan_resident(gofann_ctx* c, const gofann_rabitq_view* rq,
+                                      const gofann_rabitq_queries* prepared,
+                                      const gofann_predicate_view* predicate,
+                                      const gofann_routes* routes,
+                                      const uint32_t* posting_sample_ids, uint64_t resident_rows,
+                                      const uint8_t* posting_codes, const uint32_t* posting_aux,
+                                      const gofann_posting_segments* segments, int shortlist_k,
+                                      int score_first, uint32_t* out_ids, float* out_dists,
+                                      uint32_t* pass_counts)
+{
+    return guarded(c, [&](Context* ctx) {
+        if (!posting_codes || !posting_aux)
+            return ctx->fail(GOFANN_ERR_INVALID, "posting codes and aux required");
+        return gofann::rabitq_range_scan(ctx, rq, prepared, predicate, routes, posting_sample_ids,
+                                         resident_rows, segments, shortlist_k, score_first,
+                                         out_ids, out_dists, pass_counts, posting_codes,
+                                         posting_aux);
+    });
+}
+
 int gofann_exact_rerank(gofann_ctx* c, const void* base, int base_elem, uint32_t dim,
                         uint32_t samples, const void* queries, const uint32_t* route_query,
                         const uint32_t* shortlist, uint32_t width, uint32_t routes, uint32_t topk,

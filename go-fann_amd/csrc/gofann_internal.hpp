@@ -100,7 +100,10 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
                       const gofann_routes* routes, const uint32_t* posting,
                       uint64_t resident_rows, const gofann_posting_segments* seg,
                       int shortlist_k, int score_first, uint32_t* out_ids, float* out_dists,
-                      uint32_t* pass_counts);
+                      uint32_t* pass_counts, const uint8_t* posting_codes = nullptr,
+                      const uint32_t* posting_aux = nullptr);
+int rabitq_posting_rows(Context* ctx, const gofann_rabitq_view* rq, const uint32_t* posting,
+                        uint64_t rows, uint8_t* out_codes, uint32_t* out_aux);
 int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
                  const void* queries, const gofann_graph_view* g, const uint32_t* label_size,
                  const gofann_predicate_view* pred, const gofann_routes* r,

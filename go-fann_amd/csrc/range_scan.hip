@@ -79,6 +79,11 @@ struct RangeScanArgs {
     const uint32_t* cand_offsets;
     const uint32_t* cand_sizes;
     uint32_t slices;
+    // Posting-order copies of the rows (range mode, group kernel; may be
+    // null): codes [rows][padded_dim/8] and aux [rows] = {f_add, f_rescale,
+    // anchor, 0}.  Row r of the posting is read from them, not gathered.
+    const uint4* pcodes;
+    const uint4* paux;
 };
 
 __device__ __forceinline__ bool pair_le(float ad, uint32_t aid, float bd, uint32_t bid)
@@ -362,6 +367,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     uint32_t* s_id = reinterpret_cast<uint32_t*>(s_d + a.slots);
     float* s_f1 = reinterpret_cast<float*>(s_id + a.slots);
     int* s_ip = reinterpret_cast<int*>(s_f1 + a.chunk);
+    uint32_t* s_prow = reinterpret_cast<uint32_t*>(s_ip + a.chunk);  // segment-relative row
 
     const bool label_mode = a.label_mode != 0;
     const uint32_t route = label_mode ? seg / a.slices : a.seg_route[seg];
@@ -382,7 +388,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     const int grp = tid / G;
     // plane-major copy of the word-major planes sc.setup wrote
     const uint32_t words = sc.padded_dim / 32;
-    uint32_t* planes_t = reinterpret_cast<uint32_t*>(s_ip + a.chunk);
+    uint32_t* planes_t = reinterpret_cast<uint32_t*>(s_prow + a.chunk);
     for (uint32_t e = tid; e < words * 8; e += kScanThreads)
         planes_t[(e & 7) * words + (e >> 3)] = sc.planes[e];
     __syncthreads();
@@ -450,9 +456,15 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
                 // filter-first counts every passing row; a label posting
                 // (backend_rabitq.cu:5494-5682) only predicate-checked ones
                 if (label_mode ? enabled : !score_first) ++passes;
-                const uint32_t anchor = sc.anchor_ids[s];
-                add0 = sc.factors[static_cast<size_t>(s) * 3] + sc.g_row[anchor];
-                f1 = sc.factors[static_cast<size_t>(s) * 3 + 1];
+                if (a.paux) {
+                    const uint4 x = a.paux[begin + j];
+                    add0 = __uint_as_float(x.x) + sc.g_row[x.z];
+                    f1 = __uint_as_float(x.y);
+                } else {
+                    const uint32_t anchor = sc.anchor_ids[s];
+                    add0 = sc.factors[static_cast<size_t>(s) * 3] + sc.g_row[anchor];
+                    f1 = sc.factors[static_cast<size_t>(s) * 3 + 1];
+                }
             }
             int pos = i;
             if (!score_first) {
@@ -469,6 +481,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
                 s_id[kp + pos] = ok ? s : UINT32_MAX;
                 s_d[kp + pos] = add0;
                 s_f1[pos] = f1;
+                s_prow[pos] = static_cast<uint32_t>(j);
             }
         }
         __syncthreads();
@@ -494,7 +507,8 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
                 const int i = i0 + u * kGroups;
                 sid[u] = i < n_rows ? s_id[kp + i] : UINT32_MAX;
                 if (sid[u] != UINT32_MAX) {
-                    const uint4* row = codes + static_cast<size_t>(sid[u]) * row_vecs;
+                    const uint4* row = a.pcodes ? a.pcodes + (begin + s_prow[i]) * row_vecs
+                                                : codes + static_cast<size_t>(sid[u]) * row_vecs;
 #pragma unroll
                     for (int w = 0; w < W; ++w) c[u][w] = row[lg + G * w];
                 }
@@ -649,6 +663,57 @@ __global__ __launch_bounds__(kScanThreads) void segment_merge_kernel(SegmentMerg
     if (tid == 0 && a.out_pass) a.out_pass[p] = passes;
 }
 
+// Posting-order copies of the RaBitQ rows: one thread per 16-byte vector
+// of a code row, and per aux record.
+__global__ __launch_bounds__(256) void posting_rows_kernel(const uint4* codes, const float* factors,
+                                                           const uint32_t* anchors,
+                                                           const uint32_t* posting, uint64_t rows,
+                                                           uint32_t vecs, uint32_t samples,
+                                                           uint4* out_codes, uint4* out_aux)
+{
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
+    const uint64_t total = rows * (vecs + 1u);
+    for (uint64_t t = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; t < total;
+         t += stride) {
+        const uint64_t r = t / (vecs + 1u);
+        const uint32_t v = static_cast<uint32_t>(t % (vecs + 1u));
+        const uint32_t s = posting[r];
+        const bool ok = s < samples;
+        if (v < vecs) {
+            out_codes[r * vecs + v] =
+                ok ? codes[static_cast<uint64_t>(s) * vecs + v] : make_uint4(0, 0, 0, 0);
+        } else {
+            out_aux[r] = ok ? make_uint4(__float_as_uint(factors[static_cast<uint64_t>(s) * 3]),
+                                         __float_as_uint(factors[static_cast<uint64_t>(s) * 3 + 1]),
+                                         anchors[s], 0u)
+                            : make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+int rabitq_posting_rows(Context* ctx, const gofann_rabitq_view* rq, const uint32_t* posting,
+                        uint64_t rows, uint8_t* out_codes, uint32_t* out_aux)
+{
+    if (!rq || !rq->codes || !rq->factors || !rq->anchor_ids || rq->padded_dim == 0 ||
+        rq->padded_dim % 128 != 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view invalid for posting rows");
+    if (rows == 0) return GOFANN_OK;
+    if (!posting || !out_codes || !out_aux)
+        return ctx->fail(GOFANN_ERR_INVALID, "posting rows arrays missing");
+    if ((reinterpret_cast<uintptr_t>(out_codes) | reinterpret_cast<uintptr_t>(out_aux) |
+         reinterpret_cast<uintptr_t>(rq->codes)) & 15u)
+        return ctx->fail(GOFANN_ERR_INVALID, "code and aux arrays must be 16-byte aligned");
+    const uint32_t vecs = rq->padded_dim / 128;
+    const uint64_t total = rows * (vecs + 1u);
+    const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((total + 255) / 256, 1u << 20));
+    hipLaunchKernelGGL(posting_rows_kernel, dim3(blocks), dim3(256), 0, ctx->stream,
+                       reinterpret_cast<const uint4*>(rq->codes), rq->factors, rq->anchor_ids,
+                       posting, rows, vecs, rq->samples, reinterpret_cast<uint4*>(out_codes),
+                       reinterpret_cast<uint4*>(out_aux));
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("posting rows launch");
+    return GOFANN_OK;
+}
+
 namespace {
 int pow2_at_least(int x)
 {
@@ -763,8 +828,10 @@ int rabitq_posting_scan_group(Context* ctx, const gofann_rabitq_view* rq,
     a.cand_offsets = cand_offsets;
     a.cand_sizes = cand_sizes;
     a.slices = slices;
+    a.pcodes = nullptr;
+    a.paux = nullptr;
     const size_t lds = 2 * static_cast<size_t>(a.planes_bytes) + static_cast<size_t>(a.slots) * 8 +
-                       static_cast<size_t>(a.chunk) * 8;
+                       static_cast<size_t>(a.chunk) * 12;
     if (lds > static_cast<size_t>(ctx->lds_per_block))
         return ctx->fail(GOFANN_ERR_UNSUPPORTED, "posting scan LDS exceeds the workgroup limit");
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -805,8 +872,11 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
                       const gofann_routes* routes, const uint32_t* posting,
                       uint64_t resident_rows, const gofann_posting_segments* seg,
                       int shortlist_k, int score_first, uint32_t* out_ids, float* out_dists,
-                      uint32_t* pass_counts)
+                      uint32_t* pass_counts, const uint8_t* posting_codes,
+                      const uint32_t* posting_aux)
 {
+    if ((posting_codes == nullptr) != (posting_aux == nullptr))
+        return ctx->fail(GOFANN_ERR_INVALID, "posting codes and aux come together");
     if (!rq || !pre || !rq->codes || !rq->factors || !rq->anchor_ids || rq->padded_dim == 0 ||
         rq->padded_dim % 128 != 0)
         return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view invalid for range scan");
@@ -866,6 +936,10 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
     a.cand_offsets = nullptr;
     a.cand_sizes = nullptr;
     a.slices = 1;
+    // The thread-per-row kernel gathers (same results); the group kernel
+    // streams the copies when given.
+    a.pcodes = reinterpret_cast<const uint4*>(posting_codes);
+    a.paux = reinterpret_cast<const uint4*>(posting_aux);
     if (a.chunk % kScanThreads != 0 || a.chunk / kScanThreads > 8 || a.slots < 2 * a.k_pow2 ||
         a.slots < a.k_pow2 + a.chunk)
         return ctx->fail(GOFANN_ERR_INVALID, "range scan chunk layout invalid");
@@ -882,7 +956,7 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
         // [0, 2 kp); then per chunk row f_rescale and the inner product.
         a.slots = std::max(2 * a.k_pow2, a.k_pow2 + a.chunk);
         lds = 2 * static_cast<size_t>(a.planes_bytes) + static_cast<size_t>(a.slots) * 8 +
-              static_cast<size_t>(a.chunk) * 8;
+              static_cast<size_t>(a.chunk) * 12;
     } else {
         kern = reinterpret_cast<const void*>(range_scan_kernel);
         lds = a.planes_bytes + static_cast<size_t>(a.slots) * 8;

@@ -136,6 +136,13 @@ SIGNATURES = {
                                            C.POINTER(PredicateView), C.POINTER(Routes), P,
                                            C.c_uint64, C.POINTER(PostingSegments), C.c_int,
                                            C.c_int, P, P, P]),
+    "gofann_rabitq_posting_rows": (C.c_int, [P, C.POINTER(RabitqView), P, C.c_uint64, P, P]),
+    "gofann_rabitq_range_scan_resident": (C.c_int, [P, C.POINTER(RabitqView),
+                                                    C.POINTER(RabitqQueries),
+                                                    C.POINTER(PredicateView), C.POINTER(Routes),
+                                                    P, C.c_uint64, P, P,
+                                                    C.POINTER(PostingSegments), C.c_int,
+                                                    C.c_int, P, P, P]),
     "gofann_exact_rerank": (C.c_int, [P, P, C.c_int, U32, U32, P, P, P, U32, U32, U32, P, P]),
     "gofann_merge_routes": (C.c_int, [P, P, P, P, P, U32, U32, U32, P, P]),
     "gofann_predicate_masks": (C.c_int, [P, C.POINTER(PredicateView), P, P, U32, P]),

@@ -266,18 +266,44 @@ def route_postings(index: RangePostingIndex, slices: np.ndarray):
     return offsets, sizes
 
 
+class PostingRows:
+    """Posting-order copies of the RaBitQ rows (gofann_rabitq_posting_rows):
+    codes [rows][padded_dim/8] and aux [rows][4] u32, so the range scan
+    streams them instead of gathering by sample id."""
+
+    def __init__(self, ctx: _lib.Context, rv: _lib.RabitqView, postings: torch.Tensor,
+                 rows: int):
+        self.rows = int(rows)
+        dev = postings.device
+        self.codes = torch.empty(max(self.rows, 1), rv.padded_dim // 8, dtype=torch.uint8,
+                                 device=dev)
+        self.aux = torch.empty(max(self.rows, 1), 4, dtype=torch.int32, device=dev)
+        ctx.check(ctx.lib.gofann_rabitq_posting_rows(ctx.handle, rv, _lib.ptr(postings),
+                                                      self.rows, _lib.ptr(self.codes),
+                                                      _lib.ptr(self.aux)))
+
+
 def rabitq_range_scan(ctx: _lib.Context, rv: _lib.RabitqView, rq: _lib.RabitqQueries,
                       pred: _lib.PredicateView, routes: _lib.Routes, postings: torch.Tensor,
                       resident_rows: int, segs: DeviceSegments, shortlist_k: int,
-                      score_first: bool = False):
-    """Runs gofann_rabitq_range_scan; returns (ids int32, dists, passes) on
-    the device, [rows][shortlist_k]."""
-    rows = segs.positions
-    ids = torch.empty(max(rows, 1) * shortlist_k, dtype=torch.int32, device=postings.device)
-    dists = torch.empty(max(rows, 1) * shortlist_k, dtype=torch.float32, device=postings.device)
-    passes = torch.empty(max(rows, 1), dtype=torch.int32, device=postings.device)
-    ctx.check(ctx.lib.gofann_rabitq_range_scan(
-        ctx.handle, rv, rq, pred, routes, _lib.ptr(postings), resident_rows, segs.view(),
-        shortlist_k, 1 if score_first else 0, _lib.ptr(ids), _lib.ptr(dists), _lib.ptr(passes)))
+                      score_first: bool = False, rows: PostingRows | None = None):
+    """Runs gofann_rabitq_range_scan (or, given posting-order `rows`,
+    gofann_rabitq_range_scan_resident); returns (ids int32, dists, passes)
+    on the device, [rows][shortlist_k]."""
+    n = segs.positions
+    ids = torch.empty(max(n, 1) * shortlist_k, dtype=torch.int32, device=postings.device)
+    dists = torch.empty(max(n, 1) * shortlist_k, dtype=torch.float32, device=postings.device)
+    passes = torch.empty(max(n, 1), dtype=torch.int32, device=postings.device)
+    if rows is None:
+        ctx.check(ctx.lib.gofann_rabitq_range_scan(
+            ctx.handle, rv, rq, pred, routes, _lib.ptr(postings), resident_rows, segs.view(),
+            shortlist_k, 1 if score_first else 0, _lib.ptr(ids), _lib.ptr(dists),
+            _lib.ptr(passes)))
+    else:
+        ctx.check(ctx.lib.gofann_rabitq_range_scan_resident(
+            ctx.handle, rv, rq, pred, routes, _lib.ptr(postings), resident_rows,
+            _lib.ptr(rows.codes), _lib.ptr(rows.aux), segs.view(), shortlist_k,
+            1 if score_first else 0, _lib.ptr(ids), _lib.ptr(dists), _lib.ptr(passes)))
+    rows = n
     return (ids[: rows * shortlist_k].view(rows, shortlist_k),
             dists[: rows * shortlist_k].view(rows, shortlist_k), passes[:rows])

@@ -355,6 +355,29 @@ int gofann_rabitq_range_scan(gofann_ctx* ctx, const gofann_rabitq_view* rq,
                              int shortlist_k, int score_first, uint32_t* out_ids,
                              float* out_dists, uint32_t* pass_counts);
 
+/* ---- posting-resident RaBitQ rows: no counterpart in the reference, whose
+ * range scan gathers every row by sample id (backend_rabitq.cu:5920-5960).
+ * A copy of each posting row's RaBitQ row in posting order lets the scan
+ * stream both arrays instead of gathering: codes [rows][padded_dim/8] and
+ * aux [rows][4] u32 = {f_add bits, f_rescale bits, anchor id, 0}.  Rows
+ * whose sample is >= rq->samples are zero.  gofann_rabitq_posting_rows
+ * fills them from rq (device gather); gofann_rabitq_range_scan_resident is
+ * gofann_rabitq_range_scan reading row r of every segment from the copies
+ * (the same results, bit for bit). */
+int gofann_rabitq_posting_rows(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                               const uint32_t* posting_sample_ids, uint64_t rows,
+                               uint8_t* out_codes, uint32_t* out_aux);
+
+int gofann_rabitq_range_scan_resident(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                                      const gofann_rabitq_queries* prepared,
+                                      const gofann_predicate_view* predicate,
+                                      const gofann_routes* routes,
+                                      const uint32_t* posting_sample_ids, uint64_t resident_rows,
+                                      const uint8_t* posting_codes, const uint32_t* posting_aux,
+                                      const gofann_posting_segments* segments, int shortlist_k,
+                                      int score_first, uint32_t* out_ids, float* out_dists,
+                                      uint32_t* pass_counts);
+
 /* ---- exact rerank on the GPU: per route, unique valid candidates of the
  * shortlist, exact L2 against base[samples][dim] (u8 / f32 / f16 with f32
  * queries for f32 and f16, u8 queries for u8), top-k by (distance, id). */

@@ -164,6 +164,58 @@ def test_range_scan_matches_oracle(gpu_ctx, rangeworld, k, segment_rows, score_f
     assert (oi[:, 0] != U32MAX).sum() > w["routes"] // 2      # most routes find candidates
 
 
+def test_posting_rows_copy(gpu_ctx, rangeworld):
+    """gofann_rabitq_posting_rows: row r is the code row and {f_add,
+    f_rescale, anchor} of posting sample r, zeros past the base rows."""
+    w = rangeworld
+    post = w["dev"]["postings"]
+    rows = int(post.shape[0])
+    pr = rp.PostingRows(gpu_ctx, w["rv"], post, rows)
+    torch.cuda.synchronize()
+    ps = post.cpu().numpy().view(np.uint32)
+    ok = ps < w["wl"].n
+    got_c = pr.codes.cpu().numpy()[:rows]
+    got_a = pr.aux.cpu().numpy().view(np.uint32)[:rows]
+    assert np.array_equal(got_c[ok], w["codes"][ps[ok]])
+    assert np.array_equal(got_a[ok, 0], w["fac"][ps[ok], 0].view(np.uint32))
+    assert np.array_equal(got_a[ok, 1], w["fac"][ps[ok], 1].view(np.uint32))
+    assert np.array_equal(got_a[ok, 2], w["aid"][ps[ok]])
+    assert not got_c[~ok].any() and not got_a[~ok].any()
+
+
+@pytest.mark.parametrize("k", [200, 4096])
+@pytest.mark.parametrize("segment_rows", [0, 700])
+@pytest.mark.parametrize("score_first,with_pred", [(False, False), (True, True)])
+def test_range_scan_resident_matches_oracle(gpu_ctx, rangeworld, k, segment_rows, score_first,
+                                            with_pred):
+    """The scan over posting-order copies returns the gathering scan's
+    results bit for bit (the oracle's)."""
+    w = rangeworld
+    say("resident range scan k", k, "segment_rows", segment_rows, "score_first", score_first)
+    routes = np.arange(w["routes"], dtype=np.uint32)
+    pred_o = (po.PredicateArrays.from_plan(w["rs"].predicate, w["li"], base_ranges=w["base_ranges"])
+              if with_pred else None)
+    pred_g = w["dr"].predicate_view(w["dg"], 0.0, False) if with_pred else _lib.PredicateView()
+    plan = rp.segment_plan(routes, w["offsets"], w["sizes"], segment_rows or (1 << 30))
+    if segment_rows:
+        si, sd, sp = _oracle(w, pred_o, plan.route_ids, plan.offsets, plan.sizes, k, score_first)
+        oi, od, op = po.merge_segments(plan.query_indptr, si, sd, sp, k)
+        segs = rp.DeviceSegments(plan, merged=True)
+    else:
+        oi, od, op = _oracle(w, pred_o, routes, w["offsets"], w["sizes"], k, score_first)
+        segs = rp.DeviceSegments(plan, merged=False)
+    post = w["dev"]["postings"]
+    rows = rp.PostingRows(gpu_ctx, w["rv"], post, w["index"].resident_rows)
+    ids, dists, passes = rp.rabitq_range_scan(gpu_ctx, w["rv"], w["rq"], pred_g, _routes_view(w),
+                                              post, w["index"].resident_rows, segs, k,
+                                              score_first, rows=rows)
+    torch.cuda.synchronize()
+    _explain(as_u32(ids), dists.cpu().numpy(), oi, od)
+    assert np.array_equal(as_u32(ids), oi)
+    assert np.array_equal(dists.cpu().numpy().view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(as_u32(passes), op)
+
+
 def test_range_scan_clips_resident_rows(gpu_ctx, rangeworld):
     w = rangeworld
     say("range scan resident clip")
