@@ -101,6 +101,37 @@ class PostingSegments(C.Structure):
                 ("query_indptr", P), ("positions", U32)]
 
 
+U64 = C.c_uint64
+CS = C.c_char_p
+
+
+class GraphFileHeader(C.Structure):
+    _fields_ = [("magic", U32), ("version", U32), ("block_size", U32), ("header_size", U32),
+                ("rows", U64), ("degree", U32), ("row_size_bytes", U32),
+                ("rows_per_block", U64)]
+
+
+class GraphMetadataHeader(C.Structure):
+    _fields_ = [("version", U32), ("reserved", U32)] + [
+        (n, U64) for n in ("label_count", "group_count", "original_label_count", "num_points",
+                           "row_limit", "graph_rows", "total_rows", "graph_degree",
+                           "specificity_threshold", "group_layout_checksum")]
+
+
+class GraphSeedHeader(C.Structure):
+    _fields_ = [("version", U32), ("reserved", U32)] + [
+        (n, U64) for n in ("label_count", "num_points", "graph_rows", "graph_degree",
+                           "specificity_threshold")]
+
+
+class RabitqFileHeader(C.Structure):
+    _fields_ = [("version", U32), ("dim", U32), ("num_anchors", U32), ("code_bytes", U32),
+                ("num_points", U64)] + [
+        (n, U32) for n in ("padded_dim", "bits_per_dim", "short_code_words",
+                           "long_code_bytes", "layout_flags", "short_factor_count",
+                           "ex_factor_count")]
+
+
 # Every symbol include/gofann_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "gofann_create": (C.c_int, [C.c_int, C.POINTER(P)]),
@@ -158,6 +189,33 @@ SIGNATURES = {
                                                C.POINTER(Routes), C.POINTER(SearchParams), P,
                                                U32, U32, P, P, P]),
     "gofann_host_merge_routes": (C.c_int, [P, P, P, P, U32, U32, U32, P, P]),
+    "gofann_io_last_error": (C.c_char_p, []),
+    "gofann_graph_file_has_magic": (C.c_int, [CS]),
+    "gofann_graph_file_read_header": (C.c_int, [CS, C.POINTER(GraphFileHeader)]),
+    "gofann_graph_file_read_rows": (C.c_int, [CS, U64, U64, P]),
+    "gofann_graph_file_write": (C.c_int, [CS, P, U64, U32]),
+    "gofann_graph_file_convert_legacy": (C.c_int, [CS, CS]),
+    "gofann_graph_metadata_read_header": (C.c_int, [CS, C.POINTER(GraphMetadataHeader)]),
+    "gofann_graph_metadata_read": (C.c_int, [CS, P, P, P, P, P, P, P]),
+    "gofann_graph_metadata_write": (C.c_int, [CS, C.POINTER(GraphMetadataHeader), P, P, P, P,
+                                              P, P, P]),
+    "gofann_group_layout_checksum": (U64, [P, P, U32, U32]),
+    "gofann_graph_seeds_read_header": (C.c_int, [CS, C.POINTER(GraphSeedHeader)]),
+    "gofann_graph_seeds_read": (C.c_int, [CS, P, P]),
+    "gofann_graph_seeds_write": (C.c_int, [CS, C.POINTER(GraphSeedHeader), P]),
+    "gofann_spmat_read_header": (C.c_int, [CS, C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
+    "gofann_spmat_read": (C.c_int, [CS, U32, P, P, U64, C.POINTER(U64)]),
+    "gofann_query_range_read_header": (C.c_int, [CS, U32, C.POINTER(U32), C.POINTER(U32)]),
+    "gofann_query_range_read": (C.c_int, [CS, U32, P, P, P]),
+    "gofann_rabitq_file_read_header": (C.c_int, [CS, C.POINTER(RabitqFileHeader)]),
+    "gofann_rabitq_file_read": (C.c_int, [CS, P, P, P, P, P, P, P, P]),
+    "gofann_rabitq_file_write": (C.c_int, [CS, C.POINTER(RabitqFileHeader), P, P, P, P, P, P, P,
+                                           P]),
+    "gofann_pq_pivots_read_header": (C.c_int, [CS, C.POINTER(U32), C.POINTER(U32)]),
+    "gofann_pq_pivots_read": (C.c_int, [CS, U32, P]),
+    "gofann_pq_codes_read_header": (C.c_int, [CS, C.POINTER(U64), C.POINTER(U32)]),
+    "gofann_pq_codes_read": (C.c_int, [CS, U64, U64, P, U32]),
+    "gofann_pq_files_write": (C.c_int, [CS, CS, P, U32, U32, P, U64]),
 }
 
 _lib = None

@@ -453,6 +453,175 @@ int gofann_host_merge_routes(const uint32_t* query_route_offsets, const uint32_t
                              const uint32_t* route_ids, const float* route_dists, uint32_t width,
                              uint32_t queries, uint32_t topk, uint32_t* out_ids, float* out_dists);
 
+/* ---- Reference artifacts on disk (host only).  Readers validate what the
+ * reference's loaders validate; each returns GOFANN_OK or a negative status
+ * with a message from gofann_io_last_error() (per host thread).  Outputs are
+ * caller-allocated host arrays sized from the matching *_read_header call;
+ * pinned buffers stream straight into device memory.  Output pointers noted
+ * "may be NULL" skip that array. */
+const char* gofann_io_last_error(void);
+
+/* FDRG graph file (src/index/graph_file_format.h:16-25): 4096-byte header
+ * block, rows of `degree` u32 packed 4096/(4*degree) to a 4096-byte block,
+ * block tails zero. */
+typedef struct {
+    uint32_t magic;          /* 0x47524446 "FDRG" */
+    uint32_t version;        /* 1 */
+    uint32_t block_size;     /* 4096 */
+    uint32_t header_size;    /* 4096 */
+    uint64_t rows;
+    uint32_t degree;
+    uint32_t row_size_bytes; /* 4 * degree */
+    uint64_t rows_per_block; /* 4096 / row_size_bytes */
+} gofann_graph_file_header;
+
+/* has_graph_file_magic (graph_file_format.cpp): 1 / 0, or a negative status
+ * when the file has no 4-byte marker. */
+int gofann_graph_file_has_magic(const char* path);
+/* read_graph_file_header (graph_file_format.cpp) with all of its checks. */
+int gofann_graph_file_read_header(const char* path, gofann_graph_file_header* out);
+/* Rows [row_begin, row_begin + row_count) as a row-major [row_count][degree]
+ * matrix (load_graph_file_as_contiguous_matrix over a window). */
+int gofann_graph_file_read_rows(const char* path, uint64_t row_begin, uint64_t row_count,
+                                uint32_t* out);
+/* GraphFileSequentialWriter (graph_file_format.h:40-55) over a whole
+ * [row_count][degree] matrix; byte-identical to the reference's file. */
+int gofann_graph_file_write(const char* path, const uint32_t* rows, uint64_t row_count,
+                            uint32_t degree);
+/* convert_legacy_graph_file (graph_file_format.cpp): u64 rows, u64 cols,
+ * then rows*cols u32 -> FDRG. */
+int gofann_graph_file_convert_legacy(const char* legacy_path, const char* path);
+
+/* Graph metadata sidecar (GraphMetadataSidecarHeader, src/data/
+ * dataloader.h:630-644; payload dataloader.cpp:7782-7821): the arrays a
+ * gofann_graph_view and gofann_routes take (label_offset, row_to_sample,
+ * row_filter_mask) with label_size, cat_freq and label_filter_bit. */
+typedef struct {
+    uint32_t version;  /* 1 */
+    uint32_t reserved;
+    uint64_t label_count;  /* groups */
+    uint64_t group_count;
+    uint64_t original_label_count;
+    uint64_t num_points;
+    uint64_t row_limit;
+    uint64_t graph_rows;
+    uint64_t total_rows;
+    uint64_t graph_degree;
+    uint64_t specificity_threshold;
+    uint64_t group_layout_checksum;
+} gofann_graph_metadata_header;
+
+int gofann_graph_metadata_read_header(const char* path, gofann_graph_metadata_header* out);
+/* [label_count] u32 x4, row_to_sample [total_rows] u32, row_filter_mask
+ * [total_rows] u64, label_filter_bit [original_label_count] u64; any output
+ * may be NULL.  Checks load_metadata_sidecar's vector rules
+ * (dataloader.cpp:7612-7690) that need no group layout. */
+int gofann_graph_metadata_read(const char* path, uint32_t* cat_freq, uint32_t* group_posting_size,
+                               uint32_t* label_size, uint32_t* label_offset,
+                               uint32_t* row_to_sample, uint64_t* row_filter_mask,
+                               uint64_t* label_filter_bit);
+/* save_metadata_sidecar (dataloader.cpp:7782-7821); row_filter_mask NULL
+ * writes all-ones (one label per group). */
+int gofann_graph_metadata_write(const char* path, const gofann_graph_metadata_header* header,
+                                const uint32_t* cat_freq, const uint32_t* group_posting_size,
+                                const uint32_t* label_size, const uint32_t* label_offset,
+                                const uint32_t* row_to_sample, const uint64_t* row_filter_mask,
+                                const uint64_t* label_filter_bit);
+/* group_layout_checksum (dataloader.cpp:320-332) of groups given as CSR
+ * (group_offsets [groups+1], group_labels); both NULL = one label per group. */
+uint64_t gofann_group_layout_checksum(const uint32_t* group_offsets, const uint32_t* group_labels,
+                                      uint32_t groups, uint32_t label_count);
+
+/* Seed sidecar (GraphSeedFileHeader, dataloader.h:609-617): label-local
+ * seed row per group, UINT32_MAX for an empty group. */
+typedef struct {
+    uint32_t version;  /* 2 */
+    uint32_t reserved;
+    uint64_t label_count;
+    uint64_t num_points;
+    uint64_t graph_rows;
+    uint64_t graph_degree;
+    uint64_t specificity_threshold;
+} gofann_graph_seed_header;
+
+int gofann_graph_seeds_read_header(const char* path, gofann_graph_seed_header* out);
+/* seeds [label_count]; label_size (may be NULL) enables load_seed_sidecar's
+ * per-label check (dataloader.cpp:7538-7550). */
+int gofann_graph_seeds_read(const char* path, const uint32_t* label_size, uint32_t* seeds);
+int gofann_graph_seeds_write(const char* path, const gofann_graph_seed_header* header,
+                             const uint32_t* seeds);
+
+/* .spmat label matrix (load_spmat_labels, dataloader.cpp:6663-6760): u64
+ * rows, cols, nnz, indptr [rows+1] u64, indices [nnz] u32. */
+int gofann_spmat_read_header(const char* path, uint64_t* rows, uint64_t* cols, uint64_t* nnz);
+/* First min(row_limit, rows) rows (row_limit 0 = all) as CSR with each row
+ * sorted and de-duplicated: indptr [rows'+1], indices capacity >= header
+ * nnz; *out_nnz receives the compacted count. */
+int gofann_spmat_read(const char* path, uint32_t row_limit, uint64_t* indptr, uint32_t* indices,
+                      uint64_t capacity, uint64_t* out_nnz);
+
+/* query_range.bin (load_query_range_binary, dataloader.cpp:6780-6880):
+ * u32 query_count, [u32 range_count], records {u8 mode, f32 upper, f32
+ * lower} packed (9 bytes) or aligned (12).  path NULL or "" = one zero range
+ * per query.  *record_bytes receives 9, 12 or 0 (no file). */
+int gofann_query_range_read_header(const char* path, uint32_t expected_queries,
+                                   uint32_t* range_count, uint32_t* record_bytes);
+/* modes/lower/upper [expected_queries][range_count]: the layout of
+ * gofann_routes' range table. */
+int gofann_query_range_read(const char* path, uint32_t expected_queries, uint8_t* modes,
+                            float* lower, float* upper);
+
+/* rabitq.b1.bin v2 (RabitqArtifactHeader + RabitqCodecSpec, backend_rabitq.
+ * cuh:16-32; arrays backend_rabitq.cu:2748-2845).  The rotation on disk is
+ * [padded_dim][padded_dim]; its first dim rows are the [dim][padded_dim]
+ * matrix gofann_rabitq_prepare_queries takes.  anchors, anchor_ids, codes
+ * and factors are gofann_rabitq_view's arrays as they lie. */
+typedef struct {
+    uint32_t version;  /* 2 */
+    uint32_t dim;
+    uint32_t num_anchors;
+    uint32_t code_bytes;  /* 4 * short_code_words */
+    uint64_t num_points;
+    uint32_t padded_dim;  /* multiple of 64, >= dim */
+    uint32_t bits_per_dim;
+    uint32_t short_code_words;
+    uint32_t long_code_bytes;
+    uint32_t layout_flags;  /* bits 0..2 set */
+    uint32_t short_factor_count;  /* 3 */
+    uint32_t ex_factor_count;     /* 2 */
+} gofann_rabitq_file_header;
+
+/* load_rabitq_index's header, codec and payload-size checks. */
+int gofann_rabitq_file_read_header(const char* path, gofann_rabitq_file_header* out);
+/* Arrays in file order; every output may be NULL (anchor ids are range
+ * checked either way). */
+int gofann_rabitq_file_read(const char* path, float* anchors, float* rotation,
+                            float* query_scaling_factors, uint32_t* anchor_ids, uint8_t* codes,
+                            uint8_t* long_codes, float* factors, float* ex_factors);
+/* save_rabitq_index; rotation, query_scaling_factors and ex_factors may be
+ * NULL (written as zeros). */
+int gofann_rabitq_file_write(const char* path, const gofann_rabitq_file_header* header,
+                             const float* anchors, const float* rotation,
+                             const float* query_scaling_factors, const uint32_t* anchor_ids,
+                             const uint8_t* codes, const uint8_t* long_codes, const float* factors,
+                             const float* ex_factors);
+
+/* DiskANN-style PQ files (writer tools/quantization/pq_builder.cu:110-122;
+ * loader load_pq_pivots_local / load_pq_index, backend_pq.cu:1716-1823). */
+int gofann_pq_pivots_read_header(const char* path, uint32_t* dim, uint32_t* pq_dim);
+/* centroids [256][dim] = centre + mean (one f32 add, as load_pq_index);
+ * pq_dim 0 accepts the file's.  Non-uniform chunk boundaries are
+ * GOFANN_ERR_UNSUPPORTED. */
+int gofann_pq_pivots_read(const char* path, uint32_t pq_dim, float* centroids);
+int gofann_pq_codes_read_header(const char* path, uint64_t* rows, uint32_t* pq_dim);
+/* Code rows [row_begin, row_begin + row_count); out_stride 0 = pq_dim, or
+ * the byte stride of wider per-sample records (gofann_pq_view.code_stride). */
+int gofann_pq_codes_read(const char* path, uint64_t row_begin, uint64_t row_count, uint8_t* out,
+                         uint32_t out_stride);
+/* Both files, with a zero mean and uniform boundaries, as pq_builder. */
+int gofann_pq_files_write(const char* pivots_path, const char* codes_path, const float* centroids,
+                          uint32_t dim, uint32_t pq_dim, const uint8_t* codes, uint64_t rows);
+
 #ifdef __cplusplus
 }
 #endif

@@ -380,6 +380,65 @@ def ref_range_slices(path, modes, lower, upper):
     return out[:n], rows.value
 
 
+def _ref_graph_fn(name, argtypes):
+    R = ref()
+    if R is None or not hasattr(R, name):
+        return None
+    fn = getattr(R, name)
+    fn.argtypes = argtypes
+    return fn
+
+
+def ref_graph_file_header(path):
+    """read_graph_file_header -> 40 header bytes, or (None, message)."""
+    fn = _ref_graph_fn("ref_graph_file_header", [C.c_char_p, P, C.c_char_p, U32])
+    if fn is None:
+        return None
+    out = np.zeros(40, np.uint8)
+    err = C.create_string_buffer(512)
+    if fn(str(path).encode(), p(out), err, U32(512)) != 0:
+        return None, err.value.decode()
+    return out.tobytes()
+
+
+def ref_graph_file_load(path, capacity_words):
+    """load_graph_file_as_contiguous_matrix -> [rows][cols] u32, or (None, message)."""
+    fn = _ref_graph_fn("ref_graph_file_load",
+                       [C.c_char_p, P, C.c_uint64, P, P, C.c_char_p, U32])
+    if fn is None:
+        return None
+    out = np.zeros(max(capacity_words, 1), np.uint32)
+    rows, cols = C.c_uint64(0), C.c_uint64(0)
+    err = C.create_string_buffer(512)
+    code = fn(str(path).encode(), p(out), C.c_uint64(capacity_words), C.byref(rows),
+              C.byref(cols), err, U32(512))
+    if code != 0:
+        return None, err.value.decode() if code == -1 else "capacity"
+    return out[: rows.value * cols.value].reshape(rows.value, cols.value)
+
+
+def ref_graph_file_write(path, rows, chunk=7):
+    """GraphFileSequentialWriter, rows appended `chunk` at a time -> True or message."""
+    fn = _ref_graph_fn("ref_graph_file_write",
+                       [C.c_char_p, P, C.c_uint64, U32, C.c_uint64, C.c_char_p, U32])
+    if fn is None:
+        return None
+    rows = np.ascontiguousarray(rows, np.uint32)
+    err = C.create_string_buffer(512)
+    code = fn(str(path).encode(), p(rows), C.c_uint64(rows.shape[0]), U32(rows.shape[1]),
+              C.c_uint64(chunk), err, U32(512))
+    return True if code == 0 else err.value.decode()
+
+
+def ref_graph_file_convert_legacy(legacy_path, path):
+    fn = _ref_graph_fn("ref_graph_file_convert_legacy", [C.c_char_p, C.c_char_p, C.c_char_p, U32])
+    if fn is None:
+        return None
+    err = C.create_string_buffer(512)
+    code = fn(str(legacy_path).encode(), str(path).encode(), err, U32(512))
+    return True if code == 0 else err.value.decode()
+
+
 def rabitq_range_scan(pred, modes, lower, upper, base_values, codes, factors, anchor_ids, q8,
                       q_scale, q_k1, centroid_dists, route_query, posting, resident_rows,
                       base_rows, seg_routes, seg_offsets, seg_sizes, k, score_first=False):

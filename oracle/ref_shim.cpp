@@ -12,6 +12,7 @@
 //   src/data/fp16_l2.h                       (decode, scalar L2)
 //   src/execution/posting_segment_plan.h     (posting segment plan)
 //   src/index/range_posting_index.{h,cpp}    (FARPIDX1 loader, smallest slice)
+//   src/index/graph_file_format.{h,cpp}      (FDRG graph file reader/writer)
 #include "predicates/gpu_predicate_index.cuh"
 #include "predicates/range_filter.cuh"
 #include "search/common/posting_shortlist_heap.cuh"
@@ -20,6 +21,7 @@
 #include "data/fp16_l2.h"
 #include "execution/posting_segment_plan.h"
 #include "index/range_posting_index.h"
+#include "index/graph_file_format.h"
 
 #include <cstdint>
 #include <cstring>
@@ -252,6 +254,74 @@ int ref_range_slices(const char* path, const uint8_t* modes, const float* lower,
             error[error_bytes - 1] = 0;
         }
         return -1;
+    }
+}
+
+namespace {
+int ref_error(const std::exception& e, char* error, uint32_t error_bytes)
+{
+    if (error && error_bytes) {
+        std::strncpy(error, e.what(), error_bytes - 1);
+        error[error_bytes - 1] = 0;
+    }
+    return -1;
+}
+}  // namespace
+
+// FDRG: the header as read_graph_file_header returns it (40 bytes).
+int ref_graph_file_header(const char* path, void* out, char* error, uint32_t error_bytes)
+{
+    try {
+        const go_fann::graph_file::GraphFileHeader h = go_fann::graph_file::read_graph_file_header(path);
+        std::memcpy(out, &h, sizeof(h));
+        return 0;
+    } catch (const std::exception& e) {
+        return ref_error(e, error, error_bytes);
+    }
+}
+
+// FDRG: load_graph_file_as_contiguous_matrix into out (capacity words);
+// *rows/*cols receive the shape.
+int ref_graph_file_load(const char* path, uint32_t* out, uint64_t capacity, uint64_t* rows,
+                        uint64_t* cols, char* error, uint32_t error_bytes)
+{
+    try {
+        const auto m = go_fann::graph_file::load_graph_file_as_contiguous_matrix(path);
+        *rows = m.rows;
+        *cols = m.cols;
+        if (m.data.size() > capacity) return -2;
+        if (!m.data.empty()) std::memcpy(out, m.data.data(), m.data.size() * sizeof(uint32_t));
+        return 0;
+    } catch (const std::exception& e) {
+        return ref_error(e, error, error_bytes);
+    }
+}
+
+// FDRG: GraphFileSequentialWriter, rows appended in chunks of `chunk`.
+int ref_graph_file_write(const char* path, const uint32_t* rows, uint64_t row_count, uint32_t degree,
+                         uint64_t chunk, char* error, uint32_t error_bytes)
+{
+    try {
+        go_fann::graph_file::GraphFileSequentialWriter w(path, row_count, degree);
+        for (uint64_t r = 0; r < row_count; r += chunk) {
+            const uint64_t n = row_count - r < chunk ? row_count - r : chunk;
+            w.append_rows(rows + r * degree, n);
+        }
+        w.close();
+        return 0;
+    } catch (const std::exception& e) {
+        return ref_error(e, error, error_bytes);
+    }
+}
+
+int ref_graph_file_convert_legacy(const char* legacy_path, const char* path, char* error,
+                                  uint32_t error_bytes)
+{
+    try {
+        go_fann::graph_file::convert_legacy_graph_file(legacy_path, path);
+        return 0;
+    } catch (const std::exception& e) {
+        return ref_error(e, error, error_bytes);
     }
 }
 

@@ -1,0 +1,444 @@
+"""Reference artifacts on disk (CPU): the library's readers and writers
+against files laid out byte by byte here from the reference's format
+definitions, and -- for the FDRG graph file -- against the reference's own
+reader/writer (src/index/graph_file_format.cpp compiled under oracle/_ref).
+
+Formats: FDRG graph.bin (graph_file_format.h:16-25), metadata and seed
+sidecars (dataloader.h:609-644, dataloader.cpp:7503-7821), .spmat
+(dataloader.cpp:6663-6760), query_range.bin (:6780-6880), rabitq.b1.bin v2
+(backend_rabitq.cu:2748-2845), DiskANN PQ pivots/codes (pq_builder.cu:
+110-122, backend_pq.cu:1716-1823)."""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from gofann_amd import artifacts as ga
+from gofann_amd import index as gi
+from gofann_amd import synth
+
+U32MAX = 0xFFFFFFFF
+
+
+# ------------------------------------------------------------------ FDRG
+def _fdrg_bytes(rows: np.ndarray) -> bytes:
+    """The FDRG file of a [rows][degree] matrix, laid out from the format's
+    definition: 40-byte header zero-padded to 4096, then 4096-byte blocks of
+    floor(4096 / (4 degree)) rows each, block tails zero."""
+    n, d = rows.shape
+    rpb = 4096 // (4 * d)
+    head = struct.pack("<IIIIQIIQ", 0x47524446, 1, 4096, 4096, n, d, 4 * d, rpb)
+    out = bytearray(head + bytes(4096 - len(head)))
+    for b in range(0, n, rpb):
+        blk = rows[b:b + rpb].astype("<u4").tobytes()
+        out += blk + bytes(4096 - len(blk))
+    return bytes(out)
+
+
+def _rows(n, d, seed=0):
+    return np.random.default_rng(seed).integers(0, U32MAX, size=(n, d), dtype=np.uint32)
+
+
+@pytest.mark.parametrize("degree", [1, 3, 16, 24, 64, 100, 1024])
+@pytest.mark.parametrize("nrows", [0, 1, 5, 41, 42, 43, 300])
+def test_graph_file_write_matches_layout_and_reference(tmp_path, degree, nrows):
+    g = _rows(nrows, degree, seed=degree * 1000 + nrows)
+    ours = tmp_path / "ours.bin"
+    ga.write_graph(ours, g)
+    assert ours.read_bytes() == _fdrg_bytes(g)
+    ref_path = tmp_path / "ref.bin"
+    wrote = po.ref_graph_file_write(ref_path, g)
+    if wrote is not None:          # oracle/_ref built: byte-identical files
+        assert wrote is True
+        assert ref_path.read_bytes() == ours.read_bytes()
+        loaded = po.ref_graph_file_load(ours, g.size)
+        assert np.array_equal(loaded, g)
+    assert np.array_equal(ga.read_graph(ours), g)
+    h = ga.graph_file_header(ours)
+    assert (h["rows"], h["degree"], h["rows_per_block"]) == (nrows, degree, 4096 // (4 * degree))
+    assert ga.is_graph_file(ours)
+
+
+@pytest.mark.parametrize("degree", [3, 32, 100])
+def test_graph_file_row_windows(tmp_path, degree):
+    g = _rows(1000, degree, seed=degree)
+    path = tmp_path / "g.bin"
+    path.write_bytes(_fdrg_bytes(g))
+    rng = np.random.default_rng(1)
+    for _ in range(20):
+        b = int(rng.integers(0, 1000))
+        c = int(rng.integers(0, 1000 - b + 1))
+        assert np.array_equal(ga.read_graph(path, b, c), g[b:b + c])
+    with pytest.raises(ga.ArtifactError, match="row window"):
+        ga.read_graph(path, 990, 11)
+
+
+def _patch(src: bytes, off: int, fmt: str, value) -> bytes:
+    b = bytearray(src)
+    struct.pack_into(fmt, b, off, value)
+    return bytes(b)
+
+
+@pytest.mark.parametrize("case,off,fmt,value,msg", [
+    ("magic", 0, "<I", 0x12345678, "invalid magic"),
+    ("version", 4, "<I", 2, "unsupported graph file version"),
+    ("block", 8, "<I", 8192, "unexpected block/header size"),
+    ("degree0", 24, "<I", 0, "degree must be > 0"),
+    ("rowsize", 28, "<I", 36, "row_size_bytes does not match degree"),
+    ("rpb", 32, "<Q", 7, "rows_per_block is invalid"),
+])
+def test_graph_file_rejects_what_the_reference_rejects(tmp_path, case, off, fmt, value, msg):
+    good = _fdrg_bytes(_rows(50, 8))
+    path = tmp_path / f"{case}.bin"
+    path.write_bytes(_patch(good, off, fmt, value))
+    with pytest.raises(ga.ArtifactError, match=msg):
+        ga.read_graph(path)
+    ref = po.ref_graph_file_header(path)
+    if ref is not None:
+        assert ref[0] is None and msg in ref[1]
+
+
+def test_graph_file_truncated_block(tmp_path):
+    good = _fdrg_bytes(_rows(300, 8))           # 128 rows per block, 3 blocks
+    path = tmp_path / "t.bin"
+    path.write_bytes(good[:-100])
+    assert np.array_equal(ga.read_graph(path, 0, 256), _rows(300, 8)[:256])
+    with pytest.raises(ga.ArtifactError, match="failed reading graph file block"):
+        ga.read_graph(path)
+    ref = po.ref_graph_file_load(path, 300 * 8)
+    if ref is not None:
+        assert ref[0] is None and "failed reading graph file block" in ref[1]
+
+
+@pytest.mark.parametrize("degree,nrows", [(24, 100), (64, 129), (1, 0)])
+def test_graph_file_convert_legacy(tmp_path, degree, nrows):
+    g = _rows(nrows, degree, seed=3)
+    legacy = tmp_path / "legacy.bin"
+    legacy.write_bytes(struct.pack("<QQ", nrows, degree) + g.tobytes())
+    ga.convert_legacy_graph(legacy, tmp_path / "ours.bin")
+    assert (tmp_path / "ours.bin").read_bytes() == _fdrg_bytes(g)
+    ok = po.ref_graph_file_convert_legacy(legacy, tmp_path / "ref.bin")
+    if ok is not None:
+        assert ok is True
+        assert (tmp_path / "ref.bin").read_bytes() == (tmp_path / "ours.bin").read_bytes()
+    legacy.write_bytes(struct.pack("<QQ", 2, 2000) + bytes(16000))
+    with pytest.raises(ga.ArtifactError, match="degree too large"):
+        ga.convert_legacy_graph(legacy, tmp_path / "x.bin")
+
+
+# -------------------------------------------------------------- sidecars
+# The reference's offset basis (dataloader.cpp:55) is 1469598103934665603,
+# one decimal digit short of FNV's published 14695981039346656037; files
+# it wrote carry checksums under its own constant, so that one is used.
+REF_FNV_BASIS = 1469598103934665603
+FNV_BASIS = 14695981039346656037
+
+
+def _fnv1a(data: bytes, basis: int) -> int:
+    h = basis
+    for byte in data:
+        h ^= byte
+        h = (h * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def _fnv1a_words(words, basis=REF_FNV_BASIS) -> int:
+    """FNV-1a 64 over the little-endian bytes of u64 words."""
+    return _fnv1a(b"".join(struct.pack("<Q", w) for w in words), basis)
+
+
+def test_fnv1a_restatement_pinned():
+    # Published FNV-1a 64 vectors pin the mixing step: "" and "a".
+    assert FNV_BASIS == 0xcbf29ce484222325
+    assert _fnv1a(b"", FNV_BASIS) == FNV_BASIS and _fnv1a(b"a", FNV_BASIS) == 0xaf63dc4c8601ec8c
+
+
+def test_group_layout_checksum():
+    # groups [[0], [1], [2]] over 3 labels, and a grouped layout [[0, 2], [1]]
+    assert ga.group_layout_checksum(3) == _fnv1a_words([3, 3, 1, 0, 1, 1, 1, 2])
+    assert ga.group_layout_checksum(3, [0, 2, 3], [0, 2, 1]) == _fnv1a_words([2, 3, 2, 0, 2, 1, 1])
+
+
+@pytest.fixture(scope="module")
+def small_index():
+    wl = synth.small_labelled(n=3000, nq=4, dim=16, k=8, labels=6, seed=11)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=8, threshold=300)
+    return wl, li
+
+
+def test_label_index_round_trip(tmp_path, small_index):
+    wl, li = small_index
+    paths = [tmp_path / f for f in ("graph.bin", "meta.bin", "seeds.bin", "labels.spmat")]
+    ga.save_label_index(li, *paths)
+    # metadata sidecar bytes, laid out from GraphMetadataSidecarHeader
+    L, R, n = li.num_labels, li.rows, 3000
+    head = struct.pack("<II10Q", 1, 0, L, L, L, n, n, R, R, li.degree, li.threshold,
+                       _fnv1a_words([L, L] + sum(([1, g] for g in range(L)), [])))
+    body = b"".join(np.asarray(a, "<u4").tobytes() for a in
+                    (li.cat_freq, li.cat_freq, li.label_size, li.label_offset, li.row_to_sample))
+    body += np.full(R, U32MAX | (U32MAX << 32), "<u8").tobytes() + np.ones(L, "<u8").tobytes()
+    assert paths[1].read_bytes() == head + body
+    seeds_bytes = struct.pack("<II5Q", 2, 0, L, n, R, li.degree, li.threshold)
+    assert paths[2].read_bytes() == seeds_bytes + np.asarray(li.seed_local, "<u4").tobytes()
+    back = ga.load_label_index(*paths)
+    for f in ("cat_freq", "label_offset", "label_size", "row_to_sample", "graph", "seed_local",
+              "posting_offset", "posting_ids", "csr_offsets", "csr_labels"):
+        assert np.array_equal(np.asarray(getattr(back, f)), np.asarray(getattr(li, f))), f
+    assert (back.num_labels, back.threshold, back.degree) == (li.num_labels, li.threshold, li.degree)
+
+
+def _meta_file(tmp_path, small_index, mutate):
+    _, li = small_index
+    paths = [tmp_path / f for f in ("graph.bin", "meta.bin", "seeds.bin")]
+    ga.save_label_index(li, *paths)
+    b = bytearray(paths[1].read_bytes())
+    mutate(b, li)
+    paths[1].write_bytes(bytes(b))
+    return paths[1]
+
+
+@pytest.mark.parametrize("name,msg", [
+    ("version", "unsupported metadata sidecar version"),
+    ("offset", "label_offset is not contiguous"),
+    ("catfreq", "cat_freq/group_posting_size mismatch"),
+    ("sample", "row_to_sample exceeds num_points"),
+    ("short", "ended"),
+])
+def test_metadata_sidecar_rejects(tmp_path, small_index, name, msg):
+    L = small_index[1].num_labels
+
+    def mutate(b, li):
+        base = 88
+        if name == "version":
+            struct.pack_into("<I", b, 0, 2)
+        elif name == "offset":
+            g = int(np.flatnonzero(li.label_size)[-1])
+            struct.pack_into("<I", b, base + 12 * L + 4 * g, li.label_offset[g] + 1)
+        elif name == "catfreq":
+            struct.pack_into("<I", b, base, li.cat_freq[0] + 1)
+        elif name == "sample":
+            struct.pack_into("<I", b, base + 16 * L, 3000)
+        else:
+            del b[len(b) - 4:]
+    path = _meta_file(tmp_path, small_index, mutate)
+    with pytest.raises(ga.ArtifactError, match=msg):
+        ga.read_metadata(path)
+
+
+def test_seed_sidecar_checks_seeds(tmp_path, small_index):
+    _, li = small_index
+    hdr = struct.pack("<II5Q", 2, 0, 3, 100, 10, 8, 300)
+    path = tmp_path / "s.bin"
+    path.write_bytes(hdr + np.array([4, U32MAX, 0], "<u4").tobytes())
+    _, seeds = ga.read_seeds(path, np.array([5, 0, 5], np.uint32))
+    assert seeds.tolist() == [4, U32MAX, 0]
+    for bad in ([5, U32MAX, 0], [4, 0, 0], [4, U32MAX, U32MAX]):
+        path.write_bytes(hdr + np.array(bad, "<u4").tobytes())
+        with pytest.raises(ga.ArtifactError, match="seed"):
+            ga.read_seeds(path, np.array([5, 0, 5], np.uint32))
+
+
+# ----------------------------------------------------------------- spmat
+def test_spmat_sorts_dedupes_and_limits(tmp_path):
+    rows = [[3, 1, 3, 0], [], [2, 2, 2], [4, 0], [1]]
+    indptr = np.cumsum([0] + [len(r) for r in rows]).astype(np.uint64)
+    path = tmp_path / "l.spmat"
+    ga.write_spmat(path, indptr, np.array(sum(rows, []), np.uint32), 5)
+    raw = path.read_bytes()
+    assert raw[:24] == struct.pack("<QQQ", 5, 5, 10)
+    for limit in (0, 2, 4, 5, 9):
+        ip, ix, cols = ga.read_spmat(path, limit)
+        eff = len(rows) if limit == 0 or limit >= len(rows) else limit
+        want = [sorted(set(r)) for r in rows[:eff]]
+        assert cols == 5 and len(ip) == eff + 1
+        assert [ix[ip[i]:ip[i + 1]].tolist() for i in range(eff)] == want
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda b: struct.pack_into("<Q", b, 24, 1), "must start at 0"),
+    (lambda b: struct.pack_into("<Q", b, 40, 1), "not monotonic"),
+    (lambda b: struct.pack_into("<Q", b, 48, 99), "exceeds nnz"),
+    (lambda b: struct.pack_into("<I", b, 24 + 32, 7), "out of range"),
+])
+def test_spmat_rejects(tmp_path, mutate, msg):
+    path = tmp_path / "l.spmat"
+    ga.write_spmat(path, np.array([0, 2, 3, 4], np.uint64), np.array([1, 0, 2, 1], np.uint32), 3)
+    b = bytearray(path.read_bytes())
+    mutate(b)
+    path.write_bytes(bytes(b))
+    with pytest.raises(ga.ArtifactError, match=msg):
+        ga.read_spmat(path)
+
+
+# ------------------------------------------------------------ query ranges
+def _records(modes, upper, lower, aligned):
+    out = b""
+    for m, u, lo in zip(modes, upper, lower):
+        out += struct.pack("<B3xff" if aligned else "<Bff", m, u, lo)
+    return out
+
+
+@pytest.mark.parametrize("aligned", [False, True])
+@pytest.mark.parametrize("rc", [None, 1, 3])
+def test_query_range_layouts(tmp_path, aligned, rc):
+    q = 7
+    r = rc or 1
+    rng = np.random.default_rng(r + 10 * aligned)
+    modes = rng.integers(0, 4, size=q * r).astype(np.uint8)
+    lower = rng.normal(size=q * r).astype(np.float32)
+    upper = (lower + 1).astype(np.float32)
+    head = struct.pack("<I", q) + (b"" if rc is None else struct.pack("<I", rc))
+    path = tmp_path / "query_range.bin"
+    path.write_bytes(head + _records(modes, upper, lower, aligned))
+    m, lo, up = ga.read_query_ranges(path, q)
+    assert m.shape == (q, r)
+    assert np.array_equal(m.ravel(), modes) and np.array_equal(lo.ravel(), lower)
+    assert np.array_equal(up.ravel(), upper)
+
+
+def test_query_range_defaults_and_errors(tmp_path):
+    m, lo, up = ga.read_query_ranges(None, 4)
+    assert m.shape == (4, 1) and not m.any() and not lo.any() and not up.any()
+    path = tmp_path / "q.bin"
+    path.write_bytes(struct.pack("<I", 3) + _records([1, 2, 3], [1, 2, 3], [0, 0, 0], False))
+    with pytest.raises(ga.ArtifactError, match="does not match query vector rows"):
+        ga.read_query_ranges(path, 4)
+    path.write_bytes(struct.pack("<I", 3) + bytes(10))
+    with pytest.raises(ga.ArtifactError, match="packed/aligned"):
+        ga.read_query_ranges(path, 3)
+
+
+# ------------------------------------------------------------------ RaBitQ
+@pytest.fixture(scope="module")
+def rabitq_parts():
+    torch.manual_seed(0)
+    dim, P, A, n = 40, 64, 4, 500
+    x = torch.randn(n, dim)
+    rot = gi.random_rotation(dim, P, seed=3, device="cpu")
+    cen = torch.randn(A, dim)
+    codes, factors, aid, anchors = gi.rabitq_encode(x, rot, cen)
+    return dict(dim=dim, P=P, A=A, n=n, rotation=rot.numpy(), codes=codes.numpy(),
+                factors=factors.numpy(), anchor_ids=aid.numpy().astype(np.uint32),
+                anchors=anchors.numpy())
+
+
+def _rabitq_bytes(t, ex=None, qs=None):
+    n, P, A = t["n"], t["P"], t["A"]
+    rot = np.zeros((P, P), np.float32)
+    rot[: t["dim"]] = t["rotation"]
+    arrays = [t["anchors"], rot, np.zeros(2, np.float32) if qs is None else qs,
+              t["anchor_ids"], t["codes"], np.zeros(0, np.uint8), t["factors"],
+              np.zeros((n, 2), np.float32) if ex is None else ex]
+    out = struct.pack("<IIIIQ", 2, t["dim"], A, P // 8, n)
+    out += struct.pack("<7I", P, 1, P // 32, 0, 7, 3, 2)
+    for a in arrays:
+        a = np.ascontiguousarray(a)
+        out += struct.pack("<Q", a.size) + a.tobytes()
+    return out
+
+
+def test_rabitq_artifact_round_trip(tmp_path, rabitq_parts):
+    t = rabitq_parts
+    path = tmp_path / "rabitq.b1.bin"
+    ga.write_rabitq(path, t["dim"], t["anchors"], t["anchor_ids"], t["codes"], t["factors"],
+                    rotation=t["rotation"])
+    assert path.read_bytes() == _rabitq_bytes(t)
+    ex = np.random.default_rng(0).normal(size=(t["n"], 2)).astype(np.float32)
+    qs = np.array([0.5, 2.0], np.float32)
+    path.write_bytes(_rabitq_bytes(t, ex, qs))
+    got = ga.read_rabitq(path)
+    assert (got["num_points"], got["padded_dim"], got["code_bytes"]) == (t["n"], t["P"], t["P"] // 8)
+    for k in ("anchors", "codes", "factors", "anchor_ids"):
+        assert np.array_equal(got[k], t[k]), k
+    assert np.array_equal(got["rotation"][: t["dim"]], t["rotation"])
+    assert not got["rotation"][t["dim"]:].any()
+    assert np.array_equal(got["ex_factors"], ex) and np.array_equal(got["query_scaling_factors"], qs)
+
+
+@pytest.mark.parametrize("off,fmt,value,msg", [
+    (0, "<I", 1, "unsupported artifact version"),
+    (4, "<I", 0, "zero-sized"),
+    (24, "<I", 96, "padded_dim is invalid"),
+    (28, "<I", 10, "bits_per_dim is invalid"),
+    (32, "<I", 3, "short_code_words is invalid"),
+    (40, "<I", 3, "layout_flags"),
+    (48, "<I", 1, "factor counts"),
+    (12, "<I", 12, "code_bytes does not match"),
+    (52, "<Q", 255, "payload sizes do not match"),
+])
+def test_rabitq_artifact_rejects(tmp_path, rabitq_parts, off, fmt, value, msg):
+    path = tmp_path / "r.bin"
+    path.write_bytes(_patch(_rabitq_bytes(rabitq_parts), off, fmt, value))
+    with pytest.raises(ga.ArtifactError, match=msg):
+        ga.read_rabitq(path)
+
+
+def test_rabitq_artifact_rejects_anchor_id(tmp_path, rabitq_parts):
+    t = dict(rabitq_parts)
+    t["anchor_ids"] = t["anchor_ids"].copy()
+    t["anchor_ids"][17] = t["A"]
+    path = tmp_path / "r.bin"
+    path.write_bytes(_rabitq_bytes(t))
+    with pytest.raises(ga.ArtifactError, match="out-of-range anchor id"):
+        ga.read_rabitq(path)
+
+
+# ---------------------------------------------------------------------- PQ
+def _pivots_bytes(table, mean, bounds, five=False):
+    """DiskANN pivot file: offset table, then bin matrices at those offsets."""
+    D = table.shape[1]
+    mats = [(256, D, table.astype("<f4").tobytes()), (D, 1, mean.astype("<f4").tobytes()),
+            (len(bounds), 1, np.asarray(bounds, "<u4").tobytes())]
+    if five:
+        mats.insert(2, (1, 1, struct.pack("<f", 0.0)))
+    nr = 5 if five else 4
+    first = 8 + nr * 8
+    offs, pos, body = [], first, b""
+    for r, c, data in mats:
+        offs.append(pos)
+        body += struct.pack("<ii", r, c) + data
+        pos += 8 + len(data)
+    offs += [pos] * (nr - len(offs))
+    return struct.pack("<ii", nr, 1) + struct.pack(f"<{nr}Q", *offs) + body
+
+
+def test_pq_files_round_trip_and_layout(tmp_path):
+    rng = np.random.default_rng(5)
+    D, M, n = 48, 12, 300
+    cent = rng.normal(size=(256, D)).astype(np.float32)
+    codes = rng.integers(0, 256, size=(n, M), dtype=np.uint8)
+    pv, cd = tmp_path / "pivots.bin", tmp_path / "codes.bin"
+    ga.write_pq(pv, cd, cent, codes)
+    bounds = [i * (D // M) for i in range(M + 1)]
+    assert pv.read_bytes() == _pivots_bytes(cent, np.zeros(D, np.float32), bounds)
+    assert cd.read_bytes() == struct.pack("<ii", n, M) + codes.tobytes()
+    c2, k2 = ga.read_pq(pv, cd, M)
+    assert np.array_equal(c2, cent + np.float32(0)) and np.array_equal(k2, codes)
+    _, win = ga.read_pq(pv, cd, M, row_begin=100, row_count=50, code_stride=64)
+    assert np.array_equal(win[:, :M], codes[100:150]) and not win[:, M:].any()
+
+
+@pytest.mark.parametrize("five", [False, True])
+def test_pq_pivots_add_mean(tmp_path, five):
+    rng = np.random.default_rng(6)
+    D, M = 32, 8
+    table = rng.normal(size=(256, D)).astype(np.float32)
+    mean = rng.normal(size=D).astype(np.float32)
+    pv = tmp_path / "p.bin"
+    pv.write_bytes(_pivots_bytes(table, mean, [i * 4 for i in range(M + 1)], five))
+    cent = np.empty((256, D), np.float32)
+    got, _ = None, None
+    (tmp_path / "c.bin").write_bytes(struct.pack("<ii", 0, M))
+    got, _ = ga.read_pq(pv, tmp_path / "c.bin", M)
+    np.add(table, mean[None, :], out=cent)     # one f32 add per entry
+    assert np.array_equal(got, cent)
+    with pytest.raises(ga.ArtifactError, match="chunk offsets shape"):
+        ga.read_pq(pv, tmp_path / "c.bin", M + 1)
+    pv.write_bytes(_pivots_bytes(table, mean, [0, 3] + [4 + i * 4 for i in range(1, M)], five))
+    with pytest.raises(ga.ArtifactError, match="not uniform"):
+        ga.read_pq(pv, tmp_path / "c.bin", M)
