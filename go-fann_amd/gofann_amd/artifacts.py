@@ -160,6 +160,70 @@ def read_query_ranges(path, queries: int) -> tuple[np.ndarray, np.ndarray, np.nd
     return modes, lower, upper
 
 
+# ----------------------------------------------------------- dense vectors
+_VECS = {".bvecs": np.uint8, ".fvecs": np.float32, ".hvecs": np.float16}
+
+
+def read_vectors(path, row_limit: int = 0) -> np.ndarray:
+    """A dense vector file as a read-only [rows][dim] memory map
+    (inspect_dense_vector_file and its loaders, dataloader.cpp:1321-1480):
+    .u8bin/.ibin u32 rows, u32 cols, u8 rows; .fbin the same with f32 rows
+    and an exact file size; .bvecs/.fvecs/.hvecs one u32 dim before every row
+    (u8 / f32 / f16).  row_limit > 0 keeps the first rows."""
+    path = os.fspath(path)
+    ext = os.path.splitext(path)[1].lower()
+    size = os.path.getsize(path)
+    if ext in (".u8bin", ".ibin", ".fbin"):
+        rows, cols = (int(v) for v in np.fromfile(path, np.uint32, 2))
+        dt = np.float32 if ext == ".fbin" else np.uint8
+        if cols == 0 or (ext == ".fbin" and rows == 0):
+            raise ArtifactError(f"invalid vector header in {path}")
+        if ext == ".fbin" and size != 8 + rows * cols * 4:
+            raise ArtifactError(f"fbin file size does not match header in {path}")
+        if size < 8 + rows * cols * np.dtype(dt).itemsize:
+            raise ArtifactError(f"failed to read payload from {path}")
+        keep = rows if row_limit <= 0 or row_limit >= rows else row_limit
+        return np.memmap(path, dt, "r", offset=8, shape=(keep, cols))
+    if ext in _VECS:
+        dt = np.dtype(_VECS[ext])
+        dim = int(np.fromfile(path, np.uint32, 1)[0]) if size >= 4 else 0
+        if dim == 0:
+            raise ArtifactError(f"invalid {ext} dimension in {path}")
+        rec = 4 + dim * dt.itemsize
+        if size % rec:
+            raise ArtifactError(f"{ext} file size is not row-aligned for {path}")
+        rows = size // rec
+        keep = rows if row_limit <= 0 or row_limit >= rows else row_limit
+        raw = np.memmap(path, np.uint8, "r", shape=(rows, rec))[:keep]
+        dims = np.ascontiguousarray(raw[:, :4]).view(np.uint32).ravel()
+        bad = np.flatnonzero(dims != dim)
+        if bad.size:
+            raise ArtifactError(f"inconsistent {ext} dimension at row {int(bad[0])} in {path}")
+        return np.ascontiguousarray(raw[:, 4:]).view(dt)
+    raise ArtifactError(f"unsupported dense vector extension for {path} "
+                        "(supported: .bvecs, .ibin, .u8bin, .fbin, .fvecs, .hvecs)")
+
+
+def write_vectors(path, x: np.ndarray) -> None:
+    """The inverse of read_vectors for the extension of `path`."""
+    path = os.fspath(path)
+    ext = os.path.splitext(path)[1].lower()
+    x = np.ascontiguousarray(x)
+    n, d = x.shape
+    with open(path, "wb") as f:
+        if ext in (".u8bin", ".ibin", ".fbin"):
+            dt = np.float32 if ext == ".fbin" else np.uint8
+            f.write(np.array([n, d], np.uint32).tobytes())
+            f.write(x.astype(dt).tobytes())
+        elif ext in _VECS:
+            rec = np.empty((n, 4 + d * np.dtype(_VECS[ext]).itemsize), np.uint8)
+            rec[:, :4] = np.frombuffer(np.uint32(d).tobytes(), np.uint8)
+            rec[:, 4:] = x.astype(_VECS[ext]).view(np.uint8).reshape(n, -1)
+            f.write(rec.tobytes())
+        else:
+            raise ArtifactError(f"unsupported dense vector extension for {path}")
+
+
 # ------------------------------------------------------------------ RaBitQ
 RABITQ_ARRAYS = ("anchors", "rotation", "query_scaling_factors", "anchor_ids", "codes",
                  "long_codes", "factors", "ex_factors")
@@ -290,3 +354,60 @@ def load_label_index(graph_path, metadata_path, seeds_path, spmat_path) -> Label
                       label_size=md.label_size, row_to_sample=md.row_to_sample, graph=g,
                       seed_local=seeds, posting_offset=posting_offset, posting_ids=posting_ids,
                       csr_offsets=csr_offsets, csr_labels=indices, degree=int(g.shape[1]))
+
+
+# ------------------------------------------------------- streamed to HBM
+def graph_to_device(path, device, chunk_rows: int = 1 << 20):
+    """The whole graph file as a [rows][degree] int32 device tensor (u32 bit
+    patterns), read in windows of chunk_rows rows into two pinned staging
+    buffers that alternate, so a file larger than host memory never needs a
+    host copy and the disk read of one window overlaps the copy of the last."""
+    import torch
+    h = graph_file_header(path)
+    rows, degree = h["rows"], h["degree"]
+    out = torch.empty((rows, degree), dtype=torch.int32, device=device)
+    if rows == 0:
+        return out
+    chunk = max(1, min(chunk_rows, rows))
+    stage = [torch.empty((chunk, degree), dtype=torch.int32, pin_memory=True) for _ in range(2)]
+    done = [None, None]
+    for i, r in enumerate(range(0, rows, chunk)):
+        c = min(chunk, rows - r)
+        s = stage[i % 2]
+        if done[i % 2] is not None:
+            done[i % 2].synchronize()       # the copy out of this buffer has finished
+        view = s.numpy().view(np.uint32)
+        _call("gofann_graph_file_read_rows", _b(path), r, c, _p(view))
+        out[r:r + c].copy_(s[:c], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        done[i % 2] = ev
+    torch.cuda.synchronize(device)
+    return out
+
+
+def pq_codes_to_device(path, device, code_stride: int = 0, chunk_rows: int = 1 << 22):
+    """DiskANN code file as a [rows][stride or pq_dim] uint8 device tensor,
+    streamed as graph_to_device."""
+    import torch
+    rows, m = C.c_uint64(), C.c_uint32()
+    _call("gofann_pq_codes_read_header", _b(path), C.byref(rows), C.byref(m))
+    n, width = rows.value, code_stride or m.value
+    out = torch.zeros((n, width), dtype=torch.uint8, device=device)
+    if n == 0:
+        return out
+    chunk = max(1, min(chunk_rows, n))
+    stage = [torch.zeros((chunk, width), dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+    done = [None, None]
+    for i, r in enumerate(range(0, n, chunk)):
+        c = min(chunk, n - r)
+        s = stage[i % 2]
+        if done[i % 2] is not None:
+            done[i % 2].synchronize()
+        _call("gofann_pq_codes_read", _b(path), r, c, _p(s.numpy()), code_stride)
+        out[r:r + c].copy_(s[:c], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        done[i % 2] = ev
+    torch.cuda.synchronize(device)
+    return out

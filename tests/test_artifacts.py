@@ -442,3 +442,35 @@ def test_pq_pivots_add_mean(tmp_path, five):
     pv.write_bytes(_pivots_bytes(table, mean, [0, 3] + [4 + i * 4 for i in range(1, M)], five))
     with pytest.raises(ga.ArtifactError, match="not uniform"):
         ga.read_pq(pv, tmp_path / "c.bin", M)
+
+
+# ----------------------------------------------------------- dense vectors
+@pytest.mark.parametrize("ext,dt", [(".u8bin", np.uint8), (".ibin", np.uint8),
+                                    (".fbin", np.float32), (".bvecs", np.uint8),
+                                    (".fvecs", np.float32), (".hvecs", np.float16)])
+def test_dense_vector_files(tmp_path, ext, dt):
+    rng = np.random.default_rng(4)
+    x = (rng.integers(0, 256, size=(37, 12)) if dt == np.uint8 else rng.normal(size=(37, 12))).astype(dt)
+    path = tmp_path / f"base{ext}"
+    ga.write_vectors(path, x)
+    raw = path.read_bytes()
+    if ext in (".u8bin", ".ibin", ".fbin"):          # u32 rows, u32 cols, rows
+        assert raw == struct.pack("<II", 37, 12) + x.tobytes()
+    else:                                            # u32 dim before every row
+        assert raw == b"".join(struct.pack("<I", 12) + r.tobytes() for r in x)
+    assert np.array_equal(ga.read_vectors(path), x)
+    assert np.array_equal(ga.read_vectors(path, row_limit=5), x[:5])
+    if ext == ".fbin":
+        path.write_bytes(raw + b"\0")
+        with pytest.raises(ga.ArtifactError, match="does not match header"):
+            ga.read_vectors(path)
+    if ext in (".bvecs", ".fvecs", ".hvecs"):
+        b = bytearray(raw)
+        rec = 4 + 12 * np.dtype(dt).itemsize
+        struct.pack_into("<I", b, 3 * rec, 11)
+        path.write_bytes(bytes(b))
+        with pytest.raises(ga.ArtifactError, match="inconsistent .* dimension at row 3"):
+            ga.read_vectors(path)
+        path.write_bytes(raw[:-1])
+        with pytest.raises(ga.ArtifactError, match="not row-aligned"):
+            ga.read_vectors(path)
