@@ -159,3 +159,208 @@ def filter_mask(index, labels: list, ranges: list, base_ranges) -> np.ndarray:
         elif mode == 3:
             mask &= (v >= lo) & (v < hi)
     return mask
+
+
+# ---------------------------------------------------------------------------
+# Pure-range cover over interval labels (range label manifest)
+# ---------------------------------------------------------------------------
+@dataclass
+class RangeLabelIntervals:
+    """Per-label interval metadata of a range label manifest
+    (RangeLabelIntervals, src/data/dataloader.h:555-563)."""
+    range_count: int
+    has_interval: np.ndarray   # [labels] u8
+    lower: np.ndarray          # [labels] f32
+    upper: np.ndarray          # [labels] f32
+    level: np.ndarray          # [labels] u32 (UINT32_MAX: none)
+    bin: np.ndarray            # [labels] u32
+    range_index: np.ndarray    # [labels] u32
+
+
+def load_range_label_manifest(path, label_count: int) -> RangeLabelIntervals:
+    """load_range_label_manifest (dataloader.cpp:6883-7001): JSON with either
+    "ranges": [{range_index, levels: [{level_index, partitions: [{label_id,
+    interval: [lo, hi], bin_index}]}]}] or a flat "levels" array whose
+    partitions carry range_index (default 0)."""
+    import json
+    U = 0xFFFFFFFF
+    iv = RangeLabelIntervals(1, np.zeros(label_count, np.uint8), np.zeros(label_count, np.float32),
+                             np.zeros(label_count, np.float32), np.full(label_count, U, np.uint32),
+                             np.full(label_count, U, np.uint32), np.full(label_count, U, np.uint32))
+    if not path:
+        return iv
+    with open(path) as f:
+        root = json.load(f)
+    if not isinstance(root, dict):
+        raise ValueError("range label manifest root must be an object")
+
+    def note(r):
+        if r != U:
+            iv.range_count = max(iv.range_count, r + 1)
+
+    def partitions(levels, range_index):
+        for level in levels:
+            if not isinstance(level, dict) or not isinstance(level.get("partitions"), list):
+                continue
+            li = level.get("level_index", U)
+            for part in level["partitions"]:
+                if not isinstance(part, dict):
+                    continue
+                lab = part.get("label_id", U)
+                if lab >= label_count:
+                    raise ValueError("range label manifest label_id out of range")
+                pair = part.get("interval")
+                if not isinstance(pair, list) or len(pair) != 2:
+                    raise ValueError("range label manifest partition missing interval pair")
+                r = range_index if range_index is not None else part.get("range_index", 0)
+                if range_index is None:
+                    note(r)
+                iv.has_interval[lab] = 1
+                iv.lower[lab], iv.upper[lab] = pair
+                iv.level[lab], iv.bin[lab] = li, part.get("bin_index", U)
+                iv.range_index[lab] = r
+
+    if "ranges" in root:
+        if not isinstance(root["ranges"], list):
+            raise ValueError("range label manifest ranges field must be an array")
+        for pos, entry in enumerate(root["ranges"]):
+            if not isinstance(entry, dict):
+                continue
+            r = entry.get("range_index", pos)
+            note(r)
+            if isinstance(entry.get("levels"), list):
+                partitions(entry["levels"], r)
+        return iv
+    if not isinstance(root.get("levels"), list):
+        raise ValueError("range label manifest missing levels/ranges array")
+    partitions(root["levels"], None)
+    return iv
+
+
+def coarsen_range_cover_bins(child_active: np.ndarray, parent_active: np.ndarray,
+                             parent_labels: np.ndarray) -> None:
+    """In place: a parent bin whose children are all active (and that has a
+    label) becomes active and its children inactive (coarsen_range_cover_bins,
+    dataloader.cpp:9104-9130).  Child counts are an integer multiple of the
+    parent count."""
+    if (len(parent_active) == 0 or len(parent_active) != len(parent_labels)
+            or len(child_active) % len(parent_active)):
+        raise ValueError("range hierarchy levels must have dense integer-multiple bin counts")
+    per = len(child_active) // len(parent_active)
+    for p in range(len(parent_active)):
+        kids = child_active[p * per:(p + 1) * per]
+        if kids.all() and parent_labels[p] != 0xFFFFFFFF:
+            kids[:] = 0
+            parent_active[p] = 1
+
+
+@dataclass
+class RangeCoverLayout:
+    """Labels, lower and upper bounds of every (level, bin) of one range
+    dimension (build_range_cover_layout, dataloader.cpp:9141-9202)."""
+    domain_low: float
+    domain_high: float
+    labels: list      # [level] -> u32 array by bin (UINT32_MAX: missing)
+    lowers: list
+    uppers: list
+
+
+def build_range_cover_layout(iv: RangeLabelIntervals, range_index: int,
+                             usable: np.ndarray | None = None) -> RangeCoverLayout:
+    """`usable[label]`: the label has a graph or a posting list
+    (range_route_label_usable, dataloader.cpp:7872-7898); default all."""
+    U = 0xFFFFFFFF
+    mine = (iv.has_interval != 0) & (iv.range_index == range_index)
+    if not mine.any():
+        raise ValueError("pure-range query requires range_label_manifest_path with valid intervals")
+    lo = float(np.min(iv.lower[mine]))
+    hi = float(np.max(iv.upper[mine]))
+    if not (np.isfinite(lo) and np.isfinite(hi) and lo < hi):
+        raise ValueError("pure-range query requires range_label_manifest_path with valid intervals")
+    use = mine & (iv.level != U) & (iv.bin != U)
+    if usable is not None:
+        use &= np.asarray(usable, bool)
+    if not use.any():
+        raise ValueError("pure-range query requires usable range labels in manifest")
+    top = int(iv.level[use].max())
+    labels = [np.zeros(0, np.uint32) for _ in range(top + 1)]
+    lowers = [np.zeros(0, np.float32) for _ in range(top + 1)]
+    uppers = [np.zeros(0, np.float32) for _ in range(top + 1)]
+    for lab in np.flatnonzero(use):
+        lv, b = int(iv.level[lab]), int(iv.bin[lab])
+        if len(labels[lv]) <= b:
+            grow = b + 1 - len(labels[lv])
+            labels[lv] = np.concatenate([labels[lv], np.full(grow, U, np.uint32)])
+            lowers[lv] = np.concatenate([lowers[lv], np.zeros(grow, np.float32)])
+            uppers[lv] = np.concatenate([uppers[lv], np.zeros(grow, np.float32)])
+        labels[lv][b] = lab
+        lowers[lv][b] = iv.lower[lab]
+        uppers[lv][b] = iv.upper[lab]
+    return RangeCoverLayout(lo, hi, labels, lowers, uppers)
+
+
+def _overlap(a_lo, a_hi, b_lo, b_hi) -> bool:
+    # intervals_overlap (dataloader.cpp:7866-7870), in float32 as the reference
+    eps = np.float32(1e-6)
+    return bool(np.float32(a_hi) > np.float32(b_lo) + eps and np.float32(a_lo) < np.float32(b_hi) - eps)
+
+
+def plan_pure_range_cover(layout: RangeCoverLayout, mode: int, lower: float, upper: float,
+                          finest_only: bool = False) -> list:
+    """Interval labels whose routes cover a query range (plan_pure_range_cover_labels,
+    dataloader.cpp:9204-9345): the finest bins overlapping the target, bins
+    coarsened into parents whose children are all selected (unless
+    finest_only), then a gap-checked walk in (lower, upper, level, bin)
+    order.  mode 0 = inactive (no labels); 1 lower bound, 2 upper, 3 both."""
+    if mode == 0:
+        return []
+    f32 = np.float32
+    lo, hi = f32(layout.domain_low), f32(layout.domain_high)
+    if mode in (1, 3):
+        lo = max(lo, f32(lower))
+    if mode in (2, 3):
+        hi = min(hi, f32(upper))
+    if not lo < hi:
+        return []
+    top = len(layout.labels) - 1
+    if len(layout.labels[top]) == 0:
+        raise ValueError("pure-range query has no usable finest-level range labels")
+    active = [np.zeros(len(l), np.uint8) for l in layout.labels]
+    for b, lab in enumerate(layout.labels[top]):
+        if lab != 0xFFFFFFFF and _overlap(layout.lowers[top][b], layout.uppers[top][b], lo, hi):
+            active[top][b] = 1
+    if not active[top].any():
+        raise ValueError("unable to construct pure-range cover")
+    if not finest_only:
+        for lv in range(top, 0, -1):
+            if len(active[lv]) and len(layout.labels[lv - 1]):
+                coarsen_range_cover_bins(active[lv], active[lv - 1], layout.labels[lv - 1])
+    nodes = []
+    for lv in range(top + 1):
+        for b in np.flatnonzero(active[lv]):
+            lab = layout.labels[lv][b]
+            if lab == 0xFFFFFFFF:
+                raise ValueError("pure-range planner selected missing label")
+            nodes.append((f32(layout.lowers[lv][b]), f32(layout.uppers[lv][b]), lv, int(b), int(lab)))
+    eps = f32(1e-6)
+
+    def key_cmp(x, y):
+        if abs(x[0] - y[0]) > eps:
+            return -1 if x[0] < y[0] else 1
+        if abs(x[1] - y[1]) > eps:
+            return -1 if x[1] < y[1] else 1
+        return -1 if (x[2], x[3]) < (y[2], y[3]) else (1 if (x[2], x[3]) > (y[2], y[3]) else 0)
+
+    import functools
+    nodes.sort(key=functools.cmp_to_key(key_cmp))
+    out, covered = [], lo
+    for nlo, nhi, _, _, lab in nodes:
+        if nhi <= covered + eps:
+            continue
+        if nlo > covered + eps:
+            raise ValueError("canonical pure-range cover leaves a gap")
+        covered = max(covered, nhi)
+        out.append(lab)
+    if covered < hi - eps:
+        raise ValueError("canonical pure-range cover did not reach target interval")
+    return out
