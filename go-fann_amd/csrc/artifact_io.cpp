@@ -238,6 +238,10 @@ int rabitq_validate(const gofann_rabitq_file_header& h, const char* path)
         return io_fail(GOFANN_ERR_INVALID, "artifact codec factor counts are invalid in " + p(path));
     if (h.code_bytes != h.short_code_words * 4u)
         return io_fail(GOFANN_ERR_INVALID, "artifact header code_bytes does not match dim in " + p(path));
+    // Bounds that keep every array's byte count inside 64 bits (2^40 points
+    // of at most 2^16 bytes per array row).
+    if (h.padded_dim > (1u << 16) || h.num_points > (1ull << 40))
+        return io_fail(GOFANN_ERR_INVALID, "artifact header sizes are out of range in " + p(path));
     return GOFANN_OK;
 }
 
@@ -769,6 +773,8 @@ int gofann_rabitq_file_read(const char* path, float* anchors, float* rotation, f
     for (int a = 0; a < kRabitqArrays; ++a) {
         uint64_t n = 0;
         if (!in.read(&n, 8)) return io_fail(GOFANN_ERR_INVALID, "failed to read artifact payload from " + p(path));
+        // the outputs are sized from the header: the file must still agree
+        if (n != count[a]) return io_fail(GOFANN_ERR_INVALID, "artifact payload sizes do not match header in " + p(path));
         if (a == 3) {
             // anchor ids are checked whether or not the caller wants them.
             std::vector<uint32_t> chunk(std::min<uint64_t>(n, 1u << 20));

@@ -370,6 +370,7 @@ def test_rabitq_artifact_round_trip(tmp_path, rabitq_parts):
     (48, "<I", 1, "factor counts"),
     (12, "<I", 12, "code_bytes does not match"),
     (52, "<Q", 255, "payload sizes do not match"),
+    (16, "<Q", (1 << 40) + 1, "sizes are out of range"),
 ])
 def test_rabitq_artifact_rejects(tmp_path, rabitq_parts, off, fmt, value, msg):
     path = tmp_path / "r.bin"
