@@ -768,6 +768,8 @@ int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, ui
         return ctx->fail(GOFANN_ERR_INVALID, "hash_mode in [0, 3]");
     if (!g->graph || !g->row_to_sample || !g->label_offset || g->degree == 0)
         return ctx->fail(GOFANN_ERR_INVALID, "graph view incomplete");
+    if (g->degree > static_cast<uint32_t>(kMaxDegree))
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "graph degree must be in [1, 64]");
     if (r->count == 0) return GOFANN_OK;
     if (!r->route_query || !r->route_group || !r->route_start || !out_ids || !out_dists)
         return ctx->fail(GOFANN_ERR_INVALID, "route arrays or outputs missing");

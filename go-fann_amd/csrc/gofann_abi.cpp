@@ -103,6 +103,12 @@ const char* gofann_last_error(const gofann_ctx* c)
 int gofann_set_stream(gofann_ctx* c, void* stream)
 {
     return guarded(c, [&](Context* ctx) {
+        // Work queued on the previous stream may still read the context's
+        // scratch buffers, which later calls (on the new stream) may free
+        // when they grow; drain it before switching.
+        if (ctx->stream != static_cast<hipStream_t>(stream) &&
+            hipStreamSynchronize(ctx->stream) != hipSuccess)
+            return ctx->fail_hip("set_stream: synchronize the previous stream");
         ctx->stream = static_cast<hipStream_t>(stream);
         return GOFANN_OK;
     });

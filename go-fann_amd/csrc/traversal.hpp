@@ -1139,6 +1139,11 @@ inline int check_params(Context* ctx, const gofann_graph_view* g, const gofann_r
         return ctx->fail(GOFANN_ERR_INVALID, "table_mode in [0, 2], hash_mode in [0, 3]");
     if (!g->graph || !g->row_to_sample || !g->label_offset || g->degree == 0)
         return ctx->fail(GOFANN_ERR_INVALID, "graph view incomplete");
+    // validate_pq_search_options rejects degree > FIXED_DEGREE
+    // (backend_pq.cu:11486-11488); reading only a row prefix would change
+    // results silently.
+    if (g->degree > static_cast<uint32_t>(kMaxDegree))
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "graph degree must be in [1, 64]");
     if (r->count > 0 && (!r->route_query || !r->route_group || !r->route_start))
         return ctx->fail(GOFANN_ERR_INVALID, "route arrays missing");
     return GOFANN_OK;

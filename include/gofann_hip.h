@@ -85,7 +85,8 @@ typedef struct {
     const uint32_t* row_to_sample;  /* [rows] */
     const uint32_t* label_offset;   /* [groups] */
     uint32_t rows;
-    uint32_t degree;                /* row stride; at most 64 are read */
+    uint32_t degree;                /* row stride, in [1, 64]; a larger degree is
+                                       GOFANN_ERR_UNSUPPORTED (backend_pq.cu:11486) */
     uint32_t groups;
     uint32_t samples;
     /* Optional [rows][degree] sample id of each adjacency entry
