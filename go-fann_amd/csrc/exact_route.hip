@@ -28,11 +28,47 @@
 
 #include <cfloat>
 #include <cstdint>
+#include <mutex>
+#include <string>
 
 #include "device_common.hpp"
 #include "gofann_internal.hpp"
 
+// Visited-set slabs of gofann_exact_search_noalloc: a fixed device array in
+// place of context scratch, for callers that cannot allocate.  Each GPU the
+// library runs on holds its own copy until the process ends.  Host code never
+// passes this name to a kernel (on the host it is only a stand-in for the
+// symbol); it uses the per-device address that hipGetSymbolAddress returned.
+static __device__ __align__(256) uint32_t scratch[GOFANN_EXACT_NOALLOC_MAX_ROUTES * 4096u];
+
 namespace gofann {
+
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mutex;
+uint32_t* g_noalloc_slab[kNoAllocMaxDevices] = {};
+std::string g_noalloc_error[kNoAllocMaxDevices];
+}  // namespace
+
+// Looks up this device's copy of `scratch` once (gofann_create calls it with
+// the context's device current).  A failure is kept and reported by the
+// no-alloc entry point; the other entry points do not need the array.
+void noalloc_setup(int device)
+{
+    if (device < 0 || device >= kNoAllocMaxDevices) return;
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    if (g_noalloc_slab[device] != nullptr) return;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+        (void)hipGetLastError();
+        g_noalloc_error[device] = std::string("hipGetSymbolAddress(scratch): ") +
+                                  hipGetErrorString(e);
+        return;
+    }
+    g_noalloc_slab[device] = static_cast<uint32_t*>(p);
+    g_noalloc_error[device].clear();
+}
 
 constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 
@@ -696,9 +732,12 @@ int resident(Context* ctx, uint32_t lds)
 // Visited-set placement with the most resident routes per CU (ties: the
 // full LDS table, then the spilling table, then the global slab), then the
 // launch.
+// fixed_slab: visited slabs for a placement outside LDS, holding at most
+// fixed_routes routes (the no-alloc entry point); nullptr: context scratch.
 template <int kC, bool kReg>
 int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
-                 uint32_t lds_spill, uint32_t lds_glob, uint32_t count)
+                 uint32_t lds_spill, uint32_t lds_glob, uint32_t count, uint32_t* fixed_slab,
+                 uint32_t fixed_routes)
 {
     const int rf = resident<kVisitedLds, kC, kReg>(ctx, lds_full);
     const int rs = resident<kVisitedSpill, kC, kReg>(ctx, lds_spill);
@@ -724,7 +763,15 @@ int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
     if (res <= 0)
         return ctx->fail(GOFANN_ERR_UNSUPPORTED, "per-route LDS state exceeds the workgroup limit");
     a.hash_global = nullptr;
-    if (mode != kVisitedLds) {
+    if (mode != kVisitedLds && fixed_slab != nullptr) {
+        if (count > fixed_routes)
+            return ctx->fail(GOFANN_ERR_INVALID,
+                             "no-alloc exact search: " + std::to_string(count) +
+                                 " routes need visited slabs beyond the fixed scratch (at most " +
+                                 std::to_string(fixed_routes) +
+                                 " routes per call with a visited set outside LDS)");
+        a.hash_global = fixed_slab;
+    } else if (mode != kVisitedLds) {
         const size_t need = static_cast<size_t>(count) * kHashCapacity * sizeof(uint32_t);
         a.hash_global = static_cast<uint32_t*>(ctx->scratch(Context::kScratchHash, need));
         if (!a.hash_global) return ctx->fail(GOFANN_ERR_NOMEM, "visited set scratch");
@@ -746,11 +793,12 @@ int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
 }
 
 
-int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
-                 const void* queries, const gofann_graph_view* g, const uint32_t* label_size,
-                 const gofann_predicate_view* pred, const gofann_routes* r,
-                 const gofann_exact_params* p, uint32_t* out_ids, float* out_dists,
-                 gofann_route_stats* stats)
+static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint32_t dim,
+                             uint32_t samples, const void* queries, const gofann_graph_view* g,
+                             const uint32_t* label_size, const gofann_predicate_view* pred,
+                             const gofann_routes* r, const gofann_exact_params* p,
+                             uint32_t* out_ids, float* out_dists, gofann_route_stats* stats,
+                             uint32_t* fixed_slab, uint32_t fixed_routes)
 {
     if (!g || !r || !p) return ctx->fail(GOFANN_ERR_INVALID, "null view");
     if (base_elem != GOFANN_ELEM_U8)
@@ -806,18 +854,59 @@ int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, ui
     const uint32_t n = r->count;
     if (reg) {
         switch (chunks) {
-        case 8: return launch_exact<8, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
-        case 12: return launch_exact<12, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
-        case 16: return launch_exact<16, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
-        default: return launch_exact<0, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+        case 8: return launch_exact<8, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
+        case 12: return launch_exact<12, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
+        case 16: return launch_exact<16, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
+        default: return launch_exact<0, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
         }
     }
     switch (chunks) {
-    case 8: return launch_exact<8, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
-    case 12: return launch_exact<12, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
-    case 16: return launch_exact<16, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
-    default: return launch_exact<0, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n);
+    case 8: return launch_exact<8, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
+    case 12: return launch_exact<12, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
+    case 16: return launch_exact<16, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
+    default: return launch_exact<0, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
+                                                 fixed_routes);
     }
+}
+
+int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
+                 const void* queries, const gofann_graph_view* g, const uint32_t* label_size,
+                 const gofann_predicate_view* pred, const gofann_routes* r,
+                 const gofann_exact_params* p, uint32_t* out_ids, float* out_dists,
+                 gofann_route_stats* stats)
+{
+    return exact_search_impl(ctx, base, base_elem, dim, samples, queries, g, label_size, pred, r,
+                             p, out_ids, out_dists, stats, nullptr, 0);
+}
+
+int exact_search_noalloc(Context* ctx, const void* base, int base_elem, uint32_t dim,
+                         uint32_t samples, const void* queries, const gofann_graph_view* g,
+                         const uint32_t* label_size, const gofann_predicate_view* pred,
+                         const gofann_routes* r, const gofann_exact_params* p,
+                         uint32_t* out_ids, float* out_dists, gofann_route_stats* stats)
+{
+    uint32_t* slab = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+        if (ctx->device >= 0 && ctx->device < kNoAllocMaxDevices)
+            slab = g_noalloc_slab[ctx->device];
+        if (slab == nullptr)
+            return ctx->fail(GOFANN_ERR_HIP,
+                             "no-alloc scratch unavailable on this device" +
+                                 (ctx->device >= 0 && ctx->device < kNoAllocMaxDevices &&
+                                          !g_noalloc_error[ctx->device].empty()
+                                      ? ": " + g_noalloc_error[ctx->device]
+                                      : std::string()));
+    }
+    return exact_search_impl(ctx, base, base_elem, dim, samples, queries, g, label_size, pred, r,
+                             p, out_ids, out_dists, stats, slab, GOFANN_EXACT_NOALLOC_MAX_ROUTES);
 }
 
 }  // namespace gofann

@@ -78,6 +78,7 @@ int gofann_create(int device, gofann_ctx** out)
         per_cu <= 0)
         per_cu = ctx->lds_per_block;
     ctx->lds_per_cu = per_cu;
+    gofann::noalloc_setup(device);
     *out = reinterpret_cast<gofann_ctx*>(ctx);
     return GOFANN_OK;
 }
@@ -222,6 +223,20 @@ int gofann_exact_search(gofann_ctx* c, const void* base, int base_elem, uint32_t
         return gofann::exact_search(ctx, base, base_elem, dim, samples, queries, graph,
                                     label_size, predicate, routes, params, out_ids, out_dists,
                                     stats);
+    });
+}
+
+int gofann_exact_search_noalloc(gofann_ctx* c, const void* base, int base_elem, uint32_t dim,
+                                uint32_t samples, const void* queries,
+                                const gofann_graph_view* graph, const uint32_t* label_size,
+                                const gofann_predicate_view* predicate,
+                                const gofann_routes* routes, const gofann_exact_params* params,
+                                uint32_t* out_ids, float* out_dists, gofann_route_stats* stats)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::exact_search_noalloc(ctx, base, base_elem, dim, samples, queries, graph,
+                                            label_size, predicate, routes, params, out_ids,
+                                            out_dists, stats);
     });
 }
 

@@ -109,6 +109,14 @@ int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, ui
                  const gofann_predicate_view* pred, const gofann_routes* r,
                  const gofann_exact_params* p, uint32_t* out_ids, float* out_dists,
                  gofann_route_stats* stats);
+int exact_search_noalloc(Context* ctx, const void* base, int base_elem, uint32_t dim,
+                         uint32_t samples, const void* queries, const gofann_graph_view* g,
+                         const uint32_t* label_size, const gofann_predicate_view* pred,
+                         const gofann_routes* r, const gofann_exact_params* p,
+                         uint32_t* out_ids, float* out_dists, gofann_route_stats* stats);
+// Per-device lookup of the no-alloc entry point's fixed scratch (called by
+// gofann_create with the device current).
+void noalloc_setup(int device);
 void destroy_blas(Context* ctx);
 int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
                    uint32_t count, const float* rotation, gofann_rabitq_queries* out);

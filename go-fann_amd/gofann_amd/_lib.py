@@ -160,6 +160,9 @@ SIGNATURES = {
     "gofann_exact_search": (C.c_int, [P, P, C.c_int, U32, U32, P, C.POINTER(GraphView), P,
                                       C.POINTER(PredicateView), C.POINTER(Routes),
                                       C.POINTER(ExactParams), P, P, P]),
+    "gofann_exact_search_noalloc": (C.c_int, [P, P, C.c_int, U32, U32, P, C.POINTER(GraphView),
+                                              P, C.POINTER(PredicateView), C.POINTER(Routes),
+                                              C.POINTER(ExactParams), P, P, P]),
     "gofann_posting_segment_plan": (C.c_int, [P, P, P, U32, U32, U32, P, P, P, P, P,
                                               C.POINTER(U32)]),
     "gofann_range_slices": (C.c_int, [P, P, P, U32, P, P, P, U32, P]),
@@ -270,6 +273,10 @@ class Context:
         if rc != GOFANN_OK:
             msg = self.lib.gofann_last_error(self.handle)
             raise GofannError(f"gofann call failed ({rc}): {msg.decode() if msg else ''}")
+
+    def last_error(self) -> str:
+        msg = self.lib.gofann_last_error(self.handle)
+        return msg.decode() if msg else ""
 
     def synchronize(self) -> None:
         self.check(self.lib.gofann_synchronize(self.handle))

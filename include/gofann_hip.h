@@ -297,6 +297,27 @@ int gofann_exact_search(gofann_ctx* ctx, const void* base, int base_elem, uint32
                         const gofann_routes* routes, const gofann_exact_params* params,
                         uint32_t* out_ids, float* out_dists, gofann_route_stats* stats);
 
+/* ---- full-GPU exact route that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Arguments, results and placement choice are those of
+ * gofann_exact_search, but a visited set outside LDS (hash_mode 2 or 3, or
+ * auto choosing one) lives in a fixed per-GPU device array of
+ * GOFANN_EXACT_NOALLOC_MAX_ROUTES x 4096 u32 (64 MiB, held by each GPU the
+ * library runs on until the process ends) instead of context scratch; such
+ * a call takes at most GOFANN_EXACT_NOALLOC_MAX_ROUTES routes, and a larger
+ * batch is GOFANN_ERR_INVALID before anything is launched.  No hipMalloc,
+ * hipFree or allocating library routine is called.  Every call on one GPU
+ * shares the array (each route clears its slab before use): calls that
+ * overlap on one GPU, from any context or stream, race. */
+#define GOFANN_EXACT_NOALLOC_MAX_ROUTES 4096
+int gofann_exact_search_noalloc(gofann_ctx* ctx, const void* base, int base_elem, uint32_t dim,
+                                uint32_t samples, const void* queries,
+                                const gofann_graph_view* graph, const uint32_t* label_size,
+                                const gofann_predicate_view* predicate,
+                                const gofann_routes* routes, const gofann_exact_params* params,
+                                uint32_t* out_ids, float* out_dists, gofann_route_stats* stats);
+
 /* ---- range postings ------------------------------------------------------
  * Posting segments (posting_segments::Plan, src/execution/
  * posting_segment_plan.h:12-18).  Segment s scans posting rows
