@@ -13,8 +13,18 @@
 //   src/execution/posting_segment_plan.h     (posting segment plan)
 //   src/index/range_posting_index.{h,cpp}    (FARPIDX1 loader, smallest slice)
 //   src/index/graph_file_format.{h,cpp}      (FDRG graph file reader/writer)
-#include "predicates/gpu_predicate_index.cuh"
+//   include/smmh2.h                          (symmetric min-max heap)
+//   include/bin_heap.h                       (binary max-heap push/pop)
+//   src/search/common/native_visited_hash.cuh (visited hash)
+// range_filter.cuh comes first: it defines __host__/__device__/__forceinline__
+// for a host compiler, which the three device headers above need.
+#include <cstdio>
+
 #include "predicates/range_filter.cuh"
+#include "predicates/gpu_predicate_index.cuh"
+#include "smmh2.h"
+#include "bin_heap.h"
+#include "search/common/native_visited_hash.cuh"
 #include "search/common/posting_shortlist_heap.cuh"
 #include "search/pq/pq_resident_posting.cuh"
 #include "search/rabitq/rabitq_lowfreq_merge.h"
@@ -52,7 +62,77 @@ gp::View make_view(const uint32_t* route_offsets, const uint32_t* route_handles,
 }
 }  // namespace
 
+namespace {
+
+// Result-heap entry: KernelPair<float, uint32_t> (warp_kernel.cuh:18-26)
+// orders on `first` only; warp_kernel.cuh itself needs the CUDA runtime, so
+// the pair type is written out here with that comparison.
+struct RefResultPair {
+    float first;
+    uint32_t second;
+    bool operator<(const RefResultPair& o) const { return first < o.first; }
+    bool operator>(const RefResultPair& o) const { return first > o.first; }
+};
+static_assert(sizeof(RefResultPair) == 8, "result pair layout");
+
+constexpr int kRefHashCapacity = 4096;  // backend_pq.cu:194
+
+}  // namespace
+
 extern "C" {
+
+// smmh2 over the reference's 12-byte BiasedPair (first, second, base),
+// the frontier entry of the biased PQ/RaBitQ kernels.
+void ref_smmh2_insert(void* heap, int* size, const void* entry)
+{
+    gp::BiasedPair e = *static_cast<const gp::BiasedPair*>(entry);
+    smmh2::insert(static_cast<gp::BiasedPair*>(heap), *size, e);
+}
+
+void ref_smmh2_pop_max(void* heap, int* size, void* out)
+{
+    *static_cast<gp::BiasedPair*>(out) = smmh2::pop_max(static_cast<gp::BiasedPair*>(heap), *size);
+}
+
+void ref_smmh2_pop_min(void* heap, int* size, void* out)
+{
+    *static_cast<gp::BiasedPair*>(out) = smmh2::pop_min(static_cast<gp::BiasedPair*>(heap), *size);
+}
+
+// bin_heap.h over [begin, begin + size): push after appending, pop.
+void ref_bin_heap_push(void* begin, int size_after_append)
+{
+    auto* b = static_cast<RefResultPair*>(begin);
+    ::push_heap(b, b + size_after_append);
+}
+
+void ref_bin_heap_pop(void* begin, int size, void* out)
+{
+    auto* b = static_cast<RefResultPair*>(begin);
+    *static_cast<RefResultPair*>(out) = ::pop_heap(b, b + size);
+}
+
+uint32_t ref_hash_code(uint32_t value)
+{
+    return go_fann::native_visited_hash::code<kRefHashCapacity>(value);
+}
+
+// clear as a 32-lane warp runs it: lanes 0..31 each stride by 32.
+void ref_hash_clear(uint32_t* table)
+{
+    for (int lane = 0; lane < 32; ++lane)
+        go_fann::native_visited_hash::clear<kRefHashCapacity>(table, lane);
+}
+
+int ref_hash_test(const uint32_t* table, uint32_t value)
+{
+    return go_fann::native_visited_hash::test<kRefHashCapacity>(table, value) ? 1 : 0;
+}
+
+void ref_hash_add(uint32_t* table, uint32_t value)
+{
+    go_fann::native_visited_hash::add<kRefHashCapacity>(table, value);
+}
 
 int ref_pred_matches(const uint32_t* route_offsets, const uint32_t* route_handles,
                      const void* clauses, const void* ranges, const uint8_t* route_enabled,
