@@ -287,6 +287,31 @@ def posting_scan_pq(pred, codes, table, queries, route_query, cand_ids, cand_off
     return ids[:n], dists[:n], passes[:n]
 
 
+def posting_scan_rabitq(pred, codes, factors, anchor_ids, q8, q_scale, q_k1, centroid_dists,
+                        route_query, cand_ids, cand_offsets, cand_sizes, k):
+    """orc_rabitq_posting_scan (filter-first label postings): ids, dists,
+    pass counts per route."""
+    L = lib()
+    n = len(route_query)
+    codes = c_arr(codes, np.uint8)
+    q8 = c_arr(q8, np.int8)
+    cd = c_arr(centroid_dists, np.float32)
+    ids = np.empty((max(n, 1), k), np.uint32)
+    dists = np.empty((max(n, 1), k), np.float32)
+    passes = np.empty(max(n, 1), np.uint32)
+    arrs = [codes, c_arr(factors, np.float32), c_arr(anchor_ids, np.uint32), q8,
+            c_arr(q_scale, np.float32), c_arr(q_k1, np.float32), cd,
+            c_arr(route_query, np.uint32), c_arr(cand_ids, np.uint32),
+            c_arr(cand_offsets, np.uint32), c_arr(cand_sizes, np.uint32)]
+    rc = L.orc_rabitq_posting_scan(C.byref(pred.struct) if pred else None, p(arrs[0]),
+                                   U32(codes.shape[1]), *[p(a) for a in arrs[1:7]],
+                                   U32(cd.shape[1]), U32(q8.shape[1]),
+                                   *[p(a) for a in arrs[7:]], U32(n), k, p(ids), p(dists),
+                                   p(passes))
+    assert rc == 0
+    return ids[:n], dists[:n], passes[:n]
+
+
 def rerank(base, queries, route_query, shortlist, topk):
     L = lib()
     elem = {np.dtype(np.uint8): 0, np.dtype(np.float32): 1, np.dtype(np.float16): 2}[base.dtype]
