@@ -93,6 +93,28 @@ def lib():
     return _lib
 
 
+BASELINE_LIB = HERE / "libgofann_cpu_baseline.so"
+_baseline = None
+
+
+def baseline_lib():
+    """The oracle's batch drivers over all host cores (cpu_baseline.c)."""
+    global _baseline
+    if _baseline is None:
+        if not BASELINE_LIB.exists():
+            raise RuntimeError(f"{BASELINE_LIB} missing: run make -C oracle")
+        _baseline = C.CDLL(str(BASELINE_LIB))
+    return _baseline
+
+
+def _drive(name, *args, threads=None):
+    """orc_<name>(*args) on one core, or cbl_<name>(*args, threads) on
+    `threads` host cores (0 = OpenMP's default); the results are the same."""
+    if threads is None:
+        return getattr(lib(), "orc_" + name)(*args)
+    return getattr(baseline_lib(), "cbl_" + name)(*args, C.c_int(int(threads)))
+
+
 def ref():
     """Reference-header checker, or None when oracle/_ref was not built."""
     global _ref
@@ -179,7 +201,7 @@ def graph_struct(index, route_group, route_start):
 
 
 def pq_search(index, routes, pred: PredicateArrays, prm: Params, codes, table, queries,
-              base=None):
+              base=None, threads=None):
     """Oracle beam search of every route.  Returns ids [R][W] u32,
     dists [R][W] f32, stats structured array."""
     L = lib()
@@ -195,15 +217,15 @@ def pq_search(index, routes, pred: PredicateArrays, prm: Params, codes, table, q
     q = np.ascontiguousarray(queries)
     rq = c_arr(routes.route_query, np.uint32)
     b = None if base is None else np.ascontiguousarray(base)
-    rc = L.orc_pq_search_batch(C.byref(g), C.byref(pred.struct), C.byref(prm), p(codes),
+    rc = _drive("pq_search_batch", C.byref(g), C.byref(pred.struct), C.byref(prm), p(codes),
                                p(table), p(q), 1 if qf else 0, p(b), p(rq), int(table.shape[1]),
-                               int(codes.shape[1]), n, p(ids), p(dists), stats)
+                               int(codes.shape[1]), n, p(ids), p(dists), stats, threads=threads)
     assert rc == 0
     return ids, dists, stats_array(stats, n)
 
 
 def rabitq_search(index, routes, pred: PredicateArrays, prm: Params, codes, factors,
-                  anchor_ids, q8, scale, k1, cdist, num_anchors, padded_dim):
+                  anchor_ids, q8, scale, k1, cdist, num_anchors, padded_dim, threads=None):
     L = lib()
     g, keep = graph_struct(index, routes.route_group, routes.route_start)
     n = routes.count
@@ -214,10 +236,10 @@ def rabitq_search(index, routes, pred: PredicateArrays, prm: Params, codes, fact
     arrs = [c_arr(codes, np.uint8), c_arr(factors, np.float32), c_arr(anchor_ids, np.uint32),
             c_arr(q8, np.int8), c_arr(scale, np.float32), c_arr(k1, np.float32),
             c_arr(cdist, np.float32), c_arr(routes.route_query, np.uint32)]
-    rc = L.orc_rabitq_search_batch(C.byref(g), C.byref(pred.struct), C.byref(prm), p(arrs[0]),
+    rc = _drive("rabitq_search_batch", C.byref(g), C.byref(pred.struct), C.byref(prm), p(arrs[0]),
                                    U32(padded_dim // 8), p(arrs[1]), p(arrs[2]), p(arrs[3]),
                                    p(arrs[4]), p(arrs[5]), p(arrs[6]), U32(num_anchors),
-                                   U32(padded_dim), p(arrs[7]), U32(n), p(ids), p(dists), stats)
+                                   U32(padded_dim), p(arrs[7]), U32(n), p(ids), p(dists), stats, threads=threads)
     assert rc == 0
     return ids, dists, stats_array(stats, n)
 
@@ -269,7 +291,7 @@ def rabitq_ip(q8, code, which="int"):
 
 
 def posting_scan_pq(pred, codes, table, queries, route_query, cand_ids, cand_offsets,
-                    cand_sizes, k, score_first=False):
+                    cand_sizes, k, score_first=False, threads=None):
     L = lib()
     n = len(route_query)
     ids = np.empty((max(n, 1), k), np.uint32)
@@ -278,17 +300,17 @@ def posting_scan_pq(pred, codes, table, queries, route_query, cand_ids, cand_off
     arrs = [c_arr(codes, np.uint8), c_arr(table, np.float32), np.ascontiguousarray(queries),
             c_arr(route_query, np.uint32), c_arr(cand_ids, np.uint32),
             c_arr(cand_offsets, np.uint32), c_arr(cand_sizes, np.uint32)]
-    rc = L.orc_pq_posting_scan(C.byref(pred.struct) if pred else None, p(arrs[0]), p(arrs[1]),
+    rc = _drive("pq_posting_scan", C.byref(pred.struct) if pred else None, p(arrs[0]), p(arrs[1]),
                                p(arrs[2]), 1 if queries.dtype == np.float32 else 0, p(arrs[3]),
                                p(arrs[4]), p(arrs[5]), p(arrs[6]), U32(n),
                                int(arrs[1].shape[1]), int(arrs[0].shape[1]), k,
-                               1 if score_first else 0, p(ids), p(dists), p(passes))
+                               1 if score_first else 0, p(ids), p(dists), p(passes), threads=threads)
     assert rc == 0
     return ids[:n], dists[:n], passes[:n]
 
 
 def posting_scan_rabitq(pred, codes, factors, anchor_ids, q8, q_scale, q_k1, centroid_dists,
-                        route_query, cand_ids, cand_offsets, cand_sizes, k):
+                        route_query, cand_ids, cand_offsets, cand_sizes, k, threads=None):
     """orc_rabitq_posting_scan (filter-first label postings): ids, dists,
     pass counts per route."""
     L = lib()
@@ -303,16 +325,16 @@ def posting_scan_rabitq(pred, codes, factors, anchor_ids, q8, q_scale, q_k1, cen
             c_arr(q_scale, np.float32), c_arr(q_k1, np.float32), cd,
             c_arr(route_query, np.uint32), c_arr(cand_ids, np.uint32),
             c_arr(cand_offsets, np.uint32), c_arr(cand_sizes, np.uint32)]
-    rc = L.orc_rabitq_posting_scan(C.byref(pred.struct) if pred else None, p(arrs[0]),
+    rc = _drive("rabitq_posting_scan", C.byref(pred.struct) if pred else None, p(arrs[0]),
                                    U32(codes.shape[1]), *[p(a) for a in arrs[1:7]],
                                    U32(cd.shape[1]), U32(q8.shape[1]),
                                    *[p(a) for a in arrs[7:]], U32(n), k, p(ids), p(dists),
-                                   p(passes))
+                                   p(passes), threads=threads)
     assert rc == 0
     return ids[:n], dists[:n], passes[:n]
 
 
-def rerank(base, queries, route_query, shortlist, topk):
+def rerank(base, queries, route_query, shortlist, topk, threads=None):
     L = lib()
     elem = {np.dtype(np.uint8): 0, np.dtype(np.float32): 1, np.dtype(np.float16): 2}[base.dtype]
     base_c = np.ascontiguousarray(base)
@@ -324,8 +346,8 @@ def rerank(base, queries, route_query, shortlist, topk):
     ids = np.empty((n, topk), np.uint32)
     dists = np.empty((n, topk), np.float32)
     rq = c_arr(route_query, np.uint32)
-    rc = L.orc_rerank(p(base_c), elem, U32(base.shape[1]), U32(base.shape[0]), p(q), p(rq),
-                      p(sl), U32(width), U32(n), U32(topk), p(ids), p(dists))
+    rc = _drive("rerank", p(base_c), elem, U32(base.shape[1]), U32(base.shape[0]), p(q), p(rq),
+                      p(sl), U32(width), U32(n), U32(topk), p(ids), p(dists), threads=threads)
     assert rc == 0
     return ids, dists
 
@@ -466,7 +488,7 @@ def ref_graph_file_convert_legacy(legacy_path, path):
 
 def rabitq_range_scan(pred, modes, lower, upper, base_values, codes, factors, anchor_ids, q8,
                       q_scale, q_k1, centroid_dists, route_query, posting, resident_rows,
-                      base_rows, seg_routes, seg_offsets, seg_sizes, k, score_first=False):
+                      base_rows, seg_routes, seg_offsets, seg_sizes, k, score_first=False, threads=None):
     """orc_rabitq_range_scan -> per-segment (ids, dists, passes)."""
     L = lib()
     modes = c_arr(modes, np.uint8)
@@ -487,11 +509,11 @@ def rabitq_range_scan(pred, modes, lower, upper, base_values, codes, factors, an
     ids = np.empty((max(n, 1), k), np.uint32)
     dists = np.empty((max(n, 1), k), np.float32)
     passes = np.empty(max(n, 1), np.uint32)
-    rc = L.orc_rabitq_range_scan(C.byref(pred.struct) if pred else None, C.byref(rt), p(codes),
+    rc = _drive("rabitq_range_scan", C.byref(pred.struct) if pred else None, C.byref(rt), p(codes),
                                  U32(codes.shape[1]), *[p(a) for a in arrs], U32(cd.shape[1]),
                                  U32(padded), p(rq), p(post), C.c_uint64(resident_rows), U32(base_rows),
                                  p(sr), p(so), p(ss), U32(n), k, 1 if score_first else 0,
-                                 p(ids), p(dists), p(passes))
+                                 p(ids), p(dists), p(passes), threads=threads)
     assert rc == 0
     return ids[:n], dists[:n], passes[:n]
 
@@ -518,7 +540,7 @@ class ExactParams(C.Structure):
 def exact_search(index, routes, pred, base, queries, queue_limit=64, topk=10,
                  early_stop_mode=2, finish_limit=1, max_steps=0, label_size=None,
                  row_filter_mask=None, query_filter_bits=None, range_modes=None,
-                 range_lower=None, range_upper=None, base_range_values=None):
+                 range_lower=None, range_upper=None, base_range_values=None, threads=None):
     """orc_exact_search over every route: ids [R][topk] u32, dists f32, stats."""
     L = lib()
     g, keep = graph_struct(index, routes.route_group, routes.route_start)
@@ -538,8 +560,8 @@ def exact_search(index, routes, pred, base, queries, queue_limit=64, topk=10,
     q = np.ascontiguousarray(queries, dtype=np.uint8)
     rq = c_arr(routes.route_query, np.uint32)
     prm = ExactParams(queue_limit, finish_limit, early_stop_mode, max_steps, topk)
-    rc = L.orc_exact_search(C.byref(g), p(extra["ls"]), C.byref(pred.struct) if pred else None,
+    rc = _drive("exact_search", C.byref(g), p(extra["ls"]), C.byref(pred.struct) if pred else None,
                             C.byref(prm), p(b), U32(b.shape[1]), U32(b.shape[0]), p(q), p(rq),
-                            U32(n), p(ids), p(dists), stats)
+                            U32(n), p(ids), p(dists), stats, threads=threads)
     assert rc == 0
     return ids[:n], dists[:n], stats_array(stats, n)
