@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--n", type=int, default=10_000_000, help="base vectors (C2: 10M)")
+    ap.add_argument("--coarse-lists", type=int, default=1024,
+                    help="k-means centres that bucket the C2 graph builder's rows")
     ap.add_argument("--queries", type=int, default=100_000)
     ap.add_argument("--gt-queries", type=int, default=2000)
     ap.add_argument("--queue", type=int, default=0, help="beam width; 0 = ladder search")
@@ -112,12 +114,14 @@ def build_world(args, torch):
     torch.cuda.synchronize()
     log(f"PQ M=48 trained+encoded in {time.time() - t0:.1f}s")
     t0 = time.time()
+    cen = gi.train_kmeans(wl.base, args.coarse_lists, seed=2006)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=64, threshold=2000, progress=log)
+                              cen, degree=64, threshold=2000, progress=log)
     log(f"label graphs: {int((li.label_size > 0).sum())} labels, {li.rows} rows, "
-        f"degree 64 in {time.time() - t0:.1f}s")
+        f"degree 64, buckets from {args.coarse_lists} trained k-means centres in "
+        f"{time.time() - t0:.1f}s")
     t0 = time.time()
-    pl = gp.plan_queries(li, wl.query_labels, seeds="nearest_bucket", queries=wl.queries)
+    pl = gp.plan_queries(li, wl.query_labels)
     log(f"plan: {pl.graph.count} graph routes, {pl.posting.count} posting routes "
         f"in {time.time() - t0:.1f}s")
     return wl, li, table, codes, pl
@@ -463,12 +467,32 @@ def measured_traffic(profile: str, match: bool):
     return None
 
 
-def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False):
-    """The oracle (a single-threaded C restatement of the reference path) on
-    a bounded sample of the same workload: graph search (the exact-distance
-    route, or PQ with the same inline exact ranking as the GPU step),
-    posting scan, exact rerank and merge for the first queries until
-    `seconds` elapse."""
+def host_threads() -> int:
+    """Host cores the CPU baseline uses: OMP_NUM_THREADS when set (the GPU
+    box sets it to the job's CPU share), else every core."""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
+    except ValueError:
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False, threads=1):
+    """The oracle's C restatement of the reference path, run over `threads`
+    host cores (oracle/libgofann_cpu_baseline.so: one chunk of routes per
+    OpenMP thread, -O3), on a bounded sample of the same workload: graph
+    search (the exact-distance route, or PQ with the same inline exact
+    ranking as the GPU step), posting scan, exact rerank and merge for the
+    first queries until `seconds` elapse."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import pyoracle as po
     from gofann_amd import plan as gp
@@ -479,17 +503,17 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False
     done = 0
     t0 = time.perf_counter()
     qlist = list(range(len(wl.query_labels)))
-    chunk = 64
+    chunk = 64 * threads
+    T = threads
     while done < len(qlist) and time.perf_counter() - t0 < seconds:
         sel = qlist[done: done + chunk]
-        sub = gp.plan_queries(li, [wl.query_labels[i] for i in sel], seeds="nearest_bucket",
-                              queries=qs[sel])
+        sub = gp.plan_queries(li, [wl.query_labels[i] for i in sel])
         rs = sub.graph
         res_i, res_d, r2q = [], [], []
         if rs.count and exact_route:
             pred = po.PredicateArrays.from_plan(rs.predicate, li)
             ri, rd, _ = po.exact_search(li, rs, pred, base, qs[sel], queue_limit=Q, topk=10,
-                                        early_stop_mode=2, label_size=li.label_size)
+                                        early_stop_mode=2, label_size=li.label_size, threads=T)
             res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
         elif rs.count:
             pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
@@ -498,18 +522,19 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False
                 ri, rd, _ = po.pq_search(li, rs, pred,
                                          po.params(queue_limit=Q, result_width=10,
                                                    inline_exact=True),
-                                         codes_h, table_h, qs[sel], base=base)
+                                         codes_h, table_h, qs[sel], base=base, threads=T)
             else:
                 ids, _, _ = po.pq_search(li, rs, pred,
                                          po.params(queue_limit=Q, result_width=100),
-                                         codes_h, table_h, qs[sel])
-                ri, rd = po.rerank(base, qs[sel], rs.route_query, ids, 10)
+                                         codes_h, table_h, qs[sel], threads=T)
+                ri, rd = po.rerank(base, qs[sel], rs.route_query, ids, 10, threads=T)
             res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
         if sub.posting.count:
             pr = po.PredicateArrays.from_plan(sub.posting.predicate, li)
             pi, _, _ = po.posting_scan_pq(pr, codes_h, table_h, qs[sel], sub.posting.route_query,
-                                          li.posting_ids, sub.cand_offsets, sub.cand_sizes, 100)
-            ri, rd = po.rerank(base, qs[sel], sub.posting.route_query, pi, 10)
+                                          li.posting_ids, sub.cand_offsets, sub.cand_sizes, 100,
+                                          threads=T)
+            ri, rd = po.rerank(base, qs[sel], sub.posting.route_query, pi, 10, threads=T)
             res_i.append(ri), res_d.append(rd), r2q.append(sub.posting.route_to_query)
         if res_i:
             po.merge(np.concatenate(r2q), np.concatenate(res_i), np.concatenate(res_d),
@@ -544,13 +569,14 @@ def build_world_c3(args, torch):
     torch.cuda.synchronize()
     log(f"C3 data {wl.n}x{wl.dim} fp32, {wl.queries.shape[0]} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
-    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, 1, wl.centroids,
+    cen = gi.train_kmeans(wl.base, 512, seed=3006)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, 1, cen,
                               degree=32, threshold=0, progress=log)
     log(f"C3 graph: {li.rows} rows, degree {li.degree} in {time.time() - t0:.1f}s")
     t0 = time.time()
     P = wl.dim
     rot = gi.random_rotation(wl.dim, P, 3003, "cuda")
-    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, cen)
     torch.cuda.synchronize()
     log(f"C3 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
     rpi = rp.RangePostingIndex.build(wl.base_ranges)
@@ -603,12 +629,10 @@ class RabitqRangePipeline:
         gq = np.nonzero(~post)[0].astype(np.uint32)
         pq = np.nonzero(post)[0].astype(np.uint32)
         self.ng, self.np_ = len(gq), len(pq)
-        # graph routes: one per wide-range query, seeded at the nearest bucket
+        # graph routes: one per wide-range query, seeded at the graph's medoid
         rows = [(int(q), 0, [], [tuple(wl.query_ranges[q][0])]) for q in gq]
         self.graph_rows = rows
         rs = gp._routeset(rows, li)
-        if rs.count:
-            rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
         self.rs = rs
         self.dg = gs.DeviceGraph.upload(li)
         self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
@@ -711,13 +735,16 @@ class RabitqRangePipeline:
         return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
 
 
-def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
-    """The oracle (single-threaded C restatement) on a bounded sample of a
-    RaBitQ route set (C3 or C4): for the first queries until `seconds`
-    elapse, their graph routes (RaBitQ beam, shortlist W), their range- or
-    label-posting scans, the exact rerank of the shortlists and the merge.
-    The full base vectors do not fit the host sample, so the rows the
-    shortlists name are gathered (the rerank reads exactly those rows)."""
+def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, threads=1):
+    """The oracle's C restatement over `threads` host cores (OpenMP, one
+    chunk of routes per thread, -O3) on a bounded sample of a RaBitQ route
+    set (C3 or C4): for the first queries until `seconds` elapse, their
+    graph routes (RaBitQ beam, shortlist W), their range- or label-posting
+    scans, the exact rerank of the shortlists and the merge.  The full base
+    vectors do not fit the host sample, so the rows the shortlists name are
+    gathered (the rerank reads exactly those rows)."""
+    chunk = 16 * threads
+    T = threads
     sys.path.insert(0, str(ROOT / "oracle"))
     import ctypes as C
     import torch
@@ -749,7 +776,6 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
         rows = [r for q in sel for r in by_q.get(q, [])]
         if rows:
             rs = gp._routeset(rows, li)
-            rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
             pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
                                                 pending_base_stop=True,
                                                 base_ranges=wl.base_ranges)
@@ -758,7 +784,7 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
                                                                  early_stop_mode=2, bias=True,
                                                                  rabitq_verdict=1),
                                          codes, fac, aid, pre["q8"], pre["scale"], pre["k1"],
-                                         pre["cd"], A, P)
+                                         pre["cd"], A, P, threads=T)
             lists.append(ids), r2q.append(rs.route_query)
         scans = [i for q in sel for i in scan_by_q.get(q, [])]
         if scans:  # range-posting scans over the whole smallest slice
@@ -769,7 +795,7 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
                 aid, pre["q8"], pre["scale"], pre["k1"], pre["cd"], rq_,
                 np.concatenate([d.sample_ids for d in pipe.rpi.dimensions]),
                 pipe.rpi.resident_rows, wl.n, np.arange(n, dtype=np.uint32),
-                pipe.scan_off[scans], pipe.scan_size[scans], W, False)
+                pipe.scan_off[scans], pipe.scan_size[scans], W, False, threads=T)
             lists.append(ids), r2q.append(rq_)
         posts = [t for q in sel for t in post_by_q.get(q, [])]
         if posts:  # label-posting scans
@@ -778,18 +804,9 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
             off = np.array([li.posting_offset[r[1]] for _, r in posts], np.uint32)
             size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]]
                              for _, r in posts], np.uint32)
-            n = prs.count
-            oi = np.empty((n, W), np.uint32)
-            od = np.empty((n, W), np.float32)
-            opass = np.empty(n, np.uint32)
-            arrs = [np.ascontiguousarray(a) for a in (codes, fac, aid, pre["q8"], pre["scale"],
-                                                      pre["k1"], pre["cd"], prs.route_query,
-                                                      li.posting_ids, off, size)]
-            assert L.orc_rabitq_posting_scan(
-                C.byref(pred.struct), po.p(arrs[0]), C.c_uint32(P // 8),
-                *[po.p(a) for a in arrs[1:7]], C.c_uint32(A), C.c_uint32(P),
-                *[po.p(a) for a in arrs[7:]], C.c_uint32(n), W, po.p(oi), po.p(od),
-                po.p(opass)) == 0
+            oi, _, _ = po.posting_scan_rabitq(pred, codes, fac, aid, pre["q8"], pre["scale"],
+                                              pre["k1"], pre["cd"], prs.route_query,
+                                              li.posting_ids, off, size, W, threads=T)
             lists.append(oi), r2q.append(prs.route_query)
         if lists:
             sl = np.concatenate(lists)
@@ -799,7 +816,7 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
             local[sl != 0xFFFFFFFF] = inv.astype(np.uint32)
             rows_h = wl.base[torch.as_tensor(uniq.astype(np.int64), device=wl.base.device)]
             rows_h = rows_h.cpu().numpy()
-            li_, ld_ = po.rerank(rows_h, qs, rqy, local, 10)
+            li_, ld_ = po.rerank(rows_h, qs, rqy, local, 10, threads=T)
             li_ = np.where(li_ != 0xFFFFFFFF, uniq[np.minimum(li_, max(len(uniq) - 1, 0))],
                            0xFFFFFFFF).astype(np.uint32)
             po.merge(rqy - sel[0], li_, ld_, len(sel), 10)
@@ -808,9 +825,11 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, chunk=16):
     return done / el, done, el
 
 
-def cpu_line(rate, done, el, what):
-    return {"value": round(rate, 2), "unit": "queries/s", "cores": 1, "kind": "port",
-            "sample": f"first {done} of the queries ({what}) in {el:.1f}s on one host core"}
+def cpu_line(rate, done, el, what, threads):
+    return {"value": round(rate, 2), "unit": "queries/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(),
+            "sample": f"first {done} of the queries ({what}) in {el:.1f}s on {threads} host "
+                      f"threads (oracle C code, OpenMP, -O3 -march=x86-64-v3)"}
 
 
 def main_c3(args):
@@ -893,8 +912,10 @@ def main_c3(args):
     }
     if not args.no_cpu_baseline:
         pipe.chosen = chosen
-        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds)
-        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph routes at the chosen Q, range-posting scans, exact fp32 rerank, merge")
+        T = host_threads()
+        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds, threads=T)
+        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph routes at the chosen Q, range-posting "
+                                        "scans, exact fp32 rerank, merge", T)
         log(f"cpu baseline {cr:.1f} qps over {cn} queries")
     print(json.dumps(line), flush=True)
     ctx.close()
@@ -913,8 +934,9 @@ def build_world_c4(args, torch):
     torch.cuda.synchronize()
     log(f"C4 data {wl.n}x{wl.dim} fp16, {wl.queries.shape[0]} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
+    cen = gi.train_kmeans(wl.base, 4096, seed=4006)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=32, threshold=args.c4_threshold, progress=log)
+                              cen, degree=32, threshold=args.c4_threshold, progress=log)
     torch.cuda.empty_cache()
     ng = int((li.label_size > 0).sum())
     log(f"C4 graphs: {ng} label/interval groups, {li.rows} rows, degree {li.degree} in "
@@ -922,7 +944,7 @@ def build_world_c4(args, torch):
     t0 = time.time()
     P = wl.dim
     rot = gi.random_rotation(wl.dim, P, 4005, "cuda")
-    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids, chunk=1 << 18)
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, cen, chunk=1 << 18)
     torch.cuda.synchronize()
     log(f"C4 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
     return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P)
@@ -1001,8 +1023,6 @@ class RabitqLabelPipeline:
         graph_rows.sort(key=lambda r: (r[1], r[0]))
         self.graph_rows, self.post_rows = graph_rows, post_rows
         rs = gp._routeset(graph_rows, li)
-        if rs.count:
-            rs.route_start = gp.nearest_bucket_seeds(li, rs, wl.queries)
         ps = gp._routeset(post_rows, li)
         self.rs, self.ps = rs, ps
         self.ng, self.np_ = rs.count, ps.count
@@ -1169,8 +1189,10 @@ def main_c4(args):
     }
     if not args.no_cpu_baseline:
         pipe.chosen = chosen
-        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds)
-        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph and interval routes at the chosen Q, label-posting scans, exact fp16 rerank, merge")
+        T = host_threads()
+        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds, threads=T)
+        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph and interval routes at the chosen Q, "
+                                        "label-posting scans, exact fp16 rerank, merge", T)
         log(f"cpu baseline {cr:.1f} qps over {cn} queries")
     print(json.dumps(line), flush=True)
 
@@ -1341,12 +1363,12 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
+        T = host_threads()
         cq, cn, cel = cpu_baseline(wl, li, table, codes, pl, head["queue"], args.cpu_seconds,
-                                   inline, exact_route=use_exact)
+                                   inline, exact_route=use_exact, threads=T)
         what = "exact route" if use_exact else "PQ graph search"
-        cpu = {"value": round(cq, 2), "unit": "queries/s", "cores": 1, "kind": "port",
-               "sample": f"first {cn} of the {pl.queries} C2 queries ({what} Q={head['queue']}, "
-                         f"posting scan, exact rerank, merge) in {cel:.1f}s on one host core"}
+        cpu = cpu_line(cq, cn, cel, f"{what} Q={head['queue']}, posting scan, exact rerank, "
+                                    f"merge; C2", T)
         log(f"cpu baseline {cq:.1f} qps over {cn} queries")
 
     line = {
@@ -1367,7 +1389,8 @@ def main():
                    "n": wl.n, "queries": pl.queries, "graph_routes": pl.graph.count,
                    "posting_routes": pl.posting.count, "route": head["route"],
                    "queue": head["queue"], "recall_at_10": head["recall"],
-                   "rerank": "exact u8 on GPU", "seeds": "nearest bucket representative",
+                   "rerank": "exact u8 on GPU", "seeds": "label medoid (dataloader.cpp:7361-7406)",
+                   "graph_buckets": f"{args.coarse_lists} k-means centres trained on the base",
                    "gt_queries": len(gt), "placement": head["placement"],
                    "neighbor_samples": not args.no_neighbor_samples,
                    "sample_records": not args.no_records,

@@ -80,6 +80,49 @@ def pq_encode(x: torch.Tensor, table: torch.Tensor, pq_dim: int, chunk: int = 1 
 
 
 # ---------------------------------------------------------------------------
+# Coarse k-means (graph buckets, RaBitQ anchors)
+# ---------------------------------------------------------------------------
+def train_kmeans(x: torch.Tensor, k: int, iters: int = 15, sample: int = 262144,
+                 seed: int = 6, chunk: int = 1 << 16) -> torch.Tensor:
+    """Seeded k-means over a uniform row sample of the base: k-means++
+    seeding (D^2 sampling), then Lloyd iterations; an empty cluster keeps its
+    previous centre.  Returns [k][D] float32 on x's device.  The index is
+    built from these trained centres only (never from how the data was
+    generated): they bucket the graph builder's rows and become the RaBitQ
+    anchors."""
+    dev = x.device
+    n, d = x.shape
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    m = min(n, max(sample, k))
+    idx = torch.randperm(n, generator=g)[:m].to(dev) if m < n else torch.arange(n, device=dev)
+    xs = x[idx].float()
+    xn = (xs * xs).sum(1)
+    k = min(k, m)
+    cen = torch.empty(k, d, dtype=torch.float32, device=dev)
+    first = int(torch.randint(m, (1,), generator=g))
+    cen[0] = xs[first]
+    best = (xn - 2 * xs @ cen[0] + xn[first]).clamp_(min=0)
+    u = torch.rand(k, generator=g, dtype=torch.float64).to(dev)
+    for j in range(1, k):
+        cdf = torch.cumsum(best.double(), 0)
+        pick = torch.searchsorted(cdf, (u[j] * cdf[-1]).reshape(1)).clamp_(max=m - 1)
+        c = xs[pick[0]]
+        cen[j] = c
+        dj = (xn - 2 * xs @ c + (c * c).sum()).clamp_(min=0)
+        torch.minimum(best, dj, out=best)
+    for _ in range(iters):
+        cn = (cen * cen).sum(1)
+        assign = torch.empty(m, dtype=torch.int64, device=dev)
+        for s in range(0, m, chunk):
+            assign[s:s + chunk] = (cn[None, :] - 2 * xs[s:s + chunk] @ cen.t()).argmin(1)
+        sums = torch.zeros_like(cen).index_add_(0, assign, xs)
+        cnt = torch.bincount(assign, minlength=k).float()
+        cen = torch.where(cnt[:, None] > 0, sums / cnt.clamp(min=1)[:, None], cen)
+    return cen.contiguous()
+
+
+# ---------------------------------------------------------------------------
 # RaBitQ (one bit)
 # ---------------------------------------------------------------------------
 def random_rotation(dim: int, padded: int, seed: int, device) -> torch.Tensor:
@@ -255,32 +298,62 @@ def _bucket_knn(xg: torch.Tensor, bucket_of: torch.Tensor, k: int, max_batch_ele
     return out
 
 
+def _compact_unique(cand: torch.Tensor, width: int) -> torch.Tensor:
+    """First `width` distinct non-negative entries of each row, in their
+    original order, padded with -1."""
+    n, w = cand.shape
+    srt, idx = torch.sort(cand, dim=1, stable=True)
+    dup_sorted = torch.zeros_like(srt, dtype=torch.bool)
+    dup_sorted[:, 1:] = srt[:, 1:] == srt[:, :-1]
+    dup = torch.zeros_like(dup_sorted).scatter_(1, idx, dup_sorted)
+    bad = dup | (cand < 0)
+    perm = torch.sort(bad.to(torch.int8), dim=1, stable=True).indices
+    out = torch.gather(cand, 1, perm)[:, :width]
+    out = torch.where(torch.gather(bad, 1, perm)[:, :width], torch.full_like(out, -1), out)
+    if out.shape[1] < width:
+        out = torch.cat([out, torch.full((n, width - out.shape[1]), -1, dtype=out.dtype,
+                                         device=out.device)], 1)
+    return out
+
+
 def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch.Tensor,
-                      degree: int, bridges: int = 4, rep_bridges: int | None = None,
+                      degree: int, local: int | None = None, near: int = 2,
+                      rep_local: int | None = None, rep_near: int | None = None, seed: int = 0,
                       max_batch_elems: int = 1 << 27, return_reps: bool = False):
     """Graph over the rows of one label group (rows in the given order).
 
-    Edges of a row: exact kNN inside its (label, cluster) bucket, then the
-    representative of its own bucket and of the nearest other buckets
-    (bridges).  Representatives carry `rep_bridges` bridge edges."""
+    Rows are bucketed by their nearest coarse centre; each bucket has a
+    representative (the row nearest the bucket mean).  An ordinary row links
+    to its `local` exact nearest rows inside its bucket, its bucket's
+    representative, the representatives of the `near` nearest other buckets,
+    and uniformly drawn rows of the group up to the degree.  A
+    representative links to `rep_local` rows of its bucket, the
+    representatives of the `rep_near` nearest buckets, and drawn rows.
+
+    The drawn links are what make the graph searchable from one entry row
+    when bucket centres are spread without structure (a mixture with random
+    centres): distances to the wrong buckets then carry no direction towards
+    the right one, so a beam finds a query's bucket only by seeing one of
+    its rows, and every expansion that reveals fresh buckets brings that
+    closer.  The in-bucket links then let the beam search the bucket, and
+    the nearest-bucket links cover clusters that the coarse centres split."""
     dev = xg.device
     n = xg.shape[0]
     R = degree
-    rep_bridges = rep_bridges if rep_bridges is not None else R // 2
+    local = local if local is not None else R // 2
+    rep_local = rep_local if rep_local is not None else max(R // 8, 1)
+    rep_near = rep_near if rep_near is not None else max(R // 8, 1)
     lean = n * xg.shape[1] * 4 > LEAN_GROUP_BYTES
     xg = xg.float()
     order = torch.argsort(cluster_of, stable=True)
     bs = cluster_of[order]
-    k_local = R - bridges
     xs = None if lean else xg[order]
     if lean:
-        knn = _bucket_knn(xg, bs, k_local, max_batch_elems, order=order)
+        knn = _bucket_knn(xg, bs, local, max_batch_elems, order=order)
     else:
-        knn = _bucket_knn(xs, bs, k_local, max_batch_elems)  # in sorted row space
+        knn = _bucket_knn(xs, bs, local, max_batch_elems)  # in sorted row space
     uniq, counts = torch.unique_consecutive(bs, return_counts=True)
     nb = uniq.shape[0]
-    starts = torch.zeros_like(counts)
-    starts[1:] = torch.cumsum(counts, 0)[:-1]
     bucket_idx = torch.repeat_interleave(torch.arange(nb, device=dev), counts)
     # representative: row nearest its bucket mean
     if lean:
@@ -299,42 +372,39 @@ def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch
         means = sums / counts[:, None].float()
         dm = ((xs - means[bucket_idx]) ** 2).sum(1)
     big = torch.finfo(dm.dtype).max
-    rep = torch.empty(nb, dtype=torch.int64, device=dev)
     for_min = torch.full((nb,), big, device=dev).scatter_reduce(0, bucket_idx, dm, "amin")
     is_min = dm <= for_min[bucket_idx]
     cand = torch.where(is_min, torch.arange(n, device=dev), torch.full_like(bucket_idx, n))
     rep = torch.full((nb,), n, dtype=torch.int64, device=dev).scatter_reduce(0, bucket_idx, cand, "amin")
-    # nearest other buckets by centre distance
+    # nearest other buckets by coarse-centre distance
     c = centres[uniq].float()
     cd = ((c * c).sum(1)[:, None] + (c * c).sum(1)[None, :] - 2 * c @ c.t())
     cd.fill_diagonal_(float("inf"))
-    nn_b = torch.argsort(cd, dim=1)[:, : max(rep_bridges, bridges + R)]
-    # bridge list per bucket: own representative, then the representatives
-    # of the nearest buckets
-    blist = torch.cat([rep[:, None], rep[nn_b]], dim=1)  # [nb, 1 + m]
-    fill = blist[bucket_idx]  # [n, 1+m]
+    m_near = min(max(rep_near, near), max(nb - 1, 0))
+    nn_b = torch.argsort(cd, dim=1)[:, :m_near]  # [nb, m_near]
     ar = torch.arange(n, device=dev)
-    fill = torch.where(fill == ar[:, None], torch.full_like(fill, -1), fill)
-    local = knn.clone()
-    is_rep = torch.zeros(n, dtype=torch.bool, device=dev)
-    is_rep[rep] = True
-    keep_local = max(R - rep_bridges, 0)
-    if keep_local < k_local:
-        cut = torch.arange(k_local, device=dev)[None, :] >= keep_local
-        local = torch.where(is_rep[:, None] & cut, torch.full_like(local, -1), local)
-    own_dup = (local == fill[:, :1]).any(1)
-    fill[:, 0] = torch.where(own_dup, torch.full_like(fill[:, 0], -1), fill[:, 0])
-    cand = torch.cat([local, fill], dim=1)
-    # stable compaction: valid entries first, original order kept
-    key = (cand < 0).to(torch.int8)
-    perm = torch.sort(key, dim=1, stable=True).indices
-    cand = torch.gather(cand, 1, perm)[:, :R]
-    if cand.shape[1] < R:
-        cand = torch.cat([cand, torch.full((n, R - cand.shape[1]), -1, device=dev,
-                                           dtype=cand.dtype)], 1)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(int(seed))
+    out = torch.empty(n, R, dtype=torch.int64, device=dev)
+    step = 1 << 20
+    for s0 in range(0, n, step):
+        s1 = min(n, s0 + step)
+        rows = ar[s0:s1]
+        b = bucket_idx[s0:s1]
+        own = rep[b][:, None]
+        own = torch.where(own == rows[:, None], torch.full_like(own, -1), own)
+        drawn = torch.randint(0, n, (s1 - s0, R), generator=g).to(dev)
+        drawn = torch.where(drawn == rows[:, None], torch.full_like(drawn, -1), drawn)
+        cand = torch.cat([knn[s0:s1], own, rep[nn_b[b, :near]], drawn], dim=1)
+        out[s0:s1] = _compact_unique(cand, R)
+    # representatives: a few in-bucket rows, the nearest buckets' reps, drawn rows
+    drawn = torch.randint(0, n, (nb, R), generator=g).to(dev)
+    rep_cand = torch.cat([knn[rep, :rep_local], rep[nn_b[:, :rep_near]], drawn], dim=1)
+    rep_cand = torch.where(rep_cand == rep[:, None], torch.full_like(rep_cand, -1), rep_cand)
+    out[rep] = _compact_unique(rep_cand, R)
     # back to the caller's row order
     # sorted position i is the caller's row order[i]; so are its edge targets
-    mapped = torch.where(cand >= 0, order[cand.clamp(min=0)], torch.full_like(cand, -1))
+    mapped = torch.where(out >= 0, order[out.clamp(min=0)], torch.full_like(out, -1))
     res = torch.empty_like(mapped)
     res[order] = mapped
     res_np = res.cpu().numpy()
@@ -344,6 +414,19 @@ def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch
         return graph_np, uniq.cpu().numpy().astype(np.int32), \
             order[rep].cpu().numpy().astype(np.uint32)
     return graph_np
+
+
+def entry_adjacency(seed_row: int, rows: int, degree: int, seed: int) -> np.ndarray:
+    """Adjacency of a group's entry row (its medoid, where every route of the
+    group starts): `degree` distinct rows drawn uniformly from the group, so
+    that the first expansion already reveals as many buckets as it can."""
+    rng = np.random.default_rng(seed)
+    m = min(degree, rows - 1)
+    pick = rng.choice(rows - 1, size=m, replace=False) if m > 0 else np.zeros(0, np.int64)
+    pick = pick + (pick >= seed_row)  # skip the entry row itself
+    out = np.full(degree, UINT32_MAX, dtype=np.uint32)
+    out[:m] = pick.astype(np.uint32)
+    return out
 
 
 def nearest_centre(x: torch.Tensor, centres: torch.Tensor, chunk: int = 1 << 18) -> torch.Tensor:
@@ -359,7 +442,8 @@ def nearest_centre(x: torch.Tensor, centres: torch.Tensor, chunk: int = 1 << 18)
 
 def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_values: np.ndarray,
                       num_labels: int, centres: torch.Tensor, degree: int,
-                      threshold: int = 2000, bridges: int = 4, progress=None) -> LabelIndex:
+                      threshold: int = 2000, progress=None,
+                      graph_seed: int = 6) -> LabelIndex:
     """Label-partitioned graphs for labels with more than `threshold` rows.
     `progress(msg)` (optional) is called about every 30 s of building."""
     import time
@@ -391,7 +475,7 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
         whole = len(samples) == base.shape[0] and base.dtype == torch.float32
         xg = base if whole else base[sidx].float()  # every row, in order: no copy
         graph[o:o + len(samples)], rep_cluster[l], rep_row[l] = build_group_graph(
-            xg, cluster[sidx], centres, degree, bridges, return_reps=True)
+            xg, cluster[sidx], centres, degree, seed=graph_seed + int(l), return_reps=True)
         # seed: row nearest the group mean (fp64), dataloader.cpp:7361-7406
         if xg.shape[0] * xg.shape[1] * 4 > LEAN_GROUP_BYTES:
             step = 1 << 16
@@ -407,6 +491,9 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
             xd = xg.double()
             mu = xd.mean(0, keepdim=True)
             seed_local[l] = int(((xd - mu) ** 2).sum(1).argmin())
+        # the entry row's adjacency fans out over the navigation layer
+        sl = int(seed_local[l])
+        graph[o + sl] = entry_adjacency(sl, len(samples), degree, graph_seed + 7919 * int(l))
     rep_off = np.zeros(num_labels + 1, dtype=np.int64)
     np.cumsum([len(r) for r in rep_row], out=rep_off[1:])
     return LabelIndex(num_labels, threshold, cat_freq, label_offset, label_size, row_to_sample,

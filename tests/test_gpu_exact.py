@@ -107,6 +107,34 @@ def test_exact_search_matches_oracle(gpu_ctx, eworld, place, mode, Q, with_pred)
     assert ost[:, 0].max() > 5
 
 
+@pytest.fixture(scope="module")
+def c2_shape_world(gpu_ctx):
+    """The C2 bench shape: dim 192 u8 (fixed 12-chunk rows), degree 64, tags,
+    trained k-means buckets, medoid seeds."""
+    wl = synth.small_labelled(n=9000, nq=48, dim=192, k=14, sigma=0.7, labels=6, seed=57,
+                              tags=True, dtype="u8")
+    cen = gi.train_kmeans(wl.base, 14, seed=57)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels, cen,
+                              degree=64, threshold=300)
+    return wl, li, gp.plan_queries(li, wl.query_labels).graph
+
+
+@pytest.mark.parametrize("place", list(PLACE))
+@pytest.mark.parametrize("mode,Q", [(2, 32), (2, 62), (2, 96), (0, 128)])
+def test_exact_search_degree64_c2_shape(gpu_ctx, c2_shape_world, place, mode, Q):
+    """Degree 64: lanes 32..63 of load_node/keep, the 64-bit ballot
+    compaction and admissions of more than 32 neighbours per step."""
+    wl, li, rs = c2_shape_world
+    hash_mode, nsamp = PLACE[place]
+    say("exact search degree 64", place, "mode", mode, "Q", Q)
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li)
+    oi, ost = _run(gpu_ctx, wl, li, rs, pred_o, lambda dr, dg: dr.predicate_view(dg, 0.0, False),
+                   Q, 10, mode, hash_mode, nsamp, finish=2)
+    assert (li.graph[:, 32:] != U32MAX).any(1).mean() > 0.5
+    assert ost[:, 6].max() > 32  # some step admitted more than 32 neighbours overall
+    assert (oi[:, 0] != U32MAX).sum() > rs.count // 2
+
+
 def test_exact_search_legacy_filters_and_topk1(gpu_ctx, eworld):
     wl, li, rs = eworld
     say("exact search legacy filters")

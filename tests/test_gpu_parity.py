@@ -164,6 +164,75 @@ def test_pq_search_inline_exact_matches_oracle(gpu_ctx, world, W, place):
                 assert abs(((base[i].astype(np.float64) - q) ** 2).sum() - d) <= 1e-5 * max(1.0, d)
 
 
+# ---- the shapes the benches launch: C2 (dim 192, u8, PQ M = 48, degree 64,
+# tags: traversal_kernel<PqScorer<48, 4>>) and C1 (dim 128, f32, PQ M = 32,
+# degree 32, ten labels: PqScorer<32, 4>).  Graphs are bucketed by trained
+# k-means centres and searched from each label's medoid, as the benches do.
+BENCH_SHAPES = {
+    "c2-shape": dict(dim=192, M=48, degree=64, dtype="u8", tags=True, labels=6, seed=24),
+    "c1-shape": dict(dim=128, M=32, degree=32, dtype="f32", tags=False, labels=10, seed=25),
+}
+
+
+@pytest.fixture(scope="module", params=list(BENCH_SHAPES))
+def bench_world(request):
+    cfg = BENCH_SHAPES[request.param]
+    wl = synth.small_labelled(n=9000, nq=40, dim=cfg["dim"], k=14, sigma=0.7,
+                              labels=cfg["labels"], seed=cfg["seed"], dtype=cfg["dtype"],
+                              tags=cfg["tags"])
+    cen = gi.train_kmeans(wl.base, 14, seed=cfg["seed"])
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels, cen,
+                              degree=cfg["degree"], threshold=300)
+    pl = gp.plan_queries(li, wl.query_labels)
+    table, codes = _pq(wl, cfg["M"])
+    return request.param, cfg, wl, li, pl, table, codes
+
+
+BENCH_PLACES = ["auto", "lds-lds-nsamp", "direct-spill-nsamp", "direct-global-nsamp",
+                "auto-records", "lds-records-overflow"]
+
+
+@pytest.mark.parametrize("place", BENCH_PLACES)
+@pytest.mark.parametrize("mode", ["adaptive-bias", "inline-exact", "fixed-nobias"])
+def test_pq_search_bench_shapes_match_oracle(gpu_ctx, bench_world, place, mode):
+    kind, cfg, wl, li, pl, table, codes = bench_world
+    table_mode, hash_mode, nsamp, rec = PLACEMENTS[place]
+    say("pq_search bench shape", kind, mode, place)
+    rs = pl.graph
+    inline = mode == "inline-exact"
+    bias = mode != "fixed-nobias"
+    Q, W = (64, 10) if inline else (96, 100)
+    es = 0 if mode == "fixed-nobias" else 2
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15 if bias else 0.0,
+                                          pending_base_stop=bias)
+    prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=es, finish_limit=3,
+                      bias=bias, inline_exact=inline)
+    base = wl.base.numpy()
+    oi, od, ost = po.pq_search(li, rs, pred_o, prm_o, codes.numpy(), table.numpy(),
+                               wl.queries.numpy(), base=base if inline else None)
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
+    dr = gs.DeviceRoutes.upload(rs)
+    records = records_for(codes, li, rec)
+    keep = (records if records is not None else codes.cuda(), table.cuda()) + \
+        ((wl.base.cuda(),) if inline else ())
+    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=es, finish_limit=3,
+                           bias=bias, inline_exact=inline, table_mode=table_mode,
+                           hash_mode=hash_mode)
+    ids, dists, st = gs.run_pq_routes(gpu_ctx, gs.pq_view(*keep), wl.queries.cuda(), dg, dr, prm,
+                                      alpha=0.15 if bias else 0.0, pending_base_stop=bias,
+                                      records=records)
+    torch.cuda.synchronize()
+    say("routes", rs.count, gpu_ctx.last_placement())
+    assert np.array_equal(as_u32(ids).reshape(rs.count, W), oi), "route ids differ"
+    assert np.array_equal(dists.cpu().numpy().reshape(rs.count, W).view(np.uint32),
+                          od.view(np.uint32)), "distances differ in bits"
+    assert np.array_equal(st.cpu().numpy().reshape(rs.count, 8), ost), "counters differ"
+    assert (oi[:, 0] != U32MAX).sum() > rs.count // 2
+    if cfg["degree"] == 64:
+        # lanes 32..63 of the adjacency row carry live neighbours
+        assert (li.graph[:, 32:] != U32MAX).any(1).mean() > 0.5
+
+
 @pytest.fixture(scope="module")
 def long_world():
     """One 12k-row label graph, degree 64, and PQ codes that are all zero:

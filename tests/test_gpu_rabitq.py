@@ -145,9 +145,10 @@ def test_rabitq_score_ip_exact(gpu_ctx, rworld, P):
         assert np.float32(d[i].item()) == np.float32(want)
 
 
-# Q = 40 keeps the frontier in registers (Q + 2 <= 64), Q = 96 in LDS.
-@pytest.mark.parametrize("Q", [40, 96])
-@pytest.mark.parametrize("P", [128, 2048, 4096])
+# Q = 16 (C4's beam) and 40 keep the frontier in registers (Q + 2 <= 64),
+# Q = 96 in LDS; P = 512 is C4's 64-byte code.
+@pytest.mark.parametrize("Q", [16, 40, 96])
+@pytest.mark.parametrize("P", [128, 512, 2048, 4096])
 @pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("hash_mode,nsamp", [(_lib.PLACE_AUTO, False), (_lib.PLACE_LDS, True),
                                              (_lib.PLACE_GLOBAL, True), (_lib.PLACE_SPILL, False)])
