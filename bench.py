@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--queries", type=int, default=100_000)
     ap.add_argument("--gt-queries", type=int, default=2000)
     ap.add_argument("--queue", type=int, default=0, help="beam width; 0 = ladder search")
-    ap.add_argument("--ladder", default="32,48,64,96,128,192,256,384")
+    ap.add_argument("--ladder", default="64,96,128,160,192,256,384")
     ap.add_argument("--target-recall", type=float, default=0.90)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -73,13 +73,20 @@ def parse():
     ap.add_argument("--n-c4", type=int, default=100_000_000)
     ap.add_argument("--queries-c4", type=int, default=10_000)
     ap.add_argument("--gt-queries-c4", type=int, default=1000)
-    ap.add_argument("--c4-ladder", default="16,24,32,48,64,96,128,192")
+    ap.add_argument("--c4-ladder", default="16,32,64,96,128,192,256,384,512,768,1024")
+    ap.add_argument("--c4-coarse-ladder", default="16,24,32,48,64,96,128,192")
+    ap.add_argument("--c4-local", type=int, default=8,
+                    help="in-bucket links per row of the C4 graphs (the rest are drawn)")
+    ap.add_argument("--no-c4", action="store_true",
+                    help="the default C2 run skips its C4 leg")
     ap.add_argument("--c4-threshold", type=int, default=50_000,
                     help="labels with at most this many rows are posting routes")
     ap.add_argument("--n-c3", type=int, default=2_700_000)
     ap.add_argument("--queries-c3", type=int, default=10_000)
     ap.add_argument("--gt-queries-c3", type=int, default=999)
-    ap.add_argument("--c3-ladder", default="64,96,128,192,256,384,512")
+    ap.add_argument("--c3-ladder", default="32,48,64,96,128,192,256,384,512")
+    ap.add_argument("--c3-local", type=int, default=12,
+                    help="in-bucket links per row of the C3 graph (the rest are drawn)")
     ap.add_argument("--c3-scan-rows", type=int, default=20_000,
                     help="ranges whose smallest posting slice has at most this many rows are "
                          "scanned; wider ones search the graph with the range predicate")
@@ -88,9 +95,11 @@ def parse():
                          "posting-order copies")
     ap.add_argument("--no-rabitq-prep", action="store_true",
                     help="skip the RaBitQ query-preparation (rotation GEMM) measurement")
+    ap.add_argument("--no-coarse-entry", action="store_true",
+                    help="skip the extra rows whose routes start at coarse-quantizer entries")
     ap.add_argument("--no-exact-route", action="store_true",
                     help="skip the full-GPU exact route measurement")
-    ap.add_argument("--exact-ladder", default="32,48,64,96,128,192,256",
+    ap.add_argument("--exact-ladder", default="32,48,64,80,96,128,192,256",
                     help="beam widths tried for the exact route")
     ap.add_argument("--rerank-threads", type=int, default=16,
                     help="host rerank workers (the GPU box's CPU share is 16 threads)")
@@ -124,7 +133,7 @@ def build_world(args, torch):
     pl = gp.plan_queries(li, wl.query_labels)
     log(f"plan: {pl.graph.count} graph routes, {pl.posting.count} posting routes "
         f"in {time.time() - t0:.1f}s")
-    return wl, li, table, codes, pl
+    return wl, li, table, codes, pl, cen
 
 
 def ground_truth(wl, li, torch, nq, seed=7):
@@ -324,12 +333,16 @@ class ExactRoute:
     an exact-distance u8 beam (gofann_exact_search) emitting its exact top-10;
     posting routes and the per-query merge are the pipeline's own."""
 
-    def __init__(self, pipe, li):
+    def __init__(self, pipe, li, entry=None):
         gs = pipe.gs
         self.pipe, self.gs = pipe, gs
         self.ls = gs.u32(li.label_size)
         self.pv = pipe.dr_graph.predicate_view(pipe.dg, 0.0, False)
         self.rv = pipe.dr_graph.routes_view()
+        # entry=None: every route starts at its label's medoid (the
+        # reference's rule); a gs.CoarseEntry picks entry rows inside step()
+        self.entry = entry
+        self.seed_buf = pipe.dr_graph.route_start.clone()
         self.stats = pipe.torch.zeros(max(pipe.n_graph, 1) * 8, dtype=pipe.torch.int32,
                                       device="cuda")
         self.ev = [pipe.torch.cuda.Event(enable_timing=True) for _ in range(2)]
@@ -343,13 +356,19 @@ class ExactRoute:
         L = gs._lib
         ng, npost = p.n_graph, p.n_post
         prm = L.ExactParams(Q, self.stop[1], self.stop[0], self.max_steps, 10, p.hash_mode)
+        rv = self.rv
+        if self.entry is not None and ng:
+            near = self.entry.nearest(p.q)
+            self.entry.seeds(near, p.dr_graph.route_query, p.dr_graph.route_group,
+                             out=self.seed_buf)
+            rv = p.dr_graph.routes_view(start=self.seed_buf)
         if timed_kernel:
             self.ev[0].record()
         if ng:
             p.ctx.check(p.ctx.lib.gofann_exact_search(
                 p.ctx.handle, L.ptr(p.wl.base), L.ELEM_U8, int(p.wl.base.shape[1]),
                 int(p.wl.base.shape[0]), L.ptr(p.q), p.dg.view(), L.ptr(self.ls), self.pv,
-                self.rv, prm, L.ptr(p.fin_i), L.ptr(p.fin_d), L.ptr(self.stats)))
+                rv, prm, L.ptr(p.fin_i), L.ptr(p.fin_d), L.ptr(self.stats)))
         if timed_kernel:
             self.ev[1].record()
         if npost:
@@ -571,7 +590,7 @@ def build_world_c3(args, torch):
     t0 = time.time()
     cen = gi.train_kmeans(wl.base, 512, seed=3006)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, 1, cen,
-                              degree=32, threshold=0, progress=log)
+                              degree=32, threshold=0, progress=log, local=args.c3_local)
     log(f"C3 graph: {li.rows} rows, degree {li.degree} in {time.time() - t0:.1f}s")
     t0 = time.time()
     P = wl.dim
@@ -580,7 +599,7 @@ def build_world_c3(args, torch):
     torch.cuda.synchronize()
     log(f"C3 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
     rpi = rp.RangePostingIndex.build(wl.base_ranges)
-    return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), rpi
+    return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), rpi, cen
 
 
 def ground_truth_c3(wl, torch, nq):
@@ -629,11 +648,22 @@ class RabitqRangePipeline:
         gq = np.nonzero(~post)[0].astype(np.uint32)
         pq = np.nonzero(post)[0].astype(np.uint32)
         self.ng, self.np_ = len(gq), len(pq)
-        # graph routes: one per wide-range query, seeded at the graph's medoid
+        # graph routes: one per wide-range query, seeded at the graph's medoid;
+        # ordered by selectivity class so that each class is one route range
+        sel = np.asarray(wl.meta["selectivity"], dtype=np.float64)
+        levels = sorted(set(float(x) for x in sel))
+        cls_of = {v: i for i, v in enumerate(levels)}
+        gq = np.array(sorted(gq.tolist(), key=lambda q: (cls_of[float(sel[q])], q)),
+                      dtype=np.uint32)
         rows = [(int(q), 0, [], [tuple(wl.query_ranges[q][0])]) for q in gq]
         self.graph_rows = rows
         rs = gp._routeset(rows, li)
         self.rs = rs
+        self.levels = levels
+        bounds = np.searchsorted([cls_of[float(sel[q])] for q in gq], np.arange(len(levels) + 1))
+        self.classes = [(int(bounds[i]), int(bounds[i + 1])) for i in range(len(levels))]
+        self.route_class = lambda row: cls_of[float(sel[row[0]])]
+        self.entry = None  # gs.CoarseEntry: per-route entry rows picked in step()
         self.dg = gs.DeviceGraph.upload(li)
         self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
         # posting routes: the smallest slice, in segments
@@ -676,8 +706,11 @@ class RabitqRangePipeline:
         off, order = gs.query_route_csr(r2q, nq)
         self.q_off, self.q_routes = gs.u32(off), gs.u32(order)
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        self.seed_buf = self.dr.route_start.clone()
 
-    def step(self, Q: int, timed=False):
+    def step(self, Q, timed=False):
+        """One step; Q is one beam for every graph route, or one beam per
+        route class (self.classes)."""
         L, gs, ctx, W = self.L, self.gs, self.ctx, self.W
         ev = self.ev
         if timed:
@@ -685,14 +718,25 @@ class RabitqRangePipeline:
         ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, self.rv,
                                                         L.ptr(self.wl.queries), self.nq,
                                                         L.ptr(self.dev["rot"]), self.rq))
+        start = None
+        if self.entry is not None and self.ng:
+            # the anchors are the trained centres, rotated: the preparation's
+            # query-anchor distances already rank them
+            near = self.prep["cd"].argmin(1)
+            start = self.entry.seeds(near, self.dr.route_query, self.dr.route_group,
+                                     out=self.seed_buf)
         if timed:
             ev[1].record()
-        if self.ng:
-            prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=True)
-            ctx.check(ctx.lib.gofann_rabitq_search(
-                ctx.handle, self.rv, self.rq, self.dg.view(),
-                self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(), prm,
-                L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
+        pv = self.dr.predicate_view(self.dg, 0.15, True)
+        qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
+        for (lo, hi), q in zip(self.classes, qs):
+            if hi > lo:
+                prm = gs.search_params(queue_limit=q, result_width=W, early_stop_mode=2,
+                                       bias=True)
+                ctx.check(ctx.lib.gofann_rabitq_search(
+                    ctx.handle, self.rv, self.rq, self.dg.view(), pv,
+                    self.dr.routes_view(lo, hi, start=start), prm,
+                    L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
         if timed:
             ev[2].record()
         if self.np_:
@@ -774,12 +818,20 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, threads=1):
         sel = list(range(done, min(nq, done + chunk)))
         lists, r2q = [], []
         rows = [r for q in sel for r in by_q.get(q, [])]
-        if rows:
-            rs = gp._routeset(rows, li)
+        # pipe.chosen: one beam, or one beam per route class
+        if isinstance(pipe.chosen, tuple):
+            classes = [([r for r in rows if pipe.route_class(r) == c], qc)
+                       for c, qc in enumerate(pipe.chosen)]
+        else:
+            classes = [(rows, pipe.chosen)]
+        for rows_c, Qc in classes:
+            if not rows_c:
+                continue
+            rs = gp._routeset(rows_c, li)
             pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
                                                 pending_base_stop=True,
                                                 base_ranges=wl.base_ranges)
-            ids, _, _ = po.rabitq_search(li, rs, pred, po.params(queue_limit=pipe.chosen,
+            ids, _, _ = po.rabitq_search(li, rs, pred, po.params(queue_limit=Qc,
                                                                  result_width=W,
                                                                  early_stop_mode=2, bias=True,
                                                                  rabitq_verdict=1),
@@ -832,94 +884,73 @@ def cpu_line(rate, done, el, what, threads):
                       f"threads (oracle C code, OpenMP, -O3 -march=x86-64-v3)"}
 
 
+def run_c3(args, torch, ctx) -> dict:
+    """The C3 configuration end to end: the medoid-seeded route set (one
+    beam per selectivity class) and, as an extra row, coarse entries picked
+    inside the step."""
+    from gofann_amd import search as gs
+    wl, li, rq, rpi, cen = build_world_c3(args, torch)
+    t0 = time.time()
+    gt = ground_truth_c3(wl, torch, args.gt_queries_c3)
+    log(f"C3 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
+    pipe = RabitqRangePipeline(ctx, wl, li, rq, rpi, torch, args.c3_scan_rows,
+                               resident_copies=not args.c3_gather)
+    pipe.P, pipe.li = rq["P"], li
+    log(f"C3 routes: {pipe.ng} graph (wide ranges), {pipe.np_} range-posting scans "
+        f"({pipe.scan_rows_total} rows)")
+    sel = np.asarray(wl.meta["selectivity"], dtype=np.float64)
+    class_gt = [(f"{100 * v:g}%", {q: g for q, g in gt.items() if float(sel[q]) == v})
+                for v in pipe.levels]
+    ladder = [args.queue] if args.queue else [int(x) for x in args.c3_ladder.split(",")]
+    med = rabitq_leg(args, pipe, class_gt, ladder, "C3 medoid seed", c3_kernels)
+    med["seeds"] = "graph medoid"
+    coarse = None
+    if not args.no_coarse_entry:
+        pipe.entry = gs.CoarseEntry(li, cen)
+        coarse = rabitq_leg(args, pipe, class_gt, ladder, "C3 coarse entry", c3_kernels)
+        coarse["seeds"] = ("per route: representative of the bucket of the nearest of 512 "
+                           "trained centres (from the preparation's query-anchor distances), "
+                           "inside the step")
+        pipe.entry = None
+    cpu = None
+    if not args.no_cpu_baseline:
+        qb = med["queue_by_class"]
+        pipe.chosen = tuple(qb[n] for n, _ in class_gt)
+        T = host_threads()
+        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds, threads=T)
+        cpu = cpu_line(cr, cn, cel, "graph routes at each class's beam, range-posting scans, "
+                                    "exact fp32 rerank, merge", T)
+        log(f"C3 cpu baseline {cr:.1f} qps over {cn} queries")
+    return {"workload": "C3: 2.7Mx4096 fp32 unit-norm mixture, RaBitQ 1-bit (512 B codes), "
+                        "graph R=32, int32 attribute U[0,10000), ranges at 0.5/5/50%, exact "
+                        "fp32 rerank of 200, top-10",
+            "n": wl.n, "queries": pipe.nq, "graph_routes": pipe.ng,
+            "range_posting_routes": pipe.np_, "scan_rows": pipe.scan_rows_total,
+            "shortlist": pipe.W, "gt_queries": len(gt),
+            "graph_buckets": "512 k-means centres trained on the base",
+            "data_model": "centre + rank-64 shared-basis spread 0.7 + N(0, 0.05^2), normalised",
+            "medoid_seeds": med, "coarse_entry": coarse, "cpu_baseline": cpu}
+
+
 def main_c3(args):
     import torch
     from gofann_amd import _lib
     torch.cuda.init()
-    wl, li, rq, rpi = build_world_c3(args, torch)
-    t0 = time.time()
-    gt = ground_truth_c3(wl, torch, args.gt_queries_c3)
-    log(f"C3 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     ctx = _lib.Context(0)
-    pipe = RabitqRangePipeline(ctx, wl, li, rq, rpi, torch, args.c3_scan_rows,
-                               resident_copies=not args.c3_gather)
-    log(f"C3 routes: {pipe.ng} graph (wide ranges), {pipe.np_} range-posting scans "
-        f"({pipe.scan_rows_total} rows)")
-    ladder = [args.queue] if args.queue else [int(x) for x in args.c3_ladder.split(",")]
-    chosen, rec = ladder[-1], 0.0
-    nq = wl.queries.shape[0]
-    for Q in ladder:
-        out = pipe.step(Q)
-        torch.cuda.synchronize()
-        rec = recall_at_10(out.cpu().numpy().view(np.uint32).reshape(nq, 10), gt)
-        log(f"C3 Q={Q}: recall@10={rec:.4f}")
-        chosen = Q
-        if rec >= args.target_recall:
-            break
-    for _ in range(args.warmup):
-        pipe.step(chosen)
-    torch.cuda.synchronize()
-    stages = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        out = pipe.step(chosen, timed=True)
-        torch.cuda.synchronize()
-        stages.append(pipe.stage_ms())
-    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
-    res = out.cpu().numpy().view(np.uint32).reshape(nq, 10)
-    rec = recall_at_10(res, gt)
-    sel = wl.meta["selectivity"]
-    by_sel = {}
-    for s in sorted(set(sel.tolist())):
-        qs = {q: v for q, v in gt.items() if sel[q] == s}
-        by_sel[f"{100 * s:g}%"] = round(recall_at_10(res, qs), 4) if qs else None
-    st_ms = {k: round(float(np.mean([d[k] for d in stages])), 3) for k in stages[0]}
-    st = pipe.route_stats()
-    P = rq["P"]
-    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
-    sb = pipe.scan_rows_total * (4 + P // 8 + 4 + 8) + 0.0  # posting id + C per row
-    rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 4 + 4) + 0.0
-    kern = {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
-            "range_scan_group_kernel+segment_merge_kernel (range postings)": (st_ms["range_scan"], sb),
-            "exact_rerank_kernel (f32)": (st_ms["rerank"], rb)}
-    per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
-               "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None}
-           for k, v in kern.items()}
-    top = max(kern, key=lambda k: kern[k][0])
-    ach = kern[top][1] / (kern[top][0] / 1000.0) / 1e9
-    log(f"C3 step {ms:.1f} ms, stages {st_ms}, recall {rec:.4f} {by_sel}")
+    c3 = run_c3(args, torch, ctx)
+    med = c3["medoid_seeds"]
     line = {
         "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
-        "value": round(nq / (ms / 1000.0), 1),
-        "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u8 codes / f32 rerank", "data": "synthetic",
-        "config": {"workload": "C3: 2.7Mx4096 fp32 unit-norm mixture, RaBitQ 1-bit (512 B "
-                               "codes), graph R=32, int32 attribute U[0,10000), ranges at "
-                               "0.5/5/50%, exact fp32 rerank of 200, top-10",
-                   "n": wl.n, "queries": nq, "graph_routes": pipe.ng,
-                   "range_posting_routes": pipe.np_, "scan_rows": pipe.scan_rows_total,
-                   "queue": chosen, "shortlist": pipe.W, "recall_at_10": round(rec, 4),
-                   "recall_by_selectivity": by_sel, "gt_queries": len(gt),
-                   "stage_ms": st_ms, "kernels": per, "placement": ctx.last_placement(),
-                   "data_model": "centre + rank-64 shared-basis spread 0.7 + N(0, 0.05^2), "
-                                 "normalised"},
-        "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
-                     "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5), "traffic": None,
-                     "kernel": top, "kernel_ms": kern[top][0],
-                     "algorithmic_bytes": kern[top][1]},
-        "cpu_baseline": None,
+        "value": med["qps"], "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": med["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8 codes / f32 rerank",
+        "data": "synthetic",
+        "config": {k: v for k, v in c3.items() if k != "cpu_baseline"},
+        "roofline": med["roofline"],
+        "cpu_baseline": c3["cpu_baseline"],
     }
-    if not args.no_cpu_baseline:
-        pipe.chosen = chosen
-        T = host_threads()
-        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds, threads=T)
-        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph routes at the chosen Q, range-posting "
-                                        "scans, exact fp32 rerank, merge", T)
-        log(f"cpu baseline {cr:.1f} qps over {cn} queries")
     print(json.dumps(line), flush=True)
     ctx.close()
-
 
 
 # ---------------------------------------------------------------------------
@@ -935,8 +966,11 @@ def build_world_c4(args, torch):
     log(f"C4 data {wl.n}x{wl.dim} fp16, {wl.queries.shape[0]} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     cen = gi.train_kmeans(wl.base, 4096, seed=4006)
+    # degree 32 over 4096 clusters: most of each row's links are drawn ones,
+    # which is what finds a query's cluster from the medoid
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              cen, degree=32, threshold=args.c4_threshold, progress=log)
+                              cen, degree=32, threshold=args.c4_threshold, progress=log,
+                              local=args.c4_local)
     torch.cuda.empty_cache()
     ng = int((li.label_size > 0).sum())
     log(f"C4 graphs: {ng} label/interval groups, {li.rows} rows, degree {li.degree} in "
@@ -947,7 +981,7 @@ def build_world_c4(args, torch):
     codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, cen, chunk=1 << 18)
     torch.cuda.synchronize()
     log(f"C4 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
-    return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P)
+    return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), cen
 
 
 def ground_truth_c4(wl, torch, nq, chunk=1 << 20):
@@ -1020,12 +1054,19 @@ class RabitqLabelPipeline:
                 inside = starts[i] >= lo and starts[i + 1] <= hi
                 self.interior += int(inside)
                 graph_rows.append((q, cats + i, [], [] if inside else [(0, 3, lo, hi)]))
+        # by (label, query): category routes (labels < cats) come first, so
+        # the equality and range classes are two contiguous route ranges
         graph_rows.sort(key=lambda r: (r[1], r[0]))
         self.graph_rows, self.post_rows = graph_rows, post_rows
         rs = gp._routeset(graph_rows, li)
         ps = gp._routeset(post_rows, li)
         self.rs, self.ps = rs, ps
         self.ng, self.np_ = rs.count, ps.count
+        self.n_eq = int((rs.route_group < cats).sum()) if rs.count else 0
+        self.cats = cats
+        self.classes = [(0, self.n_eq), (self.n_eq, self.ng)]
+        self.route_class = lambda row: 0 if row[1] < cats else 1
+        self.entry = None  # gs.CoarseEntry: per-route entry rows picked in step()
         self.dg = gs.DeviceGraph.upload(li)
         self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
         self.dp = gs.DeviceRoutes.upload(ps)
@@ -1057,8 +1098,11 @@ class RabitqLabelPipeline:
         off_q, order = gs.query_route_csr(r2q, nq)
         self.q_off, self.q_routes = gs.u32(off_q), gs.u32(order)
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        self.seed_buf = self.dr.route_start.clone()
 
-    def step(self, Q: int, timed=False):
+    def step(self, Q, timed=False):
+        """One step; Q is one beam for every graph route, or (equality beam,
+        range beam) for the two route classes."""
         L, gs, ctx, W = self.L, self.gs, self.ctx, self.W
         ev = self.ev
         if timed:
@@ -1066,14 +1110,25 @@ class RabitqLabelPipeline:
         ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, self.rv,
                                                         L.ptr(self.wl.queries), self.nq,
                                                         L.ptr(self.dev["rot"]), self.rq))
+        start = None
+        if self.entry is not None and self.ng:
+            # the anchors are the trained centres, rotated: the preparation's
+            # query-anchor distances already rank them
+            near = self.prep["cd"].argmin(1)
+            start = self.entry.seeds(near, self.dr.route_query, self.dr.route_group,
+                                     out=self.seed_buf)
         if timed:
             ev[1].record()
-        if self.ng:
-            prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=True)
-            ctx.check(ctx.lib.gofann_rabitq_search(
-                ctx.handle, self.rv, self.rq, self.dg.view(),
-                self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(), prm,
-                L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
+        pv = self.dr.predicate_view(self.dg, 0.15, True)
+        qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
+        for (lo, hi), q in zip(self.classes, qs):
+            if hi > lo:
+                prm = gs.search_params(queue_limit=q, result_width=W, early_stop_mode=2,
+                                       bias=True)
+                ctx.check(ctx.lib.gofann_rabitq_search(
+                    ctx.handle, self.rv, self.rq, self.dg.view(), pv,
+                    self.dr.routes_view(lo, hi, start=start), prm,
+                    L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
         if timed:
             ev[2].record()
         if self.np_:
@@ -1105,30 +1160,28 @@ class RabitqLabelPipeline:
         return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
 
 
-def main_c4(args):
-    import torch
-    from gofann_amd import _lib
-    torch.cuda.init()
-    wl, li, rq = build_world_c4(args, torch)
-    t0 = time.time()
-    gt = ground_truth_c4(wl, torch, args.gt_queries_c4)
-    log(f"C4 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
-    ctx = _lib.Context(0)
-    t0 = time.time()
-    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch)
-    log(f"C4 routes: {pipe.ng} graph ({pipe.interior} interior intervals), {pipe.np_} "
-        f"label-posting scans ({pipe.post_rows_total} rows), planned in {time.time() - t0:.1f}s")
-    ladder = [args.queue] if args.queue else [int(x) for x in args.c4_ladder.split(",")]
-    chosen, rec = ladder[-1], 0.0
-    nq = wl.queries.shape[0]
+def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
+    """Smallest beam per route class (pipe.classes, named with ground truth
+    in class_gt) that reaches the target recall on that class's queries,
+    then the timed steps at those beams.  A class without graph routes
+    takes the first rung (its recall does not depend on the beam)."""
+    torch = pipe.torch
+    nq = pipe.nq
+    gt = {q: v for _, g in class_gt for q, v in g.items()}
+    chosen = [None if hi > lo else ladder[0] for lo, hi in pipe.classes]
     for Q in ladder:
         out = pipe.step(Q)
         torch.cuda.synchronize()
-        rec = recall_at_10(out.cpu().numpy().view(np.uint32).reshape(nq, 10), gt)
-        log(f"C4 Q={Q}: recall@10={rec:.4f}")
-        chosen = Q
-        if rec >= args.target_recall:
+        res = out.cpu().numpy().view(np.uint32).reshape(nq, 10)
+        recs = [recall_at_10(res, g) if g else None for _, g in class_gt]
+        log(f"{label} Q={Q}: recall@10 " + ", ".join(
+            f"{n} {r:.4f}" for (n, _), r in zip(class_gt, recs) if r is not None))
+        for i, r in enumerate(recs):
+            if chosen[i] is None and (r is None or r >= args.target_recall):
+                chosen[i] = Q
+        if all(c is not None for c in chosen):
             break
+    chosen = tuple(c if c is not None else ladder[-1] for c in chosen)
     for _ in range(args.warmup):
         pipe.step(chosen)
     torch.cuda.synchronize()
@@ -1141,60 +1194,122 @@ def main_c4(args):
     ms = (time.perf_counter() - t0) * 1000.0 / args.steps
     res = out.cpu().numpy().view(np.uint32).reshape(nq, 10)
     rec = recall_at_10(res, gt)
-    rec_eq = recall_at_10(res, {q: v for q, v in gt.items() if wl.query_labels[q]})
-    rec_rg = recall_at_10(res, {q: v for q, v in gt.items() if not wl.query_labels[q]})
+    by_class = {n: round(recall_at_10(res, g), 4) if g else None for n, g in class_gt}
     st_ms = {k: round(float(np.mean([d[k] for d in stages])), 3) for k in stages[0]}
     st = pipe.route_stats()
-    E = st[:, 1].astype(np.float64)
-    log(f"C4 expansions per graph route: mean {E.mean():.1f}, p50 {np.percentile(E, 50):.0f}, "
-        f"p99 {np.percentile(E, 99):.0f}, max {E.max():.0f}; scored per route "
-        f"{st[:, 3].astype(np.float64).mean():.1f}")
-    P = rq["P"]
-    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
-    pb = pipe.post_rows_total * (4 + P // 8 + 4 + 8) + 0.0
-    rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 2 + 4) + 0.0
-    kern = {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
-            "range_scan_group_kernel+segment_merge_kernel (label postings)": (st_ms["posting_scan"], pb),
-            "exact_rerank_kernel (f16)": (st_ms["rerank"], rb)}
+    E = st[:, 1].astype(np.float64) if len(st) else np.zeros(1)
+    log(f"{label}: expansions per graph route: mean {E.mean():.1f}, p50 "
+        f"{np.percentile(E, 50):.0f}, p99 {np.percentile(E, 99):.0f}; scored per route "
+        f"{(st[:, 3].astype(np.float64).mean() if len(st) else 0):.1f}")
+    kern = kernels(pipe, st_ms, st)
     per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
                "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None}
            for k, v in kern.items()}
     top = max(kern, key=lambda k: kern[k][0])
     ach = kern[top][1] / (kern[top][0] / 1000.0) / 1e9
-    log(f"C4 step {ms:.1f} ms, stages {st_ms}, recall {rec:.4f} (equality {rec_eq:.4f}, "
-        f"range {rec_rg:.4f})")
-    line = {
-        "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
-        "value": round(nq / (ms / 1000.0), 1),
-        "unit": "queries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "u8 codes / f16 rerank", "data": "synthetic",
-        "config": {"workload": "C4: 100Mx512 fp16 unit-norm 4096-centre mixture, RaBitQ 1-bit "
-                               "(64 B codes), graph R=32 per label and per 1% attribute "
-                               "interval, label Zipf(1.1) over 1000, uint32 attribute "
-                               "U[0,2^24), equality or 1-10% range, fp16->fp32 rerank of 100, "
-                               "top-10",
-                   "n": wl.n, "queries": nq, "graph_routes": pipe.ng,
-                   "interior_interval_routes": pipe.interior,
-                   "posting_routes": pipe.np_, "posting_rows": pipe.post_rows_total,
-                   "queue": chosen, "shortlist": pipe.W, "recall_at_10": round(rec, 4),
-                   "recall_equality": round(rec_eq, 4), "recall_range": round(rec_rg, 4),
-                   "gt_queries": len(gt), "stage_ms": st_ms, "kernels": per,
-                   "placement": ctx.last_placement()},
-        "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
-                     "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5), "traffic": None,
-                     "kernel": top, "kernel_ms": kern[top][0],
-                     "algorithmic_bytes": kern[top][1]},
-        "cpu_baseline": None,
-    }
+    log(f"{label}: step {ms:.1f} ms, stages {st_ms}, recall {rec:.4f} {by_class}, "
+        f"beams {dict(zip([n for n, _ in class_gt], chosen))}")
+    return {"qps": round(nq / (ms / 1000.0), 1), "ms_per_step": round(ms, 3),
+            "queue_by_class": dict(zip([n for n, _ in class_gt], chosen)),
+            "recall_at_10": round(rec, 4), "recall_by_class": by_class,
+            "expansions_per_route": round(float(E.mean()), 1), "stage_ms": st_ms,
+            "kernels": per, "placement": pipe.ctx.last_placement(),
+            "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
+                         "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5), "traffic": None,
+                         "kernel": top, "kernel_ms": kern[top][0],
+                         "algorithmic_bytes": kern[top][1]}}
+
+
+def c4_kernels(pipe, st_ms, st):
+    P, wl, li = pipe.P, pipe.wl, pipe.li
+    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
+    pb = pipe.post_rows_total * (4 + P // 8 + 4 + 8) + 0.0
+    rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 2 + 4) + 0.0
+    return {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
+            "range_scan_group_kernel+segment_merge_kernel (label postings)":
+                (st_ms["posting_scan"], pb),
+            "exact_rerank_kernel (f16)": (st_ms["rerank"], rb)}
+
+
+def c3_kernels(pipe, st_ms, st):
+    P, wl, li = pipe.P, pipe.wl, pipe.li
+    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
+    sb = pipe.scan_rows_total * (4 + P // 8 + 4 + 8) + 0.0  # posting id + C per row
+    rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 4 + 4) + 0.0
+    return {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
+            "range_scan_group_kernel+segment_merge_kernel (range postings)":
+                (st_ms["range_scan"], sb),
+            "exact_rerank_kernel (f32)": (st_ms["rerank"], rb)}
+
+
+def run_c4(args, torch, ctx) -> dict:
+    """The C4 configuration end to end: build, ground truth, the medoid-seeded
+    route set (the reference's seed rule) and, as an extra row, the same
+    routes entered at coarse-quantizer entries picked inside the step."""
+    from gofann_amd import search as gs
+    wl, li, rq, cen = build_world_c4(args, torch)
+    t0 = time.time()
+    gt = ground_truth_c4(wl, torch, args.gt_queries_c4)
+    log(f"C4 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch)
+    pipe.P, pipe.li = rq["P"], li
+    log(f"C4 routes: {pipe.ng} graph ({pipe.n_eq} equality, {pipe.interior} interior "
+        f"intervals), {pipe.np_} label-posting scans ({pipe.post_rows_total} rows), planned "
+        f"in {time.time() - t0:.1f}s")
+    ladder = [args.queue] if args.queue else [int(x) for x in args.c4_ladder.split(",")]
+    class_gt = [("equality", {q: v for q, v in gt.items() if wl.query_labels[q]}),
+                ("range", {q: v for q, v in gt.items() if not wl.query_labels[q]})]
+    med = rabitq_leg(args, pipe, class_gt, ladder, "C4 medoid seeds", c4_kernels)
+    med["seeds"] = "label medoid"
+    coarse = None
+    if not args.no_coarse_entry:
+        pipe.entry = gs.CoarseEntry(li, cen)
+        coarse = rabitq_leg(args, pipe, class_gt,
+                            [int(x) for x in args.c4_coarse_ladder.split(",")],
+                            "C4 coarse entry", c4_kernels)
+        coarse["seeds"] = ("per route: representative of the bucket of the nearest of 4096 "
+                           "trained centres (from the preparation's query-anchor distances), "
+                           "inside the step")
+        pipe.entry = None
+    cpu = None
     if not args.no_cpu_baseline:
-        pipe.chosen = chosen
+        pipe.chosen = (med["queue_by_class"]["equality"], med["queue_by_class"]["range"])
         T = host_threads()
         cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds, threads=T)
-        line["cpu_baseline"] = cpu_line(cr, cn, cel, "graph and interval routes at the chosen Q, "
-                                        "label-posting scans, exact fp16 rerank, merge", T)
-        log(f"cpu baseline {cr:.1f} qps over {cn} queries")
+        cpu = cpu_line(cr, cn, cel, "graph and interval routes at the chosen beams, "
+                                    "label-posting scans, exact fp16 rerank, merge", T)
+        log(f"C4 cpu baseline {cr:.1f} qps over {cn} queries")
+    return {"workload": "C4: 100Mx512 fp16 unit-norm 4096-centre mixture, RaBitQ 1-bit (64 B "
+                        "codes), graph R=32 per label and per 1% attribute interval, label "
+                        "Zipf(1.1) over 1000, uint32 attribute U[0,2^24), equality or 1-10% "
+                        "range, fp16->fp32 rerank of 100, top-10",
+            "n": wl.n, "queries": pipe.nq, "graph_routes": pipe.ng,
+            "interior_interval_routes": pipe.interior, "posting_routes": pipe.np_,
+            "posting_rows": pipe.post_rows_total, "shortlist": pipe.W, "gt_queries": len(gt),
+            "graph_buckets": "4096 k-means centres trained on the base",
+            "medoid_seeds": med, "coarse_entry": coarse, "cpu_baseline": cpu}
+
+
+def main_c4(args):
+    import torch
+    from gofann_amd import _lib
+    torch.cuda.init()
+    ctx = _lib.Context(0)
+    c4 = run_c4(args, torch, ctx)
+    med = c4["medoid_seeds"]
+    line = {
+        "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
+        "value": med["qps"], "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": med["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8 codes / f16 rerank",
+        "data": "synthetic",
+        "config": {k: v for k, v in c4.items() if k != "cpu_baseline"},
+        "roofline": med["roofline"],
+        "cpu_baseline": c4["cpu_baseline"],
+    }
     print(json.dumps(line), flush=True)
+
 
 def main():
     args = parse()
@@ -1211,7 +1326,7 @@ def main():
     import torch
     from gofann_amd import _lib
     torch.cuda.init()
-    wl, li, table, codes, pl = build_world(args, torch)
+    wl, li, table, codes, pl, cen = build_world(args, torch)
     t0 = time.time()
     gt = ground_truth(wl, li, torch, args.gt_queries)
     log(f"ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
@@ -1285,15 +1400,13 @@ def main():
         log(f"GPU+CPU-rerank route: {route2}")
         r2.close()
 
-    route3 = None
-    if not args.no_exact_route and inline:
-        er = ExactRoute(pipe, li)
-        q3, rec3 = int(args.exact_ladder.split(",")[-1]), 0.0
-        for Q3 in [int(x) for x in args.exact_ladder.split(",")]:
+    def exact_leg(er, ladder, label):
+        q3, rec3 = ladder[-1], 0.0
+        for Q3 in ladder:
             out3 = er.step(Q3)
             torch.cuda.synchronize()
             rec3 = recall_at_10(out3.cpu().numpy().view(np.uint32).reshape(pl.queries, 10), gt)
-            log(f"exact route Q={Q3}: recall@10={rec3:.4f}")
+            log(f"{label} Q={Q3}: recall@10={rec3:.4f}")
             q3 = Q3
             if rec3 >= args.target_recall:
                 break
@@ -1312,22 +1425,37 @@ def main():
         b3 = exact_route_bytes(st3, li.degree, wl.dim, not args.no_neighbor_samples)
         pl3 = ctx.last_placement()
         ach3 = b3 / (kms3 / 1000.0) / 1e9
-        route3 = {"qps": round(pl.queries / (ms3 / 1000.0), 1), "ms_per_step": round(ms3, 3),
-                  "kernel_ms": round(kms3, 3), "queue": q3, "recall_at_10": round(rec3, 4),
-                  "placement": pl3,
-                  "steps_per_route": round(float(st3[:, 0].mean()), 1),
-                  "scored_per_route": round(float(st3[:, 3].mean()), 1),
-                  "admitted_per_route": round(float(st3[:, 6].mean()), 1),
-                  "roofline": {"bound": "hbm", "achieved": round(ach3, 2),
-                               "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                               "frac": round(ach3 / PEAK_HBM_GBPS, 5),
-                               "traffic": measured_traffic(
-                                   "exact_route_c2_traffic.md",
-                                   q3 == 32 and pl3.get("hash_in_lds") == 2
-                                   and not args.no_neighbor_samples),
-                               "kernel": "exact_route_kernel", "kernel_ms": round(kms3, 3),
-                               "algorithmic_bytes": b3}}
-        log(f"exact route: {route3}")
+        res = {"qps": round(pl.queries / (ms3 / 1000.0), 1), "ms_per_step": round(ms3, 3),
+               "kernel_ms": round(kms3, 3), "queue": q3, "recall_at_10": round(rec3, 4),
+               "placement": pl3,
+               "steps_per_route": round(float(st3[:, 0].mean()), 1),
+               "scored_per_route": round(float(st3[:, 3].mean()), 1),
+               "admitted_per_route": round(float(st3[:, 6].mean()), 1),
+               "roofline": {"bound": "hbm", "achieved": round(ach3, 2),
+                            "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                            "frac": round(ach3 / PEAK_HBM_GBPS, 5),
+                            "traffic": None,
+                            "kernel": "exact_route_kernel", "kernel_ms": round(kms3, 3),
+                            "algorithmic_bytes": b3}}
+        log(f"{label}: {res}")
+        return res
+
+    route3 = coarse3 = None
+    ladder3 = [int(x) for x in args.exact_ladder.split(",")]
+    if not args.no_exact_route and inline:
+        route3 = exact_leg(ExactRoute(pipe, li), ladder3, "exact route (medoid seeds)")
+        route3["roofline"]["traffic"] = measured_traffic(
+            "exact_route_c2_traffic.md",
+            route3["queue"] == 96 and route3["placement"].get("hash_in_lds") == 2
+            and not args.no_neighbor_samples)
+        route3["seeds"] = "label medoid"
+        if not args.no_coarse_entry:
+            from gofann_amd import search as gs
+            coarse3 = exact_leg(ExactRoute(pipe, li, entry=gs.CoarseEntry(li, cen)), ladder3,
+                                "exact route (coarse entry)")
+            coarse3["seeds"] = (f"per route: representative of the bucket of the query's "
+                                f"nearest of {cen.shape[0]} trained centres, picked on the GPU "
+                                f"inside the step")
 
     prep = None
     if not args.no_rabitq_prep:
@@ -1396,11 +1524,22 @@ def main():
                    "sample_records": not args.no_records,
                    "pq_route": pq_route,
                    "full_gpu_exact_route": route3,
+                   "full_gpu_exact_route_coarse_entry": coarse3,
                    "gpu_cpu_rerank_route": route2,
                    "rabitq_query_prep": prep},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
     }
+    if not args.no_c4:
+        # the second target configuration, in the same run: free the C2
+        # world first (C4's base alone is 100 GB of HBM)
+        import gc
+        pipe = wl = li = table = codes = pl = cen = gt = out = res = r2 = None
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        c4 = run_c4(args, torch, ctx)
+        line["config"]["c4"] = c4
     print(json.dumps(line), flush=True)
     if args.calibrate_copy:
         x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")

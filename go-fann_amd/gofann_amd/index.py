@@ -443,7 +443,7 @@ def nearest_centre(x: torch.Tensor, centres: torch.Tensor, chunk: int = 1 << 18)
 def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_values: np.ndarray,
                       num_labels: int, centres: torch.Tensor, degree: int,
                       threshold: int = 2000, progress=None,
-                      graph_seed: int = 6) -> LabelIndex:
+                      graph_seed: int = 6, local: int | None = None) -> LabelIndex:
     """Label-partitioned graphs for labels with more than `threshold` rows.
     `progress(msg)` (optional) is called about every 30 s of building."""
     import time
@@ -475,7 +475,8 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
         whole = len(samples) == base.shape[0] and base.dtype == torch.float32
         xg = base if whole else base[sidx].float()  # every row, in order: no copy
         graph[o:o + len(samples)], rep_cluster[l], rep_row[l] = build_group_graph(
-            xg, cluster[sidx], centres, degree, seed=graph_seed + int(l), return_reps=True)
+            xg, cluster[sidx], centres, degree, local=local, seed=graph_seed + int(l),
+            return_reps=True)
         # seed: row nearest the group mean (fp64), dataloader.cpp:7361-7406
         if xg.shape[0] * xg.shape[1] * 4 > LEAN_GROUP_BYTES:
             step = 1 << 16

@@ -1,18 +1,20 @@
 """Route planning and device-predicate compilation (host side).
 
-A filtered query (AND of labels, optional range atoms) becomes one or more
-routes:
-  * every label has a graph (frequency above the threshold): one graph route
-    per label (dual AND routing -- and_dual_route_posting_ratio_threshold
-    defaults to 1e30, src/app/runtime_defaults.h:31, so two graph labels
-    always give two routes; src/data/dataloader.cpp:9064-9080, 9804-9810);
-  * some label is rare: one posting route over the rarest rare label
-    (dataloader.cpp:9793-9808).
-Each route's residual predicate is the query's labels minus the route's
-anchor plus its range atoms, compiled to one DNF clause
-(route_predicate::compile / finish, src/planning/route_predicate_plan.h:
-88-101, 134-144; device packing backend_pq.cu:5815-5832).  An empty residual
-is entailed: one empty clause.
+A filtered query is an OR of conjunctions (clauses); a clause is an AND of
+labels, optionally with the query's range atoms.  Each clause becomes routes
+(clause_anchors; prepare_query_route_chunk and plan_hybrid_clause_routes,
+src/data/dataloader.cpp:9741-9853, 10860-10960):
+  * some label of the clause has no graph: one posting route over the
+    rarest such label;
+  * two graph labels: a graph route per label (dual AND routing:
+    and_dual_route_posting_ratio_threshold defaults to 1e30,
+    src/app/runtime_defaults.h:31, dataloader.cpp:9066-9077);
+  * otherwise: a graph route over the label with the smallest posting list.
+Each route's residual predicate is its clause minus the route's anchor plus
+the clause's range atoms, compiled to one DNF clause (route_predicate::
+compile / finish, src/planning/route_predicate_plan.h:175-315; device
+packing backend_pq.cu:5815-5832).  An empty residual is entailed: one empty
+clause.  Routes of one query merge per query.
 """
 from __future__ import annotations
 
@@ -110,23 +112,86 @@ def nearest_bucket_seeds(index, rs: RouteSet, queries) -> np.ndarray:
     return out
 
 
+def clause_anchors(index, labels: list, dual_ratio: float = 1e30,
+                   routing_mode: str = "greedy_min_posting") -> tuple:
+    """Anchor labels of one conjunction (the route choice of
+    prepare_query_route_chunk, dataloader.cpp:10860-10960, and of
+    plan_hybrid_clause_routes, :9741-9853): ("posting", [l]) for the rarest
+    label without a graph when there is one; ("graph", [a, b]) for two graph
+    labels whose posting sizes are within dual_ratio of each other
+    (should_dual_route_and_labels, :9066-9077; the default threshold 1e30,
+    runtime_defaults.h:31, routes both), the smaller first; otherwise
+    ("graph", [l]) for the label of least posting size (greedy_min_posting;
+    greedy_max_posting takes the largest), the first of equals.  Labels with
+    neither a graph nor a posting list are not routable; ("none", [])
+    when no label is."""
+    cand = [l for l in labels if int(index.cat_freq[l]) > 0]
+    rare = [l for l in cand if not index.has_graph(l)]
+    if rare:
+        best = rare[0]
+        for l in rare[1:]:
+            if int(index.cat_freq[l]) < int(index.cat_freq[best]):
+                best = l
+        return "posting", [best]
+    if not cand:
+        return "none", []
+    if routing_mode == "per_label_multi_route":
+        return "graph", list(cand)
+    if len(cand) == 2:
+        a, b = (int(index.cat_freq[cand[0]]), int(index.cat_freq[cand[1]]))
+        if max(a, b) / min(a, b) < dual_ratio:
+            return "graph", [cand[1], cand[0]] if b < a else [cand[0], cand[1]]
+    best = cand[0]
+    for l in cand[1:]:
+        f, fb = int(index.cat_freq[l]), int(index.cat_freq[best])
+        if (f < fb) if routing_mode == "greedy_min_posting" else (f > fb):
+            best = l
+    return "graph", [best]
+
+
 def plan_queries(index, query_labels: list, query_ranges: list | None = None,
-                 sort_by_group: bool = True, seeds: str = "medoid", queries=None) -> Plan:
-    """Routes for every query (see module docstring).  seeds="medoid" keeps
+                 sort_by_group: bool = True, seeds: str = "medoid", queries=None,
+                 dual_ratio: float = 1e30) -> Plan:
+    """Routes for every query: an AND of labels plus optional range atoms
+    (one conjunction per query, see clause_anchors).  seeds="medoid" keeps
     the reference's one seed per label; "nearest_bucket" needs `queries`."""
-    graph_rows, post_rows = [], []
-    for q, labels in enumerate(query_labels):
-        rng = [tuple(a) for a in (query_ranges[q] if query_ranges is not None else [])]
-        labels = sorted(set(int(l) for l in labels))
-        if not labels:
+    clauses = [[(sorted(set(int(l) for l in labels)), True)] for labels in query_labels]
+    for q, cl in enumerate(clauses):
+        if not cl[0][0]:
             raise ValueError("queries without a label route are not planned here")
-        rare = [l for l in labels if not index.has_graph(l)]
-        if rare:
-            anchor = min(rare, key=lambda l: (int(index.cat_freq[l]), l))
-            post_rows.append((q, anchor, [l for l in labels if l != anchor], rng))
-        else:
-            for anchor in labels:
-                graph_rows.append((q, anchor, [l for l in labels if l != anchor], rng))
+    return plan_dnf(index, clauses, query_ranges, sort_by_group=sort_by_group, seeds=seeds,
+                    queries=queries, dual_ratio=dual_ratio)
+
+
+def plan_dnf(index, query_clauses: list, query_ranges: list | None = None,
+             sort_by_group: bool = True, seeds: str = "medoid", queries=None,
+             dual_ratio: float = 1e30) -> Plan:
+    """Routes of queries given in disjunctive normal form: query q is the OR
+    of its clauses, clause = (labels, uses_range), where uses_range puts the
+    query's range atoms into the clause.  Each clause gets its own routes
+    (plan_hybrid_clause_routes, dataloader.cpp:9741-9853, via
+    clause_anchors), and each route owns the clause it was planned for: its
+    residual predicate is that clause without the anchor label (a singleton
+    label group or posting list proves its label, route_predicate_plan.h:
+    226-234, 260-276) plus the range atoms when the clause uses them
+    (RouteResidualMode::RemainingConjunction, :9513-9609).  Routes of one
+    query merge their results (rabitq_lowfreq_merge.h:709-815).  A clause
+    with ranges but no label needs a range-posting route, which this
+    planner does not produce (ValueError)."""
+    graph_rows, post_rows = [], []
+    for q, clauses in enumerate(query_clauses):
+        rng = [tuple(a) for a in (query_ranges[q] if query_ranges is not None else [])]
+        for labels, uses_range in clauses:
+            labels = [int(l) for l in labels]
+            cr = rng if uses_range else []
+            if not labels:
+                raise ValueError(f"query {q}: a range-only clause needs a range-posting route")
+            kind, anchors = clause_anchors(index, labels, dual_ratio)
+            if kind == "none":
+                continue
+            for anchor in anchors:
+                row = (q, anchor, [l for l in labels if l != anchor], cr)
+                (post_rows if kind == "posting" else graph_rows).append(row)
     if sort_by_group:
         graph_rows.sort(key=lambda r: (r[1], r[0]))
     g = _routeset(graph_rows, index)
@@ -138,7 +203,7 @@ def plan_queries(index, query_labels: list, query_ranges: list | None = None,
     off = np.array([index.posting_offset[r[1]] for r in post_rows], dtype=np.uint64)
     size = np.array([index.posting_offset[r[1] + 1] - index.posting_offset[r[1]]
                      for r in post_rows], dtype=np.uint64)
-    return Plan(g, p, off.astype(np.uint32), size.astype(np.uint32), len(query_labels))
+    return Plan(g, p, off.astype(np.uint32), size.astype(np.uint32), len(query_clauses))
 
 
 def filter_mask(index, labels: list, ranges: list, base_ranges) -> np.ndarray:

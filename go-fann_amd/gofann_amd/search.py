@@ -189,11 +189,15 @@ class DeviceRoutes:
                    to_dev(p.compiled if rs.count else np.zeros(1, np.uint8)),
                    br, stride, rs.count)
 
-    def routes_view(self, begin: int = 0, end: int | None = None) -> Routes:
+    def routes_view(self, begin: int = 0, end: int | None = None,
+                    start: torch.Tensor | None = None) -> Routes:
+        """`start`: per-route entry rows to use instead of route_start
+        (e.g. CoarseEntry.seeds)."""
         end = self.count if end is None else end
         order = self.launch_order[begin:end]
+        st = self.route_start if start is None else start
         return Routes(_lib.ptr(self.route_query), _lib.ptr(self.route_group),
-                      _lib.ptr(self.route_start), None, None, None, None, None, None, 0,
+                      _lib.ptr(st), None, None, None, None, None, None, 0,
                       end - begin, _lib.ptr(order))
 
     def predicate_view(self, dg: DeviceGraph, alpha: float, pending_base_stop: bool,
@@ -207,6 +211,50 @@ class DeviceRoutes:
                              _lib.ptr(dg.csr_offsets), _lib.ptr(dg.csr_labels),
                              dg.samples, self.range_stride, float(alpha),
                              1 if pending_base_stop else 0, slab, slab_stride)
+
+
+class CoarseEntry:
+    """Per-route entry rows picked on the GPU from trained coarse centres (an
+    IVF-style entry; no counterpart in the reference, which starts every
+    route of a label at the label's medoid, dataloader.cpp:7361-7406).
+
+    For route (query q, label group g): the centre c nearest q, then the
+    representative row of bucket (g, c) -- the row of g nearest that bucket's
+    mean, kept by the graph builder -- or g's medoid when g has no row in
+    that bucket.  Everything runs on the device (one GEMM of queries against
+    centres, an argmin, a gather), so a step that uses it pays for it."""
+
+    def __init__(self, index, centres: torch.Tensor):
+        K = int(centres.shape[0])
+        L = int(index.num_labels)
+        table = np.repeat(index.seed_local.astype(np.uint32)[:, None], K, axis=1)
+        for g in range(L):
+            lo, hi = int(index.rep_offset[g]), int(index.rep_offset[g + 1])
+            if hi > lo:
+                table[g, index.rep_cluster[lo:hi].astype(np.int64)] = index.rep_row[lo:hi]
+        self.table = torch.from_numpy(table.reshape(-1).view(np.int32)).to(DEV)
+        self.K = K
+        self.centres = centres.to(DEV).float().contiguous()
+        self.cnorm = (self.centres * self.centres).sum(1)
+
+    def nearest(self, queries: torch.Tensor, chunk: int = 1 << 15) -> torch.Tensor:
+        """Nearest centre of every query row (int64 [n])."""
+        out = torch.empty(queries.shape[0], dtype=torch.int64, device=DEV)
+        for s in range(0, queries.shape[0], chunk):
+            q = queries[s:s + chunk].float()
+            out[s:s + chunk] = torch.addmm(self.cnorm[None, :], q, self.centres.t(),
+                                           alpha=-2.0).argmin(1)
+        return out
+
+    def seeds(self, nearest: torch.Tensor, route_query: torch.Tensor, route_group: torch.Tensor,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+        """int32 [routes] entry rows for routes (route_query, route_group)."""
+        c = nearest[route_query.long()]
+        idx = route_group.long() * self.K + c
+        if out is None:
+            return self.table[idx]
+        torch.index_select(self.table, 0, idx, out=out)
+        return out
 
 
 def search_params(queue_limit=64, result_width=100, early_stop_mode=_lib.EARLY_STOP_ADAPTIVE,
