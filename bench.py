@@ -66,7 +66,7 @@ def parse():
                     help="separate code rows and CSR labels instead of 64-byte sample records")
     ap.add_argument("--no-cpu-rerank-route", action="store_true",
                     help="skip the GPU+CPU-rerank route measurement")
-    ap.add_argument("--config", choices=("c2", "c3", "c4"), default="c2",
+    ap.add_argument("--config", choices=("c2", "c3", "c4", "c5"), default="c2",
                     help="c2 (default): 10Mx192 u8 PQ/exact routes; c3: 2.7Mx4096 fp32 RaBitQ "
                          "with range predicates; c4: 100Mx512 fp16 RaBitQ with categorical "
                          "and range predicates")
@@ -852,7 +852,7 @@ def cpu_baseline_rabitq(pipe, wl, li, rq, seconds, threads=1):
         posts = [t for q in sel for t in post_by_q.get(q, [])]
         if posts:  # label-posting scans
             prs = gp._routeset([r for _, r in posts], li)
-            pred = po.PredicateArrays.from_plan(prs.predicate, li)
+            pred = po.PredicateArrays.from_plan(prs.predicate, li, base_ranges=wl.base_ranges)
             off = np.array([li.posting_offset[r[1]] for _, r in posts], np.uint32)
             size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]]
                              for _, r in posts], np.uint32)
@@ -1021,6 +1021,11 @@ def ground_truth_c4(wl, torch, nq, chunk=1 << 20):
     return gt
 
 
+def synth_types():
+    from gofann_amd import synth
+    return synth.QUERY_TYPES_C5
+
+
 class RabitqLabelPipeline:
     """One step of the C4 route set on the GPU: query preparation, one
     RaBitQ graph traversal over every graph route (equality queries on a
@@ -1042,7 +1047,17 @@ class RabitqLabelPipeline:
         starts = [-(-(i * amax) // nint) for i in range(nint + 1)]  # ceil(i * amax / nint)
         graph_rows, post_rows = [], []
         self.interior = 0
-        for q in range(nq):
+        dnf = wl.meta.get("query_clauses")
+        if dnf is not None:
+            # C5: every query is a DNF filter; routes per clause, graph
+            # routes ordered by query type so each type is one route range
+            types = wl.meta["query_types"]
+            kinds = sorted(set(types), key=list(synth_types()).index)
+            cls_of = {k: i for i, k in enumerate(kinds)}
+            graph_rows, post_rows = gp.dnf_route_rows(li, dnf, wl.query_ranges)
+            graph_rows.sort(key=lambda r: (cls_of[types[r[0]]], r[1], r[0]))
+            self.class_names = kinds
+        for q in range(nq if dnf is None else 0):
             if wl.query_labels[q]:
                 lab = wl.query_labels[q][0]
                 (graph_rows if li.has_graph(lab) else post_rows).append((q, lab, [], []))
@@ -1054,9 +1069,10 @@ class RabitqLabelPipeline:
                 inside = starts[i] >= lo and starts[i + 1] <= hi
                 self.interior += int(inside)
                 graph_rows.append((q, cats + i, [], [] if inside else [(0, 3, lo, hi)]))
-        # by (label, query): category routes (labels < cats) come first, so
-        # the equality and range classes are two contiguous route ranges
-        graph_rows.sort(key=lambda r: (r[1], r[0]))
+        if dnf is None:
+            # by (label, query): category routes (labels < cats) come first,
+            # so the equality and range classes are two contiguous ranges
+            graph_rows.sort(key=lambda r: (r[1], r[0]))
         self.graph_rows, self.post_rows = graph_rows, post_rows
         rs = gp._routeset(graph_rows, li)
         ps = gp._routeset(post_rows, li)
@@ -1064,12 +1080,18 @@ class RabitqLabelPipeline:
         self.ng, self.np_ = rs.count, ps.count
         self.n_eq = int((rs.route_group < cats).sum()) if rs.count else 0
         self.cats = cats
-        self.classes = [(0, self.n_eq), (self.n_eq, self.ng)]
-        self.route_class = lambda row: 0 if row[1] < cats else 1
+        if dnf is None:
+            self.classes = [(0, self.n_eq), (self.n_eq, self.ng)]
+            self.route_class = lambda row: 0 if row[1] < cats else 1
+        else:
+            cl = np.array([cls_of[types[r[0]]] for r in graph_rows], dtype=np.int64)
+            b = np.searchsorted(cl, np.arange(len(kinds) + 1))
+            self.classes = [(int(b[i]), int(b[i + 1])) for i in range(len(kinds))]
+            self.route_class = lambda row: cls_of[types[row[0]]]
         self.entry = None  # gs.CoarseEntry: per-route entry rows picked in step()
         self.dg = gs.DeviceGraph.upload(li)
         self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
-        self.dp = gs.DeviceRoutes.upload(ps)
+        self.dp = gs.DeviceRoutes.upload(ps, wl.base_ranges)
         off = np.array([li.posting_offset[r[1]] for r in post_rows], dtype=np.uint32)
         size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]]
                          for r in post_rows], dtype=np.uint32)
@@ -1291,6 +1313,148 @@ def run_c4(args, torch, ctx) -> dict:
             "medoid_seeds": med, "coarse_entry": coarse, "cpu_baseline": cpu}
 
 
+# ---------------------------------------------------------------------------
+# C5: C4 plus a Markov string attribute; exact, fuzzy (3-gram Jaccard >= 0.6)
+# and category AND range AND string filters (--config c5).
+# ---------------------------------------------------------------------------
+def build_world_c5(args, torch):
+    from gofann_amd import index as gi
+    from gofann_amd import synth
+    t0 = time.time()
+    wl = synth.config5(n=args.n_c4, nq=args.queries_c4, device="cuda")
+    torch.cuda.synchronize()
+    nstr = len(wl.meta["strings"])
+    log(f"C5 data {wl.n}x{wl.dim} fp16, {nstr} distinct strings, {wl.queries.shape[0]} "
+        f"queries in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    cen = gi.train_kmeans(wl.base, 4096, seed=4006)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              cen, degree=32, threshold=args.c4_threshold, progress=log,
+                              local=args.c4_local)
+    torch.cuda.empty_cache()
+    base = wl.meta["string_label_base"]
+    ng = int((li.label_size > 0).sum())
+    ngs = int((li.label_size[base:] > 0).sum())
+    log(f"C5 graphs: {ng} label groups ({ngs} string tokens), {li.rows} rows, degree "
+        f"{li.degree} in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    P = wl.dim
+    rot = gi.random_rotation(wl.dim, P, 4005, "cuda")
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, cen, chunk=1 << 18)
+    torch.cuda.synchronize()
+    log(f"C5 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
+    return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), cen
+
+
+def ground_truth_c5(wl, li, torch, nq, chunk=1 << 21):
+    """Exact filtered top-10 (fp32 L2 of the fp16 rows) of the first nq
+    queries: the union over the query's clauses of the rows holding the
+    clause's token, restricted by the clause's category and range."""
+    cat = wl.label_values[0::3]
+    attr = wl.base_ranges[:, 0]
+    base_label = wl.meta["string_label_base"]
+    gt = {}
+    for q in range(min(nq, wl.queries.shape[0])):
+        rng = wl.query_ranges[q]
+        parts = []
+        for labels, uses_range in wl.meta["query_clauses"][q]:
+            tok = [l for l in labels if l >= base_label]
+            rest = [l for l in labels if l < base_label]
+            t = tok[0]
+            rows = li.posting_ids[int(li.posting_offset[t]):int(li.posting_offset[t + 1])]
+            if rest:
+                rows = rows[cat[rows] == rest[0]]
+            if uses_range and rng:
+                (_, _, lo, hi), = rng
+                rows = rows[(attr[rows] >= lo) & (attr[rows] < hi)]
+            parts.append(rows)
+        cand = np.unique(np.concatenate(parts)) if parts else np.zeros(0, np.uint32)
+        if cand.size == 0:
+            continue
+        qv = wl.queries[q].float()
+        best_d = torch.full((0,), 0.0, device="cuda")
+        best_i = torch.full((0,), 0, dtype=torch.int64, device="cuda")
+        for s0 in range(0, cand.size, chunk):
+            ids = torch.as_tensor(cand[s0:s0 + chunk].astype(np.int64), device="cuda")
+            x = wl.base[ids].float()
+            d = ((x - qv[None, :]) ** 2).sum(1)
+            cd, ci = torch.cat([best_d, d]), torch.cat([best_i, ids])
+            k = min(10, cd.numel())
+            v, j = torch.topk(cd, k, largest=False)
+            best_d, best_i = v, ci[j]
+        gt[q] = best_i.cpu().numpy().astype(np.uint32)
+    return gt
+
+
+def run_c5(args, torch, ctx) -> dict:
+    from gofann_amd import search as gs
+    wl, li, rq, cen = build_world_c5(args, torch)
+    t0 = time.time()
+    gt = ground_truth_c5(wl, li, torch, args.gt_queries_c4)
+    log(f"C5 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch)
+    pipe.P, pipe.li = rq["P"], li
+    types = wl.meta["query_types"]
+    log(f"C5 routes: {pipe.ng} graph, {pipe.np_} label-posting scans ({pipe.post_rows_total} "
+        f"rows), classes {dict(zip(pipe.class_names, pipe.classes))}, planned in "
+        f"{time.time() - t0:.1f}s")
+    class_gt = [(k, {q: v for q, v in gt.items() if types[q] == k}) for k in pipe.class_names]
+    ladder = [args.queue] if args.queue else [int(x) for x in args.c4_ladder.split(",")]
+    med = rabitq_leg(args, pipe, class_gt, ladder, "C5 medoid seeds", c4_kernels)
+    med["seeds"] = "label medoid"
+    coarse = None
+    if not args.no_coarse_entry:
+        pipe.entry = gs.CoarseEntry(li, cen)
+        coarse = rabitq_leg(args, pipe, class_gt,
+                            [int(x) for x in args.c4_coarse_ladder.split(",")],
+                            "C5 coarse entry", c4_kernels)
+        coarse["seeds"] = ("per route: representative of the bucket of the nearest of 4096 "
+                           "trained centres (from the preparation's query-anchor distances), "
+                           "inside the step")
+        pipe.entry = None
+    cpu = None
+    if not args.no_cpu_baseline:
+        qb = med["queue_by_class"]
+        pipe.chosen = tuple(qb[n] for n in pipe.class_names)
+        T = host_threads()
+        cr, cn, cel = cpu_baseline_rabitq(pipe, wl, li, rq, args.cpu_seconds, threads=T)
+        cpu = cpu_line(cr, cn, cel, "graph routes at each class's beam, label-posting scans "
+                                    "with residual predicates, exact fp16 rerank, merge", T)
+        log(f"C5 cpu baseline {cr:.1f} qps over {cn} queries")
+    nclauses = [len(c) for c in wl.meta["query_clauses"]]
+    return {"workload": "C5: the C4 set plus a string attribute (8-32 lowercase characters, "
+                        "order-2 character Markov chain, 50k distinct, Zipf reuse); exact "
+                        "string, fuzzy string (3-gram Jaccard >= 0.6) and category AND range "
+                        "AND string filters, compiled to label routes; top-10",
+            "n": wl.n, "queries": pipe.nq, "graph_routes": pipe.ng, "posting_routes": pipe.np_,
+            "posting_rows": pipe.post_rows_total, "shortlist": pipe.W, "gt_queries": len(gt),
+            "clauses_per_query_mean": round(float(np.mean(nclauses)), 2),
+            "clauses_per_fuzzy_query_mean": round(float(np.mean(
+                [c for c, t in zip(nclauses, types) if "fuzzy" in t])), 2),
+            "medoid_seeds": med, "coarse_entry": coarse, "cpu_baseline": cpu}
+
+
+def main_c5(args):
+    import torch
+    from gofann_amd import _lib
+    torch.cuda.init()
+    ctx = _lib.Context(0)
+    c5 = run_c5(args, torch, ctx)
+    med = c5["medoid_seeds"]
+    line = {
+        "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
+        "value": med["qps"], "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": med["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8 codes / f16 rerank",
+        "data": "synthetic",
+        "config": {k: v for k, v in c5.items() if k != "cpu_baseline"},
+        "roofline": med["roofline"],
+        "cpu_baseline": c5["cpu_baseline"],
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main_c4(args):
     import torch
     from gofann_amd import _lib
@@ -1318,6 +1482,9 @@ def main():
         return
     if args.config == "c4" and args.gpus == 1:
         main_c4(args)
+        return
+    if args.config == "c5" and args.gpus == 1:
+        main_c5(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build's "

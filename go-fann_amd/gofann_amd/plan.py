@@ -163,6 +163,27 @@ def plan_queries(index, query_labels: list, query_ranges: list | None = None,
                     queries=queries, dual_ratio=dual_ratio)
 
 
+def dnf_route_rows(index, query_clauses: list, query_ranges: list | None = None,
+                   dual_ratio: float = 1e30) -> tuple:
+    """(graph rows, posting rows) of plan_dnf, unsorted: one tuple
+    (query, anchor label, residual labels, residual range atoms) per route."""
+    graph_rows, post_rows = [], []
+    for q, clauses in enumerate(query_clauses):
+        rng = [tuple(a) for a in (query_ranges[q] if query_ranges is not None else [])]
+        for labels, uses_range in clauses:
+            labels = [int(l) for l in labels]
+            cr = rng if uses_range else []
+            if not labels:
+                raise ValueError(f"query {q}: a range-only clause needs a range-posting route")
+            kind, anchors = clause_anchors(index, labels, dual_ratio)
+            if kind == "none":
+                continue
+            for anchor in anchors:
+                row = (q, anchor, [l for l in labels if l != anchor], cr)
+                (post_rows if kind == "posting" else graph_rows).append(row)
+    return graph_rows, post_rows
+
+
 def plan_dnf(index, query_clauses: list, query_ranges: list | None = None,
              sort_by_group: bool = True, seeds: str = "medoid", queries=None,
              dual_ratio: float = 1e30) -> Plan:
@@ -178,20 +199,7 @@ def plan_dnf(index, query_clauses: list, query_ranges: list | None = None,
     query merge their results (rabitq_lowfreq_merge.h:709-815).  A clause
     with ranges but no label needs a range-posting route, which this
     planner does not produce (ValueError)."""
-    graph_rows, post_rows = [], []
-    for q, clauses in enumerate(query_clauses):
-        rng = [tuple(a) for a in (query_ranges[q] if query_ranges is not None else [])]
-        for labels, uses_range in clauses:
-            labels = [int(l) for l in labels]
-            cr = rng if uses_range else []
-            if not labels:
-                raise ValueError(f"query {q}: a range-only clause needs a range-posting route")
-            kind, anchors = clause_anchors(index, labels, dual_ratio)
-            if kind == "none":
-                continue
-            for anchor in anchors:
-                row = (q, anchor, [l for l in labels if l != anchor], cr)
-                (post_rows if kind == "posting" else graph_rows).append(row)
+    graph_rows, post_rows = dnf_route_rows(index, query_clauses, query_ranges, dual_ratio)
     if sort_by_group:
         graph_rows.sort(key=lambda r: (r[1], r[0]))
     g = _routeset(graph_rows, index)

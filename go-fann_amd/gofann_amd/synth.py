@@ -309,3 +309,94 @@ def config4(n=100_000_000, nq=10_000, device="cuda", dim=512, k=4096, rank=64, s
                     meta=dict(selectivity=np.where(np.arange(nq) % 2 == 1, width / attr_max, 0.0),
                               categories=labels, intervals=intervals, attr_max=attr_max,
                               zipf_s=zipf_s, spread=spread, rank=rank, noise=noise))
+
+
+QUERY_TYPES_C5 = ("exact", "fuzzy", "hybrid_exact", "hybrid_fuzzy")
+
+
+def config5(n=100_000_000, nq=10_000, device="cuda", vocab=50_000, zipf_strings=1.0,
+            min_score=0.6, fuzzy_edits=1, seed=5, **c4_kw):
+    """C5: the C4 set plus a string attribute per vector and string filters.
+
+    Vectors, categories and the uint32 attribute are config4's.  The string
+    attribute takes one of `vocab` distinct 8..32-character strings from a
+    seeded order-2 character Markov chain (strings.markov_strings), reused
+    Zipf(zipf_strings) over a random rank order.  Each distinct string is a
+    token label: label categories + intervals + string id.  Row labels are
+    [category, categories + interval, token].
+
+    Query q has type QUERY_TYPES_C5[q % 4] and a filter in disjunctive
+    normal form (meta["query_clauses"][q]: list of (labels, uses_range)):
+      * exact: the token of a string drawn by row frequency;
+      * fuzzy: a string drawn by row frequency with `fuzzy_edits` character
+        substitutions, expanded by the 3-gram index to the tokens whose
+        3-gram Jaccard score is >= min_score; one clause per token;
+      * hybrid_exact: category AND range AND token, all taken from a random
+        row (so the filter matches at least that row), the range [lo, lo+w)
+        with w uniform in 1-10% of the attribute domain around the row's
+        value;
+      * hybrid_fuzzy: as hybrid_exact with the row's string fuzzed and
+        expanded: one clause (category, token) with the range per token.
+    A fuzzy pattern that expands to no token is drawn again."""
+    from . import strings as st
+    wl = config4(n=n, nq=nq, device=device, **c4_kw)
+    cats, nint, amax = wl.meta["categories"], wl.meta["intervals"], wl.meta["attr_max"]
+    base_label = cats + nint
+    texts = st.markov_strings(vocab, 1000 * seed + 7)
+    index = st.NgramIndex(texts)
+    rng = np.random.default_rng(1000 * seed + 8)
+    probs = _zipf_probs(vocab, zipf_strings)
+    rank_to_sid = rng.permutation(vocab)
+    sid = rank_to_sid[rng.choice(vocab, size=n, p=probs)].astype(np.uint32)
+    lv = np.empty(3 * n, dtype=np.uint32)
+    lv[0::3] = wl.label_values[0::2]
+    lv[1::3] = wl.label_values[1::2]
+    lv[2::3] = base_label + sid
+    lo_off = np.arange(0, 3 * n + 1, 3, dtype=np.uint64)
+    if lo_off[-1] < 1 << 32:
+        lo_off = lo_off.astype(np.uint32)
+    cat = wl.label_values[0::2]
+    attr = wl.base_ranges[:, 0]
+    qrng = np.random.default_rng(1000 * seed + 9)
+    clauses, ranges, qtypes, patterns = [], [], [], []
+    for i in range(nq):
+        kind = QUERY_TYPES_C5[i % 4]
+        qtypes.append(kind)
+        if kind in ("exact", "fuzzy"):
+            while True:
+                s = int(rank_to_sid[qrng.choice(vocab, p=probs)])
+                if kind == "exact":
+                    toks, pat = [s], texts[s]
+                else:
+                    pat = st.mutate(texts[s], qrng, fuzzy_edits)
+                    toks = index.expand(pat, min_score).tolist()
+                if toks:
+                    break
+            clauses.append([([base_label + t], False) for t in toks])
+            ranges.append([])
+            patterns.append(pat)
+            continue
+        while True:
+            r = int(qrng.integers(0, n))
+            s = int(sid[r])
+            if kind == "hybrid_exact":
+                toks, pat = [s], texts[s]
+            else:
+                pat = st.mutate(texts[s], qrng, fuzzy_edits)
+                toks = index.expand(pat, min_score).tolist()
+            if toks:
+                break
+        w = int(max(1, round(qrng.uniform(0.01, 0.10) * amax)))
+        a = int(attr[r])
+        lo = int(qrng.integers(max(0, a - w + 1), min(a, amax - w) + 1))
+        c = int(cat[r])
+        clauses.append([(sorted([c, base_label + t]), True) for t in toks])
+        ranges.append([(0, 3, float(lo), float(lo + w))])
+        patterns.append(pat)
+    meta = dict(wl.meta)
+    meta.update(strings=texts, string_label_base=base_label, string_ids=sid,
+                query_clauses=clauses, query_types=qtypes, patterns=patterns,
+                min_score=min_score, ngram_index=index)
+    return Workload("config5", wl.base, wl.queries, wl.cluster_of, wl.centroids, lo_off, lv,
+                    base_label + vocab, [[] for _ in range(nq)], wl.base_ranges, ranges,
+                    meta=meta)
