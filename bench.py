@@ -66,26 +66,31 @@ def parse():
                     help="separate code rows and CSR labels instead of 64-byte sample records")
     ap.add_argument("--no-cpu-rerank-route", action="store_true",
                     help="skip the GPU+CPU-rerank route measurement")
-    ap.add_argument("--config", choices=("c2", "c3", "c4", "c5"), default="c2",
+    ap.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2",
                     help="c2 (default): 10Mx192 u8 PQ/exact routes; c3: 2.7Mx4096 fp32 RaBitQ "
                          "with range predicates; c4: 100Mx512 fp16 RaBitQ with categorical "
                          "and range predicates")
+    ap.add_argument("--n-c1", type=int, default=1_000_000)
+    ap.add_argument("--queries-c1", type=int, default=10_000)
     ap.add_argument("--n-c4", type=int, default=100_000_000)
     ap.add_argument("--queries-c4", type=int, default=10_000)
     ap.add_argument("--gt-queries-c4", type=int, default=1000)
-    ap.add_argument("--c4-ladder", default="16,32,64,96,128,192,256,384,512,768,1024")
-    ap.add_argument("--c4-coarse-ladder", default="16,24,32,48,64,96,128,192")
+    ap.add_argument("--c4-ladder", default="16,32,64,96,128,192,256,384,448,512,768,1024")
+    ap.add_argument("--c4-coarse-ladder", default="16,24,32,48,64,96,128,192,256,384")
     ap.add_argument("--c4-local", type=int, default=8,
                     help="in-bucket links per row of the C4 graphs (the rest are drawn)")
     ap.add_argument("--no-c4", action="store_true",
                     help="the default C2 run skips its C4 leg")
+    ap.add_argument("--no-c1", action="store_true", help="skip the C1 leg of the default run")
+    ap.add_argument("--no-c3", action="store_true", help="skip the C3 leg of the default run")
+    ap.add_argument("--no-c5", action="store_true", help="skip the C5 leg of the default run")
     ap.add_argument("--c4-threshold", type=int, default=50_000,
                     help="labels with at most this many rows are posting routes")
     ap.add_argument("--n-c3", type=int, default=2_700_000)
     ap.add_argument("--queries-c3", type=int, default=10_000)
     ap.add_argument("--gt-queries-c3", type=int, default=999)
     ap.add_argument("--c3-ladder", default="32,48,64,96,128,192,256,384,512")
-    ap.add_argument("--c3-local", type=int, default=12,
+    ap.add_argument("--c3-local", type=int, default=24,
                     help="in-bucket links per row of the C3 graph (the rest are drawn)")
     ap.add_argument("--c3-scan-rows", type=int, default=20_000,
                     help="ranges whose smallest posting slice has at most this many rows are "
@@ -564,6 +569,145 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False
 
 
 # ---------------------------------------------------------------------------
+# C1: 1M x 128 fp32, PQ M=32, degree 32, ten uniform labels, beam 64, exact
+# fp32 rerank of 100 -- the reference's CPU-runnable configuration.  Runs on
+# the GPU (one step = every query's route, rerank and merge) and through the
+# oracle's C restatement over the host cores, both at the configured beam.
+# ---------------------------------------------------------------------------
+def ground_truth_c1(wl, torch, nq, device):
+    """Exact single-label filtered top-10 (fp32) of the first nq queries."""
+    lab = torch.as_tensor(wl.label_values.astype(np.int64), device=device)
+    x = wl.base.to(device)
+    xn = (x * x).sum(1)
+    gt = {}
+    for s in range(0, nq, 64):
+        e = min(nq, s + 64)
+        q = wl.queries[s:e].to(device)
+        d = xn[None, :] + (q * q).sum(1)[:, None] - 2.0 * (q @ x.t())
+        want = torch.as_tensor([wl.query_labels[i][0] for i in range(s, e)], device=device)
+        d = torch.where(lab[None, :] == want[:, None], d, torch.full_like(d, float("inf")))
+        _, idx = torch.topk(d, 10, dim=1, largest=False)
+        for j in range(e - s):
+            gt[s + j] = idx[j].cpu().numpy().astype(np.uint32)
+    return gt
+
+
+def run_c1(args, torch, ctx) -> dict:
+    """C1 at its configured beam (64) and shortlist (100)."""
+    from gofann_amd import index as gi
+    from gofann_amd import plan as gp
+    from gofann_amd import synth
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle as po
+    dev = "cuda" if ctx is not None else "cpu"
+    t0 = time.time()
+    wl = synth.config1(n=args.n_c1, nq=args.queries_c1, device=dev)
+    table = gi.train_pq(wl.base, 32, iters=25, sample=65536, seed=1005)
+    codes = gi.pq_encode(wl.base, table, 32)
+    cen = gi.train_kmeans(wl.base, 256, seed=1006)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels, cen,
+                              degree=32, threshold=2000, local=16)
+    pl = gp.plan_queries(li, wl.query_labels)
+    log(f"C1 world {wl.n}x{wl.dim} f32, PQ M=32, {int((li.label_size > 0).sum())} label graphs, "
+        f"{pl.graph.count} graph routes, built in {time.time() - t0:.1f}s")
+    gt = ground_truth_c1(wl, torch, min(args.gt_queries, wl.queries.shape[0]), dev)
+    W = 100
+    out = {"workload": "C1: 1Mx128 fp32 256-centre mixture (centres N(0,1), sigma 0.3), PQ "
+                       "M=32, graph R=32 per label, 10 uniform labels, single-label equality, "
+                       "configured beam 64, exact fp32 rerank of 100, top-10",
+           "n": wl.n, "queries": wl.queries.shape[0], "graph_routes": pl.graph.count,
+           "shortlist": W, "gt_queries": len(gt), "seeds": "label medoid"}
+    ladder = [64, 96, 128, 192, 256, 384]
+    q90 = None
+    if ctx is not None:
+        pipe = Pipeline(ctx, wl, li, table, codes, pl, torch, inline=False, width=W)
+        runs = {}
+        for Q in ladder:
+            res = pipe.step(Q)
+            torch.cuda.synchronize()
+            rec = recall_at_10(res.cpu().numpy().view(np.uint32).reshape(pl.queries, 10), gt)
+            log(f"C1 GPU Q={Q}: recall@10={rec:.4f}")
+            runs[Q] = rec
+            if rec >= args.target_recall:
+                q90 = Q
+                break
+        for label, Q in (("gpu_configured_beam", 64), ("gpu", q90 or ladder[-1])):
+            for _ in range(args.warmup):
+                pipe.step(Q)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                res = pipe.step(Q)
+                torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+            rec = recall_at_10(res.cpu().numpy().view(np.uint32).reshape(pl.queries, 10), gt)
+            out[label] = {"qps": round(pl.queries / (ms / 1000.0), 1),
+                          "ms_per_step": round(ms, 3), "queue": Q,
+                          "recall_at_10": round(rec, 4),
+                          "route": "PQ graph search (shortlist 100), exact fp32 rerank on the "
+                                   "GPU, merge"}
+            log(f"C1 {label}: {out[label]}")
+        pipe = None
+    # the reference's CPU path: the oracle's C code over the host cores
+    T = host_threads()
+    base = wl.base.cpu().numpy()
+    qs = wl.queries.cpu().numpy()
+    rs = pl.graph
+    pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15, pending_base_stop=True)
+    codes_h, table_h = codes.cpu().numpy(), table.cpu().numpy()
+    if q90 is None and ctx is None:
+        # no GPU: the CPU path finds its own recall-0.90 beam
+        for Q in ladder:
+            ids, _, _ = po.pq_search(li, rs, pred, po.params(queue_limit=Q, result_width=W),
+                                     codes_h, table_h, qs, threads=T)
+            ri, rd = po.rerank(base, qs, rs.route_query, ids, 10, threads=T)
+            mi, _ = po.merge(rs.route_to_query, ri, rd, pl.queries, 10)
+            rec = recall_at_10(mi, gt)
+            log(f"C1 CPU Q={Q}: recall@10={rec:.4f}")
+            if rec >= args.target_recall:
+                q90 = Q
+                break
+    for label, Q in (("cpu_configured_beam", 64), ("cpu", q90 or ladder[-1])):
+        t0 = time.perf_counter()
+        ids, _, _ = po.pq_search(li, rs, pred, po.params(queue_limit=Q, result_width=W),
+                                 codes_h, table_h, qs, threads=T)
+        ri, rd = po.rerank(base, qs, rs.route_query, ids, 10, threads=T)
+        mi, _ = po.merge(rs.route_to_query, ri, rd, pl.queries, 10)
+        el = time.perf_counter() - t0
+        rec = recall_at_10(mi, gt)
+        out[label] = {"qps": round(pl.queries / el, 1), "seconds": round(el, 3), "queue": Q,
+                      "recall_at_10": round(rec, 4), "cores": T, "cpu": cpu_model(),
+                      "kind": "port",
+                      "route": "oracle C code (OpenMP, -O3): PQ graph search, exact fp32 rerank, "
+                               "merge, every query"}
+        log(f"C1 {label}: {out[label]}")
+    return out
+
+
+def main_c1(args):
+    import torch
+    ctx = None
+    if torch.cuda.is_available():
+        from gofann_amd import _lib
+        torch.cuda.init()
+        ctx = _lib.Context(0)
+    c1 = run_c1(args, torch, ctx)
+    head = c1.get("gpu") or c1["cpu"]
+    line = {
+        "metric": "filtered QPS @ recall@10>=0.90 on 1xMI355X; % of HBM roofline",
+        "value": head["qps"], "unit": "queries/s", "n_gpus": 1 if ctx else 0,
+        "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": head.get("ms_per_step", round(1000.0 * head.get("seconds", 0), 3)),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8 codes / f32",
+        "data": "synthetic", "config": c1, "roofline": None,
+        "cpu_baseline": {"value": c1["cpu"]["qps"], "unit": "queries/s",
+                         "cores": c1["cpu"]["cores"], "kind": "port", "cpu": c1["cpu"]["cpu"],
+                         "sample": "every C1 query"},
+    }
+    print(json.dumps(line), flush=True)
+
+
+# ---------------------------------------------------------------------------
 # C3: 2.7M x 4096 fp32, one-bit RaBitQ, range predicates (--config c3).
 # ---------------------------------------------------------------------------
 def rabitq_traversal_bytes(st: np.ndarray, degree: int, code_bytes: int) -> float:
@@ -990,7 +1134,7 @@ def ground_truth_c4(wl, torch, nq, chunk=1 << 20):
     n = wl.n
     q = wl.queries[:nq].float()
     qn = (q * q).sum(1)
-    cat = torch.as_tensor(wl.label_values[0::2].astype(np.int32), device="cuda")
+    cat = torch.as_tensor(wl.meta["row_category"].astype(np.int32), device="cuda")
     attr = torch.as_tensor(wl.base_ranges[:, 0], device="cuda")
     qlab = torch.tensor([ql[0] if ql else -1 for ql in wl.query_labels[:nq]], device="cuda",
                         dtype=torch.int32)
@@ -1054,7 +1198,8 @@ class RabitqLabelPipeline:
             types = wl.meta["query_types"]
             kinds = sorted(set(types), key=list(synth_types()).index)
             cls_of = {k: i for i, k in enumerate(kinds)}
-            graph_rows, post_rows = gp.dnf_route_rows(li, dnf, wl.query_ranges)
+            graph_rows, post_rows = gp.dnf_route_rows(li, dnf, wl.query_ranges,
+                                                      clause_scans=True)
             graph_rows.sort(key=lambda r: (cls_of[types[r[0]]], r[1], r[0]))
             self.class_names = kinds
         for q in range(nq if dnf is None else 0):
@@ -1264,12 +1409,18 @@ def c3_kernels(pipe, st_ms, st):
             "exact_rerank_kernel (f32)": (st_ms["rerank"], rb)}
 
 
-def run_c4(args, torch, ctx) -> dict:
-    """The C4 configuration end to end: build, ground truth, the medoid-seeded
+def run_c4(args, torch, ctx, world=None) -> dict:
+    """The C4 configuration end to end: build (or take `world`, a C5 world
+    whose C4 view carries C4's filters), ground truth, the medoid-seeded
     route set (the reference's seed rule) and, as an extra row, the same
     routes entered at coarse-quantizer entries picked inside the step."""
     from gofann_amd import search as gs
-    wl, li, rq, cen = build_world_c4(args, torch)
+    from gofann_amd import synth
+    if world is None:
+        wl, li, rq, cen = build_world_c4(args, torch)
+    else:
+        wl5, li, rq, cen = world
+        wl = synth.c4_view(wl5)
     t0 = time.time()
     gt = ground_truth_c4(wl, torch, args.gt_queries_c4)
     log(f"C4 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
@@ -1350,7 +1501,7 @@ def ground_truth_c5(wl, li, torch, nq, chunk=1 << 21):
     """Exact filtered top-10 (fp32 L2 of the fp16 rows) of the first nq
     queries: the union over the query's clauses of the rows holding the
     clause's token, restricted by the clause's category and range."""
-    cat = wl.label_values[0::3]
+    cat = wl.meta["row_category"]
     attr = wl.base_ranges[:, 0]
     base_label = wl.meta["string_label_base"]
     gt = {}
@@ -1386,9 +1537,9 @@ def ground_truth_c5(wl, li, torch, nq, chunk=1 << 21):
     return gt
 
 
-def run_c5(args, torch, ctx) -> dict:
+def run_c5(args, torch, ctx, world=None) -> dict:
     from gofann_amd import search as gs
-    wl, li, rq, cen = build_world_c5(args, torch)
+    wl, li, rq, cen = world if world is not None else build_world_c5(args, torch)
     t0 = time.time()
     gt = ground_truth_c5(wl, li, torch, args.gt_queries_c4)
     log(f"C5 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
@@ -1477,6 +1628,9 @@ def main_c4(args):
 
 def main():
     args = parse()
+    if args.config == "c1" and args.gpus == 1:
+        main_c1(args)
+        return
     if args.config == "c3" and args.gpus == 1:
         main_c3(args)
         return
@@ -1697,16 +1851,31 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
     }
-    if not args.no_c4:
-        # the second target configuration, in the same run: free the C2
-        # world first (C4's base alone is 100 GB of HBM)
-        import gc
-        pipe = wl = li = table = codes = pl = cen = gt = out = res = r2 = None
+    # the other configurations, in the same run: free the C2 world first
+    import gc
+    pipe = wl = li = table = codes = pl = cen = gt = out = res = r2 = None
+
+    def free():
         gc.collect()
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
-        c4 = run_c4(args, torch, ctx)
-        line["config"]["c4"] = c4
+
+    free()
+    if not args.no_c1:
+        line["config"]["c1"] = run_c1(args, torch, ctx)
+        free()
+    if not args.no_c3:
+        line["config"]["c3"] = run_c3(args, torch, ctx)
+        free()
+    if not (args.no_c4 and args.no_c5):
+        # C5 is C4 plus a string attribute: one world serves both
+        world = build_world_c5(args, torch)
+        if not args.no_c4:
+            line["config"]["c4"] = run_c4(args, torch, ctx, world=world)
+        if not args.no_c5:
+            line["config"]["c5"] = run_c5(args, torch, ctx, world=world)
+        world = None
+        free()
     print(json.dumps(line), flush=True)
     if args.calibrate_copy:
         x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")

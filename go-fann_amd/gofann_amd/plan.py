@@ -164,9 +164,19 @@ def plan_queries(index, query_labels: list, query_ranges: list | None = None,
 
 
 def dnf_route_rows(index, query_clauses: list, query_ranges: list | None = None,
-                   dual_ratio: float = 1e30) -> tuple:
+                   dual_ratio: float = 1e30, clause_scans: bool = False) -> tuple:
     """(graph rows, posting rows) of plan_dnf, unsorted: one tuple
-    (query, anchor label, residual labels, residual range atoms) per route."""
+    (query, anchor label, residual labels, residual range atoms) per route.
+
+    clause_scans: a clause that carries range atoms and labels also gets the
+    route that enumerates its candidates exhaustively -- the reference's
+    range route of a hybrid clause (plan.append_range_route,
+    dataloader.cpp:9755-9757, appended at :9874-9885), whose candidates are
+    the rows of the range slice that satisfy the clause's labels.  Here it
+    is a filter-first posting scan over the clause's label of least posting
+    size, with the rest of the clause (labels and ranges) as its residual:
+    the same candidate set, from a smaller list.  It is not added when the
+    clause's own route already is that scan."""
     graph_rows, post_rows = [], []
     for q, clauses in enumerate(query_clauses):
         rng = [tuple(a) for a in (query_ranges[q] if query_ranges is not None else [])]
@@ -181,6 +191,11 @@ def dnf_route_rows(index, query_clauses: list, query_ranges: list | None = None,
             for anchor in anchors:
                 row = (q, anchor, [l for l in labels if l != anchor], cr)
                 (post_rows if kind == "posting" else graph_rows).append(row)
+            if clause_scans and cr:
+                cand = [l for l in labels if int(index.cat_freq[l]) > 0]
+                src = min(cand, key=lambda l: (int(index.cat_freq[l]), l))
+                if not (kind == "posting" and anchors == [src]):
+                    post_rows.append((q, src, [l for l in labels if l != src], cr))
     return graph_rows, post_rows
 
 

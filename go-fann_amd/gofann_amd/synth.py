@@ -307,6 +307,7 @@ def config4(n=100_000_000, nq=10_000, device="cuda", dim=512, k=4096, rank=64, s
     return Workload("config4", base, queries, cl, cn, lo_off, lv, labels + intervals,
                     query_labels, attr.astype(np.float32)[:, None], query_ranges,
                     meta=dict(selectivity=np.where(np.arange(nq) % 2 == 1, width / attr_max, 0.0),
+                              row_category=cat,
                               categories=labels, intervals=intervals, attr_max=attr_max,
                               zipf_s=zipf_s, spread=spread, rank=rank, noise=noise))
 
@@ -394,9 +395,21 @@ def config5(n=100_000_000, nq=10_000, device="cuda", vocab=50_000, zipf_strings=
         ranges.append([(0, 3, float(lo), float(lo + w))])
         patterns.append(pat)
     meta = dict(wl.meta)
-    meta.update(strings=texts, string_label_base=base_label, string_ids=sid,
+    meta.update(c4_query_labels=wl.query_labels, c4_query_ranges=wl.query_ranges,
+                strings=texts, string_label_base=base_label, string_ids=sid,
                 query_clauses=clauses, query_types=qtypes, patterns=patterns,
                 min_score=min_score, ngram_index=index)
     return Workload("config5", wl.base, wl.queries, wl.cluster_of, wl.centroids, lo_off, lv,
                     base_label + vocab, [[] for _ in range(nq)], wl.base_ranges, ranges,
+                    meta=meta)
+
+
+def c4_view(wl5: Workload) -> Workload:
+    """The C4 workload over a C5 world: the same vectors, categories and
+    attribute (a superset of C4's labels), with C4's query filters."""
+    meta = {k: v for k, v in wl5.meta.items()
+            if k not in ("query_clauses", "query_types", "patterns")}
+    return Workload("config4", wl5.base, wl5.queries, wl5.cluster_of, wl5.centroids,
+                    wl5.label_offsets, wl5.label_values, wl5.num_labels,
+                    wl5.meta["c4_query_labels"], wl5.base_ranges, wl5.meta["c4_query_ranges"],
                     meta=meta)

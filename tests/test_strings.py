@@ -128,6 +128,13 @@ def test_plan_dnf_residuals():
     assert res == [[2], [1], []]
     with pytest.raises(ValueError):
         gp.plan_dnf(Ix(), [[([], True)]], [rng])
+    # clause scans: a ranged clause with graph anchors also gets the
+    # exhaustive scan over its least-posting label (the reference's range
+    # route); a clause already routed as that scan gets no second one
+    g_rows, p_rows = gp.dnf_route_rows(Ix(), clauses, [rng, []], clause_scans=True)
+    assert [(r[0], r[1], r[2]) for r in p_rows] == [(0, 3, [1]), (0, 1, [2])]
+    assert all(r[3] == rng for r in p_rows)
+    assert len(g_rows) == 3
 
 
 @pytest.fixture(scope="module")
@@ -162,7 +169,8 @@ def test_c5_routes_end_to_end_through_oracle(c5_small):
     wl, li, cen = c5_small
     types = wl.meta["query_types"]
     assert set(types) == set(synth.QUERY_TYPES_C5)
-    g_rows, p_rows = gp.dnf_route_rows(li, wl.meta["query_clauses"], wl.query_ranges)
+    g_rows, p_rows = gp.dnf_route_rows(li, wl.meta["query_clauses"], wl.query_ranges,
+                                       clause_scans=True)
     assert g_rows and p_rows
     rs, ps = gp._routeset(g_rows, li), gp._routeset(p_rows, li)
     x = wl.base.float()
@@ -210,4 +218,4 @@ def test_c5_routes_end_to_end_through_oracle(c5_small):
         want = cand[np.lexsort((cand, d))[:10]]
         recalls[types[q]].append(len(set(got) & set(want.tolist())) / len(want))
     for t, r in recalls.items():
-        assert r and np.mean(r) > 0.75, (t, np.mean(r) if r else None)
+        assert r and np.mean(r) > 0.8, (t, np.mean(r) if r else None)
