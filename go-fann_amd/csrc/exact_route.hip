@@ -79,6 +79,20 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_FIXED_ROWS 0
 #endif
 
+// Minimum waves per SIMD the kernel is compiled for (register budget).
+#ifndef GOFANN_EXACT_MIN_WAVES
+#define GOFANN_EXACT_MIN_WAVES 1
+#endif
+
+// Most registers per lane a register frontier may use (Q + 2 <= 64 x this).
+// 2 lets beams of 63..126 keep the frontier in registers; measured at
+// Q = 80 on 10M rows (degree 64) it is 3% slower than the LDS frontier,
+// because the larger register file pushes the visited table out of LDS,
+// so the default is 1.
+#ifndef GOFANN_EXACT_MAX_REGS
+#define GOFANN_EXACT_MAX_REGS 1
+#endif
+
 struct ExactArgs {
     gofann_graph_view graph;
     const uint32_t* label_size;
@@ -232,44 +246,70 @@ __device__ __forceinline__ bool best_insert(BestK& b, float d, uint32_t id, uint
 }
 
 // ---------------------------------------------------------------------------
-// Register frontier (capacity Q + 2 <= 64): lane i holds smmh2 entry i.  The
-// heap code is the LDS version's (include/smmh2.h:77-147) with every index
-// wave-uniform: an entry is read with v_readlane and written by the one lane
-// that owns it, so each heap step costs a few VALU/SALU instructions instead
-// of a dependent LDS round trip.  The array layout -- and with it every
-// tie-break of pickup and pop_max -- is the LDS heap's.
+// Register frontier (capacity Q + 2 <= 64 N): entry i lives in lane i % 64 of
+// register i / 64, so the array is the LDS heap's.  The heap code is the LDS
+// version's (include/smmh2.h:77-147) with every index wave-uniform: an entry
+// is read with v_readlane and written by the one lane that owns it, so each
+// heap step costs a few VALU/SALU instructions instead of a dependent LDS
+// round trip.  The array layout -- and with it every tie-break of pickup and
+// pop_max -- is the LDS heap's.
 // ---------------------------------------------------------------------------
+template <int N>
 struct RegHeap {
-    float first;
-    uint32_t second;
-    uint32_t sample;
+    float first[N];
+    uint32_t second[N];
+    uint32_t sample[N];
 };
 
-__device__ __forceinline__ float rh_first(const RegHeap& h, int i)
+template <int N>
+__device__ __forceinline__ void rh_init(RegHeap<N>& h)
 {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first), i));
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        h.first[r] = FLT_MAX;
+        h.second[r] = UINT32_MAX;
+        h.sample[r] = UINT32_MAX;
+    }
 }
 
-__device__ __forceinline__ Entry rh_get(const RegHeap& h, int i)
+// Readers: the register index i / 64 is wave-uniform, so each is one
+// v_readlane of the owning register.
+template <int N>
+__device__ __forceinline__ float rh_first(const RegHeap<N>& h, int i)
 {
+    if (N == 1 || i < kWave)
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first[0]), i));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first[N - 1]), i - kWave));
+}
+
+template <int N>
+__device__ __forceinline__ Entry rh_get(const RegHeap<N>& h, int i)
+{
+    const int r = (N == 1 || i < kWave) ? 0 : N - 1;
+    const int l = i - r * kWave;
     Entry e;
-    e.first = rh_first(h, i);
-    e.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.second), i));
-    e.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.sample), i));
+    e.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first[r]), l));
+    e.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.second[r]), l));
+    e.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.sample[r]), l));
     e.base = e.first;
     return e;
 }
 
-__device__ __forceinline__ void rh_set(RegHeap& h, int i, const Entry& e, int lane)
+template <int N>
+__device__ __forceinline__ void rh_set(RegHeap<N>& h, int i, const Entry& e, int lane)
 {
-    const bool me = lane == i;
-    h.first = me ? e.first : h.first;
-    h.second = me ? e.second : h.second;
-    h.sample = me ? e.sample : h.sample;
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        const bool me = lane + r * kWave == i;
+        h.first[r] = me ? e.first : h.first[r];
+        h.second[r] = me ? e.second : h.second[r];
+        h.sample[r] = me ? e.sample : h.sample[r];
+    }
 }
 
 // Entry i moves to slot y (the hole).
-__device__ __forceinline__ void rh_move(RegHeap& h, int i, int y, int lane)
+template <int N>
+__device__ __forceinline__ void rh_move(RegHeap<N>& h, int i, int y, int lane)
 {
     rh_set(h, y, rh_get(h, i), lane);
 }
@@ -278,7 +318,8 @@ __device__ __forceinline__ void rh_move(RegHeap& h, int i, int y, int lane)
 // entry it passes into the hole, writing the moving entry once at its final
 // slot.  Every comparison is the swap formulation's (smmh2.h:77-147), so the
 // array -- and with it every later tie-break -- is identical.
-__device__ __forceinline__ void rh_insert(RegHeap& h, int& size, const Entry& e, int lane)
+template <int N>
+__device__ __forceinline__ void rh_insert(RegHeap<N>& h, int& size, const Entry& e, int lane)
 {
     int y = size++;
     for (;;) {
@@ -314,7 +355,8 @@ __device__ __forceinline__ void rh_insert(RegHeap& h, int& size, const Entry& e,
     rh_set(h, y, e, lane);
 }
 
-__device__ __forceinline__ void rh_pop_max(RegHeap& h, int& size, int lane)
+template <int N>
+__device__ __forceinline__ void rh_pop_max(RegHeap<N>& h, int& size, int lane)
 {
     --size;
     Entry x = rh_get(h, size);  // the last entry refills the max slot
@@ -378,18 +420,39 @@ __device__ __forceinline__ void rh_pop_max(RegHeap& h, int& size, int lane)
 
 // Unused entry of least `first`, lowest index on ties; marked used.  The
 // frontier's keys are exact squared distances (>= 0), whose float bits
-// order as unsigned integers: one unsigned minimum, then the lowest lane
-// holding it.
-__device__ __forceinline__ bool rh_pickup(RegHeap& h, int size, Entry& out, int lane)
+// order as unsigned integers: one unsigned minimum over every register,
+// then the lowest index holding it (register 0's lanes come first).
+template <int N>
+__device__ __forceinline__ bool rh_pickup(RegHeap<N>& h, int size, Entry& out, int lane)
 {
-    const bool live = lane >= 1 && lane < size && !(h.second & kPoolUsed);
-    const uint32_t key = live ? __float_as_uint(h.first) : UINT32_MAX;
-    const uint32_t mn = wave_min_u32(key);
-    const uint64_t at = ballot(live && key == mn);
-    if (at == 0) return false;
-    const int best = __builtin_ctzll(at);
+    uint32_t key[N];
+    uint32_t m = UINT32_MAX;
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        const int idx = lane + r * kWave;
+        const bool live = idx >= 1 && idx < size && !(h.second[r] & kPoolUsed);
+        key[r] = live ? __float_as_uint(h.first[r]) : UINT32_MAX;
+        m = key[r] < m ? key[r] : m;
+    }
+    const uint32_t mn = wave_min_u32(m);
+    if (mn == UINT32_MAX) {
+        // no live entry holds a key below the sentinel; an unused entry
+        // keyed UINT32_MAX cannot occur (keys are finite distances)
+        return false;
+    }
+    int best = -1;
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        const int idx = lane + r * kWave;
+        const bool live = idx >= 1 && idx < size && !(h.second[r] & kPoolUsed);
+        const uint64_t at = ballot(live && key[r] == mn);
+        if (best < 0 && at != 0) best = __builtin_ctzll(at) + r * kWave;
+    }
+    if (best < 0) return false;
     out = rh_get(h, best);
-    if (lane == best) h.second |= kPoolUsed;
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+        if (lane + r * kWave == best) h.second[r] |= kPoolUsed;
     return true;
 }
 
@@ -422,10 +485,11 @@ __device__ __forceinline__ void load_node(const gofann_graph_view& g,
     }
 }
 
-// kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  kReg: the
-// frontier lives in registers (Q + 2 <= 64), else in LDS.
-template <int kVisited, int kC, bool kReg>
-__global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
+// kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  kRegs > 0:
+// the frontier lives in kRegs registers per lane (Q + 2 <= 64 kRegs), 0: in
+// LDS.
+template <int kVisited, int kC, int kRegs>
+__global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel(ExactArgs a)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ uint32_t s_row[kMaxDegree];
@@ -484,7 +548,8 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
     bool done = false;
     const Entry sentinel = {FLT_MAX, UINT32_MAX, FLT_MAX, UINT32_MAX};
     Entry now = sentinel, next = sentinel;
-    RegHeap rh{FLT_MAX, UINT32_MAX, UINT32_MAX};
+    RegHeap<(kRegs > 0 ? kRegs : 1)> rh;
+    rh_init(rh);
 
     // Seed (:1793-1850).
     if (gsize == 0 || seed == UINT32_MAX || seed >= gsize) {
@@ -497,7 +562,7 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
                                 l2_u8_row(a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn))
                           : 0.0f);
             const Entry kp = {d0, seed, d0, s0};
-            if constexpr (kReg) {
+            if constexpr (kRegs > 0) {
                 rh_insert(rh, heap_size, kp, lane);
             } else {
                 if (lane == 0) smmh_insert(frontier, heap_size, kp);
@@ -514,7 +579,7 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
     __syncthreads();
     if (!done) {
         bool found;
-        if constexpr (kReg)
+        if constexpr (kRegs > 0)
             found = rh_pickup(rh, heap_size, now, lane);
         else
             found = pickup(frontier, heap_size, now, lane);
@@ -587,7 +652,7 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
         const bool full = heap_size > 2 && heap_size >= Q + 1;
         float thr = 0.0f;
         if (full) {
-            if constexpr (kReg)
+            if constexpr (kRegs > 0)
                 thr = rh_first(rh, 2);
             else
                 thr = frontier[2].first;
@@ -595,7 +660,7 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
         const bool cand = keep && !(full && thr < dist);
         const uint64_t cand_mask = ballot(cand);
         uint64_t adm = 0;  // admitted lanes
-        if constexpr (kReg) {
+        if constexpr (kRegs > 0) {
             for (uint64_t m = cand_mask; m; m &= m - 1) {
                 const int j = __builtin_ctzll(m);
                 Entry kp;
@@ -656,7 +721,7 @@ __global__ __launch_bounds__(64) void exact_route_kernel(ExactArgs a)
 
         // Pickup and early stop (:1985-2030).
         bool found;
-        if constexpr (kReg)
+        if constexpr (kRegs > 0)
             found = rh_pickup(rh, heap_size, next, lane);
         else
             found = pickup(frontier, heap_size, next, lane);
@@ -709,11 +774,11 @@ namespace {
 
 inline uint32_t align16u(uint32_t x) { return (x + 15u) & ~15u; }
 
-template <int kVisited, int kC, bool kReg>
+template <int kVisited, int kC, int kRegs>
 int resident(Context* ctx, uint32_t lds)
 {
     if (lds > static_cast<uint32_t>(ctx->lds_per_block)) return 0;
-    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited, kC, kReg>);
+    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited, kC, kRegs>);
     if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lds)) != hipSuccess) {
         (void)hipGetLastError();
@@ -734,14 +799,14 @@ int resident(Context* ctx, uint32_t lds)
 // launch.
 // fixed_slab: visited slabs for a placement outside LDS, holding at most
 // fixed_routes routes (the no-alloc entry point); nullptr: context scratch.
-template <int kC, bool kReg>
+template <int kC, int kRegs>
 int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
                  uint32_t lds_spill, uint32_t lds_glob, uint32_t count, uint32_t* fixed_slab,
                  uint32_t fixed_routes)
 {
-    const int rf = resident<kVisitedLds, kC, kReg>(ctx, lds_full);
-    const int rs = resident<kVisitedSpill, kC, kReg>(ctx, lds_spill);
-    const int rg = resident<kVisitedGlobal, kC, kReg>(ctx, lds_glob);
+    const int rf = resident<kVisitedLds, kC, kRegs>(ctx, lds_full);
+    const int rs = resident<kVisitedSpill, kC, kRegs>(ctx, lds_spill);
+    const int rg = resident<kVisitedGlobal, kC, kRegs>(ctx, lds_glob);
     int mode = kVisitedLds;
     int res = rf;
     if (hash_mode == GOFANN_PLACE_GLOBAL) {
@@ -779,11 +844,11 @@ int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
     const uint32_t lds = mode == kVisitedLds ? lds_full : (mode == kVisitedSpill ? lds_spill : lds_glob);
     const dim3 grid(count), block(kWave);
     if (mode == kVisitedLds)
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedLds, kC, kReg>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedLds, kC, kRegs>), grid, block, lds, ctx->stream, a);
     else if (mode == kVisitedSpill)
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedSpill, kC, kReg>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedSpill, kC, kRegs>), grid, block, lds, ctx->stream, a);
     else
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedGlobal, kC, kReg>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedGlobal, kC, kRegs>), grid, block, lds, ctx->stream, a);
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("exact route launch");
     ctx->last_table_in_lds = 0;
     ctx->last_hash_in_lds = mode == kVisitedGlobal ? 0 : (mode == kVisitedLds ? 1 : 2);
@@ -792,6 +857,40 @@ int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
     return GOFANN_OK;
 }
 
+
+struct LaunchShape {
+    Context* ctx;
+    ExactArgs* a;
+    int hash_mode;
+    uint32_t lds_full, lds_spill, lds_glob, count;
+    uint32_t* fixed_slab;
+    uint32_t fixed_routes;
+};
+
+// Row length fixed at compile time only in builds that ask for it.
+template <int kRegs>
+int launch_rows(const LaunchShape& s, int chunks)
+{
+#if GOFANN_EXACT_FIXED_ROWS
+    switch (chunks) {
+    case 8:
+        return launch_exact<8, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                      s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
+    case 12:
+        return launch_exact<12, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                       s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
+    case 16:
+        return launch_exact<16, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                       s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
+    default:
+        break;
+    }
+#else
+    (void)chunks;
+#endif
+    return launch_exact<0, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill, s.lds_glob,
+                                  s.count, s.fixed_slab, s.fixed_routes);
+}
 
 static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint32_t dim,
                              uint32_t samples, const void* queries, const gofann_graph_view* g,
@@ -838,41 +937,29 @@ static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint
     a.out_dists = out_dists;
     a.stats = stats;
     // LDS: the query row, then (LDS frontier only) Q + 2 entries, then the
-    // visited table of the chosen placement.
-    const bool reg = p->queue_limit + 2 <= kWave;
+    // visited table of the chosen placement.  Beams with Q + 2 <= 128 keep
+    // the frontier in one or two registers per lane.
+    const int regs = p->queue_limit + 2 <= kWave
+                         ? 1
+                         : (GOFANN_EXACT_MAX_REGS >= 2 && p->queue_limit + 2 <= 2 * kWave ? 2 : 0);
     a.off_frontier = align16u((dim + 15u) / 16u * 16u);
-    a.off_hash = reg ? a.off_frontier
-                     : align16u(a.off_frontier + static_cast<uint32_t>(p->queue_limit + 2) *
-                                                     sizeof(Entry));
+    a.off_hash = regs ? a.off_frontier
+                      : align16u(a.off_frontier + static_cast<uint32_t>(p->queue_limit + 2) *
+                                                      sizeof(Entry));
     const uint32_t lds_full = a.off_hash + kHashCapacity * 4u;
     const uint32_t lds_spill = a.off_hash + kSpillSlots * 4u;
     const uint32_t lds_glob = a.off_hash;
     const int chunks = (GOFANN_EXACT_FIXED_ROWS && (dim == 128 || dim == 192 || dim == 256))
                            ? static_cast<int>(dim / 16)
                            : 0;
-    const int h = p->hash_mode;
-    const uint32_t n = r->count;
-    if (reg) {
-        switch (chunks) {
-        case 8: return launch_exact<8, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
-        case 12: return launch_exact<12, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
-        case 16: return launch_exact<16, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
-        default: return launch_exact<0, true>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
-        }
-    }
-    switch (chunks) {
-    case 8: return launch_exact<8, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
-    case 12: return launch_exact<12, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
-    case 16: return launch_exact<16, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
-    default: return launch_exact<0, false>(ctx, a, h, lds_full, lds_spill, lds_glob, n, fixed_slab,
-                                                 fixed_routes);
+    const LaunchShape sh{ctx, &a, p->hash_mode, lds_full, lds_spill, lds_glob, r->count,
+                         fixed_slab, fixed_routes};
+    switch (regs) {
+    case 1: return launch_rows<1>(sh, chunks);
+#if GOFANN_EXACT_MAX_REGS >= 2
+    case 2: return launch_rows<2>(sh, chunks);
+#endif
+    default: return launch_rows<0>(sh, chunks);
     }
 }
 
