@@ -84,6 +84,12 @@ def parse():
     ap.add_argument("--no-c1", action="store_true", help="skip the C1 leg of the default run")
     ap.add_argument("--no-c3", action="store_true", help="skip the C3 leg of the default run")
     ap.add_argument("--no-c5", action="store_true", help="skip the C5 leg of the default run")
+    ap.add_argument("--posting-layout", choices=("columns", "gather"), default="columns",
+                    help="C4/C5 label-posting scans: 'columns' = segmented scan over "
+                         "posting-order copies of the rows' codes and predicate columns; "
+                         "'gather' = one workgroup per route, rows gathered by sample id")
+    ap.add_argument("--posting-segment-rows", type=int, default=32768,
+                    help="rows per segment of the segmented label-posting scan")
     ap.add_argument("--c4-threshold", type=int, default=50_000,
                     help="labels with at most this many rows are posting routes")
     ap.add_argument("--n-c3", type=int, default=2_700_000)
@@ -1187,14 +1193,17 @@ class RabitqLabelPipeline:
     equality queries on rare labels, exact fp16->fp32 rerank of the W-wide
     shortlists, and the per-query merge."""
 
-    def __init__(self, ctx, wl, li, rq, torch, width=100):
+    def __init__(self, ctx, wl, li, rq, torch, width=100, posting_layout="columns",
+                 segment_rows=32768):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
+        from gofann_amd import range_posting as rp
         from gofann_amd import search as gs
-        self.ctx, self.wl, self.torch, self.L, self.gs = ctx, wl, torch, _lib, gs
+        self.ctx, self.wl, self.torch, self.L, self.gs, self.rp = ctx, wl, torch, _lib, gs, rp
         nq = wl.queries.shape[0]
         self.nq, self.W = nq, width
         P = rq["P"]
+        self.P = P
         cats, nint, amax = wl.meta["categories"], wl.meta["intervals"], wl.meta["attr_max"]
         starts = [-(-(i * amax) // nint) for i in range(nint + 1)]  # ceil(i * amax / nint)
         graph_rows, post_rows = [], []
@@ -1274,6 +1283,36 @@ class RabitqLabelPipeline:
         self.q_off, self.q_routes = gs.u32(off_q), gs.u32(order)
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
         self.seed_buf = self.dr.route_start.clone()
+        self.posting_layout = posting_layout if self.np_ else "gather"
+        if self.posting_layout == "columns":
+            self._posting_columns(li, post_rows, segment_rows)
+
+    def _posting_columns(self, li, post_rows, segment_rows):
+        """The label-posting scan's layout: the postings of the labels the
+        posting routes scan, concatenated; posting-order copies of their
+        RaBitQ rows and predicate columns; a segment plan over the routes."""
+        torch, rp = self.torch, self.rp
+        labs = np.array([r[1] for r in post_rows], dtype=np.int64)
+        uniq, inv = np.unique(labs, return_inverse=True)
+        lo = li.posting_offset[uniq].astype(np.int64)
+        lens = (li.posting_offset[uniq + 1] - li.posting_offset[uniq]).astype(np.int64)
+        coff = np.concatenate([[0], np.cumsum(lens)])
+        total = int(coff[-1])
+        shift = torch.from_numpy(lo - coff[:-1]).cuda()
+        idx = torch.repeat_interleave(shift, torch.from_numpy(lens).cuda(), output_size=total)
+        idx += torch.arange(total, device="cuda")
+        self.scan_ids = self.dg.posting_ids[idx].contiguous()
+        del idx
+        pv = self.dp.predicate_view(self.dg, 0.0, False)
+        self.scan_rows = rp.PostingRows(self.ctx, self.rv, self.scan_ids, total)
+        self.scan_cols = rp.PostingPredicateColumns(self.ctx, pv, self.scan_ids, total)
+        plan = rp.segment_plan(np.arange(self.np_), coff[:-1][inv].astype(np.uint64),
+                               lens[inv].astype(np.uint64), segment_rows)
+        self.scan_segs = rp.DeviceSegments(plan)
+        self.scan_total = total
+        log(f"label postings in posting order: {len(uniq)} labels, {total} rows, "
+            f"{plan.count} segments of <= {segment_rows} rows "
+            f"({total * (self.P // 8 + 16 + 16 + 4 * self.dp.range_stride) / 2**30:.1f} GiB)")
 
     def step(self, Q, timed=False):
         """One step; Q is one beam for every graph route, or (equality beam,
@@ -1306,7 +1345,13 @@ class RabitqLabelPipeline:
                     L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
         if timed:
             ev[2].record()
-        if self.np_:
+        if self.np_ and self.posting_layout == "columns":
+            self.rp.rabitq_posting_scan_segments(
+                ctx, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
+                self.dp.route_query, self.scan_ids, self.scan_total, self.scan_segs, W,
+                rows=self.scan_rows, cols=self.scan_cols,
+                out=(self.sl_i[self.ng * W:], self.sl_d[self.ng * W:], self.passes))
+        elif self.np_:
             ctx.check(ctx.lib.gofann_rabitq_posting_scan(
                 ctx.handle, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
                 L.ptr(self.dp.route_query), L.ptr(self.dg.posting_ids), L.ptr(self.co),
@@ -1378,7 +1423,8 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
         f"{(st[:, 3].astype(np.float64).mean() if len(st) else 0):.1f}")
     kern = kernels(pipe, st_ms, st)
     per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
-               "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None}
+               "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None,
+               **(v[2] if len(v) > 2 else {})}
            for k, v in kern.items()}
     top = max(kern, key=lambda k: kern[k][0])
     ach = kern[top][1] / (kern[top][0] / 1000.0) / 1e9
@@ -1398,11 +1444,22 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
 def c4_kernels(pipe, st_ms, st):
     P, wl, li = pipe.P, pipe.wl, pipe.li
     tb = rabitq_traversal_bytes(st, li.degree, P // 8)
-    pb = pipe.post_rows_total * (4 + P // 8 + 4 + 8) + 0.0
+    # posting scan: rows * (sample id + code, anchor id, two factors) plus
+    # the predicate's inputs per row (16-byte label slab + range row); a
+    # filter-first scan needs the code terms of passing rows only
+    C = P // 8 + 4 + 8
+    pred = 16 + 4 * pipe.dp.range_stride
+    rows = pipe.post_rows_total
+    pb = rows * (4 + C + pred) + 0.0
+    passed = int(pipe.passes[: pipe.np_].sum().item()) if pipe.np_ else 0
+    ff = rows * (4 + pred) + passed * C + 0.0
+    extra = {"passing_rows": passed, "filter_first_bytes": ff,
+             "filter_first_gbps": round(ff / (st_ms["posting_scan"] / 1000.0) / 1e9, 2)
+             if st_ms["posting_scan"] > 0 else None, "layout": pipe.posting_layout}
     rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 2 + 4) + 0.0
     return {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
             "range_scan_group_kernel+segment_merge_kernel (label postings)":
-                (st_ms["posting_scan"], pb),
+                (st_ms["posting_scan"], pb, extra),
             "exact_rerank_kernel (f16)": (st_ms["rerank"], rb)}
 
 
@@ -1433,7 +1490,8 @@ def run_c4(args, torch, ctx, world=None) -> dict:
     gt = ground_truth_c4(wl, torch, args.gt_queries_c4)
     log(f"C4 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
-    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch)
+    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
+                               segment_rows=args.posting_segment_rows)
     pipe.P, pipe.li = rq["P"], li
     log(f"C4 routes: {pipe.ng} graph ({pipe.n_eq} equality, {pipe.interior} interior "
         f"intervals), {pipe.np_} label-posting scans ({pipe.post_rows_total} rows), planned "
@@ -1552,7 +1610,8 @@ def run_c5(args, torch, ctx, world=None) -> dict:
     gt = ground_truth_c5(wl, li, torch, args.gt_queries_c4)
     log(f"C5 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
-    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch)
+    pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
+                               segment_rows=args.posting_segment_rows)
     pipe.P, pipe.li = rq["P"], li
     types = wl.meta["query_types"]
     log(f"C5 routes: {pipe.ng} graph, {pipe.np_} label-posting scans ({pipe.post_rows_total} "
@@ -1775,7 +1834,7 @@ def main():
         route3 = exact_leg(ExactRoute(pipe, li), ladder3, "exact route (medoid seeds)")
         route3["roofline"]["traffic"] = measured_traffic(
             "exact_route_c2_traffic.md",
-            route3["queue"] == 96 and route3["placement"].get("hash_in_lds") == 2
+            route3["queue"] == 80 and route3["placement"].get("hash_in_lds") == 2
             and not args.no_neighbor_samples)
         route3["seeds"] = "label medoid"
         if not args.no_coarse_entry:
@@ -1801,7 +1860,7 @@ def main():
                              "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                              "frac": round(achieved / PEAK_HBM_GBPS, 5),
                              "traffic": measured_traffic(
-                                 "traversal_pq48_c2_traffic.md",
+                                 "traversal_pq48_c2_medoid_traffic.md",
                                  chosen == 128 and not args.no_records
                                  and placed.get("table_in_lds") == 0
                                  and placed.get("hash_in_lds") == 2),

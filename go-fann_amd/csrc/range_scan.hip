@@ -71,20 +71,75 @@ struct RangeScanArgs {
     uint32_t* out_ids;
     float* out_dists;
     uint32_t* pass_counts;
-    // Label-posting mode (group-per-row kernel only): segment s is slice
-    // s % slices of route s / slices over cand_ids[cand_offsets[route] ..
-    // + cand_sizes[route]); the rows are filtered by the route predicate
-    // alone and counted when it is enabled.
+    // Label-posting modes (group-per-row kernel only); the rows are
+    // filtered by the route predicate alone and counted when it is enabled.
+    // kLabelSlices: segment s is slice s % slices of route s / slices over
+    // cand_ids[cand_offsets[route] .. + cand_sizes[route]).  kLabelSegments:
+    // segment s scans posting[seg_offset[s] .. + seg_size[s]) (clipped to
+    // resident_rows) for route seg_route[s].
     int label_mode;
     const uint32_t* cand_offsets;
     const uint32_t* cand_sizes;
     uint32_t slices;
-    // Posting-order copies of the rows (range mode, group kernel; may be
-    // null): codes [rows][padded_dim/8] and aux [rows] = {f_add, f_rescale,
-    // anchor, 0}.  Row r of the posting is read from them, not gathered.
+    // Posting-order copies of the rows (group kernel; may be null): codes
+    // [rows][padded_dim/8] and aux [rows] = {f_add, f_rescale, anchor, 0}.
+    // Row r of the posting is read from them, not gathered.
     const uint4* pcodes;
     const uint4* paux;
+    // Posting-order predicate columns (label modes; may be null): the
+    // row's label slab and its base range row [rows][pred.range_stride].
+    const uint4* pslab;
+    const float* pranges;
 };
+
+constexpr int kRangeMode = 0;
+constexpr int kLabelSlices = 1;
+constexpr int kLabelSegments = 2;
+
+// pred_matches for a posting row whose label slab and range row were read
+// in posting order: the same clause walk, each label test the serial scan
+// of pred_contains over the slab's labels (the first label >= handle
+// decides).  The slab must not be the overflow form.
+// `prange` is the row's range row; with range_stride 1 its value is passed
+// as `r0`, loaded with the slab.
+__device__ __forceinline__ bool slab_pred_matches(const gofann_predicate_view& v, uint32_t route,
+                                                  uint32_t sample, const uint4& slab,
+                                                  const float* prange, float r0)
+{
+    if (sample >= v.rows) return false;
+    const uint32_t n = slab_count(slab);
+    auto contains = [&](uint32_t handle) {
+        if (v.csr_offsets == nullptr) return false;
+        for (uint32_t k = 0; k < n; ++k) {
+            const uint32_t label = slab_label(slab, k);
+            if (label >= handle) return label == handle;
+        }
+        return false;
+    };
+    if (v.clauses) {
+        for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i) {
+            const gofann_clause cl = v.clauses[i];
+            bool pass = true;
+            for (uint32_t j = cl.label_begin; pass && j < cl.label_end; ++j)
+                pass = contains(v.route_handles[j]);
+            for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
+                const gofann_range_atom a = v.ranges[j];
+                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                       range_matches(a.mode, a.lower, a.upper,
+                                     !prange ? v.base_ranges[static_cast<uint64_t>(sample) *
+                                                                 v.range_stride +
+                                                             a.dimension]
+                                     : v.range_stride == 1 ? r0
+                                                           : prange[a.dimension]);
+            }
+            if (pass) return true;
+        }
+        return false;
+    }
+    for (uint32_t i = v.route_offsets[route]; i < v.route_offsets[route + 1]; ++i)
+        if (!contains(v.route_handles[i])) return false;
+    return true;
+}
 
 __device__ __forceinline__ bool pair_le(float ad, uint32_t aid, float bd, uint32_t bid)
 {
@@ -369,8 +424,8 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     int* s_ip = reinterpret_cast<int*>(s_f1 + a.chunk);
     uint32_t* s_prow = reinterpret_cast<uint32_t*>(s_ip + a.chunk);  // segment-relative row
 
-    const bool label_mode = a.label_mode != 0;
-    const uint32_t route = label_mode ? seg / a.slices : a.seg_route[seg];
+    const bool label_mode = a.label_mode != kRangeMode;
+    const uint32_t route = a.label_mode == kLabelSlices ? seg / a.slices : a.seg_route[seg];
     const uint32_t query = a.routes.route_query[route];
     sc.setup(query, tid, lds);
     for (int i = tid; i < a.slots; i += kScanThreads) {
@@ -399,13 +454,20 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
 
     uint64_t begin, count;
     uint32_t active = 0;
-    if (label_mode) {
+    if (a.label_mode == kLabelSlices) {
         // near-equal slices of the route's posting
         const uint64_t size = a.cand_sizes[route];
         const uint64_t part = (size + a.slices - 1) / a.slices;
         const uint64_t lo = std::min<uint64_t>(size, (seg % a.slices) * part);
         begin = static_cast<uint64_t>(a.cand_offsets[route]) + lo;
         count = std::min<uint64_t>(size, lo + part) - lo;
+    } else if (a.label_mode == kLabelSegments) {
+        begin = a.seg_offset[seg];
+        count = a.seg_size[seg];
+        if (begin > a.resident_rows)
+            count = 0;
+        else if (count > a.resident_rows - begin)
+            count = a.resident_rows - begin;
     } else {
         // :5895-5902
         begin = a.seg_offset[seg];
@@ -419,6 +481,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     }
     const bool enabled = pred_enabled(a.pred, route);
     const bool score_first = !label_mode && a.score_first != 0 && enabled;
+    const bool cols = label_mode && enabled && a.pslab != nullptr;
     const int k = a.k, kp = a.k_pow2;
     const int chunk = a.chunk;
     const int per = chunk / kScanThreads;
@@ -431,41 +494,76 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
         __syncthreads();
         const float kth_d = s_d[k - 1];
         const uint32_t kth_id = s_id[k - 1];
-        // Pass 1, one row per thread: posting id, filter, code-free terms.
+        // Pass 1, one row per thread: posting id, filter, code-free terms,
+        // in three rounds so that each round's loads are in flight together:
+        // (1) sample ids and, with posting-order columns, the label slab
+        // and range value; (2) the filter and the passing rows' aux terms;
+        // (3) the LDS writes.
+        uint32_t sv[8];
+        uint4 slv[8];
+        float r0v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            sv[t] = UINT32_MAX;
+            slv[t] = make_uint4(kSlabOverflow, 0, 0, 0);
+            r0v[t] = 0.0f;
+            if (t >= per) continue;
+            const uint64_t j = base + static_cast<uint64_t>(tid + t * kScanThreads);
+            if (j < count) {
+                sv[t] = a.posting[begin + j];
+                if (cols) {
+                    slv[t] = a.pslab[begin + j];
+                    if (a.pranges && a.pred.range_stride == 1) r0v[t] = a.pranges[begin + j];
+                }
+            }
+        }
+        bool okv[8];
+        float add0v[8], f1v[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            okv[t] = false;
+            add0v[t] = FLT_MAX;
+            f1v[t] = 0.0f;
+            if (t >= per) continue;
+            const uint64_t j = base + static_cast<uint64_t>(tid + t * kScanThreads);
+            const uint32_t s = sv[t];
+            bool ok = j < count && s < a.base_rows;  // UINT32_MAX never is
+            if (ok) {
+                if (cols && slab_count(slv[t]) != kSlabOverflow) {
+                    const float* prange =
+                        a.pranges && a.pred.range_stride > 0
+                            ? a.pranges + (begin + j) * a.pred.range_stride
+                            : nullptr;
+                    ok = slab_pred_matches(a.pred, route, s, slv[t], prange, r0v[t]);
+                } else if (enabled) {
+                    PredCounters c{0, 0};
+                    ok = pred_matches(a.pred, route, s, c);
+                } else if (active > 1) {
+                    ok = count_matching_ranges(a.routes, route, s) == active;
+                }
+            }
+            okv[t] = ok;
+            if (ok) {
+                if (a.paux) {
+                    const uint4 x = a.paux[begin + j];
+                    add0v[t] = __uint_as_float(x.x) + sc.g_row[x.z];
+                    f1v[t] = __uint_as_float(x.y);
+                } else {
+                    const uint32_t anchor = sc.anchor_ids[s];
+                    add0v[t] = sc.factors[static_cast<size_t>(s) * 3] + sc.g_row[anchor];
+                    f1v[t] = sc.factors[static_cast<size_t>(s) * 3 + 1];
+                }
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             if (t >= per) break;
             const int i = tid + t * kScanThreads;
             const uint64_t j = base + static_cast<uint64_t>(i);
-            uint32_t s = UINT32_MAX;
-            bool ok = false;
-            if (j < count) {
-                s = a.posting[begin + j];
-                ok = s < a.base_rows;  // UINT32_MAX never is
-                if (ok) {
-                    if (enabled) {
-                        PredCounters c{0, 0};
-                        ok = pred_matches(a.pred, route, s, c);
-                    } else if (active > 1) {
-                        ok = count_matching_ranges(a.routes, route, s) == active;
-                    }
-                }
-            }
-            float add0 = FLT_MAX, f1 = 0.0f;
-            if (ok) {
-                // filter-first counts every passing row; a label posting
-                // (backend_rabitq.cu:5494-5682) only predicate-checked ones
-                if (label_mode ? enabled : !score_first) ++passes;
-                if (a.paux) {
-                    const uint4 x = a.paux[begin + j];
-                    add0 = __uint_as_float(x.x) + sc.g_row[x.z];
-                    f1 = __uint_as_float(x.y);
-                } else {
-                    const uint32_t anchor = sc.anchor_ids[s];
-                    add0 = sc.factors[static_cast<size_t>(s) * 3] + sc.g_row[anchor];
-                    f1 = sc.factors[static_cast<size_t>(s) * 3 + 1];
-                }
-            }
+            const bool ok = okv[t];
+            // filter-first counts every passing row; a label posting
+            // (backend_rabitq.cu:5494-5682) only predicate-checked ones
+            if (ok && (label_mode ? enabled : !score_first)) ++passes;
             int pos = i;
             if (!score_first) {
                 // pack the passing rows: a wave reserves its slots at once
@@ -478,9 +576,9 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
                       __popcll(mask & ((1ull << __lane_id()) - 1ull));
             }
             if (ok || score_first) {
-                s_id[kp + pos] = ok ? s : UINT32_MAX;
-                s_d[kp + pos] = add0;
-                s_f1[pos] = f1;
+                s_id[kp + pos] = ok ? sv[t] : UINT32_MAX;
+                s_d[kp + pos] = add0v[t];
+                s_f1[pos] = f1v[t];
                 s_prow[pos] = static_cast<uint32_t>(j);
             }
         }
@@ -714,6 +812,72 @@ int rabitq_posting_rows(Context* ctx, const gofann_rabitq_view* rq, const uint32
     return GOFANN_OK;
 }
 
+// Posting-order predicate columns: row r of the posting gets its sample's
+// label slab -- u16 count, then the first labels of the CSR row in CSR
+// order as u16 -- or the overflow form (count kSlabOverflow: the scan reads
+// the CSR row) when the row has more than kSlabCapacity labels, a label
+// above 0xFFFF, no CSR, or the sample is out of range; and its base range
+// row (zeros without base ranges or for an out-of-range sample).
+__global__ __launch_bounds__(256) void posting_pred_rows_kernel(gofann_predicate_view v,
+                                                                const uint32_t* posting,
+                                                                uint64_t rows, uint4* out_slab,
+                                                                float* out_ranges)
+{
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
+    for (uint64_t r = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; r < rows;
+         r += stride) {
+        const uint32_t s = posting[r];
+        const bool in = s < v.rows;
+        uint32_t w[4] = {kSlabOverflow, 0u, 0u, 0u};
+        if (in && v.csr_offsets != nullptr) {
+            const uint32_t b = v.csr_offsets[s];
+            const uint32_t e = v.csr_offsets[s + 1];
+            const uint32_t n = e - b;
+            bool ok = e >= b && n <= kSlabCapacity;
+            uint32_t x[4] = {n, 0u, 0u, 0u};
+            for (uint32_t k = 0; ok && k < n; ++k) {
+                const uint32_t label = v.csr_labels[b + k];
+                ok = label <= 0xFFFFu;
+                const uint32_t h = k + 1;  // u16 index
+                x[h >> 1] |= (label & 0xFFFFu) << (16 * (h & 1));
+            }
+            if (ok) {
+                w[0] = x[0];
+                w[1] = x[1];
+                w[2] = x[2];
+                w[3] = x[3];
+            }
+        }
+        out_slab[r] = make_uint4(w[0], w[1], w[2], w[3]);
+        if (out_ranges) {
+            for (uint32_t d = 0; d < v.range_stride; ++d)
+                out_ranges[r * v.range_stride + d] =
+                    in && v.base_ranges ? v.base_ranges[static_cast<uint64_t>(s) * v.range_stride + d]
+                                        : 0.0f;
+        }
+    }
+}
+
+int posting_predicate_rows(Context* ctx, const gofann_predicate_view* pred,
+                           const uint32_t* posting, uint64_t rows, uint32_t* out_slab,
+                           float* out_ranges)
+{
+    if (!pred) return ctx->fail(GOFANN_ERR_INVALID, "predicate view missing");
+    if (rows == 0) return GOFANN_OK;
+    if (!posting || !out_slab)
+        return ctx->fail(GOFANN_ERR_INVALID, "posting predicate rows arrays missing");
+    if (pred->csr_offsets && !pred->csr_labels)
+        return ctx->fail(GOFANN_ERR_INVALID, "CSR labels missing");
+    if (reinterpret_cast<uintptr_t>(out_slab) & 15u)
+        return ctx->fail(GOFANN_ERR_INVALID, "slab array must be 16-byte aligned");
+    const uint32_t blocks = static_cast<uint32_t>(std::min<uint64_t>((rows + 255) / 256, 1u << 20));
+    hipLaunchKernelGGL(posting_pred_rows_kernel, dim3(blocks), dim3(256), 0, ctx->stream, *pred,
+                       posting, rows, reinterpret_cast<uint4*>(out_slab),
+                       pred->range_stride ? out_ranges : nullptr);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("posting predicate rows launch");
+    return GOFANN_OK;
+}
+
 namespace {
 int pow2_at_least(int x)
 {
@@ -867,6 +1031,122 @@ int rabitq_posting_scan_group(Context* ctx, const gofann_rabitq_view* rq,
     return GOFANN_OK;
 }
 
+// Label-posting scan over an explicit segment plan: the results of
+// rabitq_posting_scan_group for the routes whose postings the plan covers
+// (a route's k least pairs over the union of its segments, pass counts
+// summed), with long postings cut into many workgroups and, when given,
+// the rows' codes and predicate columns read in posting order.
+int rabitq_posting_scan_segments(Context* ctx, const gofann_rabitq_view* rq,
+                                 const gofann_rabitq_queries* pre,
+                                 const gofann_predicate_view* pred, const uint32_t* route_query,
+                                 const uint32_t* posting, uint64_t posting_rows,
+                                 const gofann_posting_segments* seg, int shortlist_k,
+                                 const uint8_t* posting_codes, const uint32_t* posting_aux,
+                                 const uint32_t* posting_slab, const float* posting_ranges,
+                                 uint32_t* out_ids, float* out_dists, uint32_t* pass_counts)
+{
+    if ((posting_codes == nullptr) != (posting_aux == nullptr))
+        return ctx->fail(GOFANN_ERR_INVALID, "posting codes and aux come together");
+    if (posting_ranges && !posting_slab)
+        return ctx->fail(GOFANN_ERR_INVALID, "posting ranges need the posting slab");
+    if (!rq || !pre || !rq->codes || !rq->factors || !rq->anchor_ids || rq->padded_dim == 0 ||
+        rq->padded_dim % 128 != 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view invalid for posting scan");
+    const void* kern = group_scan_kernel(rq->padded_dim);
+    if (!kern) return ctx->fail(GOFANN_ERR_UNSUPPORTED, "padded_dim has no grouped posting scan");
+    if (!pre->q8 || !pre->scale || !pre->k1 || !pre->centroid_dists)
+        return ctx->fail(GOFANN_ERR_INVALID, "prepared RaBitQ queries incomplete");
+    if (!seg) return ctx->fail(GOFANN_ERR_INVALID, "segment plan missing");
+    if (shortlist_k < 1 || shortlist_k > kRangeMaxShortlist)
+        return ctx->fail(GOFANN_ERR_INVALID, "shortlist_k must be in [1, 4096]");
+    if (seg->count == 0) {
+        if (seg->query_indptr && seg->positions)
+            return ctx->fail(GOFANN_ERR_INVALID, "segment plan has positions but no segments");
+        return GOFANN_OK;
+    }
+    if (!seg->route_ids || !seg->offsets || !seg->sizes || !posting || !route_query)
+        return ctx->fail(GOFANN_ERR_INVALID, "segment plan or posting arrays missing");
+    if (!out_ids || !out_dists) return ctx->fail(GOFANN_ERR_INVALID, "posting scan outputs missing");
+    if ((reinterpret_cast<uintptr_t>(posting_codes) | reinterpret_cast<uintptr_t>(posting_aux) |
+         reinterpret_cast<uintptr_t>(posting_slab)) & 15u)
+        return ctx->fail(GOFANN_ERR_INVALID, "posting-order arrays must be 16-byte aligned");
+
+    const bool merged = seg->query_indptr != nullptr;
+    uint32_t* scan_ids = out_ids;
+    float* scan_dists = out_dists;
+    uint32_t* scan_pass = pass_counts;
+    const size_t slots_out = static_cast<size_t>(seg->count) * static_cast<size_t>(shortlist_k);
+    if (merged) {
+        const size_t bytes = slots_out * 8 + static_cast<size_t>(seg->count) * 4 + 64;
+        unsigned char* buf = static_cast<unsigned char*>(ctx->scratch(Context::kScratchRange, bytes));
+        if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "posting segment scratch allocation failed");
+        scan_ids = reinterpret_cast<uint32_t*>(buf);
+        scan_dists = reinterpret_cast<float*>(buf + slots_out * 4);
+        scan_pass = reinterpret_cast<uint32_t*>(buf + slots_out * 8);
+    }
+
+    RangeScanArgs a{};
+    a.pred = pred ? *pred : gofann_predicate_view{};
+    a.routes.route_query = route_query;
+    a.posting = posting;
+    a.resident_rows = posting_rows;
+    a.seg_route = seg->route_ids;
+    a.seg_offset = seg->offsets;
+    a.seg_size = seg->sizes;
+    a.segments = seg->count;
+    a.base_rows = rq->samples ? rq->samples : UINT32_MAX;
+    a.k = shortlist_k;
+    a.k_pow2 = pow2_at_least(shortlist_k);
+    a.chunk = a.k_pow2 <= 1024 ? 1024 : 2048;
+    a.slots = std::max(2 * a.k_pow2, a.k_pow2 + a.chunk);
+    a.planes_bytes = rq->padded_dim;
+    a.score_first = 0;
+    a.out_ids = scan_ids;
+    a.out_dists = scan_dists;
+    a.pass_counts = merged || pass_counts ? scan_pass : nullptr;
+    a.label_mode = kLabelSegments;
+    a.slices = 1;
+    a.pcodes = reinterpret_cast<const uint4*>(posting_codes);
+    a.paux = reinterpret_cast<const uint4*>(posting_aux);
+    a.pslab = reinterpret_cast<const uint4*>(posting_slab);
+    a.pranges = posting_ranges;
+    const size_t lds = 2 * static_cast<size_t>(a.planes_bytes) + static_cast<size_t>(a.slots) * 8 +
+                       static_cast<size_t>(a.chunk) * 12;
+    if (lds > static_cast<size_t>(ctx->lds_per_block))
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "posting scan LDS exceeds the workgroup limit");
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute posting scan");
+    RabitqScanScorer sc = scan_scorer(rq, pre);
+    void* kargs[] = {&a, &sc};
+    if (hipLaunchKernel(kern, dim3(seg->count), dim3(kScanThreads), kargs, lds, ctx->stream) !=
+        hipSuccess)
+        return ctx->fail_hip("posting scan launch");
+    if (!merged || seg->positions == 0) return GOFANN_OK;
+
+    SegmentMergeArgs m;
+    m.query_indptr = seg->query_indptr;
+    m.stride = 0;
+    m.positions = seg->positions;
+    m.seg_ids = scan_ids;
+    m.seg_dists = scan_dists;
+    m.seg_pass = scan_pass;
+    m.k = shortlist_k;
+    m.k_pow2 = a.k_pow2;
+    m.out_ids = out_ids;
+    m.out_dists = out_dists;
+    m.out_pass = pass_counts;
+    const size_t mlds = static_cast<size_t>(2 * a.k_pow2) * 8;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(segment_merge_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mlds)) !=
+        hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute posting merge");
+    hipLaunchKernelGGL(segment_merge_kernel, dim3(seg->positions), dim3(kScanThreads), mlds,
+                       ctx->stream, m);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("posting merge launch");
+    return GOFANN_OK;
+}
+
 int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
                       const gofann_rabitq_queries* pre, const gofann_predicate_view* pred,
                       const gofann_routes* routes, const uint32_t* posting,
@@ -940,6 +1220,8 @@ int rabitq_range_scan(Context* ctx, const gofann_rabitq_view* rq,
     // streams the copies when given.
     a.pcodes = reinterpret_cast<const uint4*>(posting_codes);
     a.paux = reinterpret_cast<const uint4*>(posting_aux);
+    a.pslab = nullptr;
+    a.pranges = nullptr;
     if (a.chunk % kScanThreads != 0 || a.chunk / kScanThreads > 8 || a.slots < 2 * a.k_pow2 ||
         a.slots < a.k_pow2 + a.chunk)
         return ctx->fail(GOFANN_ERR_INVALID, "range scan chunk layout invalid");

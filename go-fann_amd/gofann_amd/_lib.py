@@ -177,6 +177,13 @@ SIGNATURES = {
                                                     P, C.c_uint64, P, P,
                                                     C.POINTER(PostingSegments), C.c_int,
                                                     C.c_int, P, P, P]),
+    "gofann_posting_predicate_rows": (C.c_int, [P, C.POINTER(PredicateView), P, C.c_uint64,
+                                                P, P]),
+    "gofann_rabitq_posting_scan_segments": (C.c_int, [P, C.POINTER(RabitqView),
+                                                      C.POINTER(RabitqQueries),
+                                                      C.POINTER(PredicateView), P, P, C.c_uint64,
+                                                      C.POINTER(PostingSegments), C.c_int, P, P,
+                                                      P, P, P, P, P]),
     "gofann_exact_rerank": (C.c_int, [P, P, C.c_int, U32, U32, P, P, P, U32, U32, U32, P, P]),
     "gofann_merge_routes": (C.c_int, [P, P, P, P, P, U32, U32, U32, P, P]),
     "gofann_predicate_masks": (C.c_int, [P, C.POINTER(PredicateView), P, P, U32, P]),

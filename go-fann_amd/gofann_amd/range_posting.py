@@ -283,6 +283,53 @@ class PostingRows:
                                                       _lib.ptr(self.aux)))
 
 
+class PostingPredicateColumns:
+    """Posting-order predicate columns (gofann_posting_predicate_rows): each
+    posting row's 16-byte label slab [rows][4] u32 and base range row
+    [rows][range_stride] f32, so a label-posting scan streams its filter's
+    inputs instead of gathering them by sample id."""
+
+    def __init__(self, ctx: _lib.Context, pred: _lib.PredicateView, postings: torch.Tensor,
+                 rows: int):
+        self.rows = int(rows)
+        dev = postings.device
+        stride = int(pred.range_stride)
+        self.slab = torch.empty(max(self.rows, 1), 4, dtype=torch.int32, device=dev)
+        self.ranges = (torch.empty(max(self.rows * stride, 1), dtype=torch.float32, device=dev)
+                       if stride else None)
+        ctx.check(ctx.lib.gofann_posting_predicate_rows(
+            ctx.handle, pred, _lib.ptr(postings), self.rows, _lib.ptr(self.slab),
+            _lib.ptr(self.ranges) if self.ranges is not None else None))
+
+
+def rabitq_posting_scan_segments(ctx: _lib.Context, rv: _lib.RabitqView,
+                                 rq: _lib.RabitqQueries, pred: _lib.PredicateView,
+                                 route_query: torch.Tensor, postings: torch.Tensor,
+                                 posting_rows: int, segs: DeviceSegments, shortlist_k: int,
+                                 rows: PostingRows | None = None,
+                                 cols: PostingPredicateColumns | None = None, out=None):
+    """Runs gofann_rabitq_posting_scan_segments; returns (ids int32, dists,
+    passes) on the device, [positions][shortlist_k] (into `out` =
+    (ids, dists, passes) flat tensors when given)."""
+    n = segs.positions
+    dev = postings.device
+    if out is None:
+        out = (torch.empty(max(n, 1) * shortlist_k, dtype=torch.int32, device=dev),
+               torch.empty(max(n, 1) * shortlist_k, dtype=torch.float32, device=dev),
+               torch.empty(max(n, 1), dtype=torch.int32, device=dev))
+    ids, dists, passes = out
+    ctx.check(ctx.lib.gofann_rabitq_posting_scan_segments(
+        ctx.handle, rv, rq, pred, _lib.ptr(route_query), _lib.ptr(postings), int(posting_rows),
+        segs.view(), shortlist_k,
+        _lib.ptr(rows.codes) if rows is not None else None,
+        _lib.ptr(rows.aux) if rows is not None else None,
+        _lib.ptr(cols.slab) if cols is not None else None,
+        _lib.ptr(cols.ranges) if cols is not None and cols.ranges is not None else None,
+        _lib.ptr(ids), _lib.ptr(dists), _lib.ptr(passes)))
+    return (ids[: n * shortlist_k].view(n, shortlist_k),
+            dists[: n * shortlist_k].view(n, shortlist_k), passes[:n])
+
+
 def rabitq_range_scan(ctx: _lib.Context, rv: _lib.RabitqView, rq: _lib.RabitqQueries,
                       pred: _lib.PredicateView, routes: _lib.Routes, postings: torch.Tensor,
                       resident_rows: int, segs: DeviceSegments, shortlist_k: int,

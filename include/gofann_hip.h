@@ -400,6 +400,47 @@ int gofann_rabitq_range_scan_resident(gofann_ctx* ctx, const gofann_rabitq_view*
                                       int score_first, uint32_t* out_ids, float* out_dists,
                                       uint32_t* pass_counts);
 
+/* ---- label postings in posting order: gofann_rabitq_posting_scan
+ * (lowfreq_rabitq_resident_posting_kernel, backend_rabitq.cu:5494-5682)
+ * over an explicit segment plan, so that a long posting is scanned by many
+ * workgroups, with optional posting-order copies of what each row's filter
+ * and score read.  No counterpart in the reference, whose scan gathers the
+ * label row, range value and code of every posting row by sample id.
+ *
+ * gofann_posting_predicate_rows fills, for rows [0, rows) of a posting
+ * array: out_slab [rows][4] u32 -- the sample's label row as a 16-byte slab
+ * (u16 count, then up to 7 u16 labels in CSR order; count 0xFFFF when the
+ * row has more labels, a label above 0xFFFF, no CSR, or the sample is
+ * >= predicate->rows) -- and out_ranges [rows][predicate->range_stride]
+ * (the sample's base range row; zeros without base ranges; may be NULL).
+ *
+ * gofann_rabitq_posting_scan_segments: segment s scans
+ * posting_sample_ids[offsets[s] .. + sizes[s]) (clipped to posting_rows)
+ * for route route_ids[s], filtered by the route's predicate alone, as
+ * gofann_rabitq_posting_scan does; with segments->query_indptr, output row
+ * p is route p's merge of segments [query_indptr[p], query_indptr[p+1]).
+ * With a plan from gofann_posting_segment_plan over (cand_offsets,
+ * cand_sizes) the outputs equal gofann_rabitq_posting_scan's bit for bit.
+ * posting_codes/posting_aux (gofann_rabitq_posting_rows over the same
+ * posting array, together or both NULL) and posting_slab/posting_ranges
+ * (gofann_posting_predicate_rows; ranges need the slab) are read at the
+ * row's posting position instead of gathered by sample id; any may be
+ * NULL.  shortlist_k <= 4096. */
+int gofann_posting_predicate_rows(gofann_ctx* ctx, const gofann_predicate_view* predicate,
+                                  const uint32_t* posting_sample_ids, uint64_t rows,
+                                  uint32_t* out_slab, float* out_ranges);
+
+int gofann_rabitq_posting_scan_segments(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                                        const gofann_rabitq_queries* prepared,
+                                        const gofann_predicate_view* predicate,
+                                        const uint32_t* route_query,
+                                        const uint32_t* posting_sample_ids, uint64_t posting_rows,
+                                        const gofann_posting_segments* segments, int shortlist_k,
+                                        const uint8_t* posting_codes, const uint32_t* posting_aux,
+                                        const uint32_t* posting_slab,
+                                        const float* posting_ranges, uint32_t* out_ids,
+                                        float* out_dists, uint32_t* pass_counts);
+
 /* ---- exact rerank on the GPU: per route, unique valid candidates of the
  * shortlist, exact L2 against base[samples][dim] (u8 / f32 / f16 with f32
  * queries for f32 and f16, u8 queries for u8), top-k by (distance, id). */

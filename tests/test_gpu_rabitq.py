@@ -230,3 +230,89 @@ def test_rabitq_posting_scan_matches_oracle(gpu_ctx, rworld, P, reps, k):
     assert np.array_equal(dists.cpu().numpy().reshape(n, k).view(np.uint32), od.view(np.uint32))
     assert np.array_equal(as_u32(passes), opass)
     assert (oi[:, 0] != U32MAX).sum() > n // 2 and opass.max() > 0
+
+
+@pytest.fixture(scope="module")
+def cworld():
+    """Label rows of 1..10 labels out of 12 (so some overflow the 7-label
+    slab), one label id above 0xFFFF, and one range attribute."""
+    wl = synth.small_labelled(n=7000, nq=48, dim=60, k=10, sigma=0.7, labels=4, seed=33,
+                              ranges=True)
+    rng = np.random.default_rng(3301)
+    ids = np.array(list(range(11)) + [70000], np.uint32)
+    cnt = rng.integers(1, 11, size=wl.n)
+    rows = [np.sort(ids[rng.choice(12, size=int(c), replace=False)]) for c in cnt]
+    wl.label_offsets = np.concatenate([[0], np.cumsum(cnt)]).astype(np.uint32)
+    wl.label_values = np.concatenate(rows).astype(np.uint32)
+    wl.num_labels = 70001
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=32, threshold=10**9)
+    P = 128
+    rot = gi.random_rotation(wl.dim, P, 33005, "cpu")
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
+    # routes: anchor label, 0..2 residual labels, the query's range on half
+    routes = []
+    for rep in range(3):
+        for qi in range(wl.queries.shape[0]):
+            lab = [int(x) for x in rng.choice(ids, size=int(rng.integers(1, 4)), replace=False)]
+            rngs = wl.query_ranges[qi] if (qi + rep) % 2 == 0 else []
+            routes.append((qi, lab[0], lab[1:], rngs))
+    return wl, li, routes, rot, codes, fac, aid, anchors, P
+
+
+# target_rows 97 cuts every posting into many segments; 1 << 20 keeps one
+# segment per route.  Each column set (none, codes, predicate columns,
+# both) must give the oracle's results bit for bit.
+@pytest.mark.parametrize("target", [97, 1 << 20])
+@pytest.mark.parametrize("codes_cols,pred_cols", [(False, False), (True, False), (False, True),
+                                                  (True, True)])
+def test_rabitq_posting_scan_segments_matches_oracle(gpu_ctx, cworld, target, codes_cols,
+                                                     pred_cols):
+    from gofann_amd import range_posting as rp
+    wl, li, routes, rot, codes, fac, aid, anchors, P = cworld
+    k = 40
+    say("posting scan segments target", target, "codes", codes_cols, "pred", pred_cols)
+    dev, rv = _rviews((wl, li, None, rot, codes, fac, aid, anchors, P))
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rs = gp._routeset(routes, li)
+    n = rs.count
+    off = np.array([li.posting_offset[r[1]] for r in routes], np.uint32)
+    size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]] for r in routes],
+                    np.uint32)
+    pred = po.PredicateArrays.from_plan(rs.predicate, li, base_ranges=wl.base_ranges)
+    oi, od, opass = po.posting_scan_rabitq(
+        pred, codes.numpy(), fac.numpy(), aid.numpy().astype(np.uint32),
+        out["q8"].cpu().numpy(), out["scale"].cpu().numpy(), out["k1"].cpu().numpy(),
+        out["cd"].cpu().numpy(), rs.route_query, li.posting_ids, off, size, k)
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+    pv = dr.predicate_view(dg, 0.0, False)
+    total = int(li.posting_offset[-1])
+    plan = rp.segment_plan(np.arange(n), off.astype(np.uint64), size.astype(np.uint64), target)
+    assert target > 1000 or plan.count > 4 * n
+    segs = rp.DeviceSegments(plan)
+    rows = rp.PostingRows(gpu_ctx, rv, dg.posting_ids, total) if codes_cols else None
+    cols = rp.PostingPredicateColumns(gpu_ctx, pv, dg.posting_ids, total) if pred_cols else None
+    ids, dists, passes = rp.rabitq_posting_scan_segments(
+        gpu_ctx, rv, rq, pv, dr.route_query, dg.posting_ids, total, segs, k, rows=rows, cols=cols)
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids).reshape(n, k), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(n, k).view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(as_u32(passes), opass)
+    assert (oi[:, 0] != U32MAX).sum() > n // 2 and opass.max() > 0
+    if cols is not None:
+        # the slab of a row with more than 7 labels, or with label 70000,
+        # is the overflow form; the others hold the row's labels
+        slab = cols.slab.cpu().numpy().view(np.uint32)
+        pid = li.posting_ids
+        lo, lv = wl.label_offsets, wl.label_values
+        for r in range(0, total, 97):
+            s = int(pid[r])
+            labs = lv[lo[s]:lo[s + 1]]
+            cnt = slab[r, 0] & 0xFFFF
+            if len(labs) > 7 or labs.max() > 0xFFFF:
+                assert cnt == 0xFFFF
+            else:
+                got = [(slab[r, (h >> 1)] >> (16 * (h & 1))) & 0xFFFF for h in range(1, cnt + 1)]
+                assert cnt == len(labs) and got == labs.tolist()
+            assert cols.ranges[r].item() == wl.base_ranges[s, 0]
