@@ -164,9 +164,12 @@ def plan_queries(index, query_labels: list, query_ranges: list | None = None,
 
 
 def dnf_route_rows(index, query_clauses: list, query_ranges: list | None = None,
-                   dual_ratio: float = 1e30, clause_scans: bool = False) -> tuple:
+                   dual_ratio: float = 1e30, clause_scans: bool = False,
+                   with_clause: bool = False) -> tuple:
     """(graph rows, posting rows) of plan_dnf, unsorted: one tuple
-    (query, anchor label, residual labels, residual range atoms) per route.
+    (query, anchor label, residual labels, residual range atoms) per route,
+    with the ordinal of the clause the route owns (its position in the
+    query's clause list) appended when `with_clause`.
 
     clause_scans: a clause that carries range atoms and labels also gets the
     route that enumerates its candidates exhaustively -- the reference's
@@ -180,7 +183,7 @@ def dnf_route_rows(index, query_clauses: list, query_ranges: list | None = None,
     graph_rows, post_rows = [], []
     for q, clauses in enumerate(query_clauses):
         rng = [tuple(a) for a in (query_ranges[q] if query_ranges is not None else [])]
-        for labels, uses_range in clauses:
+        for k, (labels, uses_range) in enumerate(clauses):
             labels = [int(l) for l in labels]
             cr = rng if uses_range else []
             if not labels:
@@ -188,14 +191,15 @@ def dnf_route_rows(index, query_clauses: list, query_ranges: list | None = None,
             kind, anchors = clause_anchors(index, labels, dual_ratio)
             if kind == "none":
                 continue
+            tag = (k,) if with_clause else ()
             for anchor in anchors:
-                row = (q, anchor, [l for l in labels if l != anchor], cr)
+                row = (q, anchor, [l for l in labels if l != anchor], cr) + tag
                 (post_rows if kind == "posting" else graph_rows).append(row)
             if clause_scans and cr:
                 cand = [l for l in labels if int(index.cat_freq[l]) > 0]
                 src = min(cand, key=lambda l: (int(index.cat_freq[l]), l))
                 if not (kind == "posting" and anchors == [src]):
-                    post_rows.append((q, src, [l for l in labels if l != src], cr))
+                    post_rows.append((q, src, [l for l in labels if l != src], cr) + tag)
     return graph_rows, post_rows
 
 

@@ -16,6 +16,9 @@
 //   include/smmh2.h                          (symmetric min-max heap)
 //   include/bin_heap.h                       (binary max-heap push/pop)
 //   src/search/common/native_visited_hash.cuh (visited hash)
+//   src/planning/route_predicate_plan.h      (route residual compile; with
+//                                             src/data/dataloader.h's inline
+//                                             runtime and clause-table types)
 // range_filter.cuh comes first: it defines __host__/__device__/__forceinline__
 // for a host compiler, which the three device headers above need.
 #include <cstdio>
@@ -32,6 +35,7 @@
 #include "execution/posting_segment_plan.h"
 #include "index/range_posting_index.h"
 #include "index/graph_file_format.h"
+#include "planning/route_predicate_plan.h"
 
 #include <cstdint>
 #include <cstring>
@@ -399,6 +403,116 @@ int ref_graph_file_convert_legacy(const char* legacy_path, const char* path, cha
 {
     try {
         go_fann::graph_file::convert_legacy_graph_file(legacy_path, path);
+        return 0;
+    } catch (const std::exception& e) {
+        return ref_error(e, error, error_bytes);
+    }
+}
+
+// route_predicate::compile (route_predicate_plan.h:175-315) for graph routes
+// (producer 0) or label-posting routes (producer 1) that own DNF clauses of
+// their original query, on an ungrouped label layout (group g is label g).
+// Query q owns clauses [q_indptr[q], q_indptr[q+1]); clause c has labels
+// [label_indptr[c], label_indptr[c+1]) and uses the query's range row when
+// uses_range[c].  Route r: original query route_query[r], anchor label
+// route_anchor[r] (its group), owned clauses [route_clause_indptr[r], +1).
+// label_rows[l]: posting size of label l (label-posting producer).
+//
+// Output, u32 words per route: available, entailed, clause count, then per
+// clause: label count, labels, range count, then per atom: dimension,
+// mode, lower bits, upper bits.  *out_words receives the length; returns
+// -2 when it exceeds `capacity`, -1 on a reference exception.
+int ref_route_compile(int producer, uint32_t queries, const uint64_t* q_indptr,
+                      const uint64_t* label_indptr, const uint32_t* labels,
+                      const uint8_t* uses_range, uint32_t range_count, const uint8_t* modes,
+                      const float* lower, const float* upper, uint32_t num_labels,
+                      uint32_t samples, const uint32_t* label_rows, uint32_t routes,
+                      const uint32_t* route_query, const uint32_t* route_anchor,
+                      const uint64_t* route_clause_indptr, const uint32_t* route_clause_ids,
+                      uint32_t* out, uint64_t capacity, uint64_t* out_words, char* error,
+                      uint32_t error_bytes)
+{
+    try {
+        namespace rp = go_fann::route_predicate;
+        GraphRuntime rt;
+        const uint64_t clauses = q_indptr[queries];
+        rt.original_query_count = queries;
+        rt.base_range_count = range_count;
+        rt.base_vectors.rows = samples;
+        rt.data_labels.rows = samples;
+        rt.data_labels.cols = num_labels;
+        rt.query_vectors.rows = routes;
+        auto& t = rt.original_query_clauses;
+        t.rows = queries;
+        t.query_indptr.assign(q_indptr, q_indptr + queries + 1);
+        t.label_indptr.assign(label_indptr, label_indptr + clauses + 1);
+        t.labels.assign(labels, labels + label_indptr[clauses]);
+        t.top_branch_ids.assign(clauses, 0u);
+        t.uses_original_range.assign(uses_range, uses_range + clauses);
+        auto& qr = rt.original_query_ranges;
+        qr.rows = queries;
+        qr.range_count = range_count;
+        qr.modes.assign(modes, modes + static_cast<size_t>(queries) * range_count);
+        qr.lower_bounds.assign(lower, lower + static_cast<size_t>(queries) * range_count);
+        qr.upper_bounds.assign(upper, upper + static_cast<size_t>(queries) * range_count);
+        rt.group_layout.groups.resize(num_labels);
+        rt.group_layout.label_to_group.resize(num_labels);
+        for (uint32_t l = 0; l < num_labels; ++l) {
+            rt.group_layout.groups[l] = {l};
+            rt.group_layout.label_to_group[l] = l;
+        }
+        rt.route_to_original_query.assign(route_query, route_query + routes);
+        rt.query_group_ids.assign(route_anchor, route_anchor + routes);
+        rt.query_filter_labels.assign(route_anchor, route_anchor + routes);
+        rt.route_clause_indptr.assign(route_clause_indptr, route_clause_indptr + routes + 1);
+        rt.route_clause_ids.assign(route_clause_ids, route_clause_ids + route_clause_indptr[routes]);
+        rp::Producer prod = rp::Producer::Graph;
+        if (producer == 0) {
+            rt.high_query_indices.resize(routes);
+            for (uint32_t r = 0; r < routes; ++r) rt.high_query_indices[r] = r;
+        } else {
+            prod = rp::Producer::LabelPosting;
+            rt.query_is_lowfreq.assign(routes, 1);
+            rt.route_providers.assign(routes, QueryRouteProvider::Label);
+            rt.route_candidate_sources.assign(routes, QueryCandidateSource::LabelPosting);
+            rt.route_execution_modes.assign(routes, QueryRouteExecution::GpuResidentScan);
+            auto& ix = rt.lowfreq_index;
+            ix.group_count = num_labels;
+            ix.label_size.assign(label_rows, label_rows + num_labels);
+            ix.label_offset.resize(num_labels);
+            uint64_t total = 0;
+            for (uint32_t l = 0; l < num_labels; ++l) {
+                ix.label_offset[l] = static_cast<uint32_t>(total);
+                total += label_rows[l];
+            }
+            ix.total_rows = static_cast<uint32_t>(total);
+            ix.sample_ids.assign(total, 0u);
+            ix.row_filter_mask.assign(total, 0ull);
+        }
+        const rp::Plan plan = rp::compile(rt, prod);
+        std::vector<uint32_t> w;
+        for (const rp::Route& route : plan.routes) {
+            w.push_back(route.available ? 1u : 0u);
+            w.push_back(route.entailed ? 1u : 0u);
+            w.push_back(static_cast<uint32_t>(route.clauses.size()));
+            for (const rp::Clause& c : route.clauses) {
+                w.push_back(static_cast<uint32_t>(c.labels.size()));
+                w.insert(w.end(), c.labels.begin(), c.labels.end());
+                w.push_back(static_cast<uint32_t>(c.ranges.size()));
+                for (const rp::RangeAtom& a : c.ranges) {
+                    uint32_t lo, hi;
+                    std::memcpy(&lo, &a.lower, 4);
+                    std::memcpy(&hi, &a.upper, 4);
+                    w.push_back(a.dimension);
+                    w.push_back(a.mode);
+                    w.push_back(lo);
+                    w.push_back(hi);
+                }
+            }
+        }
+        *out_words = w.size();
+        if (w.size() > capacity) return -2;
+        std::memcpy(out, w.data(), w.size() * 4);
         return 0;
     } catch (const std::exception& e) {
         return ref_error(e, error, error_bytes);
