@@ -21,6 +21,7 @@ measures one GPU.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -873,30 +874,56 @@ class RabitqRangePipeline:
         ev = self.ev
         if timed:
             ev[0].record()
+        start = self._prep()
+        if timed:
+            ev[1].record()
+        qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
+        for (lo, hi), q in zip(self.classes, qs):
+            if hi > lo:
+                self._graph(q, start, lo, hi)
+        if timed:
+            ev[2].record()
+        self._scan()
+        if timed:
+            ev[3].record()
+        n = self.ng + self.np_
+        fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
+                                       self.sl_i, W, n, 10)
+        if timed:
+            ev[4].record()
+        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, fin_i, fin_d, 10,
+                                       self.nq, 10)
+        if timed:
+            ev[5].record()
+        return out_i
+
+    def _prep(self):
+        """Query preparation; the per-route entry rows when a coarse entry
+        is set (else None: every route starts at its medoid)."""
+        L, ctx = self.L, self.ctx
         ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, self.rv,
                                                         L.ptr(self.wl.queries), self.nq,
                                                         L.ptr(self.dev["rot"]), self.rq))
-        start = None
         if self.entry is not None and self.ng:
             # the anchors are the trained centres, rotated: the preparation's
             # query-anchor distances already rank them
             near = self.prep["cd"].argmin(1)
-            start = self.entry.seeds(near, self.dr.route_query, self.dr.route_group,
-                                     out=self.seed_buf)
-        if timed:
-            ev[1].record()
-        pv = self.dr.predicate_view(self.dg, 0.15, True)
-        qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
-        for (lo, hi), q in zip(self.classes, qs):
-            if hi > lo:
-                prm = gs.search_params(queue_limit=q, result_width=W, early_stop_mode=2,
-                                       bias=True)
-                ctx.check(ctx.lib.gofann_rabitq_search(
-                    ctx.handle, self.rv, self.rq, self.dg.view(), pv,
-                    self.dr.routes_view(lo, hi, start=start), prm,
-                    L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
-        if timed:
-            ev[2].record()
+            return self.entry.seeds(near, self.dr.route_query, self.dr.route_group,
+                                    out=self.seed_buf)
+        return None
+
+    def _graph(self, q, start, lo, hi):
+        """RaBitQ traversal of graph routes [lo, hi) at beam q."""
+        L, gs, ctx = self.L, self.gs, self.ctx
+        prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
+        ctx.check(ctx.lib.gofann_rabitq_search(
+            ctx.handle, self.rv, self.rq, self.dg.view(),
+            self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(lo, hi, start=start),
+            prm, L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
+
+    def _scan(self):
+        """The range-posting scan of the posting routes (rows [ng, ng + np_))."""
+        L, ctx, W = self.L, self.ctx, self.W
         if self.np_:
             routes = L.Routes(L.ptr(self.post_query), None, None, None, None, L.ptr(self.modes_p),
                               L.ptr(self.lo_p), L.ptr(self.hi_p), L.ptr(self.brv), 1, self.np_,
@@ -914,18 +941,6 @@ class RabitqRangePipeline:
                     L.ptr(self.postings), self.resident, self.segs.view(), W, 0,
                     L.ptr(self.sl_i[self.ng * W:]), L.ptr(self.sl_d[self.ng * W:]),
                     L.ptr(self.passes)))
-        if timed:
-            ev[3].record()
-        n = self.ng + self.np_
-        fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
-                                       self.sl_i, W, n, 10)
-        if timed:
-            ev[4].record()
-        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, fin_i, fin_d, 10,
-                                       self.nq, 10)
-        if timed:
-            ev[5].record()
-        return out_i
 
     def stage_ms(self):
         e = self.ev
@@ -1070,6 +1085,13 @@ def run_c3(args, torch, ctx) -> dict:
                            "trained centres (from the preparation's query-anchor distances), "
                            "inside the step")
         pipe.entry = None
+    cpu_route = None
+    if not args.no_cpu_rerank_route:
+        qb = med["queue_by_class"]
+        cpu_route = cpu_rerank_leg(args, pipe, tuple(qb[n] for n, _ in class_gt), class_gt,
+                                   "C3 GPU + CPU rerank", wl.base.cpu().numpy(),
+                                   wl.queries.cpu().numpy())
+        gc.collect()
     cpu = None
     if not args.no_cpu_baseline:
         qb = med["queue_by_class"]
@@ -1087,7 +1109,8 @@ def run_c3(args, torch, ctx) -> dict:
             "shortlist": pipe.W, "gt_queries": len(gt),
             "graph_buckets": "512 k-means centres trained on the base",
             "data_model": "centre + rank-64 shared-basis spread 0.7 + N(0, 0.05^2), normalised",
-            "medoid_seeds": med, "coarse_entry": coarse, "cpu_baseline": cpu}
+            "medoid_seeds": med, "coarse_entry": coarse, "gpu_cpu_rerank_route": cpu_route,
+            "cpu_baseline": cpu}
 
 
 def main_c3(args):
@@ -1321,42 +1344,16 @@ class RabitqLabelPipeline:
         ev = self.ev
         if timed:
             ev[0].record()
-        ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, self.rv,
-                                                        L.ptr(self.wl.queries), self.nq,
-                                                        L.ptr(self.dev["rot"]), self.rq))
-        start = None
-        if self.entry is not None and self.ng:
-            # the anchors are the trained centres, rotated: the preparation's
-            # query-anchor distances already rank them
-            near = self.prep["cd"].argmin(1)
-            start = self.entry.seeds(near, self.dr.route_query, self.dr.route_group,
-                                     out=self.seed_buf)
+        start = self._prep()
         if timed:
             ev[1].record()
-        pv = self.dr.predicate_view(self.dg, 0.15, True)
         qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
         for (lo, hi), q in zip(self.classes, qs):
             if hi > lo:
-                prm = gs.search_params(queue_limit=q, result_width=W, early_stop_mode=2,
-                                       bias=True)
-                ctx.check(ctx.lib.gofann_rabitq_search(
-                    ctx.handle, self.rv, self.rq, self.dg.view(), pv,
-                    self.dr.routes_view(lo, hi, start=start), prm,
-                    L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
+                self._graph(q, start, lo, hi)
         if timed:
             ev[2].record()
-        if self.np_ and self.posting_layout == "columns":
-            self.rp.rabitq_posting_scan_segments(
-                ctx, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
-                self.dp.route_query, self.scan_ids, self.scan_total, self.scan_segs, W,
-                rows=self.scan_rows, cols=self.scan_cols,
-                out=(self.sl_i[self.ng * W:], self.sl_d[self.ng * W:], self.passes))
-        elif self.np_:
-            ctx.check(ctx.lib.gofann_rabitq_posting_scan(
-                ctx.handle, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
-                L.ptr(self.dp.route_query), L.ptr(self.dg.posting_ids), L.ptr(self.co),
-                L.ptr(self.cs), self.np_, W, L.ptr(self.sl_i[self.ng * W:]),
-                L.ptr(self.sl_d[self.ng * W:]), L.ptr(self.passes)))
+        self._scan()
         if timed:
             ev[3].record()
         n = self.ng + self.np_
@@ -1369,6 +1366,46 @@ class RabitqLabelPipeline:
         if timed:
             ev[5].record()
         return out_i
+
+    def _prep(self):
+        """Query preparation; the per-route entry rows when a coarse entry
+        is set (else None: every route starts at its medoid)."""
+        L, ctx = self.L, self.ctx
+        ctx.check(ctx.lib.gofann_rabitq_prepare_queries(ctx.handle, self.rv,
+                                                        L.ptr(self.wl.queries), self.nq,
+                                                        L.ptr(self.dev["rot"]), self.rq))
+        if self.entry is not None and self.ng:
+            # the anchors are the trained centres, rotated: the preparation's
+            # query-anchor distances already rank them
+            near = self.prep["cd"].argmin(1)
+            return self.entry.seeds(near, self.dr.route_query, self.dr.route_group,
+                                    out=self.seed_buf)
+        return None
+
+    def _graph(self, q, start, lo, hi):
+        """RaBitQ traversal of graph routes [lo, hi) at beam q."""
+        L, gs, ctx = self.L, self.gs, self.ctx
+        prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
+        ctx.check(ctx.lib.gofann_rabitq_search(
+            ctx.handle, self.rv, self.rq, self.dg.view(),
+            self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(lo, hi, start=start),
+            prm, L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
+
+    def _scan(self):
+        """The label-posting scan of the posting routes (rows [ng, ng + np_))."""
+        L, ctx, W = self.L, self.ctx, self.W
+        if self.np_ and self.posting_layout == "columns":
+            self.rp.rabitq_posting_scan_segments(
+                ctx, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
+                self.dp.route_query, self.scan_ids, self.scan_total, self.scan_segs, W,
+                rows=self.scan_rows, cols=self.scan_cols,
+                out=(self.sl_i[self.ng * W:], self.sl_d[self.ng * W:], self.passes))
+        elif self.np_:
+            ctx.check(ctx.lib.gofann_rabitq_posting_scan(
+                ctx.handle, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
+                L.ptr(self.dp.route_query), L.ptr(self.dg.posting_ids), L.ptr(self.co),
+                L.ptr(self.cs), self.np_, W, L.ptr(self.sl_i[self.ng * W:]),
+                L.ptr(self.sl_d[self.ng * W:]), L.ptr(self.passes)))
 
     def stage_ms(self):
         e = self.ev
@@ -1441,6 +1478,89 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
                          "algorithmic_bytes": kern[top][1]}}
 
 
+def cpu_rerank_leg(args, pipe, beams, class_gt, label, host_base, host_queries, chunks=1):
+    """The GPU + CPU-rerank route of C3/C4: the configs' exact host rerank of
+    the W-wide shortlists (fp32 for C3; fp16 decoded to fp32 for C4,
+    fp16_l2.h:93-179) instead of the GPU rerank.  The GPU runs the same route
+    set at the same per-class beams: the posting scan first, then `chunks`
+    launches per route class (one by default, so every launch fills the
+    GPU as in the all-GPU step); each task's shortlists are copied to pinned
+    host memory and reranked by the host pool while later tasks run
+    (search.StreamedRerank); routes merge per query on the host.  Reported
+    as the reference reports this route (tools/reproduce/reference/
+    window.csv): GPU-only time, the overlapped wall time and the exposed
+    rerank time, plus the host rerank of the whole shortlist set alone."""
+    gs, torch = pipe.gs, pipe.torch
+    T = host_threads()
+    n, W = pipe.ng + pipe.np_, pipe.W
+    r2q = pipe.route_query.cpu().numpy().view(np.uint32)[:n].copy()
+    hr = gs.HostRerank(host_base, host_queries, threads=T)
+    sr = gs.StreamedRerank(hr, n, W)
+    ids = np.empty((n, 10), np.uint32)
+    dists = np.empty((n, 10), np.float32)
+    def tasks():
+        out = []
+        first = [True]
+
+        def prep_once():
+            if first[0]:
+                pipe._prep()
+                first[0] = False
+
+        def graph(q, c0, c1):
+            def go():
+                prep_once()
+                pipe._graph(q, None, c0, c1)
+            return go
+
+        if pipe.np_:
+            def scan():
+                prep_once()
+                pipe._scan()
+            out.append((pipe.ng, n, scan))
+        for (lo, hi), q in zip(pipe.classes, beams):
+            if hi <= lo:
+                continue
+            per = max(1, -(-(hi - lo) // chunks))
+            for c0 in range(lo, hi, per):
+                out.append((c0, min(hi, c0 + per), graph(q, c0, min(hi, c0 + per))))
+        return out
+
+    def one():
+        t0 = time.perf_counter()
+        sr.run(tasks(), pipe.sl_i, r2q, 10, ids, dists)
+        mi, _ = gs.host_merge_routes(r2q, ids, dists, pipe.nq, 10)
+        return mi, (time.perf_counter() - t0) * 1000.0
+
+    for _ in range(args.warmup):
+        one()
+    walls, split = [], []
+    for _ in range(args.steps):
+        mi, ms = one()
+        walls.append(ms)
+        split.append(dict(sr.timing))
+    gt = {q: v for _, g in class_gt for q, v in g.items()}
+    rec = recall_at_10(mi, gt)
+    by_class = {nm: round(recall_at_10(mi, g), 4) if g else None for nm, g in class_gt}
+    # the host rerank of the whole shortlist set, alone
+    sl = sr.pinned[: n * W].numpy().view(np.uint32).reshape(n, W)
+    t0 = time.perf_counter()
+    hr.rerank(sl, r2q, 10)
+    alone = (time.perf_counter() - t0) * 1000.0
+    hr.close()
+    ms = float(np.mean(walls))
+    avg = {k: round(float(np.mean([d[k] for d in split])), 3) for k in split[0]}
+    res = {"qps": round(pipe.nq / (ms / 1000.0), 1), "ms_per_step": round(ms, 3),
+           "queue_by_class": dict(zip([nm for nm, _ in class_gt], beams)),
+           "recall_at_10": round(rec, 4), "recall_by_class": by_class,
+           "graph_only_ms": avg["gpu_ms"], "overlapped_ms": avg["wall_ms"],
+           "exposed_rerank_ms": avg["exposed_ms"], "host_rerank_alone_ms": round(alone, 3),
+           "host_threads": T, "tasks": len(tasks()), "cpu": cpu_model(),
+           "rerank": f"exact {host_base.dtype} on the host, streamed behind the GPU search"}
+    log(f"{label}: {res}")
+    return res
+
+
 def c4_kernels(pipe, st_ms, st):
     P, wl, li = pipe.P, pipe.wl, pipe.li
     tb = rabitq_traversal_bytes(st, li.degree, P // 8)
@@ -1511,6 +1631,13 @@ def run_c4(args, torch, ctx, world=None) -> dict:
                            "trained centres (from the preparation's query-anchor distances), "
                            "inside the step")
         pipe.entry = None
+    cpu_route = None
+    if not args.no_cpu_rerank_route:
+        qb = med["queue_by_class"]
+        cpu_route = cpu_rerank_leg(args, pipe, (qb["equality"], qb["range"]), class_gt,
+                                   "C4 GPU + CPU rerank", wl.base.cpu().numpy(),
+                                   wl.queries.cpu().numpy())
+        gc.collect()
     cpu = None
     if not args.no_cpu_baseline:
         pipe.chosen = (med["queue_by_class"]["equality"], med["queue_by_class"]["range"])
@@ -1527,7 +1654,8 @@ def run_c4(args, torch, ctx, world=None) -> dict:
             "interior_interval_routes": pipe.interior, "posting_routes": pipe.np_,
             "posting_rows": pipe.post_rows_total, "shortlist": pipe.W, "gt_queries": len(gt),
             "graph_buckets": "4096 k-means centres trained on the base",
-            "medoid_seeds": med, "coarse_entry": coarse, "cpu_baseline": cpu}
+            "medoid_seeds": med, "coarse_entry": coarse, "gpu_cpu_rerank_route": cpu_route,
+            "cpu_baseline": cpu}
 
 
 # ---------------------------------------------------------------------------

@@ -13,6 +13,14 @@
 //     enter the result heap), as the reference assumes for its GPU predicate
 //     mode (shortlist_verified, backend_pq.cu:9725), so labels are not
 //     re-checked here;
+//   * fp16 rows: the reference picks its fp16 L2 kernel at run time
+//     (fp16_l2::select, src/data/fp16_l2.h:53-70; GO_FANN_FP16_RERANK_KERNEL,
+//     dataloader.cpp:2131-2133): AVX-512 when the CPU has it, else AVX2, else
+//     scalar, and each kernel has its own summation order (16 or 8 lane
+//     partial sums, then the lanes in order, then the tail; scalar: the
+//     dimensions in order).  The same choice and the same orders are made
+//     here (GOFANN_FP16_RERANK_KERNEL = auto | scalar | avx2 | avx512), so a
+//     distance equals the reference's on the same machine;
 //   * streaming (run_highfreq_streaming_rerank, backend_pq.cu:9646-9738):
 //     the reference polls per-route mapped status flags; here routes run in
 //     chunks on the compute stream, each chunk's shortlist is copied into
@@ -21,8 +29,13 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#if defined(__x86_64__) && !defined(__HIP_DEVICE_COMPILE__)
+#include <immintrin.h>
+#endif
+
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <cfloat>
 #include <condition_variable>
 #include <cstdint>
@@ -45,6 +58,7 @@ struct gofann_host_rerank {
     uint32_t samples = 0;
     const void* queries = nullptr;   // host [queries][dim] (u8 for u8 base, else f32)
     uint32_t threads = 1;
+    int fp16_kernel = 0;             // kFp16Scalar / kFp16Avx2 / kFp16Avx512
     std::string error;
 
     // Worker pool: a queue of jobs, each a half-open route range.
@@ -96,6 +110,35 @@ float l2_f32(const float* q, const float* b, uint32_t dim)
     return dist;
 }
 
+constexpr int kFp16Scalar = 0;
+constexpr int kFp16Avx2 = 1;
+constexpr int kFp16Avx512 = 2;
+
+const char* fp16_kernel_name(int k)
+{
+    return k == kFp16Avx512 ? "avx512" : (k == kFp16Avx2 ? "avx2" : "scalar");
+}
+
+// The x86 kernels exist in the host pass only (hipcc also compiles this
+// file for the device, where there is no CPU to ask).
+#if defined(__x86_64__) && !defined(__HIP_DEVICE_COMPILE__)
+#define GOFANN_HOST_X86 1
+#else
+#define GOFANN_HOST_X86 0
+#endif
+
+bool fp16_kernel_supported(int k)
+{
+    if (k == kFp16Scalar) return true;
+#if GOFANN_HOST_X86
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("f16c") && __builtin_cpu_supports("avx2") &&
+           (k != kFp16Avx512 || __builtin_cpu_supports("avx512f"));
+#else
+    return false;
+#endif
+}
+
 float l2_f16(const float* q, const __half* b, uint32_t dim)
 {
     float dist = 0.0f;
@@ -105,6 +148,58 @@ float l2_f16(const float* q, const __half* b, uint32_t dim)
     }
     return dist;
 }
+
+#if GOFANN_HOST_X86
+// Lane-partial sums: lane l accumulates the squared differences of the
+// dimensions d = l (mod lanes) of the whole blocks, in block order; the lane
+// sums are then added in lane order, then the tail dimensions in order.
+// Products and sums are separate roundings (no fused multiply-add).
+__attribute__((target("avx2,f16c"))) float l2_f16_avx2(const float* q, const __half* b,
+                                                        uint32_t dim)
+{
+    __m256 acc = _mm256_setzero_ps();
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+    uint32_t d = 0;
+    for (; d + 8 <= dim; d += 8) {
+        const __m256 x = _mm256_cvtph_ps(_mm_loadu_si128(reinterpret_cast<const __m128i*>(h + d)));
+        const __m256 diff = _mm256_sub_ps(_mm256_loadu_ps(q + d), x);
+        acc = _mm256_add_ps(acc, _mm256_mul_ps(diff, diff));
+    }
+    alignas(32) float lane[8];
+    _mm256_store_ps(lane, acc);
+    float dist = 0.0f;
+    for (int l = 0; l < 8; ++l) dist += lane[l];
+    for (; d < dim; ++d) {
+        const float diff = q[d] - __half2float(b[d]);
+        dist += diff * diff;
+    }
+    return dist;
+}
+
+__attribute__((target("avx512f,avx2,f16c"))) float l2_f16_avx512(const float* q,
+                                                                   const __half* b,
+                                                                   uint32_t dim)
+{
+    __m512 acc = _mm512_setzero_ps();
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+    uint32_t d = 0;
+    for (; d + 16 <= dim; d += 16) {
+        const __m512 x =
+            _mm512_cvtph_ps(_mm256_loadu_si256(reinterpret_cast<const __m256i*>(h + d)));
+        const __m512 diff = _mm512_sub_ps(_mm512_loadu_ps(q + d), x);
+        acc = _mm512_add_ps(acc, _mm512_mul_ps(diff, diff));
+    }
+    alignas(64) float lane[16];
+    _mm512_store_ps(lane, acc);
+    float dist = 0.0f;
+    for (int l = 0; l < 16; ++l) dist += lane[l];
+    for (; d < dim; ++d) {
+        const float diff = q[d] - __half2float(b[d]);
+        dist += diff * diff;
+    }
+    return dist;
+}
+#endif
 
 float exact_distance(const gofann_host_rerank* hr, uint32_t query, uint32_t sample)
 {
@@ -116,8 +211,13 @@ float exact_distance(const gofann_host_rerank* hr, uint32_t query, uint32_t samp
     if (hr->elem == GOFANN_ELEM_F32)
         return l2_f32(static_cast<const float*>(hr->queries) + qo,
                       static_cast<const float*>(hr->base) + bo, hr->dim);
-    return l2_f16(static_cast<const float*>(hr->queries) + qo,
-                  static_cast<const __half*>(hr->base) + bo, hr->dim);
+    const float* qf = static_cast<const float*>(hr->queries) + qo;
+    const __half* bh = static_cast<const __half*>(hr->base) + bo;
+#if GOFANN_HOST_X86
+    if (hr->fp16_kernel == kFp16Avx512) return l2_f16_avx512(qf, bh, hr->dim);
+    if (hr->fp16_kernel == kFp16Avx2) return l2_f16_avx2(qf, bh, hr->dim);
+#endif
+    return l2_f16(qf, bh, hr->dim);
 }
 
 bool pair_less(float ad, uint32_t ai, float bd, uint32_t bi)
@@ -231,6 +331,31 @@ int gofann_host_rerank_create(const void* base, int base_elem, uint32_t dim, uin
     hr->samples = samples;
     hr->queries = queries;
     hr->threads = threads == 0 ? 1 : threads;
+    {
+        // the reference's fp16 kernel choice (fp16_l2::select)
+        const char* env = std::getenv("GOFANN_FP16_RERANK_KERNEL");
+        const std::string req = env ? env : "auto";
+        int k;
+        if (req.empty() || req == "auto") {
+            k = fp16_kernel_supported(kFp16Avx512)
+                    ? kFp16Avx512
+                    : (fp16_kernel_supported(kFp16Avx2) ? kFp16Avx2 : kFp16Scalar);
+        } else if (req == "scalar") {
+            k = kFp16Scalar;
+        } else if (req == "avx2") {
+            k = kFp16Avx2;
+        } else if (req == "avx512") {
+            k = kFp16Avx512;
+        } else {
+            delete hr;
+            return GOFANN_ERR_INVALID;  // unknown kernel name
+        }
+        if (!fp16_kernel_supported(k)) {
+            delete hr;
+            return GOFANN_ERR_UNSUPPORTED;  // the CPU lacks the requested ISA
+        }
+        hr->fp16_kernel = k;
+    }
     try {
         for (uint32_t t = 0; t < hr->threads; ++t) hr->workers.emplace_back(worker_loop, hr);
     } catch (...) {
@@ -267,6 +392,11 @@ void gofann_host_rerank_destroy(gofann_host_rerank* hr)
 const char* gofann_host_rerank_last_error(const gofann_host_rerank* hr)
 {
     return hr ? hr->error.c_str() : "null rerank handle";
+}
+
+const char* gofann_host_rerank_fp16_kernel(const gofann_host_rerank* hr)
+{
+    return hr ? fp16_kernel_name(hr->fp16_kernel) : "";
 }
 
 int gofann_host_rerank_routes(gofann_host_rerank* hr, const uint32_t* shortlist, uint32_t width,

@@ -193,6 +193,7 @@ SIGNATURES = {
     "gofann_host_rerank_create": (C.c_int, [P, C.c_int, U32, U32, P, U32, C.POINTER(P)]),
     "gofann_host_rerank_destroy": (None, [P]),
     "gofann_host_rerank_last_error": (C.c_char_p, [P]),
+    "gofann_host_rerank_fp16_kernel": (C.c_char_p, [P]),
     "gofann_host_rerank_routes": (C.c_int, [P, P, U32, P, U32, U32, P, P]),
     "gofann_pq_search_host_rerank": (C.c_int, [P, P, C.POINTER(PqView), P, C.c_int,
                                                C.POINTER(GraphView), C.POINTER(PredicateView),

@@ -417,6 +417,11 @@ class HostRerank:
             raise _lib.GofannError(f"gofann_host_rerank_create failed ({rc})")
         self.handle = h
 
+    @property
+    def fp16_kernel(self) -> str:
+        """The fp16 L2 kernel chosen at create ("scalar", "avx2", "avx512")."""
+        return self.lib.gofann_host_rerank_fp16_kernel(self.handle).decode()
+
     def _check(self, rc):
         if rc != 0:
             msg = self.lib.gofann_host_rerank_last_error(self.handle)
@@ -465,6 +470,87 @@ class HostRerank:
             self.close()
         except Exception:
             pass
+
+
+class StreamedRerank:
+    """Host exact rerank streamed behind GPU work in route chunks, for any
+    producer of device shortlists (the schedule of the reference's
+    run_highfreq_streaming_rerank, backend_pq.cu:9646-9738, which overlaps
+    the host rerank of finished routes with the search of the next ones).
+
+    run() takes tasks (r0, r1, launch): launch() enqueues, on the current
+    stream, the GPU work that writes the shortlist rows [r0, r1) of `d_ids`
+    (width ids each).  After each task an event is recorded; a copy stream
+    waits for it and copies the task's rows into pinned host memory; a host
+    thread waits for each copy and reranks those routes with the HostRerank
+    pool while the GPU runs later tasks.  Timing of the last run:
+    gpu_ms = GPU time from the first launch to the end of the last (events
+    on the compute stream), wall_ms = the whole call, exposed_ms =
+    wall_ms - gpu_ms (rerank time not hidden behind the GPU)."""
+
+    def __init__(self, hr: HostRerank, rows: int, width: int):
+        self.hr, self.width = hr, int(width)
+        self.pinned = torch.empty(max(int(rows), 1) * self.width, dtype=torch.int32,
+                                  pin_memory=True)
+        self.copy_stream = torch.cuda.Stream()
+        self.timing = {}
+
+    def run(self, tasks, d_ids: torch.Tensor, route_query: np.ndarray, topk: int,
+            out_ids: np.ndarray, out_dists: np.ndarray):
+        import queue
+        import threading
+        import time
+        W = self.width
+        rq = np.ascontiguousarray(route_query, dtype=np.uint32)
+        base = self.pinned.data_ptr()
+        lib, handle = self.hr.lib, self.hr.handle
+        work: queue.Queue = queue.Queue()
+        errors = []
+
+        def worker():
+            while True:
+                item = work.get()
+                if item is None:
+                    return
+                r0, r1, done = item
+                done.synchronize()
+                if errors:
+                    continue
+                rc = lib.gofann_host_rerank_routes(
+                    handle, base + r0 * W * 4, W, _np_ptr(rq) + r0 * 4, r1 - r0, topk,
+                    _np_ptr(out_ids) + r0 * topk * 4, _np_ptr(out_dists) + r0 * topk * 4)
+                if rc != 0:
+                    errors.append(rc)
+
+        cur = torch.cuda.current_stream()
+        t0 = time.perf_counter()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        th = threading.Thread(target=worker, daemon=True)
+        th.start()
+        try:
+            e0.record(cur)
+            for r0, r1, launch in tasks:
+                launch()
+                ready = torch.cuda.Event()
+                ready.record(cur)
+                self.copy_stream.wait_event(ready)
+                with torch.cuda.stream(self.copy_stream):
+                    self.pinned[r0 * W:r1 * W].copy_(d_ids[r0 * W:r1 * W], non_blocking=True)
+                    done = torch.cuda.Event()
+                    done.record(self.copy_stream)
+                work.put((r0, r1, done))
+            e1.record(cur)
+        finally:
+            work.put(None)
+            th.join()
+        wall = (time.perf_counter() - t0) * 1000.0
+        e1.synchronize()
+        gpu = e0.elapsed_time(e1)
+        if errors:
+            self.hr._check(errors[0])
+        self.timing = {"gpu_ms": gpu, "wall_ms": wall, "exposed_ms": max(0.0, wall - gpu)}
+        return out_ids, out_dists
 
 
 def host_merge_routes(route_to_query: np.ndarray, ids: np.ndarray, dists: np.ndarray,

@@ -490,6 +490,14 @@ int gofann_host_rerank_create(const void* base, int base_elem, uint32_t dim, uin
                               const void* queries, uint32_t threads, gofann_host_rerank** out);
 void gofann_host_rerank_destroy(gofann_host_rerank* hr);
 const char* gofann_host_rerank_last_error(const gofann_host_rerank* hr);
+/* fp16 rows: the L2 kernel chosen at create, as the reference chooses it
+ * (fp16_l2::select, src/data/fp16_l2.h:53-70): environment variable
+ * GOFANN_FP16_RERANK_KERNEL = auto (AVX-512 if the CPU has it, else AVX2,
+ * else scalar) | scalar | avx2 | avx512, each with the reference kernel's
+ * summation order.  An unknown name makes create return GOFANN_ERR_INVALID,
+ * an ISA the CPU lacks GOFANN_ERR_UNSUPPORTED.  Returns "scalar", "avx2"
+ * or "avx512". */
+const char* gofann_host_rerank_fp16_kernel(const gofann_host_rerank* hr);
 /* Host arrays only: shortlist [routes][width], route_query [routes],
  * outputs [routes][topk]. */
 int gofann_host_rerank_routes(gofann_host_rerank* hr, const uint32_t* shortlist, uint32_t width,

@@ -316,3 +316,48 @@ def test_rabitq_posting_scan_segments_matches_oracle(gpu_ctx, cworld, target, co
                 got = [(slab[r, (h >> 1)] >> (16 * (h & 1))) & 0xFFFF for h in range(1, cnt + 1)]
                 assert cnt == len(labs) and got == labs.tolist()
             assert cols.ranges[r].item() == wl.base_ranges[s, 0]
+
+
+def test_streamed_host_rerank_matches_direct(gpu_ctx, rworld):
+    """RaBitQ traversal in route chunks with each chunk's shortlist streamed
+    to the host rerank pool (search.StreamedRerank): the chunked shortlists
+    equal one unchunked launch, and the streamed rerank equals the pool's
+    direct rerank of the same shortlists, bit for bit."""
+    wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
+    say("streamed host rerank")
+    dev, rv = _rviews(rworld)
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rs = pl.graph
+    n, W = rs.count, 30
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs)
+    pv = dr.predicate_view(dg, 0.15, True)
+    prm = gs.search_params(queue_limit=40, result_width=W, early_stop_mode=2, bias=True)
+
+    def launch(ids, dists, c0, c1):
+        gpu_ctx.check(gpu_ctx.lib.gofann_rabitq_search(
+            gpu_ctx.handle, rv, rq, dg.view(), pv, dr.routes_view(c0, c1), prm, _lib.ptr(ids),
+            _lib.ptr(dists), None))
+
+    ids_a = torch.empty(n * W, dtype=torch.int32, device="cuda")
+    d_a = torch.empty(n * W, device="cuda")
+    launch(ids_a, d_a, 0, n)
+    torch.cuda.synchronize()
+    sl = as_u32(ids_a).reshape(n, W)
+    hr = gs.HostRerank(wl.base.numpy(), wl.queries.numpy(), threads=4)
+    want_i, want_d = hr.rerank(sl, rs.route_query, 10)
+    ids_b = torch.full((n * W,), -1, dtype=torch.int32, device="cuda")
+    d_b = torch.empty(n * W, device="cuda")
+    sr = gs.StreamedRerank(hr, n, W)
+    tasks = [(c0, min(n, c0 + 7), (lambda c0=c0: launch(ids_b, d_b, c0, min(n, c0 + 7))))
+             for c0 in range(0, n, 7)]
+    got_i = np.empty((n, 10), np.uint32)
+    got_d = np.empty((n, 10), np.float32)
+    sr.run(tasks, ids_b, rs.route_query, 10, got_i, got_d)
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids_b).reshape(n, W), sl)
+    assert np.array_equal(got_i, want_i)
+    assert np.array_equal(got_d.view(np.uint32), want_d.view(np.uint32))
+    assert sr.timing["gpu_ms"] > 0 and sr.timing["wall_ms"] >= sr.timing["gpu_ms"] * 0.5
+    assert (want_i[:, 0] != U32MAX).sum() > n // 2
+    hr.close()

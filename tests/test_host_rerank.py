@@ -81,3 +81,70 @@ def test_host_merge_matches_oracle():
     hi, hd = gs.host_merge_routes(r2q, ids, d, queries, topk)
     assert np.array_equal(hi, oi)
     assert np.array_equal(hd.view(np.uint32), od.view(np.uint32))
+
+
+def _lane_order_l2(q, b, lanes):
+    """Squared L2 in one fp16 kernel's summation order, float32 throughout:
+    lane l sums the squared differences of dimensions d = l (mod lanes) of
+    the whole blocks, the lane sums are added in lane order, then the tail
+    in order (lanes = 1: the dimensions in order)."""
+    q = q.astype(np.float32)
+    b = b.astype(np.float32)  # fp16 -> fp32 is exact
+    dim = q.shape[0]
+    main = dim - dim % lanes if lanes > 1 else 0
+    total = np.float32(0)
+    if main:
+        sq = (q[:main] - b[:main]) * (q[:main] - b[:main])
+        acc = np.zeros(lanes, np.float32)
+        for blk in range(main // lanes):
+            acc = acc + sq[blk * lanes:(blk + 1) * lanes]
+        for l in range(lanes):
+            total = np.float32(total + acc[l])
+    for d in range(main, dim):
+        diff = np.float32(q[d] - b[d])
+        total = np.float32(total + np.float32(diff * diff))
+    return total
+
+
+@pytest.mark.parametrize("kernel,lanes", [("scalar", 1), ("avx2", 8), ("avx512", 16)])
+@pytest.mark.parametrize("dim", [40, 512, 77])
+def test_host_rerank_fp16_kernels_follow_their_order(monkeypatch, kernel, lanes, dim):
+    """Each fp16 kernel (fp16_l2.h's scalar / avx2 / avx512) computes every
+    distance in its own summation order, bit for bit; "auto" picks the
+    widest the CPU supports, as fp16_l2::select does."""
+    lib = gs._lib.load()
+    monkeypatch.setenv("GOFANN_FP16_RERANK_KERNEL", kernel)
+    rng = np.random.default_rng(dim)
+    n, nq, routes, width = 600, 8, 40, 30
+    base = (rng.standard_normal((n, dim)) * 3).astype(np.float16)
+    queries = (rng.standard_normal((nq, dim)) * 3).astype(np.float32)
+    rq = rng.integers(0, nq, size=routes).astype(np.uint32)
+    sl = _shortlists(rng, routes, width, n, dup=False)
+    try:
+        hr = gs.HostRerank(base, queries, threads=2)
+    except gs._lib.GofannError:
+        pytest.skip(f"this CPU lacks the {kernel} kernel's ISA")
+    assert hr.fp16_kernel == kernel
+    hi, hd = hr.rerank(sl, rq, 10)
+    hr.close()
+    for r in range(routes):
+        for i, d in zip(hi[r], hd[r]):
+            if i == U32MAX:
+                continue
+            want = _lane_order_l2(queries[rq[r]], base[i], lanes)
+            assert np.float32(d).view(np.uint32) == want.view(np.uint32), (r, i)
+    # auto = the reference's rule
+    monkeypatch.setenv("GOFANN_FP16_RERANK_KERNEL", "auto")
+    hr = gs.HostRerank(base, queries, threads=1)
+    import ctypes as C
+    avail = ["scalar"]
+    if all(f in open("/proc/cpuinfo").read() for f in (" avx2", " f16c")):
+        avail.append("avx2")
+        if " avx512f" in open("/proc/cpuinfo").read():
+            avail.append("avx512")
+    assert hr.fp16_kernel == avail[-1]
+    hr.close()
+    monkeypatch.setenv("GOFANN_FP16_RERANK_KERNEL", "bogus")
+    with pytest.raises(gs._lib.GofannError):
+        gs.HostRerank(base, queries, threads=1)
+    assert lib is not None and C is not None
