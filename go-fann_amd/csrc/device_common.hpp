@@ -374,6 +374,154 @@ __device__ __forceinline__ void smmh_pop_max(Entry* h, int& size)
 }
 
 // ---------------------------------------------------------------------------
+// The same two operations executed by the whole wave, for a heap of at most
+// 128 slots (64 pairs), leaving the array exactly as smmh_insert /
+// smmh_pop_max do (tie for tie); every lane passes the same arguments.
+//
+// Insert: after the bottom sibling step the new entry only ever moves up
+// one chain -- the left slots of its ancestor pairs when it is below the
+// parent pair's minimum, the right slots when it is above the maximum --
+// and the sifted values along a chain are sorted, so the levels it climbs
+// are a prefix of that chain: lane j reads ancestor j, a ballot counts the
+// prefix, the prefix moves down one level and the entry lands on top.
+//
+// Pop max: the serial sift walks from slot 2 to the larger right slot of
+// the two child pairs at every level; that path depends only on values
+// below the walk, so each lane q picks pair q's larger child, and the path
+// is a chase through those picks.  Lane k then holds path slot k and its
+// left sibling; the moving entry's fate (sibling swaps, where it stops) is a
+// short uniform loop over those values; the writes are parallel.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ Entry shfl_entry(const Entry& e, int src)
+{
+    Entry r;
+    r.first = __int_as_float(__shfl(__float_as_int(e.first), src, kWave));
+    r.second = static_cast<uint32_t>(__shfl(static_cast<int>(e.second), src, kWave));
+    r.base = __int_as_float(__shfl(__float_as_int(e.base), src, kWave));
+    r.sample = static_cast<uint32_t>(__shfl(static_cast<int>(e.sample), src, kWave));
+    return r;
+}
+
+__device__ __forceinline__ Entry readlane_entry(const Entry& e, int src)
+{
+    Entry r;
+    r.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e.first), src));
+    r.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e.second), src));
+    r.base = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e.base), src));
+    r.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e.sample), src));
+    return r;
+}
+
+constexpr int kWaveHeapSlots = 128;  // slots 0..127: 64 pairs
+
+__device__ __forceinline__ void wave_smmh_insert(Entry* h, int& size, const Entry& e, int lane)
+{
+    int y = size;
+    ++size;
+    if (!(y & 1) && e.first < h[y - 1].first) {
+        // bottom sibling step: the pair's left entry moves right
+        const Entry left = h[y - 1];
+        if (lane == 0) h[y] = left;
+        --y;
+    }
+    const int pair = (y - 1) >> 1;
+    const int depth = pair > 0 ? 31 - __clz(pair + 1) : 0;  // ancestor pairs
+    int side = -1;  // 0: climbs the left (minimum) slots, 1: the right slots
+    if (depth > 0) {
+        const int p1 = ((pair + 1) >> 1) - 1;
+        if (h[2 * p1 + 1].first > e.first)
+            side = 0;
+        else if (h[2 * p1 + 2].first < e.first)
+            side = 1;
+    }
+    if (side < 0) {
+        if (lane == 0) h[y] = e;
+        return;
+    }
+    const bool act = lane >= 1 && lane <= depth;
+    // lanes past the chain read slot 1 (always present) and stay out
+    const Entry v = h[act ? 2 * (((pair + 1) >> lane) - 1) + 1 + side : 1];
+    const bool climb = act && (side == 0 ? v.first > e.first : v.first < e.first);
+    const uint64_t mask = ballot(climb);
+    const int t = __builtin_ctzll(~(mask >> 1));  // levels climbed
+    if (act && lane <= t)
+        h[lane == 1 ? y : 2 * (((pair + 1) >> (lane - 1)) - 1) + 1 + side] = v;
+    if (lane == 0) h[t == 0 ? y : 2 * (((pair + 1) >> t) - 1) + 1 + side] = e;
+}
+
+__device__ __forceinline__ void wave_smmh_pop_max(Entry* h, int& size, int lane)
+{
+    --size;
+    const Entry v = h[size];  // the last entry replaces the maximum
+    // pair `lane`: the larger right slot of its two child pairs (ties: the
+    // first), or -1 without children
+    int choice = -1;
+    {
+        const int cl = 4 * lane + 4;
+        const int cr = 4 * lane + 6;
+        if (cl < size) {
+            choice = cl;
+            if (cr < size && h[cr].first > h[cl].first) choice = cr;
+        }
+    }
+    int slot = lane == 0 ? 2 : -1;  // lane k: path slot k
+    int cur = 2;
+    int depth = 0;
+    for (;;) {
+        const int c = __builtin_amdgcn_readlane(choice, (cur - 2) >> 1);
+        if (c < 0) break;
+        ++depth;
+        if (lane == depth) slot = c;
+        cur = c;
+    }
+    // lanes past the path read slot 2 and its sibling (always present)
+    const int at = lane <= depth ? slot : 2;
+    const Entry R = h[at];
+    const Entry L = h[at - 1];
+    // the moving entry: swapped with the left sibling where it is smaller,
+    // then moved down while the next path slot holds a larger value
+    float vf = v.first;
+    uint64_t swapped = 0;
+    int stop = depth;
+    for (int k = 0; k <= depth; ++k) {
+        const float lk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L.first), k));
+        if (vf < lk) {
+            swapped |= 1ull << k;
+            vf = lk;
+        }
+        if (k < depth &&
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(R.first), k + 1)) > vf)
+            continue;
+        stop = k;
+        break;
+    }
+    // entering level k: the last left entry swapped in above k, else v
+    const uint64_t above = swapped & ((1ull << lane) - 1ull);
+    const Entry lsrc = shfl_entry(L, above ? 63 - __builtin_clzll(above) : 0);
+    const Entry rnext = shfl_entry(R, lane + 1 < kWave ? lane + 1 : lane);
+    // where it stops: the left entry swapped in there or above, else v
+    const uint64_t upto = swapped & ((2ull << stop) - 1ull);
+    const Entry lfin = readlane_entry(L, upto ? 63 - __builtin_clzll(upto) : 0);
+    if (lane <= stop) {
+        const bool last = lane == stop;
+        Entry w;
+        w.first = last ? (upto ? lfin.first : v.first) : rnext.first;
+        w.second = last ? (upto ? lfin.second : v.second) : rnext.second;
+        w.base = last ? (upto ? lfin.base : v.base) : rnext.base;
+        w.sample = last ? (upto ? lfin.sample : v.sample) : rnext.sample;
+        h[slot] = w;
+        if ((swapped >> lane) & 1ull) {
+            Entry u;
+            u.first = above ? lsrc.first : v.first;
+            u.second = above ? lsrc.second : v.second;
+            u.base = above ? lsrc.base : v.base;
+            u.sample = above ? lsrc.sample : v.sample;
+            h[slot - 1] = u;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Bounded max-heaps of include/bin_heap.h:4-64 (push sifts the appended
 // element up; pop returns the root and sifts the former tail down without
 // storing the root at the tail).

@@ -673,6 +673,21 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
                 adm |= 1ull << j;
                 if (heap_size >= Q + 2) rh_pop_max(rh, heap_size, lane);
             }
+        } else if (Q + 2 <= kWaveHeapSlots) {
+            // the whole wave runs each heap operation (same array as the
+            // lane-0 sifts below)
+            for (uint64_t m = cand_mask; m; m &= m - 1) {
+                const int j = __builtin_ctzll(m);
+                Entry kp;
+                kp.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dist), j));
+                kp.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(adj), j));
+                kp.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), j));
+                kp.base = kp.first;
+                if (heap_size > 2 && heap_size >= Q + 1 && frontier[2].first < kp.first) continue;
+                wave_smmh_insert(frontier, heap_size, kp, lane);
+                adm |= 1ull << j;
+                if (heap_size >= Q + 2) wave_smmh_pop_max(frontier, heap_size, lane);
+            }
         } else {
             const int n_cand = __popcll(cand_mask);
             const uint32_t pos = lanes_below(cand_mask);

@@ -90,7 +90,7 @@ PLACE = {"auto": (_lib.PLACE_AUTO, False), "lds-nsamp": (_lib.PLACE_LDS, True),
 
 @pytest.mark.parametrize("place", list(PLACE))
 # Q + 2 <= 64 keeps the frontier in registers, larger beams in LDS.
-@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (1, 128)])
+@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (2, 80), (1, 128)])
 @pytest.mark.parametrize("with_pred", [False, True])
 def test_exact_search_matches_oracle(gpu_ctx, eworld, place, mode, Q, with_pred):
     wl, li, rs = eworld
@@ -120,7 +120,7 @@ def c2_shape_world(gpu_ctx):
 
 
 @pytest.mark.parametrize("place", list(PLACE))
-@pytest.mark.parametrize("mode,Q", [(2, 32), (2, 62), (2, 96), (0, 128)])
+@pytest.mark.parametrize("mode,Q", [(2, 32), (2, 62), (2, 96), (2, 126), (0, 128)])
 def test_exact_search_degree64_c2_shape(gpu_ctx, c2_shape_world, place, mode, Q):
     """Degree 64: lanes 32..63 of load_node/keep, the 64-bit ballot
     compaction and admissions of more than 32 neighbours per step."""
