@@ -375,7 +375,7 @@ __device__ __forceinline__ void smmh_pop_max(Entry* h, int& size)
 
 // ---------------------------------------------------------------------------
 // The same two operations executed by the whole wave, for a heap of at most
-// 128 slots (64 pairs), leaving the array exactly as smmh_insert /
+// 512 slots (256 pairs), leaving the array exactly as smmh_insert /
 // smmh_pop_max do (tie for tie); every lane passes the same arguments.
 //
 // Insert: after the bottom sibling step the new entry only ever moves up
@@ -388,7 +388,8 @@ __device__ __forceinline__ void smmh_pop_max(Entry* h, int& size)
 // Pop max: the serial sift walks from slot 2 to the larger right slot of
 // the two child pairs at every level; that path depends only on values
 // below the walk, so each lane q picks pair q's larger child, and the path
-// is a chase through those picks.  Lane k then holds path slot k and its
+// is a chase through those picks (a pair past 63, on the last levels of a
+// large heap, is picked when the chase reaches it).  Lane k then holds path slot k and its
 // left sibling; the moving entry's fate (sibling swaps, where it stops) is a
 // short uniform loop over those values; the writes are parallel.
 // ---------------------------------------------------------------------------
@@ -412,7 +413,7 @@ __device__ __forceinline__ Entry readlane_entry(const Entry& e, int src)
     return r;
 }
 
-constexpr int kWaveHeapSlots = 128;  // slots 0..127: 64 pairs
+constexpr int kWaveHeapSlots = 512;  // slots 0..511: 256 pairs
 
 __device__ __forceinline__ void wave_smmh_insert(Entry* h, int& size, const Entry& e, int lane)
 {
@@ -468,7 +469,22 @@ __device__ __forceinline__ void wave_smmh_pop_max(Entry* h, int& size, int lane)
     int cur = 2;
     int depth = 0;
     for (;;) {
-        const int c = __builtin_amdgcn_readlane(choice, (cur - 2) >> 1);
+        const int pr = (cur - 2) >> 1;  // pair of slot `cur` (uniform)
+        int c;
+        if (pr < kWave) {
+            c = __builtin_amdgcn_readlane(choice, pr);
+        } else {
+            // past pair 63 (the last level or two of a heap over 260 slots)
+            // the pick is read directly, the same address on every lane
+            const int cl = 4 * pr + 4;
+            const int cr = 4 * pr + 6;
+            c = -1;
+            if (cl < size) {
+                c = cl;
+                if (cr < size && h[cr].first > h[cl].first) c = cr;
+            }
+            c = __builtin_amdgcn_readfirstlane(c);
+        }
         if (c < 0) break;
         ++depth;
         if (lane == depth) slot = c;

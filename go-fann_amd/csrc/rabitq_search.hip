@@ -2,6 +2,14 @@
 #include "traversal.hpp"
 
 namespace gofann {
+// rabitq_pair.hip: the two-routes-per-wave traversal for degree <= 32.
+bool rabitq_pair_eligible(const gofann_rabitq_view* rq, const gofann_graph_view* g,
+                          const gofann_search_params* p);
+int rabitq_pair_search(Context* ctx, const RabitqScorer& sc, const gofann_graph_view* g,
+                       const gofann_predicate_view* pred, const gofann_routes* r,
+                       const gofann_search_params* p, uint32_t* out_ids, float* out_dists,
+                       gofann_route_stats* stats);
+
 __global__ __launch_bounds__(64) void rabitq_score_kernel(RabitqScorer sc, const uint32_t* q_idx,
                                                          const uint32_t* s_idx, uint32_t n,
                                                          float* out, int32_t* ip_out)
@@ -83,6 +91,10 @@ int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabit
         return launch_traversal<RabitqScorer, true>(ctx, make_rabitq_scorer(rq, pre), l, pl, g,
                                                     pred, r, p, out_ids, out_dists, stats, 1);
     }
+    // Degree <= 32: two routes per wave (rabitq_pair.hip), same results.
+    if (rabitq_pair_eligible(rq, g, p))
+        return rabitq_pair_search(ctx, make_rabitq_scorer(rq, pre), g, pred, r, p, out_ids,
+                                  out_dists, stats);
     const Placement pl = choose_visited<RabitqScorer, false>(ctx, l, p->hash_mode);
     return launch_traversal<RabitqScorer, false>(ctx, make_rabitq_scorer(rq, pre), l, pl, g, pred,
                                                  r, p, out_ids, out_dists, stats, 1);

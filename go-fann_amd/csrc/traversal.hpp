@@ -998,6 +998,23 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
                 if (heap_size >= Q + 2) rf_pop_max(rf, heap_size, lane);
             }
             mine = (adm_lanes >> lane) & 1ull;
+        } else if (Q + 2 <= kWaveHeapSlots) {
+            // the whole wave runs each insert / pop_max on the LDS frontier
+            adm_lanes = 0;
+            for (uint64_t m = cand_mask; m; m &= m - 1) {
+                const int j = __builtin_ctzll(m);
+                Entry kp;
+                kp.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(first), j));
+                kp.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(idx), j));
+                kp.base = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(base), j));
+                kp.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_sample), j));
+                if (heap_size >= Q + 1 && frontier[2].first < kp.first) continue;
+                wave_smmh_insert(frontier, heap_size, kp, lane);
+                adm_lanes |= 1ull << j;
+                ++admitted;
+                if (heap_size >= Q + 2) wave_smmh_pop_max(frontier, heap_size, lane);
+            }
+            mine = (adm_lanes >> lane) & 1ull;
         } else {
             const int n_cand = __popcll(cand_mask);
             const uint32_t pos = lanes_below(cand_mask);

@@ -90,7 +90,7 @@ PLACE = {"auto": (_lib.PLACE_AUTO, False), "lds-nsamp": (_lib.PLACE_LDS, True),
 
 @pytest.mark.parametrize("place", list(PLACE))
 # Q + 2 <= 64 keeps the frontier in registers, larger beams in LDS.
-@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (2, 80), (1, 128)])
+@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (2, 80), (1, 128), (2, 300)])
 @pytest.mark.parametrize("with_pred", [False, True])
 def test_exact_search_matches_oracle(gpu_ctx, eworld, place, mode, Q, with_pred):
     wl, li, rs = eworld
@@ -120,7 +120,7 @@ def c2_shape_world(gpu_ctx):
 
 
 @pytest.mark.parametrize("place", list(PLACE))
-@pytest.mark.parametrize("mode,Q", [(2, 32), (2, 62), (2, 96), (2, 126), (0, 128)])
+@pytest.mark.parametrize("mode,Q", [(2, 32), (2, 62), (2, 96), (2, 126), (0, 128), (2, 300)])
 def test_exact_search_degree64_c2_shape(gpu_ctx, c2_shape_world, place, mode, Q):
     """Degree 64: lanes 32..63 of load_node/keep, the 64-bit ballot
     compaction and admissions of more than 32 neighbours per step."""
@@ -132,6 +132,8 @@ def test_exact_search_degree64_c2_shape(gpu_ctx, c2_shape_world, place, mode, Q)
                    Q, 10, mode, hash_mode, nsamp, finish=2)
     assert (li.graph[:, 32:] != U32MAX).any(1).mean() > 0.5
     assert ost[:, 6].max() > 32  # some step admitted more than 32 neighbours overall
+    if Q > 260:  # some frontier grew past 260 slots: pairs 64.. have children
+        assert ost[:, 6].max() > 300
     assert (oi[:, 0] != U32MAX).sum() > rs.count // 2
 
 

@@ -249,12 +249,14 @@ def long_world():
 
 
 @pytest.mark.parametrize("place", list(PLACEMENTS))
-def test_pq_search_visited_fill_matches_oracle(gpu_ctx, long_world, place):
+# all-tie frontiers of 258 and 402 slots (past 260, pairs 64.. have children)
+@pytest.mark.parametrize("Q", [256, 400])
+def test_pq_search_visited_fill_matches_oracle(gpu_ctx, long_world, place, Q):
     wl, li, pl, table, codes = long_world
     table_mode, hash_mode, nsamp, rec = PLACEMENTS[place]
-    say("pq_search visited fill", place)
+    say("pq_search visited fill", place, "Q", Q)
     rs = pl.graph
-    Q, W, steps = 256, 40, 450
+    W, steps = 40, 450
     pred_o = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.0, pending_base_stop=False)
     prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=1, max_steps=steps,
                       bias=False)

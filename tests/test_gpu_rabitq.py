@@ -361,3 +361,54 @@ def test_streamed_host_rerank_matches_direct(gpu_ctx, rworld):
     assert sr.timing["gpu_ms"] > 0 and sr.timing["wall_ms"] >= sr.timing["gpu_ms"] * 0.5
     assert (want_i[:, 0] != U32MAX).sum() > n // 2
     hr.close()
+
+
+@pytest.mark.parametrize("Q,W", [(80, 30), (200, 100), (448, 100)])
+@pytest.mark.parametrize("hash_mode", [_lib.PLACE_LDS, _lib.PLACE_GLOBAL])
+@pytest.mark.parametrize("bias", [True, False])
+def test_rabitq_pair_kernel_matches_oracle(gpu_ctx, rworld, Q, W, hash_mode, bias, monkeypatch):
+    """Two routes per wave (degree 32, LDS frontier, rabitq_pair.hip, asked
+    for by GOFANN_RABITQ_PAIR=1) on an odd number of routes, so the last wave
+    runs one, and the one-route kernel with its wave-parallel frontier (Q + 2
+    up to 512 slots, so pop_max follows pairs past 64): ids, distance bits
+    and counters identical to the oracle in both."""
+    wl, li, pl, rot, codes, fac, aid, anchors, P = _at_dim(rworld, 512)
+    say("rabitq pair kernel Q", Q, "W", W, "hash", hash_mode, "bias", bias)
+    dev, rv = _rviews((wl, li, pl, rot, codes, fac, aid, anchors, P))
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rs = pl.graph
+    n = rs.count if rs.count % 2 else rs.count - 1
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15 if bias else 0.0,
+                                          pending_base_stop=bias)
+    prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias,
+                      rabitq_verdict=1)
+    oi, od, ost = po.rabitq_search(li, rs, pred_o, prm_o, codes.numpy(), fac.numpy(),
+                                   aid.numpy().astype(np.uint32), out["q8"].cpu().numpy(),
+                                   out["scale"].cpu().numpy(), out["k1"].cpu().numpy(),
+                                   out["cd"].cpu().numpy(), anchors.shape[0], P)
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=True)
+    dr = gs.DeviceRoutes.upload(rs)
+    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias,
+                           hash_mode=hash_mode)
+
+    def run():
+        ids = torch.full((rs.count * W,), -7, dtype=torch.int32, device="cuda")
+        dists = torch.empty(rs.count * W, device="cuda")
+        st = torch.zeros(rs.count * 8, dtype=torch.int32, device="cuda")
+        gpu_ctx.check(gpu_ctx.lib.gofann_rabitq_search(
+            gpu_ctx.handle, rv, rq, dg.view(), dr.predicate_view(dg, 0.15 if bias else 0.0, bias),
+            dr.routes_view(0, n), prm, _lib.ptr(ids), _lib.ptr(dists), _lib.ptr(st)))
+        torch.cuda.synchronize()
+        return (as_u32(ids).reshape(rs.count, W), dists.cpu().numpy().reshape(rs.count, W),
+                st.cpu().numpy().reshape(rs.count, 8))
+
+    for pair in ("1", "0"):
+        monkeypatch.setenv("GOFANN_RABITQ_PAIR", pair)
+        gi_, gd, gst = run()
+        assert np.array_equal(gi_[:n], oi[:n]), pair
+        assert np.array_equal(gd[:n].view(np.uint32), od[:n].view(np.uint32)), pair
+        assert np.array_equal(gst[:n], ost[:n]), pair
+        assert np.all(gi_[n:] == np.uint32(0xFFFFFFF9))  # routes outside the launch untouched
+    assert (oi[:n, 0] != U32MAX).sum() > n // 2
+    if Q > 300:  # some frontier grew past 260 slots: pairs 64.. have children
+        assert ost[:n, 6].max() > 300
