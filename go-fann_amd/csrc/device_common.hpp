@@ -382,16 +382,19 @@ __device__ __forceinline__ void smmh_pop_max(Entry* h, int& size)
 // one chain -- the left slots of its ancestor pairs when it is below the
 // parent pair's minimum, the right slots when it is above the maximum --
 // and the sifted values along a chain are sorted, so the levels it climbs
-// are a prefix of that chain: lane j reads ancestor j, a ballot counts the
-// prefix, the prefix moves down one level and the entry lands on top.
+// are a prefix of that chain.  Lane j reads both slots of ancestor j (and
+// every lane the new slot's sibling) in one round trip, a ballot counts
+// the prefix, the prefix moves down one level and the entry lands on top.
 //
 // Pop max: the serial sift walks from slot 2 to the larger right slot of
-// the two child pairs at every level; that path depends only on values
-// below the walk, so each lane q picks pair q's larger child, and the path
-// is a chase through those picks (a pair past 63, on the last levels of a
-// large heap, is picked when the chase reaches it).  Lane k then holds path slot k and its
-// left sibling; the moving entry's fate (sibling swaps, where it stops) is a
-// short uniform loop over those values; the writes are parallel.
+// the two child pairs at every level; that walk depends only on values
+// below it, so lane q compares pair q's two children (and pair q + 64's in
+// a heap over 260 slots), a ballot packs the picks, and the walk is a
+// scalar loop over those bits.  Lane k then holds path slot k and its left
+// sibling.  The moving value after level k is the maximum of itself and
+// the left siblings of levels 0..k (a swap takes a strictly larger left
+// entry), a prefix maximum over the path lanes; it stops at the first level
+// whose next path slot is not larger.  The writes are parallel.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ Entry shfl_entry(const Entry& e, int src)
 {
@@ -413,35 +416,67 @@ __device__ __forceinline__ Entry readlane_entry(const Entry& e, int src)
     return r;
 }
 
-constexpr int kWaveHeapSlots = 512;  // slots 0..511: 256 pairs
+// DPP moves within rows of 16 lanes; a lane whose source is outside its row
+// keeps `old`.  Row shift right by n: lane i reads lane i - n; row shift
+// left by 1: lane i reads lane i + 1.
+template <int kCtrl>
+__device__ __forceinline__ int dpp_row(int old, int x)
+{
+    return __builtin_amdgcn_update_dpp(old, x, kCtrl, 0xF, 0xF, false);
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_row_f(float old, float x)
+{
+    return __int_as_float(dpp_row<kCtrl>(__float_as_int(old), __float_as_int(x)));
+}
+constexpr int kDppRowShl1 = 0x101;
+constexpr int kDppRowShr1 = 0x111;
+constexpr int kDppRowShr2 = 0x112;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowShr8 = 0x118;
+
+constexpr int kWaveHeapSlots = 512;  // slots 0..511: 256 pairs, paths of <= 8 levels
+
+__device__ __forceinline__ Entry select_entry(bool c, const Entry& a, const Entry& b)
+{
+    Entry r;
+    r.first = c ? a.first : b.first;
+    r.second = c ? a.second : b.second;
+    r.base = c ? a.base : b.base;
+    r.sample = c ? a.sample : b.sample;
+    return r;
+}
 
 __device__ __forceinline__ void wave_smmh_insert(Entry* h, int& size, const Entry& e, int lane)
 {
-    int y = size;
-    ++size;
-    if (!(y & 1) && e.first < h[y - 1].first) {
+    int y = __builtin_amdgcn_readfirstlane(size);
+    size = y + 1;
+    // the pair of slot y (and of y - 1 when y is even); its ancestor pairs
+    const int pair = (y - 1) >> 1;
+    const int depth = pair > 0 ? 31 - __clz(pair + 1) : 0;
+    const bool act = lane >= 1 && lane <= depth;
+    // lanes past the chain read slots 1 and 2 (inside the frontier) and stay out
+    const int a1 = act ? 2 * (((pair + 1) >> lane) - 1) + 1 : 1;
+    const Entry al = h[a1];
+    const Entry ar = h[a1 + 1];
+    const Entry sib = h[y - 1];
+    if (!(y & 1) && e.first < sib.first) {
         // bottom sibling step: the pair's left entry moves right
-        const Entry left = h[y - 1];
-        if (lane == 0) h[y] = left;
+        if (lane == 0) h[y] = sib;
         --y;
     }
-    const int pair = (y - 1) >> 1;
-    const int depth = pair > 0 ? 31 - __clz(pair + 1) : 0;  // ancestor pairs
     int side = -1;  // 0: climbs the left (minimum) slots, 1: the right slots
     if (depth > 0) {
-        const int p1 = ((pair + 1) >> 1) - 1;
-        if (h[2 * p1 + 1].first > e.first)
+        if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(al.first), 1)) > e.first)
             side = 0;
-        else if (h[2 * p1 + 2].first < e.first)
+        else if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ar.first), 1)) < e.first)
             side = 1;
     }
     if (side < 0) {
         if (lane == 0) h[y] = e;
         return;
     }
-    const bool act = lane >= 1 && lane <= depth;
-    // lanes past the chain read slot 1 (always present) and stay out
-    const Entry v = h[act ? 2 * (((pair + 1) >> lane) - 1) + 1 + side : 1];
+    const Entry v = select_entry(side != 0, ar, al);
     const bool climb = act && (side == 0 ? v.first > e.first : v.first < e.first);
     const uint64_t mask = ballot(climb);
     const int t = __builtin_ctzll(~(mask >> 1));  // levels climbed
@@ -450,91 +485,65 @@ __device__ __forceinline__ void wave_smmh_insert(Entry* h, int& size, const Entr
     if (lane == 0) h[t == 0 ? y : 2 * (((pair + 1) >> t) - 1) + 1 + side] = e;
 }
 
-__device__ __forceinline__ void wave_smmh_pop_max(Entry* h, int& size, int lane)
+// Returns the new maximum (slot 2's `first`); the heap keeps >= 3 slots.
+__device__ __forceinline__ float wave_smmh_pop_max(Entry* h, int& size, int lane)
 {
-    --size;
-    const Entry v = h[size];  // the last entry replaces the maximum
-    // pair `lane`: the larger right slot of its two child pairs (ties: the
-    // first), or -1 without children
-    int choice = -1;
+    const int n = __builtin_amdgcn_readfirstlane(size) - 1;
+    size = n;
+    const Entry v = h[n];  // the last entry replaces the maximum
+    // bit q: pair q's larger child is its right one (ties: the left)
+    uint64_t pick0, pick1 = 0;
     {
         const int cl = 4 * lane + 4;
-        const int cr = 4 * lane + 6;
-        if (cl < size) {
-            choice = cl;
-            if (cr < size && h[cr].first > h[cl].first) choice = cr;
+        const int cr = cl + 2;
+        const float fl = h[min(cl, n - 1)].first;
+        const float fr = h[min(cr, n - 1)].first;
+        pick0 = ballot(cr < n && fr > fl);
+        if (n > 260) {
+            const float gl = h[min(cl + 256, n - 1)].first;
+            const float gr = h[min(cr + 256, n - 1)].first;
+            pick1 = ballot(cr + 256 < n && gr > gl);
         }
     }
-    int slot = lane == 0 ? 2 : -1;  // lane k: path slot k
-    int cur = 2;
+    int p = 0;  // scalar walk to the last pair of the path
     int depth = 0;
-    for (;;) {
-        const int pr = (cur - 2) >> 1;  // pair of slot `cur` (uniform)
-        int c;
-        if (pr < kWave) {
-            c = __builtin_amdgcn_readlane(choice, pr);
-        } else {
-            // past pair 63 (the last level or two of a heap over 260 slots)
-            // the pick is read directly, the same address on every lane
-            const int cl = 4 * pr + 4;
-            const int cr = 4 * pr + 6;
-            c = -1;
-            if (cl < size) {
-                c = cl;
-                if (cr < size && h[cr].first > h[cl].first) c = cr;
-            }
-            c = __builtin_amdgcn_readfirstlane(c);
-        }
-        if (c < 0) break;
+    while (4 * p + 4 < n) {
+        const uint64_t bits = p < kWave ? pick0 : pick1;
+        p = 2 * p + 1 + static_cast<int>((bits >> (p & (kWave - 1))) & 1ull);
         ++depth;
-        if (lane == depth) slot = c;
-        cur = c;
     }
-    // lanes past the path read slot 2 and its sibling (always present)
-    const int at = lane <= depth ? slot : 2;
-    const Entry R = h[at];
-    const Entry L = h[at - 1];
-    // the moving entry: swapped with the left sibling where it is smaller,
-    // then moved down while the next path slot holds a larger value
-    float vf = v.first;
-    uint64_t swapped = 0;
-    int stop = depth;
-    for (int k = 0; k <= depth; ++k) {
-        const float lk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(L.first), k));
-        if (vf < lk) {
-            swapped |= 1ull << k;
-            vf = lk;
-        }
-        if (k < depth &&
-            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(R.first), k + 1)) > vf)
-            continue;
-        stop = k;
-        break;
-    }
+    // lane k <= depth: path slot k; lanes past the path read slot 2
+    const int k = lane <= depth ? lane : 0;
+    const int slot = 2 * (((p + 1) >> (depth - k)) - 1) + 2;
+    const Entry R = h[slot];
+    const Entry L = h[slot - 1];
+    float x = L.first;
+    const float ninf = -__builtin_inff();
+    x = fmaxf(x, dpp_row_f<kDppRowShr1>(ninf, x));
+    x = fmaxf(x, dpp_row_f<kDppRowShr2>(ninf, x));
+    x = fmaxf(x, dpp_row_f<kDppRowShr4>(ninf, x));
+    x = fmaxf(x, dpp_row_f<kDppRowShr8>(ninf, x));
+    const float vf = fmaxf(v.first, x);                        // after level `lane`
+    const float prev = dpp_row_f<kDppRowShr1>(v.first, vf);    // entering level `lane`
+    const uint64_t swapped = ballot(lane <= depth && L.first > prev);
+    Entry rnext;  // path slot lane + 1
+    rnext.first = dpp_row_f<kDppRowShl1>(R.first, R.first);
+    rnext.second = static_cast<uint32_t>(dpp_row<kDppRowShl1>(static_cast<int>(R.second), static_cast<int>(R.second)));
+    rnext.base = dpp_row_f<kDppRowShl1>(R.base, R.base);
+    rnext.sample = static_cast<uint32_t>(dpp_row<kDppRowShl1>(static_cast<int>(R.sample), static_cast<int>(R.sample)));
+    const int stop = __builtin_ctzll(~ballot(lane < depth && rnext.first > vf));
     // entering level k: the last left entry swapped in above k, else v
     const uint64_t above = swapped & ((1ull << lane) - 1ull);
     const Entry lsrc = shfl_entry(L, above ? 63 - __builtin_clzll(above) : 0);
-    const Entry rnext = shfl_entry(R, lane + 1 < kWave ? lane + 1 : lane);
     // where it stops: the left entry swapped in there or above, else v
     const uint64_t upto = swapped & ((2ull << stop) - 1ull);
     const Entry lfin = readlane_entry(L, upto ? 63 - __builtin_clzll(upto) : 0);
+    const Entry fin = select_entry(upto != 0, lfin, v);
     if (lane <= stop) {
-        const bool last = lane == stop;
-        Entry w;
-        w.first = last ? (upto ? lfin.first : v.first) : rnext.first;
-        w.second = last ? (upto ? lfin.second : v.second) : rnext.second;
-        w.base = last ? (upto ? lfin.base : v.base) : rnext.base;
-        w.sample = last ? (upto ? lfin.sample : v.sample) : rnext.sample;
-        h[slot] = w;
-        if ((swapped >> lane) & 1ull) {
-            Entry u;
-            u.first = above ? lsrc.first : v.first;
-            u.second = above ? lsrc.second : v.second;
-            u.base = above ? lsrc.base : v.base;
-            u.sample = above ? lsrc.sample : v.sample;
-            h[slot - 1] = u;
-        }
+        h[slot] = select_entry(lane == stop, fin, rnext);
+        if ((swapped >> lane) & 1ull) h[slot - 1] = select_entry(above != 0, lsrc, v);
     }
+    return stop == 0 ? fin.first : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(R.first), 1));
 }
 
 // ---------------------------------------------------------------------------

@@ -675,7 +675,10 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
             }
         } else if (Q + 2 <= kWaveHeapSlots) {
             // the whole wave runs each heap operation (same array as the
-            // lane-0 sifts below)
+            // lane-0 sifts below); hmax: the largest `first` in the heap
+            float hmax = heap_size >= 3   ? frontier[2].first
+                         : heap_size == 2 ? frontier[1].first
+                                          : -__builtin_inff();
             for (uint64_t m = cand_mask; m; m &= m - 1) {
                 const int j = __builtin_ctzll(m);
                 Entry kp;
@@ -683,10 +686,11 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
                 kp.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(adj), j));
                 kp.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), j));
                 kp.base = kp.first;
-                if (heap_size > 2 && heap_size >= Q + 1 && frontier[2].first < kp.first) continue;
+                if (heap_size > 2 && heap_size >= Q + 1 && hmax < kp.first) continue;
                 wave_smmh_insert(frontier, heap_size, kp, lane);
+                hmax = fmaxf(hmax, kp.first);
                 adm |= 1ull << j;
-                if (heap_size >= Q + 2) wave_smmh_pop_max(frontier, heap_size, lane);
+                if (heap_size >= Q + 2) hmax = wave_smmh_pop_max(frontier, heap_size, lane);
             }
         } else {
             const int n_cand = __popcll(cand_mask);

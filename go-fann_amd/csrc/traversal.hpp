@@ -999,8 +999,12 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
             }
             mine = (adm_lanes >> lane) & 1ull;
         } else if (Q + 2 <= kWaveHeapSlots) {
-            // the whole wave runs each insert / pop_max on the LDS frontier
+            // the whole wave runs each insert / pop_max on the LDS frontier;
+            // hmax: the largest `first` in it (frontier[2] once full)
             adm_lanes = 0;
+            float hmax = heap_size >= 3   ? frontier[2].first
+                         : heap_size == 2 ? frontier[1].first
+                                          : -__builtin_inff();
             for (uint64_t m = cand_mask; m; m &= m - 1) {
                 const int j = __builtin_ctzll(m);
                 Entry kp;
@@ -1008,11 +1012,12 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
                 kp.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(idx), j));
                 kp.base = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(base), j));
                 kp.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_sample), j));
-                if (heap_size >= Q + 1 && frontier[2].first < kp.first) continue;
+                if (heap_size >= Q + 1 && hmax < kp.first) continue;
                 wave_smmh_insert(frontier, heap_size, kp, lane);
+                hmax = fmaxf(hmax, kp.first);
                 adm_lanes |= 1ull << j;
                 ++admitted;
-                if (heap_size >= Q + 2) wave_smmh_pop_max(frontier, heap_size, lane);
+                if (heap_size >= Q + 2) hmax = wave_smmh_pop_max(frontier, heap_size, lane);
             }
             mine = (adm_lanes >> lane) & 1ull;
         } else {
