@@ -725,17 +725,21 @@ def main_c1(args):
 # ---------------------------------------------------------------------------
 # C3: 2.7M x 4096 fp32, one-bit RaBitQ, range predicates (--config c3).
 # ---------------------------------------------------------------------------
-def rabitq_traversal_bytes(st: np.ndarray, degree: int, code_bytes: int) -> float:
-    """Bytes the RaBitQ traversal must move: the adjacency row and
-    row_to_sample word of each expanded node; per scored candidate its code
-    row, anchor id and f_add/f_rescale (C = P/8 + 4 + 8) and row_to_sample
-    word, plus its base range value (the route predicate is a range atom);
-    and the CSR words of label checks."""
+def rabitq_traversal_bytes(st: np.ndarray, degree: int, code_bytes: int,
+                           neighbor_samples: bool = False) -> float:
+    """Bytes the RaBitQ traversal must move: the adjacency row (and with a
+    neighbour-sample table, its sample row) and row_to_sample word of each
+    expanded node; per scored candidate its code row, anchor id and
+    f_add/f_rescale (C = P/8 + 4 + 8), its row_to_sample word when there is
+    no sample table, plus its base range value (the route predicate is a
+    range atom); and the CSR words of label checks."""
     E = st[:, 1].astype(np.float64).sum()
     V = st[:, 3].astype(np.float64).sum()
     rows = st[:, 4].astype(np.float64).sum()
     labels = st[:, 5].astype(np.float64).sum()
-    return E * (4 * degree + 4) + V * (code_bytes + 4 + 8 + 4 + 4) + rows * 8 + labels * 4
+    adj = 8 * degree if neighbor_samples else 4 * degree
+    code = code_bytes + 4 + 8 + 4 + (0 if neighbor_samples else 4)
+    return E * (adj + 4) + V * code + rows * 8 + labels * 4
 
 
 def build_world_c3(args, torch):
@@ -790,7 +794,7 @@ class RabitqRangePipeline:
     rerank of the 200, and the per-query merge."""
 
     def __init__(self, ctx, wl, li, rq, rpi, torch, scan_rows, width=200, segment_rows=4096,
-                 resident_copies=True):
+                 resident_copies=True, neighbor_samples=True):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
         from gofann_amd import range_posting as rp
@@ -823,7 +827,8 @@ class RabitqRangePipeline:
         self.classes = [(int(bounds[i]), int(bounds[i + 1])) for i in range(len(levels))]
         self.route_class = lambda row: cls_of[float(sel[row[0]])]
         self.entry = None  # gs.CoarseEntry: per-route entry rows picked in step()
-        self.dg = gs.DeviceGraph.upload(li)
+        self.nsamp = neighbor_samples
+        self.dg = gs.DeviceGraph.upload(li, neighbor_samples=neighbor_samples)
         self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
         # posting routes: the smallest slice, in segments
         self.post_query = gs.u32(pq if len(pq) else np.zeros(1, np.uint32))
@@ -1067,7 +1072,8 @@ def run_c3(args, torch, ctx) -> dict:
     gt = ground_truth_c3(wl, torch, args.gt_queries_c3)
     log(f"C3 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     pipe = RabitqRangePipeline(ctx, wl, li, rq, rpi, torch, args.c3_scan_rows,
-                               resident_copies=not args.c3_gather)
+                               resident_copies=not args.c3_gather,
+                               neighbor_samples=not args.no_neighbor_samples)
     pipe.P, pipe.li = rq["P"], li
     log(f"C3 routes: {pipe.ng} graph (wide ranges), {pipe.np_} range-posting scans "
         f"({pipe.scan_rows_total} rows)")
@@ -1217,7 +1223,7 @@ class RabitqLabelPipeline:
     shortlists, and the per-query merge."""
 
     def __init__(self, ctx, wl, li, rq, torch, width=100, posting_layout="columns",
-                 segment_rows=32768):
+                 segment_rows=32768, neighbor_samples=True):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
         from gofann_amd import range_posting as rp
@@ -1274,7 +1280,8 @@ class RabitqLabelPipeline:
             self.classes = [(int(b[i]), int(b[i + 1])) for i in range(len(kinds))]
             self.route_class = lambda row: cls_of[types[row[0]]]
         self.entry = None  # gs.CoarseEntry: per-route entry rows picked in step()
-        self.dg = gs.DeviceGraph.upload(li)
+        self.nsamp = neighbor_samples
+        self.dg = gs.DeviceGraph.upload(li, neighbor_samples=neighbor_samples)
         self.dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
         self.dp = gs.DeviceRoutes.upload(ps, wl.base_ranges)
         off = np.array([li.posting_offset[r[1]] for r in post_rows], dtype=np.uint32)
@@ -1563,7 +1570,7 @@ def cpu_rerank_leg(args, pipe, beams, class_gt, label, host_base, host_queries, 
 
 def c4_kernels(pipe, st_ms, st):
     P, wl, li = pipe.P, pipe.wl, pipe.li
-    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
+    tb = rabitq_traversal_bytes(st, li.degree, P // 8, pipe.nsamp)
     # posting scan: rows * (sample id + code, anchor id, two factors) plus
     # the predicate's inputs per row (16-byte label slab + range row); a
     # filter-first scan needs the code terms of passing rows only
@@ -1585,7 +1592,7 @@ def c4_kernels(pipe, st_ms, st):
 
 def c3_kernels(pipe, st_ms, st):
     P, wl, li = pipe.P, pipe.wl, pipe.li
-    tb = rabitq_traversal_bytes(st, li.degree, P // 8)
+    tb = rabitq_traversal_bytes(st, li.degree, P // 8, pipe.nsamp)
     sb = pipe.scan_rows_total * (4 + P // 8 + 4 + 8) + 0.0  # posting id + C per row
     rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 4 + 4) + 0.0
     return {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
@@ -1611,7 +1618,8 @@ def run_c4(args, torch, ctx, world=None) -> dict:
     log(f"C4 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
-                               segment_rows=args.posting_segment_rows)
+                               segment_rows=args.posting_segment_rows,
+                               neighbor_samples=not args.no_neighbor_samples)
     pipe.P, pipe.li = rq["P"], li
     log(f"C4 routes: {pipe.ng} graph ({pipe.n_eq} equality, {pipe.interior} interior "
         f"intervals), {pipe.np_} label-posting scans ({pipe.post_rows_total} rows), planned "
@@ -1739,7 +1747,8 @@ def run_c5(args, torch, ctx, world=None) -> dict:
     log(f"C5 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
-                               segment_rows=args.posting_segment_rows)
+                               segment_rows=args.posting_segment_rows,
+                               neighbor_samples=not args.no_neighbor_samples)
     pipe.P, pipe.li = rq["P"], li
     types = wl.meta["query_types"]
     log(f"C5 routes: {pipe.ng} graph, {pipe.np_} label-posting scans ({pipe.post_rows_total} "

@@ -987,18 +987,24 @@ __device__ __forceinline__ int wave_sum(int v)
 // Frontier pickup (wave-cooperative).
 // pickup_next_unused_from_native_frontier (backend_pq.cu:844-892): unused
 // entry of least `first`, lowest index on ties; lane 0 marks it used.
-__device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane)
+// With `min_base`, the same pass also returns the least `base` over the
+// entries that were unused before the pickup (the picked one included).
+__device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane,
+                                       float* min_base = nullptr)
 {
     int best = -1;
     float bv = 0.0f;
+    float mb = FLT_MAX;
     for (int i = lane + 1; i < size; i += kWave) {
         const Entry e = f[i];
         if (e.second & kPoolUsed) continue;
+        if (min_base) mb = fminf(mb, e.base);
         if (best < 0 || e.first < bv) {
             best = i;
             bv = e.first;
         }
     }
+    if (min_base) *min_base = wave_min(mb);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const int ob = __shfl_xor(best, off, kWave);

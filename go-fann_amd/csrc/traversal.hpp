@@ -463,26 +463,6 @@ struct RabitqScorer {
 };
 
 // ---------------------------------------------------------------------------
-// Frontier helpers (wave-cooperative).
-// ---------------------------------------------------------------------------
-
-// minimum_pending_base (gpu_predicate_index.cuh:147-160) over the reserved
-// current/next entries and every unused frontier entry.
-__device__ __forceinline__ float min_pending_base(const Entry* f, int size, const Entry& now, const Entry& next,
-                                  int lane)
-{
-    float m = FLT_MAX;
-    for (int i = lane + 1; i < size; i += kWave) {
-        const Entry e = f[i];
-        if (!(e.second & kPoolUsed)) m = fminf(m, e.base);
-    }
-    m = wave_min(m);
-    m = fminf(m, now.base);
-    m = fminf(m, next.base);
-    return m;
-}
-
-// ---------------------------------------------------------------------------
 // Frontier in registers for beams with Q + 2 <= 64: lane i holds smmh2 entry
 // i (the array layout of the LDS heap), read with v_readlane and written with
 // a lane select, so the serial admission runs at register speed instead of
@@ -803,10 +783,16 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
 
         if (step != 1) {
             bool found;
+            // the pending-base stop needs minimum_pending_base
+            // (gpu_predicate_index.cuh:147-160): the least base over the
+            // current/next entries and every unused frontier entry; the LDS
+            // pickup finds it in the same pass
+            const bool want_base = stop_size == SW && a.pred.pending_base_stop && enabled;
+            float unused_base = FLT_MAX;
             if constexpr (kReg)
                 found = rf_pickup(rf, heap_size, next, lane);
             else
-                found = pickup(frontier, heap_size, next, lane);
+                found = pickup(frontier, heap_size, next, lane, want_base ? &unused_base : nullptr);
             if (!found) {
                 exhausted = 1;
                 next = sentinel;
@@ -814,11 +800,11 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
                 load_node(a, sc, label_offset, degree, next, enabled, exact, lane, nxt);
                 if (stop_size == SW) {
                     float pending = next.first;
-                    if (a.pred.pending_base_stop && enabled) {
+                    if (want_base) {
                         if constexpr (kReg)
                             pending = rf_min_pending_base(rf, heap_size, now, next, lane);
                         else
-                            pending = min_pending_base(frontier, heap_size, now, next, lane);
+                            pending = fminf(unused_base, now.base);
                     }
                     if (mode != GOFANN_EARLY_STOP_OFF && stop_worst <= pending) ++finished;
                 }
