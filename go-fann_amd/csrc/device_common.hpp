@@ -72,7 +72,7 @@ constexpr int kWave = 64;
 // score `base` (gpu_predicate::BiasedPair, gpu_predicate_index.cuh:137-144)
 // and the row's sample id, carried so that expanding the entry needs no
 // row -> sample lookup (16 B, one ds_read_b128).
-struct Entry {
+struct alignas(16) Entry {  // one 16-byte LDS access per entry
     float first;
     uint32_t second;
     float base;
@@ -449,40 +449,45 @@ __device__ __forceinline__ Entry select_entry(bool c, const Entry& a, const Entr
 
 __device__ __forceinline__ void wave_smmh_insert(Entry* h, int& size, const Entry& e, int lane)
 {
-    int y = __builtin_amdgcn_readfirstlane(size);
-    size = y + 1;
-    // the pair of slot y (and of y - 1 when y is even); its ancestor pairs
-    const int pair = (y - 1) >> 1;
+    const int y0 = __builtin_amdgcn_readfirstlane(size);
+    size = y0 + 1;
+    // the pair of slot y0 (and of y0 - 1 when y0 is even); its ancestor pairs
+    const int pair = (y0 - 1) >> 1;
     const int depth = pair > 0 ? 31 - __clz(pair + 1) : 0;
     const bool act = lane >= 1 && lane <= depth;
     // lanes past the chain read slots 1 and 2 (inside the frontier) and stay out
     const int a1 = act ? 2 * (((pair + 1) >> lane) - 1) + 1 : 1;
     const Entry al = h[a1];
     const Entry ar = h[a1 + 1];
-    const Entry sib = h[y - 1];
-    if (!(y & 1) && e.first < sib.first) {
-        // bottom sibling step: the pair's left entry moves right
-        if (lane == 0) h[y] = sib;
-        --y;
-    }
-    int side = -1;  // 0: climbs the left (minimum) slots, 1: the right slots
+    const Entry sib = h[y0 - 1];
+    // bottom sibling step: the pair's left entry moves right (lane 63 writes it)
+    const bool moved =
+        !(y0 & 1) && e.first < __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sib.first)));
+    const int y = moved ? y0 - 1 : y0;
+    // side 0 climbs the left (minimum) slots, 1 the right slots, -1 stays
+    int side = -1;
     if (depth > 0) {
         if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(al.first), 1)) > e.first)
             side = 0;
         else if (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(ar.first), 1)) < e.first)
             side = 1;
     }
-    if (side < 0) {
-        if (lane == 0) h[y] = e;
-        return;
+    const Entry v = select_entry(side == 1, ar, al);
+    const float sg = side == 1 ? -1.0f : 1.0f;  // climb: v > e on the left side, v < e on the right
+    const uint64_t mask = ballot(side >= 0 && act && sg * v.first > sg * e.first);
+    const int t = __builtin_ctzll(~(mask >> 1));  // levels climbed (0 when it stays)
+    const int sd = side == 1 ? 1 : 0;
+    // lane 0: the new entry; lanes 1..t: the chain moves down one level
+    const int lv = lane == 0 ? t : lane - 1;
+    int dst = lv == 0 ? y : 2 * (((pair + 1) >> lv) - 1) + 1 + sd;
+    Entry w = select_entry(lane == 0, e, v);
+    bool wr = lane == 0 || (act && lane <= t);
+    if (lane == kWave - 1) {
+        dst = y0;
+        w = sib;
+        wr = moved;
     }
-    const Entry v = select_entry(side != 0, ar, al);
-    const bool climb = act && (side == 0 ? v.first > e.first : v.first < e.first);
-    const uint64_t mask = ballot(climb);
-    const int t = __builtin_ctzll(~(mask >> 1));  // levels climbed
-    if (act && lane <= t)
-        h[lane == 1 ? y : 2 * (((pair + 1) >> (lane - 1)) - 1) + 1 + side] = v;
-    if (lane == 0) h[t == 0 ? y : 2 * (((pair + 1) >> t) - 1) + 1 + side] = e;
+    if (wr) h[dst] = w;
 }
 
 // Returns the new maximum (slot 2's `first`); the heap keeps >= 3 slots.
