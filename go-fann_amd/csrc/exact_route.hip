@@ -79,9 +79,11 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_FIXED_ROWS 0
 #endif
 
-// Minimum waves per SIMD the kernel is compiled for (register budget).
+// Minimum waves per SIMD the kernel is compiled for (register budget).  5
+// holds the LDS-frontier kernels to 96 VGPRs (20 routes per CU instead of
+// 16, a few spills in cold paths): 55.5 against 57.0 ms at C2, Q = 80.
 #ifndef GOFANN_EXACT_MIN_WAVES
-#define GOFANN_EXACT_MIN_WAVES 1
+#define GOFANN_EXACT_MIN_WAVES 5
 #endif
 
 // Most registers per lane a register frontier may use (Q + 2 <= 64 x this).
