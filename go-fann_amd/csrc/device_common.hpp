@@ -857,16 +857,19 @@ __device__ __forceinline__ bool lane_row_contains(const gofann_predicate_view& v
 __device__ __forceinline__ void lane_row_bounds(const gofann_predicate_view& v, uint32_t sample,
                                                 bool active, LaneRow& r, uint4& slab)
 {
-    r.begin = 0;
-    r.end = 0;
-    slab = make_uint4(kSlabOverflow, 0, 0, 0);
-    if (!active) return;
-    if (slab_usable(v, sample)) {
-        slab = slab_load(v, sample);
-    } else if (sample < v.rows && v.csr_offsets != nullptr) {
-        r.begin = v.csr_offsets[sample];
-        r.end = v.csr_offsets[sample + 1];
+    // computed in locals and stored once, so the row stays in registers
+    uint32_t b = 0, e = 0;
+    uint4 sl = make_uint4(kSlabOverflow, 0, 0, 0);
+    const bool use_slab = active && slab_usable(v, sample);
+    if (use_slab) {
+        sl = slab_load(v, sample);
+    } else if (active && sample < v.rows && v.csr_offsets != nullptr) {
+        b = v.csr_offsets[sample];
+        e = v.csr_offsets[sample + 1];
     }
+    r.begin = b;
+    r.end = e;
+    slab = sl;
 }
 
 __device__ __forceinline__ void lane_row_fill(const gofann_predicate_view& v, LaneRow& r,
@@ -885,17 +888,22 @@ __device__ __forceinline__ void lane_row_fill(const gofann_predicate_view& v, La
                                : UINT32_MAX;
             return;
         }
-        r.begin = v.csr_offsets[sample];
-        r.end = v.csr_offsets[sample + 1];
     }
-    const uint32_t last = r.end > r.begin ? r.end - 1 : r.begin;
+    // the bounds in locals (an overflowing slab reads them from the CSR), so
+    // the row stays in registers
+    const bool overflow = slab_usable(v, sample);
+    const uint32_t b = overflow ? v.csr_offsets[sample] : r.begin;
+    const uint32_t e = overflow ? v.csr_offsets[sample + 1] : r.end;
+    r.begin = b;
+    r.end = e;
+    const uint32_t last = e > b ? e - 1 : b;
 #pragma unroll
     for (int k = 0; k < kLaneRowBatch; ++k) {
         // Clamped address: every load is in bounds, so the batch issues as
         // independent loads; entries past the end are masked afterwards.
-        const uint32_t i = r.begin + static_cast<uint32_t>(k) < last ? r.begin + k : last;
-        const uint32_t x = r.end > r.begin ? v.csr_labels[i] : UINT32_MAX;
-        r.lab[k] = r.begin + static_cast<uint32_t>(k) < r.end ? x : UINT32_MAX;
+        const uint32_t i = b + static_cast<uint32_t>(k) < last ? b + k : last;
+        const uint32_t x = e > b ? v.csr_labels[i] : UINT32_MAX;
+        r.lab[k] = b + static_cast<uint32_t>(k) < e ? x : UINT32_MAX;
     }
 }
 
@@ -992,10 +1000,11 @@ __device__ __forceinline__ int wave_sum(int v)
 // Frontier pickup (wave-cooperative).
 // pickup_next_unused_from_native_frontier (backend_pq.cu:844-892): unused
 // entry of least `first`, lowest index on ties; lane 0 marks it used.
-// With `min_base`, the same pass also returns the least `base` over the
-// entries that were unused before the pickup (the picked one included).
+// With `want_base`, the same pass also returns in `min_base` the least
+// `base` over the entries that were unused before the pickup (the picked one
+// included).
 __device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane,
-                                       float* min_base = nullptr)
+                                       bool want_base, float& min_base)
 {
     int best = -1;
     float bv = 0.0f;
@@ -1003,13 +1012,13 @@ __device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane,
     for (int i = lane + 1; i < size; i += kWave) {
         const Entry e = f[i];
         if (e.second & kPoolUsed) continue;
-        if (min_base) mb = fminf(mb, e.base);
+        if (want_base) mb = fminf(mb, e.base);
         if (best < 0 || e.first < bv) {
             best = i;
             bv = e.first;
         }
     }
-    if (min_base) *min_base = wave_min(mb);
+    if (want_base) min_base = wave_min(mb);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const int ob = __shfl_xor(best, off, kWave);
@@ -1026,6 +1035,12 @@ __device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane,
     if (lane == 0) f[best].second |= kPoolUsed;
     __syncthreads();
     return true;
+}
+
+__device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane)
+{
+    float unused;
+    return pickup(f, size, out, lane, false, unused);
 }
 
 // XCD-aware block -> slot mapping: the dispatcher deals consecutive

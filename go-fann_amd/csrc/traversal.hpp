@@ -793,7 +793,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
             if constexpr (kReg)
                 found = rf_pickup(rf, heap_size, next, lane);
             else
-                found = pickup(frontier, heap_size, next, lane, want_base ? &unused_base : nullptr);
+                found = pickup(frontier, heap_size, next, lane, want_base, unused_base);
             if (!found) {
                 exhausted = 1;
                 next = sentinel;
