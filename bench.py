@@ -89,6 +89,9 @@ def parse():
                     help="C4/C5 label-posting scans: 'columns' = segmented scan over "
                          "posting-order copies of the rows' codes and predicate columns; "
                          "'gather' = one workgroup per route, rows gathered by sample id")
+    ap.add_argument("--no-posting-share", action="store_true",
+                    help="label postings: scan route by route instead of sharing each label "
+                         "segment's rows among its routes")
     ap.add_argument("--posting-segment-rows", type=int, default=32768,
                     help="rows per segment of the segmented label-posting scan")
     ap.add_argument("--c4-threshold", type=int, default=50_000,
@@ -1223,7 +1226,7 @@ class RabitqLabelPipeline:
     shortlists, and the per-query merge."""
 
     def __init__(self, ctx, wl, li, rq, torch, width=100, posting_layout="columns",
-                 segment_rows=32768, neighbor_samples=True):
+                 segment_rows=32768, neighbor_samples=True, posting_share=True):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
         from gofann_amd import range_posting as rp
@@ -1314,8 +1317,18 @@ class RabitqLabelPipeline:
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
         self.seed_buf = self.dr.route_start.clone()
         self.posting_layout = posting_layout if self.np_ else "gather"
+        self.scan_share = None
         if self.posting_layout == "columns":
             self._posting_columns(li, post_rows, segment_rows)
+            # Sharing pays where routes re-read the same postings (C5: 21x);
+            # with little reuse (C4: 1.8x) the route-by-route scan has more
+            # workgroups to fill the chip.
+            reuse = self.post_rows_total / max(self.scan_total, 1)
+            if posting_share and reuse >= 4.0 and width <= 128 and self.P <= 1024:
+                sp = self.rp.share_plan(self.scan_segs.plan)
+                self.scan_share = self.rp.DeviceShare(sp)
+                log(f"label postings shared (rows re-read {reuse:.1f}x): {sp.items} items for "
+                    f"{plan_count(self.scan_segs)} segments")
 
     def _posting_columns(self, li, post_rows, segment_rows):
         """The label-posting scan's layout: the postings of the labels the
@@ -1406,7 +1419,8 @@ class RabitqLabelPipeline:
                 ctx, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
                 self.dp.route_query, self.scan_ids, self.scan_total, self.scan_segs, W,
                 rows=self.scan_rows, cols=self.scan_cols,
-                out=(self.sl_i[self.ng * W:], self.sl_d[self.ng * W:], self.passes))
+                out=(self.sl_i[self.ng * W:], self.sl_d[self.ng * W:], self.passes),
+                share=self.scan_share)
         elif self.np_:
             ctx.check(ctx.lib.gofann_rabitq_posting_scan(
                 ctx.handle, self.rv, self.rq, self.dp.predicate_view(self.dg, 0.0, False),
@@ -1422,6 +1436,10 @@ class RabitqLabelPipeline:
 
     def route_stats(self):
         return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
+
+
+def plan_count(segs) -> int:
+    return segs.plan.count
 
 
 def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
@@ -1582,7 +1600,8 @@ def c4_kernels(pipe, st_ms, st):
     ff = rows * (4 + pred) + passed * C + 0.0
     extra = {"passing_rows": passed, "filter_first_bytes": ff,
              "filter_first_gbps": round(ff / (st_ms["posting_scan"] / 1000.0) / 1e9, 2)
-             if st_ms["posting_scan"] > 0 else None, "layout": pipe.posting_layout}
+             if st_ms["posting_scan"] > 0 else None, "layout": pipe.posting_layout,
+             "shared": pipe.scan_share is not None}
     rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 2 + 4) + 0.0
     return {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
             "range_scan_group_kernel+segment_merge_kernel (label postings)":
@@ -1619,7 +1638,8 @@ def run_c4(args, torch, ctx, world=None) -> dict:
     t0 = time.time()
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
                                segment_rows=args.posting_segment_rows,
-                               neighbor_samples=not args.no_neighbor_samples)
+                               neighbor_samples=not args.no_neighbor_samples,
+                               posting_share=not args.no_posting_share)
     pipe.P, pipe.li = rq["P"], li
     log(f"C4 routes: {pipe.ng} graph ({pipe.n_eq} equality, {pipe.interior} interior "
         f"intervals), {pipe.np_} label-posting scans ({pipe.post_rows_total} rows), planned "
@@ -1748,7 +1768,8 @@ def run_c5(args, torch, ctx, world=None) -> dict:
     t0 = time.time()
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
                                segment_rows=args.posting_segment_rows,
-                               neighbor_samples=not args.no_neighbor_samples)
+                               neighbor_samples=not args.no_neighbor_samples,
+                               posting_share=not args.no_posting_share)
     pipe.P, pipe.li = rq["P"], li
     types = wl.meta["query_types"]
     log(f"C5 routes: {pipe.ng} graph, {pipe.np_} label-posting scans ({pipe.post_rows_total} "

@@ -313,6 +313,26 @@ int gofann_rabitq_posting_scan_segments(gofann_ctx* c, const gofann_rabitq_view*
     });
 }
 
+int gofann_rabitq_posting_scan_shared(gofann_ctx* c, const gofann_rabitq_view* rq,
+                                      const gofann_rabitq_queries* prepared,
+                                      const gofann_predicate_view* predicate,
+                                      const uint32_t* route_query,
+                                      const uint32_t* posting_sample_ids, uint64_t posting_rows,
+                                      const gofann_posting_segments* segments,
+                                      const gofann_posting_share* share, int shortlist_k,
+                                      const uint8_t* posting_codes, const uint32_t* posting_aux,
+                                      const uint32_t* posting_slab,
+                                      const float* posting_ranges, uint32_t* out_ids,
+                                      float* out_dists, uint32_t* pass_counts)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::rabitq_posting_scan_shared(
+            ctx, rq, prepared, predicate, route_query, posting_sample_ids, posting_rows, segments,
+            share, shortlist_k, posting_codes, posting_aux, posting_slab, posting_ranges, out_ids,
+            out_dists, pass_counts);
+    });
+}
+
 int gofann_exact_rerank(gofann_ctx* c, const void* base, int base_elem, uint32_t dim,
                         uint32_t samples, const void* queries, const uint32_t* route_query,
                         const uint32_t* shortlist, uint32_t width, uint32_t routes, uint32_t topk,

@@ -115,6 +115,15 @@ int rabitq_posting_scan_segments(Context* ctx, const gofann_rabitq_view* rq,
                                  const uint8_t* posting_codes, const uint32_t* posting_aux,
                                  const uint32_t* posting_slab, const float* posting_ranges,
                                  uint32_t* out_ids, float* out_dists, uint32_t* pass_counts);
+int rabitq_posting_scan_shared(Context* ctx, const gofann_rabitq_view* rq,
+                               const gofann_rabitq_queries* pre,
+                               const gofann_predicate_view* pred, const uint32_t* route_query,
+                               const uint32_t* posting, uint64_t posting_rows,
+                               const gofann_posting_segments* seg,
+                               const gofann_posting_share* share, int shortlist_k,
+                               const uint8_t* posting_codes, const uint32_t* posting_aux,
+                               const uint32_t* posting_slab, const float* posting_ranges,
+                               uint32_t* out_ids, float* out_dists, uint32_t* pass_counts);
 int exact_search(Context* ctx, const void* base, int base_elem, uint32_t dim, uint32_t samples,
                  const void* queries, const gofann_graph_view* g, const uint32_t* label_size,
                  const gofann_predicate_view* pred, const gofann_routes* r,

@@ -706,6 +706,247 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
     if (tid == 0 && a.pass_counts) a.pass_counts[seg] = s_pass;
 }
 
+// ---------------------------------------------------------------------------
+// Label-shared posting scan (no counterpart in the reference, whose label
+// postings are scanned route by route): the label-posting segments that scan
+// the same posting rows -- the routes of one label -- share one workgroup.
+// The workgroup loads a tile of the rows' posting-order columns (sample id,
+// label slab, range value) into LDS once; each wave owns up to
+// kShareRoutesPerWave of the routes and, per tile, filters the tile for
+// each of them from LDS, queues the passing rows, scores them 64 at a time
+// (one row per lane, codes and aux from the posting-order copies) and
+// merges the survivors into the route's shortlist by rank, with no
+// workgroup barrier per route.  Every route's output for the segment is the
+// k least (distance, id) pairs of its passing rows and its pass count --
+// the group kernel's output for that segment, bit for bit.
+// ---------------------------------------------------------------------------
+constexpr int kShareTile = 1024;          // rows per LDS tile
+constexpr int kShareRoutesPerWave = 4;
+constexpr int kShareRoutes = kShareRoutesPerWave * (kScanThreads / kWave);  // 16 per item
+constexpr int kShareMaxKp = 128;          // shortlist_k <= 128
+
+struct ShareScanArgs {
+    gofann_predicate_view pred;
+    const uint32_t* route_query;
+    const uint32_t* posting;
+    uint64_t resident_rows;
+    const uint32_t* seg_route;
+    const uint64_t* item_offset;
+    const uint64_t* item_size;
+    const uint32_t* item_begin;  // [items + 1] into item_slots
+    const uint32_t* item_slots;  // plan segment indices
+    uint32_t items;
+    uint32_t base_rows;
+    int k;
+    int k_pow2;
+    const uint4* pcodes;
+    const uint4* paux;
+    const uint4* pslab;
+    const float* pranges;
+    uint32_t* out_ids;
+    float* out_dists;
+    uint32_t* pass_counts;
+};
+
+template <int V>
+__global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareScanArgs a,
+                                                                        RabitqScanScorer sc)
+{
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ uint32_t s_pass[kShareRoutes];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const uint32_t item = blockIdx.x;
+    if (item >= a.items) return;
+    const int k = a.k, kp = a.k_pow2;
+    // LDS: tile columns, then per route slot its query planes (plane-major,
+    // 8 x V 16-byte vectors) and its shortlist (kp pairs), then per wave a
+    // queue of tile rows to score.
+    uint32_t* t_ids = reinterpret_cast<uint32_t*>(lds);
+    uint4* t_slab = reinterpret_cast<uint4*>(t_ids + kShareTile);
+    float* t_r0 = reinterpret_cast<float*>(t_slab + kShareTile);
+    uint4* planes_all = reinterpret_cast<uint4*>(t_r0 + kShareTile);
+    float* lst_d_all = reinterpret_cast<float*>(planes_all + kShareRoutes * 8 * V);
+    uint32_t* lst_id_all = reinterpret_cast<uint32_t*>(lst_d_all + kShareRoutes * kp);
+    uint32_t* queue_all = lst_id_all + kShareRoutes * kp;
+
+    const uint32_t first = a.item_begin[item];
+    const int n_routes = static_cast<int>(a.item_begin[item + 1] - first);
+    const uint64_t begin = a.item_offset[item];
+    uint64_t count = a.item_size[item];
+    if (begin > a.resident_rows)
+        count = 0;
+    else if (count > a.resident_rows - begin)
+        count = a.resident_rows - begin;
+
+    // Route slots q = wave + 4 i: query planes and an empty shortlist.
+    for (int i = 0; i < kShareRoutesPerWave; ++i) {
+        const int q = wave + i * (kScanThreads / kWave);
+        if (q >= n_routes) break;
+        const uint32_t route = a.seg_route[a.item_slots[first + q]];
+        const uint32_t query = a.route_query[route];
+        uint32_t* pl = reinterpret_cast<uint32_t*>(planes_all + q * 8 * V);
+        const int8_t* qrow = sc.q8 + static_cast<size_t>(query) * sc.padded_dim;
+        const int words = 4 * V;  // padded_dim / 32
+        if (lane < words) {
+            uint32_t bits[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int b = 0; b < 32; ++b) {
+                const uint32_t v = static_cast<uint8_t>(qrow[lane * 32 + b]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bits[j] |= ((v >> j) & 1u) << (31 - b);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pl[j * words + lane] = bits[j];
+        }
+        for (int e = lane; e < kp; e += kWave) {
+            lst_d_all[q * kp + e] = FLT_MAX;
+            lst_id_all[q * kp + e] = UINT32_MAX;
+        }
+        if (lane == 0) s_pass[q] = 0;
+    }
+    uint32_t* queue = queue_all + wave * kWave;
+    const bool r0_tile = a.pranges && a.pred.range_stride == 1;
+
+    for (uint64_t t0 = 0; t0 < count; t0 += kShareTile) {
+        __syncthreads();  // the previous tile's reads end here
+        const int n = static_cast<int>(count - t0 < kShareTile ? count - t0 : kShareTile);
+        for (int r = tid; r < n; r += kScanThreads) {
+            const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
+            t_ids[r] = a.posting[j];
+            t_slab[r] = a.pslab[j];
+            if (r0_tile) t_r0[r] = a.pranges[j];
+        }
+        __syncthreads();
+        for (int i = 0; i < kShareRoutesPerWave; ++i) {
+            const int q = wave + i * (kScanThreads / kWave);
+            if (q >= n_routes) break;
+            const uint32_t route = a.seg_route[a.item_slots[first + q]];
+            const uint32_t query = a.route_query[route];
+            const bool enabled = pred_enabled(a.pred, route);
+            const float scale = sc.q_scale[query];
+            const float k1 = sc.q_k1[query];
+            const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
+            const uint4* planes = planes_all + q * 8 * V;
+            float* ld = lst_d_all + q * kp;
+            uint32_t* lid = lst_id_all + q * kp;
+            uint32_t passes = 0;
+            int qn = 0;  // queued rows (uniform)
+            // Score the queued rows (lane i < qn takes queue[i]) and merge
+            // the survivors into the shortlist by rank.
+            auto flush = [&]() {
+                const bool have = lane < qn;
+                const int r = have ? static_cast<int>(queue[lane]) : 0;
+                const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
+                uint32_t sid = UINT32_MAX;
+                float v = FLT_MAX;
+                if (have) {
+                    sid = t_ids[r];
+                    const uint4 x = a.paux[j];
+                    uint4 c[V];
+#pragma unroll
+                    for (int w = 0; w < V; ++w) c[w] = a.pcodes[j * V + w];
+                    const float add0 = __uint_as_float(x.x) + g_row[x.z];
+                    const int ip = lane_ip_lds<1, V>(c, planes, V, 0);
+                    const float short_ip = static_cast<float>(ip) * scale;
+                    const float tt = short_ip + k1;
+                    v = fmaf(__uint_as_float(x.y), tt, add0);
+                }
+                const float kd = ld[k - 1];
+                const uint32_t kid = lid[k - 1];
+                const bool in = have && admissible(v, sid) && pair_less(v, sid, kd, kid);
+                const uint64_t sm = ballot(in);
+                qn = 0;
+                if (!sm) return;
+                // ranks: list entry e moves up by the survivors below it; a
+                // survivor lands after the list entries and survivors below it
+                int c_self = 0;
+                if (in) {
+                    int lo = 0, hi = k;
+                    while (lo < hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (pair_less(ld[mid], lid[mid], v, sid))
+                            lo = mid + 1;
+                        else
+                            hi = mid;
+                    }
+                    c_self = lo;
+                }
+                const int e0 = lane, e1 = lane + kWave;
+                const float d0 = e0 < k ? ld[e0] : FLT_MAX;
+                const uint32_t i0 = e0 < k ? lid[e0] : UINT32_MAX;
+                const float d1 = e1 < k ? ld[e1] : FLT_MAX;
+                const uint32_t i1 = e1 < k ? lid[e1] : UINT32_MAX;
+                int c0 = 0, c1 = 0;
+                for (uint64_t m = sm; m; m &= m - 1) {
+                    const int src = __builtin_ctzll(m);
+                    const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+                    const uint32_t si = static_cast<uint32_t>(
+                        __builtin_amdgcn_readlane(static_cast<int>(sid), src));
+                    c0 += pair_less(sv, si, d0, i0) ? 1 : 0;
+                    c1 += pair_less(sv, si, d1, i1) ? 1 : 0;
+                    c_self += pair_less(sv, si, v, sid) ? 1 : 0;
+                }
+                // all reads of the old list precede these writes (one wave)
+                if (e0 < k && e0 + c0 < k) {
+                    ld[e0 + c0] = d0;
+                    lid[e0 + c0] = i0;
+                }
+                if (e1 < k && e1 + c1 < k) {
+                    ld[e1 + c1] = d1;
+                    lid[e1 + c1] = i1;
+                }
+                if (in && c_self < k) {
+                    ld[c_self] = v;
+                    lid[c_self] = sid;
+                }
+            };
+            for (int r0 = 0; r0 < n; r0 += kWave) {
+                const int r = r0 + lane;
+                bool ok = false;
+                if (r < n) {
+                    const uint32_t s = t_ids[r];
+                    ok = s < a.base_rows;
+                    if (ok && enabled) {
+                        const uint4 slab = t_slab[r];
+                        if (slab_count(slab) != kSlabOverflow) {
+                            const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
+                            const float* prange = a.pranges && a.pred.range_stride > 0
+                                                      ? a.pranges + j * a.pred.range_stride
+                                                      : nullptr;
+                            ok = slab_pred_matches(a.pred, route, s, slab, prange,
+                                                   r0_tile ? t_r0[r] : 0.0f);
+                        } else {
+                            PredCounters pc{0, 0};
+                            ok = pred_matches(a.pred, route, s, pc);
+                        }
+                    }
+                }
+                const uint64_t om = ballot(ok);
+                const int c = __popcll(om);
+                if (enabled) passes += static_cast<uint32_t>(c);
+                if (c == 0) continue;
+                if (qn + c > kWave) flush();
+                if (ok) queue[qn + static_cast<int>(lanes_below(om))] = static_cast<uint32_t>(r);
+                qn += c;
+            }
+            if (qn) flush();
+            if (lane == 0) s_pass[q] += passes;
+        }
+    }
+    __syncthreads();
+    for (int i = 0; i < kShareRoutesPerWave; ++i) {
+        const int q = wave + i * (kScanThreads / kWave);
+        if (q >= n_routes) break;
+        const uint32_t slot = a.item_slots[first + q];
+        for (int e = lane; e < k; e += kWave) {
+            a.out_ids[static_cast<size_t>(slot) * k + e] = lst_id_all[q * kp + e];
+            a.out_dists[static_cast<size_t>(slot) * k + e] = lst_d_all[q * kp + e];
+        }
+        if (lane == 0 && a.pass_counts) a.pass_counts[slot] = s_pass[q];
+    }
+}
+
 struct SegmentMergeArgs {
     const uint32_t* query_indptr;  // null: position p takes [p * stride, (p + 1) * stride)
     uint32_t stride;
@@ -1122,6 +1363,130 @@ int rabitq_posting_scan_segments(Context* ctx, const gofann_rabitq_view* rq,
     if (hipLaunchKernel(kern, dim3(seg->count), dim3(kScanThreads), kargs, lds, ctx->stream) !=
         hipSuccess)
         return ctx->fail_hip("posting scan launch");
+    if (!merged || seg->positions == 0) return GOFANN_OK;
+
+    SegmentMergeArgs m;
+    m.query_indptr = seg->query_indptr;
+    m.stride = 0;
+    m.positions = seg->positions;
+    m.seg_ids = scan_ids;
+    m.seg_dists = scan_dists;
+    m.seg_pass = scan_pass;
+    m.k = shortlist_k;
+    m.k_pow2 = a.k_pow2;
+    m.out_ids = out_ids;
+    m.out_dists = out_dists;
+    m.out_pass = pass_counts;
+    const size_t mlds = static_cast<size_t>(2 * a.k_pow2) * 8;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(segment_merge_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(mlds)) !=
+        hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute posting merge");
+    hipLaunchKernelGGL(segment_merge_kernel, dim3(seg->positions), dim3(kScanThreads), mlds,
+                       ctx->stream, m);
+    if (hipGetLastError() != hipSuccess) return ctx->fail_hip("posting merge launch");
+    return GOFANN_OK;
+}
+
+// The label-shared variant of rabitq_posting_scan_segments: `share` lists
+// the plan's segments by the rows they scan (items of at most kShareRoutes
+// segments with equal offset and size).  Needs the posting-order codes, aux
+// and slab; the outputs equal rabitq_posting_scan_segments' bit for bit.
+int rabitq_posting_scan_shared(Context* ctx, const gofann_rabitq_view* rq,
+                               const gofann_rabitq_queries* pre,
+                               const gofann_predicate_view* pred, const uint32_t* route_query,
+                               const uint32_t* posting, uint64_t posting_rows,
+                               const gofann_posting_segments* seg,
+                               const gofann_posting_share* share, int shortlist_k,
+                               const uint8_t* posting_codes, const uint32_t* posting_aux,
+                               const uint32_t* posting_slab, const float* posting_ranges,
+                               uint32_t* out_ids, float* out_dists, uint32_t* pass_counts)
+{
+    if (!share) return ctx->fail(GOFANN_ERR_INVALID, "share plan missing");
+    if (!posting_codes || !posting_aux || !posting_slab)
+        return ctx->fail(GOFANN_ERR_INVALID, "the shared scan reads posting-order codes, aux and slab");
+    if (posting_ranges && !posting_slab)
+        return ctx->fail(GOFANN_ERR_INVALID, "posting ranges need the posting slab");
+    if (!rq || !pre || !rq->codes || !rq->factors || !rq->anchor_ids || rq->padded_dim == 0 ||
+        rq->padded_dim % 128 != 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view invalid for posting scan");
+    if (!pre->q8 || !pre->scale || !pre->k1 || !pre->centroid_dists)
+        return ctx->fail(GOFANN_ERR_INVALID, "prepared RaBitQ queries incomplete");
+    if (!seg) return ctx->fail(GOFANN_ERR_INVALID, "segment plan missing");
+    if (shortlist_k < 1 || shortlist_k > kShareMaxKp)
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "the shared scan takes shortlist_k <= 128");
+    const void* kern = nullptr;
+    switch (rq->padded_dim / 128) {
+        case 1: kern = reinterpret_cast<const void*>(label_share_scan_kernel<1>); break;
+        case 2: kern = reinterpret_cast<const void*>(label_share_scan_kernel<2>); break;
+        case 4: kern = reinterpret_cast<const void*>(label_share_scan_kernel<4>); break;
+        case 8: kern = reinterpret_cast<const void*>(label_share_scan_kernel<8>); break;
+        default: return ctx->fail(GOFANN_ERR_UNSUPPORTED, "the shared scan takes padded_dim <= 1024");
+    }
+    if (seg->count == 0) {
+        if (seg->query_indptr && seg->positions)
+            return ctx->fail(GOFANN_ERR_INVALID, "segment plan has positions but no segments");
+        return GOFANN_OK;
+    }
+    if (!seg->route_ids || !posting || !route_query)
+        return ctx->fail(GOFANN_ERR_INVALID, "segment plan or posting arrays missing");
+    if (!share->item_offsets || !share->item_sizes || !share->item_begin || !share->item_slots ||
+        share->items == 0)
+        return ctx->fail(GOFANN_ERR_INVALID, "share plan arrays missing");
+    if (!out_ids || !out_dists) return ctx->fail(GOFANN_ERR_INVALID, "posting scan outputs missing");
+    if ((reinterpret_cast<uintptr_t>(posting_codes) | reinterpret_cast<uintptr_t>(posting_aux) |
+         reinterpret_cast<uintptr_t>(posting_slab)) & 15u)
+        return ctx->fail(GOFANN_ERR_INVALID, "posting-order arrays must be 16-byte aligned");
+
+    const bool merged = seg->query_indptr != nullptr;
+    uint32_t* scan_ids = out_ids;
+    float* scan_dists = out_dists;
+    uint32_t* scan_pass = pass_counts;
+    const size_t slots_out = static_cast<size_t>(seg->count) * static_cast<size_t>(shortlist_k);
+    if (merged) {
+        const size_t bytes = slots_out * 8 + static_cast<size_t>(seg->count) * 4 + 64;
+        unsigned char* buf = static_cast<unsigned char*>(ctx->scratch(Context::kScratchRange, bytes));
+        if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "posting segment scratch allocation failed");
+        scan_ids = reinterpret_cast<uint32_t*>(buf);
+        scan_dists = reinterpret_cast<float*>(buf + slots_out * 4);
+        scan_pass = reinterpret_cast<uint32_t*>(buf + slots_out * 8);
+    }
+    ShareScanArgs a{};
+    a.pred = pred ? *pred : gofann_predicate_view{};
+    a.route_query = route_query;
+    a.posting = posting;
+    a.resident_rows = posting_rows;
+    a.seg_route = seg->route_ids;
+    a.item_offset = share->item_offsets;
+    a.item_size = share->item_sizes;
+    a.item_begin = share->item_begin;
+    a.item_slots = share->item_slots;
+    a.items = share->items;
+    a.base_rows = rq->samples ? rq->samples : UINT32_MAX;
+    a.k = shortlist_k;
+    a.k_pow2 = pow2_at_least(shortlist_k);
+    a.pcodes = reinterpret_cast<const uint4*>(posting_codes);
+    a.paux = reinterpret_cast<const uint4*>(posting_aux);
+    a.pslab = reinterpret_cast<const uint4*>(posting_slab);
+    a.pranges = posting_ranges;
+    a.out_ids = scan_ids;
+    a.out_dists = scan_dists;
+    a.pass_counts = merged || pass_counts ? scan_pass : nullptr;
+    const size_t vecs = rq->padded_dim / 128;
+    const size_t lds = static_cast<size_t>(kShareTile) * 24 +
+                       static_cast<size_t>(kShareRoutes) * 8 * vecs * 16 +
+                       static_cast<size_t>(kShareRoutes) * a.k_pow2 * 8 +
+                       static_cast<size_t>(kScanThreads) * 4;
+    if (lds > static_cast<size_t>(ctx->lds_per_block))
+        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "shared posting scan LDS exceeds the workgroup limit");
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) != hipSuccess)
+        return ctx->fail_hip("hipFuncSetAttribute shared posting scan");
+    RabitqScanScorer sc = scan_scorer(rq, pre);
+    void* kargs[] = {&a, &sc};
+    if (hipLaunchKernel(kern, dim3(share->items), dim3(kScanThreads), kargs, lds, ctx->stream) !=
+        hipSuccess)
+        return ctx->fail_hip("shared posting scan launch");
     if (!merged || seg->positions == 0) return GOFANN_OK;
 
     SegmentMergeArgs m;

@@ -101,6 +101,11 @@ class PostingSegments(C.Structure):
                 ("query_indptr", P), ("positions", U32)]
 
 
+class PostingShare(C.Structure):
+    _fields_ = [("item_offsets", P), ("item_sizes", P), ("item_begin", P), ("item_slots", P),
+                ("items", U32)]
+
+
 U64 = C.c_uint64
 CS = C.c_char_p
 
@@ -184,6 +189,12 @@ SIGNATURES = {
                                                       C.POINTER(PredicateView), P, P, C.c_uint64,
                                                       C.POINTER(PostingSegments), C.c_int, P, P,
                                                       P, P, P, P, P]),
+    "gofann_rabitq_posting_scan_shared": (C.c_int, [P, C.POINTER(RabitqView),
+                                                    C.POINTER(RabitqQueries),
+                                                    C.POINTER(PredicateView), P, P, C.c_uint64,
+                                                    C.POINTER(PostingSegments),
+                                                    C.POINTER(PostingShare), C.c_int, P, P,
+                                                    P, P, P, P, P]),
     "gofann_exact_rerank": (C.c_int, [P, P, C.c_int, U32, U32, P, P, P, U32, U32, U32, P, P]),
     "gofann_merge_routes": (C.c_int, [P, P, P, P, P, U32, U32, U32, P, P]),
     "gofann_predicate_masks": (C.c_int, [P, C.POINTER(PredicateView), P, P, U32, P]),

@@ -257,6 +257,71 @@ class DeviceSegments:
                                     _lib.ptr(self.indptr), self.positions if self.indptr is not None else 0)
 
 
+SHARE_ROUTES = 16  # segments per share item (kShareRoutes)
+
+
+@dataclass
+class SharePlan:
+    """Segments of a SegmentPlan that scan the same posting rows, grouped:
+    item i covers rows [offsets[i], + sizes[i]) for plan segments
+    slots[begin[i] .. begin[i + 1])."""
+    offsets: np.ndarray
+    sizes: np.ndarray
+    begin: np.ndarray
+    slots: np.ndarray
+
+    @property
+    def items(self) -> int:
+        return int(self.offsets.size)
+
+
+def share_plan(plan: SegmentPlan, routes_per_item: int = SHARE_ROUTES) -> SharePlan:
+    """Groups the plan's segments by (offset, size) -- the routes of one
+    label cut the same way -- into items of at most `routes_per_item`,
+    the heaviest items (rows x routes) first."""
+    m = plan.count
+    if m == 0:
+        z = np.zeros(0, np.uint64)
+        return SharePlan(z, z, np.zeros(1, np.uint32), np.zeros(0, np.uint32))
+    order = np.lexsort((np.arange(m), plan.sizes, plan.offsets))
+    o, sz = plan.offsets[order], plan.sizes[order]
+    new = np.ones(m, bool)
+    new[1:] = (o[1:] != o[:-1]) | (sz[1:] != sz[:-1])
+    gid = np.cumsum(new) - 1
+    gstart = np.flatnonzero(new)
+    # position inside the group, then items of routes_per_item
+    pos = np.arange(m) - gstart[gid]
+    item_key = gid * (m + 1) + pos // routes_per_item
+    istart = np.flatnonzero(np.r_[True, item_key[1:] != item_key[:-1]])
+    counts = np.diff(np.r_[istart, m])
+    weight = sz[istart].astype(np.float64) * counts
+    iorder = np.argsort(-weight, kind="stable")
+    slots, offs, sizes, begin = [], [], [], [0]
+    for i in iorder:
+        a = istart[i]
+        slots.append(order[a:a + counts[i]])
+        offs.append(o[a])
+        sizes.append(sz[a])
+        begin.append(begin[-1] + int(counts[i]))
+    return SharePlan(np.array(offs, np.uint64), np.array(sizes, np.uint64),
+                     np.array(begin, np.uint32), np.concatenate(slots).astype(np.uint32))
+
+
+class DeviceShare:
+    """A SharePlan on the device and its gofann_posting_share view."""
+
+    def __init__(self, sp: SharePlan, device="cuda"):
+        self.sp = sp
+        self.offsets = torch.from_numpy(sp.offsets.view(np.int64)).to(device)
+        self.sizes = torch.from_numpy(sp.sizes.view(np.int64)).to(device)
+        self.begin = torch.from_numpy(sp.begin.view(np.int32)).to(device)
+        self.slots = torch.from_numpy(sp.slots.view(np.int32)).to(device)
+
+    def view(self) -> _lib.PostingShare:
+        return _lib.PostingShare(_lib.ptr(self.offsets), _lib.ptr(self.sizes),
+                                 _lib.ptr(self.begin), _lib.ptr(self.slots), self.sp.items)
+
+
 def route_postings(index: RangePostingIndex, slices: np.ndarray):
     """Flat device offsets and sizes of each route's chosen slice."""
     rng = slices[:, 2].astype(np.int64)
@@ -307,10 +372,12 @@ def rabitq_posting_scan_segments(ctx: _lib.Context, rv: _lib.RabitqView,
                                  route_query: torch.Tensor, postings: torch.Tensor,
                                  posting_rows: int, segs: DeviceSegments, shortlist_k: int,
                                  rows: PostingRows | None = None,
-                                 cols: PostingPredicateColumns | None = None, out=None):
-    """Runs gofann_rabitq_posting_scan_segments; returns (ids int32, dists,
-    passes) on the device, [positions][shortlist_k] (into `out` =
-    (ids, dists, passes) flat tensors when given)."""
+                                 cols: PostingPredicateColumns | None = None, out=None,
+                                 share: DeviceShare | None = None):
+    """Runs gofann_rabitq_posting_scan_segments (with `share`, and the rows
+    and columns, gofann_rabitq_posting_scan_shared: the same outputs);
+    returns (ids int32, dists, passes) on the device, [positions][shortlist_k]
+    (into `out` = (ids, dists, passes) flat tensors when given)."""
     n = segs.positions
     dev = postings.device
     if out is None:
@@ -318,6 +385,17 @@ def rabitq_posting_scan_segments(ctx: _lib.Context, rv: _lib.RabitqView,
                torch.empty(max(n, 1) * shortlist_k, dtype=torch.float32, device=dev),
                torch.empty(max(n, 1), dtype=torch.int32, device=dev))
     ids, dists, passes = out
+    if share is not None:
+        if rows is None or cols is None:
+            raise RangeIndexError("the shared scan reads the posting-order rows and columns")
+        ctx.check(ctx.lib.gofann_rabitq_posting_scan_shared(
+            ctx.handle, rv, rq, pred, _lib.ptr(route_query), _lib.ptr(postings),
+            int(posting_rows), segs.view(), share.view(), shortlist_k, _lib.ptr(rows.codes),
+            _lib.ptr(rows.aux), _lib.ptr(cols.slab),
+            _lib.ptr(cols.ranges) if cols.ranges is not None else None,
+            _lib.ptr(ids), _lib.ptr(dists), _lib.ptr(passes)))
+        return (ids[: n * shortlist_k].view(n, shortlist_k),
+                dists[: n * shortlist_k].view(n, shortlist_k), passes[:n])
     ctx.check(ctx.lib.gofann_rabitq_posting_scan_segments(
         ctx.handle, rv, rq, pred, _lib.ptr(route_query), _lib.ptr(postings), int(posting_rows),
         segs.view(), shortlist_k,

@@ -441,6 +441,39 @@ int gofann_rabitq_posting_scan_segments(gofann_ctx* ctx, const gofann_rabitq_vie
                                         const float* posting_ranges, uint32_t* out_ids,
                                         float* out_dists, uint32_t* pass_counts);
 
+/* ---- label-shared posting scan: no counterpart in the reference, which
+ * scans every label posting route by route (the label-posting scan of
+ * backend_rabitq.cu:5494-5682, which gofann_rabitq_posting_scan_segments
+ * restates).  The segments of a plan that scan the same posting rows (the
+ * routes of one label) are listed together in a share plan: item i covers
+ * posting rows [item_offsets[i], + item_sizes[i]) for the plan segments
+ * item_slots[item_begin[i] .. item_begin[i+1]) (at most 16 per item, each
+ * with exactly that offset and size).  One workgroup per item reads the
+ * rows' posting-order columns once and filters and scores them for every
+ * route of the item.  Takes posting_codes, posting_aux and posting_slab
+ * (posting_ranges optional), shortlist_k <= 128 and padded_dim <= 1024
+ * (GOFANN_ERR_UNSUPPORTED otherwise); every output equals
+ * gofann_rabitq_posting_scan_segments' for the same plan, bit for bit. */
+typedef struct {
+    const uint64_t* item_offsets; /* [items] */
+    const uint64_t* item_sizes;   /* [items] */
+    const uint32_t* item_begin;   /* [items + 1] into item_slots */
+    const uint32_t* item_slots;   /* plan segment indices */
+    uint32_t items;
+} gofann_posting_share;
+
+int gofann_rabitq_posting_scan_shared(gofann_ctx* ctx, const gofann_rabitq_view* rq,
+                                      const gofann_rabitq_queries* prepared,
+                                      const gofann_predicate_view* predicate,
+                                      const uint32_t* route_query,
+                                      const uint32_t* posting_sample_ids, uint64_t posting_rows,
+                                      const gofann_posting_segments* segments,
+                                      const gofann_posting_share* share, int shortlist_k,
+                                      const uint8_t* posting_codes, const uint32_t* posting_aux,
+                                      const uint32_t* posting_slab,
+                                      const float* posting_ranges, uint32_t* out_ids,
+                                      float* out_dists, uint32_t* pass_counts);
+
 /* ---- exact rerank on the GPU: per route, unique valid candidates of the
  * shortlist, exact L2 against base[samples][dim] (u8 / f32 / f16 with f32
  * queries for f32 and f16, u8 queries for u8), top-k by (distance, id). */

@@ -318,6 +318,56 @@ def test_rabitq_posting_scan_segments_matches_oracle(gpu_ctx, cworld, target, co
             assert cols.ranges[r].item() == wl.base_ranges[s, 0]
 
 
+_SHARE_CODES = {}
+
+
+# The label-shared scan (one workgroup per label segment, a wave per route):
+# P 128 and 512 (one or four code vectors per row), segments cut small,
+# across tile boundaries (700 rows) and whole; shortlists of 40 and 100.
+@pytest.mark.parametrize("P", [128, 512])
+@pytest.mark.parametrize("target", [97, 700, 1 << 20])
+@pytest.mark.parametrize("k", [40, 100])
+def test_rabitq_posting_scan_shared_matches_oracle(gpu_ctx, cworld, P, target, k):
+    from gofann_amd import range_posting as rp
+    wl, li, routes, _rot, _codes, _fac, _aid, _anchors, _P = cworld
+    say("posting scan shared P", P, "target", target, "k", k)
+    if P not in _SHARE_CODES:
+        rot = gi.random_rotation(wl.dim, P, 33005 + P, "cpu")
+        _SHARE_CODES[P] = (rot,) + tuple(gi.rabitq_encode(wl.base, rot, wl.centroids))
+    rot, codes, fac, aid, anchors = _SHARE_CODES[P]
+    dev, rv = _rviews((wl, li, None, rot, codes, fac, aid, anchors, P))
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rs = gp._routeset(routes, li)
+    n = rs.count
+    off = np.array([li.posting_offset[r[1]] for r in routes], np.uint32)
+    size = np.array([li.posting_offset[r[1] + 1] - li.posting_offset[r[1]] for r in routes],
+                    np.uint32)
+    pred = po.PredicateArrays.from_plan(rs.predicate, li, base_ranges=wl.base_ranges)
+    oi, od, opass = po.posting_scan_rabitq(
+        pred, codes.numpy(), fac.numpy(), aid.numpy().astype(np.uint32),
+        out["q8"].cpu().numpy(), out["scale"].cpu().numpy(), out["k1"].cpu().numpy(),
+        out["cd"].cpu().numpy(), rs.route_query, li.posting_ids, off, size, k)
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+    pv = dr.predicate_view(dg, 0.0, False)
+    total = int(li.posting_offset[-1])
+    plan = rp.segment_plan(np.arange(n), off.astype(np.uint64), size.astype(np.uint64), target)
+    segs = rp.DeviceSegments(plan)
+    sp = rp.share_plan(plan)
+    assert sp.items < plan.count  # segments of one label share items
+    share = rp.DeviceShare(sp)
+    rows = rp.PostingRows(gpu_ctx, rv, dg.posting_ids, total)
+    cols = rp.PostingPredicateColumns(gpu_ctx, pv, dg.posting_ids, total)
+    ids, dists, passes = rp.rabitq_posting_scan_segments(
+        gpu_ctx, rv, rq, pv, dr.route_query, dg.posting_ids, total, segs, k, rows=rows,
+        cols=cols, share=share)
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(ids).reshape(n, k), oi)
+    assert np.array_equal(dists.cpu().numpy().reshape(n, k).view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(as_u32(passes), opass)
+    assert (oi[:, 0] != U32MAX).sum() > n // 2 and opass.max() > 0
+
+
 def test_streamed_host_rerank_matches_direct(gpu_ctx, rworld):
     """RaBitQ traversal in route chunks with each chunk's shortlist streamed
     to the host rerank pool (search.StreamedRerank): the chunked shortlists

@@ -373,3 +373,32 @@ def test_oracle_range_scan_clipping():
     bi, _, _ = _run_scan(cs, routes, cs["offsets"], cs["sizes"], k, base_rows=lim)
     assert np.all((bi == U32MAX) | (bi < lim))
     assert full_p[0] == 0 and np.all(full_i[0] == U32MAX)   # no active range
+
+
+def test_share_plan_groups_segments_that_scan_the_same_rows():
+    """share_plan: every plan segment lands in exactly one item; an item's
+    segments scan the same rows (equal offset and size); at most 16 per
+    item; heavier items (rows x segments) first."""
+    from gofann_amd import range_posting as rp
+    rng = np.random.default_rng(5)
+    # 40 routes over 7 labels of different posting sizes, cut at 300 rows
+    lab_off = np.array([0, 50, 1250, 1260, 4000, 4001, 9000, 9500], np.uint64)
+    labels = rng.choice([0, 2, 3, 4, 5, 6], 40)
+    labels[:20] = 1  # one label (1200 rows, 4 segments) scanned by 20 routes
+    off = lab_off[labels]
+    size = lab_off[labels + 1] - lab_off[labels]
+    plan = rp.segment_plan(np.arange(40), off, size, 300)
+    sp = rp.share_plan(plan)
+    assert sp.begin[0] == 0 and sp.begin[-1] == plan.count
+    assert np.array_equal(np.sort(sp.slots), np.arange(plan.count))
+    counts = np.diff(sp.begin.astype(np.int64))
+    assert counts.min() >= 1 and counts.max() <= rp.SHARE_ROUTES
+    for i in range(sp.items):
+        sl = sp.slots[sp.begin[i]:sp.begin[i + 1]]
+        assert np.all(plan.offsets[sl] == sp.offsets[i]) and np.all(plan.sizes[sl] == sp.sizes[i])
+    w = sp.sizes.astype(np.float64) * counts
+    assert np.all(np.diff(w) <= 0)
+    # per segment of the shared label, its 20 routes split into items of 16 and 4
+    big = [i for i in range(sp.items) if lab_off[1] <= sp.offsets[i] < lab_off[2]]
+    assert sorted(counts[big].tolist()) == [4] * 4 + [16] * 4
+    assert sorted(set(sp.offsets[big].tolist())) == [50, 350, 650, 950]
