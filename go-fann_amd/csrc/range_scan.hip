@@ -748,6 +748,82 @@ struct ShareScanArgs {
     uint32_t* pass_counts;
 };
 
+// A route predicate of one clause with at most 3 label and 2 range atoms,
+// held in registers for the row loop (the clause walk of slab_pred_matches,
+// unrolled); other predicates keep the general walk.
+struct ShortClause {
+    bool simple;
+    int nl, nr;
+    uint32_t h[3];
+    gofann_range_atom r[2];
+};
+
+__device__ __forceinline__ ShortClause short_clause(const gofann_predicate_view& v, uint32_t route)
+{
+    ShortClause c{};
+    c.simple = false;
+    if (v.csr_offsets == nullptr) return c;
+    uint32_t lb, le, rb = 0, re = 0;
+    if (v.clauses) {
+        if (v.route_offsets[route + 1] - v.route_offsets[route] != 1) return c;
+        const gofann_clause cl = v.clauses[v.route_offsets[route]];
+        lb = cl.label_begin;
+        le = cl.label_end;
+        rb = cl.range_begin;
+        re = cl.range_end;
+    } else {
+        lb = v.route_offsets[route];
+        le = v.route_offsets[route + 1];
+    }
+    if (le - lb > 3 || re - rb > 2) return c;
+    c.nl = static_cast<int>(le - lb);
+    c.nr = static_cast<int>(re - rb);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) c.h[i] = i < c.nl ? v.route_handles[lb + i] : 0u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (i < c.nr) c.r[i] = v.ranges[rb + i];
+    c.simple = true;
+    return c;
+}
+
+// slab_pred_matches for a ShortClause route (same label scans and range
+// tests, in the same order of evaluation results).
+__device__ __forceinline__ bool short_clause_matches(const gofann_predicate_view& v,
+                                                     const ShortClause& c, uint32_t sample,
+                                                     const uint4& slab, const float* prange,
+                                                     float r0)
+{
+    if (sample >= v.rows) return false;
+    const uint32_t n = slab_count(slab);
+    bool pass = true;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (i >= c.nl) break;
+        bool hit = false;  // the first label >= handle decides
+        for (uint32_t k = 0; k < n; ++k) {
+            const uint32_t label = slab_label(slab, k);
+            if (label >= c.h[i]) {
+                hit = label == c.h[i];
+                break;
+            }
+        }
+        pass = pass && hit;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (i >= c.nr) break;
+        const gofann_range_atom at = c.r[i];
+        pass = pass && v.base_ranges != nullptr && at.dimension < v.range_stride &&
+               range_matches(at.mode, at.lower, at.upper,
+                             !prange ? v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
+                                                     at.dimension]
+                             : v.range_stride == 1 ? r0
+                                                   : prange[at.dimension]);
+    }
+    return pass;
+}
+
 template <int V>
 __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareScanArgs a,
                                                                         RabitqScanScorer sc)
@@ -824,6 +900,7 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             const uint32_t route = a.seg_route[a.item_slots[first + q]];
             const uint32_t query = a.route_query[route];
             const bool enabled = pred_enabled(a.pred, route);
+            const ShortClause sclause = enabled ? short_clause(a.pred, route) : ShortClause{};
             const float scale = sc.q_scale[query];
             const float k1 = sc.q_k1[query];
             const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
@@ -914,8 +991,10 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                             const float* prange = a.pranges && a.pred.range_stride > 0
                                                       ? a.pranges + j * a.pred.range_stride
                                                       : nullptr;
-                            ok = slab_pred_matches(a.pred, route, s, slab, prange,
-                                                   r0_tile ? t_r0[r] : 0.0f);
+                            const float rv = r0_tile ? t_r0[r] : 0.0f;
+                            ok = sclause.simple
+                                     ? short_clause_matches(a.pred, sclause, s, slab, prange, rv)
+                                     : slab_pred_matches(a.pred, route, s, slab, prange, rv);
                         } else {
                             PredCounters pc{0, 0};
                             ok = pred_matches(a.pred, route, s, pc);

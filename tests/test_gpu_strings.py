@@ -112,3 +112,13 @@ def test_c5_routes_match_oracle(gpu_ctx, c5):
     assert np.array_equal(pd.cpu().numpy().view(np.uint32), qd.view(np.uint32))
     assert np.array_equal(pp.cpu().numpy().view(np.uint32), qp)
     assert (qi[:, 0] != U32MAX).sum() > m // 2
+    # the label-shared scan (the routes of a label share each segment's rows)
+    if W <= 128:
+        share = rp.DeviceShare(rp.share_plan(segs.plan))
+        si, sd, spp = rp.rabitq_posting_scan_segments(gpu_ctx, rv, rq, pv, dp.route_query,
+                                                      dg.posting_ids, total, segs, W, rows=rows,
+                                                      cols=cols, share=share)
+        torch.cuda.synchronize()
+        assert np.array_equal(si.cpu().numpy().view(np.uint32), qi)
+        assert np.array_equal(sd.cpu().numpy().view(np.uint32), qd.view(np.uint32))
+        assert np.array_equal(spp.cpu().numpy().view(np.uint32), qp)
