@@ -720,7 +720,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
 // k least (distance, id) pairs of its passing rows and its pass count --
 // the group kernel's output for that segment, bit for bit.
 // ---------------------------------------------------------------------------
-constexpr int kShareTile = 1024;          // rows per LDS tile
+constexpr int kShareTile = 512;           // rows per LDS tile
 constexpr int kShareRoutesPerWave = 4;
 constexpr int kShareRoutes = kShareRoutesPerWave * (kScanThreads / kWave);  // 16 per item
 constexpr int kShareMaxKp = 128;          // shortlist_k <= 128
