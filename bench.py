@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--queries", type=int, default=100_000)
     ap.add_argument("--gt-queries", type=int, default=2000)
     ap.add_argument("--queue", type=int, default=0, help="beam width; 0 = ladder search")
-    ap.add_argument("--ladder", default="64,96,128,160,192,256,384")
+    ap.add_argument("--ladder", default="64,96,112,128,160,192,256,384")
     ap.add_argument("--target-recall", type=float, default=0.90)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -76,7 +76,7 @@ def parse():
     ap.add_argument("--n-c4", type=int, default=100_000_000)
     ap.add_argument("--queries-c4", type=int, default=10_000)
     ap.add_argument("--gt-queries-c4", type=int, default=1000)
-    ap.add_argument("--c4-ladder", default="16,32,64,96,128,192,256,384,448,512,768,1024")
+    ap.add_argument("--c4-ladder", default="16,32,64,96,128,192,256,320,384,416,448,512,768,1024")
     ap.add_argument("--c4-coarse-ladder", default="16,24,32,48,64,96,128,192,256,384")
     ap.add_argument("--c4-local", type=int, default=8,
                     help="in-bucket links per row of the C4 graphs (the rest are drawn)")
@@ -99,7 +99,7 @@ def parse():
     ap.add_argument("--n-c3", type=int, default=2_700_000)
     ap.add_argument("--queries-c3", type=int, default=10_000)
     ap.add_argument("--gt-queries-c3", type=int, default=999)
-    ap.add_argument("--c3-ladder", default="32,48,64,96,128,192,256,384,512")
+    ap.add_argument("--c3-ladder", default="32,48,64,96,128,192,256,320,384,448,512")
     ap.add_argument("--c3-local", type=int, default=24,
                     help="in-bucket links per row of the C3 graph (the rest are drawn)")
     ap.add_argument("--c3-scan-rows", type=int, default=20_000,
@@ -114,7 +114,7 @@ def parse():
                     help="skip the extra rows whose routes start at coarse-quantizer entries")
     ap.add_argument("--no-exact-route", action="store_true",
                     help="skip the full-GPU exact route measurement")
-    ap.add_argument("--exact-ladder", default="32,48,64,80,96,128,192,256",
+    ap.add_argument("--exact-ladder", default="32,48,64,72,80,96,128,192,256",
                     help="beam widths tried for the exact route")
     ap.add_argument("--rerank-threads", type=int, default=16,
                     help="host rerank workers (the GPU box's CPU share is 16 threads)")
