@@ -728,6 +728,37 @@ def main_c1(args):
 # ---------------------------------------------------------------------------
 # C3: 2.7M x 4096 fp32, one-bit RaBitQ, range predicates (--config c3).
 # ---------------------------------------------------------------------------
+def graph_classes(pipe, qs, start):
+    """A RaBitQ pipeline's graph routes, every class at its beam.  Adjacent
+    classes with one beam are one launch; classes with different beams run
+    concurrently, each on its own stream and context (its own scratch), so no
+    launch of a small class leaves most of the chip idle.  Every route's
+    results are those of a launch of its class alone."""
+    runs = []
+    for (lo, hi), q in zip(pipe.classes, qs):
+        if hi <= lo:
+            continue
+        if runs and runs[-1][0] == q and runs[-1][2] == lo:
+            runs[-1][2] = hi
+        else:
+            runs.append([q, lo, hi])
+    if len(runs) <= 1 or getattr(pipe, "serial_classes", False):
+        for q, lo, hi in runs:
+            pipe._graph(q, start, lo, hi)
+        return
+    torch = pipe.torch
+    main = torch.cuda.current_stream()
+    if len(getattr(pipe, "_class_streams", [])) < len(runs):
+        pipe._class_streams = [torch.cuda.Stream() for _ in runs]
+        pipe._class_ctx = [pipe.L.Context(0) for _ in runs]
+    for (q, lo, hi), st, cx in zip(runs, pipe._class_streams, pipe._class_ctx):
+        st.wait_stream(main)
+        cx.bind_stream(st)
+        pipe._graph(q, start, lo, hi, ctx=cx)
+    for st in pipe._class_streams[: len(runs)]:
+        main.wait_stream(st)
+
+
 def rabitq_traversal_bytes(st: np.ndarray, degree: int, code_bytes: int,
                            neighbor_samples: bool = False) -> float:
     """Bytes the RaBitQ traversal must move: the adjacency row (and with a
@@ -886,9 +917,7 @@ class RabitqRangePipeline:
         if timed:
             ev[1].record()
         qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
-        for (lo, hi), q in zip(self.classes, qs):
-            if hi > lo:
-                self._graph(q, start, lo, hi)
+        graph_classes(self, qs, start)
         if timed:
             ev[2].record()
         self._scan()
@@ -920,9 +949,11 @@ class RabitqRangePipeline:
                                     out=self.seed_buf)
         return None
 
-    def _graph(self, q, start, lo, hi):
-        """RaBitQ traversal of graph routes [lo, hi) at beam q."""
-        L, gs, ctx = self.L, self.gs, self.ctx
+    def _graph(self, q, start, lo, hi, ctx=None):
+        """RaBitQ traversal of graph routes [lo, hi) at beam q (on `ctx`'s
+        stream; the pipeline's context by default)."""
+        L, gs = self.L, self.gs
+        ctx = ctx or self.ctx
         prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
         ctx.check(ctx.lib.gofann_rabitq_search(
             ctx.handle, self.rv, self.rq, self.dg.view(),
@@ -1368,9 +1399,7 @@ class RabitqLabelPipeline:
         if timed:
             ev[1].record()
         qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
-        for (lo, hi), q in zip(self.classes, qs):
-            if hi > lo:
-                self._graph(q, start, lo, hi)
+        graph_classes(self, qs, start)
         if timed:
             ev[2].record()
         self._scan()
@@ -1402,9 +1431,11 @@ class RabitqLabelPipeline:
                                     out=self.seed_buf)
         return None
 
-    def _graph(self, q, start, lo, hi):
-        """RaBitQ traversal of graph routes [lo, hi) at beam q."""
-        L, gs, ctx = self.L, self.gs, self.ctx
+    def _graph(self, q, start, lo, hi, ctx=None):
+        """RaBitQ traversal of graph routes [lo, hi) at beam q (on `ctx`'s
+        stream; the pipeline's context by default)."""
+        L, gs = self.L, self.gs
+        ctx = ctx or self.ctx
         prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
         ctx.check(ctx.lib.gofann_rabitq_search(
             ctx.handle, self.rv, self.rq, self.dg.view(),
