@@ -147,6 +147,8 @@ __global__ __launch_bounds__(kRerankThreads) void exact_rerank_kernel(RerankArgs
         if (a.base_elem == GOFANN_ELEM_U8) {
             const uint8_t* b = static_cast<const uint8_t*>(a.base) + static_cast<size_t>(s) * a.dim;
             const uint8_t* qq = static_cast<const uint8_t*>(a.queries) + static_cast<size_t>(q) * a.dim;
+            // unrolled: the loads of 8 steps in flight, the sum in d order
+#pragma unroll 8
             for (uint32_t d = lane; d < a.dim; d += kWave) {
                 const float diff = static_cast<float>(qq[d]) - static_cast<float>(b[d]);
                 acc = fmaf(diff, diff, acc);
@@ -154,6 +156,8 @@ __global__ __launch_bounds__(kRerankThreads) void exact_rerank_kernel(RerankArgs
         } else if (a.base_elem == GOFANN_ELEM_F32) {
             const float* b = static_cast<const float*>(a.base) + static_cast<size_t>(s) * a.dim;
             const float* qq = static_cast<const float*>(a.queries) + static_cast<size_t>(q) * a.dim;
+            // unrolled: the loads of 8 steps in flight, the sum in d order
+#pragma unroll 8
             for (uint32_t d = lane; d < a.dim; d += kWave) {
                 const float diff = qq[d] - b[d];
                 acc = fmaf(diff, diff, acc);
@@ -161,6 +165,8 @@ __global__ __launch_bounds__(kRerankThreads) void exact_rerank_kernel(RerankArgs
         } else {
             const __half* b = static_cast<const __half*>(a.base) + static_cast<size_t>(s) * a.dim;
             const float* qq = static_cast<const float*>(a.queries) + static_cast<size_t>(q) * a.dim;
+            // unrolled: the loads of 8 steps in flight, the sum in d order
+#pragma unroll 8
             for (uint32_t d = lane; d < a.dim; d += kWave) {
                 const float diff = qq[d] - __half2float(b[d]);
                 acc = fmaf(diff, diff, acc);
