@@ -92,6 +92,8 @@ def parse():
     ap.add_argument("--no-posting-share", action="store_true",
                     help="label postings: scan route by route instead of sharing each label "
                          "segment's rows among its routes")
+    ap.add_argument("--posting-share-routes", type=int, default=16,
+                    help="label-shared scan: routes per workgroup item (at most 16)")
     ap.add_argument("--posting-segment-rows", type=int, default=32768,
                     help="rows per segment of the segmented label-posting scan")
     ap.add_argument("--c4-threshold", type=int, default=50_000,
@@ -1257,7 +1259,8 @@ class RabitqLabelPipeline:
     shortlists, and the per-query merge."""
 
     def __init__(self, ctx, wl, li, rq, torch, width=100, posting_layout="columns",
-                 segment_rows=32768, neighbor_samples=True, posting_share=True):
+                 segment_rows=32768, neighbor_samples=True, posting_share=True,
+                 share_routes=16):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
         from gofann_amd import range_posting as rp
@@ -1356,7 +1359,7 @@ class RabitqLabelPipeline:
             # workgroups to fill the chip.
             reuse = self.post_rows_total / max(self.scan_total, 1)
             if posting_share and reuse >= 4.0 and width <= 128 and self.P <= 1024:
-                sp = self.rp.share_plan(self.scan_segs.plan)
+                sp = self.rp.share_plan(self.scan_segs.plan, share_routes)
                 self.scan_share = self.rp.DeviceShare(sp)
                 log(f"label postings shared (rows re-read {reuse:.1f}x): {sp.items} items for "
                     f"{plan_count(self.scan_segs)} segments")
@@ -1670,7 +1673,8 @@ def run_c4(args, torch, ctx, world=None) -> dict:
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
                                segment_rows=args.posting_segment_rows,
                                neighbor_samples=not args.no_neighbor_samples,
-                               posting_share=not args.no_posting_share)
+                               posting_share=not args.no_posting_share,
+                               share_routes=args.posting_share_routes)
     pipe.P, pipe.li = rq["P"], li
     log(f"C4 routes: {pipe.ng} graph ({pipe.n_eq} equality, {pipe.interior} interior "
         f"intervals), {pipe.np_} label-posting scans ({pipe.post_rows_total} rows), planned "
@@ -1800,7 +1804,8 @@ def run_c5(args, torch, ctx, world=None) -> dict:
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
                                segment_rows=args.posting_segment_rows,
                                neighbor_samples=not args.no_neighbor_samples,
-                               posting_share=not args.no_posting_share)
+                               posting_share=not args.no_posting_share,
+                               share_routes=args.posting_share_routes)
     pipe.P, pipe.li = rq["P"], li
     types = wl.meta["query_types"]
     log(f"C5 routes: {pipe.ng} graph, {pipe.np_} label-posting scans ({pipe.post_rows_total} "
