@@ -730,12 +730,16 @@ def main_c1(args):
 # ---------------------------------------------------------------------------
 # C3: 2.7M x 4096 fp32, one-bit RaBitQ, range predicates (--config c3).
 # ---------------------------------------------------------------------------
-def graph_classes(pipe, qs, start):
-    """A RaBitQ pipeline's graph routes, every class at its beam.  Adjacent
-    classes with one beam are one launch; classes with different beams run
-    concurrently, each on its own stream and context (its own scratch), so no
-    launch of a small class leaves most of the chip idle.  Every route's
-    results are those of a launch of its class alone."""
+def graph_classes(pipe, qs, start, ends=None):
+    """A RaBitQ pipeline's graph routes, every class at its beam, launched
+    on the class streams (the caller joins them; `ends[i]` is recorded on
+    the i-th stream used after its launch).  Adjacent classes with one beam
+    are one launch; classes with different beams run concurrently, each on
+    its own stream and context (its own scratch), so no launch of a small
+    class leaves most of the chip idle, and the caller can overlap other
+    work on its own stream.  Every route's results are those of a launch of
+    its class alone.  Returns the streams used ([] when pipe.serial_classes
+    puts every launch on the current stream)."""
     runs = []
     for (lo, hi), q in zip(pipe.classes, qs):
         if hi <= lo:
@@ -744,21 +748,51 @@ def graph_classes(pipe, qs, start):
             runs[-1][2] = hi
         else:
             runs.append([q, lo, hi])
-    if len(runs) <= 1 or getattr(pipe, "serial_classes", False):
+    if getattr(pipe, "serial_classes", False):
         for q, lo, hi in runs:
             pipe._graph(q, start, lo, hi)
-        return
+        return []
     torch = pipe.torch
     main = torch.cuda.current_stream()
-    if len(getattr(pipe, "_class_streams", [])) < len(runs):
-        pipe._class_streams = [torch.cuda.Stream() for _ in runs]
-        pipe._class_ctx = [pipe.L.Context(0) for _ in runs]
-    for (q, lo, hi), st, cx in zip(runs, pipe._class_streams, pipe._class_ctx):
+    streams, ctxs = class_pool(torch, pipe.L)
+    used = []
+    for i, (q, lo, hi) in enumerate(runs):
+        st, cx = streams[i % len(streams)], ctxs[i % len(ctxs)]
         st.wait_stream(main)
         cx.bind_stream(st)
         pipe._graph(q, start, lo, hi, ctx=cx)
-    for st in pipe._class_streams[: len(runs)]:
-        main.wait_stream(st)
+        if ends is not None and i < len(ends):
+            ends[i].record(st)
+        used.append(st)
+    return used
+
+
+def stage_times(pipe, scan_name):
+    """Stage times (HIP events) of a timed RaBitQ step: the traversal from
+    the end of preparation to the last class stream's end, the scan on the
+    main stream (it overlaps the traversal), `graph_and_scan` to the join,
+    then rerank and merge."""
+    e = pipe.ev
+    ends = pipe.ev_class[: pipe.n_class_used]
+    trav = max((e[1].elapsed_time(x) for x in ends), default=e[1].elapsed_time(e[2]))
+    return {"prep": e[0].elapsed_time(e[1]), "traversal": trav,
+            scan_name: e[2].elapsed_time(e[3]),
+            "graph_and_scan": e[1].elapsed_time(pipe.ev_join),
+            "rerank": pipe.ev_join.elapsed_time(e[4]), "merge": e[4].elapsed_time(e[5])}
+
+
+_CLASS_POOL = None
+
+
+def class_pool(torch, L, n=3):
+    """One set of class streams and contexts for the process, shared by
+    every pipeline (the default run creates it first): a process has few
+    hardware queues (GPU_MAX_HW_QUEUES), and streams created later may share
+    one and serialize."""
+    global _CLASS_POOL
+    if _CLASS_POOL is None:
+        _CLASS_POOL = ([torch.cuda.Stream() for _ in range(n)], [L.Context(0) for _ in range(n)])
+    return _CLASS_POOL
 
 
 def rabitq_traversal_bytes(st: np.ndarray, degree: int, code_bytes: int,
@@ -906,6 +940,9 @@ class RabitqRangePipeline:
         off, order = gs.query_route_csr(r2q, nq)
         self.q_off, self.q_routes = gs.u32(off), gs.u32(order)
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        self.ev_class = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        self.ev_join = torch.cuda.Event(enable_timing=True)
+        self.n_class_used = 0
         self.seed_buf = self.dr.route_start.clone()
 
     def step(self, Q, timed=False):
@@ -919,12 +956,20 @@ class RabitqRangePipeline:
         if timed:
             ev[1].record()
         qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
-        graph_classes(self, qs, start)
+        # graph routes on the class streams, the posting scan overlapping
+        # them on this stream (disjoint output rows)
+        used = graph_classes(self, qs, start, self.ev_class if timed else None)
+        self.n_class_used = len(used)
         if timed:
             ev[2].record()
         self._scan()
         if timed:
             ev[3].record()
+        main = self.torch.cuda.current_stream()
+        for st in used:
+            main.wait_stream(st)
+        if timed:
+            self.ev_join.record()
         n = self.ng + self.np_
         fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
                                        self.sl_i, W, n, 10)
@@ -984,10 +1029,7 @@ class RabitqRangePipeline:
                     L.ptr(self.passes)))
 
     def stage_ms(self):
-        e = self.ev
-        return dict(prep=e[0].elapsed_time(e[1]), traversal=e[1].elapsed_time(e[2]),
-                    range_scan=e[2].elapsed_time(e[3]), rerank=e[3].elapsed_time(e[4]),
-                    merge=e[4].elapsed_time(e[5]))
+        return stage_times(self, "range_scan")
 
     def route_stats(self):
         return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
@@ -1349,6 +1391,9 @@ class RabitqLabelPipeline:
         off_q, order = gs.query_route_csr(r2q, nq)
         self.q_off, self.q_routes = gs.u32(off_q), gs.u32(order)
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        self.ev_class = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        self.ev_join = torch.cuda.Event(enable_timing=True)
+        self.n_class_used = 0
         self.seed_buf = self.dr.route_start.clone()
         self.posting_layout = posting_layout if self.np_ else "gather"
         self.scan_share = None
@@ -1402,12 +1447,20 @@ class RabitqLabelPipeline:
         if timed:
             ev[1].record()
         qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
-        graph_classes(self, qs, start)
+        # graph routes on the class streams, the posting scan overlapping
+        # them on this stream (disjoint output rows)
+        used = graph_classes(self, qs, start, self.ev_class if timed else None)
+        self.n_class_used = len(used)
         if timed:
             ev[2].record()
         self._scan()
         if timed:
             ev[3].record()
+        main = self.torch.cuda.current_stream()
+        for st in used:
+            main.wait_stream(st)
+        if timed:
+            self.ev_join.record()
         n = self.ng + self.np_
         fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
                                        self.sl_i, W, n, 10)
@@ -1463,10 +1516,7 @@ class RabitqLabelPipeline:
                 L.ptr(self.sl_d[self.ng * W:]), L.ptr(self.passes)))
 
     def stage_ms(self):
-        e = self.ev
-        return dict(prep=e[0].elapsed_time(e[1]), traversal=e[1].elapsed_time(e[2]),
-                    posting_scan=e[2].elapsed_time(e[3]), rerank=e[3].elapsed_time(e[4]),
-                    merge=e[4].elapsed_time(e[5]))
+        return stage_times(self, "posting_scan")
 
     def route_stats(self):
         return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
@@ -1517,7 +1567,16 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
     log(f"{label}: expansions per graph route: mean {E.mean():.1f}, p50 "
         f"{np.percentile(E, 50):.0f}, p99 {np.percentile(E, 99):.0f}; scored per route "
         f"{(st[:, 3].astype(np.float64).mean() if len(st) else 0):.1f}")
-    kern = kernels(pipe, st_ms, st)
+    # Kernel times from one more timed step with every launch on one stream
+    # (in the overlapped step a stage's events also span the time its kernel
+    # waits for CUs that the other stream holds).
+    pipe.serial_classes = True
+    pipe.step(chosen, timed=True)
+    torch.cuda.synchronize()
+    kst = pipe.stage_ms()
+    pipe.serial_classes = False
+    kst = {k: round(float(v), 3) for k, v in kst.items()}
+    kern = kernels(pipe, kst, st)
     per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
                "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None,
                **(v[2] if len(v) > 2 else {})}
@@ -1525,12 +1584,12 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
     top = max(kern, key=lambda k: kern[k][0])
     ach = kern[top][1] / (kern[top][0] / 1000.0) / 1e9
     log(f"{label}: step {ms:.1f} ms, stages {st_ms}, recall {rec:.4f} {by_class}, "
-        f"beams {dict(zip([n for n, _ in class_gt], chosen))}")
+        f"beams {dict(zip([n for n, _ in class_gt], chosen))}; kernel stages (one stream) {kst}")
     return {"qps": round(nq / (ms / 1000.0), 1), "ms_per_step": round(ms, 3),
             "queue_by_class": dict(zip([n for n, _ in class_gt], chosen)),
             "recall_at_10": round(rec, 4), "recall_by_class": by_class,
             "expansions_per_route": round(float(E.mean()), 1), "stage_ms": st_ms,
-            "kernels": per, "placement": pipe.ctx.last_placement(),
+            "kernel_stage_ms": kst, "kernels": per, "placement": pipe.ctx.last_placement(),
             "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
                          "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5), "traffic": None,
                          "kernel": top, "kernel_ms": kern[top][0],
@@ -1637,9 +1696,20 @@ def c4_kernels(pipe, st_ms, st):
              if st_ms["posting_scan"] > 0 else None, "layout": pipe.posting_layout,
              "shared": pipe.scan_share is not None}
     rb = (pipe.ng + pipe.np_) * pipe.W * (wl.dim * 2 + 4) + 0.0
+    scan_name = "range_scan_group_kernel+segment_merge_kernel (label postings)"
+    if pipe.scan_share is not None:
+        # the label-shared scan reads each item's rows once (sample id,
+        # label slab, range row) and, per passing row of a route, its code
+        # row, 16-byte aux row and g[anchor]; the per-route figure above
+        # counts every route's read of a row
+        sp = pipe.scan_share.sp
+        sb = float(sp.sizes.astype(np.float64).sum()) * (4 + pred) + passed * (P // 8 + 16 + 4)
+        extra = dict(extra, per_route_formula_bytes=pb,
+                     item_rows=int(sp.sizes.astype(np.int64).sum()), items=sp.items)
+        pb = sb
+        scan_name = "label_share_scan_kernel+segment_merge_kernel (label postings)"
     return {"traversal_kernel<RabitqScorer>": (st_ms["traversal"], tb),
-            "range_scan_group_kernel+segment_merge_kernel (label postings)":
-                (st_ms["posting_scan"], pb, extra),
+            scan_name: (st_ms["posting_scan"], pb, extra),
             "exact_rerank_kernel (f16)": (st_ms["rerank"], rb)}
 
 
@@ -1913,6 +1983,7 @@ def main():
     gt = ground_truth(wl, li, torch, args.gt_queries)
     log(f"ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     ctx = _lib.Context(0)
+    class_pool(torch, _lib)  # before any other stream
     inline = not args.no_inline_exact
     pipe = Pipeline(ctx, wl, li, table, codes, pl, torch, inline=inline,
                     table_mode=args.table_mode, hash_mode=args.hash_mode,
