@@ -121,9 +121,10 @@ __device__ __forceinline__ uint32_t l2_u8_row(const uint8_t* row, const uint32_t
     if ((dim & 15u) == 0) {
         const uint4* r4 = reinterpret_cast<const uint4*>(row);
         const uint4* q4 = reinterpret_cast<const uint4*>(q);
-        // four 16-byte chunks per round trip: two buy a sixth wave per SIMD
-        // but double the round trips, six cost a wave; both ran slower
-#pragma unroll 4
+        // three 16-byte chunks per round trip: at the 5-wave register
+        // budget four spill two 16-byte values per step (52.6 against 55.3
+        // ms at C2, Q = 80), two double the round trips (54.9 ms)
+#pragma unroll 3
         for (uint32_t i = 0; i < dim / 16; ++i) {
             const uint4 b = r4[i];
             const uint4 w = q4[i];
