@@ -79,11 +79,13 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_FIXED_ROWS 0
 #endif
 
-// Minimum waves per SIMD the kernel is compiled for (register budget).  5
-// holds the LDS-frontier kernels to 96 VGPRs (20 routes per CU instead of
-// 16, a few spills in cold paths): 55.5 against 57.0 ms at C2, Q = 80.
+// Minimum waves per SIMD the kernel is compiled for (register budget).  6
+// holds the kernels to 80 VGPRs, 24 routes per CU; the values it spills are
+// reloaded once per step, outside the row loop.  At C2, Q = 80: 50.8 ms,
+// against 52.6 at 5 waves (96 VGPRs, no spills) and 57.8 at 7 (29 spills,
+// the visited table leaves LDS).
 #ifndef GOFANN_EXACT_MIN_WAVES
-#define GOFANN_EXACT_MIN_WAVES 5
+#define GOFANN_EXACT_MIN_WAVES 6
 #endif
 
 // Most registers per lane a register frontier may use (Q + 2 <= 64 x this).
@@ -94,6 +96,16 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #ifndef GOFANN_EXACT_MAX_REGS
 #define GOFANN_EXACT_MAX_REGS 1
 #endif
+
+// 16-byte row chunks loaded per memory round trip in the any-dim row loop.
+// Three: at 5 waves four spill two 16-byte values per step (55.3 against
+// 52.6 ms at C2, Q = 80) and two add round trips (54.9 ms); at 6 waves one
+// takes 67.8 ms, two 52.8, three 50.8 and six 61.2.
+#ifndef GOFANN_EXACT_ROW_UNROLL
+#define GOFANN_EXACT_ROW_UNROLL 3
+#endif
+#define GOFANN_PRAGMA(x) _Pragma(#x)
+#define GOFANN_UNROLL(n) GOFANN_PRAGMA(unroll n)
 
 struct ExactArgs {
     gofann_graph_view graph;
@@ -121,10 +133,7 @@ __device__ __forceinline__ uint32_t l2_u8_row(const uint8_t* row, const uint32_t
     if ((dim & 15u) == 0) {
         const uint4* r4 = reinterpret_cast<const uint4*>(row);
         const uint4* q4 = reinterpret_cast<const uint4*>(q);
-        // three 16-byte chunks per round trip: at the 5-wave register
-        // budget four spill two 16-byte values per step (52.6 against 55.3
-        // ms at C2, Q = 80), two double the round trips (54.9 ms)
-#pragma unroll 3
+        GOFANN_UNROLL(GOFANN_EXACT_ROW_UNROLL)
         for (uint32_t i = 0; i < dim / 16; ++i) {
             const uint4 b = r4[i];
             const uint4 w = q4[i];
