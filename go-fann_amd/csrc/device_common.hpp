@@ -115,6 +115,17 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask)
                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
 }
 
+// The lane id behind an empty asm statement.  A route loop that takes its
+// lane from here at the top of every step recomputes what it derives from
+// the lane (lane masks such as (1 << lane) - 1, per-lane addresses) where it
+// is used, instead of the compiler hoisting those values out of the loop and
+// holding them, or spilling them, for the whole route.
+__device__ __forceinline__ int opaque_lane(int lane)
+{
+    asm volatile("" : "+v"(lane));
+    return lane;
+}
+
 // ---------------------------------------------------------------------------
 // Visited set: native_visited_hash.cuh:10-60.  Observable semantics: an exact
 // set of label-local rows that stops accepting values once it holds 4096 of

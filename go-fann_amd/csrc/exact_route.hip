@@ -80,10 +80,9 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #endif
 
 // Minimum waves per SIMD the kernel is compiled for (register budget).  6
-// holds the kernels to 80 VGPRs, 24 routes per CU; the values it spills are
-// reloaded once per step, outside the row loop.  At C2, Q = 80: 50.8 ms,
-// against 52.6 at 5 waves (96 VGPRs, no spills) and 57.8 at 7 (29 spills,
-// the visited table leaves LDS).
+// holds the kernels to 80 VGPRs, 24 routes per CU, without spills (the lane
+// id is opaque per step).  At C2, Q = 80: 46.1 ms, against 49.0 at 5 waves
+// and 54.1 at 7 (the visited table leaves LDS).
 #ifndef GOFANN_EXACT_MIN_WAVES
 #define GOFANN_EXACT_MIN_WAVES 6
 #endif
@@ -97,15 +96,14 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_MAX_REGS 1
 #endif
 
-// 16-byte row chunks loaded per memory round trip in the any-dim row loop.
-// Three: at 5 waves four spill two 16-byte values per step (55.3 against
-// 52.6 ms at C2, Q = 80) and two add round trips (54.9 ms); at 6 waves one
-// takes 67.8 ms, two 52.8, three 50.8 and six 61.2.
+// 16-byte row chunks loaded per memory round trip in the any-dim row loop
+// of the LDS-frontier kernels.  At 6 waves, C2, Q = 80: three take 49.0 ms,
+// four 46.1, six 48.9, the whole row (twelve) 47.5.  The register-frontier
+// kernels take three: four spill 12 VGPRs there.
 #ifndef GOFANN_EXACT_ROW_UNROLL
-#define GOFANN_EXACT_ROW_UNROLL 3
+#define GOFANN_EXACT_ROW_UNROLL 4
 #endif
-#define GOFANN_PRAGMA(x) _Pragma(#x)
-#define GOFANN_UNROLL(n) GOFANN_PRAGMA(unroll n)
+constexpr int kExactRegsRowUnroll = 3;
 
 struct ExactArgs {
     gofann_graph_view graph;
@@ -125,7 +123,9 @@ struct ExactArgs {
     uint32_t off_hash;
 };
 
-// Squared L2 of a u8 row against the query held in LDS (q, |q|^2).
+// Squared L2 of a u8 row against the query held in LDS (q, |q|^2); kU
+// 16-byte chunks per memory round trip when dim is a multiple of 16.
+template <int kU>
 __device__ __forceinline__ uint32_t l2_u8_row(const uint8_t* row, const uint32_t* q,
                                               uint32_t dim, uint32_t qnorm)
 {
@@ -133,7 +133,7 @@ __device__ __forceinline__ uint32_t l2_u8_row(const uint8_t* row, const uint32_t
     if ((dim & 15u) == 0) {
         const uint4* r4 = reinterpret_cast<const uint4*>(row);
         const uint4* q4 = reinterpret_cast<const uint4*>(q);
-        GOFANN_UNROLL(GOFANN_EXACT_ROW_UNROLL)
+#pragma unroll kU
         for (uint32_t i = 0; i < dim / 16; ++i) {
             const uint4 b = r4[i];
             const uint4 w = q4[i];
@@ -503,6 +503,7 @@ __device__ __forceinline__ void load_node(const gofann_graph_view& g,
 template <int kVisited, int kC, int kRegs>
 __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel(ExactArgs a)
 {
+    constexpr int kRowUnroll = kRegs > 0 ? kExactRegsRowUnroll : GOFANN_EXACT_ROW_UNROLL;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ uint32_t s_row[kMaxDegree];
     __shared__ uint32_t s_samp[kMaxDegree];
@@ -571,7 +572,7 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
         if (s0 < a.samples) {
             const float d0 = bcast0f(
                 lane == 0 ? static_cast<float>(
-                                l2_u8_row(a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn))
+                                l2_u8_row<kRowUnroll>(a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn))
                           : 0.0f);
             const Entry kp = {d0, seed, d0, s0};
             if constexpr (kRegs > 0) {
@@ -604,7 +605,11 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
 
     uint32_t steps = 0, finished = 0;
     bool first_step = true;
+    const int wave_lane = lane;
     while (!done) {
+        // per step: lane-derived values are not held across steps (no spills
+        // at 6 waves; with the lane hoisted out of the loop, 10 VGPRs spilled)
+        const int lane = opaque_lane(wave_lane);
         if (a.params.max_steps != 0 && steps >= static_cast<uint32_t>(a.params.max_steps)) break;
 
         // One memory round for the neighbours (visited tests, sample ids) and
@@ -633,7 +638,7 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
             row_load<kC>(brow, keep, rb);
             d32 = row_dist<kC>(rb, qw, qn);
         } else {
-            d32 = keep ? l2_u8_row(brow, qw, a.dim, qn) : 0u;
+            d32 = keep ? l2_u8_row<kRowUnroll>(brow, qw, a.dim, qn) : 0u;
         }
         // The distance is complete here: the rows and query words are dead
         // before the filter below.

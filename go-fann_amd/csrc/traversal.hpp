@@ -44,7 +44,8 @@
 
 // Minimum waves per SIMD the traversal kernel is compiled for (register
 // budget: 4 waves -> at most 128 VGPRs; 5 spills the scorer state and is
-// slower: C4 193.5 against 149.2 ms).
+// slower: C4 193.5 against 149.2 ms; C2 PQ route 181.1 against 180.3 ms,
+// where the visited table also leaves LDS).
 #ifndef GOFANN_TRAVERSAL_MIN_WAVES
 #define GOFANN_TRAVERSAL_MIN_WAVES 4
 #endif
@@ -778,7 +779,12 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
     }
 
     int step = 0;
+    const int wave_lane = lane;
     while (step == 0 || heap_size > 1) {
+        // per step: lane-derived values are not held across steps (PqScorer<48>
+        // 111 VGPRs, RaBitQ 118-120, no spills; with the lane hoisted out of
+        // the loop both reach the 128-VGPR budget and spill)
+        const int lane = opaque_lane(wave_lane);
         const uint32_t now_local = now.second & ~kPoolUsed;
         ++step;
 
