@@ -1313,7 +1313,6 @@ class RabitqLabelPipeline:
         P = rq["P"]
         self.P = P
         cats, nint, amax = wl.meta["categories"], wl.meta["intervals"], wl.meta["attr_max"]
-        starts = [-(-(i * amax) // nint) for i in range(nint + 1)]  # ceil(i * amax / nint)
         graph_rows, post_rows = [], []
         self.interior = 0
         dnf = wl.meta.get("query_clauses")
@@ -1327,19 +1326,11 @@ class RabitqLabelPipeline:
                                                       clause_scans=True)
             graph_rows.sort(key=lambda r: (cls_of[types[r[0]]], r[1], r[0]))
             self.class_names = kinds
-        for q in range(nq if dnf is None else 0):
-            if wl.query_labels[q]:
-                lab = wl.query_labels[q][0]
-                (graph_rows if li.has_graph(lab) else post_rows).append((q, lab, [], []))
-                continue
-            (_, _, lo, hi), = wl.query_ranges[q]
-            i0 = int(lo) * nint // amax
-            i1 = (int(hi) - 1) * nint // amax
-            for i in range(i0, i1 + 1):
-                inside = starts[i] >= lo and starts[i + 1] <= hi
-                self.interior += int(inside)
-                graph_rows.append((q, cats + i, [], [] if inside else [(0, 3, lo, hi)]))
         if dnf is None:
+            # C4: equality queries on their label, range queries one route
+            # per attribute interval they overlap
+            graph_rows, post_rows, self.interior = gp.interval_route_rows(
+                li, wl.query_labels, wl.query_ranges, cats, nint, amax)
             # by (label, query): category routes (labels < cats) come first,
             # so the equality and range classes are two contiguous ranges
             graph_rows.sort(key=lambda r: (r[1], r[0]))

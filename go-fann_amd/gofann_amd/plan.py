@@ -163,6 +163,43 @@ def plan_queries(index, query_labels: list, query_ranges: list | None = None,
                     queries=queries, dual_ratio=dual_ratio)
 
 
+def interval_route_rows(index, query_labels: list, query_ranges: list, categories: int,
+                        intervals: int, attr_max: int):
+    """Route rows of a query set in which every query is either one
+    categorical equality or one range [lo, hi) (mode 3) over an integer
+    attribute in [0, attr_max), where each row also carries the interval
+    label categories + floor(attr * intervals / attr_max) (interval virtual
+    labels: scripts/laion/range_index.py:1-12):
+      * equality on label L: a graph route over L when L has a graph, else a
+        posting route;
+      * range: one graph route per interval label it overlaps -- the
+        finest-level pure-range cover (plan_pure_range_cover_labels,
+        dataloader.cpp:9204-9345, over a one-level layout) -- whose residual
+        is the range, except on an interval that lies inside [lo, hi), where
+        the range is entailed and the residual is empty.
+    Interval i holds the integers [ceil(i attr_max / intervals),
+    ceil((i + 1) attr_max / intervals)).  Rows are (query, label, residual
+    labels, residual ranges) in query order.  Returns (graph_rows, post_rows,
+    interior), interior = routes whose residual is empty because entailed."""
+    starts = [-(-(i * attr_max) // intervals) for i in range(intervals + 1)]
+    graph_rows, post_rows, interior = [], [], 0
+    for q, labels in enumerate(query_labels):
+        if labels:
+            lab = labels[0]
+            (graph_rows if index.has_graph(lab) else post_rows).append((q, lab, [], []))
+            continue
+        (dim, mode, lo, hi), = query_ranges[q]
+        if dim != 0 or mode != 3:
+            raise ValueError("interval routes take one [lo, hi) range on dimension 0")
+        i0 = int(lo) * intervals // attr_max
+        i1 = (int(hi) - 1) * intervals // attr_max
+        for i in range(i0, i1 + 1):
+            inside = starts[i] >= lo and starts[i + 1] <= hi
+            interior += int(inside)
+            graph_rows.append((q, categories + i, [], [] if inside else [(0, 3, lo, hi)]))
+    return graph_rows, post_rows, interior
+
+
 def dnf_route_rows(index, query_clauses: list, query_ranges: list | None = None,
                    dual_ratio: float = 1e30, clause_scans: bool = False,
                    with_clause: bool = False) -> tuple:
