@@ -89,8 +89,10 @@ PLACE = {"auto": (_lib.PLACE_AUTO, False), "lds-nsamp": (_lib.PLACE_LDS, True),
 
 
 @pytest.mark.parametrize("place", list(PLACE))
-# Q + 2 <= 64 keeps the frontier in registers, larger beams in LDS.
-@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (2, 80), (1, 128), (2, 300)])
+# Q + 2 <= 64 keeps the frontier in registers, larger beams in LDS; past
+# 512 slots (Q = 600) admission takes the serial lane-0 sifts.
+@pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (2, 80), (1, 128), (2, 300),
+                                    (2, 600)])
 @pytest.mark.parametrize("with_pred", [False, True])
 def test_exact_search_matches_oracle(gpu_ctx, eworld, place, mode, Q, with_pred):
     wl, li, rs = eworld

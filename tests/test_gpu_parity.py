@@ -249,8 +249,9 @@ def long_world():
 
 
 @pytest.mark.parametrize("place", list(PLACEMENTS))
-# all-tie frontiers of 258 and 402 slots (past 260, pairs 64.. have children)
-@pytest.mark.parametrize("Q", [256, 400])
+# all-tie frontiers of 258 and 402 slots (past 260, pairs 64.. have children);
+# 602 slots: past the wave-parallel frontier's 512, the serial lane-0 sifts
+@pytest.mark.parametrize("Q", [256, 400, 600])
 def test_pq_search_visited_fill_matches_oracle(gpu_ctx, long_world, place, Q):
     wl, li, pl, table, codes = long_world
     table_mode, hash_mode, nsamp, rec = PLACEMENTS[place]
