@@ -123,7 +123,10 @@ def parse():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with a 1 GiB fp32 negation (reads and writes 1 GiB) as the "
                          "copy kernel that calibrates FETCH_SIZE / WRITE_SIZE counters")
-    return ap.parse_args()
+    args = ap.parse_args()
+    if not 1 <= args.posting_share_routes <= 16:
+        ap.error("--posting-share-routes takes 1..16 (route slots per pass of the shared scan)")
+    return args
 
 
 def build_world(args, torch):

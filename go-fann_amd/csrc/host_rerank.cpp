@@ -331,9 +331,14 @@ int gofann_host_rerank_create(const void* base, int base_elem, uint32_t dim, uin
     hr->samples = samples;
     hr->queries = queries;
     hr->threads = threads == 0 ? 1 : threads;
-    {
-        // the reference's fp16 kernel choice (fp16_l2::select)
+    hr->fp16_kernel = kFp16Scalar;
+    if (base_elem == GOFANN_ELEM_F16) {
+        // the reference's fp16 kernel choice (fp16_l2::select), read only
+        // for fp16 rows as the reference reads it only when it opens an fp16
+        // source (dataloader.cpp:2132); the reference's own variable name is
+        // taken when this library's is unset
         const char* env = std::getenv("GOFANN_FP16_RERANK_KERNEL");
+        if (env == nullptr) env = std::getenv("GO_FANN_FP16_RERANK_KERNEL");
         const std::string req = env ? env : "auto";
         int k;
         if (req.empty() || req == "auto") {

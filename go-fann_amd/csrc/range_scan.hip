@@ -847,8 +847,8 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
     uint32_t* lst_id_all = reinterpret_cast<uint32_t*>(lst_d_all + kShareRoutes * kp);
     uint32_t* queue_all = lst_id_all + kShareRoutes * kp;
 
-    const uint32_t first = a.item_begin[item];
-    const int n_routes = static_cast<int>(a.item_begin[item + 1] - first);
+    const uint32_t first_all = a.item_begin[item];
+    const int n_all = static_cast<int>(a.item_begin[item + 1] - first_all);
     const uint64_t begin = a.item_offset[item];
     uint64_t count = a.item_size[item];
     if (begin > a.resident_rows)
@@ -856,173 +856,180 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
     else if (count > a.resident_rows - begin)
         count = a.resident_rows - begin;
 
-    // Route slots q = wave + 4 i: query planes and an empty shortlist.
-    for (int i = 0; i < kShareRoutesPerWave; ++i) {
-        const int q = wave + i * (kScanThreads / kWave);
-        if (q >= n_routes) break;
-        const uint32_t route = a.seg_route[a.item_slots[first + q]];
-        const uint32_t query = a.route_query[route];
-        uint32_t* pl = reinterpret_cast<uint32_t*>(planes_all + q * 8 * V);
-        const int8_t* qrow = sc.q8 + static_cast<size_t>(query) * sc.padded_dim;
-        const int words = 4 * V;  // padded_dim / 32
-        if (lane < words) {
-            uint32_t bits[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int b = 0; b < 32; ++b) {
-                const uint32_t v = static_cast<uint8_t>(qrow[lane * 32 + b]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) bits[j] |= ((v >> j) & 1u) << (31 - b);
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pl[j * words + lane] = bits[j];
-        }
-        for (int e = lane; e < kp; e += kWave) {
-            lst_d_all[q * kp + e] = FLT_MAX;
-            lst_id_all[q * kp + e] = UINT32_MAX;
-        }
-        if (lane == 0) s_pass[q] = 0;
-    }
-    uint32_t* queue = queue_all + wave * kWave;
-    const bool r0_tile = a.pranges && a.pred.range_stride == 1;
-
-    for (uint64_t t0 = 0; t0 < count; t0 += kShareTile) {
-        __syncthreads();  // the previous tile's reads end here
-        const int n = static_cast<int>(count - t0 < kShareTile ? count - t0 : kShareTile);
-        for (int r = tid; r < n; r += kScanThreads) {
-            const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
-            t_ids[r] = a.posting[j];
-            t_slab[r] = a.pslab[j];
-            if (r0_tile) t_r0[r] = a.pranges[j];
-        }
-        __syncthreads();
+    // An item of more than kShareRoutes routes is served in passes of
+    // kShareRoutes slots, each re-reading the item's tiles, so every slot
+    // is written whatever plan the caller built.
+    for (int pass0 = 0; pass0 < n_all; pass0 += kShareRoutes) {
+        const uint32_t first = first_all + static_cast<uint32_t>(pass0);
+        const int n_routes = n_all - pass0 < kShareRoutes ? n_all - pass0 : kShareRoutes;
+        // Route slots q = wave + 4 i: query planes and an empty shortlist.
         for (int i = 0; i < kShareRoutesPerWave; ++i) {
             const int q = wave + i * (kScanThreads / kWave);
             if (q >= n_routes) break;
             const uint32_t route = a.seg_route[a.item_slots[first + q]];
             const uint32_t query = a.route_query[route];
-            const bool enabled = pred_enabled(a.pred, route);
-            const ShortClause sclause = enabled ? short_clause(a.pred, route) : ShortClause{};
-            const float scale = sc.q_scale[query];
-            const float k1 = sc.q_k1[query];
-            const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
-            const uint4* planes = planes_all + q * 8 * V;
-            float* ld = lst_d_all + q * kp;
-            uint32_t* lid = lst_id_all + q * kp;
-            uint32_t passes = 0;
-            int qn = 0;  // queued rows (uniform)
-            // Score the queued rows (lane i < qn takes queue[i]) and merge
-            // the survivors into the shortlist by rank.
-            auto flush = [&]() {
-                const bool have = lane < qn;
-                const int r = have ? static_cast<int>(queue[lane]) : 0;
+            uint32_t* pl = reinterpret_cast<uint32_t*>(planes_all + q * 8 * V);
+            const int8_t* qrow = sc.q8 + static_cast<size_t>(query) * sc.padded_dim;
+            const int words = 4 * V;  // padded_dim / 32
+            if (lane < words) {
+                uint32_t bits[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                for (int b = 0; b < 32; ++b) {
+                    const uint32_t v = static_cast<uint8_t>(qrow[lane * 32 + b]);
+    #pragma unroll
+                    for (int j = 0; j < 8; ++j) bits[j] |= ((v >> j) & 1u) << (31 - b);
+                }
+    #pragma unroll
+                for (int j = 0; j < 8; ++j) pl[j * words + lane] = bits[j];
+            }
+            for (int e = lane; e < kp; e += kWave) {
+                lst_d_all[q * kp + e] = FLT_MAX;
+                lst_id_all[q * kp + e] = UINT32_MAX;
+            }
+            if (lane == 0) s_pass[q] = 0;
+        }
+        uint32_t* queue = queue_all + wave * kWave;
+        const bool r0_tile = a.pranges && a.pred.range_stride == 1;
+
+        for (uint64_t t0 = 0; t0 < count; t0 += kShareTile) {
+            __syncthreads();  // the previous tile's reads end here
+            const int n = static_cast<int>(count - t0 < kShareTile ? count - t0 : kShareTile);
+            for (int r = tid; r < n; r += kScanThreads) {
                 const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
-                uint32_t sid = UINT32_MAX;
-                float v = FLT_MAX;
-                if (have) {
-                    sid = t_ids[r];
-                    const uint4 x = a.paux[j];
-                    uint4 c[V];
-#pragma unroll
-                    for (int w = 0; w < V; ++w) c[w] = a.pcodes[j * V + w];
-                    const float add0 = __uint_as_float(x.x) + g_row[x.z];
-                    const int ip = lane_ip_lds<1, V>(c, planes, V, 0);
-                    const float short_ip = static_cast<float>(ip) * scale;
-                    const float tt = short_ip + k1;
-                    v = fmaf(__uint_as_float(x.y), tt, add0);
-                }
-                const float kd = ld[k - 1];
-                const uint32_t kid = lid[k - 1];
-                const bool in = have && admissible(v, sid) && pair_less(v, sid, kd, kid);
-                const uint64_t sm = ballot(in);
-                qn = 0;
-                if (!sm) return;
-                // ranks: list entry e moves up by the survivors below it; a
-                // survivor lands after the list entries and survivors below it
-                int c_self = 0;
-                if (in) {
-                    int lo = 0, hi = k;
-                    while (lo < hi) {
-                        const int mid = (lo + hi) >> 1;
-                        if (pair_less(ld[mid], lid[mid], v, sid))
-                            lo = mid + 1;
-                        else
-                            hi = mid;
+                t_ids[r] = a.posting[j];
+                t_slab[r] = a.pslab[j];
+                if (r0_tile) t_r0[r] = a.pranges[j];
+            }
+            __syncthreads();
+            for (int i = 0; i < kShareRoutesPerWave; ++i) {
+                const int q = wave + i * (kScanThreads / kWave);
+                if (q >= n_routes) break;
+                const uint32_t route = a.seg_route[a.item_slots[first + q]];
+                const uint32_t query = a.route_query[route];
+                const bool enabled = pred_enabled(a.pred, route);
+                const ShortClause sclause = enabled ? short_clause(a.pred, route) : ShortClause{};
+                const float scale = sc.q_scale[query];
+                const float k1 = sc.q_k1[query];
+                const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
+                const uint4* planes = planes_all + q * 8 * V;
+                float* ld = lst_d_all + q * kp;
+                uint32_t* lid = lst_id_all + q * kp;
+                uint32_t passes = 0;
+                int qn = 0;  // queued rows (uniform)
+                // Score the queued rows (lane i < qn takes queue[i]) and merge
+                // the survivors into the shortlist by rank.
+                auto flush = [&]() {
+                    const bool have = lane < qn;
+                    const int r = have ? static_cast<int>(queue[lane]) : 0;
+                    const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
+                    uint32_t sid = UINT32_MAX;
+                    float v = FLT_MAX;
+                    if (have) {
+                        sid = t_ids[r];
+                        const uint4 x = a.paux[j];
+                        uint4 c[V];
+    #pragma unroll
+                        for (int w = 0; w < V; ++w) c[w] = a.pcodes[j * V + w];
+                        const float add0 = __uint_as_float(x.x) + g_row[x.z];
+                        const int ip = lane_ip_lds<1, V>(c, planes, V, 0);
+                        const float short_ip = static_cast<float>(ip) * scale;
+                        const float tt = short_ip + k1;
+                        v = fmaf(__uint_as_float(x.y), tt, add0);
                     }
-                    c_self = lo;
-                }
-                const int e0 = lane, e1 = lane + kWave;
-                const float d0 = e0 < k ? ld[e0] : FLT_MAX;
-                const uint32_t i0 = e0 < k ? lid[e0] : UINT32_MAX;
-                const float d1 = e1 < k ? ld[e1] : FLT_MAX;
-                const uint32_t i1 = e1 < k ? lid[e1] : UINT32_MAX;
-                int c0 = 0, c1 = 0;
-                for (uint64_t m = sm; m; m &= m - 1) {
-                    const int src = __builtin_ctzll(m);
-                    const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
-                    const uint32_t si = static_cast<uint32_t>(
-                        __builtin_amdgcn_readlane(static_cast<int>(sid), src));
-                    c0 += pair_less(sv, si, d0, i0) ? 1 : 0;
-                    c1 += pair_less(sv, si, d1, i1) ? 1 : 0;
-                    c_self += pair_less(sv, si, v, sid) ? 1 : 0;
-                }
-                // all reads of the old list precede these writes (one wave)
-                if (e0 < k && e0 + c0 < k) {
-                    ld[e0 + c0] = d0;
-                    lid[e0 + c0] = i0;
-                }
-                if (e1 < k && e1 + c1 < k) {
-                    ld[e1 + c1] = d1;
-                    lid[e1 + c1] = i1;
-                }
-                if (in && c_self < k) {
-                    ld[c_self] = v;
-                    lid[c_self] = sid;
-                }
-            };
-            for (int r0 = 0; r0 < n; r0 += kWave) {
-                const int r = r0 + lane;
-                bool ok = false;
-                if (r < n) {
-                    const uint32_t s = t_ids[r];
-                    ok = s < a.base_rows;
-                    if (ok && enabled) {
-                        const uint4 slab = t_slab[r];
-                        if (slab_count(slab) != kSlabOverflow) {
-                            const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
-                            const float* prange = a.pranges && a.pred.range_stride > 0
-                                                      ? a.pranges + j * a.pred.range_stride
-                                                      : nullptr;
-                            const float rv = r0_tile ? t_r0[r] : 0.0f;
-                            ok = sclause.simple
-                                     ? short_clause_matches(a.pred, sclause, s, slab, prange, rv)
-                                     : slab_pred_matches(a.pred, route, s, slab, prange, rv);
-                        } else {
-                            PredCounters pc{0, 0};
-                            ok = pred_matches(a.pred, route, s, pc);
+                    const float kd = ld[k - 1];
+                    const uint32_t kid = lid[k - 1];
+                    const bool in = have && admissible(v, sid) && pair_less(v, sid, kd, kid);
+                    const uint64_t sm = ballot(in);
+                    qn = 0;
+                    if (!sm) return;
+                    // ranks: list entry e moves up by the survivors below it; a
+                    // survivor lands after the list entries and survivors below it
+                    int c_self = 0;
+                    if (in) {
+                        int lo = 0, hi = k;
+                        while (lo < hi) {
+                            const int mid = (lo + hi) >> 1;
+                            if (pair_less(ld[mid], lid[mid], v, sid))
+                                lo = mid + 1;
+                            else
+                                hi = mid;
+                        }
+                        c_self = lo;
+                    }
+                    const int e0 = lane, e1 = lane + kWave;
+                    const float d0 = e0 < k ? ld[e0] : FLT_MAX;
+                    const uint32_t i0 = e0 < k ? lid[e0] : UINT32_MAX;
+                    const float d1 = e1 < k ? ld[e1] : FLT_MAX;
+                    const uint32_t i1 = e1 < k ? lid[e1] : UINT32_MAX;
+                    int c0 = 0, c1 = 0;
+                    for (uint64_t m = sm; m; m &= m - 1) {
+                        const int src = __builtin_ctzll(m);
+                        const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+                        const uint32_t si = static_cast<uint32_t>(
+                            __builtin_amdgcn_readlane(static_cast<int>(sid), src));
+                        c0 += pair_less(sv, si, d0, i0) ? 1 : 0;
+                        c1 += pair_less(sv, si, d1, i1) ? 1 : 0;
+                        c_self += pair_less(sv, si, v, sid) ? 1 : 0;
+                    }
+                    // all reads of the old list precede these writes (one wave)
+                    if (e0 < k && e0 + c0 < k) {
+                        ld[e0 + c0] = d0;
+                        lid[e0 + c0] = i0;
+                    }
+                    if (e1 < k && e1 + c1 < k) {
+                        ld[e1 + c1] = d1;
+                        lid[e1 + c1] = i1;
+                    }
+                    if (in && c_self < k) {
+                        ld[c_self] = v;
+                        lid[c_self] = sid;
+                    }
+                };
+                for (int r0 = 0; r0 < n; r0 += kWave) {
+                    const int r = r0 + lane;
+                    bool ok = false;
+                    if (r < n) {
+                        const uint32_t s = t_ids[r];
+                        ok = s < a.base_rows;
+                        if (ok && enabled) {
+                            const uint4 slab = t_slab[r];
+                            if (slab_count(slab) != kSlabOverflow) {
+                                const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
+                                const float* prange = a.pranges && a.pred.range_stride > 0
+                                                          ? a.pranges + j * a.pred.range_stride
+                                                          : nullptr;
+                                const float rv = r0_tile ? t_r0[r] : 0.0f;
+                                ok = sclause.simple
+                                         ? short_clause_matches(a.pred, sclause, s, slab, prange, rv)
+                                         : slab_pred_matches(a.pred, route, s, slab, prange, rv);
+                            } else {
+                                PredCounters pc{0, 0};
+                                ok = pred_matches(a.pred, route, s, pc);
+                            }
                         }
                     }
+                    const uint64_t om = ballot(ok);
+                    const int c = __popcll(om);
+                    if (enabled) passes += static_cast<uint32_t>(c);
+                    if (c == 0) continue;
+                    if (qn + c > kWave) flush();
+                    if (ok) queue[qn + static_cast<int>(lanes_below(om))] = static_cast<uint32_t>(r);
+                    qn += c;
                 }
-                const uint64_t om = ballot(ok);
-                const int c = __popcll(om);
-                if (enabled) passes += static_cast<uint32_t>(c);
-                if (c == 0) continue;
-                if (qn + c > kWave) flush();
-                if (ok) queue[qn + static_cast<int>(lanes_below(om))] = static_cast<uint32_t>(r);
-                qn += c;
+                if (qn) flush();
+                if (lane == 0) s_pass[q] += passes;
             }
-            if (qn) flush();
-            if (lane == 0) s_pass[q] += passes;
         }
-    }
-    __syncthreads();
-    for (int i = 0; i < kShareRoutesPerWave; ++i) {
-        const int q = wave + i * (kScanThreads / kWave);
-        if (q >= n_routes) break;
-        const uint32_t slot = a.item_slots[first + q];
-        for (int e = lane; e < k; e += kWave) {
-            a.out_ids[static_cast<size_t>(slot) * k + e] = lst_id_all[q * kp + e];
-            a.out_dists[static_cast<size_t>(slot) * k + e] = lst_d_all[q * kp + e];
+        __syncthreads();
+        for (int i = 0; i < kShareRoutesPerWave; ++i) {
+            const int q = wave + i * (kScanThreads / kWave);
+            if (q >= n_routes) break;
+            const uint32_t slot = a.item_slots[first + q];
+            for (int e = lane; e < k; e += kWave) {
+                a.out_ids[static_cast<size_t>(slot) * k + e] = lst_id_all[q * kp + e];
+                a.out_dists[static_cast<size_t>(slot) * k + e] = lst_d_all[q * kp + e];
+            }
+            if (lane == 0 && a.pass_counts) a.pass_counts[slot] = s_pass[q];
         }
-        if (lane == 0 && a.pass_counts) a.pass_counts[slot] = s_pass[q];
     }
 }
 
@@ -1468,8 +1475,8 @@ int rabitq_posting_scan_segments(Context* ctx, const gofann_rabitq_view* rq,
 }
 
 // The label-shared variant of rabitq_posting_scan_segments: `share` lists
-// the plan's segments by the rows they scan (items of at most kShareRoutes
-// segments with equal offset and size).  Needs the posting-order codes, aux
+// the plan's segments by the rows they scan (items of segments with equal
+// offset and size; kShareRoutes of them per pass over the item's rows).  Needs the posting-order codes, aux
 // and slab; the outputs equal rabitq_posting_scan_segments' bit for bit.
 int rabitq_posting_scan_shared(Context* ctx, const gofann_rabitq_view* rq,
                                const gofann_rabitq_queries* pre,

@@ -278,7 +278,11 @@ class SharePlan:
 def share_plan(plan: SegmentPlan, routes_per_item: int = SHARE_ROUTES) -> SharePlan:
     """Groups the plan's segments by (offset, size) -- the routes of one
     label cut the same way -- into items of at most `routes_per_item`,
-    the heaviest items (rows x routes) first."""
+    the heaviest items (rows x routes) first.  `routes_per_item` is 1 to
+    SHARE_ROUTES: the kernel holds that many route slots per pass over an
+    item's rows, so a larger item would re-read its rows."""
+    if not 1 <= int(routes_per_item) <= SHARE_ROUTES:
+        raise ValueError(f"routes_per_item must be 1..{SHARE_ROUTES}, got {routes_per_item}")
     m = plan.count
     if m == 0:
         z = np.zeros(0, np.uint64)

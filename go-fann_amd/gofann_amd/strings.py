@@ -16,12 +16,20 @@ Semantics follow the reference:
     :2993-3011);
   * score of a token against a pattern: |G_p & G_t| / |G_p | G_t| in
     float32, kept when >= min_score; prefix / suffix / contains modes keep a
-    direct match whatever its score (ManifestNgramIndex::expand,
-    :3647-3760).  Output: ascending distinct token ids.
+    direct match whatever its score, ranked as max(1, score)
+    (ManifestNgramIndex::expand, :3647-3760);
+  * at most max_terms tokens (query_manifest_max_fuzzy_terms, default 64,
+    dataloader.h:1032): the kept tokens are ranked direct matches first,
+    then by score descending, then by token id ascending, and the first
+    max_terms are returned (:3748-3762).  Output: ascending distinct token
+    ids.
 """
 from __future__ import annotations
 
 import numpy as np
+
+# query_manifest_max_fuzzy_terms (dataloader.h:1032)
+MAX_FUZZY_TERMS = 64
 
 
 def normalize(text: str) -> str:
@@ -74,8 +82,12 @@ class NgramIndex:
         self.post_offsets = np.zeros(len(gram_id) + 1, dtype=np.int64)
         np.cumsum(np.bincount(pg, minlength=len(gram_id)), out=self.post_offsets[1:])
 
-    def expand(self, pattern: str, min_score: float = 0.25, mode: str = "") -> np.ndarray:
-        """Token ids matching `pattern`, ascending."""
+    def expand(self, pattern: str, min_score: float = 0.25, mode: str = "",
+               max_terms: int = MAX_FUZZY_TERMS) -> np.ndarray:
+        """Token ids matching `pattern`, at most `max_terms` of them by the
+        reference's ranking, ascending."""
+        if int(max_terms) <= 0:
+            raise ValueError("max_terms (query_manifest_max_fuzzy_terms) must be positive")
         norm = normalize(pattern)
         if not norm:
             return np.zeros(0, dtype=np.int64)
@@ -89,12 +101,18 @@ class NgramIndex:
         union = len(grams) + self.gram_counts[toks] - overlap
         score = np.where(union == 0, np.float32(0),
                          overlap.astype(np.float32) / union.astype(np.float32))
-        keep = score >= np.float32(min_score)
+        direct = np.zeros(toks.shape[0], bool)
         mode = mode.lower()
         if mode in ("prefix", "suffix", "contains", "substring"):
             direct = np.array([self._direct(self.texts[t], norm, mode) for t in toks], bool)
-            keep |= direct
-        return toks[keep]
+        keep = direct | (score >= np.float32(min_score))
+        toks, score, direct = toks[keep], score[keep], direct[keep]
+        if toks.shape[0] > max_terms:
+            rank = np.where(direct, np.maximum(np.float32(1), score), score).astype(np.float32)
+            # direct first, then score descending, then token id ascending
+            order = np.lexsort((toks, -rank.astype(np.float64), ~direct))
+            toks = np.sort(toks[order[:int(max_terms)]])
+        return toks
 
     @staticmethod
     def _direct(text: str, pattern: str, mode: str) -> bool:

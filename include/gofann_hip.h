@@ -447,10 +447,11 @@ int gofann_rabitq_posting_scan_segments(gofann_ctx* ctx, const gofann_rabitq_vie
  * restates).  The segments of a plan that scan the same posting rows (the
  * routes of one label) are listed together in a share plan: item i covers
  * posting rows [item_offsets[i], + item_sizes[i]) for the plan segments
- * item_slots[item_begin[i] .. item_begin[i+1]) (at most 16 per item, each
- * with exactly that offset and size).  One workgroup per item reads the
- * rows' posting-order columns once and filters and scores them for every
- * route of the item.  Takes posting_codes, posting_aux and posting_slab
+ * item_slots[item_begin[i] .. item_begin[i+1]) (each with exactly that
+ * offset and size).  One workgroup per item reads the rows' posting-order
+ * columns once and filters and scores them for every route of the item, 16
+ * route slots per pass over the rows: items of at most 16 routes take one
+ * pass, larger items re-read their rows once per further 16.  Takes posting_codes, posting_aux and posting_slab
  * (posting_ranges optional), shortlist_k <= 128 and padded_dim <= 1024
  * (GOFANN_ERR_UNSUPPORTED otherwise); every output equals
  * gofann_rabitq_posting_scan_segments' for the same plan, bit for bit. */
@@ -525,11 +526,14 @@ void gofann_host_rerank_destroy(gofann_host_rerank* hr);
 const char* gofann_host_rerank_last_error(const gofann_host_rerank* hr);
 /* fp16 rows: the L2 kernel chosen at create, as the reference chooses it
  * (fp16_l2::select, src/data/fp16_l2.h:53-70): environment variable
- * GOFANN_FP16_RERANK_KERNEL = auto (AVX-512 if the CPU has it, else AVX2,
+ * GOFANN_FP16_RERANK_KERNEL (or, when that is unset, the reference's
+ * GO_FANN_FP16_RERANK_KERNEL) = auto (AVX-512 if the CPU has it, else AVX2,
  * else scalar) | scalar | avx2 | avx512, each with the reference kernel's
- * summation order.  An unknown name makes create return GOFANN_ERR_INVALID,
- * an ISA the CPU lacks GOFANN_ERR_UNSUPPORTED.  Returns "scalar", "avx2"
- * or "avx512". */
+ * summation order.  Read only when base_elem is GOFANN_ELEM_F16, as the
+ * reference reads it only for fp16 sources (dataloader.cpp:2132): for those
+ * an unknown name makes create return GOFANN_ERR_INVALID, an ISA the CPU
+ * lacks GOFANN_ERR_UNSUPPORTED.  Returns "scalar", "avx2" or "avx512"
+ * ("scalar" for u8 and f32 rows, which take no fp16 kernel). */
 const char* gofann_host_rerank_fp16_kernel(const gofann_host_rerank* hr);
 /* Host arrays only: shortlist [routes][width], route_query [routes],
  * outputs [routes][topk]. */

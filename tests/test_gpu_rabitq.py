@@ -321,16 +321,24 @@ def test_rabitq_posting_scan_segments_matches_oracle(gpu_ctx, cworld, target, co
 _SHARE_CODES = {}
 
 
-# The label-shared scan (one workgroup per label segment, a wave per route):
-# P 128 and 512 (one or four code vectors per row), segments cut small,
-# across tile boundaries (700 rows) and whole; shortlists of 40 and 100.
-@pytest.mark.parametrize("P", [128, 512])
-@pytest.mark.parametrize("target", [97, 700, 1 << 20])
-@pytest.mark.parametrize("k", [40, 100])
-def test_rabitq_posting_scan_shared_matches_oracle(gpu_ctx, cworld, P, target, k):
+def _uncapped_share_plan(rp, plan):
+    """Every plan segment of one (offset, size) in a single item, however
+    many: items above 16 routes take the kernel's extra passes."""
+    order = np.lexsort((np.arange(plan.count), plan.sizes, plan.offsets))
+    o, sz = plan.offsets[order], plan.sizes[order]
+    new = np.r_[True, (o[1:] != o[:-1]) | (sz[1:] != sz[:-1])]
+    starts = np.flatnonzero(new)
+    begin = np.r_[starts, plan.count].astype(np.uint32)
+    return rp.SharePlan(o[starts].astype(np.uint64), sz[starts].astype(np.uint64), begin,
+                        order.astype(np.uint32))
+
+
+def _shared_scan_case(gpu_ctx, cworld, P, target, k, per_item, repeat=1):
     from gofann_amd import range_posting as rp
     wl, li, routes, _rot, _codes, _fac, _aid, _anchors, _P = cworld
-    say("posting scan shared P", P, "target", target, "k", k)
+    routes = list(routes) * repeat
+    say("posting scan shared P", P, "target", target, "k", k, "per_item", per_item,
+        "routes", len(routes))
     if P not in _SHARE_CODES:
         rot = gi.random_rotation(wl.dim, P, 33005 + P, "cpu")
         _SHARE_CODES[P] = (rot,) + tuple(gi.rabitq_encode(wl.base, rot, wl.centroids))
@@ -353,8 +361,13 @@ def test_rabitq_posting_scan_shared_matches_oracle(gpu_ctx, cworld, P, target, k
     total = int(li.posting_offset[-1])
     plan = rp.segment_plan(np.arange(n), off.astype(np.uint64), size.astype(np.uint64), target)
     segs = rp.DeviceSegments(plan)
-    sp = rp.share_plan(plan)
+    sp = rp.share_plan(plan, per_item) if per_item else _uncapped_share_plan(rp, plan)
+    counts = np.diff(sp.begin.astype(np.int64))
     assert sp.items < plan.count  # segments of one label share items
+    if per_item:
+        assert counts.max() <= per_item
+    else:
+        assert counts.max() > 2 * rp.SHARE_ROUTES  # three passes over some items
     share = rp.DeviceShare(sp)
     rows = rp.PostingRows(gpu_ctx, rv, dg.posting_ids, total)
     cols = rp.PostingPredicateColumns(gpu_ctx, pv, dg.posting_ids, total)
@@ -366,6 +379,26 @@ def test_rabitq_posting_scan_shared_matches_oracle(gpu_ctx, cworld, P, target, k
     assert np.array_equal(dists.cpu().numpy().reshape(n, k).view(np.uint32), od.view(np.uint32))
     assert np.array_equal(as_u32(passes), opass)
     assert (oi[:, 0] != U32MAX).sum() > n // 2 and opass.max() > 0
+
+
+# The label-shared scan (one workgroup per label segment, a wave per route):
+# P 128 to 1024 (one to eight code vectors per row; 1024 is the largest LDS
+# layout, 32 plane words per route), segments cut small, across tile
+# boundaries (700 rows) and whole; shortlists of 40 and 100.
+@pytest.mark.parametrize("P", [128, 256, 512, 1024])
+@pytest.mark.parametrize("target", [97, 700, 1 << 20])
+@pytest.mark.parametrize("k", [40, 100])
+def test_rabitq_posting_scan_shared_matches_oracle(gpu_ctx, cworld, P, target, k):
+    _shared_scan_case(gpu_ctx, cworld, P, target, k, 16)
+
+
+# Items of fewer than 16 routes (5 per item), and items of more than 32
+# routes (every route of a label segment in one item; the route set is
+# repeated three times), which the kernel serves in passes of 16 slots.
+@pytest.mark.parametrize("P", [256, 1024])
+@pytest.mark.parametrize("per_item", [5, 0])
+def test_rabitq_posting_scan_shared_item_sizes(gpu_ctx, cworld, P, per_item):
+    _shared_scan_case(gpu_ctx, cworld, P, 700, 40, per_item, repeat=1 if per_item else 3)
 
 
 def test_streamed_host_rerank_matches_direct(gpu_ctx, rworld):

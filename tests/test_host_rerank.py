@@ -148,3 +148,31 @@ def test_host_rerank_fp16_kernels_follow_their_order(monkeypatch, kernel, lanes,
     with pytest.raises(gs._lib.GofannError):
         gs.HostRerank(base, queries, threads=1)
     assert lib is not None and C is not None
+
+
+def test_host_rerank_fp16_variable_read_for_fp16_rows_only(monkeypatch):
+    """The fp16 kernel variable is read only for fp16 rows, as the
+    reference reads GO_FANN_FP16_RERANK_KERNEL only for fp16 sources
+    (dataloader.cpp:2132): an unknown name fails an fp16 create and leaves
+    u8 and f32 creates alone; the reference's variable name is honoured when
+    this library's is unset."""
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((4, 16)).astype(np.float32)
+    monkeypatch.delenv("GOFANN_FP16_RERANK_KERNEL", raising=False)
+    monkeypatch.setenv("GO_FANN_FP16_RERANK_KERNEL", "bogus")
+    for base in (rng.integers(0, 255, (50, 16)).astype(np.uint8),
+                 rng.standard_normal((50, 16)).astype(np.float32)):
+        hr = gs.HostRerank(base, q if base.dtype != np.uint8 else q.astype(np.uint8), threads=1)
+        assert hr.fp16_kernel == "scalar"
+        hr.close()
+    f16 = rng.standard_normal((50, 16)).astype(np.float16)
+    with pytest.raises(gs._lib.GofannError):
+        gs.HostRerank(f16, q, threads=1)
+    monkeypatch.setenv("GO_FANN_FP16_RERANK_KERNEL", "scalar")
+    hr = gs.HostRerank(f16, q, threads=1)
+    assert hr.fp16_kernel == "scalar"
+    hr.close()
+    # this library's name wins when both are set
+    monkeypatch.setenv("GOFANN_FP16_RERANK_KERNEL", "bogus")
+    with pytest.raises(gs._lib.GofannError):
+        gs.HostRerank(f16, q, threads=1)

@@ -402,3 +402,17 @@ def test_share_plan_groups_segments_that_scan_the_same_rows():
     big = [i for i in range(sp.items) if lab_off[1] <= sp.offsets[i] < lab_off[2]]
     assert sorted(counts[big].tolist()) == [4] * 4 + [16] * 4
     assert sorted(set(sp.offsets[big].tolist())) == [50, 350, 650, 950]
+
+
+def test_share_plan_rejects_route_counts_outside_the_kernel_slots():
+    """share_plan holds items to 1..SHARE_ROUTES routes (the shared scan's
+    route slots per pass over an item's rows)."""
+    from gofann_amd import range_posting as rp
+    plan = rp.segment_plan(np.arange(4), np.zeros(4, np.uint64), np.full(4, 100, np.uint64), 64)
+    for bad in (0, rp.SHARE_ROUTES + 1, 17, -3):
+        with pytest.raises(ValueError):
+            rp.share_plan(plan, bad)
+    for ok in (1, 5, rp.SHARE_ROUTES):
+        sp = rp.share_plan(plan, ok)
+        assert np.diff(sp.begin.astype(np.int64)).max() <= ok
+

@@ -60,9 +60,54 @@ def test_expand_matches_brute_force_jaccard(n, min_score):
     pats = [st.mutate(vocab[int(rng.integers(0, len(vocab)))], rng, int(rng.integers(0, 3)))
             for _ in range(150)] + ["ab", "ABC!", "mixed case token", "zz", ""]
     for pat in pats:
-        got = ix.expand(pat, min_score).tolist()
+        got = ix.expand(pat, min_score, max_terms=1 << 30).tolist()
         want = sorted(t for t, sc in _jaccard_brute(pat, vocab, n) if sc >= np.float32(min_score))
         assert got == want, pat
+
+
+def _capped_brute(pattern, tokens, n, min_score, mode, max_terms):
+    """ManifestNgramIndex::expand's selection restated by brute force
+    (dataloader.cpp:3700-3786): every token sharing a gram with the pattern,
+    kept if a direct match (ranked as max(1, score)) or if score >=
+    min_score; sorted direct first, score descending, token id ascending;
+    the first max_terms, returned ascending."""
+    norm = st.normalize(pattern)
+    cands = []
+    for t, sc in _jaccard_brute(pattern, tokens, n):
+        text = st.normalize(tokens[t])
+        direct = (mode == "prefix" and text.startswith(norm)) or \
+                 (mode == "suffix" and text.endswith(norm)) or \
+                 (mode in ("contains", "substring") and norm in text)
+        if not direct and sc < np.float32(min_score):
+            continue
+        cands.append((t, max(np.float32(1), sc) if direct else sc, direct))
+    cands.sort(key=lambda c: (not c[2], -float(c[1]), c[0]))
+    return sorted(c[0] for c in cands[:max_terms])
+
+
+@pytest.mark.parametrize("mode", ["", "contains", "prefix"])
+def test_expand_caps_terms_by_reference_ranking(mode):
+    """A pattern that matches more than max_terms tokens keeps the
+    reference's top max_terms (query_manifest_max_fuzzy_terms, 64 by
+    default): direct matches first, then the highest scores, ties by the
+    lower token id.  The vocabulary holds many tokens of equal score, so a
+    wrong tie order or a missing cap changes the returned set."""
+    rng = np.random.default_rng(71)
+    stem = "abcdefgh"
+    vocab = [stem + "".join(rng.choice(list("xyz"), 3)) for _ in range(300)]
+    vocab += ["".join(rng.choice(list("xyz"), 3)) + stem for _ in range(100)]
+    vocab += [stem, stem[:6] + "qq", "zz" + stem[2:]]
+    vocab += st.markov_strings(500, 5)
+    ix = st.NgramIndex(vocab, 3)
+    for pat, ms in ((stem, 0.25), (stem + "x", 0.3), ("bcdefg", 0.2)):
+        full = ix.expand(pat, ms, mode, max_terms=1 << 30)
+        assert len(full) > 64, (pat, len(full))
+        for cap in (64, 7, 1):
+            got = ix.expand(pat, ms, mode, max_terms=cap).tolist()
+            assert got == _capped_brute(pat, vocab, 3, ms, mode, cap), (pat, mode, cap)
+        assert ix.expand(pat, ms, mode).tolist() == _capped_brute(pat, vocab, 3, ms, mode, 64)
+    with pytest.raises(ValueError):
+        ix.expand(stem, 0.25, mode, max_terms=0)
 
 
 def test_expand_direct_modes():
