@@ -387,4 +387,114 @@ int gofann_rabitq_score(gofann_ctx* c, const gofann_rabitq_view* rq,
     });
 }
 
+int gofann_build_assign(gofann_ctx* c, const void* rows, int elem, uint32_t dim, uint64_t n,
+                        const float* centres, uint32_t k, uint32_t* out_idx, float* out_score)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_assign(ctx, rows, elem, dim, n, centres, k, out_idx, out_score);
+    });
+}
+
+int gofann_build_kmeanspp(gofann_ctx* c, const void* rows, int elem, uint32_t dim, uint64_t n,
+                          uint32_t k, uint64_t seed, float* centres)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_kmeanspp(ctx, rows, elem, dim, n, k, seed, centres);
+    });
+}
+
+int gofann_build_kmeans(gofann_ctx* c, const void* rows, int elem, uint32_t dim, uint64_t n,
+                        uint32_t k, uint32_t iters, float* centres)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_kmeans(ctx, rows, elem, dim, n, k, iters, centres);
+    });
+}
+
+int gofann_build_knn(gofann_ctx* c, const void* rows, int elem, uint32_t dim,
+                     const gofann_build_buckets* buckets, uint32_t k, uint32_t* out_ids,
+                     float* out_dists)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_knn(ctx, rows, elem, dim, buckets, k, out_ids, out_dists);
+    });
+}
+
+int gofann_build_pq_train(gofann_ctx* c, const void* rows, int elem, uint32_t dim, uint64_t n,
+                          uint32_t pq_dim, uint32_t iters, float* centroids)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_pq_train(ctx, rows, elem, dim, n, pq_dim, iters, centroids);
+    });
+}
+
+int gofann_build_pq_encode(gofann_ctx* c, const void* rows, int elem, uint32_t dim, uint64_t n,
+                           uint32_t pq_dim, const float* centroids, uint8_t* codes,
+                           uint32_t code_stride)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_pq_encode(ctx, rows, elem, dim, n, pq_dim, centroids, codes,
+                                       code_stride);
+    });
+}
+
+int gofann_build_rotate(gofann_ctx* c, const void* rows, int elem, uint32_t dim, uint32_t n,
+                        const float* rotation, uint32_t padded_dim, float* out)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_rotate(ctx, rows, elem, dim, n, rotation, padded_dim, out);
+    });
+}
+
+int gofann_build_rabitq_encode(gofann_ctx* c, const float* rotated, uint32_t n,
+                               uint32_t padded_dim, const float* anchors, uint32_t num_anchors,
+                               uint32_t* anchor_ids, uint8_t* codes, float* factors)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_rabitq_encode(ctx, rotated, n, padded_dim, anchors, num_anchors,
+                                           anchor_ids, codes, factors);
+    });
+}
+
+int gofann_build_medoid(gofann_ctx* c, const void* rows, int elem, uint32_t dim, uint64_t n,
+                        uint32_t* out_row)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_medoid(ctx, rows, elem, dim, n, out_row);
+    });
+}
+
+int gofann_build_bucket_reps(gofann_ctx* c, const void* rows, int elem, uint32_t dim,
+                             const uint32_t* bucket_offsets, uint32_t buckets, float* means,
+                             uint32_t* reps)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_bucket_reps(ctx, rows, elem, dim, bucket_offsets, buckets, means, reps);
+    });
+}
+
+int gofann_build_links(gofann_ctx* c, const gofann_build_link_inputs* inputs,
+                       const gofann_build_link_params* params, uint32_t* out_graph)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_links(ctx, inputs, params, out_graph);
+    });
+}
+
+int gofann_build_cagra_optimize(gofann_ctx* c, const uint32_t* knn, uint32_t n, uint32_t kin,
+                                uint32_t degree, uint32_t* pruned, uint32_t* out_graph)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_cagra_optimize(ctx, knn, n, kin, degree, pruned, out_graph);
+    });
+}
+
+int gofann_build_reach(gofann_ctx* c, const uint32_t* graph, uint32_t n, uint32_t degree,
+                       uint32_t entry_row, uint32_t* reached, uint32_t* reached_count)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::build_reach(ctx, graph, n, degree, entry_row, reached, reached_count);
+    });
+}
+
 }  // extern "C"

@@ -21,7 +21,8 @@ struct Context {
         kScratchSegments = 1,
         kScratchMisc = 2,
         kScratchRange = 3,  // per-segment range-scan shortlists before the merge
-        kScratchCount = 4
+        kScratchBuild = 4,  // index construction (k-means, kNN, graph optimisation)
+        kScratchCount = 5
     };
 
     int device = 0;
@@ -138,6 +139,32 @@ int exact_search_noalloc(Context* ctx, const void* base, int base_elem, uint32_t
 // gofann_create with the device current).
 void noalloc_setup(int device);
 void destroy_blas(Context* ctx);
+int build_assign(Context* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                 const float* centres, uint32_t k, uint32_t* out_idx, float* out_score);
+int build_kmeanspp(Context* ctx, const void* rows, int elem, uint32_t dim, uint64_t n, uint32_t k,
+                   uint64_t seed, float* centres);
+int build_kmeans(Context* ctx, const void* rows, int elem, uint32_t dim, uint64_t n, uint32_t k,
+                 uint32_t iters, float* centres);
+int build_knn(Context* ctx, const void* rows, int elem, uint32_t dim,
+              const gofann_build_buckets* b, uint32_t k, uint32_t* out_ids, float* out_dists);
+int build_pq_train(Context* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                   uint32_t pq_dim, uint32_t iters, float* centroids);
+int build_pq_encode(Context* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                    uint32_t pq_dim, const float* centroids, uint8_t* codes, uint32_t code_stride);
+int build_rotate(Context* ctx, const void* rows, int elem, uint32_t dim, uint32_t n,
+                 const float* rotation, uint32_t padded_dim, float* out);
+int build_rabitq_encode(Context* ctx, const float* rotated, uint32_t n, uint32_t padded_dim,
+                        const float* anchors, uint32_t num_anchors, uint32_t* anchor_ids,
+                        uint8_t* codes, float* factors);
+int build_medoid(Context* ctx, const void* rows, int elem, uint32_t dim, uint64_t n, uint32_t* out);
+int build_bucket_reps(Context* ctx, const void* rows, int elem, uint32_t dim,
+                      const uint32_t* bucket_offsets, uint32_t buckets, float* means, uint32_t* reps);
+int build_links(Context* ctx, const gofann_build_link_inputs* in, const gofann_build_link_params* p,
+                uint32_t* out_graph);
+int build_cagra_optimize(Context* ctx, const uint32_t* knn, uint32_t n, uint32_t kin, uint32_t degree,
+                         uint32_t* pruned, uint32_t* out_graph);
+int build_reach(Context* ctx, const uint32_t* graph, uint32_t n, uint32_t degree, uint32_t entry,
+                uint32_t* reached, uint32_t* out_count);
 int rabitq_prepare(Context* ctx, const gofann_rabitq_view* rq, const float* queries,
                    uint32_t count, const float* rotation, gofann_rabitq_queries* out);
 

@@ -110,6 +110,21 @@ U64 = C.c_uint64
 CS = C.c_char_p
 
 
+class BuildBuckets(C.Structure):
+    _fields_ = [("bucket_offsets", P), ("buckets", U32), ("rows", U32), ("probe_offsets", P),
+                ("probe_buckets", P)]
+
+
+class BuildLinkInputs(C.Structure):
+    _fields_ = [("rows", U32), ("knn", P), ("knn_width", U32), ("bucket_of", P), ("reps", P),
+                ("near_buckets", P), ("near_width", U32), ("buckets", U32), ("order", P)]
+
+
+class BuildLinkParams(C.Structure):
+    _fields_ = [("degree", U32), ("local", U32), ("near_links", U32), ("rep_local", U32),
+                ("rep_near", U32), ("entry_row", U32), ("seed", U64)]
+
+
 class GraphFileHeader(C.Structure):
     _fields_ = [("magic", U32), ("version", U32), ("block_size", U32), ("header_size", U32),
                 ("rows", U64), ("degree", U32), ("row_size_bytes", U32),
@@ -238,6 +253,20 @@ SIGNATURES = {
     "gofann_pq_codes_read_header": (C.c_int, [CS, C.POINTER(U64), C.POINTER(U32)]),
     "gofann_pq_codes_read": (C.c_int, [CS, U64, U64, P, U32]),
     "gofann_pq_files_write": (C.c_int, [CS, CS, P, U32, U32, P, U64]),
+    "gofann_build_assign": (C.c_int, [P, P, C.c_int, U32, U64, P, U32, P, P]),
+    "gofann_build_kmeanspp": (C.c_int, [P, P, C.c_int, U32, U64, U32, U64, P]),
+    "gofann_build_kmeans": (C.c_int, [P, P, C.c_int, U32, U64, U32, U32, P]),
+    "gofann_build_knn": (C.c_int, [P, P, C.c_int, U32, C.POINTER(BuildBuckets), U32, P, P]),
+    "gofann_build_pq_train": (C.c_int, [P, P, C.c_int, U32, U64, U32, U32, P]),
+    "gofann_build_pq_encode": (C.c_int, [P, P, C.c_int, U32, U64, U32, P, P, U32]),
+    "gofann_build_rotate": (C.c_int, [P, P, C.c_int, U32, U32, P, U32, P]),
+    "gofann_build_rabitq_encode": (C.c_int, [P, P, U32, U32, P, U32, P, P, P]),
+    "gofann_build_medoid": (C.c_int, [P, P, C.c_int, U32, U64, C.POINTER(U32)]),
+    "gofann_build_bucket_reps": (C.c_int, [P, P, C.c_int, U32, P, U32, P, P]),
+    "gofann_build_links": (C.c_int, [P, C.POINTER(BuildLinkInputs), C.POINTER(BuildLinkParams),
+                                     P]),
+    "gofann_build_cagra_optimize": (C.c_int, [P, P, U32, U32, U32, P, P]),
+    "gofann_build_reach": (C.c_int, [P, P, U32, U32, U32, P, C.POINTER(U32)]),
 }
 
 _lib = None

@@ -1,8 +1,14 @@
-"""Offline index construction for the synthetic workloads (torch, CPU or GPU).
+"""Offline index construction for the synthetic workloads, on the GPU.
 
 This is the build side the GPU search path consumes; the reference builds it
-with cuVS (CAGRA graphs, PQ, IVF-RaBitQ).  Formats follow the reference's
-in-memory layouts:
+with cuVS (CAGRA graphs, PQ, IVF-RaBitQ).  Every computation here runs in
+the HIP kernels behind gofann_build_* (gofann_amd.builder.HipBuild, the
+default backend); this module holds the host orchestration: samples, row
+orders, bucket offsets and the connectivity repair.  A backend object
+(builder.HipBuild, or the oracle's restatement of the same primitives)
+is passed as `backend=`.
+
+Formats follow the reference's in-memory layouts:
 
   * PQ: centroid table C[256][D] (subspace m owns dims [m*D/M, (m+1)*D/M)),
     codes u8 [N][M] by sample id (backend_pq.cu:1760-1823,
@@ -18,9 +24,14 @@ in-memory layouts:
     group mean (src/data/dataloader.cpp:7154-7251, 7361-7406).  Rare labels
     are served by posting lists.
 
-The graph builder is this project's own (the reference's CAGRA build is out
-of scope): exact kNN inside (label, cluster) buckets plus bridge edges
-between bucket representatives, so a single seed reaches every cluster.
+Two graph designs:
+  * "navigable" (default, this project's own): exact kNN inside (label,
+    cluster) buckets plus links to bucket representatives and uniformly
+    drawn links, so a single seed reaches every cluster;
+  * "cagra": the reference's recipe (graph_builder.cu:1279-1315): exact kNN
+    at 2R over each row's bucket and its nearest buckets, CAGRA's rank-based
+    pruning to R and reverse-edge merge, then every row made reachable from
+    the seed.
 """
 from __future__ import annotations
 
@@ -32,94 +43,76 @@ import torch
 UINT32_MAX = np.uint32(0xFFFFFFFF)
 
 
+def _backend(backend):
+    if backend is not None:
+        return backend
+    from .builder import default_backend
+    return default_backend()
+
+
+def _torch(be, a, like=None) -> torch.Tensor:
+    """A backend array as a torch tensor on the device of `like` (the
+    caller's input) when that is a torch tensor, else where it lies."""
+    t = a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(be.host(a)))
+    if isinstance(like, torch.Tensor) and t.device != like.device:
+        t = t.to(like.device)
+    return t
+
+
+def _sample(n: int, m: int, seed: int) -> np.ndarray:
+    """`m` distinct rows of `n`, drawn with numpy's PCG64 under `seed`,
+    ascending (all rows when m >= n)."""
+    if m >= n:
+        return np.arange(n, dtype=np.int64)
+    return np.sort(np.random.default_rng(seed).choice(n, size=m, replace=False)).astype(np.int64)
+
+
 # ---------------------------------------------------------------------------
 # PQ
 # ---------------------------------------------------------------------------
 def train_pq(x: torch.Tensor, pq_dim: int, iters: int = 25, sample: int = 65536,
-             seed: int = 5) -> torch.Tensor:
-    """Per-subspace k-means (256 centres).  Returns C [256][D] float32."""
-    dev = x.device
+             seed: int = 5, backend=None) -> torch.Tensor:
+    """Per-subspace k-means (256 centres) on a row sample, from 256 distinct
+    sample rows (gofann_build_pq_train).  Returns C [256][D] float32."""
+    be = _backend(backend)
     n, d = x.shape
     assert d % pq_dim == 0
-    sub = d // pq_dim
-    g = torch.Generator(device="cpu")
-    g.manual_seed(seed)
-    idx = torch.randperm(n, generator=g)[: min(sample, n)].to(dev)
-    xs = x[idx].float().reshape(-1, pq_dim, sub).permute(1, 0, 2).contiguous()  # [M, s, sub]
-    s = xs.shape[1]
-    init = torch.randperm(s, generator=g)[:256].to(dev)
-    if s < 256:
-        init = torch.arange(256, device=dev) % s
-    cen = xs[:, init, :].clone()  # [M, 256, sub]
-    for _ in range(iters):
-        d2 = (xs * xs).sum(-1, keepdim=True) - 2 * torch.bmm(xs, cen.transpose(1, 2)) + \
-            (cen * cen).sum(-1)[:, None, :]
-        a = d2.argmin(-1)  # [M, s]
-        sums = torch.zeros_like(cen)
-        cnt = torch.zeros(pq_dim, 256, device=dev)
-        sums.scatter_add_(1, a[..., None].expand(-1, -1, sub), xs)
-        cnt.scatter_add_(1, a, torch.ones_like(a, dtype=torch.float32))
-        upd = cnt > 0
-        cen = torch.where(upd[..., None], sums / cnt.clamp(min=1)[..., None], cen)
-    return cen.permute(1, 0, 2).reshape(256, d).contiguous()
+    xb = be.rows(x)
+    idx = _sample(n, sample, seed)
+    xs = be.take(xb, idx)
+    s = len(idx)
+    rng = np.random.default_rng(seed + 1)
+    init = rng.choice(s, size=256, replace=False) if s >= 256 else np.arange(256) % s
+    c0 = be.take(xs, init)
+    c0 = c0.float() if isinstance(c0, torch.Tensor) else c0.astype(np.float32)
+    return _torch(be, be.pq_train(xs, c0, pq_dim, iters), x)
 
 
-def pq_encode(x: torch.Tensor, table: torch.Tensor, pq_dim: int, chunk: int = 1 << 18) -> torch.Tensor:
-    """Nearest centre per subspace -> codes u8 [N][M]."""
-    n, d = x.shape
-    sub = d // pq_dim
-    cen = table.reshape(256, pq_dim, sub).permute(1, 0, 2).contiguous()  # [M,256,sub]
-    cn = (cen * cen).sum(-1)  # [M,256]
-    out = torch.empty(n, pq_dim, dtype=torch.uint8, device=x.device)
-    for s in range(0, n, chunk):
-        e = min(n, s + chunk)
-        xs = x[s:e].float().reshape(e - s, pq_dim, sub).permute(1, 0, 2)  # [M,c,sub]
-        d2 = cn[:, None, :] - 2 * torch.bmm(xs, cen.transpose(1, 2))
-        out[s:e] = d2.argmin(-1).t().to(torch.uint8)
-    return out
+def pq_encode(x: torch.Tensor, table: torch.Tensor, pq_dim: int, backend=None) -> torch.Tensor:
+    """Nearest centre per subspace -> codes u8 [N][M] (gofann_build_pq_encode)."""
+    be = _backend(backend)
+    return _torch(be, be.pq_encode(be.rows(x), be.dev(table), pq_dim), x)
 
 
 # ---------------------------------------------------------------------------
 # Coarse k-means (graph buckets, RaBitQ anchors)
 # ---------------------------------------------------------------------------
 def train_kmeans(x: torch.Tensor, k: int, iters: int = 15, sample: int = 262144,
-                 seed: int = 6, chunk: int = 1 << 16) -> torch.Tensor:
+                 seed: int = 6, backend=None) -> torch.Tensor:
     """Seeded k-means over a uniform row sample of the base: k-means++
     seeding (D^2 sampling), then Lloyd iterations; an empty cluster keeps its
-    previous centre.  Returns [k][D] float32 on x's device.  The index is
-    built from these trained centres only (never from how the data was
-    generated): they bucket the graph builder's rows and become the RaBitQ
-    anchors."""
-    dev = x.device
-    n, d = x.shape
-    g = torch.Generator(device="cpu")
-    g.manual_seed(seed)
-    m = min(n, max(sample, k))
-    idx = torch.randperm(n, generator=g)[:m].to(dev) if m < n else torch.arange(n, device=dev)
-    xs = x[idx].float()
-    xn = (xs * xs).sum(1)
-    k = min(k, m)
-    cen = torch.empty(k, d, dtype=torch.float32, device=dev)
-    first = int(torch.randint(m, (1,), generator=g))
-    cen[0] = xs[first]
-    best = (xn - 2 * xs @ cen[0] + xn[first]).clamp_(min=0)
-    u = torch.rand(k, generator=g, dtype=torch.float64).to(dev)
-    for j in range(1, k):
-        cdf = torch.cumsum(best.double(), 0)
-        pick = torch.searchsorted(cdf, (u[j] * cdf[-1]).reshape(1)).clamp_(max=m - 1)
-        c = xs[pick[0]]
-        cen[j] = c
-        dj = (xn - 2 * xs @ c + (c * c).sum()).clamp_(min=0)
-        torch.minimum(best, dj, out=best)
-    for _ in range(iters):
-        cn = (cen * cen).sum(1)
-        assign = torch.empty(m, dtype=torch.int64, device=dev)
-        for s in range(0, m, chunk):
-            assign[s:s + chunk] = (cn[None, :] - 2 * xs[s:s + chunk] @ cen.t()).argmin(1)
-        sums = torch.zeros_like(cen).index_add_(0, assign, xs)
-        cnt = torch.bincount(assign, minlength=k).float()
-        cen = torch.where(cnt[:, None] > 0, sums / cnt.clamp(min=1)[:, None], cen)
-    return cen.contiguous()
+    previous centre (gofann_build_kmeanspp, gofann_build_kmeans).  Returns
+    [k][D] float32.  The index is built from these trained centres only
+    (never from how the data was generated): they bucket the graph builder's
+    rows and become the RaBitQ anchors.  Deterministic for a given seed."""
+    be = _backend(backend)
+    xb = be.rows(x)
+    n = x.shape[0]
+    idx = _sample(n, max(sample, k), seed)
+    xs = be.take(xb, idx)
+    k = min(k, len(idx))
+    c = be.kmeanspp(xs, k, seed)
+    return _torch(be, be.kmeans(xs, c, iters), x)
 
 
 # ---------------------------------------------------------------------------
@@ -138,47 +131,32 @@ def random_rotation(dim: int, padded: int, seed: int, device) -> torch.Tensor:
 
 
 def rabitq_encode(x: torch.Tensor, rotation: torch.Tensor, centroids: torch.Tensor,
-                  chunk: int = 1 << 16):
-    """Returns (codes u8 [N][P/8], factors f32 [N][3], anchor_ids u32 [N],
-    anchors f32 [A][P]).  Residual r = x R - c R; bit = r > 0 (MSB-first in
-    u32 words); f_add = |r|^2 + 2|r|^2 <c,xu>/<r,xu>, f_rescale =
-    -2|r|^2/<r,xu> with xu = bit - 0.5 (quantizer_gpu_fast.cu:207-235)."""
-    dev = x.device
-    n, d = x.shape
-    P = rotation.shape[1]
-    anchors = centroids.float() @ rotation  # [A, P]
-    an = (anchors * anchors).sum(1)
-    codes = torch.empty(n, P // 8, dtype=torch.uint8, device=dev)
-    factors = torch.empty(n, 3, dtype=torch.float32, device=dev)
-    aid = torch.empty(n, dtype=torch.int64, device=dev)
-    shifts = (31 - torch.arange(32, device=dev, dtype=torch.int64))
+                  chunk: int = 1 << 18, backend=None):
+    """Returns (codes u8 [N][P/8], factors f32 [N][3], anchor_ids i32 [N],
+    anchors f32 [A][P]).  Anchors = centroids R; each chunk of rows is
+    rotated (gofann_build_rotate) and encoded against its nearest anchor
+    (gofann_build_rabitq_encode): bit = (x R - c R) > 0, MSB-first in u32
+    words, f_add / f_rescale / f_err as quantizer_gpu_fast.cu:200-245."""
+    be = _backend(backend)
+    xb = be.rows(x)
+    n = x.shape[0]
+    anchors = be.rotate(be.rows(centroids), rotation)
+    parts = []
     for s in range(0, n, chunk):
         e = min(n, s + chunk)
-        xr = x[s:e].float() @ rotation  # [c, P]
-        a = ((xr * xr).sum(1, keepdim=True) - 2 * xr @ anchors.t() + an[None, :]).argmin(1)
-        aid[s:e] = a
-        c = anchors[a]
-        r = xr - c
-        bits = (r > 0)
-        xu = bits.float() - 0.5
-        l2 = (r * r).sum(1)
-        ip_r = (r * xu).sum(1)
-        ip_r = torch.where(ip_r == 0, torch.full_like(ip_r, float("inf")), ip_r)
-        ip_c = (c * xu).sum(1)
-        xu_sq = (xu * xu).sum(1)
-        f_add = l2 + 2.0 * l2 * (ip_c / ip_r)
-        f_rescale = -2.0 * l2 / ip_r
-        ratio = (l2 * xu_sq) / (ip_r * ip_r)
-        inner = torch.clamp((ratio - 1.0) / max(P - 1, 1), min=0.0)
-        f_err = 2.0 * torch.sqrt(l2.clamp(min=0)) * 1.9 * torch.sqrt(inner)
-        factors[s:e, 0] = f_add
-        factors[s:e, 1] = f_rescale
-        factors[s:e, 2] = f_err
-        w = bits.reshape(e - s, P // 32, 32).to(torch.int64)
-        words = (w << shifts).sum(-1)  # [c, P/32] values < 2^32
-        le = torch.stack([(words >> (8 * k)) & 0xFF for k in range(4)], dim=-1)
-        codes[s:e] = le.reshape(e - s, P // 8).to(torch.uint8)
-    return codes, factors, aid.to(torch.int32), anchors.contiguous()
+        xc = xb[s:e]
+        parts.append(be.rabitq_encode(be.rotate(xc, rotation), anchors))
+    if isinstance(anchors, torch.Tensor):
+        aid = torch.cat([p[0] for p in parts])
+        codes = torch.cat([p[1] for p in parts])
+        fac = torch.cat([p[2] for p in parts])
+        return (_torch(be, codes, x), _torch(be, fac, x), _torch(be, aid, x),
+                _torch(be, anchors.contiguous(), x))
+    aid = np.concatenate([p[0] for p in parts]).view(np.int32)
+    codes = np.concatenate([p[1] for p in parts])
+    fac = np.concatenate([p[2] for p in parts])
+    return (torch.from_numpy(codes), torch.from_numpy(fac), torch.from_numpy(aid),
+            torch.from_numpy(np.ascontiguousarray(anchors)))
 
 
 # ---------------------------------------------------------------------------
@@ -230,223 +208,168 @@ def postings_from_csr(offsets: np.ndarray, values: np.ndarray, num_labels: int):
     return cat_freq, post_off, post_ids
 
 
-def _row_norms(x: torch.Tensor, chunk: int = 1 << 18) -> torch.Tensor:
-    """Squared row norms of a large matrix, a chunk of rows at a time."""
-    out = torch.empty(x.shape[0], dtype=torch.float32, device=x.device)
-    for s0 in range(0, x.shape[0], chunk):
-        xs = x[s0:s0 + chunk].float()
-        out[s0:s0 + chunk] = (xs * xs).sum(1)
-    return out
+def _bucket_order(cl: np.ndarray):
+    """Rows of one label group ordered by bucket (stable: ascending row within
+    a bucket): the order, the distinct buckets, their row offsets in the
+    sorted space and each sorted row's bucket index."""
+    order = np.argsort(cl, kind="stable").astype(np.int64)
+    uniq, counts = np.unique(cl[order], return_counts=True)
+    off = np.zeros(len(uniq) + 1, np.uint32)
+    np.cumsum(counts, out=off[1:])
+    bucket_of = np.repeat(np.arange(len(uniq), dtype=np.uint32), counts)
+    return order, uniq, off, bucket_of
 
 
-# Groups above this many bytes of fp32 rows are built without full copies
-# (rows gathered per bucket batch, means and distances a chunk at a time).
-LEAN_GROUP_BYTES = 8 << 30
+def _u32h(be, a) -> np.ndarray:
+    h = be.host(a)
+    return h.view(np.uint32) if h.dtype == np.int32 else h.astype(np.uint32)
 
 
-def _bucket_knn(xg: torch.Tensor, bucket_of: torch.Tensor, k: int, max_batch_elems: int,
-                order: torch.Tensor | None = None):
-    """Exact k nearest rows inside each bucket (self excluded).  The rows
-    xg[order[i]] (xg[i] without `order`) are sorted by bucket.  Returns int64
-    [n, k] ids in that sorted row space, -1 where missing."""
-    dev = xg.device
-    n = xg.shape[0]
-    out = torch.full((n, k), -1, dtype=torch.int64, device=dev)
-    if n == 0 or k == 0:
-        return out
-    uniq, counts = torch.unique_consecutive(bucket_of, return_counts=True)
-    starts = torch.zeros_like(counts)
-    starts[1:] = torch.cumsum(counts, 0)[:-1]
-    counts_h = counts.cpu().numpy()
-    starts_h = starts.cpu().numpy()
-    i = 0
-    if order is None:
-        xn = (xg * xg).sum(1)
-    else:
-        xn = _row_norms(xg)[order]
-    border = order
-    order = np.argsort(counts_h, kind="stable")
-    while i < len(order):
-        bm = int(counts_h[order[i]])
-        j = i
-        # batch buckets of similar size (padding to the batch maximum)
-        while j < len(order) and counts_h[order[j]] <= max(bm, 1) * 1.25 + 8 and \
-                (j - i + 1) * int(counts_h[order[j]]) ** 2 <= max_batch_elems:
-            j += 1
-        j = max(j, i + 1)
-        sel = order[i:j]
-        bmax = int(counts_h[sel].max())
-        nb = len(sel)
-        st = torch.as_tensor(starts_h[sel], device=dev)
-        ct = torch.as_tensor(counts_h[sel], device=dev)
-        ar = torch.arange(bmax, device=dev)
-        rows = st[:, None] + ar[None, :]  # [nb, bmax]
-        valid = ar[None, :] < ct[:, None]
-        rows_c = torch.where(valid, rows, torch.zeros_like(rows))
-        xb = xg[rows_c] if border is None else xg[border[rows_c]]  # [nb, bmax, D]
-        d2 = xn[rows_c][:, :, None] + xn[rows_c][:, None, :] - 2 * torch.bmm(xb, xb.transpose(1, 2))
-        big = torch.finfo(d2.dtype).max
-        d2 = d2.masked_fill(~valid[:, None, :], big)
-        d2 = d2.masked_fill(torch.eye(bmax, dtype=torch.bool, device=dev)[None], big)
-        kk = min(k, bmax)
-        val, idx = torch.topk(d2, kk, dim=2, largest=False)
-        loc = torch.gather(rows_c, 1, idx.reshape(nb, -1)).reshape(nb, bmax, kk)
-        loc = torch.where(val < big, loc, torch.full_like(loc, -1))
-        dst = rows_c[valid]
-        out[dst, :kk] = loc[valid]
-        i = j
-    return out
+def _draw_unit(seed: int, stream: int, index: int) -> float:
+    """The build's counter-based uniform draw (SplitMix64's finaliser; the
+    same function as the device's draw64 in build_kernels.hip)."""
+    M = (1 << 64) - 1
+
+    def mix(z):
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return z ^ (z >> 31)
+    r = mix((mix(seed ^ ((stream * 0xD1B54A32D192ED03) & M)) + index * 0x9E3779B97F4A7C15) & M)
+    return (r >> 11) * (1.0 / 9007199254740992.0)
 
 
-def _compact_unique(cand: torch.Tensor, width: int) -> torch.Tensor:
-    """First `width` distinct non-negative entries of each row, in their
-    original order, padded with -1."""
-    n, w = cand.shape
-    srt, idx = torch.sort(cand, dim=1, stable=True)
-    dup_sorted = torch.zeros_like(srt, dtype=torch.bool)
-    dup_sorted[:, 1:] = srt[:, 1:] == srt[:, :-1]
-    dup = torch.zeros_like(dup_sorted).scatter_(1, idx, dup_sorted)
-    bad = dup | (cand < 0)
-    perm = torch.sort(bad.to(torch.int8), dim=1, stable=True).indices
-    out = torch.gather(cand, 1, perm)[:, :width]
-    out = torch.where(torch.gather(bad, 1, perm)[:, :width], torch.full_like(out, -1), out)
-    if out.shape[1] < width:
-        out = torch.cat([out, torch.full((n, width - out.shape[1]), -1, dtype=out.dtype,
-                                         device=out.device)], 1)
-    return out
+def repair_reach(be, graph: np.ndarray, entry: int, bucket_of: np.ndarray, seed: int,
+                 max_rounds: int = 64) -> int:
+    """Makes every row reachable from `entry` (the connectivity guarantee of
+    the reference's CAGRA build, graph_builder.cu:1295).  Each round walks
+    the graph from the entry (gofann_build_reach); in every bucket with
+    unreached rows the lowest unreached row becomes a root, and root u gets
+    an edge from reached row number floor(d_u * reached) (ascending rows;
+    d_u the build's draw (seed, stream 4, round * 2^32 + u)), written into
+    that row's last slot not yet used by the repair (at most half its
+    slots; a full row passes the edge to the next reached row).  Rounds
+    repeat until every row is reached.  Edits `graph` in place; returns the
+    number of edges added."""
+    n, R = graph.shape
+    uses = {}
+    added = 0
+    for rnd in range(max_rounds):
+        reached, cnt = be.reach(graph, entry)
+        if cnt >= n:
+            return added
+        rows_un = np.flatnonzero(~reached)
+        _, first = np.unique(bucket_of[rows_un], return_index=True)
+        roots = rows_un[first]
+        reached_rows = np.flatnonzero(reached)
+        for u in roots.tolist():
+            k = min(int(_draw_unit(seed, 4, (rnd << 32) + u) * cnt), cnt - 1)
+            for _ in range(cnt):
+                w = int(reached_rows[k])
+                used = uses.get(w, 0)
+                if used < R // 2:
+                    graph[w, R - 1 - used] = u
+                    uses[w] = used + 1
+                    added += 1
+                    break
+                k = (k + 1) % cnt
+    reached, cnt = be.reach(graph, entry)
+    if cnt < n:
+        raise RuntimeError(f"graph repair left {n - cnt} of {n} rows unreachable")
+    return added
 
 
-def build_group_graph(xg: torch.Tensor, cluster_of: torch.Tensor, centres: torch.Tensor,
-                      degree: int, local: int | None = None, near: int = 2,
-                      rep_local: int | None = None, rep_near: int | None = None, seed: int = 0,
-                      max_batch_elems: int = 1 << 27, return_reps: bool = False):
-    """Graph over the rows of one label group (rows in the given order).
+def build_group_graph(be, xs, order: np.ndarray, uniq: np.ndarray, off: np.ndarray,
+                      bucket_of: np.ndarray, centres, degree: int, local: int | None = None,
+                      near: int = 2, rep_local: int | None = None, rep_near: int | None = None,
+                      seed: int = 0, entry: int | None = None, design: str = "navigable",
+                      probe: int = 3):
+    """Graph over the rows of one label group.  `xs` holds the group's rows
+    sorted by bucket (`order[i]` is the caller row of sorted row i; `off`
+    the bucket offsets, `uniq` the bucket ids, `bucket_of` each sorted row's
+    bucket index); `entry` is the caller row every route starts from.
+    Returns (graph u32 [n][degree] in the caller's row order and ids,
+    bucket ids, bucket representatives as caller rows).
 
-    Rows are bucketed by their nearest coarse centre; each bucket has a
-    representative (the row nearest the bucket mean).  An ordinary row links
-    to its `local` exact nearest rows inside its bucket, its bucket's
-    representative, the representatives of the `near` nearest other buckets,
-    and uniformly drawn rows of the group up to the degree.  A
-    representative links to `rep_local` rows of its bucket, the
-    representatives of the `rep_near` nearest buckets, and drawn rows.
+    "navigable": a row links to its `local` exact nearest rows inside its
+    bucket, its bucket's representative (the row nearest the bucket mean),
+    the representatives of the `near` nearest other buckets (by centre
+    distance) and uniformly drawn rows up to the degree; a representative
+    links to `rep_local` rows of its bucket, the representatives of the
+    `rep_near` nearest buckets, and drawn rows; the entry row links to
+    `degree` drawn rows.  The drawn links make the graph searchable from
+    one entry row when bucket centres are spread without structure (a
+    mixture with random centres): distances to the wrong buckets then carry
+    no direction towards the right one, so a beam finds a query's bucket
+    only by seeing one of its rows, and every expansion that reveals fresh
+    buckets brings that closer.
 
-    The drawn links are what make the graph searchable from one entry row
-    when bucket centres are spread without structure (a mixture with random
-    centres): distances to the wrong buckets then carry no direction towards
-    the right one, so a beam finds a query's bucket only by seeing one of
-    its rows, and every expansion that reveals fresh buckets brings that
-    closer.  The in-bucket links then let the beam search the bucket, and
-    the nearest-bucket links cover clusters that the coarse centres split."""
-    dev = xg.device
-    n = xg.shape[0]
+    "cagra": the reference's recipe (build_cagra_graph_chunk,
+    graph_builder.cu:1279-1315; graph_degree R, intermediate degree 2R,
+    guarantee_connectivity): exact 2R nearest rows over the row's bucket and
+    its `probe` - 1 nearest buckets (gofann_build_knn), CAGRA's rank-based
+    pruning to R and reverse-edge merge (gofann_build_cagra_optimize), and
+    every row made reachable from the entry (repair_reach)."""
+    n = len(order)
     R = degree
+    nb = len(uniq)
+    cen = be.take(be.rows(centres), uniq)
+    cen = cen.float() if isinstance(cen, torch.Tensor) else cen.astype(np.float32)
+    inv = np.empty(n, np.int64)
+    inv[order] = np.arange(n)
+    entry_s = int(inv[entry]) if entry is not None else None
+    _, reps = be.bucket_reps(xs, off)
+    rep_row = order[_u32h(be, reps).astype(np.int64)].astype(np.uint32)
+    if design == "cagra":
+        kin = min(2 * R, 128)
+        p = max(1, min(probe, nb))
+        if p > 1:
+            near_b = _u32h(be, be.knn(cen, np.array([0, nb], np.uint32), p - 1))
+        else:
+            near_b = np.zeros((nb, 0), np.uint32)
+        plist = np.concatenate([np.arange(nb, dtype=np.uint32)[:, None], near_b], 1)
+        probe_off = np.arange(nb + 1, dtype=np.uint32) * p
+        knn = be.knn(xs, off, kin, probe_off, plist.reshape(-1))
+        _, g = be.cagra_optimize(knn, R)
+        g = _u32h(be, g).copy()
+        if entry_s is not None:
+            repair_reach(be, g, entry_s, bucket_of, seed)
+        out = np.full((n, R), UINT32_MAX, np.uint32)
+        valid = g < n
+        out[order] = np.where(valid, order[np.minimum(g, n - 1)], UINT32_MAX).astype(np.uint32)
+        return out, uniq.astype(np.int32), rep_row
     local = local if local is not None else R // 2
     rep_local = rep_local if rep_local is not None else max(R // 8, 1)
     rep_near = rep_near if rep_near is not None else max(R // 8, 1)
-    lean = n * xg.shape[1] * 4 > LEAN_GROUP_BYTES
-    xg = xg.float()
-    order = torch.argsort(cluster_of, stable=True)
-    bs = cluster_of[order]
-    xs = None if lean else xg[order]
-    if lean:
-        knn = _bucket_knn(xg, bs, local, max_batch_elems, order=order)
-    else:
-        knn = _bucket_knn(xs, bs, local, max_batch_elems)  # in sorted row space
-    uniq, counts = torch.unique_consecutive(bs, return_counts=True)
-    nb = uniq.shape[0]
-    bucket_idx = torch.repeat_interleave(torch.arange(nb, device=dev), counts)
-    # representative: row nearest its bucket mean
-    if lean:
-        b_orig = torch.searchsorted(uniq, cluster_of)
-        sums = torch.zeros(nb, xg.shape[1], device=dev)
-        for s0 in range(0, n, 1 << 18):
-            sums.index_add_(0, b_orig[s0:s0 + (1 << 18)], xg[s0:s0 + (1 << 18)])
-        means = sums / counts[:, None].float()
-        dm_o = torch.empty(n, dtype=torch.float32, device=dev)
-        for s0 in range(0, n, 1 << 18):
-            d = xg[s0:s0 + (1 << 18)] - means[b_orig[s0:s0 + (1 << 18)]]
-            dm_o[s0:s0 + (1 << 18)] = (d * d).sum(1)
-        dm = dm_o[order]
-    else:
-        sums = torch.zeros(nb, xs.shape[1], device=dev).index_add_(0, bucket_idx, xs)
-        means = sums / counts[:, None].float()
-        dm = ((xs - means[bucket_idx]) ** 2).sum(1)
-    big = torch.finfo(dm.dtype).max
-    for_min = torch.full((nb,), big, device=dev).scatter_reduce(0, bucket_idx, dm, "amin")
-    is_min = dm <= for_min[bucket_idx]
-    cand = torch.where(is_min, torch.arange(n, device=dev), torch.full_like(bucket_idx, n))
-    rep = torch.full((nb,), n, dtype=torch.int64, device=dev).scatter_reduce(0, bucket_idx, cand, "amin")
-    # nearest other buckets by coarse-centre distance
-    c = centres[uniq].float()
-    cd = ((c * c).sum(1)[:, None] + (c * c).sum(1)[None, :] - 2 * c @ c.t())
-    cd.fill_diagonal_(float("inf"))
+    kk = max(local, rep_local)
+    knn = be.knn(xs, off, kk) if kk > 0 else None
     m_near = min(max(rep_near, near), max(nb - 1, 0))
-    nn_b = torch.argsort(cd, dim=1)[:, :m_near]  # [nb, m_near]
-    ar = torch.arange(n, device=dev)
-    g = torch.Generator(device="cpu")
-    g.manual_seed(int(seed))
-    out = torch.empty(n, R, dtype=torch.int64, device=dev)
-    step = 1 << 20
-    for s0 in range(0, n, step):
-        s1 = min(n, s0 + step)
-        rows = ar[s0:s1]
-        b = bucket_idx[s0:s1]
-        own = rep[b][:, None]
-        own = torch.where(own == rows[:, None], torch.full_like(own, -1), own)
-        drawn = torch.randint(0, n, (s1 - s0, R), generator=g).to(dev)
-        drawn = torch.where(drawn == rows[:, None], torch.full_like(drawn, -1), drawn)
-        cand = torch.cat([knn[s0:s1], own, rep[nn_b[b, :near]], drawn], dim=1)
-        out[s0:s1] = _compact_unique(cand, R)
-    # representatives: a few in-bucket rows, the nearest buckets' reps, drawn rows
-    drawn = torch.randint(0, n, (nb, R), generator=g).to(dev)
-    rep_cand = torch.cat([knn[rep, :rep_local], rep[nn_b[:, :rep_near]], drawn], dim=1)
-    rep_cand = torch.where(rep_cand == rep[:, None], torch.full_like(rep_cand, -1), rep_cand)
-    out[rep] = _compact_unique(rep_cand, R)
-    # back to the caller's row order
-    # sorted position i is the caller's row order[i]; so are its edge targets
-    mapped = torch.where(out >= 0, order[out.clamp(min=0)], torch.full_like(out, -1))
-    res = torch.empty_like(mapped)
-    res[order] = mapped
-    res_np = res.cpu().numpy()
-    graph_np = np.where(res_np >= 0, res_np, 0xFFFFFFFF).astype(np.uint32)
-    if return_reps:
-        # (cluster id, representative row in the caller's order) per bucket
-        return graph_np, uniq.cpu().numpy().astype(np.int32), \
-            order[rep].cpu().numpy().astype(np.uint32)
-    return graph_np
+    if m_near > 0:
+        near_b = be.knn(cen, np.array([0, nb], np.uint32), m_near)
+    else:
+        near_b = np.zeros((nb, 0), np.uint32)
+    graph = be.links(knn, bucket_of, reps, near_b, order.astype(np.uint32), R, local,
+                     min(near, m_near), rep_local, min(rep_near, m_near), entry_s, seed)
+    return graph, uniq.astype(np.int32), rep_row
 
 
-def entry_adjacency(seed_row: int, rows: int, degree: int, seed: int) -> np.ndarray:
-    """Adjacency of a group's entry row (its medoid, where every route of the
-    group starts): `degree` distinct rows drawn uniformly from the group, so
-    that the first expansion already reveals as many buckets as it can."""
-    rng = np.random.default_rng(seed)
-    m = min(degree, rows - 1)
-    pick = rng.choice(rows - 1, size=m, replace=False) if m > 0 else np.zeros(0, np.int64)
-    pick = pick + (pick >= seed_row)  # skip the entry row itself
-    out = np.full(degree, UINT32_MAX, dtype=np.uint32)
-    out[:m] = pick.astype(np.uint32)
-    return out
-
-
-def nearest_centre(x: torch.Tensor, centres: torch.Tensor, chunk: int = 1 << 18) -> torch.Tensor:
-    c = centres.float()
-    cn = (c * c).sum(1)
-    out = torch.empty(x.shape[0], dtype=torch.int64, device=x.device)
-    for s in range(0, x.shape[0], chunk):
-        e = min(x.shape[0], s + chunk)
-        xs = x[s:e].float()
-        out[s:e] = (cn[None, :] - 2 * xs @ c.t()).argmin(1)
-    return out
+def nearest_centre(x: torch.Tensor, centres: torch.Tensor, backend=None) -> np.ndarray:
+    """Nearest trained centre of each row (gofann_build_assign), on the host."""
+    be = _backend(backend)
+    return _u32h(be, be.assign(be.rows(x), be.rows(centres))).astype(np.int64)
 
 
 def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_values: np.ndarray,
                       num_labels: int, centres: torch.Tensor, degree: int,
                       threshold: int = 2000, progress=None,
-                      graph_seed: int = 6, local: int | None = None) -> LabelIndex:
-    """Label-partitioned graphs for labels with more than `threshold` rows.
+                      graph_seed: int = 6, local: int | None = None, design: str = "navigable",
+                      probe: int = 3, backend=None) -> LabelIndex:
+    """Label-partitioned graphs for labels with more than `threshold` rows,
+    built on the GPU (`design` "navigable" or "cagra", see
+    build_group_graph).  Rows are bucketed by their nearest trained centre;
+    each group's seed is its medoid (gofann_build_medoid).
     `progress(msg)` (optional) is called about every 30 s of building."""
     import time
+    be = _backend(backend)
     cat_freq, post_off, post_ids = postings_from_csr(label_offsets, label_values, num_labels)
     graph_labels = np.nonzero(cat_freq > threshold)[0]
     label_size = np.zeros(num_labels, dtype=np.uint32)
@@ -459,7 +382,9 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
     row_to_sample = np.zeros(total, dtype=np.uint32)
     graph = np.full((total, degree), UINT32_MAX, dtype=np.uint32)
     seed_local = np.full(num_labels, UINT32_MAX, dtype=np.uint32)
-    cluster = nearest_centre(base, centres)
+    xb = be.rows(base)
+    cen = be.rows(centres)
+    cluster = nearest_centre(xb, cen, backend=be)
     rep_cluster = [np.zeros(0, np.int32)] * num_labels
     rep_row = [np.zeros(0, np.uint32)] * num_labels
     t_last = time.time()
@@ -468,37 +393,25 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
             progress(f"label graphs: {done}/{len(graph_labels)} labels built")
             t_last = time.time()
         s0, s1 = int(post_off[l]), int(post_off[l + 1])
-        samples = post_ids[s0:s1]
+        samples = post_ids[s0:s1].astype(np.int64)
         o = int(label_offset[l])
         row_to_sample[o:o + len(samples)] = samples
-        sidx = torch.as_tensor(samples.astype(np.int64), device=base.device)
-        whole = len(samples) == base.shape[0] and base.dtype == torch.float32
-        xg = base if whole else base[sidx].float()  # every row, in order: no copy
+        whole = len(samples) == int(base.shape[0])
+        # seed: row nearest the group mean (fp64), dataloader.cpp:7361-7406,
+        # on the group's rows in their local (ascending sample) order
+        xg = xb if whole else be.take(xb, samples)
+        seed_local[l] = be.medoid(xg)
+        xg = None
+        order, uniq, off, bucket_of = _bucket_order(cluster[samples])
+        xs = be.take(xb, samples[order])
         graph[o:o + len(samples)], rep_cluster[l], rep_row[l] = build_group_graph(
-            xg, cluster[sidx], centres, degree, local=local, seed=graph_seed + int(l),
-            return_reps=True)
-        # seed: row nearest the group mean (fp64), dataloader.cpp:7361-7406
-        if xg.shape[0] * xg.shape[1] * 4 > LEAN_GROUP_BYTES:
-            step = 1 << 16
-            mu = torch.zeros(1, xg.shape[1], dtype=torch.float64, device=xg.device)
-            for s0 in range(0, xg.shape[0], step):
-                mu += xg[s0:s0 + step].double().sum(0, keepdim=True)
-            mu /= xg.shape[0]
-            dist = torch.empty(xg.shape[0], dtype=torch.float64, device=xg.device)
-            for s0 in range(0, xg.shape[0], step):
-                dist[s0:s0 + step] = ((xg[s0:s0 + step].double() - mu) ** 2).sum(1)
-            seed_local[l] = int(dist.argmin())
-        else:
-            xd = xg.double()
-            mu = xd.mean(0, keepdim=True)
-            seed_local[l] = int(((xd - mu) ** 2).sum(1).argmin())
-        # the entry row's adjacency fans out over the navigation layer
-        sl = int(seed_local[l])
-        graph[o + sl] = entry_adjacency(sl, len(samples), degree, graph_seed + 7919 * int(l))
+            be, xs, order, uniq, off, bucket_of, cen, degree, local=local,
+            seed=graph_seed + int(l), entry=int(seed_local[l]), design=design, probe=probe)
+        xs = None
     rep_off = np.zeros(num_labels + 1, dtype=np.int64)
     np.cumsum([len(r) for r in rep_row], out=rep_off[1:])
     return LabelIndex(num_labels, threshold, cat_freq, label_offset, label_size, row_to_sample,
                       graph, seed_local, post_off, post_ids,
                       label_offsets.astype(np.uint32), label_values.astype(np.uint32), degree,
                       rep_off, np.concatenate(rep_cluster), np.concatenate(rep_row),
-                      centres.detach().float().cpu().numpy())
+                      be.host(cen).astype(np.float32))

@@ -730,6 +730,170 @@ int gofann_pq_codes_read(const char* path, uint64_t row_begin, uint64_t row_coun
 int gofann_pq_files_write(const char* pivots_path, const char* codes_path, const float* centroids,
                           uint32_t dim, uint32_t pq_dim, const uint8_t* codes, uint64_t rows);
 
+/* ---- index construction on the GPU (offline build).  The reference builds
+ * its per-label graphs with cuVS CAGRA (build_cagra_graph_chunk,
+ * src/index/graph_builder.cu:1279-1315: graph_degree R, intermediate degree
+ * 2R, guarantee_connectivity), its PQ codebooks and codes with cuVS PQ
+ * (tools/quantization/pq_builder.cu:49-153) and its RaBitQ codes with the
+ * vendored IVF-RaBitQ encoder (third_party/cuvs_rabitq/src/neighbors/
+ * ivf_rabitq/gpu_index/quantizer_gpu_fast.cu:39-101, 180-265).  These entry
+ * points replace those calls.  Every output is defined by a fixed
+ * arithmetic order and is deterministic:
+ *   score of a row x against a centre c: |c|^2 - 2 <x, c>, both sums in
+ *     fp32 with fmaf over d ascending; the nearest centre is the least
+ *     (score, index);
+ *   distance between two rows: sum_d (x_d - y_d)^2, fmaf over d ascending;
+ *   ties always go to the lower index.
+ * All arrays are device memory unless stated; rows are [n][dim] of
+ * elem (GOFANN_ELEM_U8 / F32 / F16), centres f32. */
+
+/* Nearest centre of each row: out_idx[i] = the least (score, k) over the k
+ * centres [k][dim]; out_score (optional) = that score. */
+int gofann_build_assign(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                        const float* centres, uint32_t k, uint32_t* out_idx, float* out_score);
+
+/* k-means++ seeding (D^2 sampling) of k centres from the rows: the first
+ * centre is row floor(u_0 n); centre j is the first row whose running sum
+ * of best distances (fp64, rows ascending, in 1024 chunks whose sums are
+ * added in order) reaches u_j times the total, where best is each row's
+ * distance to its nearest chosen centre (lane-strided fmaf sums over 64
+ * lanes, then an xor butterfly) and u_j the j-th uniform draw of SplitMix64
+ * under `seed`.  Writes centres [k][dim]. */
+int gofann_build_kmeanspp(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                          uint32_t k, uint64_t seed, float* centres);
+
+/* `iters` Lloyd iterations on centres [k][dim] in place: assign each row to
+ * its nearest centre, then each centre becomes the mean of its rows (fp64
+ * sums over its rows in ascending order, rounded to fp32); a centre with no
+ * row keeps its value.  n < 2^31. */
+int gofann_build_kmeans(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                        uint32_t k, uint32_t iters, float* centres);
+
+/* Rows sorted by bucket: bucket b holds rows [bucket_offsets[b],
+ * bucket_offsets[b+1]) and bucket_offsets[buckets] == rows.  A row's
+ * candidates are the rows of every bucket on its bucket's probe list
+ * (probe_buckets[probe_offsets[b] .. probe_offsets[b+1]), no repeats), or of
+ * its own bucket when probe_offsets is NULL. */
+typedef struct {
+    const uint32_t* bucket_offsets; /* [buckets + 1] */
+    uint32_t buckets;
+    uint32_t rows;
+    const uint32_t* probe_offsets;  /* [buckets + 1] or NULL */
+    const uint32_t* probe_buckets;
+} gofann_build_buckets;
+
+/* Exact k nearest candidates of every row (the row itself excluded), as
+ * (distance, row) pairs ascending: out_ids [rows][k] rows of the sorted
+ * space (UINT32_MAX past the candidates), out_dists [rows][k] (optional;
+ * FLT_MAX past them).  k <= 128.  Replaces the kNN stage of the CAGRA build
+ * (intermediate_graph_degree, graph_builder.cu:1293). */
+int gofann_build_knn(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim,
+                     const gofann_build_buckets* buckets, uint32_t k, uint32_t* out_ids,
+                     float* out_dists);
+
+/* PQ codebook training: `iters` Lloyd iterations per subspace on
+ * centroids [256][dim] in place (subspace m owns dims [m dim/pq_dim,
+ * (m+1) dim/pq_dim)); codes by the rule of gofann_build_pq_encode, means as
+ * gofann_build_kmeans.  Replaces pq::build (pq_builder.cu:92). */
+int gofann_build_pq_train(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                          uint32_t pq_dim, uint32_t iters, float* centroids);
+
+/* PQ codes: codes[i * code_stride + m] = the least (sum_t (x - c)^2 over the
+ * subspace's dims, fmaf ascending; centre index) over the 256 centres.
+ * Replaces pq::transform (pq_builder.cu:129). */
+int gofann_build_pq_encode(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                           uint32_t pq_dim, const float* centroids, uint8_t* codes,
+                           uint32_t code_stride);
+
+/* Rotation of base rows for RaBitQ: out [n][padded_dim] = rows [n][dim]
+ * (as f32) times rotation [dim][padded_dim] (FP32 SGEMM through rocBLAS, as
+ * the query rotation).  The caller takes rows in chunks. */
+int gofann_build_rotate(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim, uint32_t n,
+                        const float* rotation, uint32_t padded_dim, float* out);
+
+/* One-bit RaBitQ encoding of rotated rows [n][padded_dim] against anchors
+ * [num_anchors][padded_dim] (the rotated centres): anchor_ids = nearest
+ * anchor (gofann_build_assign's rule); r = row - anchor; codes [n][P/8]
+ * MSB-first u32 words (dim d is bit 31 - d % 32 of word d / 32, bit = r > 0);
+ * factors [n][3] = f_add, f_rescale, f_err by the reference encoder's
+ * formulas (quantizer_gpu_fast.cu:200-245), the sums over lanes d % 64
+ * (fmaf) followed by an xor butterfly. */
+int gofann_build_rabitq_encode(gofann_ctx* ctx, const float* rotated, uint32_t n,
+                               uint32_t padded_dim, const float* anchors, uint32_t num_anchors,
+                               uint32_t* anchor_ids, uint8_t* codes, float* factors);
+
+/* The row nearest the rows' mean (the graph seed of a label group,
+ * build_seed_local_ids_typed, dataloader.cpp:7361-7406): the mean in fp64
+ * (sums over blocks of 4096 rows, rows ascending, blocks added in order,
+ * divided by n), distances in fp64 (fma over d ascending), the least
+ * (distance, row).  *out_row is a host pointer. */
+int gofann_build_medoid(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim, uint64_t n,
+                        uint32_t* out_row);
+
+/* Per bucket of bucket-sorted rows: means [buckets][dim] (fp64 sums over the
+ * bucket's rows ascending, rounded to fp32) and reps [buckets], the row
+ * nearest the mean (fp32 distance, least (distance, row); UINT32_MAX for an
+ * empty bucket). */
+int gofann_build_bucket_reps(gofann_ctx* ctx, const void* rows, int elem, uint32_t dim,
+                             const uint32_t* bucket_offsets, uint32_t buckets, float* means,
+                             uint32_t* reps);
+
+/* This repo's graph (no counterpart in the reference, whose CAGRA graphs
+ * it replaces): for row i of the bucket-sorted space, the candidate
+ * sequence is
+ *   ordinary row: knn[i][0 .. local), reps[bucket_of[i]], reps of
+ *     near_buckets[b][0 .. near_links), then R draws;
+ *   bucket representative: knn[i][0 .. rep_local), reps of
+ *     near_buckets[b][0 .. rep_near), then R draws;
+ *   entry_row: 4 R draws;
+ * where draw j of row i is SplitMix64(seed, stream, i * 256 + j) mod rows
+ * (streams 1, 2 and 3 for the three kinds).  The row keeps the first
+ * `degree` distinct valid candidates other than itself; UINT32_MAX pads.
+ * out_graph [rows][degree] is in the caller's row order: row order[i] of
+ * out_graph holds order[candidate]. */
+typedef struct {
+    uint32_t rows;
+    const uint32_t* knn;          /* [rows][knn_width] sorted-space rows */
+    uint32_t knn_width;
+    const uint32_t* bucket_of;    /* [rows] */
+    const uint32_t* reps;         /* [buckets] */
+    const uint32_t* near_buckets; /* [buckets][near_width] */
+    uint32_t near_width;
+    uint32_t buckets;
+    const uint32_t* order;        /* [rows] caller row of each sorted row */
+} gofann_build_link_inputs;
+typedef struct {
+    uint32_t degree;
+    uint32_t local;
+    uint32_t near_links;
+    uint32_t rep_local;
+    uint32_t rep_near;
+    uint32_t entry_row;  /* sorted space; UINT32_MAX: none */
+    uint64_t seed;
+} gofann_build_link_params;
+int gofann_build_links(gofann_ctx* ctx, const gofann_build_link_inputs* inputs,
+                       const gofann_build_link_params* params, uint32_t* out_graph);
+
+/* CAGRA's graph optimisation, written from the published method (Ootomo
+ * et al., ICDE 2024, sec. IV-B) for the reference's graph_degree /
+ * intermediate_graph_degree recipe (graph_builder.cu:1291-1293): knn
+ * [n][kin] lists ascending by (distance, row); pruned [n][degree] = each
+ * row's entries of least (detour count, rank), where the entry at rank j
+ * counts a detour for every entry u at rank m whose own list holds it at
+ * rank r with max(m, r) < j; out_graph [n][degree] = the first degree / 2
+ * pruned edges, then reverse edges in order of (rank in the source's
+ * pruned list, source row), then the remaining pruned edges, without
+ * repeats (at most 2 degree reverse edges are considered).  n < 2^27,
+ * degree <= kin <= 128. */
+int gofann_build_cagra_optimize(gofann_ctx* ctx, const uint32_t* knn, uint32_t n, uint32_t kin,
+                                uint32_t degree, uint32_t* pruned, uint32_t* out_graph);
+
+/* Rows reachable from entry_row by the graph's edges: reached [n] u32 flags
+ * (device), *reached_count (host) their number.  The connectivity check of
+ * guarantee_connectivity (graph_builder.cu:1295). */
+int gofann_build_reach(gofann_ctx* ctx, const uint32_t* graph, uint32_t n, uint32_t degree,
+                       uint32_t entry_row, uint32_t* reached, uint32_t* reached_count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -342,6 +342,40 @@ int orc_merge_routes(const uint32_t* route_to_query, uint32_t routes,
                      const float* route_dists, uint32_t width, uint32_t topk,
                      uint32_t* out_ids, float* out_dists);
 
+
+/* ---- index construction (oracle/build_oracle.c): the GPU build's
+ * definitions (include/gofann_hip.h gofann_build_*), restated.  elem: 0 u8,
+ * 1 f32, 2 f16 (as uint16 bits). */
+uint64_t orc_build_draw64(uint64_t seed, uint64_t stream, uint64_t index);
+double orc_build_draw_unit(uint64_t seed, uint64_t stream, uint64_t index);
+void orc_build_assign(const void* rows, int elem, uint32_t dim, uint64_t n, const float* centres,
+                      uint32_t k, uint32_t* out_idx, float* out_score);
+void orc_build_kmeanspp(const void* rows, int elem, uint32_t dim, uint64_t n, uint32_t k,
+                        uint64_t seed, float* centres);
+void orc_build_kmeans(const void* rows, int elem, uint32_t dim, uint64_t n, uint32_t k,
+                      uint32_t iters, float* centres);
+void orc_build_knn(const void* rows, int elem, uint32_t dim, const uint32_t* bucket_off,
+                   uint32_t buckets, const uint32_t* probe_off, const uint32_t* probe, uint32_t k,
+                   uint32_t* out_ids, float* out_d);
+void orc_build_pq_encode(const void* rows, int elem, uint32_t dim, uint64_t n, uint32_t pq_dim,
+                         const float* centroids, uint8_t* codes, uint32_t code_stride);
+void orc_build_pq_train(const void* rows, int elem, uint32_t dim, uint64_t n, uint32_t pq_dim,
+                        uint32_t iters, float* centroids);
+void orc_build_rabitq_encode(const float* xr, uint32_t n, uint32_t P, const float* anchors,
+                             uint32_t A, uint32_t* aid, uint8_t* codes, float* factors);
+uint32_t orc_build_medoid(const void* rows, int elem, uint32_t dim, uint64_t n);
+void orc_build_bucket_reps(const void* rows, int elem, uint32_t dim, const uint32_t* bucket_off,
+                           uint32_t buckets, float* means, uint32_t* reps);
+void orc_build_links(uint32_t n, const uint32_t* knn, uint32_t knn_width, const uint32_t* bucket_of,
+                     const uint32_t* reps, const uint32_t* near, uint32_t near_width, uint32_t buckets,
+                     const uint32_t* order, uint32_t degree, uint32_t local, uint32_t near_links,
+                     uint32_t rep_local, uint32_t rep_near, uint32_t entry, uint64_t seed,
+                     uint32_t* out);
+void orc_build_cagra_optimize(const uint32_t* knn, uint32_t n, uint32_t kin, uint32_t degree,
+                              uint32_t* pruned, uint32_t* out);
+uint32_t orc_build_reach(const uint32_t* graph, uint32_t n, uint32_t degree, uint32_t entry,
+                         uint32_t* reached);
+
 #ifdef __cplusplus
 }
 #endif

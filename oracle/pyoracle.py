@@ -565,3 +565,231 @@ def exact_search(index, routes, pred, base, queries, queue_limit=64, topk=10,
                             U32(n), p(ids), p(dists), stats, threads=threads)
     assert rc == 0
     return ids[:n], dists[:n], stats_array(stats, n)
+
+
+# ---- index construction (build_oracle.c) --------------------------------
+U64 = C.c_uint64
+_BUILD_SIGS = {
+    "orc_build_draw64": (U64, [U64, U64, U64]),
+    "orc_build_draw_unit": (C.c_double, [U64, U64, U64]),
+    "orc_build_assign": (None, [P, C.c_int, U32, U64, P, U32, P, P]),
+    "orc_build_kmeanspp": (None, [P, C.c_int, U32, U64, U32, U64, P]),
+    "orc_build_kmeans": (None, [P, C.c_int, U32, U64, U32, U32, P]),
+    "orc_build_knn": (None, [P, C.c_int, U32, P, U32, P, P, U32, P, P]),
+    "orc_build_pq_encode": (None, [P, C.c_int, U32, U64, U32, P, P, U32]),
+    "orc_build_pq_train": (None, [P, C.c_int, U32, U64, U32, U32, P]),
+    "orc_build_rabitq_encode": (None, [P, U32, U32, P, U32, P, P, P]),
+    "orc_build_medoid": (U32, [P, C.c_int, U32, U64]),
+    "orc_build_bucket_reps": (None, [P, C.c_int, U32, P, U32, P, P]),
+    "orc_build_links": (None, [U32, P, U32, P, P, P, U32, U32, P, U32, U32, U32, U32, U32, U32,
+                               U64, P]),
+    "orc_build_cagra_optimize": (None, [P, U32, U32, U32, P, P]),
+    "orc_build_reach": (U32, [P, U32, U32, U32, P]),
+}
+
+
+def _blib():
+    L = lib()
+    if not getattr(L, "_build_ready", False):
+        for name, (res, args) in _BUILD_SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        L._build_ready = True
+    return L
+
+
+def _rows(rows):
+    """(contiguous array, elem code) of a row matrix: u8 0, f32 1, f16 2."""
+    a = np.ascontiguousarray(rows)
+    elem = {np.dtype(np.uint8): 0, np.dtype(np.float32): 1, np.dtype(np.float16): 2}[a.dtype]
+    return a, elem
+
+
+def build_draw64(seed, stream, index):
+    return int(_blib().orc_build_draw64(seed, stream, index))
+
+
+def build_draw_unit(seed, stream, index):
+    return float(_blib().orc_build_draw_unit(seed, stream, index))
+
+
+def build_assign(rows, centres):
+    a, elem = _rows(rows)
+    c = np.ascontiguousarray(centres, np.float32)
+    idx = np.empty(a.shape[0], np.uint32)
+    score = np.empty(a.shape[0], np.float32)
+    _blib().orc_build_assign(p(a), elem, a.shape[1], a.shape[0], p(c), c.shape[0], p(idx), p(score))
+    return idx, score
+
+
+def build_kmeanspp(rows, k, seed):
+    a, elem = _rows(rows)
+    out = np.empty((k, a.shape[1]), np.float32)
+    _blib().orc_build_kmeanspp(p(a), elem, a.shape[1], a.shape[0], k, seed, p(out))
+    return out
+
+
+def build_kmeans(rows, centres, iters):
+    a, elem = _rows(rows)
+    c = np.array(centres, np.float32, copy=True)
+    _blib().orc_build_kmeans(p(a), elem, a.shape[1], a.shape[0], c.shape[0], iters, p(c))
+    return c
+
+
+def build_knn(rows, bucket_off, k, probe_off=None, probe=None):
+    a, elem = _rows(rows)
+    bo = np.ascontiguousarray(bucket_off, np.uint32)
+    po = c_arr(probe_off, np.uint32)
+    pb = c_arr(probe, np.uint32)
+    n = int(bo[-1])
+    ids = np.empty((n, k), np.uint32)
+    d = np.empty((n, k), np.float32)
+    _blib().orc_build_knn(p(a), elem, a.shape[1], p(bo), len(bo) - 1, p(po), p(pb), k, p(ids), p(d))
+    return ids, d
+
+
+def build_pq_encode(rows, centroids, pq_dim):
+    a, elem = _rows(rows)
+    c = np.ascontiguousarray(centroids, np.float32)
+    codes = np.empty((a.shape[0], pq_dim), np.uint8)
+    _blib().orc_build_pq_encode(p(a), elem, a.shape[1], a.shape[0], pq_dim, p(c), p(codes), pq_dim)
+    return codes
+
+
+def build_pq_train(rows, centroids, pq_dim, iters):
+    a, elem = _rows(rows)
+    c = np.array(centroids, np.float32, copy=True)
+    _blib().orc_build_pq_train(p(a), elem, a.shape[1], a.shape[0], pq_dim, iters, p(c))
+    return c
+
+
+def build_rabitq_encode(rotated, anchors):
+    x = np.ascontiguousarray(rotated, np.float32)
+    an = np.ascontiguousarray(anchors, np.float32)
+    n, P_ = x.shape
+    aid = np.empty(n, np.uint32)
+    codes = np.empty((n, P_ // 8), np.uint8)
+    fac = np.empty((n, 3), np.float32)
+    _blib().orc_build_rabitq_encode(p(x), n, P_, p(an), an.shape[0], p(aid), p(codes), p(fac))
+    return aid, codes, fac
+
+
+def build_medoid(rows):
+    a, elem = _rows(rows)
+    return int(_blib().orc_build_medoid(p(a), elem, a.shape[1], a.shape[0]))
+
+
+def build_bucket_reps(rows, bucket_off):
+    a, elem = _rows(rows)
+    bo = np.ascontiguousarray(bucket_off, np.uint32)
+    nb = len(bo) - 1
+    means = np.empty((nb, a.shape[1]), np.float32)
+    reps = np.empty(nb, np.uint32)
+    _blib().orc_build_bucket_reps(p(a), elem, a.shape[1], p(bo), nb, p(means), p(reps))
+    return means, reps
+
+
+def build_links(knn, bucket_of, reps, near, order, degree, local, near_links, rep_local,
+                rep_near, entry, seed):
+    knn = np.ascontiguousarray(knn, np.uint32)
+    n = int(bucket_of.shape[0])
+    bo = np.ascontiguousarray(bucket_of, np.uint32)
+    rp = np.ascontiguousarray(reps, np.uint32)
+    nr = np.ascontiguousarray(near, np.uint32)
+    od = np.ascontiguousarray(order, np.uint32)
+    out = np.empty((n, degree), np.uint32)
+    _blib().orc_build_links(n, p(knn), knn.shape[1] if knn.ndim == 2 else 0, p(bo), p(rp), p(nr),
+                            nr.shape[1] if nr.ndim == 2 else 0, rp.shape[0], p(od), degree, local,
+                            near_links, rep_local, rep_near,
+                            0xFFFFFFFF if entry is None else int(entry), seed, p(out))
+    return out
+
+
+def build_cagra_optimize(knn, degree):
+    knn = np.ascontiguousarray(knn, np.uint32)
+    n, kin = knn.shape
+    pruned = np.empty((n, degree), np.uint32)
+    out = np.empty((n, degree), np.uint32)
+    _blib().orc_build_cagra_optimize(p(knn), n, kin, degree, p(pruned), p(out))
+    return pruned, out
+
+
+def build_reach(graph, entry):
+    g = np.ascontiguousarray(graph, np.uint32)
+    n, deg = g.shape
+    reached = np.empty(n, np.uint32)
+    cnt = _blib().orc_build_reach(p(g), n, deg, entry, p(reached))
+    return reached.astype(bool), int(cnt)
+
+
+class OracleBuild:
+    """The index-construction primitives of gofann_amd.builder.HipBuild,
+    restated on the CPU (build_oracle.c), over numpy arrays.  Tests pass it
+    to gofann_amd.index's builders to build fixtures on the CPU, and to
+    check the GPU build step for step; the product never selects it."""
+
+    def rows(self, x):
+        if hasattr(x, "detach"):
+            x = x.detach().cpu().numpy()
+        x = np.asarray(x)
+        if x.dtype not in (np.uint8, np.float32, np.float16):
+            x = x.astype(np.float32)
+        return np.ascontiguousarray(x)
+
+    def take(self, rows, idx):
+        return np.ascontiguousarray(rows[np.asarray(idx, np.int64)])
+
+    def host(self, a):
+        if hasattr(a, "detach"):
+            a = a.detach().cpu().numpy()
+        return np.asarray(a)
+
+    def dev(self, a, dtype=None):
+        a = self.host(a)
+        return a if dtype is None else a.astype(dtype)
+
+    def assign(self, rows, centres):
+        return build_assign(rows, self.host(centres))[0]
+
+    def kmeanspp(self, rows, k, seed):
+        return build_kmeanspp(rows, k, seed)
+
+    def kmeans(self, rows, centres, iters):
+        return build_kmeans(rows, self.host(centres), iters)
+
+    def knn(self, rows, bucket_off, k, probe_off=None, probe=None):
+        return build_knn(rows, bucket_off, k, probe_off, probe)[0]
+
+    def bucket_reps(self, rows, bucket_off):
+        return build_bucket_reps(rows, bucket_off)
+
+    def medoid(self, rows):
+        return build_medoid(rows)
+
+    def links(self, knn, bucket_of, reps, near, order, degree, local, near_links, rep_local,
+              rep_near, entry, seed):
+        knn = np.zeros((len(bucket_of), 0), np.uint32) if knn is None else self.host(knn)
+        return build_links(knn.view(np.uint32) if knn.dtype == np.int32 else knn, bucket_of,
+                           self.host(reps), self.host(near), order, degree, local, near_links,
+                           rep_local, rep_near, 0xFFFFFFFF if entry is None else int(entry), seed)
+
+    def cagra_optimize(self, knn, degree):
+        return build_cagra_optimize(self.host(knn), degree)
+
+    def reach(self, graph, entry):
+        return build_reach(self.host(graph), int(entry))
+
+    def pq_train(self, rows, centroids, pq_dim, iters):
+        return build_pq_train(rows, self.host(centroids), pq_dim, iters)
+
+    def pq_encode(self, rows, centroids, pq_dim):
+        return build_pq_encode(rows, self.host(centroids), pq_dim)
+
+    def rotate(self, rows, rotation):
+        # fp64 product rounded to fp32 (the GPU's rocBLAS SGEMM is checked
+        # against the same fp64 product within a tolerance)
+        return (rows.astype(np.float64) @ self.host(rotation).astype(np.float64)).astype(np.float32)
+
+    def rabitq_encode(self, rotated, anchors):
+        return build_rabitq_encode(rotated, self.host(anchors))

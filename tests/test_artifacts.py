@@ -21,6 +21,9 @@ from gofann_amd import artifacts as ga
 from gofann_amd import index as gi
 from gofann_amd import synth
 
+# the index is built by the oracle's restatement of the GPU build (no GPU here)
+CPU_BUILD = po.OracleBuild()
+
 U32MAX = 0xFFFFFFFF
 
 
@@ -167,7 +170,8 @@ def test_group_layout_checksum():
 def small_index():
     wl = synth.small_labelled(n=3000, nq=4, dim=16, k=8, labels=6, seed=11)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=8, threshold=300)
+                              wl.centroids, degree=8, threshold=300,
+                              backend=CPU_BUILD)
     return wl, li
 
 
@@ -321,7 +325,7 @@ def rabitq_parts():
     x = torch.randn(n, dim)
     rot = gi.random_rotation(dim, P, seed=3, device="cpu")
     cen = torch.randn(A, dim)
-    codes, factors, aid, anchors = gi.rabitq_encode(x, rot, cen)
+    codes, factors, aid, anchors = gi.rabitq_encode(x, rot, cen, backend=CPU_BUILD)
     return dict(dim=dim, P=P, A=A, n=n, rotation=rot.numpy(), codes=codes.numpy(),
                 factors=factors.numpy(), anchor_ids=aid.numpy().astype(np.uint32),
                 anchors=anchors.numpy())

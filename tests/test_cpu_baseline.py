@@ -12,14 +12,17 @@ from gofann_amd import index as gi
 from gofann_amd import plan as gp
 from gofann_amd import synth
 
+# the index is built by the oracle's restatement of the GPU build (no GPU here)
+CPU_BUILD = po.OracleBuild()
+
 
 @pytest.fixture(scope="module")
 def world():
     wl = synth.small_labelled(n=5000, nq=70, dim=32, k=8, sigma=0.7, labels=5, seed=41,
                               tags=True, ranges=True, dtype="u8")
-    cen = gi.train_kmeans(wl.base, 8, seed=41)
+    cen = gi.train_kmeans(wl.base, 8, seed=41, backend=CPU_BUILD)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels, cen,
-                              degree=32, threshold=150)
+                              degree=32, threshold=150, backend=CPU_BUILD)
     pl = gp.plan_queries(li, wl.query_labels, wl.query_ranges)
     assert pl.graph.count > 40
     return wl, li, pl, cen
@@ -46,8 +49,8 @@ def test_exact_search_threads_identical(world, threads):
 def test_pq_search_threads_identical(world, inline):
     wl, li, pl, _ = world
     rs = pl.graph
-    table = gi.train_pq(wl.base, 8, iters=4)
-    codes = gi.pq_encode(wl.base, table, 8).numpy()
+    table = gi.train_pq(wl.base, 8, iters=4, backend=CPU_BUILD)
+    codes = gi.pq_encode(wl.base, table, 8, backend=CPU_BUILD).numpy()
     pred = po.PredicateArrays.from_plan(rs.predicate, li, wl.base_ranges, alpha=0.15,
                                         pending_base_stop=True)
     prm = po.params(queue_limit=40, result_width=10 if inline else 30, inline_exact=inline)
@@ -69,7 +72,7 @@ def test_rabitq_drivers_threads_identical(world):
     P = 64
     x = wl.base.float()
     rot = gi.random_rotation(wl.dim, P, 41, "cpu")
-    codes, fac, aid, anchors = gi.rabitq_encode(x, rot, cen)
+    codes, fac, aid, anchors = gi.rabitq_encode(x, rot, cen, backend=CPU_BUILD)
     qr = (wl.queries.float() @ rot).numpy()
     nq = qr.shape[0]
     q8 = np.empty((nq, P), np.int8)

@@ -17,6 +17,9 @@ from gofann_amd import synth
 
 from test_oracle_search import complete_graph_index
 
+# the index is built by the oracle's restatement of the GPU build (no GPU here)
+CPU_BUILD = po.OracleBuild()
+
 U32MAX = 0xFFFFFFFF
 FLT_MAX = np.float32(3.4028234663852886e38)
 
@@ -26,7 +29,8 @@ def u8world():
     wl = synth.small_labelled(n=900, nq=12, dim=48, k=6, sigma=0.8, labels=3, seed=15, tags=True,
                               dtype="u8")
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=24, threshold=50)
+                              wl.centroids, degree=24, threshold=50,
+                              backend=CPU_BUILD)
     return wl, li
 
 

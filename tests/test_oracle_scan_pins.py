@@ -14,6 +14,9 @@ import pyoracle as po
 from gofann_amd import index as gi
 from gofann_amd import plan as gp
 
+# the index is built by the oracle's restatement of the GPU build (no GPU here)
+CPU_BUILD = po.OracleBuild()
+
 U32MAX = 0xFFFFFFFF
 
 
@@ -203,7 +206,8 @@ def test_rabitq_encode_closed_form(dim, P):
     cen = rng.normal(0, 1, (A, dim)).astype(np.float32)
     x = (cen[rng.integers(0, A, n)] + 0.4 * rng.normal(0, 1, (n, dim))).astype(np.float32)
     rot = gi.random_rotation(dim, P, 11 + dim, "cpu")
-    codes, fac, aid, anchors = gi.rabitq_encode(torch.from_numpy(x), rot, torch.from_numpy(cen))
+    codes, fac, aid, anchors = gi.rabitq_encode(torch.from_numpy(x), rot, torch.from_numpy(cen),
+                                                 backend=CPU_BUILD)
     codes, fac, aid, anchors = codes.numpy(), fac.numpy(), aid.numpy(), anchors.numpy()
     R = rot.numpy().astype(np.float64)
     xr = x.astype(np.float64) @ R

@@ -13,6 +13,9 @@ from gofann_amd import index as gi
 from gofann_amd import plan as gp
 from gofann_amd import synth
 
+# the index is built by the oracle's restatement of the GPU build (no GPU here)
+CPU_BUILD = po.OracleBuild()
+
 U32MAX = 0xFFFFFFFF
 
 
@@ -20,9 +23,10 @@ U32MAX = 0xFFFFFFFF
 def tiny():
     wl = synth.small_labelled(n=900, nq=12, dim=32, k=6, sigma=0.8, labels=3, seed=5, tags=True)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=24, threshold=50)
-    table = gi.train_pq(wl.base, 8, iters=8)
-    codes = gi.pq_encode(wl.base, table, 8)
+                              wl.centroids, degree=24, threshold=50,
+                              backend=CPU_BUILD)
+    table = gi.train_pq(wl.base, 8, iters=8, backend=CPU_BUILD)
+    codes = gi.pq_encode(wl.base, table, 8, backend=CPU_BUILD)
     pl = gp.plan_queries(li, wl.query_labels)
     return wl, li, table.numpy(), codes.numpy(), pl
 
@@ -39,7 +43,8 @@ def complete_graph_index(wl, group_cap=60):
     loop leaves unexpanded is the farthest, so the top W (W < group size - 1)
     are exactly the brute-force W best passing rows."""
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=64, threshold=50)
+                              wl.centroids, degree=64, threshold=50,
+                              backend=CPU_BUILD)
     sizes = np.minimum(li.label_size, group_cap).astype(np.uint32)
     offs = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.uint32)
     r2s = np.concatenate([li.row_to_sample[li.label_offset[l]:li.label_offset[l] + sizes[l]]
@@ -118,7 +123,7 @@ def test_oracle_rabitq_full_beam(tiny):
     x = wl.base
     P = 64
     rot = gi.random_rotation(x.shape[1], P, 5, "cpu")
-    rcodes, fac, aid, anchors = gi.rabitq_encode(x, rot, wl.centroids)
+    rcodes, fac, aid, anchors = gi.rabitq_encode(x, rot, wl.centroids, backend=CPU_BUILD)
     qr = (wl.queries.float() @ rot).numpy()
     nq = qr.shape[0]
     q8 = np.empty((nq, P), np.int8)
@@ -194,9 +199,10 @@ def test_inline_exact_u8_distances_are_integer_exact():
     wl = synth.small_labelled(n=700, nq=8, dim=48, k=5, sigma=0.8, labels=2, seed=9, tags=True,
                               dtype="u8")
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=16, threshold=40)
-    table = gi.train_pq(wl.base, 8, iters=6)
-    codes = gi.pq_encode(wl.base, table, 8)
+                              wl.centroids, degree=16, threshold=40,
+                              backend=CPU_BUILD)
+    table = gi.train_pq(wl.base, 8, iters=6, backend=CPU_BUILD)
+    codes = gi.pq_encode(wl.base, table, 8, backend=CPU_BUILD)
     rs = gp.plan_queries(li, wl.query_labels).graph
     pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15, pending_base_stop=True)
     prm = po.params(queue_limit=64, result_width=10, inline_exact=True)

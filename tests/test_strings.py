@@ -15,6 +15,9 @@ from gofann_amd import plan as gp
 from gofann_amd import strings as st
 from gofann_amd import synth
 
+# the index is built by the oracle's restatement of the GPU build (no GPU here)
+CPU_BUILD = po.OracleBuild()
+
 U32MAX = 0xFFFFFFFF
 
 
@@ -186,9 +189,10 @@ def test_plan_dnf_residuals():
 def c5_small():
     wl = synth.config5(n=60_000, nq=160, device="cpu", dim=64, k=32, labels=20, intervals=10,
                        vocab=600)
-    cen = gi.train_kmeans(wl.base, 32, seed=4)
+    cen = gi.train_kmeans(wl.base, 32, seed=4, backend=CPU_BUILD)
     li = gi.build_label_index(wl.base.float(), wl.label_offsets, wl.label_values, wl.num_labels,
-                              cen, degree=32, threshold=800, local=12)
+                              cen, degree=32, threshold=800, local=12,
+                              backend=CPU_BUILD)
     return wl, li, cen
 
 
@@ -221,7 +225,7 @@ def test_c5_routes_end_to_end_through_oracle(c5_small):
     x = wl.base.float()
     P = 64
     rot = gi.random_rotation(wl.dim, P, 5, "cpu")
-    codes, fac, aid, anchors = gi.rabitq_encode(x, rot, cen)
+    codes, fac, aid, anchors = gi.rabitq_encode(x, rot, cen, backend=CPU_BUILD)
     qr = (wl.queries.float() @ rot).numpy()
     nq = qr.shape[0]
     q8 = np.empty((nq, P), np.int8)
