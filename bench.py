@@ -49,7 +49,8 @@ def parse():
     ap.add_argument("--coarse-lists", type=int, default=1024,
                     help="k-means centres that bucket the C2 graph builder's rows")
     ap.add_argument("--queries", type=int, default=100_000)
-    ap.add_argument("--gt-queries", type=int, default=2000)
+    ap.add_argument("--gt-queries", type=int, default=10_000,
+                    help="C2 queries with exact ground truth (a seeded sample of the 100k)")
     ap.add_argument("--queue", type=int, default=0, help="beam width; 0 = ladder search")
     ap.add_argument("--ladder", default="64,96,112,128,160,192,256,384")
     ap.add_argument("--target-recall", type=float, default=0.90)
@@ -75,9 +76,13 @@ def parse():
     ap.add_argument("--queries-c1", type=int, default=10_000)
     ap.add_argument("--n-c4", type=int, default=100_000_000)
     ap.add_argument("--queries-c4", type=int, default=10_000)
-    ap.add_argument("--gt-queries-c4", type=int, default=1000)
+    ap.add_argument("--gt-queries-c4", type=int, default=10_000)
+    ap.add_argument("--gt-queries-c5", type=int, default=10_000)
     ap.add_argument("--c4-ladder", default="16,32,64,96,128,192,256,320,384,416,448,512,768,1024")
     ap.add_argument("--c4-coarse-ladder", default="16,24,32,48,64,96,128,192,256,384")
+    ap.add_argument("--graph-design", choices=("navigable", "cagra"), default="navigable",
+                    help="C4/C5 label graphs: this repo's navigable design, or the reference's "
+                         "CAGRA recipe (2R kNN, rank pruning, reverse edges, reachability)")
     ap.add_argument("--c4-local", type=int, default=8,
                     help="in-bucket links per row of the C4 graphs (the rest are drawn)")
     ap.add_argument("--no-c4", action="store_true",
@@ -100,7 +105,7 @@ def parse():
                     help="labels with at most this many rows are posting routes")
     ap.add_argument("--n-c3", type=int, default=2_700_000)
     ap.add_argument("--queries-c3", type=int, default=10_000)
-    ap.add_argument("--gt-queries-c3", type=int, default=999)
+    ap.add_argument("--gt-queries-c3", type=int, default=10_000)
     ap.add_argument("--c3-ladder", default="32,48,64,96,128,192,256,320,384,448,512")
     ap.add_argument("--c3-local", type=int, default=24,
                     help="in-bucket links per row of the C3 graph (the rest are drawn)")
@@ -141,14 +146,19 @@ def build_world(args, torch):
     table = gi.train_pq(wl.base, 48, iters=25, sample=65536, seed=2005)
     codes = gi.pq_encode(wl.base, table, 48)
     torch.cuda.synchronize()
-    log(f"PQ M=48 trained+encoded in {time.time() - t0:.1f}s")
+    t_pq = time.time() - t0
+    log(f"PQ M=48 trained+encoded in {t_pq:.1f}s")
     t0 = time.time()
     cen = gi.train_kmeans(wl.base, args.coarse_lists, seed=2006)
+    torch.cuda.synchronize()
+    t_km = time.time() - t0
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
                               cen, degree=64, threshold=2000, progress=log)
+    t_g = time.time() - t0 - t_km
     log(f"label graphs: {int((li.label_size > 0).sum())} labels, {li.rows} rows, "
-        f"degree 64, buckets from {args.coarse_lists} trained k-means centres in "
-        f"{time.time() - t0:.1f}s")
+        f"degree 64, buckets from {args.coarse_lists} trained k-means centres "
+        f"(k-means {t_km:.1f}s, graphs {t_g:.1f}s, on the GPU)")
+    wl.meta["build_s"] = {"pq": round(t_pq, 1), "kmeans": round(t_km, 1), "graphs": round(t_g, 1)}
     t0 = time.time()
     pl = gp.plan_queries(li, wl.query_labels)
     log(f"plan: {pl.graph.count} graph routes, {pl.posting.count} posting routes "
@@ -506,6 +516,94 @@ def measured_traffic(profile: str, match: bool):
     return None
 
 
+def index_digest(li, codes) -> str:
+    """A hash of the built index (graph, seeds, codes): equal across
+    processes when the build is deterministic."""
+    import hashlib
+    h = hashlib.sha256()
+    h.update(np.ascontiguousarray(li.graph).tobytes())
+    h.update(np.ascontiguousarray(li.seed_local).tobytes())
+    h.update(codes.cpu().numpy().tobytes())
+    return h.hexdigest()[:16]
+
+
+def _pick(d, keys):
+    return None if d is None else {k: d[k] for k in keys if k in d}
+
+
+def _kernel_alias(name: str) -> str:
+    if name.startswith("traversal"):
+        return "traversal"
+    if name.startswith("exact_rerank"):
+        return "rerank"
+    if name.startswith("label_share"):
+        return "label_share_scan"
+    if "label postings" in name:
+        return "label_postings_scan"
+    if "range" in name:
+        return "range_scan"
+    return name.split("<")[0]
+
+
+def _compact_rabitq_leg(leg):
+    if leg is None:
+        return None
+    out = _pick(leg, ("qps", "ms_per_step", "queue_by_class", "recall_at_10", "recall_by_class",
+                      "gt_by_class", "expansions_per_route"))
+    out["kernels_ms_gbps"] = {_kernel_alias(k): [v["ms"], v.get("achieved_gbps")]
+                              for k, v in (leg.get("kernels") or {}).items()}
+    r = leg.get("roofline") or {}
+    out["roofline"] = _pick(r, ("kernel", "frac", "traffic"))
+    return out
+
+
+def compact_record(line: dict) -> dict:
+    """The driver's JSON line: the contract fields, the headline's roofline
+    and CPU baseline, and per leg the figures a reader compares (QPS, beam,
+    recall with its ground-truth counts, kernel times).  The full record
+    goes to stderr."""
+    c = line["config"]
+    cc = {k: c[k] for k in ("workload", "n", "queries", "graph_routes", "posting_routes", "route",
+                            "queue", "recall_at_10", "recall_by_class", "gt_queries",
+                            "gt_by_class", "build_s", "seeds") if k in c}
+    pq = c.get("pq_route")
+    if pq:
+        cc["pq_route"] = dict(_pick(pq, ("qps", "queue", "recall_at_10", "kernel_ms")),
+                              frac=(pq.get("roofline") or {}).get("frac"),
+                              traffic=(pq.get("roofline") or {}).get("traffic"))
+    for key in ("full_gpu_exact_route", "full_gpu_exact_route_coarse_entry"):
+        r = c.get(key)
+        if r:
+            cc[key] = dict(_pick(r, ("qps", "queue", "recall_at_10", "kernel_ms",
+                                     "steps_per_route", "scored_per_route")),
+                           frac=(r.get("roofline") or {}).get("frac"))
+    cc["gpu_cpu_rerank_route"] = _pick(c.get("gpu_cpu_rerank_route"),
+                                       ("qps", "queue", "shortlist", "recall_at_10"))
+    cc["rabitq_query_prep"] = _pick(c.get("rabitq_query_prep"),
+                                    ("ms", "gemm_tflops_lower_bound", "frac_lower_bound"))
+    c1 = c.get("c1")
+    if c1:
+        ie, ad = c1.get("inline_exact") or {}, c1.get("adc_shortlist_rerank") or {}
+        cc["c1"] = {"inline_exact": _pick(ie.get("gpu"), ("qps", "queue", "recall_at_10")),
+                    "inline_exact_configured_beam": _pick(ie.get("gpu_configured_beam"),
+                                                          ("qps", "queue", "recall_at_10")),
+                    "adc_shortlist_rerank": _pick(ad.get("gpu"), ("qps", "queue", "recall_at_10")),
+                    "cpu_qps": (ie.get("cpu") or {}).get("qps"), "gt_queries": c1.get("gt_queries")}
+    for cfg in ("c3", "c4", "c5"):
+        x = c.get(cfg)
+        if not x:
+            continue
+        cc[cfg] = {"gt_queries": x.get("gt_queries"), "build_s": x.get("build_s"),
+                   "medoid_seeds": _compact_rabitq_leg(x.get("medoid_seeds")),
+                   "coarse_entry": _compact_rabitq_leg(x.get("coarse_entry")),
+                   "gpu_cpu_rerank_route": _pick(x.get("gpu_cpu_rerank_route"),
+                                                 ("qps", "recall_at_10", "exposed_rerank_ms")),
+                   "cpu_qps": (x.get("cpu_baseline") or {}).get("value")}
+    out = {k: v for k, v in line.items() if k != "config"}
+    out["config"] = cc
+    return out
+
+
 def host_threads() -> int:
     """Host cores the CPU baseline uses: OMP_NUM_THREADS when set (the GPU
     box sets it to the job's CPU share), else every core."""
@@ -825,38 +923,90 @@ def build_world_c3(args, torch):
     log(f"C3 data {wl.n}x{wl.dim} fp32, {wl.queries.shape[0]} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     cen = gi.train_kmeans(wl.base, 512, seed=3006)
+    torch.cuda.synchronize()
+    t_km = time.time() - t0
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, 1, cen,
                               degree=32, threshold=0, progress=log, local=args.c3_local)
-    log(f"C3 graph: {li.rows} rows, degree {li.degree} in {time.time() - t0:.1f}s")
+    t_g = time.time() - t0 - t_km
+    log(f"C3 graph: {li.rows} rows, degree {li.degree} (k-means {t_km:.1f}s, graph "
+        f"{t_g:.1f}s, on the GPU)")
     t0 = time.time()
     P = wl.dim
     rot = gi.random_rotation(wl.dim, P, 3003, "cuda")
     codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, cen)
     torch.cuda.synchronize()
-    log(f"C3 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
+    t_c = time.time() - t0
+    log(f"C3 RaBitQ codes {codes.shape[1]} B/row in {t_c:.1f}s")
+    wl.meta["build_s"] = {"kmeans": round(t_km, 1), "graphs": round(t_g, 1),
+                          "rabitq_codes": round(t_c, 1)}
+    wl.meta["index_digest"] = index_digest(li, codes)
     rpi = rp.RangePostingIndex.build(wl.base_ranges)
     return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), rpi, cen
 
 
-def ground_truth_c3(wl, torch, nq):
-    """Exact filtered top-10 (fp32 L2 over the rows whose attribute lies in
-    the query's range) for the first nq queries."""
-    attr = torch.as_tensor(wl.base_ranges[:, 0], device="cuda")
-    bn = (wl.base * wl.base).sum(1)
+def dense_ground_truth(torch, base, queries, mask, nq, q_chunk=2500, row_chunk=1 << 18,
+                       m=32):
+    """Exact filtered top-10 of the first nq queries over every row: fp32
+    norm-expansion distances (a GEMM per chunk of rows and queries) with
+    mask(s, e, q0, q1) -> bool [q1 - q0][e - s] applied, the m least kept
+    per query, then those m re-ranked by fp64 squared L2 (ties to the lower
+    sample id).  The fp32 error is far below the gap between the 10th and
+    the 32nd candidate, so the result is the fp64 top-10."""
+    n = base.shape[0]
     gt = {}
-    for s in range(0, nq, 32):
-        e = min(nq, s + 32)
-        q = wl.queries[s:e]
-        d = bn[None, :] + (q * q).sum(1)[:, None] - 2.0 * (q @ wl.base.t())
-        for j in range(e - s):
-            _, _, lo, hi = wl.query_ranges[s + j][0]
-            m = (attr >= lo) & (attr < hi)
-            dj = torch.where(m, d[j], torch.full_like(d[j], float("inf")))
-            v, i = torch.topk(dj, 10, largest=False)
-            ids = i[torch.isfinite(v)].cpu().numpy()
-            if ids.size:
-                gt[s + j] = ids
+    bn = torch.empty(n, device="cuda")
+    for s in range(0, n, row_chunk):
+        xf = base[s:s + row_chunk].float()
+        bn[s:s + row_chunk] = (xf * xf).sum(1)
+    del xf
+    for q0 in range(0, nq, q_chunk):
+        q1 = min(nq, q0 + q_chunk)
+        q = queries[q0:q1].float()
+        qn = (q * q).sum(1)
+        best_d = torch.full((q1 - q0, m), float("inf"), device="cuda")
+        best_i = torch.full((q1 - q0, m), -1, dtype=torch.int64, device="cuda")
+        for s in range(0, n, row_chunk):
+            e = min(n, s + row_chunk)
+            xf = base[s:e].float()
+            d = torch.addmm(bn[None, s:e], q, xf.t(), beta=1.0, alpha=-2.0)
+            d += qn[:, None]                                 # [nqc, rows]
+            d.masked_fill_(~mask(s, e, q0, q1), float("inf"))
+            v, i = torch.topk(d, min(m, e - s), dim=1, largest=False)
+            cd = torch.cat([best_d, v], 1)
+            ci = torch.cat([best_i, i + s], 1)
+            v2, j = torch.topk(cd, m, dim=1, largest=False)
+            best_d, best_i = v2, torch.gather(ci, 1, j)
+            del d
+        ids = best_i                                       # [nqc, m]
+        valid = torch.isfinite(best_d)
+        x = base[ids.clamp(min=0)].double()                # [nqc, m, D]
+        d64 = ((x - q.double()[:, None, :]) ** 2).sum(-1)
+        d64 = torch.where(valid, d64, torch.full_like(d64, float("inf")))
+        # (fp64 distance, id): sort by id, then stably by distance
+        o1 = torch.sort(ids, dim=1, stable=True).indices
+        d1, i1 = torch.gather(d64, 1, o1), torch.gather(ids, 1, o1)
+        o2 = torch.sort(d1, dim=1, stable=True).indices[:, :10]
+        dd, ii = torch.gather(d1, 1, o2).cpu().numpy(), torch.gather(i1, 1, o2).cpu().numpy()
+        for r in range(q1 - q0):
+            sel = np.isfinite(dd[r])
+            if sel.any():
+                gt[q0 + r] = ii[r][sel].astype(np.uint32)
+        del x, d64
     return gt
+
+
+def ground_truth_c3(wl, torch, nq):
+    """Exact filtered top-10 (fp64 after fp32 candidates) of the first nq
+    queries over the rows whose attribute lies in the query's range."""
+    attr = torch.as_tensor(wl.base_ranges[:, 0], device="cuda")
+    lo = torch.tensor([r[0][2] for r in wl.query_ranges], device="cuda")
+    hi = torch.tensor([r[0][3] for r in wl.query_ranges], device="cuda")
+
+    def mask(s, e, q0, q1):
+        a = attr[None, s:e]
+        return (a >= lo[q0:q1, None]) & (a < hi[q0:q1, None])
+    return dense_ground_truth(torch, wl.base, wl.queries, mask, min(nq, wl.queries.shape[0]),
+                              q_chunk=1000)
 
 
 class RabitqRangePipeline:
@@ -1193,7 +1343,8 @@ def run_c3(args, torch, ctx) -> dict:
                         "fp32 rerank of 200, top-10",
             "n": wl.n, "queries": pipe.nq, "graph_routes": pipe.ng,
             "range_posting_routes": pipe.np_, "scan_rows": pipe.scan_rows_total,
-            "shortlist": pipe.W, "gt_queries": len(gt),
+            "shortlist": pipe.W, "gt_queries": len(gt), "build_s": wl.meta.get("build_s"),
+            "index_digest": wl.meta.get("index_digest"),
             "graph_buckets": "512 k-means centres trained on the base",
             "data_model": "centre + rank-64 shared-basis spread 0.7 + N(0, 0.05^2), normalised",
             "medoid_seeds": med, "coarse_entry": coarse, "gpu_cpu_rerank_route": cpu_route,
@@ -1238,8 +1389,10 @@ def build_world_c4(args, torch):
     # which is what finds a query's cluster from the medoid
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
                               cen, degree=32, threshold=args.c4_threshold, progress=log,
-                              local=args.c4_local)
+                              local=args.c4_local, design=args.graph_design)
     torch.cuda.empty_cache()
+    wl.meta["build_s"] = {"kmeans_and_graphs": round(time.time() - t0, 1),
+                          "graph_design": args.graph_design}
     ng = int((li.label_size > 0).sum())
     log(f"C4 graphs: {ng} label/interval groups, {li.rows} rows, degree {li.degree} in "
         f"{time.time() - t0:.1f}s")
@@ -1252,12 +1405,10 @@ def build_world_c4(args, torch):
     return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), cen
 
 
-def ground_truth_c4(wl, torch, nq, chunk=1 << 20):
-    """Exact filtered top-10 (fp32 L2 of the fp16 rows) for the first nq
+def ground_truth_c4(wl, torch, nq):
+    """Exact filtered top-10 (fp64 after fp32 candidates) of the first nq
     queries: equality on the categorical label, or the attribute range."""
-    n = wl.n
-    q = wl.queries[:nq].float()
-    qn = (q * q).sum(1)
+    nq = min(nq, wl.queries.shape[0])
     cat = torch.as_tensor(wl.meta["row_category"].astype(np.int32), device="cuda")
     attr = torch.as_tensor(wl.base_ranges[:, 0], device="cuda")
     qlab = torch.tensor([ql[0] if ql else -1 for ql in wl.query_labels[:nq]], device="cuda",
@@ -1265,28 +1416,12 @@ def ground_truth_c4(wl, torch, nq, chunk=1 << 20):
     lo = torch.tensor([qr[0][2] if qr else 0.0 for qr in wl.query_ranges[:nq]], device="cuda")
     hi = torch.tensor([qr[0][3] if qr else 0.0 for qr in wl.query_ranges[:nq]], device="cuda")
     is_rng = qlab < 0
-    best_d = torch.full((10, nq), float("inf"), device="cuda")
-    best_i = torch.full((10, nq), -1, dtype=torch.int64, device="cuda")
-    for s in range(0, n, chunk):
-        e = min(n, s + chunk)
-        xf = wl.base[s:e].float()
-        d = (xf * xf).sum(1)[:, None] + qn[None, :] - 2.0 * (xf @ q.t())
-        a = attr[s:e, None]
-        ok = torch.where(is_rng[None, :], (a >= lo[None, :]) & (a < hi[None, :]),
-                         cat[s:e, None] == qlab[None, :])
-        d = torch.where(ok, d, torch.full_like(d, float("inf")))
-        v, i = torch.topk(d, min(10, e - s), dim=0, largest=False)
-        cd = torch.cat([best_d, v], 0)
-        ci = torch.cat([best_i, i + s], 0)
-        v2, j = torch.topk(cd, 10, dim=0, largest=False)
-        best_d, best_i = v2, torch.gather(ci, 0, j)
-    bd, bi = best_d.t().cpu().numpy(), best_i.t().cpu().numpy()
-    gt = {}
-    for r in range(nq):
-        ids = bi[r][np.isfinite(bd[r])]
-        if ids.size:
-            gt[r] = ids
-    return gt
+
+    def mask(s, e, q0, q1):
+        a = attr[None, s:e]
+        return torch.where(is_rng[q0:q1, None], (a >= lo[q0:q1, None]) & (a < hi[q0:q1, None]),
+                           cat[None, s:e] == qlab[q0:q1, None])
+    return dense_ground_truth(torch, wl.base, wl.queries, mask, nq)
 
 
 def synth_types():
@@ -1582,6 +1717,7 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
     return {"qps": round(nq / (ms / 1000.0), 1), "ms_per_step": round(ms, 3),
             "queue_by_class": dict(zip([n for n, _ in class_gt], chosen)),
             "recall_at_10": round(rec, 4), "recall_by_class": by_class,
+            "gt_by_class": {n: len(g) for n, g in class_gt},
             "expansions_per_route": round(float(E.mean()), 1), "stage_ms": st_ms,
             "kernel_stage_ms": kst, "kernels": per, "placement": pipe.ctx.last_placement(),
             "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
@@ -1780,6 +1916,7 @@ def run_c4(args, torch, ctx, world=None) -> dict:
             "n": wl.n, "queries": pipe.nq, "graph_routes": pipe.ng,
             "interior_interval_routes": pipe.interior, "posting_routes": pipe.np_,
             "posting_rows": pipe.post_rows_total, "shortlist": pipe.W, "gt_queries": len(gt),
+            "build_s": wl.meta.get("build_s"),
             "graph_buckets": "4096 k-means centres trained on the base",
             "medoid_seeds": med, "coarse_entry": coarse, "gpu_cpu_rerank_route": cpu_route,
             "cpu_baseline": cpu}
@@ -1800,69 +1937,74 @@ def build_world_c5(args, torch):
         f"queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     cen = gi.train_kmeans(wl.base, 4096, seed=4006)
+    torch.cuda.synchronize()
+    t_km = time.time() - t0
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
                               cen, degree=32, threshold=args.c4_threshold, progress=log,
-                              local=args.c4_local)
+                              local=args.c4_local, design=args.graph_design)
     torch.cuda.empty_cache()
+    t_g = time.time() - t0 - t_km
     base = wl.meta["string_label_base"]
     ng = int((li.label_size > 0).sum())
     ngs = int((li.label_size[base:] > 0).sum())
-    log(f"C5 graphs: {ng} label groups ({ngs} string tokens), {li.rows} rows, degree "
-        f"{li.degree} in {time.time() - t0:.1f}s")
+    log(f"C5 graphs ({args.graph_design}): {ng} label groups ({ngs} string tokens), {li.rows} "
+        f"rows, degree {li.degree} (k-means {t_km:.1f}s, graphs {t_g:.1f}s, on the GPU)")
     t0 = time.time()
     P = wl.dim
     rot = gi.random_rotation(wl.dim, P, 4005, "cuda")
     codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, cen, chunk=1 << 18)
     torch.cuda.synchronize()
-    log(f"C5 RaBitQ codes {codes.shape[1]} B/row in {time.time() - t0:.1f}s")
+    t_c = time.time() - t0
+    log(f"C5 RaBitQ codes {codes.shape[1]} B/row in {t_c:.1f}s")
+    wl.meta["build_s"] = {"kmeans": round(t_km, 1), "graphs": round(t_g, 1),
+                          "rabitq_codes": round(t_c, 1), "graph_design": args.graph_design}
     return wl, li, dict(rot=rot, codes=codes, fac=fac, aid=aid, anchors=anchors, P=P), cen
 
 
-def ground_truth_c5(wl, li, torch, nq, chunk=1 << 21):
-    """Exact filtered top-10 (fp32 L2 of the fp16 rows) of the first nq
-    queries: the union over the query's clauses of the rows holding the
-    clause's token, restricted by the clause's category and range."""
-    cat = wl.meta["row_category"]
-    attr = wl.base_ranges[:, 0]
+def ground_truth_c5(wl, li, torch, nq):
+    """Exact filtered top-10 (fp64 after fp32 candidates) of the first nq
+    queries.  A query's clauses share one token set (its expanded string),
+    and a hybrid query's clauses share its category and range, so its
+    filter is: the row's token in the set, and for hybrids the row's
+    category and attribute range."""
+    nq = min(nq, wl.queries.shape[0])
     base_label = wl.meta["string_label_base"]
-    gt = {}
-    for q in range(min(nq, wl.queries.shape[0])):
-        rng = wl.query_ranges[q]
-        parts = []
-        for labels, uses_range in wl.meta["query_clauses"][q]:
-            tok = [l for l in labels if l >= base_label]
-            rest = [l for l in labels if l < base_label]
-            t = tok[0]
-            rows = li.posting_ids[int(li.posting_offset[t]):int(li.posting_offset[t + 1])]
-            if rest:
-                rows = rows[cat[rows] == rest[0]]
-            if uses_range and rng:
-                (_, _, lo, hi), = rng
-                rows = rows[(attr[rows] >= lo) & (attr[rows] < hi)]
-            parts.append(rows)
-        cand = np.unique(np.concatenate(parts)) if parts else np.zeros(0, np.uint32)
-        if cand.size == 0:
-            continue
-        qv = wl.queries[q].float()
-        best_d = torch.full((0,), 0.0, device="cuda")
-        best_i = torch.full((0,), 0, dtype=torch.int64, device="cuda")
-        for s0 in range(0, cand.size, chunk):
-            ids = torch.as_tensor(cand[s0:s0 + chunk].astype(np.int64), device="cuda")
-            x = wl.base[ids].float()
-            d = ((x - qv[None, :]) ** 2).sum(1)
-            cd, ci = torch.cat([best_d, d]), torch.cat([best_i, ids])
-            k = min(10, cd.numel())
-            v, j = torch.topk(cd, k, largest=False)
-            best_d, best_i = v, ci[j]
-        gt[q] = best_i.cpu().numpy().astype(np.uint32)
-    return gt
+    vocab = wl.num_labels - base_label
+    tokmask = torch.zeros(nq, vocab, dtype=torch.bool)
+    qcat = torch.full((nq,), -1, dtype=torch.int32)
+    lo = torch.zeros(nq)
+    hi = torch.zeros(nq)
+    hyb = torch.zeros(nq, dtype=torch.bool)
+    for q in range(nq):
+        cl = wl.meta["query_clauses"][q]
+        cats = set()
+        for labels, uses_range in cl:
+            tok = [l - base_label for l in labels if l >= base_label]
+            tokmask[q, tok] = True
+            cats.update(l for l in labels if l < base_label)
+        if cl and cl[0][1]:
+            assert len(cats) == 1 and all(u for _, u in cl)
+            hyb[q] = True
+            qcat[q] = next(iter(cats))
+            (_, _, lo[q], hi[q]), = wl.query_ranges[q]
+    tokmask, qcat, lo, hi, hyb = (t.cuda() for t in (tokmask, qcat, lo, hi, hyb))
+    sid = torch.as_tensor(wl.meta["string_ids"].astype(np.int64), device="cuda")
+    cat = torch.as_tensor(wl.meta["row_category"].astype(np.int32), device="cuda")
+    attr = torch.as_tensor(wl.base_ranges[:, 0], device="cuda")
+
+    def mask(s, e, q0, q1):
+        ok = tokmask[q0:q1][:, sid[s:e]]                   # [nqc, rows]
+        a = attr[None, s:e]
+        h = (cat[None, s:e] == qcat[q0:q1, None]) & (a >= lo[q0:q1, None]) & (a < hi[q0:q1, None])
+        return ok & (h | ~hyb[q0:q1, None])
+    return dense_ground_truth(torch, wl.base, wl.queries, mask, nq)
 
 
 def run_c5(args, torch, ctx, world=None) -> dict:
     from gofann_amd import search as gs
     wl, li, rq, cen = world if world is not None else build_world_c5(args, torch)
     t0 = time.time()
-    gt = ground_truth_c5(wl, li, torch, args.gt_queries_c4)
+    gt = ground_truth_c5(wl, li, torch, args.gt_queries_c5)
     log(f"C5 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
@@ -1905,6 +2047,7 @@ def run_c5(args, torch, ctx, world=None) -> dict:
                         "AND string filters, compiled to label routes; top-10",
             "n": wl.n, "queries": pipe.nq, "graph_routes": pipe.ng, "posting_routes": pipe.np_,
             "posting_rows": pipe.post_rows_total, "shortlist": pipe.W, "gt_queries": len(gt),
+            "build_s": wl.meta.get("build_s"),
             "clauses_per_query_mean": round(float(np.mean(nclauses)), 2),
             "clauses_per_fuzzy_query_mean": round(float(np.mean(
                 [c for c, t in zip(nclauses, types) if "fuzzy" in t])), 2),
@@ -1975,7 +2118,11 @@ def main():
     wl, li, table, codes, pl, cen = build_world(args, torch)
     t0 = time.time()
     gt = ground_truth(wl, li, torch, args.gt_queries)
-    log(f"ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
+    # classes: queries of one tag and of two tags
+    class_gt2 = [(name, {q: g for q, g in gt.items() if len(wl.query_labels[q]) == k})
+                 for name, k in (("1 tag", 1), ("2 tags", 2))]
+    log(f"ground truth for {len(gt)} queries in {time.time() - t0:.1f}s "
+        f"({', '.join(f'{n}: {len(g)}' for n, g in class_gt2)})")
     ctx = _lib.Context(0)
     class_pool(torch, _lib)  # before any other stream
     inline = not args.no_inline_exact
@@ -2066,7 +2213,9 @@ def main():
             torch.cuda.synchronize()
             k3.append(er.kernel_ms())
         ms3 = (time.perf_counter() - t0) * 1000.0 / args.steps
-        rec3 = recall_at_10(out3.cpu().numpy().view(np.uint32).reshape(pl.queries, 10), gt)
+        res3 = out3.cpu().numpy().view(np.uint32).reshape(pl.queries, 10)
+        rec3 = recall_at_10(res3, gt)
+        by3 = {n: round(recall_at_10(res3, g), 4) for n, g in class_gt2 if g}
         st3 = er.route_stats()
         kms3 = float(np.mean(k3))
         b3 = exact_route_bytes(st3, li.degree, wl.dim, not args.no_neighbor_samples)
@@ -2074,6 +2223,7 @@ def main():
         ach3 = b3 / (kms3 / 1000.0) / 1e9
         res = {"qps": round(pl.queries / (ms3 / 1000.0), 1), "ms_per_step": round(ms3, 3),
                "kernel_ms": round(kms3, 3), "queue": q3, "recall_at_10": round(rec3, 4),
+               "recall_by_class": by3, "gt_by_class": {n: len(g) for n, g in class_gt2},
                "placement": pl3,
                "steps_per_route": round(float(st3[:, 0].mean()), 1),
                "scored_per_route": round(float(st3[:, 3].mean()), 1),
@@ -2130,11 +2280,12 @@ def main():
     if use_exact:
         head = dict(value=route3["qps"], ms=route3["ms_per_step"], queue=route3["queue"],
                     recall=route3["recall_at_10"], route="full-GPU exact (exact-distance u8 beam)",
-                    roofline=route3.pop("roofline"), placement=route3["placement"])
+                    roofline=route3.pop("roofline"), placement=route3["placement"],
+                    by_class=route3["recall_by_class"])
     else:
         head = dict(value=pq_route["qps"], ms=pq_route["ms_per_step"], queue=chosen,
                     recall=pq_route["recall_at_10"], route="PQ graph search, inline exact u8",
-                    roofline=pq_route.pop("roofline"), placement=placed)
+                    roofline=pq_route.pop("roofline"), placement=placed, by_class=None)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -2166,7 +2317,9 @@ def main():
                    "queue": head["queue"], "recall_at_10": head["recall"],
                    "rerank": "exact u8 on GPU", "seeds": "label medoid (dataloader.cpp:7361-7406)",
                    "graph_buckets": f"{args.coarse_lists} k-means centres trained on the base",
-                   "gt_queries": len(gt), "placement": head["placement"],
+                   "gt_queries": len(gt), "recall_by_class": head["by_class"],
+                   "gt_by_class": {n: len(g) for n, g in class_gt2},
+                   "build_s": wl.meta.get("build_s"), "placement": head["placement"],
                    "neighbor_samples": not args.no_neighbor_samples,
                    "sample_records": not args.no_records,
                    "pq_route": pq_route,
@@ -2202,7 +2355,8 @@ def main():
             line["config"]["c5"] = run_c5(args, torch, ctx, world=world)
         world = None
         free()
-    print(json.dumps(line), flush=True)
+    log("full record: " + json.dumps(line, default=float))
+    print(json.dumps(compact_record(line), default=float), flush=True)
     if args.calibrate_copy:
         x = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         y = torch.empty_like(x)

@@ -24,7 +24,6 @@
 // product: 256 threads own a 64 x 64 tile, 4 x 4 per thread, with 32-dim
 // chunks of both operands staged in LDS as fp32.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
 #include <rocblas/rocblas.h>
 
 #include <cfloat>
@@ -450,44 +449,87 @@ __global__ void copy_row_kernel(const T* rows, uint32_t dim, const uint32_t* pic
     for (uint32_t d = threadIdx.x; d < dim; d += blockDim.x) centre[d] = to_f(x[d]);
 }
 
-// Segment starts of sorted keys: start[c] = first i with keys[i] >= c.
-__global__ void key_starts_kernel(const uint32_t* keys, uint64_t n, uint32_t segments,
-                                  uint32_t* start)
+// Exclusive prefix sums of counts[0 .. m) into out[0 .. m] (out[m] = the
+// total), one 1024-thread workgroup: thread t adds a contiguous chunk in
+// order, thread 0 scans the 1024 chunk sums, then each thread writes its
+// chunk's prefixes.
+__global__ __launch_bounds__(1024) void exclusive_scan_kernel(const uint32_t* counts, uint64_t m,
+                                                              uint32_t* out)
 {
-    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c > segments) return;
-    uint64_t lo = 0, hi = n;
-    while (lo < hi) {
-        const uint64_t mid = (lo + hi) >> 1;
-        if (keys[mid] < c)
-            lo = mid + 1;
-        else
-            hi = mid;
+    __shared__ uint32_t part[1024];
+    const uint32_t t = threadIdx.x;
+    const uint64_t chunk = (m + 1023) / 1024;
+    const uint64_t b0 = static_cast<uint64_t>(t) * chunk;
+    const uint64_t b1 = b0 + chunk < m ? b0 + chunk : m;
+    uint32_t s = 0;
+    for (uint64_t i = b0; i < b1; ++i) s += counts[i];
+    part[t] = s;
+    __syncthreads();
+    if (t == 0) {
+        uint32_t run = 0;
+        for (int i = 0; i < 1024; ++i) {
+            const uint32_t v = part[i];
+            part[i] = run;
+            run += v;
+        }
+        out[m] = run;
     }
-    start[c] = static_cast<uint32_t>(lo);
+    __syncthreads();
+    uint32_t run = part[t];
+    for (uint64_t i = b0; i < b1; ++i) {
+        out[i] = run;
+        run += counts[i];
+    }
 }
 
-__global__ void iota_kernel(uint32_t* v, uint64_t n)
+// counts[c] = number of i with keys[i] == c (keys >= K are skipped).
+__global__ void key_count_kernel(const uint32_t* keys, uint64_t n, uint32_t K, uint32_t* counts)
 {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) v[i] = static_cast<uint32_t>(i);
+    if (i >= n) return;
+    const uint32_t k = keys[i];
+    if (k < K) atomicAdd(&counts[k], 1u);
+}
+
+// The rows of each key in ascending order: one wave per key scans the keys
+// in row order and compacts its matches with a ballot into
+// order[start[c] ..).
+__global__ __launch_bounds__(kThreads) void key_lists_kernel(const uint32_t* keys, uint64_t n,
+                                                             uint32_t K, const uint32_t* start,
+                                                             uint32_t* order)
+{
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const uint32_t c = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+    if (c >= K) return;
+    uint32_t pos = start[c];
+    const uint64_t below = (1ull << lane) - 1;
+    for (uint64_t i0 = 0; i0 < n; i0 += kWave) {
+        const uint64_t i = i0 + static_cast<uint64_t>(lane);
+        const bool hit = i < n && keys[i] == c;
+        const uint64_t m = __ballot(hit);
+        if (hit) order[pos + static_cast<uint32_t>(__popcll(m & below))] = static_cast<uint32_t>(i);
+        pos += static_cast<uint32_t>(__popcll(m));
+    }
 }
 
 // Centre update: centre c = mean of its rows (fp64 sums over the rows in
 // ascending order, then the quotient rounded to fp32); a centre with no row
 // keeps its value.  One workgroup per centre, threads over dims.
 template <class T>
-__global__ __launch_bounds__(kThreads) void centre_mean_kernel(const T* rows, uint32_t dim,
+__global__ __launch_bounds__(kThreads) void centre_mean_kernel(const T* rows, uint32_t dim, uint64_t n,
                                                                const uint32_t* order,
                                                                const uint32_t* start,
                                                                float* centres)
 {
     const uint32_t c = blockIdx.x;
     const uint32_t s = start[c], e = start[c + 1];
-    if (s == e) return;
+    if (s >= e || e > n) return;
     for (uint32_t d = threadIdx.x; d < dim; d += kThreads) {
         double sum = 0.0;
-        for (uint32_t i = s; i < e; ++i) sum += static_cast<double>(to_f(rows[static_cast<size_t>(order[i]) * dim + d]));
+        for (uint32_t i = s; i < e; ++i) {
+            const uint32_t r = order[i];
+            if (r < n) sum += static_cast<double>(to_f(rows[static_cast<size_t>(r) * dim + d]));
+        }
         centres[static_cast<size_t>(c) * dim + d] = static_cast<float>(sum / static_cast<double>(e - s));
     }
 }
@@ -546,32 +588,55 @@ __global__ __launch_bounds__(kThreads) void pq_assign_kernel(const T* rows, uint
     codes[r * code_stride + m] = static_cast<uint8_t>(bk);
 }
 
-// PQ keys of (row, m) pairs for the codebook update: m * 256 + code.
-__global__ void pq_keys_kernel(const uint8_t* codes, uint64_t n, uint32_t pq_dim, uint32_t* keys,
-                               uint32_t* vals)
+// PQ codebook update grouping: key m * 256 + code of each (row, subspace).
+__global__ void pq_key_count_kernel(const uint8_t* codes, uint64_t n, uint32_t pq_dim,
+                                    uint32_t* counts)
 {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n * pq_dim) return;
     const uint32_t m = static_cast<uint32_t>(i % pq_dim);
-    keys[i] = m * 256u + codes[i];
-    vals[i] = static_cast<uint32_t>(i / pq_dim);
+    atomicAdd(&counts[m * 256u + codes[i]], 1u);
+}
+
+// The rows of each PQ key in ascending order (one wave per key, as
+// key_lists_kernel, reading the key's subspace column of the codes).
+__global__ __launch_bounds__(kThreads) void pq_key_lists_kernel(const uint8_t* codes, uint64_t n,
+                                                                uint32_t pq_dim,
+                                                                const uint32_t* start,
+                                                                uint32_t* order)
+{
+    const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+    const uint32_t c = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+    if (c >= pq_dim * 256u) return;
+    const uint32_t m = c / 256u, code = c % 256u;
+    uint32_t pos = start[c];
+    const uint64_t below = (1ull << lane) - 1;
+    for (uint64_t r0 = 0; r0 < n; r0 += kWave) {
+        const uint64_t r = r0 + static_cast<uint64_t>(lane);
+        const bool hit = r < n && codes[r * pq_dim + m] == code;
+        const uint64_t mk = __ballot(hit);
+        if (hit) order[pos + static_cast<uint32_t>(__popcll(mk & below))] = static_cast<uint32_t>(r);
+        pos += static_cast<uint32_t>(__popcll(mk));
+    }
 }
 
 // PQ codebook update: entry (m, k) = mean over its rows of the subspace's
 // dims (fp64 sums over rows ascending, rounded to fp32); empty keeps.
 template <class T>
-__global__ void pq_mean_kernel(const T* rows, uint32_t dim, uint32_t pq_dim, const uint32_t* order,
-                               const uint32_t* start, float* centroids)
+__global__ void pq_mean_kernel(const T* rows, uint32_t dim, uint64_t n, uint32_t pq_dim,
+                               const uint32_t* order, const uint32_t* start, float* centroids)
 {
     const uint32_t key = blockIdx.x;
     const uint32_t m = key / 256u, k = key % 256u;
     const uint32_t sub = dim / pq_dim;
     const uint32_t s = start[key], e = start[key + 1];
-    if (s == e) return;
+    if (s >= e || e > n * pq_dim) return;
     for (uint32_t t = threadIdx.x; t < sub; t += blockDim.x) {
         double sum = 0.0;
-        for (uint32_t i = s; i < e; ++i)
-            sum += static_cast<double>(to_f(rows[static_cast<size_t>(order[i]) * dim + m * sub + t]));
+        for (uint32_t i = s; i < e; ++i) {
+            const uint32_t r = order[i];
+            if (r < n) sum += static_cast<double>(to_f(rows[static_cast<size_t>(r) * dim + m * sub + t]));
+        }
         centroids[static_cast<size_t>(k) * dim + m * sub + t] =
             static_cast<float>(sum / static_cast<double>(e - s));
     }
@@ -975,34 +1040,28 @@ __global__ __launch_bounds__(kThreads) void cagra_prune_kernel(const uint32_t* k
     }
 }
 
-// Reverse-edge keys of a graph: edge u -> v at position k is the key
-// (v << 34) | (k << 27) | u (n < 2^27, degree <= 128).
-__global__ void reverse_keys_kernel(const uint32_t* g, uint32_t n, uint32_t degree, uint64_t* keys)
+// Reverse edges: counts per target row, then each edge u -> v at position
+// k stored as the key (k << 27) | u in v's segment (n < 2^27, degree <=
+// 128); a segment's order is arbitrary, its set is fixed.
+__global__ void reverse_count_kernel(const uint32_t* g, uint32_t n, uint32_t degree, uint32_t* counts)
 {
     const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= static_cast<uint64_t>(n) * degree) return;
-    const uint32_t u = static_cast<uint32_t>(e / degree);
-    const uint32_t k = static_cast<uint32_t>(e % degree);
     const uint32_t v = g[e];
-    keys[e] = v >= n ? ~0ull
-                     : (static_cast<uint64_t>(v) << 34) | (static_cast<uint64_t>(k) << 27) | u;
+    if (v < n) atomicAdd(&counts[v], 1u);
 }
 
-__global__ void reverse_starts_kernel(const uint64_t* keys, uint64_t count, uint32_t n,
-                                      uint32_t* start)
+__global__ void reverse_fill_kernel(const uint32_t* g, uint32_t n, uint32_t degree,
+                                    const uint32_t* rstart, uint32_t* fill, uint64_t* rkeys)
 {
-    const uint32_t v = blockIdx.x * blockDim.x + threadIdx.x;
-    if (v > n) return;
-    const uint64_t want = static_cast<uint64_t>(v) << 34;
-    uint64_t lo = 0, hi = count;
-    while (lo < hi) {
-        const uint64_t mid = (lo + hi) >> 1;
-        if (keys[mid] < want)
-            lo = mid + 1;
-        else
-            hi = mid;
-    }
-    start[v] = static_cast<uint32_t>(lo);
+    const uint64_t e = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= static_cast<uint64_t>(n) * degree) return;
+    const uint32_t v = g[e];
+    if (v >= n) return;
+    const uint32_t u = static_cast<uint32_t>(e / degree);
+    const uint32_t k = static_cast<uint32_t>(e % degree);
+    const uint32_t slot = rstart[v] + atomicAdd(&fill[v], 1u);
+    rkeys[slot] = (static_cast<uint64_t>(k) << 27) | u;
 }
 
 // CAGRA's reverse-edge merge (same paper, sec. IV-B): row i keeps the first
@@ -1030,10 +1089,21 @@ __global__ void reverse_merge_kernel(const uint32_t* pruned, const uint64_t* rke
         if (v == kNone || v == i || has(v)) continue;
         o[k++] = v;
     }
+    // the reverse edges in (position, source) order: the segment's keys
+    // taken by successive minima, the first 2 degree of them
     const uint32_t rs = rstart[i], re = rstart[i + 1];
-    const uint32_t rcap = rs + 2 * degree < re ? rs + 2 * degree : re;
-    for (uint32_t r = rs; r < rcap && k < degree; ++r) {
-        const uint32_t v = static_cast<uint32_t>(rkeys[r] & ((1ull << 27) - 1));
+    uint64_t prev = 0;
+    bool have_prev = false;
+    for (uint32_t t = 0; t < 2 * degree && k < degree; ++t) {
+        uint64_t best = ~0ull;
+        for (uint32_t r = rs; r < re; ++r) {
+            const uint64_t key = rkeys[r];
+            if ((!have_prev || key > prev) && key < best) best = key;
+        }
+        if (best == ~0ull) break;
+        prev = best;
+        have_prev = true;
+        const uint32_t v = static_cast<uint32_t>(best & ((1ull << 27) - 1));
         if (v == i || has(v)) continue;
         o[k++] = v;
     }
@@ -1160,41 +1230,34 @@ template <class T>
 int kmeans_t(Context* ctx, const T* rows, uint32_t dim, uint64_t n, uint32_t k, uint32_t iters,
              float* centres)
 {
-    size_t sort_bytes = 0;
-    if (hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr), static_cast<int>(n), 0,
-                                           32, ctx->stream) != hipSuccess)
-        return ctx->fail_hip("k-means sort size");
     unsigned char* buf = static_cast<unsigned char*>(ctx->scratch(
         Context::kScratchBuild,
-        carve_size({n * 4, n * 4, n * 4, n * 4, (static_cast<size_t>(k) + 1) * 4, k * 4ull, sort_bytes})));
+        carve_size({n * 4, n * 4, (static_cast<size_t>(k) + 1) * 4, (static_cast<size_t>(k) + 1) * 4,
+                    k * 4ull})));
     if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "k-means scratch allocation failed");
     Carve cv{buf, 0};
     uint32_t* idx = cv.take<uint32_t>(n);
-    uint32_t* keys = cv.take<uint32_t>(n);
-    uint32_t* iota = cv.take<uint32_t>(n);
     uint32_t* order = cv.take<uint32_t>(n);
+    uint32_t* counts = cv.take<uint32_t>(static_cast<size_t>(k) + 1);
     uint32_t* start = cv.take<uint32_t>(static_cast<size_t>(k) + 1);
     float* cnorm = cv.take<float>(k);
-    void* tmp = cv.take<unsigned char>(sort_bytes);
-    hipLaunchKernelGGL(iota_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0,
-                       ctx->stream, iota, n);
     for (uint32_t it = 0; it < iters; ++it) {
         hipLaunchKernelGGL(row_sqnorm_kernel, dim3((k + 255) / 256), dim3(256), 0, ctx->stream, centres,
                            k, dim, cnorm);
         hipLaunchKernelGGL(assign_kernel<T>, dim3(static_cast<uint32_t>((n + kTile - 1) / kTile)),
                            dim3(kThreads), 0, ctx->stream, rows, static_cast<size_t>(dim), dim, n,
                            centres, cnorm, k, idx, static_cast<float*>(nullptr));
-        size_t tb = sort_bytes;
-        if (hipcub::DeviceRadixSort::SortPairs(tmp, tb, idx, keys, iota, order, static_cast<int>(n), 0,
-                                               32, ctx->stream) != hipSuccess)
-            return ctx->fail_hip("k-means sort");
-        hipLaunchKernelGGL(key_starts_kernel, dim3((k + 256) / 256), dim3(256), 0, ctx->stream, keys, n,
-                           k, start);
+        // the rows of each centre in ascending order
+        if (hipMemsetAsync(counts, 0, (static_cast<size_t>(k) + 1) * 4, ctx->stream) != hipSuccess)
+            return ctx->fail_hip("k-means counts clear");
+        hipLaunchKernelGGL(key_count_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0,
+                           ctx->stream, idx, n, k, counts);
+        hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, counts,
+                           static_cast<uint64_t>(k), start);
+        hipLaunchKernelGGL(key_lists_kernel, dim3((k + 3) / 4), dim3(kThreads), 0, ctx->stream, idx, n,
+                           k, start, order);
         hipLaunchKernelGGL(centre_mean_kernel<T>, dim3(k), dim3(kThreads), 0, ctx->stream, rows, dim,
-                           order, start, centres);
+                           n, order, start, centres);
     }
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("k-means launch");
     return GOFANN_OK;
@@ -1239,31 +1302,21 @@ int knn_t(Context* ctx, const T* rows, uint32_t dim, const gofann_build_buckets*
         }
     }
     // query tiles per bucket: counts, exclusive sum, fill
-    size_t scan_bytes = 0;
-    if (hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<uint32_t*>(nullptr),
-                                         static_cast<uint32_t*>(nullptr), static_cast<int>(nb) + 1,
-                                         ctx->stream) != hipSuccess)
-        return ctx->fail_hip("kNN scan size");
-    // tiles <= rows / 64 + buckets
+    // (tiles <= rows / 64 + buckets)
     const size_t max_tiles = static_cast<size_t>(b->rows) / kTile + nb + 1;
     unsigned char* buf = static_cast<unsigned char*>(ctx->scratch(
         Context::kScratchBuild,
-        carve_size({(nb + 1ull) * 4, (nb + 1ull) * 4, max_tiles * 4, max_tiles * 4, scan_bytes, 16})));
+        carve_size({(nb + 1ull) * 4, (nb + 1ull) * 4, max_tiles * 4, max_tiles * 4})));
     if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "kNN scratch allocation failed");
     Carve cv{buf, 0};
     uint32_t* counts = cv.take<uint32_t>(nb + 1ull);
     uint32_t* tile_off = cv.take<uint32_t>(nb + 1ull);
     uint32_t* tile_bucket = cv.take<uint32_t>(max_tiles);
     uint32_t* tile_row0 = cv.take<uint32_t>(max_tiles);
-    void* tmp = cv.take<unsigned char>(scan_bytes);
-    if (hipMemsetAsync(counts, 0, (nb + 1ull) * 4, ctx->stream) != hipSuccess)
-        return ctx->fail_hip("kNN counts clear");
     hipLaunchKernelGGL(knn_tile_count_kernel, dim3((nb + 255) / 256), dim3(256), 0, ctx->stream,
                        b->bucket_offsets, nb, counts);
-    size_t sb = scan_bytes;
-    if (hipcub::DeviceScan::ExclusiveSum(tmp, sb, counts, tile_off, static_cast<int>(nb) + 1,
-                                         ctx->stream) != hipSuccess)
-        return ctx->fail_hip("kNN tile scan");
+    hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, counts,
+                       static_cast<uint64_t>(nb), tile_off);
     uint32_t tiles = 0;
     if (hipMemcpyAsync(&tiles, tile_off + nb, 4, hipMemcpyDeviceToHost, ctx->stream) != hipSuccess ||
         hipStreamSynchronize(ctx->stream) != hipSuccess)
@@ -1392,38 +1445,29 @@ int pq_train_t(Context* ctx, const T* rows, uint32_t dim, uint64_t n, uint32_t p
                float* centroids, int elem)
 {
     const uint64_t pairs = n * pq_dim;
-    size_t sort_bytes = 0;
-    if (hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr),
-                                           static_cast<uint32_t*>(nullptr), static_cast<int>(pairs), 0,
-                                           32, ctx->stream) != hipSuccess)
-        return ctx->fail_hip("PQ sort size");
     const uint32_t nkeys = pq_dim * 256u;
     unsigned char* buf = static_cast<unsigned char*>(ctx->scratch(
         Context::kScratchBuild,
-        carve_size({pairs, pairs * 4, pairs * 4, pairs * 4, pairs * 4, (nkeys + 1ull) * 4, sort_bytes})));
+        carve_size({pairs, pairs * 4, (nkeys + 1ull) * 4, (nkeys + 1ull) * 4})));
     if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "PQ training scratch allocation failed");
     Carve cv{buf, 0};
     uint8_t* codes = cv.take<uint8_t>(pairs);
-    uint32_t* keys = cv.take<uint32_t>(pairs);
-    uint32_t* vals = cv.take<uint32_t>(pairs);
-    uint32_t* skeys = cv.take<uint32_t>(pairs);
     uint32_t* order = cv.take<uint32_t>(pairs);
+    uint32_t* counts = cv.take<uint32_t>(nkeys + 1ull);
     uint32_t* start = cv.take<uint32_t>(nkeys + 1ull);
-    void* tmp = cv.take<unsigned char>(sort_bytes);
     for (uint32_t it = 0; it < iters; ++it) {
         if (int rc = build_pq_encode(ctx, rows, elem, dim, n, pq_dim, centroids, codes, pq_dim)) return rc;
-        hipLaunchKernelGGL(pq_keys_kernel, dim3(static_cast<uint32_t>((pairs + 255) / 256)), dim3(256), 0,
-                           ctx->stream, codes, n, pq_dim, keys, vals);
-        size_t tb = sort_bytes;
-        if (hipcub::DeviceRadixSort::SortPairs(tmp, tb, keys, skeys, vals, order, static_cast<int>(pairs),
-                                               0, 32, ctx->stream) != hipSuccess)
-            return ctx->fail_hip("PQ sort");
-        hipLaunchKernelGGL(key_starts_kernel, dim3((nkeys + 256) / 256), dim3(256), 0, ctx->stream, skeys,
-                           pairs, nkeys, start);
-        hipLaunchKernelGGL(pq_mean_kernel<T>, dim3(nkeys), dim3(64), 0, ctx->stream, rows, dim, pq_dim,
-                           order, start, centroids);
+        // the rows of each (subspace, centre) in ascending order
+        if (hipMemsetAsync(counts, 0, (nkeys + 1ull) * 4, ctx->stream) != hipSuccess)
+            return ctx->fail_hip("PQ counts clear");
+        hipLaunchKernelGGL(pq_key_count_kernel, dim3(static_cast<uint32_t>((pairs + 255) / 256)), dim3(256),
+                           0, ctx->stream, codes, n, pq_dim, counts);
+        hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, counts,
+                           static_cast<uint64_t>(nkeys), start);
+        hipLaunchKernelGGL(pq_key_lists_kernel, dim3((nkeys + 3) / 4), dim3(kThreads), 0, ctx->stream,
+                           codes, n, pq_dim, start, order);
+        hipLaunchKernelGGL(pq_mean_kernel<T>, dim3(nkeys), dim3(64), 0, ctx->stream, rows, dim, n,
+                           pq_dim, order, start, centroids);
     }
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("PQ training launch");
     return GOFANN_OK;
@@ -1644,28 +1688,24 @@ int build_cagra_optimize(Context* ctx, const uint32_t* knn, uint32_t n, uint32_t
     hipLaunchKernelGGL(cagra_prune_kernel, dim3((n + 3) / 4), dim3(kThreads), 0, ctx->stream, knn, n, kin,
                        degree, pruned);
     const uint64_t edges = static_cast<uint64_t>(n) * degree;
-    size_t sort_bytes = 0;
-    if (hipcub::DeviceRadixSort::SortKeys(nullptr, sort_bytes, static_cast<uint64_t*>(nullptr),
-                                          static_cast<uint64_t*>(nullptr), static_cast<int>(edges), 0, 64,
-                                          ctx->stream) != hipSuccess)
-        return ctx->fail_hip("reverse sort size");
     unsigned char* buf = static_cast<unsigned char*>(ctx->scratch(
-        Context::kScratchBuild, carve_size({edges * 8, edges * 8, (n + 1ull) * 4, sort_bytes})));
+        Context::kScratchBuild, carve_size({edges * 8, (n + 1ull) * 4, (n + 1ull) * 4, (n + 1ull) * 4})));
     if (!buf) return ctx->fail(GOFANN_ERR_NOMEM, "CAGRA optimise scratch allocation failed");
     Carve cv{buf, 0};
-    uint64_t* keys = cv.take<uint64_t>(edges);
-    uint64_t* skeys = cv.take<uint64_t>(edges);
+    uint64_t* rkeys = cv.take<uint64_t>(edges);
+    uint32_t* counts = cv.take<uint32_t>(n + 1ull);
     uint32_t* rstart = cv.take<uint32_t>(n + 1ull);
-    void* tmp = cv.take<unsigned char>(sort_bytes);
-    hipLaunchKernelGGL(reverse_keys_kernel, dim3(static_cast<uint32_t>((edges + 255) / 256)), dim3(256), 0,
-                       ctx->stream, pruned, n, degree, keys);
-    size_t tb = sort_bytes;
-    if (hipcub::DeviceRadixSort::SortKeys(tmp, tb, keys, skeys, static_cast<int>(edges), 0, 64,
-                                          ctx->stream) != hipSuccess)
-        return ctx->fail_hip("reverse sort");
-    hipLaunchKernelGGL(reverse_starts_kernel, dim3((n + 256) / 256), dim3(256), 0, ctx->stream, skeys,
-                       edges, n, rstart);
-    hipLaunchKernelGGL(reverse_merge_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, pruned, skeys,
+    uint32_t* fill = cv.take<uint32_t>(n + 1ull);
+    if (hipMemsetAsync(counts, 0, (n + 1ull) * 4, ctx->stream) != hipSuccess ||
+        hipMemsetAsync(fill, 0, (n + 1ull) * 4, ctx->stream) != hipSuccess)
+        return ctx->fail_hip("reverse counts clear");
+    const dim3 eg(static_cast<uint32_t>((edges + 255) / 256));
+    hipLaunchKernelGGL(reverse_count_kernel, eg, dim3(256), 0, ctx->stream, pruned, n, degree, counts);
+    hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, ctx->stream, counts,
+                       static_cast<uint64_t>(n), rstart);
+    hipLaunchKernelGGL(reverse_fill_kernel, eg, dim3(256), 0, ctx->stream, pruned, n, degree, rstart, fill,
+                       rkeys);
+    hipLaunchKernelGGL(reverse_merge_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, pruned, rkeys,
                        rstart, n, degree, out_graph);
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("CAGRA optimise launch");
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) return ctx->fail_hip("CAGRA optimise synchronize");

@@ -204,3 +204,28 @@ def test_label_index_build_matches_oracle(gpu_ctx, design, dtype):
     assert np.array_equal(tg.cpu().numpy().view(np.uint32), to.numpy().view(np.uint32))
     assert np.array_equal(gi.pq_encode(wl.base, tg, 12, backend=hip).cpu().numpy(),
                           gi.pq_encode(wl.base, to, 12, backend=ORC).numpy())
+
+
+def test_grouping_at_larger_sizes_matches_oracle(hip):
+    """The build's grouping steps (counts, the one-workgroup scan and the
+    per-key row lists) at sizes above a million keys: PQ training over 1.15M
+    (row, subspace) pairs, k-means over 70k rows, and the reverse edges of a
+    20k-row CAGRA graph; each equal to the oracle."""
+    say("grouping at larger sizes")
+    rng = np.random.default_rng(99)
+    x = rng.integers(0, 256, size=(24000, 192)).astype(np.uint8)
+    c0 = x[rng.choice(24000, 256, replace=False)].astype(np.float32)
+    wc = po.build_pq_train(x, c0, 48, 2)
+    gc = hip.pq_train(hip.rows(torch.from_numpy(x)), torch.from_numpy(c0), 48, 2)
+    assert np.array_equal(gc.cpu().numpy().view(np.uint32), wc.view(np.uint32))
+    y = (rng.standard_normal((70000, 24)) * 3).astype(np.float32)
+    k0 = y[:64].copy()
+    wk = po.build_kmeans(y, k0, 2)
+    gk = hip.kmeans(hip.rows(torch.from_numpy(y)), torch.from_numpy(k0), 2)
+    assert np.array_equal(gk.cpu().numpy().view(np.uint32), wk.view(np.uint32))
+    z = rng.standard_normal((20000, 8)).astype(np.float32)
+    off = np.array([0, 20000], np.uint32)
+    knn = _u32(hip.knn(hip.rows(torch.from_numpy(z)), off, 64))
+    wp, wg = po.build_cagra_optimize(knn, 32)
+    gp_, gg = hip.cagra_optimize(torch.from_numpy(knn.view(np.int32)), 32)
+    assert np.array_equal(_u32(gp_), wp) and np.array_equal(_u32(gg), wg)
