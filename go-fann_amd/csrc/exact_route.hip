@@ -3,17 +3,21 @@
 // Reference: run_full_gpu_highfreq_route (src/search/full_gpu/
 // backend_full_gpu.cu:1682-2042) launched by full_gpu_highfreq_kernel
 // (:2045-2122).  A beam search whose frontier is keyed by the exact squared
-// L2 distance of u8 vectors (l2_distance_device :1199-1244: an integer, here
-// |b|^2 + |q|^2 - 2 b.q in u32 through v_dot4_u32_u8, converted to float),
-// with the route filter applied to every expanded node and a sorted best-k
-// with sample dedup (insert_best_result :1342-1375).
+// L2 distance (u8 vectors: l2_distance_device :1199-1244, an integer, here
+// |b|^2 + |q|^2 - 2 b.q in u32 through v_dot4_u32_u8, converted to float;
+// f32 and f16 vectors: :1107-1160, in that function's warp order, with the
+// query in LDS as f32), with the route filter applied to every expanded
+// node and a sorted best-k with sample dedup (insert_best_result
+// :1342-1375).
 //
 // Per step (one wave64 per route):
 //  * lane 0: filter of the expanded node (row mask & route bits, every active
 //    legacy range, the route predicate when enabled) and its best-k insert;
 //  * lane j: adjacency entry j of the node (prefetched at pickup), its
-//    visited test, group bound and sample id, then the exact distance of its
-//    own base row -- every lane streams a different row, 16 bytes a load;
+//    visited test, group bound and sample id, then (u8) the exact distance
+//    of its own base row -- every lane streams a different row, 16 bytes a
+//    load; float rows are scored two at a time, one per 32-lane half, in
+//    the reference's warp order (exact_dist.hpp);
 //  * candidates that cannot enter a full frontier are dropped in parallel,
 //    the rest are admitted by lane 0 in adjacency order (smmh2 insert,
 //    pop_max at Q+2), and the admitted rows enter the visited set;
@@ -32,6 +36,7 @@
 #include <string>
 
 #include "device_common.hpp"
+#include "exact_dist.hpp"
 #include "gofann_internal.hpp"
 
 // Visited-set slabs of gofann_exact_search_noalloc: a fixed device array in
@@ -497,10 +502,48 @@ __device__ __forceinline__ void load_node(const gofann_graph_view& g,
     }
 }
 
+// Float rows (f32 / f16): the neighbours' exact distances in the warp
+// order, two rows at a time (one per 32-lane half, candidates taken in lane
+// order); lane j of the wave returns the distance of its own candidate
+// (FLT_MAX where keep is false).
+template <int kElem>
+__device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t dim,
+                                                  const float* qf, bool keep, uint32_t samp,
+                                                  int lane)
+{
+    float out = FLT_MAX;
+    const size_t row_bytes = static_cast<size_t>(dim) * elem_bytes(kElem);
+    uint64_t m = ballot(keep);
+    while (m) {
+        const int ja = __builtin_ctzll(m);
+        m &= m - 1;
+        int jb = -1;
+        if (m) {
+            jb = __builtin_ctzll(m);
+            m &= m - 1;
+        }
+        const uint32_t sa = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), ja));
+        const uint32_t sb = jb >= 0
+                                ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), jb))
+                                : sa;
+        const uint32_t s = lane < 32 ? sa : sb;
+        const float t = w32_tree<kElem>(
+            l2_w32_partial<kElem>(base + static_cast<size_t>(s) * row_bytes, qf, dim,
+                                  static_cast<uint32_t>(lane) & 31u));
+        const float da = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0));
+        const float db = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32));
+        if (lane == ja) out = da;
+        if (lane == jb) out = db;
+    }
+    return out;
+}
+
 // kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  kRegs > 0:
 // the frontier lives in kRegs registers per lane (Q + 2 <= 64 kRegs), 0: in
-// LDS.
-template <int kVisited, int kC, int kRegs>
+// LDS.  kElem: the element type of base and queries (GOFANN_ELEM_*); u8
+// rows are scored per lane (integer, exact in any order), f32 / f16 rows
+// by wave_float_dists.
+template <int kVisited, int kC, int kRegs, int kElem>
 __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel(ExactArgs a)
 {
     constexpr int kRowUnroll = kRegs > 0 ? kExactRegsRowUnroll : GOFANN_EXACT_ROW_UNROLL;
@@ -533,20 +576,29 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
                                 ? a.graph.degree
                                 : static_cast<uint32_t>(kMaxDegree);
 
-    // Query row into LDS (zero-padded to 16 bytes) and |q|^2.
-    const uint8_t* qrow = a.queries + static_cast<size_t>(a.routes.route_query[route]) * a.dim;
-    const uint32_t qwords = (a.dim + 15u) / 16u * 4u;
+    // Query row into LDS: u8 as words (zero-padded to 16 bytes) with |q|^2,
+    // f32 / f16 as f32.
+    const float* qf = reinterpret_cast<const float*>(lds);
     uint32_t qn = 0;
-    for (uint32_t w = lane; w < qwords; w += kWave) {
-        uint32_t v = 0;
-        for (uint32_t b = 0; b < 4; ++b) {
-            const uint32_t d = w * 4 + b;
-            if (d < a.dim) v |= static_cast<uint32_t>(qrow[d]) << (8 * b);
+    if constexpr (kElem == GOFANN_ELEM_U8) {
+        const uint8_t* qrow = a.queries + static_cast<size_t>(a.routes.route_query[route]) * a.dim;
+        const uint32_t qwords = (a.dim + 15u) / 16u * 4u;
+        for (uint32_t w = lane; w < qwords; w += kWave) {
+            uint32_t v = 0;
+            for (uint32_t b = 0; b < 4; ++b) {
+                const uint32_t d = w * 4 + b;
+                if (d < a.dim) v |= static_cast<uint32_t>(qrow[d]) << (8 * b);
+            }
+            qw[w] = v;
+            qn = __builtin_amdgcn_udot4(v, v, qn, false);
         }
-        qw[w] = v;
-        qn = __builtin_amdgcn_udot4(v, v, qn, false);
+        for (int o = 32; o > 0; o >>= 1) qn += static_cast<uint32_t>(__shfl_xor(static_cast<int>(qn), o, kWave));
+    } else {
+        const uint8_t* qrow = a.queries + static_cast<size_t>(a.routes.route_query[route]) * a.dim *
+                                              elem_bytes(kElem);
+        float* qs = reinterpret_cast<float*>(lds);
+        for (uint32_t d = lane; d < a.dim; d += kWave) qs[d] = elem_to_float<kElem>(qrow, d);
     }
-    for (int o = 32; o > 0; o >>= 1) qn += static_cast<uint32_t>(__shfl_xor(static_cast<int>(qn), o, kWave));
     visited.init(reinterpret_cast<uint32_t*>(lds + a.off_hash),
                  a.hash_global ? a.hash_global + static_cast<size_t>(slot) * kHashCapacity : nullptr,
                  lane);
@@ -570,10 +622,17 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
     } else {
         const uint32_t s0 = a.graph.row_to_sample[off + seed];
         if (s0 < a.samples) {
-            const float d0 = bcast0f(
-                lane == 0 ? static_cast<float>(
-                                l2_u8_row<kRowUnroll>(a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn))
-                          : 0.0f);
+            float d0;
+            if constexpr (kElem == GOFANN_ELEM_U8) {
+                d0 = bcast0f(lane == 0 ? static_cast<float>(l2_u8_row<kRowUnroll>(
+                                             a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn))
+                                       : 0.0f);
+            } else {
+                // both halves score the seed row; the first lane's sum is it
+                d0 = bcast0f(w32_tree<kElem>(l2_w32_partial<kElem>(
+                    a.base + static_cast<size_t>(s0) * a.dim * elem_bytes(kElem), qf, a.dim,
+                    static_cast<uint32_t>(lane) & 31u)));
+            }
             const Entry kp = {d0, seed, d0, s0};
             if constexpr (kRegs > 0) {
                 rh_insert(rh, heap_size, kp, lane);
@@ -631,18 +690,24 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
                                      a.pred.csr_offsets[sample + 1], lane);
             }
         }
-        const uint8_t* brow = a.base + static_cast<size_t>(samp) * a.dim;
-        uint32_t d32;
-        if constexpr (kC > 0) {
-            uint4 rb[kC];
-            row_load<kC>(brow, keep, rb);
-            d32 = row_dist<kC>(rb, qw, qn);
+        uint32_t d32 = 0;
+        float fdist = FLT_MAX;
+        if constexpr (kElem == GOFANN_ELEM_U8) {
+            const uint8_t* brow = a.base + static_cast<size_t>(samp) * a.dim;
+            if constexpr (kC > 0) {
+                uint4 rb[kC];
+                row_load<kC>(brow, keep, rb);
+                d32 = row_dist<kC>(rb, qw, qn);
+            } else {
+                d32 = keep ? l2_u8_row<kRowUnroll>(brow, qw, a.dim, qn) : 0u;
+            }
+            // The distance is complete here: the rows and query words are
+            // dead before the filter below.
+            asm volatile("" : "+v"(d32)::"memory");
         } else {
-            d32 = keep ? l2_u8_row<kRowUnroll>(brow, qw, a.dim, qn) : 0u;
+            fdist = wave_float_dists<kElem>(a.base, a.dim, qf, keep, samp, lane);
+            asm volatile("" : "+v"(fdist)::"memory");
         }
-        // The distance is complete here: the rows and query words are dead
-        // before the filter below.
-        asm volatile("" : "+v"(d32)::"memory");
 
         // The expanded node's filter (wave-uniform) and best-k (lane 0).
         const uint32_t grow = off + (now.second & ~kPoolUsed);
@@ -661,7 +726,8 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
         st.passed += ok ? 1 : 0;
         ++steps;
 
-        const float dist = keep ? static_cast<float>(d32) : FLT_MAX;
+        const float dist = kElem == GOFANN_ELEM_U8 ? (keep ? static_cast<float>(d32) : FLT_MAX)
+                                                   : fdist;
         st.scored += __popcll(ballot(keep));
 
         // Drop what cannot enter a full frontier (its maximum only falls
@@ -810,11 +876,11 @@ namespace {
 
 inline uint32_t align16u(uint32_t x) { return (x + 15u) & ~15u; }
 
-template <int kVisited, int kC, int kRegs>
+template <int kVisited, int kC, int kRegs, int kElem>
 int resident(Context* ctx, uint32_t lds)
 {
     if (lds > static_cast<uint32_t>(ctx->lds_per_block)) return 0;
-    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited, kC, kRegs>);
+    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited, kC, kRegs, kElem>);
     if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lds)) != hipSuccess) {
         (void)hipGetLastError();
@@ -835,14 +901,14 @@ int resident(Context* ctx, uint32_t lds)
 // launch.
 // fixed_slab: visited slabs for a placement outside LDS, holding at most
 // fixed_routes routes (the no-alloc entry point); nullptr: context scratch.
-template <int kC, int kRegs>
+template <int kC, int kRegs, int kElem>
 int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
                  uint32_t lds_spill, uint32_t lds_glob, uint32_t count, uint32_t* fixed_slab,
                  uint32_t fixed_routes)
 {
-    const int rf = resident<kVisitedLds, kC, kRegs>(ctx, lds_full);
-    const int rs = resident<kVisitedSpill, kC, kRegs>(ctx, lds_spill);
-    const int rg = resident<kVisitedGlobal, kC, kRegs>(ctx, lds_glob);
+    const int rf = resident<kVisitedLds, kC, kRegs, kElem>(ctx, lds_full);
+    const int rs = resident<kVisitedSpill, kC, kRegs, kElem>(ctx, lds_spill);
+    const int rg = resident<kVisitedGlobal, kC, kRegs, kElem>(ctx, lds_glob);
     int mode = kVisitedLds;
     int res = rf;
     if (hash_mode == GOFANN_PLACE_GLOBAL) {
@@ -880,11 +946,14 @@ int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
     const uint32_t lds = mode == kVisitedLds ? lds_full : (mode == kVisitedSpill ? lds_spill : lds_glob);
     const dim3 grid(count), block(kWave);
     if (mode == kVisitedLds)
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedLds, kC, kRegs>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedLds, kC, kRegs, kElem>), grid, block, lds,
+                           ctx->stream, a);
     else if (mode == kVisitedSpill)
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedSpill, kC, kRegs>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedSpill, kC, kRegs, kElem>), grid, block, lds,
+                           ctx->stream, a);
     else
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedGlobal, kC, kRegs>), grid, block, lds, ctx->stream, a);
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedGlobal, kC, kRegs, kElem>), grid, block, lds,
+                           ctx->stream, a);
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("exact route launch");
     ctx->last_table_in_lds = 0;
     ctx->last_hash_in_lds = mode == kVisitedGlobal ? 0 : (mode == kVisitedLds ? 1 : 2);
@@ -903,29 +972,45 @@ struct LaunchShape {
     uint32_t fixed_routes;
 };
 
-// Row length fixed at compile time only in builds that ask for it.
-template <int kRegs>
+// Row length fixed at compile time only in builds that ask for it (u8).
+template <int kRegs, int kElem>
 int launch_rows(const LaunchShape& s, int chunks)
 {
 #if GOFANN_EXACT_FIXED_ROWS
-    switch (chunks) {
-    case 8:
-        return launch_exact<8, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
-                                      s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
-    case 12:
-        return launch_exact<12, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
-                                       s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
-    case 16:
-        return launch_exact<16, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
-                                       s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
-    default:
-        break;
+    if constexpr (kElem == GOFANN_ELEM_U8) {
+        switch (chunks) {
+        case 8:
+            return launch_exact<8, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                                 s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
+        case 12:
+            return launch_exact<12, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full,
+                                                  s.lds_spill, s.lds_glob, s.count, s.fixed_slab,
+                                                  s.fixed_routes);
+        case 16:
+            return launch_exact<16, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full,
+                                                  s.lds_spill, s.lds_glob, s.count, s.fixed_slab,
+                                                  s.fixed_routes);
+        default:
+            break;
+        }
     }
 #else
     (void)chunks;
 #endif
-    return launch_exact<0, kRegs>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill, s.lds_glob,
-                                  s.count, s.fixed_slab, s.fixed_routes);
+    return launch_exact<0, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                         s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
+}
+
+template <int kElem>
+int launch_regs(const LaunchShape& s, int regs, int chunks)
+{
+    switch (regs) {
+    case 1: return launch_rows<1, kElem>(s, chunks);
+#if GOFANN_EXACT_MAX_REGS >= 2
+    case 2: return launch_rows<2, kElem>(s, chunks);
+#endif
+    default: return launch_rows<0, kElem>(s, chunks);
+    }
 }
 
 static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint32_t dim,
@@ -936,8 +1021,8 @@ static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint
                              uint32_t* fixed_slab, uint32_t fixed_routes)
 {
     if (!g || !r || !p) return ctx->fail(GOFANN_ERR_INVALID, "null view");
-    if (base_elem != GOFANN_ELEM_U8)
-        return ctx->fail(GOFANN_ERR_UNSUPPORTED, "the exact route takes u8 vectors");
+    if (base_elem != GOFANN_ELEM_U8 && base_elem != GOFANN_ELEM_F32 && base_elem != GOFANN_ELEM_F16)
+        return ctx->fail(GOFANN_ERR_INVALID, "base_elem must be u8, f32 or f16");
     if (!base || !queries || dim == 0)
         return ctx->fail(GOFANN_ERR_INVALID, "exact route vectors missing");
     if (dim > 65536) return ctx->fail(GOFANN_ERR_INVALID, "dim must be <= 65536 (u32 distances)");
@@ -978,7 +1063,8 @@ static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint
     const int regs = p->queue_limit + 2 <= kWave
                          ? 1
                          : (GOFANN_EXACT_MAX_REGS >= 2 && p->queue_limit + 2 <= 2 * kWave ? 2 : 0);
-    a.off_frontier = align16u((dim + 15u) / 16u * 16u);
+    a.off_frontier = base_elem == GOFANN_ELEM_U8 ? align16u((dim + 15u) / 16u * 16u)
+                                                 : align16u(dim * 4u);
     a.off_hash = regs ? a.off_frontier
                       : align16u(a.off_frontier + static_cast<uint32_t>(p->queue_limit + 2) *
                                                       sizeof(Entry));
@@ -990,12 +1076,10 @@ static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint
                            : 0;
     const LaunchShape sh{ctx, &a, p->hash_mode, lds_full, lds_spill, lds_glob, r->count,
                          fixed_slab, fixed_routes};
-    switch (regs) {
-    case 1: return launch_rows<1>(sh, chunks);
-#if GOFANN_EXACT_MAX_REGS >= 2
-    case 2: return launch_rows<2>(sh, chunks);
-#endif
-    default: return launch_rows<0>(sh, chunks);
+    switch (base_elem) {
+    case GOFANN_ELEM_F32: return launch_regs<GOFANN_ELEM_F32>(sh, regs, 0);
+    case GOFANN_ELEM_F16: return launch_regs<GOFANN_ELEM_F16>(sh, regs, 0);
+    default: return launch_regs<GOFANN_ELEM_U8>(sh, regs, chunks);
     }
 }
 

@@ -346,6 +346,21 @@ int gofann_exact_rerank(gofann_ctx* c, const void* base, int base_elem, uint32_t
     });
 }
 
+int gofann_exact_posting_scan(gofann_ctx* c, const void* base, int base_elem, uint32_t dim,
+                              uint32_t samples, const void* queries,
+                              const gofann_predicate_view* predicate,
+                              const uint32_t* route_query, const uint32_t* cand_ids,
+                              const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                              uint32_t routes, int topk, int order, uint32_t* out_ids,
+                              float* out_dists, uint32_t* pass_counts)
+{
+    return guarded(c, [&](Context* ctx) {
+        return gofann::exact_posting_scan(ctx, base, base_elem, dim, samples, queries, predicate,
+                                          route_query, cand_ids, cand_offsets, cand_sizes, routes,
+                                          topk, order, out_ids, out_dists, pass_counts);
+    });
+}
+
 int gofann_predicate_masks(gofann_ctx* c, const gofann_predicate_view* predicate,
                            const uint32_t* route_ids, const uint32_t* sample_ids, uint32_t n,
                            uint32_t* masks)

@@ -91,6 +91,12 @@ int exact_rerank(Context* ctx, const void* base, int base_elem, uint32_t dim, ui
                  const void* queries, const uint32_t* route_query, const uint32_t* shortlist,
                  uint32_t width, uint32_t routes, uint32_t topk, uint32_t* out_ids,
                  float* out_dists);
+int exact_posting_scan(Context* ctx, const void* base, int base_elem, uint32_t dim,
+                       uint32_t samples, const void* queries, const gofann_predicate_view* pred,
+                       const uint32_t* route_query, const uint32_t* cand_ids,
+                       const uint32_t* cand_offsets, const uint32_t* cand_sizes, uint32_t routes,
+                       int topk, int order, uint32_t* out_ids, float* out_dists,
+                       uint32_t* pass_counts);
 int predicate_masks(Context* ctx, const gofann_predicate_view* pred, const uint32_t* route_ids,
                     const uint32_t* sample_ids, uint32_t n, uint32_t* masks);
 int merge_routes(Context* ctx, const uint32_t* q_route_offsets, const uint32_t* q_routes,

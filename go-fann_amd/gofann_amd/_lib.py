@@ -19,6 +19,7 @@ GOFANN_OK = 0
 OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM = 0, -1, -2, -3, -4
 EARLY_STOP_FIXED, EARLY_STOP_OFF, EARLY_STOP_ADAPTIVE = 0, 1, 2
 ELEM_U8, ELEM_F32, ELEM_F16 = 0, 1, 2
+EXACT_ORDER_SERIAL, EXACT_ORDER_WARP = 0, 1
 PLACE_AUTO, PLACE_LDS, PLACE_GLOBAL, PLACE_SPILL = 0, 1, 2, 3
 
 P = C.c_void_p
@@ -211,6 +212,8 @@ SIGNATURES = {
                                                     C.POINTER(PostingShare), C.c_int, P, P,
                                                     P, P, P, P, P]),
     "gofann_exact_rerank": (C.c_int, [P, P, C.c_int, U32, U32, P, P, P, U32, U32, U32, P, P]),
+    "gofann_exact_posting_scan": (C.c_int, [P, P, C.c_int, U32, U32, P, C.POINTER(PredicateView),
+                                            P, P, P, P, U32, C.c_int, C.c_int, P, P, P]),
     "gofann_merge_routes": (C.c_int, [P, P, P, P, P, U32, U32, U32, P, P]),
     "gofann_predicate_masks": (C.c_int, [P, C.POINTER(PredicateView), P, P, U32, P]),
     "gofann_pq_score": (C.c_int, [P, C.POINTER(PqView), P, C.c_int, P, P, U32, P]),

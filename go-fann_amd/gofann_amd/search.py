@@ -338,6 +338,38 @@ def exact_rerank(ctx, base: torch.Tensor, queries: torch.Tensor, route_query: to
     return ids, dists
 
 
+def exact_posting(ctx, base: torch.Tensor, queries: torch.Tensor, route_query, cand_ids,
+                  cand_offsets, cand_sizes, topk: int, order: int = _lib.EXACT_ORDER_SERIAL,
+                  predicate: PredicateView | None = None):
+    """Exact posting scan (gofann_exact_posting_scan; the full-GPU backend's
+    posting routes, backend_full_gpu.cu:1383-1493 and 2124-2262): per route
+    the topk distinct listed samples by exact (distance, id), in the serial
+    or the warp summation order.  base and queries: device rows of one
+    element type.  Returns (ids, dists, pass counts) device tensors."""
+    if queries.dtype != base.dtype:
+        raise ValueError("queries must have the element type of the base rows")
+    elem = {torch.uint8: ELEM_U8, torch.float32: ELEM_F32, torch.float16: ELEM_F16}[base.dtype]
+    def dev(a):
+        return a.to(DEV, torch.int32).contiguous() if isinstance(a, torch.Tensor) else u32(a)
+
+    rq = dev(route_query)
+    n = int(rq.shape[0])
+    ids = torch.empty(max(n, 1) * topk, dtype=torch.int32, device=DEV)
+    dists = torch.empty(max(n, 1) * topk, dtype=torch.float32, device=DEV)
+    passes = torch.empty(max(n, 1), dtype=torch.int32, device=DEV)
+    if n == 0:
+        return ids[:0], dists[:0], passes[:0]
+    ci, co, cs = dev(cand_ids), dev(cand_offsets), dev(cand_sizes)
+    pv = predicate if predicate is not None else PredicateView()
+    ctx.check(ctx.lib.gofann_exact_posting_scan(ctx.handle, _lib.ptr(base), elem,
+                                                int(base.shape[1]), int(base.shape[0]),
+                                                _lib.ptr(queries), pv, _lib.ptr(rq),
+                                                _lib.ptr(ci), _lib.ptr(co), _lib.ptr(cs), n, topk,
+                                                order, _lib.ptr(ids), _lib.ptr(dists),
+                                                _lib.ptr(passes)))
+    return ids, dists, passes
+
+
 def merge_routes(route_to_query: np.ndarray, ids: np.ndarray, dists: np.ndarray, queries: int,
                  topk: int):
     """Route -> original query merge (rabitq_lowfreq_merge.h:709-815):

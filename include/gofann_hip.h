@@ -274,11 +274,14 @@ int gofann_rabitq_posting_scan(gofann_ctx* ctx, const gofann_rabitq_view* rq,
 
 /* ---- full-GPU exact route (run_full_gpu_highfreq_route, src/search/
  * full_gpu/backend_full_gpu.cu:1682-2042, launched by full_gpu_highfreq_kernel
- * :2045-2122).  Beam search keyed by the exact squared L2 of u8 vectors
- * (integer, returned as float); every expanded node is filtered (row mask &
- * route bits, all active legacy ranges of `routes`, the route predicate when
- * enabled) and a passing node enters a sorted best-topk with sample dedup.
- * base [samples][dim] u8 (16-byte aligned), queries [n][dim] u8.  label_size
+ * :2045-2122).  Beam search keyed by the exact squared L2 (u8: the integer,
+ * returned as float; f32 and f16: l2_distance_device's warp order,
+ * :1107-1160, as GOFANN_EXACT_ORDER_WARP below); every expanded node is
+ * filtered (row mask & route bits, all active legacy ranges of `routes`,
+ * the route predicate when enabled) and a passing node enters a sorted
+ * best-topk with sample dedup.  base [samples][dim] and queries [n][dim]
+ * both of base_elem (u8, f32 or f16 -- the reference's template T for both;
+ * base 16-byte aligned).  label_size
  * [groups] (device; NULL: adjacency entries are trusted) bounds each group's
  * local ids.  Outputs [routes][topk] ascending by (distance, id), padded
  * UINT32_MAX / FLT_MAX; stats (may be NULL) per route. */
@@ -317,6 +320,33 @@ int gofann_exact_search_noalloc(gofann_ctx* ctx, const void* base, int base_elem
                                 const gofann_predicate_view* predicate,
                                 const gofann_routes* routes, const gofann_exact_params* params,
                                 uint32_t* out_ids, float* out_dists, gofann_route_stats* stats);
+
+/* ---- exact posting scans of the full-GPU backend (full_gpu_range_posting_
+ * kernel, src/search/full_gpu/backend_full_gpu.cu:1383-1493, and
+ * full_gpu_lowfreq_kernel :2124-2262).  Route r scans the sample ids
+ * cand_ids[cand_offsets[r] .. + cand_sizes[r]) against query
+ * route_query[r]; ids UINT32_MAX or >= samples are skipped, and with the
+ * route predicate enabled only passing samples count.  Each is scored by
+ * exact squared L2 (base [samples][dim] and queries [n][dim] both of
+ * base_elem: u8, f32 or f16; base 16-byte aligned) in `order`:
+ *   GOFANN_EXACT_ORDER_SERIAL -- one chain over d ascending, the range
+ *     posting kernel's order (:1443-1469);
+ *   GOFANN_EXACT_ORDER_WARP -- l2_distance_device's warp order (:1107-1160;
+ *     u8: the integer sum), the low-frequency group kernel's.
+ * Outputs [routes][topk] (topk <= 64): the topk least (distance, id) pairs
+ * over the distinct passing samples (insert_best_result's sample dedup,
+ * :1333-1375), ascending, padded UINT32_MAX / FLT_MAX; a NaN distance is
+ * dropped.  pass_counts (may be NULL): passing listed samples per route,
+ * duplicates included. */
+#define GOFANN_EXACT_ORDER_SERIAL 0
+#define GOFANN_EXACT_ORDER_WARP 1
+int gofann_exact_posting_scan(gofann_ctx* ctx, const void* base, int base_elem, uint32_t dim,
+                              uint32_t samples, const void* queries,
+                              const gofann_predicate_view* predicate,
+                              const uint32_t* route_query, const uint32_t* cand_ids,
+                              const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                              uint32_t routes, int topk, int order,
+                              uint32_t* out_ids, float* out_dists, uint32_t* pass_counts);
 
 /* ---- range postings ------------------------------------------------------
  * Posting segments (posting_segments::Plan, src/execution/

@@ -52,8 +52,8 @@ static orc_predicate pred_at(const orc_predicate* p, uint32_t r0)
 }
 
 int cbl_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_predicate* pred,
-                     const orc_exact_params* p, const uint8_t* base, uint32_t dim,
-                     uint32_t samples, const uint8_t* queries, const uint32_t* route_query,
+                     const orc_exact_params* p, const void* base, int elem, uint32_t dim,
+                     uint32_t samples, const void* queries, const uint32_t* route_query,
                      uint32_t routes, uint32_t* out_ids, float* out_dists,
                      orc_route_stats* stats, int threads)
 {
@@ -65,7 +65,8 @@ int cbl_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_p
         orc_graph gs = graph_at(g, r0);
         orc_predicate ps;
         if (pred) ps = pred_at(pred, r0);
-        rc |= orc_exact_search(&gs, label_size, pred ? &ps : NULL, p, base, dim, samples, queries,
+        rc |= orc_exact_search(&gs, label_size, pred ? &ps : NULL, p, base, elem, dim, samples,
+                               queries,
                                route_query + r0, n, out_ids + (size_t)r0 * K,
                                out_dists + (size_t)r0 * K, stats ? stats + r0 : NULL) != 0;
     }

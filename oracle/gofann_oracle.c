@@ -1107,12 +1107,82 @@ int orc_insert_best(float dist, uint32_t id, uint32_t topk, float* bd, uint32_t*
     return 1;
 }
 
+/* Squared L2 in the order of the reference's cooperative warp distance
+ * (l2_distance_device, backend_full_gpu.cu:1107-1160): 32 partial sums,
+ * partial j a fused multiply-add chain over the elements j, j + 32, ...
+ * (f16 rows of even dim: over the element pairs j, j + 32, ..., each pair
+ * adding fma(dx, dx, dy * dy) -- the reference writes dx*dx + dy*dy and
+ * leaves its contraction to nvcc, so this grouping is the one restated
+ * here), then the shfl_down halving tree: p[j] += p[j + 16] for j < 16,
+ * then + 8, + 4, + 2, + 1; the result is p[0].  diff = base - query.  u8
+ * rows: the integer sum (the dp4a form :1199-1244), exact in any order.
+ * row and q have element type elem (0 u8, 1 f32, 2 f16 as uint16 bits). */
+static float elem_at(const void* v, int elem, uint32_t i)
+{
+    if (elem == 1) return ((const float*)v)[i];
+    if (elem == 2) return orc_half_to_float(((const uint16_t*)v)[i]);
+    return (float)((const uint8_t*)v)[i];
+}
+
+float orc_l2_w32(const void* row, const void* q, int elem, uint32_t dim)
+{
+    if (elem == 0) return (float)orc_l2_u8_int((const uint8_t*)row, (const uint8_t*)q, dim);
+    float p[32];
+    for (uint32_t j = 0; j < 32; ++j) {
+        float acc = 0.0f;
+        if (elem == 2 && (dim & 1u) == 0) {
+            for (uint32_t d2 = j; d2 < dim / 2; d2 += 32) {
+                const float dx = elem_at(row, 2, 2 * d2) - elem_at(q, 2, 2 * d2);
+                const float dy = elem_at(row, 2, 2 * d2 + 1) - elem_at(q, 2, 2 * d2 + 1);
+                acc = acc + fmaf(dx, dx, dy * dy);
+            }
+        } else {
+            for (uint32_t d = j; d < dim; d += 32) {
+                const float diff = elem_at(row, elem, d) - elem_at(q, elem, d);
+                acc = fmaf(diff, diff, acc);
+            }
+        }
+        p[j] = acc;
+    }
+    for (uint32_t off = 16; off > 0; off >>= 1)
+        for (uint32_t j = 0; j < off; ++j) p[j] = p[j] + p[j + off];
+    return p[0];
+}
+
+/* Squared L2 in the order of the reference's range-posting scan
+ * (full_gpu_range_posting_kernel, backend_full_gpu.cu:1443-1469): one
+ * fused multiply-add chain over d ascending (f16 rows of even dim: over
+ * the pairs, dist + fma(dx, dx, dy * dy) as above); u8 elements are
+ * converted to float first (T = uint8_t there), which equals the integer
+ * sum while every partial sum stays below 2^24 (dim <= 258). */
+float orc_l2_serial(const void* row, const void* q, int elem, uint32_t dim)
+{
+    float acc = 0.0f;
+    if (elem == 2 && (dim & 1u) == 0) {
+        for (uint32_t d2 = 0; d2 < dim / 2; ++d2) {
+            const float dx = elem_at(row, 2, 2 * d2) - elem_at(q, 2, 2 * d2);
+            const float dy = elem_at(row, 2, 2 * d2 + 1) - elem_at(q, 2, 2 * d2 + 1);
+            acc = acc + fmaf(dx, dx, dy * dy);
+        }
+        return acc;
+    }
+    for (uint32_t d = 0; d < dim; ++d) {
+        const float diff = elem_at(row, elem, d) - elem_at(q, elem, d);
+        acc = fmaf(diff, diff, acc);
+    }
+    return acc;
+}
+
+static size_t elem_size(int elem) { return elem == 1 ? 4u : (elem == 2 ? 2u : 1u); }
+
 int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_predicate* pred,
-                     const orc_exact_params* p, const uint8_t* base, uint32_t dim,
-                     uint32_t samples, const uint8_t* queries, const uint32_t* route_query,
+                     const orc_exact_params* p, const void* base, int elem, uint32_t dim,
+                     uint32_t samples, const void* queries, const uint32_t* route_query,
                      uint32_t routes, uint32_t* out_ids, float* out_dists,
                      orc_route_stats* stats)
 {
+    if (elem < 0 || elem > 2) return -1;
+    const size_t es = elem_size(elem);
     const int Q = p->queue_limit;
     const uint32_t K = (uint32_t)p->topk;
     if (Q < 2 || K == 0 || K > 10) return -1;
@@ -1138,7 +1208,7 @@ int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_p
         const uint32_t group = g->route_group[r];
         const uint32_t seed = g->route_start[r];
         const uint32_t gsize = label_size ? label_size[group] : UINT32_MAX;
-        const uint8_t* q = queries + (size_t)route_query[r] * dim;
+        const void* q = (const char*)queries + (size_t)route_query[r] * dim * es;
         const uint32_t off = g->label_offset[group];
         const uint64_t qfbit = g->query_filter_bits ? g->query_filter_bits[r] : ~0ULL;
         const uint32_t active = orc_count_active_ranges(g->range_modes, r, g->range_count);
@@ -1153,7 +1223,7 @@ int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_p
             orc_hash_clear(hash);
             const uint32_t s0 = g->row_to_sample[off + seed];
             if (s0 < samples && !orc_hash_test(hash, seed)) {
-                const float d0 = (float)orc_l2_u8_int(base + (size_t)s0 * dim, q, dim);
+                const float d0 = orc_l2_w32((const char*)base + (size_t)s0 * dim * es, q, elem, dim);
                 ++st.scored;
                 orc_pair kp = {d0, seed, d0};
                 orc_smmh2_insert(pool, &heap_size, kp);
@@ -1197,7 +1267,7 @@ int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_p
                 const uint32_t s = g->row_to_sample[off + local];
                 if (s >= samples) continue;
                 cl[nc] = local;
-                cd[nc] = (float)orc_l2_u8_int(base + (size_t)s * dim, q, dim);
+                cd[nc] = orc_l2_w32((const char*)base + (size_t)s * dim * es, q, elem, dim);
                 ++nc;
             }
             st.scored += nc;
@@ -1241,6 +1311,66 @@ int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_p
     }
     free(hash);
     free(pool);
+    return 0;
+}
+
+/* Exact posting scan: the full-GPU backend's posting routes
+ * (full_gpu_range_posting_kernel, backend_full_gpu.cu:1383-1493, order
+ * ORC_EXACT_ORDER_SERIAL; full_gpu_lowfreq_kernel :2124-2262, the warp
+ * order ORC_EXACT_ORDER_W32).  Per route: every listed sample s (skipped:
+ * UINT32_MAX, s >= samples, the route predicate fails when enabled) is
+ * scored by exact squared L2 and enters the best-topk with sample dedup
+ * (insert_best_result :1333-1375), so the output is the topk least
+ * (distance, id) pairs over the distinct samples, ascending, padded
+ * (FLT_MAX, UINT32_MAX).  A NaN distance (only from NaN or infinite
+ * inputs) is skipped: the reference's insertion of one depends on which
+ * thread met it first.  pass_counts: predicate passes (all listed valid
+ * samples when the predicate is off). */
+int orc_exact_posting_scan(const orc_predicate* pred, const void* base, int elem,
+                           uint32_t dim, uint32_t samples, const void* queries,
+                           const uint32_t* route_query, const uint32_t* cand_ids,
+                           const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                           uint32_t routes, int topk, int order, uint32_t* out_ids,
+                           float* out_dists, uint32_t* pass_counts)
+{
+    if (elem < 0 || elem > 2 || topk < 1 || topk > ORC_EXACT_SCAN_MAX_TOPK) return -1;
+    const size_t es = elem_size(elem);
+    const uint32_t K = (uint32_t)topk;
+    float* bd = (float*)malloc(K * sizeof(float));
+    uint32_t* bi = (uint32_t*)malloc(K * sizeof(uint32_t));
+    if (!bd || !bi) {
+        free(bd);
+        free(bi);
+        return -1;
+    }
+    for (uint32_t r = 0; r < routes; ++r) {
+        const void* q = (const char*)queries + (size_t)route_query[r] * dim * es;
+        const int enabled = orc_pred_enabled(pred, r);
+        orc_pred_counters pc = {0, 0, 0};
+        uint32_t bsize = 0, passes = 0;
+        for (uint32_t i = 0; i < K; ++i) {
+            bd[i] = FLT_MAX;
+            bi[i] = UINT32_MAX;
+        }
+        for (uint32_t j = 0; j < cand_sizes[r]; ++j) {
+            const uint32_t s = cand_ids[cand_offsets[r] + j];
+            if (s == UINT32_MAX || s >= samples) continue;
+            if (enabled && !orc_pred_matches(pred, r, s, &pc)) continue;
+            ++passes;
+            const void* row = (const char*)base + (size_t)s * dim * es;
+            const float d = order == ORC_EXACT_ORDER_W32 ? orc_l2_w32(row, q, elem, dim)
+                                                         : orc_l2_serial(row, q, elem, dim);
+            if (d != d) continue;
+            orc_insert_best(d, s, K, bd, bi, &bsize);
+        }
+        for (uint32_t i = 0; i < K; ++i) {
+            out_ids[(size_t)r * K + i] = i < bsize ? bi[i] : UINT32_MAX;
+            out_dists[(size_t)r * K + i] = i < bsize ? bd[i] : FLT_MAX;
+        }
+        if (pass_counts) pass_counts[r] = passes;
+    }
+    free(bd);
+    free(bi);
     return 0;
 }
 

@@ -245,11 +245,26 @@ int orc_insert_best(float dist, uint32_t id, uint32_t topk, float* best_d, uint3
                     uint32_t* best_size);
 /* label_size [groups] (NULL: adjacency entries are taken as valid); stats
  * may be NULL; out [routes][topk] ascending by (distance, id). */
+/* base/queries of element type elem (0 u8, 1 f32, 2 f16 as uint16 bits);
+ * distances in the warp order (orc_l2_w32). */
 int orc_exact_search(const orc_graph* g, const uint32_t* label_size, const orc_predicate* pred,
-                     const orc_exact_params* p, const uint8_t* base, uint32_t dim,
-                     uint32_t samples, const uint8_t* queries, const uint32_t* route_query,
+                     const orc_exact_params* p, const void* base, int elem, uint32_t dim,
+                     uint32_t samples, const void* queries, const uint32_t* route_query,
                      uint32_t routes, uint32_t* out_ids, float* out_dists,
                      orc_route_stats* stats);
+float orc_l2_w32(const void* row, const void* q, int elem, uint32_t dim);
+float orc_l2_serial(const void* row, const void* q, int elem, uint32_t dim);
+
+/* ---- exact posting scans (backend_full_gpu.cu:1383-1493, 2124-2262) ---- */
+#define ORC_EXACT_ORDER_SERIAL 0
+#define ORC_EXACT_ORDER_W32 1
+#define ORC_EXACT_SCAN_MAX_TOPK 64
+int orc_exact_posting_scan(const orc_predicate* pred, const void* base, int elem,
+                           uint32_t dim, uint32_t samples, const void* queries,
+                           const uint32_t* route_query, const uint32_t* cand_ids,
+                           const uint32_t* cand_offsets, const uint32_t* cand_sizes,
+                           uint32_t routes, int topk, int order, uint32_t* out_ids,
+                           float* out_dists, uint32_t* pass_counts);
 
 /* ---------------- posting scans (backend_pq.cu:2046-2133) ---------------- */
 int orc_pq_posting_scan(const orc_predicate* pred, const uint8_t* codes,

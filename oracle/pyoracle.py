@@ -74,8 +74,11 @@ def lib():
         _lib.orc_smmh2_pop_min.argtypes = [P, C.POINTER(C.c_int)]
         for name in ("orc_pq_adc", "orc_priority", "orc_bias_penalty", "orc_rabitq_score_b1",
                      "orc_l2_u8", "orc_l2_f32", "orc_l2_f16", "orc_half_to_float",
-                     "orc_minimum_pending_base", "orc_apply_filter_bonuses"):
+                     "orc_minimum_pending_base", "orc_apply_filter_bonuses", "orc_l2_w32",
+                     "orc_l2_serial"):
             getattr(_lib, name).restype = C.c_float
+        _lib.orc_l2_w32.argtypes = [P, P, C.c_int, U32]
+        _lib.orc_l2_serial.argtypes = [P, P, C.c_int, U32]
         _lib.orc_priority.argtypes = [C.c_float, C.c_float, C.c_int, P]
         _lib.orc_bias_penalty.argtypes = [C.c_float, C.c_float]
         _lib.orc_rabitq_score_b1.argtypes = [C.c_int32, C.c_float, C.c_float, C.c_float,
@@ -541,7 +544,8 @@ def exact_search(index, routes, pred, base, queries, queue_limit=64, topk=10,
                  early_stop_mode=2, finish_limit=1, max_steps=0, label_size=None,
                  row_filter_mask=None, query_filter_bits=None, range_modes=None,
                  range_lower=None, range_upper=None, base_range_values=None, threads=None):
-    """orc_exact_search over every route: ids [R][topk] u32, dists f32, stats."""
+    """orc_exact_search over every route: ids [R][topk] u32, dists f32, stats.
+    base and queries: u8, f32 or f16 rows of one element type."""
     L = lib()
     g, keep = graph_struct(index, routes.route_group, routes.route_start)
     extra = dict(rm=c_arr(row_filter_mask, np.uint64), qb=c_arr(query_filter_bits, np.uint64),
@@ -556,15 +560,56 @@ def exact_search(index, routes, pred, base, queries, queue_limit=64, topk=10,
     ids = np.empty((max(n, 1), topk), np.uint32)
     dists = np.empty((max(n, 1), topk), np.float32)
     stats = (Stats * max(n, 1))()
-    b = np.ascontiguousarray(base, dtype=np.uint8)
-    q = np.ascontiguousarray(queries, dtype=np.uint8)
+    b, elem = _rows(base)
+    q, qelem = _rows(queries)
+    assert qelem == elem, "queries have the element type of the base rows"
     rq = c_arr(routes.route_query, np.uint32)
     prm = ExactParams(queue_limit, finish_limit, early_stop_mode, max_steps, topk)
     rc = _drive("exact_search", C.byref(g), p(extra["ls"]), C.byref(pred.struct) if pred else None,
-                            C.byref(prm), p(b), U32(b.shape[1]), U32(b.shape[0]), p(q), p(rq),
-                            U32(n), p(ids), p(dists), stats, threads=threads)
+                            C.byref(prm), p(b), C.c_int(elem), U32(b.shape[1]), U32(b.shape[0]),
+                            p(q), p(rq), U32(n), p(ids), p(dists), stats, threads=threads)
     assert rc == 0
     return ids[:n], dists[:n], stats_array(stats, n)
+
+
+EXACT_ORDER_SERIAL, EXACT_ORDER_W32 = 0, 1
+
+
+def l2_w32(row, q) -> float:
+    """orc_l2_w32: the warp-order exact distance of one row and one query."""
+    r, e = _rows(np.asarray(row)[None])
+    qq, _ = _rows(np.asarray(q)[None])
+    return float(lib().orc_l2_w32(p(r), p(qq), e, r.shape[1]))
+
+
+def l2_serial(row, q) -> float:
+    """orc_l2_serial: the serial-order exact distance of one row and one query."""
+    r, e = _rows(np.asarray(row)[None])
+    qq, _ = _rows(np.asarray(q)[None])
+    return float(lib().orc_l2_serial(p(r), p(qq), e, r.shape[1]))
+
+
+def exact_posting_scan(pred, base, queries, route_query, cand_ids, cand_offsets, cand_sizes,
+                       topk, order=EXACT_ORDER_SERIAL):
+    """orc_exact_posting_scan: per route the topk distinct listed samples by
+    exact (distance, id); (ids [R][topk], dists, pass counts)."""
+    b, elem = _rows(base)
+    q, qelem = _rows(queries)
+    assert qelem == elem
+    rq = c_arr(route_query, np.uint32)
+    ci = c_arr(cand_ids, np.uint32)
+    co = c_arr(cand_offsets, np.uint32)
+    cs = c_arr(cand_sizes, np.uint32)
+    n = len(rq)
+    ids = np.empty((max(n, 1), topk), np.uint32)
+    dists = np.empty((max(n, 1), topk), np.float32)
+    passes = np.empty(max(n, 1), np.uint32)
+    rc = lib().orc_exact_posting_scan(C.byref(pred.struct) if pred else None, p(b), elem,
+                                      U32(b.shape[1]), U32(b.shape[0]), p(q), p(rq), p(ci),
+                                      p(co), p(cs), U32(n), topk, order, p(ids), p(dists),
+                                      p(passes))
+    assert rc == 0
+    return ids[:n], dists[:n], passes[:n]
 
 
 # ---- index construction (build_oracle.c) --------------------------------

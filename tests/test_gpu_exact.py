@@ -2,8 +2,9 @@
 distance bits and the eight per-route counters identical to the oracle,
 across visited-set placements, neighbour-sample tables, early-stop modes,
 beam sizes, route predicates and legacy bit/range filters, and every
-distance path (rows of fixed length 128/192/256, dim % 16 == 0, dim % 4 ==
-0, any dim)."""
+distance path (u8 rows of fixed length 128/192/256, dim % 16 == 0, dim % 4
+== 0, any dim; f32 and f16 rows in the warp order); and the exact posting
+scans in both summation orders."""
 from __future__ import annotations
 
 import sys
@@ -42,9 +43,13 @@ def eworld(gpu_ctx):
     return _world(128, 51)
 
 
+ELEM = {np.dtype(np.uint8): _lib.ELEM_U8, np.dtype(np.float32): _lib.ELEM_F32,
+        np.dtype(np.float16): _lib.ELEM_F16}
+
+
 def _run(ctx, wl, li, rs, pred_o, pred_g, Q, topk, mode, hash_mode, nsamp, max_steps=0,
-         finish=1, legacy=None):
-    base, q = wl.base.numpy(), wl.queries.numpy()
+         finish=1, legacy=None, rows=None):
+    base, q = rows if rows is not None else (wl.base.numpy(), wl.queries.numpy())
     kw = {}
     if legacy is not None:
         kw = dict(row_filter_mask=legacy["rmask"], query_filter_bits=legacy["qbits"],
@@ -55,7 +60,8 @@ def _run(ctx, wl, li, rs, pred_o, pred_g, Q, topk, mode, hash_mode, nsamp, max_s
                                   label_size=li.label_size, **kw)
     dg = gs.DeviceGraph.upload(li, neighbor_samples=nsamp)
     dr = gs.DeviceRoutes.upload(rs)
-    dev = dict(base=wl.base.cuda(), q=wl.queries.cuda(), ls=gs.u32(li.label_size))
+    dev = dict(base=torch.from_numpy(np.ascontiguousarray(base)).cuda(),
+               q=torch.from_numpy(np.ascontiguousarray(q)).cuda(), ls=gs.u32(li.label_size))
     rv = dr.routes_view()
     if legacy is not None:
         for k in ("rmask", "qbits"):
@@ -73,7 +79,7 @@ def _run(ctx, wl, li, rs, pred_o, pred_g, Q, topk, mode, hash_mode, nsamp, max_s
     dists = torch.empty(n * topk, device="cuda")
     st = torch.zeros(n * 8, dtype=torch.int32, device="cuda")
     prm = _lib.ExactParams(Q, finish, mode, max_steps, topk, hash_mode)
-    ctx.check(ctx.lib.gofann_exact_search(ctx.handle, _lib.ptr(dev["base"]), _lib.ELEM_U8, wl.dim,
+    ctx.check(ctx.lib.gofann_exact_search(ctx.handle, _lib.ptr(dev["base"]), ELEM[base.dtype], wl.dim,
                                           wl.n, _lib.ptr(dev["q"]), dg.view(), _lib.ptr(dev["ls"]),
                                           pred_g(dr, dg), rv, prm, _lib.ptr(ids), _lib.ptr(dists),
                                           _lib.ptr(st)))
@@ -163,6 +169,108 @@ def test_exact_search_distance_paths(gpu_ctx, dim):
          _lib.PLACE_AUTO, False)
 
 
+def _float_world(dim, seed, n=4000, nq=32):
+    wl = synth.small_labelled(n=n, nq=nq, dim=dim, k=10, sigma=0.7, labels=5, seed=seed,
+                              tags=True)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=32, threshold=300)
+    return wl, li, gp.plan_queries(li, wl.query_labels).graph
+
+
+@pytest.mark.parametrize("dim", [37, 100, 128, 512])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_exact_search_float_rows(gpu_ctx, dim, dtype):
+    """f32 and f16 rows (and queries of the same type): distances in the
+    reference's warp order, bit-identical to the oracle, with the frontier
+    in registers and in LDS and every visited-set placement; odd dim takes
+    the per-element f16 path, 100 leaves partials of unequal length."""
+    wl, li, rs = _float_world(dim, 70 + dim)
+    t = np.float16 if dtype == "f16" else np.float32
+    rows = (wl.base.numpy().astype(t), wl.queries.numpy().astype(t))
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li)
+    for place, mode, Q, with_pred in (("auto", 2, 32, False), ("lds-nsamp", 2, 80, True),
+                                      ("global", 0, 128, False), ("spill-nsamp", 2, 300, True)):
+        hash_mode, nsamp = PLACE[place]
+        say("exact search float rows", dtype, "dim", dim, place, "Q", Q, "pred", with_pred)
+
+        def pred_g(dr, dg):
+            return dr.predicate_view(dg, 0.0, False) if with_pred else _lib.PredicateView()
+
+        oi, ost = _run(gpu_ctx, wl, li, rs, pred_o if with_pred else None, pred_g, Q, 10, mode,
+                       hash_mode, nsamp, finish=2, rows=rows)
+        assert (oi[:, 0] != U32MAX).sum() > rs.count // 2
+        assert ost[:, 0].max() > 5
+
+
+@pytest.fixture(scope="module")
+def scan_worlds(gpu_ctx):
+    out = {}
+    for dim in (37, 128, 512):
+        wl = synth.small_labelled(n=6000, nq=24, dim=dim, k=10, sigma=0.7, labels=5,
+                                  seed=90 + dim, tags=True)
+        li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                                  wl.centroids, degree=16, threshold=300)
+        out[dim] = (wl, li)
+    return out
+
+
+def _scan_lists(rng, n, routes):
+    """Posting lists with duplicates, UINT32_MAX, ids past the base, an
+    empty list and lists longer than one LDS chunk."""
+    sizes = rng.integers(0, 700, routes).astype(np.uint32)
+    sizes[0] = 0
+    sizes[1] = 5000
+    sizes[2] = 2048
+    offs = np.zeros(routes, np.uint32)
+    offs[1:] = np.cumsum(sizes)[:-1]
+    ids = rng.integers(0, n, int(sizes.sum())).astype(np.uint32)
+    ids[offs[1] + 3000: offs[1] + 3100] = ids[offs[1]: offs[1] + 100]
+    ids[rng.integers(0, len(ids), len(ids) // 20)] = U32MAX
+    ids[rng.integers(0, len(ids), len(ids) // 20)] = n + 3
+    return ids, offs, sizes
+
+
+@pytest.mark.parametrize("dim", [37, 128, 512])
+@pytest.mark.parametrize("dtype", ["u8", "f32", "f16"])
+@pytest.mark.parametrize("order", [_lib.EXACT_ORDER_SERIAL, _lib.EXACT_ORDER_WARP])
+def test_exact_posting_scan_matches_oracle(gpu_ctx, scan_worlds, dim, dtype, order):
+    """gofann_exact_posting_scan: ids, distance bits and pass counts equal
+    the oracle's in both summation orders, with and without the route
+    predicate, for topk 1, 10 and 64."""
+    wl, li = scan_worlds[dim]
+    x, qx = wl.base.numpy(), wl.queries.numpy()
+    if dtype == "u8":
+        lo, hi = float(x.min()), float(x.max())
+        base = np.clip(np.round((x - lo) * 255.0 / (hi - lo)), 0, 255).astype(np.uint8)
+        q = np.clip(np.round((qx - lo) * 255.0 / (hi - lo)), 0, 255).astype(np.uint8)
+    else:
+        t = np.float16 if dtype == "f16" else np.float32
+        base, q = x.astype(t), qx.astype(t)
+    rows = [(qi, ls[0], list(ls), []) for qi, ls in enumerate(wl.query_labels)]
+    rs = gp._routeset(rows, li)
+    rng = np.random.default_rng(dim + order)
+    ids, offs, sizes = _scan_lists(rng, base.shape[0], rs.count)
+    dg = gs.DeviceGraph.upload(li)
+    dr = gs.DeviceRoutes.upload(rs)
+    db = torch.from_numpy(base).cuda()
+    dq = torch.from_numpy(q).cuda()
+    for with_pred in (False, True):
+        pred_o = po.PredicateArrays.from_plan(rs.predicate, li) if with_pred else None
+        pv = dr.predicate_view(dg, 0.0, False) if with_pred else None
+        for k in (1, 10, 64):
+            say("exact posting scan", dtype, "dim", dim, "order", order, "pred", with_pred, "k", k)
+            oi, od, op = po.exact_posting_scan(pred_o, base, q, rs.route_query, ids, offs, sizes,
+                                               k, order)
+            gi_, gd, gp_ = gs.exact_posting(gpu_ctx, db, dq, rs.route_query, ids, offs, sizes, k,
+                                            order, pv)
+            torch.cuda.synchronize()
+            assert np.array_equal(gi_.cpu().numpy().view(np.uint32).reshape(-1, k), oi)
+            assert np.array_equal(gd.cpu().numpy().reshape(-1, k).view(np.uint32),
+                                  od.view(np.uint32))
+            assert np.array_equal(gp_.cpu().numpy().view(np.uint32), op)
+            assert (oi[:, 0] != U32MAX).sum() > rs.count // 2
+
+
 def test_exact_search_invalid_seeds(gpu_ctx, eworld):
     wl, li, rs = eworld
     say("exact search invalid seeds")
@@ -180,7 +288,7 @@ def test_exact_search_rejects_bad_params(gpu_ctx, eworld):
     dg = gs.DeviceGraph.upload(li)
     dr = gs.DeviceRoutes.upload(rs)
     base, q = wl.base.cuda(), wl.queries.cuda()
-    for Q, k, elem in ((1, 10, _lib.ELEM_U8), (32, 11, _lib.ELEM_U8), (32, 10, _lib.ELEM_F32)):
+    for Q, k, elem in ((1, 10, _lib.ELEM_U8), (32, 11, _lib.ELEM_U8), (32, 10, 3)):
         prm = _lib.ExactParams(Q, 1, 2, 0, k, 0)
         rc = gpu_ctx.lib.gofann_exact_search(gpu_ctx.handle, _lib.ptr(base), elem, wl.dim, wl.n,
                                              _lib.ptr(q), dg.view(), None, _lib.PredicateView(),
