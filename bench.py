@@ -66,6 +66,8 @@ def parse():
                     help="gather neighbour sample ids through row_to_sample")
     ap.add_argument("--no-records", action="store_true",
                     help="separate code rows and CSR labels instead of 64-byte sample records")
+    ap.add_argument("--no-exact-float", action="store_true",
+                    help="C3/C4: skip the all-GPU exact-distance row")
     ap.add_argument("--no-cpu-rerank-route", action="store_true",
                     help="skip the GPU+CPU-rerank route measurement")
     ap.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"), default="c2",
@@ -536,6 +538,10 @@ def _kernel_alias(name: str) -> str:
         return "traversal"
     if name.startswith("exact_rerank"):
         return "rerank"
+    if name.startswith("exact_route"):
+        return "exact_route"
+    if name.startswith("exact_scan"):
+        return "exact_scan"
     if name.startswith("label_share"):
         return "label_share_scan"
     if "label postings" in name:
@@ -598,6 +604,8 @@ def compact_record(line: dict) -> dict:
                    "coarse_entry": _compact_rabitq_leg(x.get("coarse_entry")),
                    "gpu_cpu_rerank_route": _pick(x.get("gpu_cpu_rerank_route"),
                                                  ("qps", "recall_at_10", "exposed_rerank_ms")),
+                   "full_gpu_exact": _compact_rabitq_leg(x.get("full_gpu_exact_fp32") or
+                                                         x.get("full_gpu_exact_fp16")),
                    "cpu_qps": (x.get("cpu_baseline") or {}).get("value")}
     out = {k: v for k, v in line.items() if k != "config"}
     out["config"] = cc
@@ -1329,6 +1337,10 @@ def run_c3(args, torch, ctx) -> dict:
                                    "C3 GPU + CPU rerank", wl.base.cpu().numpy(),
                                    wl.queries.cpu().numpy())
         gc.collect()
+    exact = None
+    if not args.no_exact_float:
+        exact = exact_float_leg(args, pipe, li, "range", class_gt, ladder, "C3 exact fp32")
+        gc.collect()
     cpu = None
     if not args.no_cpu_baseline:
         qb = med["queue_by_class"]
@@ -1348,7 +1360,7 @@ def run_c3(args, torch, ctx) -> dict:
             "graph_buckets": "512 k-means centres trained on the base",
             "data_model": "centre + rank-64 shared-basis spread 0.7 + N(0, 0.05^2), normalised",
             "medoid_seeds": med, "coarse_entry": coarse, "gpu_cpu_rerank_route": cpu_route,
-            "cpu_baseline": cpu}
+            "full_gpu_exact_fp32": exact, "cpu_baseline": cpu}
 
 
 def main_c3(args):
@@ -1651,6 +1663,146 @@ class RabitqLabelPipeline:
         return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
 
 
+class ExactFloatPipeline:
+    """The full-GPU exact route over C3's fp32 / C4's fp16 rows
+    (full_gpu_highfreq_kernel<float / __half>, backend_full_gpu.cu:
+    2044-2122) on a RaBitQ pipeline's route set: its graph routes as
+    exact-distance beams (gofann_exact_search, l2_distance_device's warp
+    order), its posting routes as exact posting scans
+    (gofann_exact_posting_scan: C3's range postings in the range-posting
+    kernel's serial order, :1383-1493; C4's label postings in the
+    low-frequency kernel's warp order, :2124-2262), then the per-query
+    merge.  No codes and no rerank: every distance is exact.  Queries take
+    the rows' element type (the reference's T for both)."""
+
+    stop = (2, 1)  # adaptive early stop, as ExactRoute
+
+    def __init__(self, rp, li, kind):
+        from gofann_amd import plan as gp
+        torch, gs, L = rp.torch, rp.gs, rp.L
+        self.rp, self.torch, self.gs, self.L, self.ctx = rp, torch, gs, L, rp.ctx
+        self.nq, self.classes, self.ng, self.np_ = rp.nq, rp.classes, rp.ng, rp.np_
+        self.kind = kind
+        wl = rp.wl
+        self.base = wl.base
+        self.q = wl.queries.to(wl.base.dtype).contiguous()
+        self.elem = {torch.float32: L.ELEM_F32, torch.float16: L.ELEM_F16}[wl.base.dtype]
+        self.dim, self.n = int(wl.base.shape[1]), int(wl.base.shape[0])
+        self.ls = gs.u32(li.label_size)
+        self.degree, self.nsamp = li.degree, rp.nsamp
+        self.pv = rp.dr.predicate_view(rp.dg, 0.0, False)
+        n = self.ng + self.np_
+        self.fin_i = torch.empty(max(n, 1) * 10, dtype=torch.int32, device="cuda")
+        self.fin_d = torch.empty(max(n, 1) * 10, dtype=torch.float32, device="cuda")
+        self.stats = torch.zeros(max(self.ng, 1) * 8, dtype=torch.int32, device="cuda")
+        self.passes = torch.zeros(max(self.np_, 1), dtype=torch.int32, device="cuda")
+        if kind == "range":
+            # every row of the chosen slice, the query's range as predicate
+            pq = rp.scan_query
+            rows = [(int(q), 0, [], [tuple(wl.query_ranges[q][0])]) for q in pq]
+            self.dp = gs.DeviceRoutes.upload(gp._routeset(rows, li), wl.base_ranges)
+            off, size = rp.scan_off, rp.scan_size
+            if len(off) and int(off.max()) + int(size.max()) >= 2 ** 32:
+                raise ValueError("range postings past 2^32 rows")
+            self.co = gs.u32(off.astype(np.uint32) if len(off) else np.zeros(1, np.uint32))
+            self.cs = gs.u32(size.astype(np.uint32) if len(size) else np.zeros(1, np.uint32))
+            self.cand = rp.postings
+            self.order = L.EXACT_ORDER_SERIAL
+            self.scan_rows_total = rp.scan_rows_total
+        else:
+            self.dp, self.co, self.cs = rp.dp, rp.co, rp.cs
+            self.cand = rp.dg.posting_ids
+            self.order = L.EXACT_ORDER_WARP
+            self.scan_rows_total = rp.post_rows_total
+        self.ppv = self.dp.predicate_view(rp.dg, 0.0, False)
+        self.q_off, self.q_routes = rp.q_off, rp.q_routes
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        self.ev_class = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        self.ev_join = torch.cuda.Event(enable_timing=True)
+        self.n_class_used = 0
+        self.serial_classes = False
+
+    def step(self, Q, timed=False):
+        gs, ev = self.gs, self.ev
+        if timed:
+            ev[0].record()
+            ev[1].record()
+        qs = Q if isinstance(Q, (tuple, list)) else (Q,) * len(self.classes)
+        used = graph_classes(self, qs, None, self.ev_class if timed else None)
+        self.n_class_used = len(used)
+        if timed:
+            ev[2].record()
+        self._scan()
+        if timed:
+            ev[3].record()
+        main = self.torch.cuda.current_stream()
+        for st in used:
+            main.wait_stream(st)
+        if timed:
+            self.ev_join.record()
+            ev[4].record()
+        out_i, _ = gs.merge_routes_gpu(self.ctx, self.q_off, self.q_routes, self.fin_i,
+                                       self.fin_d, 10, self.nq, 10)
+        if timed:
+            ev[5].record()
+        return out_i
+
+    def _graph(self, q, start, lo, hi, ctx=None):
+        L = self.L
+        ctx = ctx or self.ctx
+        prm = L.ExactParams(q, self.stop[1], self.stop[0], 0, 10, L.PLACE_AUTO)
+        ctx.check(ctx.lib.gofann_exact_search(
+            ctx.handle, L.ptr(self.base), self.elem, self.dim, self.n, L.ptr(self.q),
+            self.rp.dg.view(), L.ptr(self.ls), self.pv, self.rp.dr.routes_view(lo, hi, start=start),
+            prm, L.ptr(self.fin_i), L.ptr(self.fin_d), L.ptr(self.stats)))
+
+    def _scan(self):
+        L, ctx = self.L, self.ctx
+        if self.np_:
+            ctx.check(ctx.lib.gofann_exact_posting_scan(
+                ctx.handle, L.ptr(self.base), self.elem, self.dim, self.n, L.ptr(self.q),
+                self.ppv, L.ptr(self.dp.route_query), L.ptr(self.cand), L.ptr(self.co),
+                L.ptr(self.cs), self.np_, 10, self.order, L.ptr(self.fin_i[self.ng * 10:]),
+                L.ptr(self.fin_d[self.ng * 10:]), L.ptr(self.passes)))
+
+    def stage_ms(self):
+        return stage_times(self, "exact_scan")
+
+    def route_stats(self):
+        return self.stats[: self.ng * 8].cpu().numpy().reshape(-1, 8)
+
+
+def exact_float_kernels(pipe, st_ms, st):
+    """Algorithmic bytes of the exact legs: the route's (exact_route_bytes
+    over row bytes dim x element size); the scan's sample id of every listed
+    row plus the row of every predicate-passing one."""
+    rb = pipe.dim * pipe.base.element_size()
+    gb = exact_route_bytes(st, pipe.degree, rb, pipe.nsamp)
+    passed = int(pipe.passes[: pipe.np_].sum().item()) if pipe.np_ else 0
+    sb = pipe.scan_rows_total * 4.0 + passed * float(rb)
+    ek = "f32" if pipe.elem == pipe.L.ELEM_F32 else "f16"
+    order = "serial" if pipe.order == pipe.L.EXACT_ORDER_SERIAL else "warp"
+    return {f"exact_route_kernel<{ek}>": (st_ms["traversal"], gb),
+            f"exact_scan_kernel<{ek},{order}> ({pipe.kind} postings)":
+                (st_ms["exact_scan"], sb, {"passing_rows": passed,
+                                           "listed_rows": pipe.scan_rows_total})}
+
+
+def exact_float_leg(args, rp, li, kind, class_gt, ladder, label):
+    """The all-GPU exact row beside a RaBitQ leg (same routes, beams chosen
+    by the same per-class recall rule)."""
+    pipe = ExactFloatPipeline(rp, li, kind)
+    out = rabitq_leg(args, pipe, class_gt, ladder, label, exact_float_kernels)
+    out["route"] = ("exact " + ("fp32" if pipe.elem == pipe.L.ELEM_F32 else "fp16") +
+                    " beams on the graph routes, exact posting scans (" +
+                    ("serial" if pipe.order == pipe.L.EXACT_ORDER_SERIAL else "warp") +
+                    " order), merge; medoid seeds")
+    st = pipe.route_stats()
+    out["scored_per_route"] = round(float(st[:, 3].astype(np.float64).mean()), 1) if len(st) else 0
+    del pipe
+    return out
+
+
 def plan_count(segs) -> int:
     return segs.plan.count
 
@@ -1901,6 +2053,10 @@ def run_c4(args, torch, ctx, world=None) -> dict:
                                    "C4 GPU + CPU rerank", wl.base.cpu().numpy(),
                                    wl.queries.cpu().numpy())
         gc.collect()
+    exact = None
+    if not args.no_exact_float:
+        exact = exact_float_leg(args, pipe, li, "label", class_gt, ladder, "C4 exact fp16")
+        gc.collect()
     cpu = None
     if not args.no_cpu_baseline:
         pipe.chosen = (med["queue_by_class"]["equality"], med["queue_by_class"]["range"])
@@ -1919,7 +2075,7 @@ def run_c4(args, torch, ctx, world=None) -> dict:
             "build_s": wl.meta.get("build_s"),
             "graph_buckets": "4096 k-means centres trained on the base",
             "medoid_seeds": med, "coarse_entry": coarse, "gpu_cpu_rerank_route": cpu_route,
-            "cpu_baseline": cpu}
+            "full_gpu_exact_fp16": exact, "cpu_baseline": cpu}
 
 
 # ---------------------------------------------------------------------------
