@@ -16,8 +16,9 @@
 //  * lane j: adjacency entry j of the node (prefetched at pickup), its
 //    visited test, group bound and sample id, then (u8) the exact distance
 //    of its own base row -- every lane streams a different row, 16 bytes a
-//    load; float rows are scored two at a time, one per 32-lane half, in
-//    the reference's warp order (exact_dist.hpp);
+//    load; float rows are scored in the reference's warp order, 16 at a
+//    time (one per quad of lanes) or, past 4 KB a row, 2 at a time (one per
+//    32-lane half) (exact_dist.hpp);
 //  * candidates that cannot enter a full frontier are dropped in parallel,
 //    the rest are admitted by lane 0 in adjacency order (smmh2 insert,
 //    pop_max at Q+2), and the admitted rows enter the visited set;
@@ -84,10 +85,11 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_FIXED_ROWS 0
 #endif
 
-// Minimum waves per SIMD the kernel is compiled for (register budget).  6
-// holds the kernels to 80 VGPRs, 24 routes per CU, without spills (the lane
-// id is opaque per step).  At C2, Q = 80: 46.1 ms, against 49.0 at 5 waves
-// and 54.1 at 7 (the visited table leaves LDS).
+// Minimum waves per SIMD the u8 kernels are compiled for (register budget).
+// 6 holds them to 80 VGPRs, 24 routes per CU, without spills (the lane id is
+// opaque per step).  At C2, Q = 80: 46.1 ms, against 49.0 at 5 waves and
+// 54.1 at 7 (the visited table leaves LDS).  The f32 / f16 kernels (eight
+// partial sums and two 16-byte loads per lane) take 5: at 6 they spill.
 #ifndef GOFANN_EXACT_MIN_WAVES
 #define GOFANN_EXACT_MIN_WAVES 6
 #endif
@@ -109,6 +111,13 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_ROW_UNROLL 4
 #endif
 constexpr int kExactRegsRowUnroll = 3;
+
+// 128-byte blocks per quad whose loads are issued together in the float
+// kernels' row loop.
+#ifndef GOFANN_EXACT_QUAD_UNROLL
+#define GOFANN_EXACT_QUAD_UNROLL 2
+#endif
+constexpr int kExactQuadUnroll = GOFANN_EXACT_QUAD_UNROLL;
 
 struct ExactArgs {
     gofann_graph_view graph;
@@ -503,39 +512,64 @@ __device__ __forceinline__ void load_node(const gofann_graph_view& g,
 }
 
 // Float rows (f32 / f16): the neighbours' exact distances in the warp
-// order, two rows at a time (one per 32-lane half, candidates taken in lane
-// order); lane j of the wave returns the distance of its own candidate
-// (FLT_MAX where keep is false).
+// order; lane j of the wave returns the distance of its own candidate
+// (FLT_MAX where keep is false).  Rows up to kQuadMaxRowBytes: 16 rows at a
+// time, one per quad of lanes (l2_w32_quad), candidates compacted through
+// LDS in lane order (s_samp and s_dist, kMaxDegree entries, are free at
+// this point of the step).  Longer rows: two at a time, one per 32-lane
+// half (l2_w32_partial + w32_tree), which keeps every lane busy; at C3's
+// 16 KB rows this took 261 ms a step against 348 for the quads, at C4's
+// 1 KB rows the quads 140 against 329.
+constexpr size_t kQuadMaxRowBytes = 4096;
+
 template <int kElem>
 __device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t dim,
                                                   const float* qf, bool keep, uint32_t samp,
-                                                  int lane)
+                                                  int lane, uint32_t* s_samp, float* s_dist)
 {
-    float out = FLT_MAX;
     const size_t row_bytes = static_cast<size_t>(dim) * elem_bytes(kElem);
     uint64_t m = ballot(keep);
-    while (m) {
-        const int ja = __builtin_ctzll(m);
-        m &= m - 1;
-        int jb = -1;
-        if (m) {
-            jb = __builtin_ctzll(m);
+    if (row_bytes > kQuadMaxRowBytes) {
+        float out = FLT_MAX;
+        while (m) {
+            const int ja = __builtin_ctzll(m);
             m &= m - 1;
+            int jb = -1;
+            if (m) {
+                jb = __builtin_ctzll(m);
+                m &= m - 1;
+            }
+            const uint32_t sa = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), ja));
+            const uint32_t sb =
+                jb >= 0 ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), jb))
+                        : sa;
+            const uint32_t s = lane < 32 ? sa : sb;
+            const float t = w32_tree<kElem>(
+                l2_w32_partial<kElem>(base + static_cast<size_t>(s) * row_bytes, qf, dim,
+                                      static_cast<uint32_t>(lane) & 31u));
+            const float da = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0));
+            const float db = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32));
+            if (lane == ja) out = da;
+            if (lane == jb) out = db;
         }
-        const uint32_t sa = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), ja));
-        const uint32_t sb = jb >= 0
-                                ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), jb))
-                                : sa;
-        const uint32_t s = lane < 32 ? sa : sb;
-        const float t = w32_tree<kElem>(
-            l2_w32_partial<kElem>(base + static_cast<size_t>(s) * row_bytes, qf, dim,
-                                  static_cast<uint32_t>(lane) & 31u));
-        const float da = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0));
-        const float db = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32));
-        if (lane == ja) out = da;
-        if (lane == jb) out = db;
+        return out;
     }
-    return out;
+    const int n = __popcll(m);
+    const uint32_t rank = lanes_below(m);
+    if (keep) s_samp[rank] = samp;
+    __threadfence_block();
+    const int quad = lane >> 2;
+    const uint32_t g = static_cast<uint32_t>(lane) & 3u;
+    for (int c = quad; c - quad < n; c += 16) {
+        if (c < n) {
+            const uint32_t s = s_samp[c];
+            const float d = l2_w32_quad<kElem, kExactQuadUnroll>(
+                base + static_cast<size_t>(s) * row_bytes, qf, dim, g);
+            if (g == 0) s_dist[c] = d;
+        }
+    }
+    __threadfence_block();
+    return keep ? s_dist[rank] : FLT_MAX;
 }
 
 // kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  kRegs > 0:
@@ -544,7 +578,7 @@ __device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t 
 // rows are scored per lane (integer, exact in any order), f32 / f16 rows
 // by wave_float_dists.
 template <int kVisited, int kC, int kRegs, int kElem>
-__global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel(ExactArgs a)
+__global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAVES : 5)) void exact_route_kernel(ExactArgs a)
 {
     constexpr int kRowUnroll = kRegs > 0 ? kExactRegsRowUnroll : GOFANN_EXACT_ROW_UNROLL;
     extern __shared__ __align__(16) unsigned char lds[];
@@ -628,10 +662,10 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
                                              a.base + static_cast<size_t>(s0) * a.dim, qw, a.dim, qn))
                                        : 0.0f);
             } else {
-                // both halves score the seed row; the first lane's sum is it
-                d0 = bcast0f(w32_tree<kElem>(l2_w32_partial<kElem>(
+                // every quad scores the seed row; lane 0's sum is it
+                d0 = bcast0f(l2_w32_quad<kElem>(
                     a.base + static_cast<size_t>(s0) * a.dim * elem_bytes(kElem), qf, a.dim,
-                    static_cast<uint32_t>(lane) & 31u)));
+                    static_cast<uint32_t>(lane) & 3u));
             }
             const Entry kp = {d0, seed, d0, s0};
             if constexpr (kRegs > 0) {
@@ -705,7 +739,7 @@ __global__ __launch_bounds__(64, GOFANN_EXACT_MIN_WAVES) void exact_route_kernel
             // dead before the filter below.
             asm volatile("" : "+v"(d32)::"memory");
         } else {
-            fdist = wave_float_dists<kElem>(a.base, a.dim, qf, keep, samp, lane);
+            fdist = wave_float_dists<kElem>(a.base, a.dim, qf, keep, samp, lane, s_samp, s_dist);
             asm volatile("" : "+v"(fdist)::"memory");
         }
 

@@ -13,8 +13,10 @@
 // LDS pair array (running top-k + chunk):
 //  * the chunk's valid, predicate-passing samples are compacted into the
 //    chunk slots (order is free: the (distance, id) sort fixes it);
-//  * serial order: a thread per row (16-byte loads, the chain in d order);
-//    warp order: a 32-lane half per row (exact_dist.hpp);
+//  * serial order: a lane per row, the chain in d order, rows read through
+//    per-wave LDS tiles so that loads cover whole lines (a thread reading
+//    its own row where the row length does not allow 16-byte words); warp
+//    order: a quad of lanes per row (exact_dist.hpp);
 //  * a bitonic sort on (distance, id) merges the chunk with the running
 //    top-k, and one lane keeps the first topk distinct ids (a duplicate has
 //    the same distance, so it sits next to its twin).
@@ -50,14 +52,20 @@ struct ExactScanArgs {
     uint32_t* out_ids;
     float* out_dists;
     uint32_t* pass_counts;
+    uint32_t tile_offset;  // bytes from the LDS base to the tiles
 };
 
 constexpr int kExactScanMaxTopk = 64;
 
-template <int kElem, int kOrder>
+// kTile: 0 -- the serial order one thread per row reading its own row (any
+// row length); 16 or 32 -- the serial order through LDS tiles of that many
+// words per row (l2_serial_tiled; row bytes % 16 == 0).  The warp order
+// takes a quad of lanes per row (l2_w32_quad) and ignores kTile.
+template <int kElem, int kOrder, int kTile>
 __global__ __launch_bounds__(kScanThreads) void exact_scan_kernel(ExactScanArgs a)
 {
-    extern __shared__ __align__(16) unsigned char lds[];  // query as f32 [dim]
+    // dynamic LDS: the query as f32 [dim], then (tiled) one tile per wave
+    extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float s_d[kScanSlots];
     __shared__ uint32_t s_id[kScanSlots];
     __shared__ uint32_t s_n;
@@ -104,7 +112,24 @@ __global__ __launch_bounds__(kScanThreads) void exact_scan_kernel(ExactScanArgs 
         }
         __syncthreads();
         const int n = static_cast<int>(s_n);
-        if constexpr (kOrder == GOFANN_EXACT_ORDER_SERIAL) {
+        if constexpr (kOrder == GOFANN_EXACT_ORDER_SERIAL && kTile > 0) {
+            const int wave = tid / kWave;
+            const int lane = tid % kWave;
+            uint32_t* tile = reinterpret_cast<uint32_t*>(lds + a.tile_offset) +
+                             wave * kWave * (kTile + 1);
+            for (int i0 = wave * kWave; i0 < n; i0 += kScanThreads) {
+                const int rows = n - i0 < kWave ? n - i0 : kWave;
+                const float d = l2_serial_tiled<kElem, kTile>(a.base, row_bytes, q,
+                                                              &s_id[a.k_pow2 + i0], rows, tile,
+                                                              lane);
+                if (lane < rows) {
+                    const int slot = a.k_pow2 + i0 + lane;
+                    const bool nan = d != d;
+                    s_d[slot] = nan ? inf : d;
+                    if (nan) s_id[slot] = UINT32_MAX;
+                }
+            }
+        } else if constexpr (kOrder == GOFANN_EXACT_ORDER_SERIAL) {
             for (int i = tid; i < n; i += kScanThreads) {
                 const int slot = a.k_pow2 + i;
                 const uint32_t s = s_id[slot];
@@ -114,16 +139,18 @@ __global__ __launch_bounds__(kScanThreads) void exact_scan_kernel(ExactScanArgs 
                 if (nan) s_id[slot] = UINT32_MAX;
             }
         } else {
-            const uint32_t j = static_cast<uint32_t>(tid) & 31u;
-            for (int i = tid >> 5; i < n; i += kScanThreads / 32) {
-                const int slot = a.k_pow2 + i;
-                const uint32_t s = s_id[slot];
-                const float d = w32_tree<kElem>(
-                    l2_w32_partial<kElem>(a.base + static_cast<size_t>(s) * row_bytes, q, a.dim, j));
-                if (j == 0) {
-                    const bool nan = d != d;
-                    s_d[slot] = nan ? inf : d;
-                    if (nan) s_id[slot] = UINT32_MAX;
+            const uint32_t g = static_cast<uint32_t>(tid) & 3u;
+            for (int i = tid >> 2; i - (tid >> 2) < n; i += kScanThreads / 4) {
+                if (i < n) {
+                    const int slot = a.k_pow2 + i;
+                    const uint32_t s = s_id[slot];
+                    const float d =
+                        l2_w32_quad<kElem>(a.base + static_cast<size_t>(s) * row_bytes, q, a.dim, g);
+                    if (g == 0) {
+                        const bool nan = d != d;
+                        s_d[slot] = nan ? inf : d;
+                        if (nan) s_id[slot] = UINT32_MAX;
+                    }
                 }
             }
         }
@@ -171,25 +198,38 @@ int pow2_ceil(int x)
     return p;
 }
 
-template <int kElem, int kOrder>
+template <int kElem, int kOrder, int kTile>
 int launch_exact_scan(Context* ctx, const ExactScanArgs& a, uint32_t lds)
 {
-    const void* k = reinterpret_cast<const void*>(exact_scan_kernel<kElem, kOrder>);
+    const void* k = reinterpret_cast<const void*>(exact_scan_kernel<kElem, kOrder, kTile>);
     if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
         hipSuccess)
         return ctx->fail_hip("hipFuncSetAttribute exact posting scan");
-    hipLaunchKernelGGL((exact_scan_kernel<kElem, kOrder>), dim3(a.routes), dim3(kScanThreads), lds,
-                       ctx->stream, a);
+    hipLaunchKernelGGL((exact_scan_kernel<kElem, kOrder, kTile>), dim3(a.routes),
+                       dim3(kScanThreads), lds, ctx->stream, a);
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("exact posting scan launch");
     return GOFANN_OK;
 }
 
+// Serial order: LDS tiles of 32 words per row where the row allows them and
+// the workgroup's LDS holds them, else of 16, else a thread per row.
 template <int kElem>
-int launch_exact_scan_order(Context* ctx, const ExactScanArgs& a, uint32_t lds, int order)
+int launch_exact_scan_order(Context* ctx, ExactScanArgs& a, uint32_t q_lds, uint32_t fixed,
+                            int order)
 {
-    return order == GOFANN_EXACT_ORDER_WARP
-               ? launch_exact_scan<kElem, GOFANN_EXACT_ORDER_WARP>(ctx, a, lds)
-               : launch_exact_scan<kElem, GOFANN_EXACT_ORDER_SERIAL>(ctx, a, lds);
+    if (order == GOFANN_EXACT_ORDER_WARP)
+        return launch_exact_scan<kElem, GOFANN_EXACT_ORDER_WARP, 0>(ctx, a, q_lds);
+    const size_t row_bytes = static_cast<size_t>(a.dim) * elem_bytes(kElem);
+    const uint32_t limit = static_cast<uint32_t>(ctx->lds_per_block);
+    a.tile_offset = q_lds;
+    const uint32_t waves = kScanThreads / kWave;
+    const uint32_t t32 = q_lds + waves * kWave * 33u * 4u;
+    const uint32_t t16 = q_lds + waves * kWave * 17u * 4u;
+    if (row_bytes % 16 == 0 && t32 + fixed <= limit)
+        return launch_exact_scan<kElem, GOFANN_EXACT_ORDER_SERIAL, 32>(ctx, a, t32);
+    if (row_bytes % 16 == 0 && t16 + fixed <= limit)
+        return launch_exact_scan<kElem, GOFANN_EXACT_ORDER_SERIAL, 16>(ctx, a, t16);
+    return launch_exact_scan<kElem, GOFANN_EXACT_ORDER_SERIAL, 0>(ctx, a, q_lds);
 }
 
 }  // namespace
@@ -236,10 +276,13 @@ int exact_posting_scan(Context* ctx, const void* base, int base_elem, uint32_t d
     a.out_ids = out_ids;
     a.out_dists = out_dists;
     a.pass_counts = pass_counts;
+    a.tile_offset = 0;
     switch (base_elem) {
-    case GOFANN_ELEM_F32: return launch_exact_scan_order<GOFANN_ELEM_F32>(ctx, a, lds, order);
-    case GOFANN_ELEM_F16: return launch_exact_scan_order<GOFANN_ELEM_F16>(ctx, a, lds, order);
-    default: return launch_exact_scan_order<GOFANN_ELEM_U8>(ctx, a, lds, order);
+    case GOFANN_ELEM_F32:
+        return launch_exact_scan_order<GOFANN_ELEM_F32>(ctx, a, lds, fixed, order);
+    case GOFANN_ELEM_F16:
+        return launch_exact_scan_order<GOFANN_ELEM_F16>(ctx, a, lds, fixed, order);
+    default: return launch_exact_scan_order<GOFANN_ELEM_U8>(ctx, a, lds, fixed, order);
     }
 }
 

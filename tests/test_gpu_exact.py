@@ -177,13 +177,14 @@ def _float_world(dim, seed, n=4000, nq=32):
     return wl, li, gp.plan_queries(li, wl.query_labels).graph
 
 
-@pytest.mark.parametrize("dim", [37, 100, 128, 512])
+@pytest.mark.parametrize("dim", [37, 100, 128, 512, 4096])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_exact_search_float_rows(gpu_ctx, dim, dtype):
     """f32 and f16 rows (and queries of the same type): distances in the
     reference's warp order, bit-identical to the oracle, with the frontier
     in registers and in LDS and every visited-set placement; odd dim takes
-    the per-element f16 path, 100 leaves partials of unequal length."""
+    the per-element f16 path, 100 leaves partials of unequal length, and
+    4096 (16 KB / 8 KB rows, C3's shape) takes the half-wave-per-row path."""
     wl, li, rs = _float_world(dim, 70 + dim)
     t = np.float16 if dtype == "f16" else np.float32
     rows = (wl.base.numpy().astype(t), wl.queries.numpy().astype(t))
@@ -205,7 +206,7 @@ def test_exact_search_float_rows(gpu_ctx, dim, dtype):
 @pytest.fixture(scope="module")
 def scan_worlds(gpu_ctx):
     out = {}
-    for dim in (37, 128, 512):
+    for dim in (37, 128, 512, 4096):
         wl = synth.small_labelled(n=6000, nq=24, dim=dim, k=10, sigma=0.7, labels=5,
                                   seed=90 + dim, tags=True)
         li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
@@ -230,13 +231,15 @@ def _scan_lists(rng, n, routes):
     return ids, offs, sizes
 
 
-@pytest.mark.parametrize("dim", [37, 128, 512])
+@pytest.mark.parametrize("dim", [37, 128, 512, 4096])
 @pytest.mark.parametrize("dtype", ["u8", "f32", "f16"])
 @pytest.mark.parametrize("order", [_lib.EXACT_ORDER_SERIAL, _lib.EXACT_ORDER_WARP])
 def test_exact_posting_scan_matches_oracle(gpu_ctx, scan_worlds, dim, dtype, order):
     """gofann_exact_posting_scan: ids, distance bits and pass counts equal
     the oracle's in both summation orders, with and without the route
-    predicate, for topk 1, 10 and 64."""
+    predicate, for topk 1, 10 and 64.  Row lengths cover the serial order's
+    LDS tiles (rows of 16-byte multiples, 4096 at the C3 shape) and its
+    thread-per-row path (dim 37), and the warp order's unaligned blocks."""
     wl, li = scan_worlds[dim]
     x, qx = wl.base.numpy(), wl.queries.numpy()
     if dtype == "u8":
