@@ -66,6 +66,9 @@ def parse():
                     help="gather neighbour sample ids through row_to_sample")
     ap.add_argument("--no-records", action="store_true",
                     help="separate code rows and CSR labels instead of 64-byte sample records")
+    ap.add_argument("--no-rabitq-records", action="store_true",
+                    help="C3/C4/C5: the RaBitQ traversal reads codes, factors, anchor ids and "
+                         "its predicate inputs from separate arrays, not per-sample records")
     ap.add_argument("--no-exact-float", action="store_true",
                     help="C3/C4: skip the all-GPU exact-distance row")
     ap.add_argument("--no-cpu-rerank-route", action="store_true",
@@ -1017,6 +1020,22 @@ def ground_truth_c3(wl, torch, nq):
                               q_chunk=1000)
 
 
+def rabitq_records(pipe, li, wl, enabled):
+    """Per-sample records for a pipeline's graph traversal
+    (gofann_amd.search.RabitqRecords: code row, f_add, f_rescale, anchor id,
+    attribute values, label slab), set on its RaBitQ view; None when
+    disabled (the traversal then reads the separate arrays)."""
+    if not enabled:
+        return None
+    t0 = time.time()
+    rec = pipe.gs.RabitqRecords.build(pipe.dev["codes"], pipe.dev["fac"], pipe.dev["aid"],
+                                      wl.base_ranges, li.csr_offsets, li.csr_labels)
+    pipe.rv.records, pipe.rv.record_stride = rec.view_fields()
+    log(f"RaBitQ records: {rec.stride} B per sample, {rec.data.numel() / 2**30:.1f} GiB, "
+        f"built in {time.time() - t0:.1f}s")
+    return rec
+
+
 class RabitqRangePipeline:
     """One step of the C3 route set on the GPU: query preparation (rotation
     SGEMM, int8, factors, centroid distances), RaBitQ graph traversal with
@@ -1025,7 +1044,7 @@ class RabitqRangePipeline:
     rerank of the 200, and the per-query merge."""
 
     def __init__(self, ctx, wl, li, rq, rpi, torch, scan_rows, width=200, segment_rows=4096,
-                 resident_copies=True, neighbor_samples=True):
+                 resident_copies=True, neighbor_samples=True, records=True):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
         from gofann_amd import range_posting as rp
@@ -1081,6 +1100,7 @@ class RabitqRangePipeline:
         self.rv = _lib.RabitqView(_lib.ptr(self.dev["codes"]), _lib.ptr(self.dev["fac"]),
                                   _lib.ptr(self.dev["aid"]), _lib.ptr(self.dev["anchors"]),
                                   wl.dim, P, rq["anchors"].shape[0], wl.n)
+        self.recs = rabitq_records(self, li, wl, records)
         # posting-order copies of the rows the range scans stream
         self.prows = (rp.PostingRows(ctx, self.rv, self.postings, self.resident)
                       if resident_copies else None)
@@ -1165,7 +1185,8 @@ class RabitqRangePipeline:
         prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
         ctx.check(ctx.lib.gofann_rabitq_search(
             ctx.handle, self.rv, self.rq, self.dg.view(),
-            self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(lo, hi, start=start),
+            self.dr.predicate_view(self.dg, 0.15, True, records=self.recs),
+            self.dr.routes_view(lo, hi, start=start),
             prm, L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
 
     def _scan(self):
@@ -1312,7 +1333,8 @@ def run_c3(args, torch, ctx) -> dict:
     log(f"C3 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     pipe = RabitqRangePipeline(ctx, wl, li, rq, rpi, torch, args.c3_scan_rows,
                                resident_copies=not args.c3_gather,
-                               neighbor_samples=not args.no_neighbor_samples)
+                               neighbor_samples=not args.no_neighbor_samples,
+                               records=not args.no_rabitq_records)
     pipe.P, pipe.li = rq["P"], li
     log(f"C3 routes: {pipe.ng} graph (wide ranges), {pipe.np_} range-posting scans "
         f"({pipe.scan_rows_total} rows)")
@@ -1452,7 +1474,7 @@ class RabitqLabelPipeline:
 
     def __init__(self, ctx, wl, li, rq, torch, width=100, posting_layout="columns",
                  segment_rows=32768, neighbor_samples=True, posting_share=True,
-                 share_routes=16):
+                 share_routes=16, records=True):
         from gofann_amd import _lib
         from gofann_amd import plan as gp
         from gofann_amd import range_posting as rp
@@ -1515,6 +1537,7 @@ class RabitqLabelPipeline:
         self.rv = _lib.RabitqView(_lib.ptr(self.dev["codes"]), _lib.ptr(self.dev["fac"]),
                                   _lib.ptr(self.dev["aid"]), _lib.ptr(self.dev["anchors"]),
                                   wl.dim, P, rq["anchors"].shape[0], wl.n)
+        self.recs = rabitq_records(self, li, wl, records)
         A = rq["anchors"].shape[0]
         self.prep = dict(rotated=torch.empty(nq, P, device="cuda"),
                          q8=torch.empty(nq, P, dtype=torch.int8, device="cuda"),
@@ -1636,7 +1659,8 @@ class RabitqLabelPipeline:
         prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
         ctx.check(ctx.lib.gofann_rabitq_search(
             ctx.handle, self.rv, self.rq, self.dg.view(),
-            self.dr.predicate_view(self.dg, 0.15, True), self.dr.routes_view(lo, hi, start=start),
+            self.dr.predicate_view(self.dg, 0.15, True, records=self.recs),
+            self.dr.routes_view(lo, hi, start=start),
             prm, L.ptr(self.sl_i), L.ptr(self.sl_d), L.ptr(self.stats)))
 
     def _scan(self):
@@ -2026,7 +2050,8 @@ def run_c4(args, torch, ctx, world=None) -> dict:
                                segment_rows=args.posting_segment_rows,
                                neighbor_samples=not args.no_neighbor_samples,
                                posting_share=not args.no_posting_share,
-                               share_routes=args.posting_share_routes)
+                               share_routes=args.posting_share_routes,
+                               records=not args.no_rabitq_records)
     pipe.P, pipe.li = rq["P"], li
     log(f"C4 routes: {pipe.ng} graph ({pipe.n_eq} equality, {pipe.interior} interior "
         f"intervals), {pipe.np_} label-posting scans ({pipe.post_rows_total} rows), planned "
@@ -2167,7 +2192,8 @@ def run_c5(args, torch, ctx, world=None) -> dict:
                                segment_rows=args.posting_segment_rows,
                                neighbor_samples=not args.no_neighbor_samples,
                                posting_share=not args.no_posting_share,
-                               share_routes=args.posting_share_routes)
+                               share_routes=args.posting_share_routes,
+                               records=not args.no_rabitq_records)
     pipe.P, pipe.li = rq["P"], li
     types = wl.meta["query_types"]
     log(f"C5 routes: {pipe.ng} graph, {pipe.np_} label-posting scans ({pipe.post_rows_total} "

@@ -647,6 +647,12 @@ __device__ __forceinline__ bool early_stop_reached(int mode, int bad, int fixed_
 // Predicates: gpu_predicate_index.cuh:52-166 (CSR storage, threshold 0) and
 // range_filter.cuh:23-124.
 // ---------------------------------------------------------------------------
+// Attribute columns of a predicate view's base_ranges.
+__device__ __forceinline__ uint32_t range_columns(const gofann_predicate_view& v)
+{
+    return v.range_columns ? v.range_columns : v.range_stride;
+}
+
 struct PredCounters {
     uint32_t rows;
     uint32_t labels;
@@ -695,7 +701,7 @@ __device__ __forceinline__ bool pred_matches(const gofann_predicate_view& v, uin
                 pass = pred_contains(v, v.route_handles[j], sample, c);
             for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
                 const gofann_range_atom a = v.ranges[j];
-                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                pass = v.base_ranges != nullptr && a.dimension < range_columns(v) &&
                        range_matches(a.mode, a.lower, a.upper,
                                      v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
                                                    a.dimension]);
@@ -803,7 +809,7 @@ __device__ __forceinline__ bool wave_pred_matches(const gofann_predicate_view& v
                 pass = wave_row_contains(v, row, v.route_handles[j], lane, c);
             for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
                 const gofann_range_atom a = v.ranges[j];
-                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                pass = v.base_ranges != nullptr && a.dimension < range_columns(v) &&
                        range_matches(a.mode, a.lower, a.upper,
                                      v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
                                                    a.dimension]);
@@ -930,7 +936,7 @@ __device__ __forceinline__ bool lane_pred_eval(const gofann_predicate_view& v, u
                 pass = lane_row_contains(v, r, v.route_handles[j], c);
             for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
                 const gofann_range_atom a = v.ranges[j];
-                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                pass = v.base_ranges != nullptr && a.dimension < range_columns(v) &&
                        range_matches(a.mode, a.lower, a.upper,
                                      v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
                                                    a.dimension]);

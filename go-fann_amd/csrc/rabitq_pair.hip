@@ -183,7 +183,7 @@ __device__ __forceinline__ bool pred_matches_h(const gofann_predicate_view& v, u
                 pass = row_contains_h(v, row, v.route_handles[j], hl, hb, c);
             for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
                 const gofann_range_atom at = v.ranges[j];
-                pass = v.base_ranges != nullptr && at.dimension < v.range_stride &&
+                pass = v.base_ranges != nullptr && at.dimension < range_columns(v) &&
                        range_matches(at.mode, at.lower, at.upper,
                                      v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
                                                    at.dimension]);

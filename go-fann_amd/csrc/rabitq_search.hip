@@ -53,6 +53,8 @@ RabitqScorer make_rabitq_scorer(const gofann_rabitq_view* rq, const gofann_rabit
     sc.scale = 0.0f;
     sc.k1 = 0.0f;
     sc.g_row = nullptr;
+    sc.records = rq->records;
+    sc.record_stride = rq->record_stride;
     return sc;
 }
 
@@ -63,6 +65,12 @@ int check_rabitq(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq
         return ctx->fail(GOFANN_ERR_INVALID, "RaBitQ view incomplete");
     if (rq->padded_dim == 0 || rq->padded_dim % 128 != 0)
         return ctx->fail(GOFANN_ERR_INVALID, "padded_dim must be a positive multiple of 128");
+    if (rq->records != nullptr &&
+        (rq->record_stride % 16 != 0 || rq->record_stride < rq->padded_dim / 8 + 12 ||
+         (reinterpret_cast<uintptr_t>(rq->records) & 15u) != 0))
+        return ctx->fail(GOFANN_ERR_INVALID,
+                         "RaBitQ records: stride a multiple of 16 of at least padded_dim/8 + 12, "
+                         "16-byte aligned");
     return GOFANN_OK;
 }
 

@@ -87,7 +87,7 @@ struct RangeScanArgs {
     const uint4* pcodes;
     const uint4* paux;
     // Posting-order predicate columns (label modes; may be null): the
-    // row's label slab and its base range row [rows][pred.range_stride].
+    // row's label slab and its base range row [rows][range_columns(pred)].
     const uint4* pslab;
     const float* pranges;
 };
@@ -100,8 +100,8 @@ constexpr int kLabelSegments = 2;
 // in posting order: the same clause walk, each label test the serial scan
 // of pred_contains over the slab's labels (the first label >= handle
 // decides).  The slab must not be the overflow form.
-// `prange` is the row's range row; with range_stride 1 its value is passed
-// as `r0`, loaded with the slab.
+// `prange` is the row's range row; with one attribute column its value is
+// passed as `r0`, loaded with the slab.
 __device__ __forceinline__ bool slab_pred_matches(const gofann_predicate_view& v, uint32_t route,
                                                   uint32_t sample, const uint4& slab,
                                                   const float* prange, float r0)
@@ -124,12 +124,12 @@ __device__ __forceinline__ bool slab_pred_matches(const gofann_predicate_view& v
                 pass = contains(v.route_handles[j]);
             for (uint32_t j = cl.range_begin; pass && j < cl.range_end; ++j) {
                 const gofann_range_atom a = v.ranges[j];
-                pass = v.base_ranges != nullptr && a.dimension < v.range_stride &&
+                pass = v.base_ranges != nullptr && a.dimension < range_columns(v) &&
                        range_matches(a.mode, a.lower, a.upper,
                                      !prange ? v.base_ranges[static_cast<uint64_t>(sample) *
                                                                  v.range_stride +
                                                              a.dimension]
-                                     : v.range_stride == 1 ? r0
+                                     : range_columns(v) == 1 ? r0
                                                            : prange[a.dimension]);
             }
             if (pass) return true;
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
                 sv[t] = a.posting[begin + j];
                 if (cols) {
                     slv[t] = a.pslab[begin + j];
-                    if (a.pranges && a.pred.range_stride == 1) r0v[t] = a.pranges[begin + j];
+                    if (a.pranges && range_columns(a.pred) == 1) r0v[t] = a.pranges[begin + j];
                 }
             }
         }
@@ -531,8 +531,8 @@ __global__ __launch_bounds__(kScanThreads) void range_scan_group_kernel(RangeSca
             if (ok) {
                 if (cols && slab_count(slv[t]) != kSlabOverflow) {
                     const float* prange =
-                        a.pranges && a.pred.range_stride > 0
-                            ? a.pranges + (begin + j) * a.pred.range_stride
+                        a.pranges && range_columns(a.pred) > 0
+                            ? a.pranges + (begin + j) * range_columns(a.pred)
                             : nullptr;
                     ok = slab_pred_matches(a.pred, route, s, slv[t], prange, r0v[t]);
                 } else if (enabled) {
@@ -814,11 +814,11 @@ __device__ __forceinline__ bool short_clause_matches(const gofann_predicate_view
     for (int i = 0; i < 2; ++i) {
         if (i >= c.nr) break;
         const gofann_range_atom at = c.r[i];
-        pass = pass && v.base_ranges != nullptr && at.dimension < v.range_stride &&
+        pass = pass && v.base_ranges != nullptr && at.dimension < range_columns(v) &&
                range_matches(at.mode, at.lower, at.upper,
                              !prange ? v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
                                                      at.dimension]
-                             : v.range_stride == 1 ? r0
+                             : range_columns(v) == 1 ? r0
                                                    : prange[at.dimension]);
     }
     return pass;
@@ -888,7 +888,7 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             if (lane == 0) s_pass[q] = 0;
         }
         uint32_t* queue = queue_all + wave * kWave;
-        const bool r0_tile = a.pranges && a.pred.range_stride == 1;
+        const bool r0_tile = a.pranges && range_columns(a.pred) == 1;
 
         for (uint64_t t0 = 0; t0 < count; t0 += kShareTile) {
             __syncthreads();  // the previous tile's reads end here
@@ -994,8 +994,8 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                             const uint4 slab = t_slab[r];
                             if (slab_count(slab) != kSlabOverflow) {
                                 const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
-                                const float* prange = a.pranges && a.pred.range_stride > 0
-                                                          ? a.pranges + j * a.pred.range_stride
+                                const float* prange = a.pranges && range_columns(a.pred) > 0
+                                                          ? a.pranges + j * range_columns(a.pred)
                                                           : nullptr;
                                 const float rv = r0_tile ? t_r0[r] : 0.0f;
                                 ok = sclause.simple
@@ -1177,8 +1177,9 @@ __global__ __launch_bounds__(256) void posting_pred_rows_kernel(gofann_predicate
         }
         out_slab[r] = make_uint4(w[0], w[1], w[2], w[3]);
         if (out_ranges) {
-            for (uint32_t d = 0; d < v.range_stride; ++d)
-                out_ranges[r * v.range_stride + d] =
+            const uint32_t cols = range_columns(v);
+            for (uint32_t d = 0; d < cols; ++d)
+                out_ranges[r * cols + d] =
                     in && v.base_ranges ? v.base_ranges[static_cast<uint64_t>(s) * v.range_stride + d]
                                         : 0.0f;
         }

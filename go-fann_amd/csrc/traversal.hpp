@@ -317,6 +317,14 @@ struct RabitqScorer {
     float scale;
     float k1;
     const float* g_row;
+    const uint8_t* records;  // per-sample records (code, f_add, f_rescale, anchor) or null
+    uint32_t record_stride;
+
+    __device__ __forceinline__ const uint8_t* code_row(uint32_t sample) const
+    {
+        return records ? records + static_cast<size_t>(sample) * record_stride
+                       : codes + static_cast<size_t>(sample) * (padded_dim / 8);
+    }
 
     __device__ void setup(uint32_t q, int lane, unsigned char* lds)
     {
@@ -382,7 +390,7 @@ struct RabitqScorer {
             for (int it = 0; it < 4; ++it) {
                 const int r = b0 + it * 4 + grp;
                 const uint32_t sj = r < n ? s_cand[r] : 0u;
-                const uint4* row = reinterpret_cast<const uint4*>(codes + static_cast<size_t>(sj) * (vecs * 16));
+                const uint4* row = reinterpret_cast<const uint4*>(code_row(sj));
 #pragma unroll
                 for (int w = 0; w < VPL; ++w)
                     cb[it][w] = r < n ? row[lg + 16 * w] : make_uint4(0, 0, 0, 0);
@@ -408,7 +416,13 @@ struct RabitqScorer {
         const uint32_t vecs = padded_dim / 128;
         uint32_t anchor = 0;
         float f_add = 0.0f, f_rescale = 0.0f;
-        if (active) {
+        if (active && records) {
+            const uint8_t* rec = records + static_cast<size_t>(sample) * record_stride + padded_dim / 8;
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(rec);
+            f_add = __uint_as_float(w[0]);
+            f_rescale = __uint_as_float(w[1]);
+            anchor = w[2];
+        } else if (active) {
             anchor = anchor_ids[sample];
             f_add = factors[static_cast<size_t>(sample) * 3];
             f_rescale = factors[static_cast<size_t>(sample) * 3 + 1];
@@ -420,7 +434,7 @@ struct RabitqScorer {
             ip = ip_coop<1>(sample, active, lane);
         } else {
             if (!active) return 0.0f;
-            const uint4* row = reinterpret_cast<const uint4*>(codes + static_cast<size_t>(sample) * (padded_dim / 8));
+            const uint4* row = reinterpret_cast<const uint4*>(code_row(sample));
             const uint4* planes4 = reinterpret_cast<const uint4*>(planes);
             uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             // Code loads go out kCodeBatch at a time before any is consumed, so
@@ -448,7 +462,7 @@ struct RabitqScorer {
     __device__ int32_t ip_int(uint32_t sample) const
     {
         const uint32_t words = padded_dim / 32;
-        const uint32_t* row = reinterpret_cast<const uint32_t*>(codes + static_cast<size_t>(sample) * (padded_dim / 8));
+        const uint32_t* row = reinterpret_cast<const uint32_t*>(code_row(sample));
         int32_t ip = 0;
         for (uint32_t w = 0; w < words; ++w) {
             const uint32_t cw = row[w];

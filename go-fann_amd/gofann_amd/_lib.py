@@ -47,7 +47,8 @@ class PredicateView(C.Structure):
                 ("ranges", P), ("route_enabled", P), ("route_compiled", P),
                 ("base_ranges", P), ("csr_offsets", P), ("csr_labels", P),
                 ("rows", U32), ("range_stride", U32), ("alpha", C.c_float),
-                ("pending_base_stop", C.c_int), ("label_slab", P), ("slab_stride", U32)]
+                ("pending_base_stop", C.c_int), ("label_slab", P), ("slab_stride", U32),
+                ("range_columns", U32)]
 
 
 class Routes(C.Structure):
@@ -83,7 +84,7 @@ class PqView(C.Structure):
 class RabitqView(C.Structure):
     _fields_ = [("codes", P), ("factors", P), ("anchor_ids", P), ("anchors", P),
                 ("dim", U32), ("padded_dim", U32), ("num_anchors", U32),
-                ("samples", U32)]
+                ("samples", U32), ("records", P), ("record_stride", U32)]
 
 
 class RabitqQueries(C.Structure):

@@ -356,13 +356,14 @@ class PostingPredicateColumns:
     """Posting-order predicate columns (gofann_posting_predicate_rows): each
     posting row's 16-byte label slab [rows][4] u32 and base range row
     [rows][range_stride] f32, so a label-posting scan streams its filter's
-    inputs instead of gathering them by sample id."""
+    inputs instead of gathering them by sample id.  The range row holds the
+    view's attribute columns (range_columns, else range_stride)."""
 
     def __init__(self, ctx: _lib.Context, pred: _lib.PredicateView, postings: torch.Tensor,
                  rows: int):
         self.rows = int(rows)
         dev = postings.device
-        stride = int(pred.range_stride)
+        stride = int(pred.range_columns or pred.range_stride)
         self.slab = torch.empty(max(self.rows, 1), 4, dtype=torch.int32, device=dev)
         self.ranges = (torch.empty(max(self.rows * stride, 1), dtype=torch.float32, device=dev)
                        if stride else None)

@@ -126,26 +126,107 @@ class SampleRecords:
         rec[:, :M] = codes.to(DEV)
         off = torch.from_numpy(csr_offsets.astype(np.int64)).to(DEV)
         lab = torch.from_numpy(csr_labels.astype(np.int64)).to(DEV)
-        cnt = off[1:] - off[:-1]
-        slab = torch.zeros(n, 8, dtype=torch.int64, device=DEV)
-        ok = cnt <= SLAB_CAPACITY
-        for k in range(SLAB_CAPACITY):
-            has = cnt > k
-            idx = torch.where(has, off[:-1] + k, torch.zeros_like(cnt))
-            v = torch.where(has, lab[idx] if lab.numel() else torch.zeros_like(cnt),
-                            torch.zeros_like(cnt))
-            ok &= v < SLAB_OVERFLOW
-            slab[:, k + 1] = v
-        if overflow_every > 0:  # test hook: force the CSR path on some rows
-            ok &= (torch.arange(n, device=DEV) % overflow_every) != 0
-        slab[:, 0] = torch.where(ok, cnt, torch.full_like(cnt, SLAB_OVERFLOW))
-        slab = torch.where(ok[:, None] | (torch.arange(8, device=DEV) == 0)[None, :], slab,
-                           torch.zeros_like(slab))
-        rec[:, slab_off:] = _u16_bytes(slab)
+        rec[:, slab_off:] = label_slabs(off, lab, 0, n, overflow_every)
         return cls(rec, M, stride, slab_off)
 
     def slab(self):
         return self.data.data_ptr() + self.slab_offset, self.stride
+
+
+def label_slabs(off: torch.Tensor, lab: torch.Tensor, s: int, e: int,
+                overflow_every: int = 0) -> torch.Tensor:
+    """The 16-byte label slabs (u8 [e - s][16]) of rows s..e of a
+    sample-major CSR (device int64 offsets [n + 1] and labels): u16 count,
+    then up to 7 u16 labels ascending; count 0xFFFF (labels zeroed) where the
+    row has more than 7 labels or a label >= 0xFFFF."""
+    o = off[s:e + 1]
+    cnt = o[1:] - o[:-1]
+    slab = torch.zeros(e - s, 8, dtype=torch.int64, device=off.device)
+    ok = cnt <= SLAB_CAPACITY
+    for k in range(SLAB_CAPACITY):
+        has = cnt > k
+        idx = torch.where(has, o[:-1] + k, torch.zeros_like(cnt))
+        v = torch.where(has, lab[idx] if lab.numel() else torch.zeros_like(cnt),
+                        torch.zeros_like(cnt))
+        ok &= v < SLAB_OVERFLOW
+        slab[:, k + 1] = v
+    if overflow_every > 0:  # test hook: force the CSR path on some rows
+        ok &= (torch.arange(s, e, device=off.device) % overflow_every) != 0
+    slab[:, 0] = torch.where(ok, cnt, torch.full_like(cnt, SLAB_OVERFLOW))
+    slab = torch.where(ok[:, None] | (torch.arange(8, device=off.device) == 0)[None, :], slab,
+                       torch.zeros_like(slab))
+    return _u16_bytes(slab)
+
+
+@dataclass
+class RabitqRecords:
+    """Per-sample RaBitQ records for the graph traversal
+    (gofann_rabitq_view.records): the code row, f_add and f_rescale, the
+    anchor id, then (optional) the sample's attribute values and its
+    16-byte label slab, padded to whole 128-byte lines -- one line per
+    scored candidate for 64-byte codes, where the separate arrays cost one
+    line each.  The predicate view reads the slab and the attribute values
+    in place (DeviceRoutes.predicate_view(records=...))."""
+    data: torch.Tensor   # u8 [samples][stride]
+    stride: int
+    range_offset: int    # -1: no attribute values
+    range_stride: int
+    slab_offset: int     # -1: no label slab
+
+    @classmethod
+    def build(cls, codes: torch.Tensor, factors: torch.Tensor, anchor_ids: torch.Tensor,
+              base_ranges=None, csr_offsets=None, csr_labels=None,
+              chunk: int = 1 << 22, overflow_every: int = 0) -> "RabitqRecords":
+        n, cb = int(codes.shape[0]), int(codes.shape[1])
+        if cb % 16:
+            raise ValueError("code rows must be a multiple of 16 bytes")
+        pos = cb + 12
+        r_off, rs = -1, 0
+        if base_ranges is not None:
+            rs = int(base_ranges.shape[1])
+            r_off, pos = pos, pos + 4 * rs
+        s_off = -1
+        if csr_offsets is not None:
+            s_off = (pos + 15) // 16 * 16
+            pos = s_off + SLAB_BYTES
+        stride = (pos + 127) // 128 * 128
+        rec = torch.zeros(n, stride, dtype=torch.uint8, device=DEV)
+        br = None
+        if base_ranges is not None:
+            br = base_ranges if isinstance(base_ranges, torch.Tensor) else \
+                torch.from_numpy(np.ascontiguousarray(base_ranges, dtype=np.float32))
+        off = lab = None
+        if csr_offsets is not None:
+            off = torch.from_numpy(np.asarray(csr_offsets).astype(np.int64)).to(DEV)
+            lab = torch.from_numpy(np.asarray(csr_labels).astype(np.int64)).to(DEV)
+        for s in range(0, n, chunk):
+            e = min(n, s + chunk)
+            rec[s:e, :cb] = codes[s:e].to(DEV)
+            f = factors[s:e, :2].to(DEV, torch.float32).reshape(-1).contiguous()
+            rec[s:e, cb:cb + 8] = f.view(torch.uint8).view(e - s, 8)
+            a = anchor_ids[s:e].to(DEV, torch.int32).contiguous()
+            rec[s:e, cb + 8:cb + 12] = a.view(torch.uint8).view(e - s, 4)
+            if br is not None:
+                v = br[s:e].to(DEV, torch.float32).reshape(-1).contiguous()
+                rec[s:e, r_off:r_off + 4 * rs] = v.view(torch.uint8).view(e - s, 4 * rs)
+            if off is not None:
+                rec[s:e, s_off:s_off + SLAB_BYTES] = label_slabs(off, lab, s, e, overflow_every)
+        return cls(rec, stride, r_off, rs, s_off)
+
+    def view_fields(self):
+        """(records pointer, stride) for gofann_rabitq_view."""
+        return self.data.data_ptr(), self.stride
+
+    def slab(self):
+        if self.slab_offset < 0:
+            return None, 0
+        return self.data.data_ptr() + self.slab_offset, self.stride
+
+    def ranges(self):
+        """(pointer, stride in floats) of the attribute values, or None."""
+        if self.range_offset < 0:
+            return None
+        return self.data.data_ptr() + self.range_offset, self.stride // 4
 
 
 def _u16_bytes(x: torch.Tensor) -> torch.Tensor:
@@ -201,16 +282,28 @@ class DeviceRoutes:
                       end - begin, _lib.ptr(order))
 
     def predicate_view(self, dg: DeviceGraph, alpha: float, pending_base_stop: bool,
-                       enabled: bool = True, records: "SampleRecords | None" = None
+                       enabled: bool = True,
+                       records: "SampleRecords | RabitqRecords | None" = None
                        ) -> PredicateView:
+        """`records`: per-sample records whose label slab (and, for
+        RabitqRecords holding them, attribute values) the predicate reads in
+        place of the separate arrays; the values are the same."""
         slab, slab_stride = records.slab() if records is not None else (None, 0)
+        base_ranges, range_stride = _lib.ptr(self.base_ranges), self.range_stride
+        columns = 0
+        rr = records.ranges() if isinstance(records, RabitqRecords) else None
+        if rr is not None and self.base_ranges is not None:
+            if records.range_stride != self.range_stride:
+                raise ValueError("records hold a different number of attribute columns")
+            base_ranges, range_stride = rr
+            columns = self.range_stride
         return PredicateView(_lib.ptr(self.pred_offsets), _lib.ptr(self.pred_handles),
                              _lib.ptr(self.pred_clauses), _lib.ptr(self.pred_ranges),
                              _lib.ptr(self.pred_enabled) if enabled else None,
-                             _lib.ptr(self.pred_compiled), _lib.ptr(self.base_ranges),
+                             _lib.ptr(self.pred_compiled), base_ranges,
                              _lib.ptr(dg.csr_offsets), _lib.ptr(dg.csr_labels),
-                             dg.samples, self.range_stride, float(alpha),
-                             1 if pending_base_stop else 0, slab, slab_stride)
+                             dg.samples, range_stride, float(alpha),
+                             1 if pending_base_stop else 0, slab, slab_stride, columns)
 
 
 class CoarseEntry:

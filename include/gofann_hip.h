@@ -127,6 +127,11 @@ typedef struct {
      * Labels must be < 0xFFFF.  NULL: CSR only.  Results are identical. */
     const uint8_t* label_slab;
     uint32_t slab_stride;
+    /* Attribute columns of base_ranges; 0: range_stride.  Set when the
+     * values sit inside wider per-sample records (range_stride is then the
+     * record stride in floats), so a range atom on a column past the last
+     * still fails as it does with the plain array. */
+    uint32_t range_columns;
 } gofann_predicate_view;
 
 /* Routes of one batch.  Route r searches group route_group[r] from the
@@ -207,6 +212,18 @@ typedef struct {
     uint32_t padded_dim;
     uint32_t num_anchors;
     uint32_t samples;
+    /* Optional per-sample records read by the graph traversal in place of
+     * the three arrays above (no counterpart in the reference, which keeps
+     * them apart): record s at records + s * record_stride holds the code
+     * row (padded_dim/8 bytes) at offset 0, then f_add and f_rescale (f32)
+     * and the anchor id (u32), so one memory line serves a scored
+     * candidate; the predicate view's label_slab and base_ranges may point
+     * into the same records.  record_stride: multiple of 16, at least
+     * padded_dim/8 + 12; records 16-byte aligned.  NULL: the arrays.
+     * Results are identical either way; the arrays stay required (the
+     * posting scans and the row builders read them). */
+    const uint8_t* records;
+    uint32_t record_stride;
 } gofann_rabitq_view;
 
 /* Prepared RaBitQ queries (init_prepared_query_state outputs). */

@@ -495,3 +495,98 @@ def test_rabitq_pair_kernel_matches_oracle(gpu_ctx, rworld, Q, W, hash_mode, bia
     assert (oi[:n, 0] != U32MAX).sum() > n // 2
     if Q > 300:  # some frontier grew past 260 slots: pairs 64.. have children
         assert ost[:n, 6].max() > 300
+
+
+@pytest.fixture(scope="module")
+def rrange_world():
+    """Tags and one numeric attribute: route predicates with label and
+    range atoms, for per-sample records that carry both."""
+    wl = synth.small_labelled(n=6000, nq=40, dim=60, k=10, sigma=0.7, labels=5, seed=37, tags=True,
+                              ranges=True)
+    li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
+                              wl.centroids, degree=32, threshold=300)
+    pl = gp.plan_queries(li, wl.query_labels, wl.query_ranges)
+    return wl, li, pl
+
+
+@pytest.mark.parametrize("P", [128, 512, 4096])
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("hash_mode,Q", [(_lib.PLACE_AUTO, 40), (_lib.PLACE_GLOBAL, 96),
+                                         (_lib.PLACE_LDS, 300)])
+@pytest.mark.parametrize("overflow", [0, 3])
+def test_rabitq_search_with_records_matches_oracle(gpu_ctx, rrange_world, P, bias, hash_mode, Q,
+                                                   overflow, monkeypatch):
+    """The traversal reading per-sample records (code row, f_add, f_rescale,
+    anchor id, attribute value, label slab in one line) in place of the
+    separate arrays, its predicate reading the slab and the attribute from
+    the same records: ids, distance bits and counters identical to the
+    oracle, in the one-route and the two-routes-per-wave kernels; overflow 3
+    forces every third row's labels through the CSR."""
+    wl, li, pl = rrange_world
+    if P <= 1024:
+        rot = gi.random_rotation(wl.dim, P, 37005 + P, "cpu")
+    else:
+        rot = torch.randn(wl.dim, P, generator=torch.Generator().manual_seed(37005 + P)) / P ** 0.5
+    codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
+    say("rabitq records P", P, "bias", bias, "hash", hash_mode, "Q", Q, "overflow", overflow)
+    rw = (wl, li, pl, rot, codes, fac, aid, anchors, P)
+    dev, rv = _rviews(rw)
+    out, rq = prepare(gpu_ctx, dev["q"], dev["rot"], dev["anchors"], wl.dim, P)
+    rs = pl.graph
+    W = 30
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li, wl.base_ranges,
+                                          alpha=0.15 if bias else 0.0, pending_base_stop=bias)
+    prm_o = po.params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias, rabitq_verdict=1)
+    oi, od, ost = po.rabitq_search(li, rs, pred_o, prm_o, codes.numpy(), fac.numpy(),
+                                   aid.numpy().astype(np.uint32), out["q8"].cpu().numpy(),
+                                   out["scale"].cpu().numpy(), out["k1"].cpu().numpy(),
+                                   out["cd"].cpu().numpy(), anchors.shape[0], P)
+    rec = gs.RabitqRecords.build(dev["codes"], dev["fac"], dev["aid"], wl.base_ranges,
+                                 li.csr_offsets, li.csr_labels, chunk=2500,
+                                 overflow_every=overflow)
+    assert rec.stride % 128 == 0 and rec.stride >= P // 8 + 12 + 4 + 16
+    rv.records, rv.record_stride = rec.view_fields()
+    dg = gs.DeviceGraph.upload(li, neighbor_samples=True)
+    dr = gs.DeviceRoutes.upload(rs, wl.base_ranges)
+    pv = dr.predicate_view(dg, 0.15 if bias else 0.0, bias, records=rec)
+    assert pv.range_columns == 1 and pv.range_stride == rec.stride // 4
+    prm = gs.search_params(queue_limit=Q, result_width=W, early_stop_mode=2, bias=bias,
+                           hash_mode=hash_mode)
+    n = rs.count
+    for pair in ("0", "1"):
+        monkeypatch.setenv("GOFANN_RABITQ_PAIR", pair)
+        ids = torch.empty(n * W, dtype=torch.int32, device="cuda")
+        dists = torch.empty(n * W, device="cuda")
+        st = torch.zeros(n * 8, dtype=torch.int32, device="cuda")
+        gpu_ctx.check(gpu_ctx.lib.gofann_rabitq_search(
+            gpu_ctx.handle, rv, rq, dg.view(), pv, dr.routes_view(), prm, _lib.ptr(ids),
+            _lib.ptr(dists), _lib.ptr(st)))
+        torch.cuda.synchronize()
+        assert np.array_equal(as_u32(ids).reshape(n, W), oi), pair
+        assert np.array_equal(dists.cpu().numpy().reshape(n, W).view(np.uint32),
+                              od.view(np.uint32)), pair
+        assert np.array_equal(st.cpu().numpy().reshape(n, 8), ost), pair
+    assert (oi[:, 0] != U32MAX).sum() > n // 3
+
+
+def test_rabitq_records_layout(gpu_ctx):
+    """Record bytes: code row at 0, f_add and f_rescale, anchor id, the
+    attribute columns, the 16-byte label slab at a 16-byte offset, stride a
+    multiple of 128."""
+    n, cb = 50, 64
+    g = torch.Generator().manual_seed(5)
+    codes = torch.randint(0, 256, (n, cb), generator=g, dtype=torch.uint8)
+    fac = torch.randn(n, 3, generator=g)
+    aid = torch.randint(0, 1000, (n,), generator=g, dtype=torch.int32)
+    br = torch.randn(n, 2, generator=g).numpy()
+    off = np.arange(0, 2 * n + 1, 2, dtype=np.uint32)
+    lab = np.tile(np.array([3, 9], np.uint32), n)
+    rec = gs.RabitqRecords.build(codes.cuda(), fac.cuda(), aid.cuda(), br, off, lab, chunk=7)
+    d = rec.data.cpu().numpy()
+    assert rec.stride == 128 and rec.range_offset == 76 and rec.slab_offset == 96
+    assert np.array_equal(d[:, :cb], codes.numpy())
+    assert np.array_equal(d[:, cb:cb + 8].copy().view(np.float32), fac[:, :2].numpy())
+    assert np.array_equal(d[:, cb + 8:cb + 12].copy().view(np.int32)[:, 0], aid.numpy())
+    assert np.array_equal(d[:, 76:84].copy().view(np.float32), br)
+    sl = d[:, 96:112].copy().view(np.uint16)
+    assert np.all(sl[:, 0] == 2) and np.all(sl[:, 1] == 3) and np.all(sl[:, 2] == 9)
