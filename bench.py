@@ -105,7 +105,11 @@ def parse():
     ap.add_argument("--posting-share-routes", type=int, default=16,
                     help="label-shared scan: routes per workgroup item (at most 16)")
     ap.add_argument("--posting-segment-rows", type=int, default=32768,
-                    help="rows per segment of the segmented label-posting scan")
+                    help="rows per segment of the segmented label-posting scan (C5)")
+    ap.add_argument("--posting-segment-rows-c4", type=int, default=8192,
+                    help="rows per segment of C4's label-posting scan (707 routes, 17M rows: "
+                         "8192 gives 2453 workgroups; 0.96 ms against 1.14 at 32768, 1.25 at "
+                         "2048)")
     ap.add_argument("--c4-threshold", type=int, default=50_000,
                     help="labels with at most this many rows are posting routes")
     ap.add_argument("--n-c3", type=int, default=2_700_000)
@@ -368,12 +372,20 @@ class ExactRoute:
     an exact-distance u8 beam (gofann_exact_search) emitting its exact top-10;
     posting routes and the per-query merge are the pipeline's own."""
 
-    def __init__(self, pipe, li, entry=None):
+    def __init__(self, pipe, li, entry=None, route_class=None):
         gs = pipe.gs
         self.pipe, self.gs = pipe, gs
         self.ls = gs.u32(li.label_size)
         self.pv = pipe.dr_graph.predicate_view(pipe.dg, 0.0, False)
         self.rv = pipe.dr_graph.routes_view()
+        # route_class: class index of every graph route; a tuple beam in
+        # step() launches each class's routes (as a launch order) at its own
+        # beam -- a route's result depends on its own beam only
+        self.class_orders = []
+        if route_class is not None:
+            rc = np.asarray(route_class)
+            self.class_orders = [gs.u32(np.nonzero(rc == c)[0].astype(np.uint32))
+                                 for c in range(int(rc.max()) + 1 if len(rc) else 0)]
         # entry=None: every route starts at its label's medoid (the
         # reference's rule); a gs.CoarseEntry picks entry rows inside step()
         self.entry = entry
@@ -381,29 +393,58 @@ class ExactRoute:
         self.stats = pipe.torch.zeros(max(pipe.n_graph, 1) * 8, dtype=pipe.torch.int32,
                                       device="cuda")
         self.ev = [pipe.torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        self.last_ctx = pipe.ctx
 
     # early-stop rule of the beam: (mode, fixed limit); step cap (0: none)
     stop = (2, 1)  # adaptive (backend_pq.cu:2822-2873)
     max_steps = 0
 
-    def step(self, Q: int, timed_kernel=False):
+    def step(self, Q, timed_kernel=False):
+        """Q: one beam for every graph route, or one per route class."""
         p, gs = self.pipe, self.gs
         L = gs._lib
         ng, npost = p.n_graph, p.n_post
-        prm = L.ExactParams(Q, self.stop[1], self.stop[0], self.max_steps, 10, p.hash_mode)
         rv = self.rv
+        start = None
         if self.entry is not None and ng:
             near = self.entry.nearest(p.q)
-            self.entry.seeds(near, p.dr_graph.route_query, p.dr_graph.route_group,
-                             out=self.seed_buf)
+            start = self.entry.seeds(near, p.dr_graph.route_query, p.dr_graph.route_group,
+                                     out=self.seed_buf)
             rv = p.dr_graph.routes_view(start=self.seed_buf)
+        if isinstance(Q, (tuple, list)):
+            runs = []
+            for order, q in zip(self.class_orders, Q):
+                if order.numel():
+                    r = p.dr_graph.routes_view(start=start)
+                    r.count, r.launch_order = int(order.numel()), L.ptr(order)
+                    runs.append((q, r))
+        else:
+            runs = [(Q, rv)]
         if timed_kernel:
             self.ev[0].record()
         if ng:
-            p.ctx.check(p.ctx.lib.gofann_exact_search(
-                p.ctx.handle, L.ptr(p.wl.base), L.ELEM_U8, int(p.wl.base.shape[1]),
-                int(p.wl.base.shape[0]), L.ptr(p.q), p.dg.view(), L.ptr(self.ls), self.pv,
-                rv, prm, L.ptr(p.fin_i), L.ptr(p.fin_d), L.ptr(self.stats)))
+            # one class: this stream; several: each on its own stream and
+            # context (its own visited-set scratch), joined below, so the
+            # tail of one launch overlaps the next
+            torch = p.torch
+            main = torch.cuda.current_stream()
+            used = []
+            streams, ctxs = class_pool(torch, L) if len(runs) > 1 else ([main], [p.ctx])
+            for i, (q, r) in enumerate(runs):
+                st, cx = streams[i % len(streams)], ctxs[i % len(ctxs)]
+                if len(runs) > 1:
+                    st.wait_stream(main)
+                    cx.bind_stream(st)
+                prm = L.ExactParams(q, self.stop[1], self.stop[0], self.max_steps, 10, p.hash_mode)
+                cx.check(cx.lib.gofann_exact_search(
+                    cx.handle, L.ptr(p.wl.base), L.ELEM_U8, int(p.wl.base.shape[1]),
+                    int(p.wl.base.shape[0]), L.ptr(p.q), p.dg.view(), L.ptr(self.ls), self.pv,
+                    r, prm, L.ptr(p.fin_i), L.ptr(p.fin_d), L.ptr(self.stats)))
+                used.append(st)
+                self.last_ctx = cx
+            for st in used:
+                if st is not main:
+                    main.wait_stream(st)
         if timed_kernel:
             self.ev[1].record()
         if npost:
@@ -438,6 +479,10 @@ def exact_route_bytes(st: np.ndarray, degree: int, dim: int, neighbor_samples: b
 
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
+
+# Per-class beams (1 tag, 2 tags) of the C2 exact-route launch that
+# profiles/exact_route_c2_traffic.md measured.
+C2_TRAFFIC_BEAMS = (80, 80)
 
 
 def rabitq_prep_leg(ctx, torch, nq=10_000, dim=4096, anchors=512, reps=3):
@@ -653,43 +698,61 @@ def cpu_baseline(wl, li, table, codes, pl, Q, seconds, inline, exact_route=False
     qlist = list(range(len(wl.query_labels)))
     chunk = 64 * threads
     T = threads
+    # Q: one beam, or one per query class (index: tag count - 1); a class's
+    # queries are planned and searched together at its beam
+    beams = tuple(Q.values()) if isinstance(Q, dict) else None
+    batches = []
     while done < len(qlist) and time.perf_counter() - t0 < seconds:
-        sel = qlist[done: done + chunk]
-        sub = gp.plan_queries(li, [wl.query_labels[i] for i in sel])
-        rs = sub.graph
-        res_i, res_d, r2q = [], [], []
-        if rs.count and exact_route:
-            pred = po.PredicateArrays.from_plan(rs.predicate, li)
-            ri, rd, _ = po.exact_search(li, rs, pred, base, qs[sel], queue_limit=Q, topk=10,
-                                        early_stop_mode=2, label_size=li.label_size, threads=T)
-            res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
-        elif rs.count:
-            pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
-                                                pending_base_stop=True)
-            if inline:
-                ri, rd, _ = po.pq_search(li, rs, pred,
-                                         po.params(queue_limit=Q, result_width=10,
-                                                   inline_exact=True),
-                                         codes_h, table_h, qs[sel], base=base, threads=T)
-            else:
-                ids, _, _ = po.pq_search(li, rs, pred,
-                                         po.params(queue_limit=Q, result_width=100),
-                                         codes_h, table_h, qs[sel], threads=T)
-                ri, rd = po.rerank(base, qs[sel], rs.route_query, ids, 10, threads=T)
-            res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
-        if sub.posting.count:
-            pr = po.PredicateArrays.from_plan(sub.posting.predicate, li)
-            pi, _, _ = po.posting_scan_pq(pr, codes_h, table_h, qs[sel], sub.posting.route_query,
-                                          li.posting_ids, sub.cand_offsets, sub.cand_sizes, 100,
-                                          threads=T)
-            ri, rd = po.rerank(base, qs[sel], sub.posting.route_query, pi, 10, threads=T)
-            res_i.append(ri), res_d.append(rd), r2q.append(sub.posting.route_to_query)
-        if res_i:
-            po.merge(np.concatenate(r2q), np.concatenate(res_i), np.concatenate(res_d),
-                     len(sel), 10)
-        done += len(sel)
+        part = qlist[done: done + chunk]
+        if beams is None:
+            batches = [(part, Q)]
+        else:
+            batches = [([i for i in part if len(wl.query_labels[i]) - 1 == c], q)
+                       for c, q in enumerate(beams)]
+        for sel, Qb in batches:
+            if sel:
+                _cpu_batch(sel, Qb, wl, li, base, qs, codes_h, table_h, inline, exact_route,
+                           T, po, gp)
+        done += len(part)
     el = time.perf_counter() - t0
     return done / el, done, el
+
+
+def _cpu_batch(sel, Q, wl, li, base, qs, codes_h, table_h, inline, exact_route, T, po, gp):
+    """One cpu_baseline batch: plan, graph search at beam Q, posting scan,
+    rerank, merge."""
+    sub = gp.plan_queries(li, [wl.query_labels[i] for i in sel])
+    rs = sub.graph
+    res_i, res_d, r2q = [], [], []
+    if rs.count and exact_route:
+        pred = po.PredicateArrays.from_plan(rs.predicate, li)
+        ri, rd, _ = po.exact_search(li, rs, pred, base, qs[sel], queue_limit=Q, topk=10,
+                                    early_stop_mode=2, label_size=li.label_size, threads=T)
+        res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
+    elif rs.count:
+        pred = po.PredicateArrays.from_plan(rs.predicate, li, alpha=0.15,
+                                            pending_base_stop=True)
+        if inline:
+            ri, rd, _ = po.pq_search(li, rs, pred,
+                                     po.params(queue_limit=Q, result_width=10,
+                                               inline_exact=True),
+                                     codes_h, table_h, qs[sel], base=base, threads=T)
+        else:
+            ids, _, _ = po.pq_search(li, rs, pred,
+                                     po.params(queue_limit=Q, result_width=100),
+                                     codes_h, table_h, qs[sel], threads=T)
+            ri, rd = po.rerank(base, qs[sel], rs.route_query, ids, 10, threads=T)
+        res_i.append(ri), res_d.append(rd), r2q.append(rs.route_to_query)
+    if sub.posting.count:
+        pr = po.PredicateArrays.from_plan(sub.posting.predicate, li)
+        pi, _, _ = po.posting_scan_pq(pr, codes_h, table_h, qs[sel], sub.posting.route_query,
+                                      li.posting_ids, sub.cand_offsets, sub.cand_sizes, 100,
+                                      threads=T)
+        ri, rd = po.rerank(base, qs[sel], sub.posting.route_query, pi, 10, threads=T)
+        res_i.append(ri), res_d.append(rd), r2q.append(sub.posting.route_to_query)
+    if res_i:
+        po.merge(np.concatenate(r2q), np.concatenate(res_i), np.concatenate(res_d),
+                 len(sel), 10)
 
 
 # ---------------------------------------------------------------------------
@@ -2047,7 +2110,7 @@ def run_c4(args, torch, ctx, world=None) -> dict:
     log(f"C4 ground truth for {len(gt)} queries in {time.time() - t0:.1f}s")
     t0 = time.time()
     pipe = RabitqLabelPipeline(ctx, wl, li, rq, torch, posting_layout=args.posting_layout,
-                               segment_rows=args.posting_segment_rows,
+                               segment_rows=args.posting_segment_rows_c4,
                                neighbor_samples=not args.no_neighbor_samples,
                                posting_share=not args.no_posting_share,
                                share_routes=args.posting_share_routes,
@@ -2377,15 +2440,22 @@ def main():
         r2.close()
 
     def exact_leg(er, ladder, label):
-        q3, rec3 = ladder[-1], 0.0
+        # the smallest beam per query class (1 tag, 2 tags) that reaches the
+        # target on that class's queries; the routes of a class run at its beam
+        chosen = [None if g else ladder[0] for _, g in class_gt2]
         for Q3 in ladder:
             out3 = er.step(Q3)
             torch.cuda.synchronize()
-            rec3 = recall_at_10(out3.cpu().numpy().view(np.uint32).reshape(pl.queries, 10), gt)
-            log(f"{label} Q={Q3}: recall@10={rec3:.4f}")
-            q3 = Q3
-            if rec3 >= args.target_recall:
+            res = out3.cpu().numpy().view(np.uint32).reshape(pl.queries, 10)
+            recs = [recall_at_10(res, g) if g else None for _, g in class_gt2]
+            log(f"{label} Q={Q3}: recall@10 {recall_at_10(res, gt):.4f} (" + ", ".join(
+                f"{n} {r:.4f}" for (n, _), r in zip(class_gt2, recs) if r is not None) + ")")
+            for i, r in enumerate(recs):
+                if chosen[i] is None and r is not None and r >= args.target_recall:
+                    chosen[i] = Q3
+            if all(c is not None for c in chosen):
                 break
+        q3 = tuple(c if c is not None else ladder[-1] for c in chosen)
         er.step(q3)
         torch.cuda.synchronize()
         k3 = []
@@ -2401,10 +2471,12 @@ def main():
         st3 = er.route_stats()
         kms3 = float(np.mean(k3))
         b3 = exact_route_bytes(st3, li.degree, wl.dim, not args.no_neighbor_samples)
-        pl3 = ctx.last_placement()
+        pl3 = er.last_ctx.last_placement()
         ach3 = b3 / (kms3 / 1000.0) / 1e9
         res = {"qps": round(pl.queries / (ms3 / 1000.0), 1), "ms_per_step": round(ms3, 3),
-               "kernel_ms": round(kms3, 3), "queue": q3, "recall_at_10": round(rec3, 4),
+               "kernel_ms": round(kms3, 3),
+               "queue": dict(zip([n for n, _ in class_gt2], q3)),
+               "recall_at_10": round(rec3, 4),
                "recall_by_class": by3, "gt_by_class": {n: len(g) for n, g in class_gt2},
                "placement": pl3,
                "steps_per_route": round(float(st3[:, 0].mean()), 1),
@@ -2422,15 +2494,20 @@ def main():
     route3 = coarse3 = None
     ladder3 = [int(x) for x in args.exact_ladder.split(",")]
     if not args.no_exact_route and inline:
-        route3 = exact_leg(ExactRoute(pipe, li), ladder3, "exact route (medoid seeds)")
+        # class of each graph route: its query's tag count (1 or 2)
+        rclass = np.array([len(wl.query_labels[q]) - 1 for q in pl.graph.route_query],
+                          dtype=np.int64)
+        route3 = exact_leg(ExactRoute(pipe, li, route_class=rclass), ladder3,
+                           "exact route (medoid seeds)")
         route3["roofline"]["traffic"] = measured_traffic(
             "exact_route_c2_traffic.md",
-            route3["queue"] == 80 and route3["placement"].get("hash_in_lds") == 2
-            and not args.no_neighbor_samples)
+            tuple(route3["queue"].values()) == C2_TRAFFIC_BEAMS
+            and route3["placement"].get("hash_in_lds") == 2 and not args.no_neighbor_samples)
         route3["seeds"] = "label medoid"
         if not args.no_coarse_entry:
             from gofann_amd import search as gs
-            coarse3 = exact_leg(ExactRoute(pipe, li, entry=gs.CoarseEntry(li, cen)), ladder3,
+            coarse3 = exact_leg(ExactRoute(pipe, li, entry=gs.CoarseEntry(li, cen),
+                                           route_class=rclass), ladder3,
                                 "exact route (coarse entry)")
             coarse3["seeds"] = (f"per route: representative of the bucket of the query's "
                                 f"nearest of {cen.shape[0]} trained centres, picked on the GPU "
