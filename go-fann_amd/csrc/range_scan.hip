@@ -724,6 +724,7 @@ constexpr int kShareTile = 512;           // rows per LDS tile
 constexpr int kShareRoutesPerWave = 4;
 constexpr int kShareRoutes = kShareRoutesPerWave * (kScanThreads / kWave);  // 16 per item
 constexpr int kShareMaxKp = 128;          // shortlist_k <= 128
+constexpr int kShareHandles = 32;         // label handles of one pass held as row bits
 
 struct ShareScanArgs {
     gofann_predicate_view pred;
@@ -824,28 +825,58 @@ __device__ __forceinline__ bool short_clause_matches(const gofann_predicate_view
     return pass;
 }
 
+// short_clause_matches with the label atoms given as the row's handle bits:
+// every handle of the clause present ((bits & need) == need), then the same
+// range tests.
+__device__ __forceinline__ bool short_clause_bits_match(const gofann_predicate_view& v,
+                                                        const ShortClause& c, uint32_t sample,
+                                                        uint32_t bits, uint32_t need,
+                                                        const float* prange, float r0)
+{
+    if (sample >= v.rows) return false;
+    bool pass = (bits & need) == need;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (i >= c.nr) break;
+        const gofann_range_atom at = c.r[i];
+        pass = pass && v.base_ranges != nullptr && at.dimension < range_columns(v) &&
+               range_matches(at.mode, at.lower, at.upper,
+                             !prange ? v.base_ranges[static_cast<uint64_t>(sample) * v.range_stride +
+                                                     at.dimension]
+                             : range_columns(v) == 1 ? r0
+                                                   : prange[at.dimension]);
+    }
+    return pass;
+}
+
 template <int V>
 __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareScanArgs a,
                                                                         RabitqScanScorer sc)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ uint32_t s_pass[kShareRoutes];
+    __shared__ uint32_t s_h[kShareHandles];     // the pass's label handles, ascending
+    __shared__ uint32_t s_need[kShareRoutes];   // per route slot: bits of its handles
+    __shared__ int s_nh;
+    __shared__ int s_use_bits;
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
     const uint32_t item = blockIdx.x;
     if (item >= a.items) return;
-    const int k = a.k, kp = a.k_pow2;
-    // LDS: tile columns, then per route slot its query planes (plane-major,
-    // 8 x V 16-byte vectors) and its shortlist (kp pairs), then per wave a
-    // queue of tile rows to score.
+    const int k = a.k;
+    // LDS: tile columns (sample ids, label slabs, first range value, label
+    // bits), then per route slot its query planes (plane-major, 8 x V
+    // 16-byte vectors) and its shortlist (k pairs), then per wave a queue of
+    // tile rows to score.
     uint32_t* t_ids = reinterpret_cast<uint32_t*>(lds);
     uint4* t_slab = reinterpret_cast<uint4*>(t_ids + kShareTile);
     float* t_r0 = reinterpret_cast<float*>(t_slab + kShareTile);
-    uint4* planes_all = reinterpret_cast<uint4*>(t_r0 + kShareTile);
+    uint32_t* t_bits = reinterpret_cast<uint32_t*>(t_r0 + kShareTile);
+    uint4* planes_all = reinterpret_cast<uint4*>(t_bits + kShareTile);
     float* lst_d_all = reinterpret_cast<float*>(planes_all + kShareRoutes * 8 * V);
-    uint32_t* lst_id_all = reinterpret_cast<uint32_t*>(lst_d_all + kShareRoutes * kp);
-    uint32_t* queue_all = lst_id_all + kShareRoutes * kp;
+    uint32_t* lst_id_all = reinterpret_cast<uint32_t*>(lst_d_all + kShareRoutes * k);
+    uint32_t* queue_all = lst_id_all + kShareRoutes * k;
 
     const uint32_t first_all = a.item_begin[item];
     const int n_all = static_cast<int>(a.item_begin[item + 1] - first_all);
@@ -881,12 +912,61 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
     #pragma unroll
                 for (int j = 0; j < 8; ++j) pl[j * words + lane] = bits[j];
             }
-            for (int e = lane; e < kp; e += kWave) {
-                lst_d_all[q * kp + e] = FLT_MAX;
-                lst_id_all[q * kp + e] = UINT32_MAX;
+            for (int e = lane; e < k; e += kWave) {
+                lst_d_all[q * k + e] = FLT_MAX;
+                lst_id_all[q * k + e] = UINT32_MAX;
             }
             if (lane == 0) s_pass[q] = 0;
         }
+        // Label bits: when every enabled route of the pass is a short clause
+        // and their label handles number at most kShareHandles, each tile row
+        // gets one bit per handle it holds (found once per row), and a
+        // route's label atoms reduce to (bits & need) == need -- the same
+        // verdicts as the per-route slab walk (a row's slab labels are
+        // distinct and ascending; a handle >= 0xFFFF is on no slab).
+        if (tid == 0) {
+            int nh = 0;
+            int use = 1;
+            for (int q = 0; q < n_routes && use; ++q) {
+                const uint32_t route = a.seg_route[a.item_slots[first + q]];
+                if (!pred_enabled(a.pred, route)) continue;
+                const ShortClause c = short_clause(a.pred, route);
+                if (!c.simple) {
+                    use = 0;
+                    break;
+                }
+                for (int i = 0; i < c.nl; ++i) {
+                    int at = 0;
+                    while (at < nh && s_h[at] < c.h[i]) ++at;
+                    if (at < nh && s_h[at] == c.h[i]) continue;
+                    if (nh == kShareHandles) {
+                        use = 0;
+                        break;
+                    }
+                    for (int m = nh; m > at; --m) s_h[m] = s_h[m - 1];
+                    s_h[at] = c.h[i];
+                    ++nh;
+                }
+            }
+            for (int q = 0; q < n_routes && use; ++q) {
+                const uint32_t route = a.seg_route[a.item_slots[first + q]];
+                uint32_t need = 0;
+                if (pred_enabled(a.pred, route)) {
+                    const ShortClause c = short_clause(a.pred, route);
+                    for (int i = 0; i < c.nl; ++i) {
+                        int at = 0;
+                        while (s_h[at] != c.h[i]) ++at;
+                        need |= 1u << at;
+                    }
+                }
+                s_need[q] = need;
+            }
+            s_nh = nh;
+            s_use_bits = use;
+        }
+        __syncthreads();
+        const bool use_bits = s_use_bits != 0;
+        const int nh = s_nh;
         uint32_t* queue = queue_all + wave * kWave;
         const bool r0_tile = a.pranges && range_columns(a.pred) == 1;
 
@@ -896,8 +976,28 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             for (int r = tid; r < n; r += kScanThreads) {
                 const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
                 t_ids[r] = a.posting[j];
-                t_slab[r] = a.pslab[j];
+                const uint4 slab = a.pslab[j];
+                t_slab[r] = slab;
                 if (r0_tile) t_r0[r] = a.pranges[j];
+                if (use_bits) {
+                    uint32_t bits = 0;
+                    const uint32_t cnt = slab_count(slab);
+                    if (cnt != kSlabOverflow) {
+                        for (uint32_t e = 0; e < cnt; ++e) {
+                            const uint32_t label = slab_label(slab, e);
+                            int lo = 0, hi = nh;  // first handle >= label
+                            while (lo < hi) {
+                                const int mid = (lo + hi) >> 1;
+                                if (s_h[mid] < label)
+                                    lo = mid + 1;
+                                else
+                                    hi = mid;
+                            }
+                            if (lo < nh && s_h[lo] == label) bits |= 1u << lo;
+                        }
+                    }
+                    t_bits[r] = bits;
+                }
             }
             __syncthreads();
             for (int i = 0; i < kShareRoutesPerWave; ++i) {
@@ -907,12 +1007,13 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                 const uint32_t query = a.route_query[route];
                 const bool enabled = pred_enabled(a.pred, route);
                 const ShortClause sclause = enabled ? short_clause(a.pred, route) : ShortClause{};
+                const uint32_t need = use_bits ? s_need[q] : 0u;
                 const float scale = sc.q_scale[query];
                 const float k1 = sc.q_k1[query];
                 const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
                 const uint4* planes = planes_all + q * 8 * V;
-                float* ld = lst_d_all + q * kp;
-                uint32_t* lid = lst_id_all + q * kp;
+                float* ld = lst_d_all + q * k;
+                uint32_t* lid = lst_id_all + q * k;
                 uint32_t passes = 0;
                 int qn = 0;  // queued rows (uniform)
                 // Score the queued rows (lane i < qn takes queue[i]) and merge
@@ -998,7 +1099,10 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                                                           ? a.pranges + j * range_columns(a.pred)
                                                           : nullptr;
                                 const float rv = r0_tile ? t_r0[r] : 0.0f;
-                                ok = sclause.simple
+                                ok = use_bits
+                                         ? short_clause_bits_match(a.pred, sclause, s, t_bits[r],
+                                                                   need, prange, rv)
+                                     : sclause.simple
                                          ? short_clause_matches(a.pred, sclause, s, slab, prange, rv)
                                          : slab_pred_matches(a.pred, route, s, slab, prange, rv);
                             } else {
@@ -1025,8 +1129,8 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             if (q >= n_routes) break;
             const uint32_t slot = a.item_slots[first + q];
             for (int e = lane; e < k; e += kWave) {
-                a.out_ids[static_cast<size_t>(slot) * k + e] = lst_id_all[q * kp + e];
-                a.out_dists[static_cast<size_t>(slot) * k + e] = lst_d_all[q * kp + e];
+                a.out_ids[static_cast<size_t>(slot) * k + e] = lst_id_all[q * k + e];
+                a.out_dists[static_cast<size_t>(slot) * k + e] = lst_d_all[q * k + e];
             }
             if (lane == 0 && a.pass_counts) a.pass_counts[slot] = s_pass[q];
         }
@@ -1560,9 +1664,9 @@ int rabitq_posting_scan_shared(Context* ctx, const gofann_rabitq_view* rq,
     a.out_dists = scan_dists;
     a.pass_counts = merged || pass_counts ? scan_pass : nullptr;
     const size_t vecs = rq->padded_dim / 128;
-    const size_t lds = static_cast<size_t>(kShareTile) * 24 +
+    const size_t lds = static_cast<size_t>(kShareTile) * 28 +
                        static_cast<size_t>(kShareRoutes) * 8 * vecs * 16 +
-                       static_cast<size_t>(kShareRoutes) * a.k_pow2 * 8 +
+                       static_cast<size_t>(kShareRoutes) * a.k * 8 +
                        static_cast<size_t>(kScanThreads) * 4;
     if (lds > static_cast<size_t>(ctx->lds_per_block))
         return ctx->fail(GOFANN_ERR_UNSUPPORTED, "shared posting scan LDS exceeds the workgroup limit");
