@@ -849,6 +849,88 @@ __device__ __forceinline__ bool short_clause_bits_match(const gofann_predicate_v
     return pass;
 }
 
+// Scores the queued rows of route slot q (lane i < qn takes queue[i], a row
+// offset in the item) and merges the survivors into its shortlist by rank
+// (the lists hold k pairs per slot).  All 64 lanes of the wave call it.
+template <int V>
+__device__ __forceinline__ void share_flush(const ShareScanArgs& a, const RabitqScanScorer& sc,
+                                            uint32_t route, int q, const uint4* planes_all,
+                                            float* lst_d_all, uint32_t* lst_id_all,
+                                            const uint32_t* queue, int qn, uint64_t begin,
+                                            int lane)
+{
+    const int k = a.k;
+    const uint32_t query = a.route_query[route];
+    const float scale = sc.q_scale[query];
+    const float k1 = sc.q_k1[query];
+    const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
+    const uint4* planes = planes_all + q * 8 * V;
+    float* ld = lst_d_all + q * k;
+    uint32_t* lid = lst_id_all + q * k;
+    const bool have = lane < qn;
+    const uint64_t j = begin + (have ? queue[lane] : 0u);
+    uint32_t sid = UINT32_MAX;
+    float v = FLT_MAX;
+    if (have) {
+        sid = a.posting[j];
+        const uint4 x = a.paux[j];
+        uint4 c[V];
+#pragma unroll
+        for (int w = 0; w < V; ++w) c[w] = a.pcodes[j * V + w];
+        const float add0 = __uint_as_float(x.x) + g_row[x.z];
+        const int ip = lane_ip_lds<1, V>(c, planes, V, 0);
+        const float short_ip = static_cast<float>(ip) * scale;
+        const float tt = short_ip + k1;
+        v = fmaf(__uint_as_float(x.y), tt, add0);
+    }
+    const float kd = ld[k - 1];
+    const uint32_t kid = lid[k - 1];
+    const bool in = have && admissible(v, sid) && pair_less(v, sid, kd, kid);
+    const uint64_t sm = ballot(in);
+    if (!sm) return;
+    // ranks: list entry e moves up by the survivors below it; a survivor
+    // lands after the list entries and survivors below it
+    int c_self = 0;
+    if (in) {
+        int lo = 0, hi = k;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (pair_less(ld[mid], lid[mid], v, sid))
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        c_self = lo;
+    }
+    const int e0 = lane, e1 = lane + kWave;
+    const float d0 = e0 < k ? ld[e0] : FLT_MAX;
+    const uint32_t i0 = e0 < k ? lid[e0] : UINT32_MAX;
+    const float d1 = e1 < k ? ld[e1] : FLT_MAX;
+    const uint32_t i1 = e1 < k ? lid[e1] : UINT32_MAX;
+    int c0 = 0, c1 = 0;
+    for (uint64_t m = sm; m; m &= m - 1) {
+        const int src = __builtin_ctzll(m);
+        const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+        const uint32_t si = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(sid), src));
+        c0 += pair_less(sv, si, d0, i0) ? 1 : 0;
+        c1 += pair_less(sv, si, d1, i1) ? 1 : 0;
+        c_self += pair_less(sv, si, v, sid) ? 1 : 0;
+    }
+    // all reads of the old list precede these writes (one wave)
+    if (e0 < k && e0 + c0 < k) {
+        ld[e0 + c0] = d0;
+        lid[e0 + c0] = i0;
+    }
+    if (e1 < k && e1 + c1 < k) {
+        ld[e1 + c1] = d1;
+        lid[e1 + c1] = i1;
+    }
+    if (in && c_self < k) {
+        ld[c_self] = v;
+        lid[c_self] = sid;
+    }
+}
+
 template <int V>
 __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareScanArgs a,
                                                                         RabitqScanScorer sc)
@@ -859,6 +941,7 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
     __shared__ uint32_t s_need[kShareRoutes];   // per route slot: bits of its handles
     __shared__ int s_nh;
     __shared__ int s_use_bits;
+    __shared__ int s_qn[kShareRoutes];
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -867,8 +950,8 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
     const int k = a.k;
     // LDS: tile columns (sample ids, label slabs, first range value, label
     // bits), then per route slot its query planes (plane-major, 8 x V
-    // 16-byte vectors) and its shortlist (k pairs), then per wave a queue of
-    // tile rows to score.
+    // 16-byte vectors), its shortlist (k pairs) and its queue of passing
+    // rows still to score (kept across tiles, scored 64 at a time).
     uint32_t* t_ids = reinterpret_cast<uint32_t*>(lds);
     uint4* t_slab = reinterpret_cast<uint4*>(t_ids + kShareTile);
     float* t_r0 = reinterpret_cast<float*>(t_slab + kShareTile);
@@ -916,7 +999,10 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                 lst_d_all[q * k + e] = FLT_MAX;
                 lst_id_all[q * k + e] = UINT32_MAX;
             }
-            if (lane == 0) s_pass[q] = 0;
+            if (lane == 0) {
+                s_pass[q] = 0;
+                s_qn[q] = 0;
+            }
         }
         // Label bits: when every enabled route of the pass is a short clause
         // and their label handles number at most kShareHandles, each tile row
@@ -967,7 +1053,6 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
         __syncthreads();
         const bool use_bits = s_use_bits != 0;
         const int nh = s_nh;
-        uint32_t* queue = queue_all + wave * kWave;
         const bool r0_tile = a.pranges && range_columns(a.pred) == 1;
 
         for (uint64_t t0 = 0; t0 < count; t0 += kShareTile) {
@@ -1004,87 +1089,12 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                 const int q = wave + i * (kScanThreads / kWave);
                 if (q >= n_routes) break;
                 const uint32_t route = a.seg_route[a.item_slots[first + q]];
-                const uint32_t query = a.route_query[route];
                 const bool enabled = pred_enabled(a.pred, route);
                 const ShortClause sclause = enabled ? short_clause(a.pred, route) : ShortClause{};
                 const uint32_t need = use_bits ? s_need[q] : 0u;
-                const float scale = sc.q_scale[query];
-                const float k1 = sc.q_k1[query];
-                const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
-                const uint4* planes = planes_all + q * 8 * V;
-                float* ld = lst_d_all + q * k;
-                uint32_t* lid = lst_id_all + q * k;
+                uint32_t* queue = queue_all + q * kWave;
+                int qn = s_qn[q];  // queued rows of this slot (uniform), kept across tiles
                 uint32_t passes = 0;
-                int qn = 0;  // queued rows (uniform)
-                // Score the queued rows (lane i < qn takes queue[i]) and merge
-                // the survivors into the shortlist by rank.
-                auto flush = [&]() {
-                    const bool have = lane < qn;
-                    const int r = have ? static_cast<int>(queue[lane]) : 0;
-                    const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
-                    uint32_t sid = UINT32_MAX;
-                    float v = FLT_MAX;
-                    if (have) {
-                        sid = t_ids[r];
-                        const uint4 x = a.paux[j];
-                        uint4 c[V];
-    #pragma unroll
-                        for (int w = 0; w < V; ++w) c[w] = a.pcodes[j * V + w];
-                        const float add0 = __uint_as_float(x.x) + g_row[x.z];
-                        const int ip = lane_ip_lds<1, V>(c, planes, V, 0);
-                        const float short_ip = static_cast<float>(ip) * scale;
-                        const float tt = short_ip + k1;
-                        v = fmaf(__uint_as_float(x.y), tt, add0);
-                    }
-                    const float kd = ld[k - 1];
-                    const uint32_t kid = lid[k - 1];
-                    const bool in = have && admissible(v, sid) && pair_less(v, sid, kd, kid);
-                    const uint64_t sm = ballot(in);
-                    qn = 0;
-                    if (!sm) return;
-                    // ranks: list entry e moves up by the survivors below it; a
-                    // survivor lands after the list entries and survivors below it
-                    int c_self = 0;
-                    if (in) {
-                        int lo = 0, hi = k;
-                        while (lo < hi) {
-                            const int mid = (lo + hi) >> 1;
-                            if (pair_less(ld[mid], lid[mid], v, sid))
-                                lo = mid + 1;
-                            else
-                                hi = mid;
-                        }
-                        c_self = lo;
-                    }
-                    const int e0 = lane, e1 = lane + kWave;
-                    const float d0 = e0 < k ? ld[e0] : FLT_MAX;
-                    const uint32_t i0 = e0 < k ? lid[e0] : UINT32_MAX;
-                    const float d1 = e1 < k ? ld[e1] : FLT_MAX;
-                    const uint32_t i1 = e1 < k ? lid[e1] : UINT32_MAX;
-                    int c0 = 0, c1 = 0;
-                    for (uint64_t m = sm; m; m &= m - 1) {
-                        const int src = __builtin_ctzll(m);
-                        const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
-                        const uint32_t si = static_cast<uint32_t>(
-                            __builtin_amdgcn_readlane(static_cast<int>(sid), src));
-                        c0 += pair_less(sv, si, d0, i0) ? 1 : 0;
-                        c1 += pair_less(sv, si, d1, i1) ? 1 : 0;
-                        c_self += pair_less(sv, si, v, sid) ? 1 : 0;
-                    }
-                    // all reads of the old list precede these writes (one wave)
-                    if (e0 < k && e0 + c0 < k) {
-                        ld[e0 + c0] = d0;
-                        lid[e0 + c0] = i0;
-                    }
-                    if (e1 < k && e1 + c1 < k) {
-                        ld[e1 + c1] = d1;
-                        lid[e1 + c1] = i1;
-                    }
-                    if (in && c_self < k) {
-                        ld[c_self] = v;
-                        lid[c_self] = sid;
-                    }
-                };
                 for (int r0 = 0; r0 < n; r0 += kWave) {
                     const int r = r0 + lane;
                     bool ok = false;
@@ -1115,13 +1125,32 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                     const int c = __popcll(om);
                     if (enabled) passes += static_cast<uint32_t>(c);
                     if (c == 0) continue;
-                    if (qn + c > kWave) flush();
-                    if (ok) queue[qn + static_cast<int>(lanes_below(om))] = static_cast<uint32_t>(r);
+                    if (qn + c > kWave) {
+                        share_flush<V>(a, sc, route, q, planes_all, lst_d_all, lst_id_all, queue,
+                                       qn, begin, lane);
+                        qn = 0;
+                    }
+                    // the row's offset in the item (items hold < 2^32 rows)
+                    if (ok)
+                        queue[qn + static_cast<int>(lanes_below(om))] =
+                            static_cast<uint32_t>(t0) + static_cast<uint32_t>(r);
                     qn += c;
                 }
-                if (qn) flush();
-                if (lane == 0) s_pass[q] += passes;
+                if (lane == 0) {
+                    s_pass[q] += passes;
+                    s_qn[q] = qn;
+                }
             }
+        }
+        // the rows still queued
+        __syncthreads();
+        for (int i = 0; i < kShareRoutesPerWave; ++i) {
+            const int q = wave + i * (kScanThreads / kWave);
+            if (q >= n_routes) break;
+            const int qn = s_qn[q];
+            if (qn)
+                share_flush<V>(a, sc, a.seg_route[a.item_slots[first + q]], q, planes_all,
+                               lst_d_all, lst_id_all, queue_all + q * kWave, qn, begin, lane);
         }
         __syncthreads();
         for (int i = 0; i < kShareRoutesPerWave; ++i) {
@@ -1667,7 +1696,7 @@ int rabitq_posting_scan_shared(Context* ctx, const gofann_rabitq_view* rq,
     const size_t lds = static_cast<size_t>(kShareTile) * 28 +
                        static_cast<size_t>(kShareRoutes) * 8 * vecs * 16 +
                        static_cast<size_t>(kShareRoutes) * a.k * 8 +
-                       static_cast<size_t>(kScanThreads) * 4;
+                       static_cast<size_t>(kShareRoutes) * kWave * 4;
     if (lds > static_cast<size_t>(ctx->lds_per_block))
         return ctx->fail(GOFANN_ERR_UNSUPPORTED, "shared posting scan LDS exceeds the workgroup limit");
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize,
