@@ -61,7 +61,8 @@ def parse():
     ap.add_argument("--table-mode", type=int, default=0,
                     help="PQ table placement: 0 auto, 1 LDS table, 2 on-demand entries")
     ap.add_argument("--hash-mode", type=int, default=0,
-                    help="visited hash placement: 0 auto, 1 LDS, 2 global")
+                    help="visited hash placement: 0 auto, 1 LDS, 2 global, 3 LDS spilling to "
+                         "global (C2 routes and the C3-C5 RaBitQ traversals)")
     ap.add_argument("--no-neighbor-samples", action="store_true",
                     help="gather neighbour sample ids through row_to_sample")
     ap.add_argument("--no-records", action="store_true",
@@ -1106,6 +1107,8 @@ class RabitqRangePipeline:
     the smallest slice for narrow ones (both shortlist 200), exact fp32
     rerank of the 200, and the per-query merge."""
 
+    hash_mode = 0  # visited-set placement of the graph traversal (PLACE_*)
+
     def __init__(self, ctx, wl, li, rq, rpi, torch, scan_rows, width=200, segment_rows=4096,
                  resident_copies=True, neighbor_samples=True, records=True):
         from gofann_amd import _lib
@@ -1245,7 +1248,8 @@ class RabitqRangePipeline:
         stream; the pipeline's context by default)."""
         L, gs = self.L, self.gs
         ctx = ctx or self.ctx
-        prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
+        prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True,
+                               hash_mode=self.hash_mode)
         ctx.check(ctx.lib.gofann_rabitq_search(
             ctx.handle, self.rv, self.rq, self.dg.view(),
             self.dr.predicate_view(self.dg, 0.15, True, records=self.recs),
@@ -1399,6 +1403,7 @@ def run_c3(args, torch, ctx) -> dict:
                                neighbor_samples=not args.no_neighbor_samples,
                                records=not args.no_rabitq_records)
     pipe.P, pipe.li = rq["P"], li
+    pipe.hash_mode = args.hash_mode
     log(f"C3 routes: {pipe.ng} graph (wide ranges), {pipe.np_} range-posting scans "
         f"({pipe.scan_rows_total} rows)")
     sel = np.asarray(wl.meta["selectivity"], dtype=np.float64)
@@ -1534,6 +1539,8 @@ class RabitqLabelPipeline:
     interval is not wholly inside it), the RaBitQ label-posting scan for
     equality queries on rare labels, exact fp16->fp32 rerank of the W-wide
     shortlists, and the per-query merge."""
+
+    hash_mode = 0  # visited-set placement of the graph traversal (PLACE_*)
 
     def __init__(self, ctx, wl, li, rq, torch, width=100, posting_layout="columns",
                  segment_rows=32768, neighbor_samples=True, posting_share=True,
@@ -1719,7 +1726,8 @@ class RabitqLabelPipeline:
         stream; the pipeline's context by default)."""
         L, gs = self.L, self.gs
         ctx = ctx or self.ctx
-        prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True)
+        prm = gs.search_params(queue_limit=q, result_width=self.W, early_stop_mode=2, bias=True,
+                               hash_mode=self.hash_mode)
         ctx.check(ctx.lib.gofann_rabitq_search(
             ctx.handle, self.rv, self.rq, self.dg.view(),
             self.dr.predicate_view(self.dg, 0.15, True, records=self.recs),
@@ -2116,6 +2124,7 @@ def run_c4(args, torch, ctx, world=None) -> dict:
                                share_routes=args.posting_share_routes,
                                records=not args.no_rabitq_records)
     pipe.P, pipe.li = rq["P"], li
+    pipe.hash_mode = args.hash_mode
     log(f"C4 routes: {pipe.ng} graph ({pipe.n_eq} equality, {pipe.interior} interior "
         f"intervals), {pipe.np_} label-posting scans ({pipe.post_rows_total} rows), planned "
         f"in {time.time() - t0:.1f}s")
@@ -2258,6 +2267,7 @@ def run_c5(args, torch, ctx, world=None) -> dict:
                                share_routes=args.posting_share_routes,
                                records=not args.no_rabitq_records)
     pipe.P, pipe.li = rq["P"], li
+    pipe.hash_mode = args.hash_mode
     types = wl.meta["query_types"]
     log(f"C5 routes: {pipe.ng} graph, {pipe.np_} label-posting scans ({pipe.post_rows_total} "
         f"rows), classes {dict(zip(pipe.class_names, pipe.classes))}, planned in "
