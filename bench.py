@@ -46,8 +46,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--n", type=int, default=10_000_000, help="base vectors (C2: 10M)")
-    ap.add_argument("--coarse-lists", type=int, default=1024,
-                    help="k-means centres that bucket the C2 graph builder's rows")
+    ap.add_argument("--coarse-lists", type=int, default=2048,
+                    help="k-means centres that bucket the C2 graph builder's rows (and give the "
+                         "coarse entries); at 24 local links: 1024 2.19M, 2048 2.27-2.29M, "
+                         "4096 2.07M QPS")
     ap.add_argument("--queries", type=int, default=100_000)
     ap.add_argument("--gt-queries", type=int, default=10_000,
                     help="C2 queries with exact ground truth (a seeded sample of the 100k)")
@@ -93,6 +95,9 @@ def parse():
                     help="C2 graphs: in-bucket nearest links per row of the 64 (0: half the "
                          "degree).  Measured at the beams the recall rule picks: 16 2.24M, "
                          "20 2.14M, 24 2.19M, 32 2.02M, 48 1.33M QPS")
+    ap.add_argument("--c2-near", type=int, default=2,
+                    help="C2 graphs: links per row to the representatives of the nearest "
+                         "other buckets")
     ap.add_argument("--c4-local", type=int, default=8,
                     help="in-bucket links per row of the C4 graphs (the rest are drawn)")
     ap.add_argument("--no-c4", action="store_true",
@@ -168,7 +173,7 @@ def build_world(args, torch):
     t_km = time.time() - t0
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
                               cen, degree=64, threshold=2000, progress=log,
-                              local=args.c2_local or None)
+                              local=args.c2_local or None, near=args.c2_near)
     t_g = time.time() - t0 - t_km
     log(f"label graphs: {int((li.label_size > 0).sum())} labels, {li.rows} rows, "
         f"degree 64, buckets from {args.coarse_lists} trained k-means centres "

@@ -362,7 +362,7 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
                       num_labels: int, centres: torch.Tensor, degree: int,
                       threshold: int = 2000, progress=None,
                       graph_seed: int = 6, local: int | None = None, design: str = "navigable",
-                      probe: int = 3, backend=None) -> LabelIndex:
+                      probe: int = 3, backend=None, near: int = 2) -> LabelIndex:
     """Label-partitioned graphs for labels with more than `threshold` rows,
     built on the GPU (`design` "navigable" or "cagra", see
     build_group_graph).  Rows are bucketed by their nearest trained centre;
@@ -405,7 +405,7 @@ def build_label_index(base: torch.Tensor, label_offsets: np.ndarray, label_value
         order, uniq, off, bucket_of = _bucket_order(cluster[samples])
         xs = be.take(xb, samples[order])
         graph[o:o + len(samples)], rep_cluster[l], rep_row[l] = build_group_graph(
-            be, xs, order, uniq, off, bucket_of, cen, degree, local=local,
+            be, xs, order, uniq, off, bucket_of, cen, degree, local=local, near=near,
             seed=graph_seed + int(l), entry=int(seed_local[l]), design=design, probe=probe)
         xs = None
     rep_off = np.zeros(num_labels + 1, dtype=np.int64)
