@@ -410,7 +410,10 @@ class ExactRoute:
         gs = pipe.gs
         self.pipe, self.gs = pipe, gs
         self.ls = gs.u32(li.label_size)
-        self.pv = pipe.dr_graph.predicate_view(pipe.dg, 0.0, False)
+        # the label slab of the PQ records (when built): a node's labels come
+        # with its adjacency row at pickup instead of a CSR read in the step
+        self.pv = pipe.dr_graph.predicate_view(pipe.dg, 0.0, False,
+                                               records=getattr(pipe, "records", None))
         self.rv = pipe.dr_graph.routes_view()
         # route_class: class index of every graph route; a tuple beam in
         # step() launches each class's routes (as a launch order) at its own

@@ -169,6 +169,24 @@ def test_exact_search_distance_paths(gpu_ctx, dim):
          _lib.PLACE_AUTO, False)
 
 
+@pytest.mark.parametrize("overflow", [0, 3])
+def test_exact_search_label_slab(gpu_ctx, eworld, overflow):
+    """The route predicate reading each node's labels from a 16-byte slab in
+    per-sample records (fetched with the adjacency row at pickup) in place
+    of the CSR: results identical to the oracle's; overflow 3 sends every
+    third row through the CSR."""
+    wl, li, rs = eworld
+    say("exact search label slab overflow", overflow)
+    rec = gs.SampleRecords.build(torch.zeros(wl.n, 16, dtype=torch.uint8), li.csr_offsets,
+                                 li.csr_labels, overflow_every=overflow)
+    pred_o = po.PredicateArrays.from_plan(rs.predicate, li)
+    for place, mode, Q in (("auto", 2, 48), ("spill-nsamp", 2, 96)):
+        hash_mode, nsamp = PLACE[place]
+        _run(gpu_ctx, wl, li, rs, pred_o,
+             lambda dr, dg: dr.predicate_view(dg, 0.0, False, records=rec), Q, 10, mode,
+             hash_mode, nsamp, finish=2)
+
+
 def _float_world(dim, seed, n=4000, nq=32):
     wl = synth.small_labelled(n=n, nq=nq, dim=dim, k=10, sigma=0.7, labels=5, seed=seed,
                               tags=True)
