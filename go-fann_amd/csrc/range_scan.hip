@@ -849,20 +849,70 @@ __device__ __forceinline__ bool short_clause_bits_match(const gofann_predicate_v
     return pass;
 }
 
+// What the tile loop and the flushes need of one route slot, read once per
+// pass into LDS (64 bytes): the route, its query's scale and k1, and its
+// predicate as a ShortClause (flags: bit 0 enabled, bit 1 simple, bits 2-3
+// label atoms, bits 4-5 range atoms).  Otherwise every tile re-reads them
+// through a chain of dependent global loads (slot -> route -> clause ->
+// handles and ranges).
+struct ShareSlot {
+    uint32_t route;
+    uint32_t query;
+    float scale;
+    float k1;
+    uint32_t flags;
+    uint32_t h[3];
+    gofann_range_atom r[2];
+};
+static_assert(sizeof(ShareSlot) == 64, "one 64-byte record per route slot");
+
+__device__ __forceinline__ ShareSlot share_slot(const gofann_predicate_view& v,
+                                                const RabitqScanScorer& sc, uint32_t route,
+                                                uint32_t query)
+{
+    ShareSlot o{};
+    o.route = route;
+    o.query = query;
+    o.scale = sc.q_scale[query];
+    o.k1 = sc.q_k1[query];
+    const bool enabled = pred_enabled(v, route);
+    const ShortClause c = enabled ? short_clause(v, route) : ShortClause{};
+    o.flags = (enabled ? 1u : 0u) | (c.simple ? 2u : 0u) | (static_cast<uint32_t>(c.nl) << 2) |
+              (static_cast<uint32_t>(c.nr) << 4);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) o.h[i] = c.h[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) o.r[i] = c.r[i];
+    return o;
+}
+
+__device__ __forceinline__ ShortClause slot_clause(const ShareSlot& s)
+{
+    ShortClause c;
+    c.simple = (s.flags & 2u) != 0;
+    c.nl = static_cast<int>((s.flags >> 2) & 3u);
+    c.nr = static_cast<int>((s.flags >> 4) & 3u);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) c.h[i] = s.h[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) c.r[i] = s.r[i];
+    return c;
+}
+
 // Scores the queued rows of route slot q (lane i < qn takes queue[i], a row
 // offset in the item) and merges the survivors into its shortlist by rank
 // (the lists hold k pairs per slot).  All 64 lanes of the wave call it.
 template <int V>
 __device__ __forceinline__ void share_flush(const ShareScanArgs& a, const RabitqScanScorer& sc,
-                                            uint32_t route, int q, const uint4* planes_all,
+                                            const ShareSlot& slot, int q, const uint4* planes_all,
                                             float* lst_d_all, uint32_t* lst_id_all,
                                             const uint32_t* queue, int qn, uint64_t begin,
                                             int lane)
 {
     const int k = a.k;
-    const uint32_t query = a.route_query[route];
-    const float scale = sc.q_scale[query];
-    const float k1 = sc.q_k1[query];
+    const uint32_t query = slot.query;
+    const float scale = slot.scale;
+    const float k1 = slot.k1;
     const float* g_row = sc.centroid_dists + static_cast<size_t>(query) * sc.num_anchors;
     const uint4* planes = planes_all + q * 8 * V;
     float* ld = lst_d_all + q * k;
@@ -932,7 +982,7 @@ __device__ __forceinline__ void share_flush(const ShareScanArgs& a, const Rabitq
 }
 
 template <int V>
-__global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareScanArgs a,
+__global__ __launch_bounds__(kScanThreads, (V <= 4 ? 4 : 3)) void label_share_scan_kernel(ShareScanArgs a,
                                                                         RabitqScanScorer sc)
 {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -942,6 +992,7 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
     __shared__ int s_nh;
     __shared__ int s_use_bits;
     __shared__ int s_qn[kShareRoutes];
+    __shared__ ShareSlot s_slot[kShareRoutes];
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -1002,8 +1053,10 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             if (lane == 0) {
                 s_pass[q] = 0;
                 s_qn[q] = 0;
+                s_slot[q] = share_slot(a.pred, sc, route, query);
             }
         }
+        __syncthreads();
         // Label bits: when every enabled route of the pass is a short clause
         // and their label handles number at most kShareHandles, each tile row
         // gets one bit per handle it holds (found once per row), and a
@@ -1014,9 +1067,8 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             int nh = 0;
             int use = 1;
             for (int q = 0; q < n_routes && use; ++q) {
-                const uint32_t route = a.seg_route[a.item_slots[first + q]];
-                if (!pred_enabled(a.pred, route)) continue;
-                const ShortClause c = short_clause(a.pred, route);
+                if (!(s_slot[q].flags & 1u)) continue;
+                const ShortClause c = slot_clause(s_slot[q]);
                 if (!c.simple) {
                     use = 0;
                     break;
@@ -1035,10 +1087,9 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                 }
             }
             for (int q = 0; q < n_routes && use; ++q) {
-                const uint32_t route = a.seg_route[a.item_slots[first + q]];
                 uint32_t need = 0;
-                if (pred_enabled(a.pred, route)) {
-                    const ShortClause c = short_clause(a.pred, route);
+                if (s_slot[q].flags & 1u) {
+                    const ShortClause c = slot_clause(s_slot[q]);
                     for (int i = 0; i < c.nl; ++i) {
                         int at = 0;
                         while (s_h[at] != c.h[i]) ++at;
@@ -1088,9 +1139,10 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             for (int i = 0; i < kShareRoutesPerWave; ++i) {
                 const int q = wave + i * (kScanThreads / kWave);
                 if (q >= n_routes) break;
-                const uint32_t route = a.seg_route[a.item_slots[first + q]];
-                const bool enabled = pred_enabled(a.pred, route);
-                const ShortClause sclause = enabled ? short_clause(a.pred, route) : ShortClause{};
+                const ShareSlot& slot = s_slot[q];
+                const uint32_t route = slot.route;
+                const bool enabled = (slot.flags & 1u) != 0;
+                const ShortClause sclause = slot_clause(slot);
                 const uint32_t need = use_bits ? s_need[q] : 0u;
                 uint32_t* queue = queue_all + q * kWave;
                 int qn = s_qn[q];  // queued rows of this slot (uniform), kept across tiles
@@ -1126,7 +1178,7 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
                     if (enabled) passes += static_cast<uint32_t>(c);
                     if (c == 0) continue;
                     if (qn + c > kWave) {
-                        share_flush<V>(a, sc, route, q, planes_all, lst_d_all, lst_id_all, queue,
+                        share_flush<V>(a, sc, slot, q, planes_all, lst_d_all, lst_id_all, queue,
                                        qn, begin, lane);
                         qn = 0;
                     }
@@ -1149,7 +1201,7 @@ __global__ __launch_bounds__(kScanThreads) void label_share_scan_kernel(ShareSca
             if (q >= n_routes) break;
             const int qn = s_qn[q];
             if (qn)
-                share_flush<V>(a, sc, a.seg_route[a.item_slots[first + q]], q, planes_all,
+                share_flush<V>(a, sc, s_slot[q], q, planes_all,
                                lst_d_all, lst_id_all, queue_all + q * kWave, qn, begin, lane);
         }
         __syncthreads();
