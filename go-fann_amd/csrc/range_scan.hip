@@ -724,7 +724,8 @@ constexpr int kShareTile = 512;           // rows per LDS tile
 constexpr int kShareRoutesPerWave = 4;
 constexpr int kShareRoutes = kShareRoutesPerWave * (kScanThreads / kWave);  // 16 per item
 constexpr int kShareMaxKp = 128;          // shortlist_k <= 128
-constexpr int kShareHandles = 32;         // label handles of one pass held as row bits
+constexpr int kShareHandles = 31;         // label handles of one pass held as row bits
+constexpr uint32_t kBitsOverflow = 1u << 31;  // the row's slab overflows: read the CSR
 
 struct ShareScanArgs {
     gofann_predicate_view pred;
@@ -1113,12 +1114,13 @@ __global__ __launch_bounds__(kScanThreads, (V <= 4 ? 4 : 3)) void label_share_sc
                 const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
                 t_ids[r] = a.posting[j];
                 const uint4 slab = a.pslab[j];
-                t_slab[r] = slab;
+                if (!use_bits) t_slab[r] = slab;
                 if (r0_tile) t_r0[r] = a.pranges[j];
                 if (use_bits) {
-                    uint32_t bits = 0;
+                    uint32_t bits = kBitsOverflow;
                     const uint32_t cnt = slab_count(slab);
                     if (cnt != kSlabOverflow) {
+                        bits = 0;
                         for (uint32_t e = 0; e < cnt; ++e) {
                             const uint32_t label = slab_label(slab, e);
                             int lo = 0, hi = nh;  // first handle >= label
@@ -1147,13 +1149,52 @@ __global__ __launch_bounds__(kScanThreads, (V <= 4 ? 4 : 3)) void label_share_sc
                 uint32_t* queue = queue_all + q * kWave;
                 int qn = s_qn[q];  // queued rows of this slot (uniform), kept across tiles
                 uint32_t passes = 0;
+                // Fast verdicts: label atoms as row bits and at most one range
+                // atom, on the column held in the tile -- a row's verdict is
+                // three LDS words and a few compares (rows whose slab
+                // overflows still take the CSR walk).  Same verdicts as
+                // short_clause_bits_match.
+                const bool fast = use_bits && enabled && sclause.simple &&
+                                  (sclause.nr == 0 || (sclause.nr == 1 && r0_tile));
+                const gofann_range_atom fat = sclause.r[0];
+                const bool fast_rng = sclause.nr != 0;
+                const bool fast_live = !fast_rng || (a.pred.base_ranges != nullptr &&
+                                                     fat.dimension < range_columns(a.pred));
+                const uint32_t fast_rows = a.base_rows < a.pred.rows ? a.base_rows : a.pred.rows;
                 for (int r0 = 0; r0 < n; r0 += kWave) {
                     const int r = r0 + lane;
                     bool ok = false;
-                    if (r < n) {
+                    if (fast) {
+                        if (r < n) {
+                            const uint32_t s = t_ids[r];
+                            const uint32_t bits = t_bits[r];
+                            if (!(bits & kBitsOverflow)) {
+                                ok = s < fast_rows && (bits & need) == need && fast_live &&
+                                     (!fast_rng ||
+                                      range_matches(fat.mode, fat.lower, fat.upper, t_r0[r]));
+                            } else if (s < a.base_rows) {
+                                PredCounters pc{0, 0};
+                                ok = pred_matches(a.pred, route, s, pc);
+                            }
+                        }
+                    } else if (r < n) {
                         const uint32_t s = t_ids[r];
                         ok = s < a.base_rows;
-                        if (ok && enabled) {
+                        if (ok && enabled && use_bits) {
+                            const uint32_t bits = t_bits[r];
+                            if (!(bits & kBitsOverflow)) {
+                                const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
+                                const float* prange = a.pranges && range_columns(a.pred) > 0
+                                                          ? a.pranges + j * range_columns(a.pred)
+                                                          : nullptr;
+                                const float rv = r0_tile ? t_r0[r] : 0.0f;
+                                ok = short_clause_bits_match(a.pred, sclause, s, bits, need, prange,
+                                                             rv);
+                            } else {
+                                PredCounters pc{0, 0};
+                                ok = pred_matches(a.pred, route, s, pc);
+                            }
+                        } else if (ok && enabled) {
                             const uint4 slab = t_slab[r];
                             if (slab_count(slab) != kSlabOverflow) {
                                 const uint64_t j = begin + t0 + static_cast<uint64_t>(r);
