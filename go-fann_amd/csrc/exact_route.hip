@@ -94,23 +94,12 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_MIN_WAVES 6
 #endif
 
-// Most registers per lane a register frontier may use (Q + 2 <= 64 x this).
-// 2 lets beams of 63..126 keep the frontier in registers; measured at
-// Q = 80 on 10M rows (degree 64) it is 3% slower than the LDS frontier,
-// because the larger register file pushes the visited table out of LDS,
-// so the default is 1.
-#ifndef GOFANN_EXACT_MAX_REGS
-#define GOFANN_EXACT_MAX_REGS 1
-#endif
-
-// 16-byte row chunks loaded per memory round trip in the any-dim row loop
-// of the LDS-frontier kernels.  At 6 waves, C2, Q = 80: three take 49.0 ms,
-// four 46.1, six 48.9, the whole row (twelve) 47.5.  The register-frontier
-// kernels take three: four spill 12 VGPRs there.
+// 16-byte row chunks loaded per memory round trip in the any-dim row loop.
+// At 6 waves, C2, Q = 80: three take 49.0 ms, four 46.1, six 48.9, the whole
+// row (twelve) 47.5.
 #ifndef GOFANN_EXACT_ROW_UNROLL
 #define GOFANN_EXACT_ROW_UNROLL 4
 #endif
-constexpr int kExactRegsRowUnroll = 3;
 
 // 128-byte blocks per quad whose loads are issued together in the float
 // kernels' row loop.
@@ -271,217 +260,6 @@ __device__ __forceinline__ bool best_insert(BestK& b, float d, uint32_t id, uint
     return true;
 }
 
-// ---------------------------------------------------------------------------
-// Register frontier (capacity Q + 2 <= 64 N): entry i lives in lane i % 64 of
-// register i / 64, so the array is the LDS heap's.  The heap code is the LDS
-// version's (include/smmh2.h:77-147) with every index wave-uniform: an entry
-// is read with v_readlane and written by the one lane that owns it, so each
-// heap step costs a few VALU/SALU instructions instead of a dependent LDS
-// round trip.  The array layout -- and with it every tie-break of pickup and
-// pop_max -- is the LDS heap's.
-// ---------------------------------------------------------------------------
-template <int N>
-struct RegHeap {
-    float first[N];
-    uint32_t second[N];
-    uint32_t sample[N];
-};
-
-template <int N>
-__device__ __forceinline__ void rh_init(RegHeap<N>& h)
-{
-#pragma unroll
-    for (int r = 0; r < N; ++r) {
-        h.first[r] = FLT_MAX;
-        h.second[r] = UINT32_MAX;
-        h.sample[r] = UINT32_MAX;
-    }
-}
-
-// Readers: the register index i / 64 is wave-uniform, so each is one
-// v_readlane of the owning register.
-template <int N>
-__device__ __forceinline__ float rh_first(const RegHeap<N>& h, int i)
-{
-    if (N == 1 || i < kWave)
-        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first[0]), i));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first[N - 1]), i - kWave));
-}
-
-template <int N>
-__device__ __forceinline__ Entry rh_get(const RegHeap<N>& h, int i)
-{
-    const int r = (N == 1 || i < kWave) ? 0 : N - 1;
-    const int l = i - r * kWave;
-    Entry e;
-    e.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first[r]), l));
-    e.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.second[r]), l));
-    e.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.sample[r]), l));
-    e.base = e.first;
-    return e;
-}
-
-template <int N>
-__device__ __forceinline__ void rh_set(RegHeap<N>& h, int i, const Entry& e, int lane)
-{
-#pragma unroll
-    for (int r = 0; r < N; ++r) {
-        const bool me = lane + r * kWave == i;
-        h.first[r] = me ? e.first : h.first[r];
-        h.second[r] = me ? e.second : h.second[r];
-        h.sample[r] = me ? e.sample : h.sample[r];
-    }
-}
-
-// Entry i moves to slot y (the hole).
-template <int N>
-__device__ __forceinline__ void rh_move(RegHeap<N>& h, int i, int y, int lane)
-{
-    rh_set(h, y, rh_get(h, i), lane);
-}
-
-// The sifts below keep the moving entry in scalar registers and shift each
-// entry it passes into the hole, writing the moving entry once at its final
-// slot.  Every comparison is the swap formulation's (smmh2.h:77-147), so the
-// array -- and with it every later tie-break -- is identical.
-template <int N>
-__device__ __forceinline__ void rh_insert(RegHeap<N>& h, int& size, const Entry& e, int lane)
-{
-    int y = size++;
-    for (;;) {
-        // sibling
-        if (y & 1) {
-            const int s = y + 1;
-            if (s < size && e.first > rh_first(h, s)) {
-                rh_move(h, s, y, lane);
-                y = s;
-            }
-        } else {
-            const int s = y - 1;
-            if (e.first < rh_first(h, s)) {
-                rh_move(h, s, y, lane);
-                y = s;
-            }
-        }
-        // grandparent
-        if (y <= 2) break;
-        const int g = (y - 3) >> 2;
-        const int gl = (g << 1) + 1;
-        const int gr = (g << 1) + 2;
-        if (rh_first(h, gl) > e.first) {
-            rh_move(h, gl, y, lane);
-            y = gl;
-        } else if (rh_first(h, gr) < e.first) {
-            rh_move(h, gr, y, lane);
-            y = gr;
-        } else {
-            break;
-        }
-    }
-    rh_set(h, y, e, lane);
-}
-
-template <int N>
-__device__ __forceinline__ void rh_pop_max(RegHeap<N>& h, int& size, int lane)
-{
-    --size;
-    Entry x = rh_get(h, size);  // the last entry refills the max slot
-    int y = 2;
-    for (;;) {
-        // sibling: a swap leaves x at the sibling for good and continues
-        // with the sibling's entry at y
-        if (y & 1) {
-            const int s = y + 1;
-            if (s < size && x.first > rh_first(h, s)) {
-                const Entry t = rh_get(h, s);
-                rh_set(h, s, x, lane);
-                x = t;
-            }
-        } else {
-            const int s = y - 1;
-            if (x.first < rh_first(h, s)) {
-                const Entry t = rh_get(h, s);
-                rh_set(h, s, x, lane);
-                x = t;
-            }
-        }
-        // grandchild
-        int c;
-        bool down;
-        if (y & 1) {
-            const int cl = (y << 1) + 1;
-            if (cl >= size) break;
-            const int cr = ((y + 1) << 1) + 1;
-            c = cl;
-            float fc = rh_first(h, cl);
-            if (cr < size) {
-                const float fr = rh_first(h, cr);
-                if (fr < fc) {
-                    c = cr;
-                    fc = fr;
-                }
-            }
-            down = fc < x.first;
-        } else {
-            const int cl = ((y - 1) << 1) + 2;
-            const int cr = (y << 1) + 2;
-            if (cl >= size) break;
-            c = cl;
-            float fc = rh_first(h, cl);
-            if (cr < size) {
-                const float fr = rh_first(h, cr);
-                if (fr > fc) {
-                    c = cr;
-                    fc = fr;
-                }
-            }
-            down = fc > x.first;
-        }
-        if (!down) break;
-        rh_move(h, c, y, lane);
-        y = c;
-    }
-    rh_set(h, y, x, lane);
-}
-
-// Unused entry of least `first`, lowest index on ties; marked used.  The
-// frontier's keys are exact squared distances (>= 0), whose float bits
-// order as unsigned integers: one unsigned minimum over every register,
-// then the lowest index holding it (register 0's lanes come first).
-template <int N>
-__device__ __forceinline__ bool rh_pickup(RegHeap<N>& h, int size, Entry& out, int lane)
-{
-    uint32_t key[N];
-    uint32_t m = UINT32_MAX;
-#pragma unroll
-    for (int r = 0; r < N; ++r) {
-        const int idx = lane + r * kWave;
-        const bool live = idx >= 1 && idx < size && !(h.second[r] & kPoolUsed);
-        key[r] = live ? __float_as_uint(h.first[r]) : UINT32_MAX;
-        m = key[r] < m ? key[r] : m;
-    }
-    const uint32_t mn = wave_min_u32(m);
-    if (mn == UINT32_MAX) {
-        // no live entry holds a key below the sentinel; an unused entry
-        // keyed UINT32_MAX cannot occur (keys are finite distances)
-        return false;
-    }
-    int best = -1;
-#pragma unroll
-    for (int r = 0; r < N; ++r) {
-        const int idx = lane + r * kWave;
-        const bool live = idx >= 1 && idx < size && !(h.second[r] & kPoolUsed);
-        const uint64_t at = ballot(live && key[r] == mn);
-        if (best < 0 && at != 0) best = __builtin_ctzll(at) + r * kWave;
-    }
-    if (best < 0) return false;
-    out = rh_get(h, best);
-#pragma unroll
-    for (int r = 0; r < N; ++r)
-        if (lane + r * kWave == best) h.second[r] |= kPoolUsed;
-    return true;
-}
-
 // Loads a picked node needs when it is expanded, issued at pickup: lane j's
 // adjacency entry j (and its sample id when the graph carries them), and the
 // node's label slab or CSR bounds (.x/.y) for the filter.
@@ -572,15 +350,14 @@ __device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t 
     return keep ? s_dist[rank] : FLT_MAX;
 }
 
-// kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  kRegs > 0:
-// the frontier lives in kRegs registers per lane (Q + 2 <= 64 kRegs), 0: in
-// LDS.  kElem: the element type of base and queries (GOFANN_ELEM_*); u8
-// rows are scored per lane (integer, exact in any order), f32 / f16 rows
-// by wave_float_dists.
-template <int kVisited, int kC, int kRegs, int kElem>
+// kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  The frontier
+// lives in LDS.  kElem: the element type of base and queries
+// (GOFANN_ELEM_*); u8 rows are scored per lane (integer, exact in any
+// order), f32 / f16 rows by wave_float_dists.
+template <int kVisited, int kC, int kElem>
 __global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAVES : 5)) void exact_route_kernel(ExactArgs a)
 {
-    constexpr int kRowUnroll = kRegs > 0 ? kExactRegsRowUnroll : GOFANN_EXACT_ROW_UNROLL;
+    constexpr int kRowUnroll = GOFANN_EXACT_ROW_UNROLL;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ uint32_t s_row[kMaxDegree];
     __shared__ uint32_t s_samp[kMaxDegree];
@@ -647,8 +424,6 @@ __global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAV
     bool done = false;
     const Entry sentinel = {FLT_MAX, UINT32_MAX, FLT_MAX, UINT32_MAX};
     Entry now = sentinel, next = sentinel;
-    RegHeap<(kRegs > 0 ? kRegs : 1)> rh;
-    rh_init(rh);
 
     // Seed (:1793-1850).
     if (gsize == 0 || seed == UINT32_MAX || seed >= gsize) {
@@ -668,12 +443,8 @@ __global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAV
                     static_cast<uint32_t>(lane) & 3u));
             }
             const Entry kp = {d0, seed, d0, s0};
-            if constexpr (kRegs > 0) {
-                rh_insert(rh, heap_size, kp, lane);
-            } else {
-                if (lane == 0) smmh_insert(frontier, heap_size, kp);
-                heap_size = bcast0(heap_size);
-            }
+            if (lane == 0) smmh_insert(frontier, heap_size, kp);
+            heap_size = bcast0(heap_size);
             if (lane == 0) (void)visited.add_serial(seed, 0);
             visited.count = 1;
             st.scored = 1;
@@ -684,12 +455,7 @@ __global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAV
     __threadfence_block();
     __syncthreads();
     if (!done) {
-        bool found;
-        if constexpr (kRegs > 0)
-            found = rh_pickup(rh, heap_size, now, lane);
-        else
-            found = pickup(frontier, heap_size, now, lane);
-        if (!found) done = true;
+        if (!pickup(frontier, heap_size, now, lane)) done = true;
     }
     if (done) st.exhausted = 1;
 
@@ -767,30 +533,11 @@ __global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAV
         // Drop what cannot enter a full frontier (its maximum only falls
         // during the step), then admit the rest in adjacency order.
         const bool full = heap_size > 2 && heap_size >= Q + 1;
-        float thr = 0.0f;
-        if (full) {
-            if constexpr (kRegs > 0)
-                thr = rh_first(rh, 2);
-            else
-                thr = frontier[2].first;
-        }
+        const float thr = full ? frontier[2].first : 0.0f;
         const bool cand = keep && !(full && thr < dist);
         const uint64_t cand_mask = ballot(cand);
         uint64_t adm = 0;  // admitted lanes
-        if constexpr (kRegs > 0) {
-            for (uint64_t m = cand_mask; m; m &= m - 1) {
-                const int j = __builtin_ctzll(m);
-                Entry kp;
-                kp.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dist), j));
-                kp.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(adj), j));
-                kp.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), j));
-                kp.base = kp.first;
-                if (heap_size > 2 && heap_size >= Q + 1 && rh_first(rh, 2) < kp.first) continue;
-                rh_insert(rh, heap_size, kp, lane);
-                adm |= 1ull << j;
-                if (heap_size >= Q + 2) rh_pop_max(rh, heap_size, lane);
-            }
-        } else if (Q + 2 <= kWaveHeapSlots) {
+        if (Q + 2 <= kWaveHeapSlots) {
             // the whole wave runs each heap operation (same array as the
             // lane-0 sifts below); hmax: the largest `first` in the heap
             float hmax = heap_size >= 3   ? frontier[2].first
@@ -856,12 +603,7 @@ __global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAV
         __syncthreads();
 
         // Pickup and early stop (:1985-2030).
-        bool found;
-        if constexpr (kRegs > 0)
-            found = rh_pickup(rh, heap_size, next, lane);
-        else
-            found = pickup(frontier, heap_size, next, lane);
-        if (!found) {
+        if (!pickup(frontier, heap_size, next, lane)) {
             st.exhausted = 1;
             break;
         }
@@ -910,11 +652,11 @@ namespace {
 
 inline uint32_t align16u(uint32_t x) { return (x + 15u) & ~15u; }
 
-template <int kVisited, int kC, int kRegs, int kElem>
+template <int kVisited, int kC, int kElem>
 int resident(Context* ctx, uint32_t lds)
 {
     if (lds > static_cast<uint32_t>(ctx->lds_per_block)) return 0;
-    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited, kC, kRegs, kElem>);
+    const void* k = reinterpret_cast<const void*>(exact_route_kernel<kVisited, kC, kElem>);
     if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
                             static_cast<int>(lds)) != hipSuccess) {
         (void)hipGetLastError();
@@ -935,14 +677,14 @@ int resident(Context* ctx, uint32_t lds)
 // launch.
 // fixed_slab: visited slabs for a placement outside LDS, holding at most
 // fixed_routes routes (the no-alloc entry point); nullptr: context scratch.
-template <int kC, int kRegs, int kElem>
+template <int kC, int kElem>
 int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
                  uint32_t lds_spill, uint32_t lds_glob, uint32_t count, uint32_t* fixed_slab,
                  uint32_t fixed_routes)
 {
-    const int rf = resident<kVisitedLds, kC, kRegs, kElem>(ctx, lds_full);
-    const int rs = resident<kVisitedSpill, kC, kRegs, kElem>(ctx, lds_spill);
-    const int rg = resident<kVisitedGlobal, kC, kRegs, kElem>(ctx, lds_glob);
+    const int rf = resident<kVisitedLds, kC, kElem>(ctx, lds_full);
+    const int rs = resident<kVisitedSpill, kC, kElem>(ctx, lds_spill);
+    const int rg = resident<kVisitedGlobal, kC, kElem>(ctx, lds_glob);
     int mode = kVisitedLds;
     int res = rf;
     if (hash_mode == GOFANN_PLACE_GLOBAL) {
@@ -980,13 +722,13 @@ int launch_exact(Context* ctx, ExactArgs& a, int hash_mode, uint32_t lds_full,
     const uint32_t lds = mode == kVisitedLds ? lds_full : (mode == kVisitedSpill ? lds_spill : lds_glob);
     const dim3 grid(count), block(kWave);
     if (mode == kVisitedLds)
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedLds, kC, kRegs, kElem>), grid, block, lds,
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedLds, kC, kElem>), grid, block, lds,
                            ctx->stream, a);
     else if (mode == kVisitedSpill)
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedSpill, kC, kRegs, kElem>), grid, block, lds,
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedSpill, kC, kElem>), grid, block, lds,
                            ctx->stream, a);
     else
-        hipLaunchKernelGGL((exact_route_kernel<kVisitedGlobal, kC, kRegs, kElem>), grid, block, lds,
+        hipLaunchKernelGGL((exact_route_kernel<kVisitedGlobal, kC, kElem>), grid, block, lds,
                            ctx->stream, a);
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("exact route launch");
     ctx->last_table_in_lds = 0;
@@ -1007,23 +749,21 @@ struct LaunchShape {
 };
 
 // Row length fixed at compile time only in builds that ask for it (u8).
-template <int kRegs, int kElem>
+template <int kElem>
 int launch_rows(const LaunchShape& s, int chunks)
 {
 #if GOFANN_EXACT_FIXED_ROWS
     if constexpr (kElem == GOFANN_ELEM_U8) {
         switch (chunks) {
         case 8:
-            return launch_exact<8, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
-                                                 s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
+            return launch_exact<8, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                          s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
         case 12:
-            return launch_exact<12, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full,
-                                                  s.lds_spill, s.lds_glob, s.count, s.fixed_slab,
-                                                  s.fixed_routes);
+            return launch_exact<12, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                           s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
         case 16:
-            return launch_exact<16, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full,
-                                                  s.lds_spill, s.lds_glob, s.count, s.fixed_slab,
-                                                  s.fixed_routes);
+            return launch_exact<16, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                           s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
         default:
             break;
         }
@@ -1031,20 +771,8 @@ int launch_rows(const LaunchShape& s, int chunks)
 #else
     (void)chunks;
 #endif
-    return launch_exact<0, kRegs, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
-                                         s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
-}
-
-template <int kElem>
-int launch_regs(const LaunchShape& s, int regs, int chunks)
-{
-    switch (regs) {
-    case 1: return launch_rows<1, kElem>(s, chunks);
-#if GOFANN_EXACT_MAX_REGS >= 2
-    case 2: return launch_rows<2, kElem>(s, chunks);
-#endif
-    default: return launch_rows<0, kElem>(s, chunks);
-    }
+    return launch_exact<0, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill, s.lds_glob,
+                                  s.count, s.fixed_slab, s.fixed_routes);
 }
 
 static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint32_t dim,
@@ -1091,17 +819,16 @@ static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint
     a.out_ids = out_ids;
     a.out_dists = out_dists;
     a.stats = stats;
-    // LDS: the query row, then (LDS frontier only) Q + 2 entries, then the
-    // visited table of the chosen placement.  Beams with Q + 2 <= 128 keep
-    // the frontier in one or two registers per lane.
-    const int regs = p->queue_limit + 2 <= kWave
-                         ? 1
-                         : (GOFANN_EXACT_MAX_REGS >= 2 && p->queue_limit + 2 <= 2 * kWave ? 2 : 0);
+    // LDS: the query row, then Q + 2 frontier entries, then the visited
+    // table of the chosen placement.  (A frontier held in registers, lane i
+    // holding entry i, was slower at every beam measured: C2 43.4 against
+    // 41.0 ms a step at Q = 56 / 88, 26.6 against 25.8 at 32 / 88 -- the
+    // wave-parallel LDS heap operations below issue fewer instructions
+    // than its serial register sifts.)
     a.off_frontier = base_elem == GOFANN_ELEM_U8 ? align16u((dim + 15u) / 16u * 16u)
                                                  : align16u(dim * 4u);
-    a.off_hash = regs ? a.off_frontier
-                      : align16u(a.off_frontier + static_cast<uint32_t>(p->queue_limit + 2) *
-                                                      sizeof(Entry));
+    a.off_hash = align16u(a.off_frontier + static_cast<uint32_t>(p->queue_limit + 2) *
+                                               sizeof(Entry));
     const uint32_t lds_full = a.off_hash + kHashCapacity * 4u;
     const uint32_t lds_spill = a.off_hash + kSpillSlots * 4u;
     const uint32_t lds_glob = a.off_hash;
@@ -1111,9 +838,9 @@ static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint
     const LaunchShape sh{ctx, &a, p->hash_mode, lds_full, lds_spill, lds_glob, r->count,
                          fixed_slab, fixed_routes};
     switch (base_elem) {
-    case GOFANN_ELEM_F32: return launch_regs<GOFANN_ELEM_F32>(sh, regs, 0);
-    case GOFANN_ELEM_F16: return launch_regs<GOFANN_ELEM_F16>(sh, regs, 0);
-    default: return launch_regs<GOFANN_ELEM_U8>(sh, regs, chunks);
+    case GOFANN_ELEM_F32: return launch_rows<GOFANN_ELEM_F32>(sh, 0);
+    case GOFANN_ELEM_F16: return launch_rows<GOFANN_ELEM_F16>(sh, 0);
+    default: return launch_rows<GOFANN_ELEM_U8>(sh, chunks);
     }
 }
 

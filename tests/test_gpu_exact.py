@@ -95,8 +95,9 @@ PLACE = {"auto": (_lib.PLACE_AUTO, False), "lds-nsamp": (_lib.PLACE_LDS, True),
 
 
 @pytest.mark.parametrize("place", list(PLACE))
-# Q + 2 <= 64 keeps the frontier in registers, larger beams in LDS; past
-# 512 slots (Q = 600) admission takes the serial lane-0 sifts.
+# Beams up to 510 admit through the wave-parallel heap operations on the
+# LDS frontier; past 512 slots (Q = 600) admission takes the serial lane-0
+# sifts.
 @pytest.mark.parametrize("mode,Q", [(2, 32), (0, 62), (2, 64), (2, 80), (1, 128), (2, 300),
                                     (2, 600)])
 @pytest.mark.parametrize("with_pred", [False, True])
