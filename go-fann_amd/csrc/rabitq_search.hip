@@ -92,20 +92,17 @@ int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabit
     const uint32_t plane_bytes = rq->padded_dim + kRabitqCoopBytes;
     const Layout l = make_layout(plane_bytes, p->queue_limit, p->result_width);
     ctx->last_table_in_lds = 1;
-    // Beams with Q + 2 <= 64 keep the frontier in registers (lane i holds
-    // entry i); larger ones in LDS.
-    if (p->queue_limit + 2 <= kWave) {
-        const Placement pl = choose_visited<RabitqScorer, true>(ctx, l, p->hash_mode);
-        return launch_traversal<RabitqScorer, true>(ctx, make_rabitq_scorer(rq, pre), l, pl, g,
-                                                    pred, r, p, out_ids, out_dists, stats, 1);
-    }
+    // Every beam keeps its frontier in LDS.  (A frontier held in registers
+    // for Q + 2 <= 64, lane i holding entry i, was slower than the
+    // wave-parallel LDS heap operations: C3 traversal 47.8 against 46.9 ms,
+    // C5 at Q = 16 1.42 against 1.36 ms.)
     // Degree <= 32: two routes per wave (rabitq_pair.hip), same results.
     if (rabitq_pair_eligible(rq, g, p))
         return rabitq_pair_search(ctx, make_rabitq_scorer(rq, pre), g, pred, r, p, out_ids,
                                   out_dists, stats);
-    const Placement pl = choose_visited<RabitqScorer, false>(ctx, l, p->hash_mode);
-    return launch_traversal<RabitqScorer, false>(ctx, make_rabitq_scorer(rq, pre), l, pl, g, pred,
-                                                 r, p, out_ids, out_dists, stats, 1);
+    const Placement pl = choose_visited<RabitqScorer>(ctx, l, p->hash_mode);
+    return launch_traversal<RabitqScorer>(ctx, make_rabitq_scorer(rq, pre), l, pl, g, pred, r, p,
+                                          out_ids, out_dists, stats, 1);
 }
 
 int rabitq_score(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre,

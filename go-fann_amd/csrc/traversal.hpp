@@ -478,172 +478,6 @@ struct RabitqScorer {
     __device__ float exact_from(uint32_t, int, const ExactWords&) const { return 0.0f; }
 };
 
-// ---------------------------------------------------------------------------
-// Frontier in registers for beams with Q + 2 <= 64: lane i holds smmh2 entry
-// i (the array layout of the LDS heap), read with v_readlane and written with
-// a lane select, so the serial admission runs at register speed instead of
-// waiting on a chain of LDS round trips.  Sifts keep the moving entry in
-// scalar registers and shift the entries it passes into the hole; every
-// comparison is the swap formulation's (smmh2.h:77-147), so the layout and
-// every later tie-break are the LDS heap's.
-// ---------------------------------------------------------------------------
-struct RegFrontier {
-    float first;
-    uint32_t second;
-    float base;
-    uint32_t sample;
-};
-
-__device__ __forceinline__ float rf_first(const RegFrontier& h, int i)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.first), i));
-}
-
-__device__ __forceinline__ Entry rf_get(const RegFrontier& h, int i)
-{
-    Entry e;
-    e.first = rf_first(h, i);
-    e.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.second), i));
-    e.base = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(h.base), i));
-    e.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(h.sample), i));
-    return e;
-}
-
-__device__ __forceinline__ void rf_set(RegFrontier& h, int i, const Entry& e, int lane)
-{
-    const bool me = lane == i;
-    h.first = me ? e.first : h.first;
-    h.second = me ? e.second : h.second;
-    h.base = me ? e.base : h.base;
-    h.sample = me ? e.sample : h.sample;
-}
-
-__device__ __forceinline__ void rf_insert(RegFrontier& h, int& size, const Entry& e, int lane)
-{
-    int y = size++;
-    for (;;) {
-        if (y & 1) {
-            const int s = y + 1;
-            if (s < size && e.first > rf_first(h, s)) {
-                rf_set(h, y, rf_get(h, s), lane);
-                y = s;
-            }
-        } else {
-            const int s = y - 1;
-            if (e.first < rf_first(h, s)) {
-                rf_set(h, y, rf_get(h, s), lane);
-                y = s;
-            }
-        }
-        if (y <= 2) break;
-        const int g = (y - 3) >> 2;
-        const int gl = (g << 1) + 1;
-        const int gr = (g << 1) + 2;
-        if (rf_first(h, gl) > e.first) {
-            rf_set(h, y, rf_get(h, gl), lane);
-            y = gl;
-        } else if (rf_first(h, gr) < e.first) {
-            rf_set(h, y, rf_get(h, gr), lane);
-            y = gr;
-        } else {
-            break;
-        }
-    }
-    rf_set(h, y, e, lane);
-}
-
-__device__ __forceinline__ void rf_pop_max(RegFrontier& h, int& size, int lane)
-{
-    --size;
-    Entry x = rf_get(h, size);
-    int y = 2;
-    for (;;) {
-        if (y & 1) {
-            const int s = y + 1;
-            if (s < size && x.first > rf_first(h, s)) {
-                const Entry t = rf_get(h, s);
-                rf_set(h, s, x, lane);
-                x = t;
-            }
-        } else {
-            const int s = y - 1;
-            if (x.first < rf_first(h, s)) {
-                const Entry t = rf_get(h, s);
-                rf_set(h, s, x, lane);
-                x = t;
-            }
-        }
-        int c;
-        bool down;
-        if (y & 1) {
-            const int cl = (y << 1) + 1;
-            if (cl >= size) break;
-            const int cr = ((y + 1) << 1) + 1;
-            c = cl;
-            float fc = rf_first(h, cl);
-            if (cr < size) {
-                const float fr = rf_first(h, cr);
-                if (fr < fc) {
-                    c = cr;
-                    fc = fr;
-                }
-            }
-            down = fc < x.first;
-        } else {
-            const int cl = ((y - 1) << 1) + 2;
-            const int cr = (y << 1) + 2;
-            if (cl >= size) break;
-            c = cl;
-            float fc = rf_first(h, cl);
-            if (cr < size) {
-                const float fr = rf_first(h, cr);
-                if (fr > fc) {
-                    c = cr;
-                    fc = fr;
-                }
-            }
-            down = fc > x.first;
-        }
-        if (!down) break;
-        rf_set(h, y, rf_get(h, c), lane);
-        y = c;
-    }
-    rf_set(h, y, x, lane);
-}
-
-// Float -> unsigned key of the same order (-0 folded onto +0, which compare
-// equal as floats).
-__device__ __forceinline__ uint32_t order_key(float f)
-{
-    const uint32_t b = __float_as_uint(f == 0.0f ? 0.0f : f);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-// pickup over the register frontier: the unused entry of least `first`,
-// lowest index on ties, marked used.
-__device__ __forceinline__ bool rf_pickup(RegFrontier& h, int size, Entry& out, int lane)
-{
-    const bool live = lane >= 1 && lane < size && !(h.second & kPoolUsed);
-    const uint32_t key = live ? order_key(h.first) : UINT32_MAX;
-    const uint32_t mn = wave_min_u32(key);
-    const uint64_t at = ballot(live && key == mn);
-    if (at == 0) return false;
-    const int best = __builtin_ctzll(at);
-    out = rf_get(h, best);
-    if (lane == best) h.second |= kPoolUsed;
-    return true;
-}
-
-__device__ __forceinline__ float rf_min_pending_base(const RegFrontier& h, int size,
-                                                     const Entry& now, const Entry& next, int lane)
-{
-    const bool live = lane >= 1 && lane < size && !(h.second & kPoolUsed);
-    float m = wave_min(live ? h.base : FLT_MAX);
-    m = fminf(m, now.base);
-    m = fminf(m, next.base);
-    return m;
-}
-
 struct TraversalArgs {
     gofann_graph_view graph;
     gofann_predicate_view pred;
@@ -692,7 +526,7 @@ __device__ __forceinline__ void load_node(const TraversalArgs& a, const Scorer& 
     }
 }
 
-template <class Scorer, int kVisited, bool kReg = false>
+template <class Scorer, int kVisited>
 __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kernel(TraversalArgs a, Scorer sc)
 {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -760,19 +594,12 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
     int passed = 0;
     float stop_worst = -FLT_MAX;
     const Entry sentinel = {FLT_MAX, UINT32_MAX, FLT_MAX, UINT32_MAX};
-    RegFrontier rf{FLT_MAX, UINT32_MAX, FLT_MAX, UINT32_MAX};  // kReg only
-    if constexpr (kReg) {
+    if (lane == 0) {
         const Entry kp = {start, begin_id, start, begin_sample};
-        rf_insert(rf, heap_size, kp, lane);
-        if (lane == 0) (void)visited.add_serial(begin_id, 0);
-    } else {
-        if (lane == 0) {
-            const Entry kp = {start, begin_id, start, begin_sample};
-            smmh_insert(frontier, heap_size, kp);
-            (void)visited.add_serial(begin_id, 0);
-        }
-        heap_size = bcast0(heap_size);
+        smmh_insert(frontier, heap_size, kp);
+        (void)visited.add_serial(begin_id, 0);
     }
+    heap_size = bcast0(heap_size);
     visited.count = 1;
     __threadfence_block();
     __syncthreads();
@@ -780,12 +607,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
     Entry now = sentinel;
     Entry next = sentinel;
     NodeLoads cur, nxt;
-    bool first_found;
-    if constexpr (kReg)
-        first_found = rf_pickup(rf, heap_size, now, lane);
-    else
-        first_found = pickup(frontier, heap_size, now, lane);
-    if (!first_found) {
+    if (!pickup(frontier, heap_size, now, lane)) {
         exhausted = 1;
         now = sentinel;
     } else {
@@ -810,10 +632,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
             // pickup finds it in the same pass
             const bool want_base = stop_size == SW && a.pred.pending_base_stop && enabled;
             float unused_base = FLT_MAX;
-            if constexpr (kReg)
-                found = rf_pickup(rf, heap_size, next, lane);
-            else
-                found = pickup(frontier, heap_size, next, lane, want_base, unused_base);
+            found = pickup(frontier, heap_size, next, lane, want_base, unused_base);
             if (!found) {
                 exhausted = 1;
                 next = sentinel;
@@ -821,12 +640,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
                 load_node(a, sc, label_offset, degree, next, enabled, exact, lane, nxt);
                 if (stop_size == SW) {
                     float pending = next.first;
-                    if (want_base) {
-                        if constexpr (kReg)
-                            pending = rf_min_pending_base(rf, heap_size, now, next, lane);
-                        else
-                            pending = fminf(unused_base, now.base);
-                    }
+                    if (want_base) pending = fminf(unused_base, now.base);
                     if (mode != GOFANN_EARLY_STOP_OFF && stop_worst <= pending) ++finished;
                 }
             }
@@ -975,13 +789,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
         // loop skips any candidate above frontier[2]; that maximum can only
         // fall during the step, so such candidates are dropped here.
         const bool full = heap_size >= Q + 1;
-        float thr = 0.0f;
-        if (full) {
-            if constexpr (kReg)
-                thr = rf_first(rf, 2);
-            else
-                thr = frontier[2].first;
-        }
+        const float thr = full ? frontier[2].first : 0.0f;
         const bool cand = keep && !(full && thr < first);
         const uint64_t cand_mask = ballot(cand);
         // Ordered admission (backend_pq.cu:4889-4907); the visited-set adds
@@ -989,23 +797,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
         // lane's candidate was admitted.
         bool mine;
         uint64_t adm_lanes;  // admitted lanes, in adjacency order
-        if constexpr (kReg) {
-            adm_lanes = 0;
-            for (uint64_t m = cand_mask; m; m &= m - 1) {
-                const int j = __builtin_ctzll(m);
-                Entry kp;
-                kp.first = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(first), j));
-                kp.second = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(idx), j));
-                kp.base = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(base), j));
-                kp.sample = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(my_sample), j));
-                if (heap_size >= Q + 1 && rf_first(rf, 2) < kp.first) continue;
-                rf_insert(rf, heap_size, kp, lane);
-                adm_lanes |= 1ull << j;
-                ++admitted;
-                if (heap_size >= Q + 2) rf_pop_max(rf, heap_size, lane);
-            }
-            mine = (adm_lanes >> lane) & 1ull;
-        } else if (Q + 2 <= kWaveHeapSlots) {
+        if (Q + 2 <= kWaveHeapSlots) {
             // the whole wave runs each insert / pop_max on the LDS frontier;
             // hmax: the largest `first` in it (frontier[2] once full)
             adm_lanes = 0;
@@ -1075,12 +867,7 @@ __global__ __launch_bounds__(64, GOFANN_TRAVERSAL_MIN_WAVES) void traversal_kern
         __syncthreads();
 
         if (step == 1) {
-            bool found;
-            if constexpr (kReg)
-                found = rf_pickup(rf, heap_size, next, lane);
-            else
-                found = pickup(frontier, heap_size, next, lane);
-            if (!found) {
+            if (!pickup(frontier, heap_size, next, lane)) {
                 exhausted = 1;
                 next = sentinel;
             } else {
@@ -1205,21 +992,20 @@ struct Placement {
     int resident;
 };
 
-// Visited-set placement for one scorer configuration (kReg: register
-// frontier).  hash_mode picks it; auto takes the most resident routes per
+// Visited-set placement for one scorer configuration.  hash_mode picks it; auto takes the most resident routes per
 // CU, preferring LDS storage on ties (full table, then the spilling table,
 // then the global slab).
-template <class Scorer, bool kReg = false>
+template <class Scorer>
 Placement choose_visited(Context* ctx, const Layout& l, int hash_mode)
 {
     const Placement full{kVisitedLds, l.bytes(kVisitedLds),
-                         resident_per_cu(ctx, traversal_kernel<Scorer, kVisitedLds, kReg>,
+                         resident_per_cu(ctx, traversal_kernel<Scorer, kVisitedLds>,
                                          l.bytes(kVisitedLds))};
     const Placement spill{kVisitedSpill, l.bytes(kVisitedSpill),
-                          resident_per_cu(ctx, traversal_kernel<Scorer, kVisitedSpill, kReg>,
+                          resident_per_cu(ctx, traversal_kernel<Scorer, kVisitedSpill>,
                                           l.bytes(kVisitedSpill))};
     const Placement glob{kVisitedGlobal, l.bytes(kVisitedGlobal),
-                         resident_per_cu(ctx, traversal_kernel<Scorer, kVisitedGlobal, kReg>,
+                         resident_per_cu(ctx, traversal_kernel<Scorer, kVisitedGlobal>,
                                          l.bytes(kVisitedGlobal))};
     if (hash_mode == GOFANN_PLACE_LDS) return full;
     if (hash_mode == GOFANN_PLACE_GLOBAL) return glob;
@@ -1230,7 +1016,7 @@ Placement choose_visited(Context* ctx, const Layout& l, int hash_mode)
     return best;
 }
 
-template <class Scorer, bool kReg = false>
+template <class Scorer>
 int launch_traversal(Context* ctx, const Scorer& sc, const Layout& l, const Placement& pl,
                      const gofann_graph_view* g, const gofann_predicate_view* pred,
                      const gofann_routes* r, const gofann_search_params* p, uint32_t* out_ids,
@@ -1259,13 +1045,13 @@ int launch_traversal(Context* ctx, const Scorer& sc, const Layout& l, const Plac
     }
     const dim3 grid(r->count), block(kWave);
     if (pl.visited == kVisitedLds) {
-        hipLaunchKernelGGL((traversal_kernel<Scorer, kVisitedLds, kReg>), grid, block, pl.lds,
+        hipLaunchKernelGGL((traversal_kernel<Scorer, kVisitedLds>), grid, block, pl.lds,
                            ctx->stream, a, sc);
     } else if (pl.visited == kVisitedSpill) {
-        hipLaunchKernelGGL((traversal_kernel<Scorer, kVisitedSpill, kReg>), grid, block, pl.lds,
+        hipLaunchKernelGGL((traversal_kernel<Scorer, kVisitedSpill>), grid, block, pl.lds,
                            ctx->stream, a, sc);
     } else {
-        hipLaunchKernelGGL((traversal_kernel<Scorer, kVisitedGlobal, kReg>), grid, block, pl.lds,
+        hipLaunchKernelGGL((traversal_kernel<Scorer, kVisitedGlobal>), grid, block, pl.lds,
                            ctx->stream, a, sc);
     }
     if (hipGetLastError() != hipSuccess) return ctx->fail_hip("traversal launch");

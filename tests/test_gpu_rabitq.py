@@ -145,8 +145,8 @@ def test_rabitq_score_ip_exact(gpu_ctx, rworld, P):
         assert np.float32(d[i].item()) == np.float32(want)
 
 
-# Q = 16 (C4's beam) and 40 keep the frontier in registers (Q + 2 <= 64),
-# Q = 96 in LDS; P = 512 is C4's 64-byte code.
+# Q = 16, 40 and 96 (small and mid beams on the LDS frontier's wave-parallel
+# heap operations); P = 512 is C4's 64-byte code.
 @pytest.mark.parametrize("Q", [16, 40, 96])
 @pytest.mark.parametrize("P", [128, 512, 2048, 4096])
 @pytest.mark.parametrize("bias", [True, False])
