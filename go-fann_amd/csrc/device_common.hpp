@@ -1015,38 +1015,51 @@ __device__ __forceinline__ int wave_sum(int v)
 }
 
 // Frontier pickup (wave-cooperative).
+// Float -> unsigned key of the same order (-0 folded onto +0, which compare
+// equal as floats), and back.  Frontier keys are distances or priorities of
+// finite vectors; a NaN would order above +inf.
+__device__ __forceinline__ uint32_t order_key(float f)
+{
+    const uint32_t b = __float_as_uint(f == 0.0f ? 0.0f : f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float order_key_float(uint32_t k)
+{
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
 // pickup_next_unused_from_native_frontier (backend_pq.cu:844-892): unused
 // entry of least `first`, lowest index on ties; lane 0 marks it used.
-// With `want_base`, the same pass also returns in `min_base` the least
-// `base` over the entries that were unused before the pickup (the picked one
-// included).
+// Each lane scans slots lane + 1, lane + 65, ... in ascending order and
+// keeps its first slot at its least key; then one unsigned wave minimum of
+// the keys and one of the slots holding it (DPP row steps, no LDS
+// permutes).  With `want_base`, the same pass also returns in `min_base`
+// the least `base` over the entries that were unused before the pickup
+// (the picked one included).
 __device__ __forceinline__ bool pickup(Entry* f, int size, Entry& out, int lane,
                                        bool want_base, float& min_base)
 {
-    int best = -1;
-    float bv = 0.0f;
-    float mb = FLT_MAX;
+    uint32_t bk = UINT32_MAX;
+    uint32_t bi = UINT32_MAX;
+    uint32_t mb = UINT32_MAX;
     for (int i = lane + 1; i < size; i += kWave) {
         const Entry e = f[i];
         if (e.second & kPoolUsed) continue;
-        if (want_base) mb = fminf(mb, e.base);
-        if (best < 0 || e.first < bv) {
-            best = i;
-            bv = e.first;
+        if (want_base) mb = min(mb, order_key(e.base));
+        const uint32_t k = order_key(e.first);
+        if (k < bk) {
+            bk = k;
+            bi = static_cast<uint32_t>(i);
         }
     }
-    if (want_base) min_base = wave_min(mb);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const int ob = __shfl_xor(best, off, kWave);
-        const float ov = __shfl_xor(bv, off, kWave);
-        if (ob >= 0 && (best < 0 || ov < bv || (!(bv < ov) && ob < best))) {
-            best = ob;
-            bv = ov;
-        }
+    if (want_base) {
+        const uint32_t m = wave_min_u32(mb);
+        min_base = m == UINT32_MAX ? FLT_MAX : order_key_float(m);
     }
-    best = bcast0(best);
-    if (best < 0) return false;
+    const uint32_t mn = wave_min_u32(bk);
+    if (mn == UINT32_MAX) return false;
+    const int best = static_cast<int>(wave_min_u32(bk == mn ? bi : UINT32_MAX));
     out = f[best];
     __syncthreads();
     if (lane == 0) f[best].second |= kPoolUsed;
