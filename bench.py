@@ -519,9 +519,6 @@ def exact_route_bytes(st: np.ndarray, degree: int, dim: int, neighbor_samples: b
 
 PEAK_FP32_MFMA_TFLOPS = 157.3
 
-# Per-class beams (1 tag, 2 tags) of the C2 exact-route launch that
-# profiles/exact_route_c2_traffic.md measured.
-C2_TRAFFIC_BEAMS = (80, 80)
 
 
 def rabitq_prep_leg(ctx, torch, nq=10_000, dim=4096, anchors=512, reps=3):
@@ -592,16 +589,29 @@ def algorithmic_bytes(st: np.ndarray, degree: int, code_bytes: int, exact_bytes:
     return E * adj + V * code + rows * 8 + labels * 4 + Pn * exact_bytes
 
 
-def measured_traffic(profile: str, match: bool):
-    """HBM bytes per launch from a committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    summary under profiles/ (its `bytes_per_launch:` line), when this run's
-    configuration is the one that summary measured (`match`); else None."""
-    path = ROOT / "profiles" / profile
-    if not match or not path.exists():
+TRAFFIC_PROFILE = "bench_kernels_traffic.md"
+
+
+def measured_traffic(leg: str, kernel: str, beams, algorithmic: float):
+    """HBM bytes per launch of `kernel` in bench leg `leg`, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/ (its
+    `traffic:` lines), when that summary measured the same beams and the
+    same algorithmic bytes (within 1%: the same index, routes and walk);
+    else None."""
+    path = ROOT / "profiles" / TRAFFIC_PROFILE
+    if not path.exists():
         return None
+    want = ",".join(str(int(b)) for b in (beams if isinstance(beams, (list, tuple)) else [beams]))
     for line in path.read_text().splitlines():
-        if line.strip().startswith("bytes_per_launch:"):
-            return float(line.split(":")[1])
+        line = line.strip()
+        if not line.startswith("traffic:"):
+            continue
+        f = dict(kv.split("=", 1) for kv in (x.strip() for x in line[8:].split(";")) if "=" in kv)
+        if f.get("leg") != leg or f.get("kernel") != kernel or f.get("beams") != want:
+            continue
+        alg = float(f.get("algorithmic", "0"))
+        if alg > 0 and abs(alg - float(algorithmic)) <= 0.01 * alg:
+            return float(f["bytes"])
     return None
 
 
@@ -643,7 +653,12 @@ def _compact_rabitq_leg(leg):
         return None
     out = _pick(leg, ("qps", "ms_per_step", "queue_by_class", "recall_at_10", "recall_by_class",
                       "gt_by_class", "expansions_per_route"))
-    out["kernels_ms_gbps"] = {_kernel_alias(k): [v["ms"], v.get("achieved_gbps")]
+    # per kernel: ms, algorithmic GB/s, HBM bytes over algorithmic bytes
+    # (counter traffic, when measured for this configuration)
+    out["kernels_ms_gbps"] = {_kernel_alias(k): [v["ms"], v.get("achieved_gbps"),
+                                                 round(v["traffic"] / v["algorithmic_bytes"], 2)
+                                                 if v.get("traffic") and v.get("algorithmic_bytes")
+                                                 else None]
                               for k, v in (leg.get("kernels") or {}).items()}
     r = leg.get("roofline") or {}
     out["roofline"] = _pick(r, ("kernel", "frac", "traffic"))
@@ -669,7 +684,8 @@ def compact_record(line: dict) -> dict:
         if r:
             cc[key] = dict(_pick(r, ("qps", "queue", "recall_at_10", "kernel_ms",
                                      "steps_per_route", "scored_per_route")),
-                           frac=(r.get("roofline") or {}).get("frac"))
+                           frac=(r.get("roofline") or {}).get("frac"),
+                           traffic=(r.get("roofline") or {}).get("traffic"))
     cc["gpu_cpu_rerank_route"] = _pick(c.get("gpu_cpu_rerank_route"),
                                        ("qps", "queue", "shortlist", "recall_at_10"))
     cc["rabitq_query_prep"] = _pick(c.get("rabitq_query_prep"),
@@ -1996,6 +2012,7 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
     kern = kernels(pipe, kst, st)
     per = {k: {"ms": v[0], "algorithmic_bytes": v[1],
                "achieved_gbps": round(v[1] / (v[0] / 1000.0) / 1e9, 2) if v[0] > 0 else None,
+               "traffic": measured_traffic(label, k, chosen, v[1]),
                **(v[2] if len(v) > 2 else {})}
            for k, v in kern.items()}
     top = max(kern, key=lambda k: kern[k][0])
@@ -2009,8 +2026,8 @@ def rabitq_leg(args, pipe, class_gt, ladder, label, kernels):
             "expansions_per_route": round(float(E.mean()), 1), "stage_ms": st_ms,
             "kernel_stage_ms": kst, "kernels": per, "placement": pipe.ctx.last_placement(),
             "roofline": {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_HBM_GBPS,
-                         "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5), "traffic": None,
-                         "kernel": top, "kernel_ms": kern[top][0],
+                         "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 5),
+                         "traffic": per[top]["traffic"], "kernel": top, "kernel_ms": kern[top][0],
                          "algorithmic_bytes": kern[top][1]}}
 
 
@@ -2544,7 +2561,7 @@ def main():
                "roofline": {"bound": "hbm", "achieved": round(ach3, 2),
                             "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                             "frac": round(ach3 / PEAK_HBM_GBPS, 5),
-                            "traffic": None,
+                            "traffic": measured_traffic(label, "exact_route_kernel", q3, b3),
                             "kernel": "exact_route_kernel", "kernel_ms": round(kms3, 3),
                             "algorithmic_bytes": b3}}
         log(f"{label}: {res}")
@@ -2558,10 +2575,6 @@ def main():
                           dtype=np.int64)
         route3 = exact_leg(ExactRoute(pipe, li, route_class=rclass), ladder3,
                            "exact route (medoid seeds)")
-        route3["roofline"]["traffic"] = measured_traffic(
-            "exact_route_c2_traffic.md",
-            tuple(route3["queue"].values()) == C2_TRAFFIC_BEAMS
-            and route3["placement"].get("hash_in_lds") == 2 and not args.no_neighbor_samples)
         route3["seeds"] = "label medoid"
         if not args.no_coarse_entry:
             from gofann_amd import search as gs
@@ -2586,11 +2599,9 @@ def main():
                 "roofline": {"bound": "hbm", "achieved": round(achieved, 2),
                              "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                              "frac": round(achieved / PEAK_HBM_GBPS, 5),
-                             "traffic": measured_traffic(
-                                 "traversal_pq48_c2_medoid_traffic.md",
-                                 chosen == 128 and not args.no_records
-                                 and placed.get("table_in_lds") == 0
-                                 and placed.get("hash_in_lds") == 2),
+                             "traffic": measured_traffic("C2 PQ route",
+                                                         "traversal_kernel<PqScorer<48>>",
+                                                         chosen, abytes),
                              "kernel": "traversal_kernel<PqScorer<48>>",
                              "kernel_ms": round(kms, 3), "algorithmic_bytes": abytes}}
     use_exact = (route3 is not None and route3["recall_at_10"] >= args.target_recall

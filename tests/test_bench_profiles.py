@@ -1,10 +1,11 @@
-"""The committed rocprofv3 summaries that bench.py reads stay consistent.
+"""The committed rocprofv3 traffic summary that bench.py reads stays consistent.
 
-bench.py copies `roofline.traffic` from the `bytes_per_launch:` line of
-profiles/exact_route_c2_traffic.md when its run is the configuration that
-summary measured.  These checks recompute that line from the summary's own
-per-launch FETCH_SIZE / WRITE_SIZE table and calibration factors, so a hand
-edit of one without the other fails here.
+bench.py copies each leg's `traffic` from the `traffic:` lines of
+profiles/bench_kernels_traffic.md when its run is the configuration that
+summary measured (same leg, kernel, beams and algorithmic bytes).  These
+checks recompute every line's bytes from its own FETCH_SIZE / WRITE_SIZE
+figures and the summary's copy calibration, so a hand edit of one without
+the other fails here, and check the lookup's matching rule.
 """
 from __future__ import annotations
 
@@ -12,47 +13,49 @@ import re
 
 import bench
 
-PROFILE = bench.ROOT / "profiles" / "exact_route_c2_traffic.md"
+PROFILE = bench.ROOT / "profiles" / bench.TRAFFIC_PROFILE
 
 
-def _table(text: str):
-    fetch, write, calib = [], [], None
-    for line in text.splitlines():
-        m = re.match(r"\| exact route, launch \d+ \| ([0-9,]+) \| ([0-9,]+) \|", line)
-        if m:
-            fetch.append(int(m.group(1).replace(",", "")))
-            write.append(int(m.group(2).replace(",", "")))
-        m = re.match(r"\| neg, 1 GiB in / 1 GiB out \| ([0-9,]+) \| ([0-9,]+) \|", line)
-        if m:
-            calib = tuple(int(x.replace(",", "")) for x in m.groups())
-    return fetch, write, calib
+def _fields(line: str) -> dict:
+    return dict(kv.split("=", 1) for kv in (x.strip() for x in line[8:].split(";")) if "=" in kv)
 
 
-def test_traffic_line_matches_its_table():
+def _lines():
     text = PROFILE.read_text()
-    fetch, write, calib = _table(text)
-    assert len(fetch) == 3 and len(write) == 3 and calib is not None
-    # a copy of 1 GiB moves 1 GiB in and 1 GiB out: the counters' scale factors
-    f_fac = (1 << 20) / calib[0]
-    w_fac = (1 << 20) / calib[1]
-    assert abs(f_fac - 2.0) < 0.01 and abs(w_fac - 1.0) < 0.01
-    expect = (sum(fetch) / 3 * 2.0 + sum(write) / 3 * 1.0) * 1024
-    got = bench.measured_traffic("exact_route_c2_traffic.md", True)
-    assert got is not None
-    assert abs(got - expect) / expect < 1e-6, (got, expect)
+    cal = re.search(r"^calibration: neg_fetch_kib=(\d+); neg_write_kib=(\d+)", text, re.M)
+    assert cal, "calibration line missing"
+    rows = [_fields(l.strip()) for l in text.splitlines() if l.strip().startswith("traffic:")]
+    return (int(cal.group(1)), int(cal.group(2))), rows
 
 
-def test_traffic_is_only_copied_for_the_measured_configuration():
-    assert bench.measured_traffic("exact_route_c2_traffic.md", False) is None
-    assert bench.measured_traffic("no_such_summary.md", True) is None
+def test_calibration_is_a_copy_of_one_gib():
+    (fk, wk), _ = _lines()
+    # a copy of 1 GiB reads 1 GiB and writes 1 GiB: the counters' scale factors
+    assert abs((1 << 20) / fk - 2.0) < 0.01
+    assert abs((1 << 20) / wk - 1.0) < 0.01
 
 
-def test_traffic_is_not_below_the_algorithmic_bytes():
-    # 138,300 routes at Q = 80 move 123.9 GB algorithmically; the measured
-    # traffic includes every row segment, so it cannot be smaller
-    text = PROFILE.read_text()
-    m = re.search(r"bench\.py `exact_route_bytes`\): ([0-9,]+) B", text)
-    assert m, "algorithmic bytes line missing"
-    alg = int(m.group(1).replace(",", ""))
-    got = bench.measured_traffic("exact_route_c2_traffic.md", True)
-    assert alg <= got <= 2 * alg
+def test_every_traffic_line_matches_its_counters():
+    (fk, wk), rows = _lines()
+    assert len(rows) >= 10
+    ff, wf = round((1 << 20) / fk, 3), round((1 << 20) / wk, 3)
+    for f in rows:
+        expect = (float(f["fetch_kib"]) * ff + float(f["write_kib"]) * wf) * 1024
+        assert abs(float(f["bytes"]) - expect) <= 1e-6 * expect + 1, f
+        # counter bytes are of the order of the algorithmic bytes: L2 hits can
+        # put them below, re-read lines above, never by orders of magnitude
+        alg = float(f["algorithmic"])
+        assert 0.3 * alg <= float(f["bytes"]) <= 30 * alg, f
+
+
+def test_lookup_matches_leg_kernel_beams_and_bytes():
+    _, rows = _lines()
+    f = rows[0]
+    beams = [int(b) for b in f["beams"].split(",")]
+    alg = float(f["algorithmic"])
+    got = bench.measured_traffic(f["leg"], f["kernel"], beams, alg)
+    assert got == float(f["bytes"])
+    # a different walk (algorithmic bytes 2% off), beam or leg is not this run
+    assert bench.measured_traffic(f["leg"], f["kernel"], beams, alg * 1.02) is None
+    assert bench.measured_traffic(f["leg"], f["kernel"], [b + 1 for b in beams], alg) is None
+    assert bench.measured_traffic("no such leg", f["kernel"], beams, alg) is None
