@@ -1014,7 +1014,6 @@ __device__ __forceinline__ int wave_sum(int v)
     return v;
 }
 
-// Frontier pickup (wave-cooperative).
 // Float -> unsigned key of the same order (-0 folded onto +0, which compare
 // equal as floats), and back.  Frontier keys are distances or priorities of
 // finite vectors; a NaN would order above +inf.
@@ -1029,6 +1028,7 @@ __device__ __forceinline__ float order_key_float(uint32_t k)
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
+// Frontier pickup (wave-cooperative).
 // pickup_next_unused_from_native_frontier (backend_pq.cu:844-892): unused
 // entry of least `first`, lowest index on ties; lane 0 marks it used.
 // Each lane scans slots lane + 1, lane + 65, ... in ascending order and

@@ -982,9 +982,11 @@ __device__ __forceinline__ void share_flush(const ShareScanArgs& a, const Rabitq
     }
 }
 
+// Waves per SIMD: 4 for query codes up to 512 bits (114-128 VGPRs, four
+// workgroups per CU as LDS allows), 3 for longer codes (at 4 they spill).
 template <int V>
-__global__ __launch_bounds__(kScanThreads, (V <= 4 ? 4 : 3)) void label_share_scan_kernel(ShareScanArgs a,
-                                                                        RabitqScanScorer sc)
+__global__ __launch_bounds__(kScanThreads, (V <= 4 ? 4 : 3)) void label_share_scan_kernel(
+    ShareScanArgs a, RabitqScanScorer sc)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ uint32_t s_pass[kShareRoutes];
