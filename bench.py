@@ -520,7 +520,6 @@ def exact_route_bytes(st: np.ndarray, degree: int, dim: int, neighbor_samples: b
 PEAK_FP32_MFMA_TFLOPS = 157.3
 
 
-
 def rabitq_prep_leg(ctx, torch, nq=10_000, dim=4096, anchors=512, reps=3):
     """RaBitQ query preparation at the C3 shape (10k queries, 4096-d, padded
     4096, 512 anchors): rotation SGEMM on MFMA, int8 quantization, factors
