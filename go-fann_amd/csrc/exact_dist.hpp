@@ -52,15 +52,28 @@ constexpr uint32_t elem_bytes(int elem)
 }
 
 // Warp order, lane j (0..31) of the half computing `row`: partial j.
-template <int kElem>
+// kBatch row words per lane are loaded before the first is consumed, so a
+// row costs about dim / (32 kBatch) memory round trips; the chain of sums
+// keeps its order whatever kBatch is.
+template <int kElem, int kBatch = 8>
 __device__ __forceinline__ float l2_w32_partial(const void* row, const float* q, uint32_t dim,
                                                 uint32_t j)
 {
     float p = 0.0f;
     if constexpr (kElem == GOFANN_ELEM_F32) {
         const float* b = static_cast<const float*>(row);
-#pragma unroll 8
-        for (uint32_t d = j; d < dim; d += 32) {
+        uint32_t d = j;
+        for (; d + 32u * (kBatch - 1) < dim; d += 32u * kBatch) {
+            float v[kBatch];
+#pragma unroll
+            for (int t = 0; t < kBatch; ++t) v[t] = b[d + 32u * t];
+#pragma unroll
+            for (int t = 0; t < kBatch; ++t) {
+                const float diff = v[t] - q[d + 32u * t];
+                p = fmaf(diff, diff, p);
+            }
+        }
+        for (; d < dim; d += 32) {
             const float diff = b[d] - q[d];
             p = fmaf(diff, diff, p);
         }
@@ -69,8 +82,21 @@ __device__ __forceinline__ float l2_w32_partial(const void* row, const float* q,
             const __half2* b2 = static_cast<const __half2*>(row);
             const float2* q2 = reinterpret_cast<const float2*>(q);
             const uint32_t dim2 = dim >> 1;
-#pragma unroll 8
-            for (uint32_t d2 = j; d2 < dim2; d2 += 32) {
+            uint32_t d2 = j;
+            for (; d2 + 32u * (kBatch - 1) < dim2; d2 += 32u * kBatch) {
+                __half2 v[kBatch];
+#pragma unroll
+                for (int t = 0; t < kBatch; ++t) v[t] = b2[d2 + 32u * t];
+#pragma unroll
+                for (int t = 0; t < kBatch; ++t) {
+                    const float2 bf = __half22float2(v[t]);
+                    const float2 qf = q2[d2 + 32u * t];
+                    const float dx = bf.x - qf.x;
+                    const float dy = bf.y - qf.y;
+                    p = p + fmaf(dx, dx, dy * dy);
+                }
+            }
+            for (; d2 < dim2; d2 += 32) {
                 const float2 bf = __half22float2(b2[d2]);
                 const float2 qf = q2[d2];
                 const float dx = bf.x - qf.x;

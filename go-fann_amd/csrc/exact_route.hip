@@ -294,20 +294,27 @@ __device__ __forceinline__ void load_node(const gofann_graph_view& g,
 // (FLT_MAX where keep is false).  Rows up to kQuadMaxRowBytes: 16 rows at a
 // time, one per quad of lanes (l2_w32_quad), candidates compacted through
 // LDS in lane order (s_samp and s_dist, kMaxDegree entries, are free at
-// this point of the step).  Longer rows: two at a time, one per 32-lane
-// half (l2_w32_partial + w32_tree), which keeps every lane busy; at C3's
-// 16 KB rows this took 261 ms a step against 348 for the quads, at C4's
-// 1 KB rows the quads 140 against 329.
+// this point of the step).  Longer rows (kLong, its own kernel): two at a
+// time, one per 32-lane half (l2_w32_partial + w32_tree), which keeps every
+// lane busy, with kExactLongBatch row words per lane in flight: at C3's
+// 16 KB rows 181 ms a step for the graph routes, against 269 with 8 words
+// and 348 for the quads; at C4's 1 KB rows the quads take 140 against 329.
+// Either form gives the same bits for any row length.
 constexpr size_t kQuadMaxRowBytes = 4096;
 
-template <int kElem>
+#ifndef GOFANN_EXACT_LONG_BATCH
+#define GOFANN_EXACT_LONG_BATCH 32
+#endif
+constexpr int kExactLongBatch = GOFANN_EXACT_LONG_BATCH;
+
+template <int kElem, bool kLong>
 __device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t dim,
                                                   const float* qf, bool keep, uint32_t samp,
                                                   int lane, uint32_t* s_samp, float* s_dist)
 {
     const size_t row_bytes = static_cast<size_t>(dim) * elem_bytes(kElem);
     uint64_t m = ballot(keep);
-    if (row_bytes > kQuadMaxRowBytes) {
+    if constexpr (kLong) {
         float out = FLT_MAX;
         while (m) {
             const int ja = __builtin_ctzll(m);
@@ -322,9 +329,8 @@ __device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t 
                 jb >= 0 ? static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(samp), jb))
                         : sa;
             const uint32_t s = lane < 32 ? sa : sb;
-            const float t = w32_tree<kElem>(
-                l2_w32_partial<kElem>(base + static_cast<size_t>(s) * row_bytes, qf, dim,
-                                      static_cast<uint32_t>(lane) & 31u));
+            const float t = w32_tree<kElem>(l2_w32_partial<kElem, kExactLongBatch>(
+                base + static_cast<size_t>(s) * row_bytes, qf, dim, static_cast<uint32_t>(lane) & 31u));
             const float da = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 0));
             const float db = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32));
             if (lane == ja) out = da;
@@ -350,8 +356,9 @@ __device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t 
     return keep ? s_dist[rank] : FLT_MAX;
 }
 
-// kC > 0: dim == 16 kC (rows loaded whole); kC == 0: any dim.  The frontier
-// lives in LDS.  kElem: the element type of base and queries
+// kC > 0 (u8): dim == 16 kC (rows loaded whole); kC == 0: any dim; kC < 0
+// (f32 / f16): rows longer than kQuadMaxRowBytes.  The frontier lives in
+// LDS.  kElem: the element type of base and queries
 // (GOFANN_ELEM_*); u8 rows are scored per lane (integer, exact in any
 // order), f32 / f16 rows by wave_float_dists.
 template <int kVisited, int kC, int kElem>
@@ -505,7 +512,8 @@ __global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAV
             // dead before the filter below.
             asm volatile("" : "+v"(d32)::"memory");
         } else {
-            fdist = wave_float_dists<kElem>(a.base, a.dim, qf, keep, samp, lane, s_samp, s_dist);
+            fdist = wave_float_dists<kElem, (kC < 0)>(a.base, a.dim, qf, keep, samp, lane, s_samp,
+                                                       s_dist);
             asm volatile("" : "+v"(fdist)::"memory");
         }
 
@@ -752,6 +760,11 @@ struct LaunchShape {
 template <int kElem>
 int launch_rows(const LaunchShape& s, int chunks)
 {
+    if constexpr (kElem != GOFANN_ELEM_U8) {
+        if (chunks < 0)
+            return launch_exact<-1, kElem>(s.ctx, *s.a, s.hash_mode, s.lds_full, s.lds_spill,
+                                           s.lds_glob, s.count, s.fixed_slab, s.fixed_routes);
+    }
 #if GOFANN_EXACT_FIXED_ROWS
     if constexpr (kElem == GOFANN_ELEM_U8) {
         switch (chunks) {
@@ -837,9 +850,11 @@ static int exact_search_impl(Context* ctx, const void* base, int base_elem, uint
                            : 0;
     const LaunchShape sh{ctx, &a, p->hash_mode, lds_full, lds_spill, lds_glob, r->count,
                          fixed_slab, fixed_routes};
+    // float rows over kQuadMaxRowBytes take the long-row kernel
+    const int fchunks = static_cast<size_t>(dim) * elem_bytes(base_elem) > kQuadMaxRowBytes ? -1 : 0;
     switch (base_elem) {
-    case GOFANN_ELEM_F32: return launch_rows<GOFANN_ELEM_F32>(sh, 0);
-    case GOFANN_ELEM_F16: return launch_rows<GOFANN_ELEM_F16>(sh, 0);
+    case GOFANN_ELEM_F32: return launch_rows<GOFANN_ELEM_F32>(sh, fchunks);
+    case GOFANN_ELEM_F16: return launch_rows<GOFANN_ELEM_F16>(sh, fchunks);
     default: return launch_rows<GOFANN_ELEM_U8>(sh, chunks);
     }
 }

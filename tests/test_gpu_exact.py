@@ -196,14 +196,16 @@ def _float_world(dim, seed, n=4000, nq=32):
     return wl, li, gp.plan_queries(li, wl.query_labels).graph
 
 
-@pytest.mark.parametrize("dim", [37, 100, 128, 512, 4096])
+@pytest.mark.parametrize("dim", [37, 100, 128, 512, 1031, 2049, 4096])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 def test_exact_search_float_rows(gpu_ctx, dim, dtype):
     """f32 and f16 rows (and queries of the same type): distances in the
-    reference's warp order, bit-identical to the oracle, with the frontier
-    in registers and in LDS and every visited-set placement; odd dim takes
-    the per-element f16 path, 100 leaves partials of unequal length, and
-    4096 (16 KB / 8 KB rows, C3's shape) takes the half-wave-per-row path."""
+    reference's warp order, bit-identical to the oracle, with every
+    visited-set placement; odd dim takes the per-element f16 path, 100
+    leaves partials of unequal length.  Rows over 4 KB (f32 1031 and up,
+    f16 2049 and up; 4096 is C3's shape) take the long-row kernel, whose
+    lanes load 32 row words at a time: 1031 and 2049 leave a tail shorter
+    than one such batch."""
     wl, li, rs = _float_world(dim, 70 + dim)
     t = np.float16 if dtype == "f16" else np.float32
     rows = (wl.base.numpy().astype(t), wl.queries.numpy().astype(t))

@@ -70,9 +70,10 @@ def test_exact_route_six_waves_without_step_spills(report):
     # every visited-set placement of the u8 kernels (last template argument
     # 0); the headline one (<2, 0, 0>: spilling LDS visited table) keeps at
     # most the one spilled VGPR it was measured with.  The f32 / f16 kernels
-    # (1, 2) are built for 5 waves and spill nothing.
+    # (1, 2), the long-row ones (middle argument -1, mangled "n1") included,
+    # are built for 5 waves and spill nothing.
     for name, r in _kernels(report["exact_route.hip"], "exact_route_kernel").items():
-        elem = int(re.search(r"ILi\d+ELi\d+ELi(\d+)EEE", name).group(1))
+        elem = int(re.search(r"ILi\d+ELin?\d+ELi(\d+)EEE", name).group(1))
         if elem == 0:
             assert r["occupancy"] >= 6, (name, r)
             assert r["vgprs"] <= 80, (name, r)
