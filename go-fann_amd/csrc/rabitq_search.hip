@@ -55,6 +55,7 @@ RabitqScorer make_rabitq_scorer(const gofann_rabitq_view* rq, const gofann_rabit
     sc.g_row = nullptr;
     sc.records = rq->records;
     sc.record_stride = rq->record_stride;
+    sc.halves = 0;
     return sc;
 }
 
@@ -101,8 +102,11 @@ int rabitq_search(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabit
         return rabitq_pair_search(ctx, make_rabitq_scorer(rq, pre), g, pred, r, p, out_ids,
                                   out_dists, stats);
     const Placement pl = choose_visited<RabitqScorer>(ctx, l, p->hash_mode);
-    return launch_traversal<RabitqScorer>(ctx, make_rabitq_scorer(rq, pre), l, pl, g, pred, r, p,
-                                          out_ids, out_dists, stats, 1);
+    RabitqScorer sc = make_rabitq_scorer(rq, pre);
+    // no neighbour past lane 31: rows scored a candidate per lane take two
+    // lanes each (the whole-wave rows of 2048 / 4096 bits are unaffected)
+    sc.halves = g->degree <= 32 ? 1 : 0;
+    return launch_traversal<RabitqScorer>(ctx, sc, l, pl, g, pred, r, p, out_ids, out_dists, stats, 1);
 }
 
 int rabitq_score(Context* ctx, const gofann_rabitq_view* rq, const gofann_rabitq_queries* pre,

@@ -299,8 +299,20 @@ struct PqScorer {
 // packed into LDS and each 16-lane group scores one row per pass (lane l
 // owns the row's 16-byte vectors l and l + 16), so every lane works and the
 // code loads are coalesced; the group's integer partials are summed by DPP.
-// Shorter or longer rows are scored one candidate per lane.
+// Shorter or longer rows are scored one candidate per lane; in a traversal
+// of a graph of degree <= 32 (lanes 32..63 never hold a candidate) lane l
+// and lane l + 32 split lane l's row instead (`halves`), the low lane
+// counting the first ceil(vectors / 2) 16-byte vectors, and the two
+// integer partials add up to the same ip.
 constexpr uint32_t kRabitqCoopBytes = 512;  // LDS after the planes: [64] ids, [64] ip
+
+// x of lane l ^ 32 (v_permlane32_swap of x with itself: the first result
+// holds the low half in both halves, the second the high half).
+__device__ __forceinline__ uint32_t swap_wave_halves(uint32_t x, int lane)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return lane < 32 ? r[1] : r[0];
+}
 
 struct RabitqScorer {
     static constexpr bool kHasExact = false;
@@ -319,6 +331,7 @@ struct RabitqScorer {
     const float* g_row;
     const uint8_t* records;  // per-sample records (code, f_add, f_rescale, anchor) or null
     uint32_t record_stride;
+    int halves;  // lanes 32..63 never score: they take half of lane l - 32's row
 
     __device__ __forceinline__ const uint8_t* code_row(uint32_t sample) const
     {
@@ -432,6 +445,32 @@ struct RabitqScorer {
             ip = ip_coop<2>(sample, active, lane);
         } else if (vecs == 16) {
             ip = ip_coop<1>(sample, active, lane);
+        } else if (halves) {
+            const bool hi = lane >= 32;
+            const uint32_t s = swap_wave_halves(sample, lane);
+            const uint64_t am = ballot(active);  // every lane votes (not inside the select)
+            const bool act = ((am >> (lane & 31)) & 1ull) != 0;
+            const uint32_t lo = (vecs + 1) / 2;
+            int32_t part = 0;
+            if (act) {
+                const uint32_t v_end = hi ? vecs : lo;
+                const uint4* row = reinterpret_cast<const uint4*>(code_row(hi ? s : sample));
+                const uint4* planes4 = reinterpret_cast<const uint4*>(planes);
+                uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                for (uint32_t v0 = hi ? lo : 0; v0 < v_end; v0 += kCodeBatch) {
+                    uint4 cb[kCodeBatch];
+#pragma unroll
+                    for (int b = 0; b < kCodeBatch; ++b)
+                        cb[b] = v0 + b < v_end ? row[v0 + b] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < kCodeBatch; ++b) {
+                        if (v0 + b >= v_end) break;
+                        count_vec(planes4, vecs, v0 + b, cb[b], cnt);
+                    }
+                }
+                part = combine(cnt);
+            }
+            ip = part + static_cast<int32_t>(swap_wave_halves(static_cast<uint32_t>(part), lane));
         } else {
             if (!active) return 0.0f;
             const uint4* row = reinterpret_cast<const uint4*>(code_row(sample));

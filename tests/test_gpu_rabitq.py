@@ -79,16 +79,25 @@ def test_rotation_and_centroids_vs_fp64(gpu_ctx, shape):
         assert np.array_equal(q8[i], oq) and sc[i] == np.float32(osc) and k1[i] == np.float32(ok1)
 
 
-@pytest.fixture(scope="module")
-def rworld():
+def _make_rworld(degree):
     wl = synth.small_labelled(n=6000, nq=40, dim=60, k=10, sigma=0.7, labels=5, seed=31, tags=True)
     li = gi.build_label_index(wl.base, wl.label_offsets, wl.label_values, wl.num_labels,
-                              wl.centroids, degree=32, threshold=300)
+                              wl.centroids, degree=degree, threshold=300)
     P = 128
     rot = gi.random_rotation(wl.dim, P, 31005, "cpu")
     codes, fac, aid, anchors = gi.rabitq_encode(wl.base, rot, wl.centroids)
     pl = gp.plan_queries(li, wl.query_labels)
     return wl, li, pl, rot, codes, fac, aid, anchors, P
+
+
+@pytest.fixture(scope="module")
+def rworld():
+    return _make_rworld(32)
+
+
+@pytest.fixture(scope="module")
+def rworld64():
+    return _make_rworld(64)
 
 
 def _rviews(rw):
@@ -146,13 +155,26 @@ def test_rabitq_score_ip_exact(gpu_ctx, rworld, P):
 
 
 # Q = 16, 40 and 96 (small and mid beams on the LDS frontier's wave-parallel
-# heap operations); P = 512 is C4's 64-byte code.
+# heap operations); P = 512 is C4's 64-byte code.  At degree 32 rows scored
+# a candidate per lane (P 128, 384, 512) are split between lanes l and
+# l + 32: one, three (two and one) and four 16-byte vectors.
 @pytest.mark.parametrize("Q", [16, 40, 96])
-@pytest.mark.parametrize("P", [128, 512, 2048, 4096])
+@pytest.mark.parametrize("P", [128, 384, 512, 2048, 4096])
 @pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("hash_mode,nsamp", [(_lib.PLACE_AUTO, False), (_lib.PLACE_LDS, True),
                                              (_lib.PLACE_GLOBAL, True), (_lib.PLACE_SPILL, False)])
 def test_rabitq_search_matches_oracle(gpu_ctx, rworld, bias, hash_mode, nsamp, P, Q):
+    _check_search(gpu_ctx, rworld, bias, hash_mode, nsamp, P, Q)
+
+
+# Degree 64: every lane may hold a candidate, so rows are scored one per lane.
+@pytest.mark.parametrize("P", [128, 384, 512, 4096])
+@pytest.mark.parametrize("bias", [True, False])
+def test_rabitq_search_degree64_matches_oracle(gpu_ctx, rworld64, bias, P):
+    _check_search(gpu_ctx, rworld64, bias, _lib.PLACE_AUTO, True, P, 40)
+
+
+def _check_search(gpu_ctx, rworld, bias, hash_mode, nsamp, P, Q):
     rworld = _at_dim(rworld, P)
     wl, li, pl, rot, codes, fac, aid, anchors, P = rworld
     say("rabitq search P", P, "Q", Q, "bias", bias, "hash", hash_mode, "nsamp", nsamp)
