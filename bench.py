@@ -994,8 +994,27 @@ def graph_classes(pipe, qs, start, ends=None):
         pipe._graph(q, start, lo, hi, ctx=cx)
         if ends is not None and i < len(ends):
             ends[i].record(st)
+        if getattr(pipe, "rerank_by_class", False):
+            # this class's rerank behind its traversal, overlapping the
+            # other classes' traversals
+            rerank_rows(pipe, cx, lo, hi)
         used.append(st)
     return used
+
+
+def rerank_rows(pipe, ctx, lo, hi):
+    """Exact rerank (gofann_exact_rerank) of a pipeline's shortlist rows
+    lo..hi into the same rows of pipe.fin_i / pipe.fin_d; each route's
+    result depends on its own row only."""
+    if hi <= lo:
+        return
+    L, W, base = pipe.L, pipe.W, pipe.wl.base
+    elem = {pipe.torch.uint8: L.ELEM_U8, pipe.torch.float32: L.ELEM_F32,
+            pipe.torch.float16: L.ELEM_F16}[base.dtype]
+    ctx.check(ctx.lib.gofann_exact_rerank(
+        ctx.handle, L.ptr(base), elem, int(base.shape[1]), int(base.shape[0]),
+        L.ptr(pipe.wl.queries), L.ptr(pipe.route_query[lo:]), L.ptr(pipe.sl_i[lo * W:]), W,
+        hi - lo, 10, L.ptr(pipe.fin_i[lo * 10:]), L.ptr(pipe.fin_d[lo * 10:])))
 
 
 def stage_times(pipe, scan_name):
@@ -1235,6 +1254,9 @@ class RabitqRangePipeline:
         n = self.ng + self.np_
         self.sl_i = torch.empty(max(n, 1) * width, dtype=torch.int32, device="cuda")
         self.sl_d = torch.empty(max(n, 1) * width, dtype=torch.float32, device="cuda")
+        self.fin_i = torch.empty(max(n, 1) * 10, dtype=torch.int32, device="cuda")
+        self.fin_d = torch.empty(max(n, 1) * 10, dtype=torch.float32, device="cuda")
+        self.rerank_by_class = True  # graph_classes reranks each class on its stream
         self.passes = torch.empty(max(self.np_, 1), dtype=torch.int32, device="cuda")
         self.stats = torch.zeros(max(self.ng, 1) * 8, dtype=torch.int32, device="cuda")
         self.route_query = gs.u32(np.concatenate([gq, pq]))
@@ -1265,6 +1287,11 @@ class RabitqRangePipeline:
         if timed:
             ev[2].record()
         self._scan()
+        n = self.ng + self.np_
+        if used:
+            # routes rerank independently: the posting routes' rows here,
+            # behind the scan, each class's rows on its stream (graph_classes)
+            rerank_rows(self, ctx, self.ng, n)
         if timed:
             ev[3].record()
         main = self.torch.cuda.current_stream()
@@ -1272,12 +1299,11 @@ class RabitqRangePipeline:
             main.wait_stream(st)
         if timed:
             self.ev_join.record()
-        n = self.ng + self.np_
-        fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
-                                       self.sl_i, W, n, 10)
+        if not used:
+            rerank_rows(self, ctx, 0, n)
         if timed:
             ev[4].record()
-        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, fin_i, fin_d, 10,
+        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, self.fin_i, self.fin_d, 10,
                                        self.nq, 10)
         if timed:
             ev[5].record()
@@ -1673,6 +1699,9 @@ class RabitqLabelPipeline:
         n = self.ng + self.np_
         self.sl_i = torch.empty(max(n, 1) * width, dtype=torch.int32, device="cuda")
         self.sl_d = torch.empty(max(n, 1) * width, dtype=torch.float32, device="cuda")
+        self.fin_i = torch.empty(max(n, 1) * 10, dtype=torch.int32, device="cuda")
+        self.fin_d = torch.empty(max(n, 1) * 10, dtype=torch.float32, device="cuda")
+        self.rerank_by_class = True  # graph_classes reranks each class on its stream
         self.passes = torch.empty(max(self.np_, 1), dtype=torch.int32, device="cuda")
         self.stats = torch.zeros(max(self.ng, 1) * 8, dtype=torch.int32, device="cuda")
         r2q = np.concatenate([rs.route_query, ps.route_query]).astype(np.uint32)
@@ -1743,6 +1772,11 @@ class RabitqLabelPipeline:
         if timed:
             ev[2].record()
         self._scan()
+        n = self.ng + self.np_
+        if used:
+            # routes rerank independently: the posting routes' rows here,
+            # behind the scan, each class's rows on its stream (graph_classes)
+            rerank_rows(self, ctx, self.ng, n)
         if timed:
             ev[3].record()
         main = self.torch.cuda.current_stream()
@@ -1750,12 +1784,11 @@ class RabitqLabelPipeline:
             main.wait_stream(st)
         if timed:
             self.ev_join.record()
-        n = self.ng + self.np_
-        fin_i, fin_d = gs.exact_rerank(ctx, self.wl.base, self.wl.queries, self.route_query,
-                                       self.sl_i, W, n, 10)
+        if not used:
+            rerank_rows(self, ctx, 0, n)
         if timed:
             ev[4].record()
-        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, fin_i, fin_d, 10,
+        out_i, _ = gs.merge_routes_gpu(ctx, self.q_off, self.q_routes, self.fin_i, self.fin_d, 10,
                                        self.nq, 10)
         if timed:
             ev[5].record()
