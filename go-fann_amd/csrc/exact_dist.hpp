@@ -225,11 +225,8 @@ __device__ __forceinline__ float l2_w32_quad(const uint8_t* row, const float* q,
         // whole blocks by two 16-byte loads where the row allows it
         const bool vec = kElem == GOFANN_ELEM_F32 ? (dim & 3u) == 0 : (dim & 7u) == 0;
         if (vec) {
-#pragma unroll kU
-            for (uint32_t t = 0; t < nb; ++t) {
-                const uint4* src = reinterpret_cast<const uint4*>(row + 128u * t + 32u * g);
-                const uint4 a = src[0];
-                const uint4 b = src[1];
+            // one 128-byte block: this lane's two 16-byte loads, summed in order
+            const auto block = [&](uint32_t t, const uint4& a, const uint4& b) {
                 const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
                 const uint32_t k0 = 32u * t + 8u * g;
                 if constexpr (kElem == GOFANN_ELEM_F32) {
@@ -255,6 +252,23 @@ __device__ __forceinline__ float l2_w32_quad(const uint8_t* row, const float* q,
                         p[i + 1] = p[i + 1] + fmaf(dx, dx, dy * dy);
                     }
                 }
+            };
+            // kU blocks' loads are issued before the first of them is summed
+            uint32_t t = 0;
+            for (; t + kU <= nb; t += kU) {
+                uint4 a[kU], b[kU];
+#pragma unroll
+                for (int u = 0; u < kU; ++u) {
+                    const uint4* src = reinterpret_cast<const uint4*>(row + 128u * (t + u) + 32u * g);
+                    a[u] = src[0];
+                    b[u] = src[1];
+                }
+#pragma unroll
+                for (int u = 0; u < kU; ++u) block(t + u, a[u], b[u]);
+            }
+            for (; t < nb; ++t) {
+                const uint4* src = reinterpret_cast<const uint4*>(row + 128u * t + 32u * g);
+                block(t, src[0], src[1]);
             }
         }
         // blocks not read above (the unaligned case), then the partial block

@@ -101,10 +101,19 @@ constexpr int kExactMaxTopk = 10;  // defaults::max_topk
 #define GOFANN_EXACT_ROW_UNROLL 4
 #endif
 
-// 128-byte blocks per quad whose loads are issued together in the float
-// kernels' row loop.
+// Waves per SIMD the f32 / f16 kernels are compiled for, and the 128-byte
+// blocks per quad whose loads are issued before any is summed.  The quad
+// kernels are bound by the loads in flight; their LDS holds them near 4
+// waves per SIMD anyway (C4, 1 KB f16 rows, Q = 448: 17 routes per CU), so
+// they take the registers for deeper batches: exact route 141.6 ms with two
+// blocks left to the compiler's unrolling at 5 waves, 119.0 with explicit
+// batches of two, 110.1 with batches of four at 4 waves (no spills; eight
+// spill 8-14 VGPRs).
+#ifndef GOFANN_EXACT_FLOAT_MIN_WAVES
+#define GOFANN_EXACT_FLOAT_MIN_WAVES 4
+#endif
 #ifndef GOFANN_EXACT_QUAD_UNROLL
-#define GOFANN_EXACT_QUAD_UNROLL 2
+#define GOFANN_EXACT_QUAD_UNROLL 4
 #endif
 constexpr int kExactQuadUnroll = GOFANN_EXACT_QUAD_UNROLL;
 
@@ -362,7 +371,7 @@ __device__ __forceinline__ float wave_float_dists(const uint8_t* base, uint32_t 
 // (GOFANN_ELEM_*); u8 rows are scored per lane (integer, exact in any
 // order), f32 / f16 rows by wave_float_dists.
 template <int kVisited, int kC, int kElem>
-__global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAVES : 5)) void exact_route_kernel(ExactArgs a)
+__global__ __launch_bounds__(64, (kElem == GOFANN_ELEM_U8 ? GOFANN_EXACT_MIN_WAVES : GOFANN_EXACT_FLOAT_MIN_WAVES)) void exact_route_kernel(ExactArgs a)
 {
     constexpr int kRowUnroll = GOFANN_EXACT_ROW_UNROLL;
     extern __shared__ __align__(16) unsigned char lds[];

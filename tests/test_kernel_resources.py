@@ -71,7 +71,8 @@ def test_exact_route_six_waves_without_step_spills(report):
     # 0); the headline one (<2, 0, 0>: spilling LDS visited table) keeps at
     # most the one spilled VGPR it was measured with.  The f32 / f16 kernels
     # (1, 2), the long-row ones (middle argument -1, mangled "n1") included,
-    # are built for 5 waves and spill nothing.
+    # are built for 4 waves (their LDS allows about that many routes) and
+    # spill nothing.
     for name, r in _kernels(report["exact_route.hip"], "exact_route_kernel").items():
         elem = int(re.search(r"ILi\d+ELin?\d+ELi(\d+)EEE", name).group(1))
         if elem == 0:
@@ -79,7 +80,7 @@ def test_exact_route_six_waves_without_step_spills(report):
             assert r["vgprs"] <= 80, (name, r)
             assert r["vgpr_spill"] <= 1, (name, r)
         else:
-            assert r["occupancy"] >= 5, (name, r)
+            assert r["occupancy"] >= 4, (name, r)
             assert r["vgpr_spill"] == 0, (name, r)
 
 
