@@ -123,6 +123,35 @@ struct RerankArgs {
 
 constexpr int kRerankThreads = 256;
 
+// One lane's chain of the rerank distance: acc = fma(diff, diff, acc) over
+// d = lane, lane + 64, ... in d order, with kRerankBatch rows elements
+// loaded before the first of them is used (the compiler's unrolling of the
+// plain loop kept the loads in small groups).  load(d): the base element as
+// float; diff(d, b): query minus base, in the element type's form.
+constexpr int kRerankBatch = 16;
+
+template <class Load, class Diff>
+__device__ __forceinline__ float lane_chain(uint32_t dim, int lane, Load load, Diff diff)
+{
+    float acc = 0.0f;
+    uint32_t d = static_cast<uint32_t>(lane);
+    for (; d + kWave * (kRerankBatch - 1) < dim; d += kWave * kRerankBatch) {
+        float bv[kRerankBatch];
+#pragma unroll
+        for (int t = 0; t < kRerankBatch; ++t) bv[t] = load(d + kWave * t);
+#pragma unroll
+        for (int t = 0; t < kRerankBatch; ++t) {
+            const float x = diff(d + kWave * t, bv[t]);
+            acc = fmaf(x, x, acc);
+        }
+    }
+    for (; d < dim; d += kWave) {
+        const float x = diff(d, load(d));
+        acc = fmaf(x, x, acc);
+    }
+    return acc;
+}
+
 __global__ __launch_bounds__(kRerankThreads) void exact_rerank_kernel(RerankArgs a)
 {
     __shared__ float s_d[kMaxShortlist];
@@ -147,30 +176,18 @@ __global__ __launch_bounds__(kRerankThreads) void exact_rerank_kernel(RerankArgs
         if (a.base_elem == GOFANN_ELEM_U8) {
             const uint8_t* b = static_cast<const uint8_t*>(a.base) + static_cast<size_t>(s) * a.dim;
             const uint8_t* qq = static_cast<const uint8_t*>(a.queries) + static_cast<size_t>(q) * a.dim;
-            // unrolled: the loads of 8 steps in flight, the sum in d order
-#pragma unroll 8
-            for (uint32_t d = lane; d < a.dim; d += kWave) {
-                const float diff = static_cast<float>(qq[d]) - static_cast<float>(b[d]);
-                acc = fmaf(diff, diff, acc);
-            }
+            acc = lane_chain(a.dim, lane, [&](uint32_t d) { return static_cast<float>(b[d]); },
+                             [&](uint32_t d, float bv) { return static_cast<float>(qq[d]) - bv; });
         } else if (a.base_elem == GOFANN_ELEM_F32) {
             const float* b = static_cast<const float*>(a.base) + static_cast<size_t>(s) * a.dim;
             const float* qq = static_cast<const float*>(a.queries) + static_cast<size_t>(q) * a.dim;
-            // unrolled: the loads of 8 steps in flight, the sum in d order
-#pragma unroll 8
-            for (uint32_t d = lane; d < a.dim; d += kWave) {
-                const float diff = qq[d] - b[d];
-                acc = fmaf(diff, diff, acc);
-            }
+            acc = lane_chain(a.dim, lane, [&](uint32_t d) { return b[d]; },
+                             [&](uint32_t d, float bv) { return qq[d] - bv; });
         } else {
             const __half* b = static_cast<const __half*>(a.base) + static_cast<size_t>(s) * a.dim;
             const float* qq = static_cast<const float*>(a.queries) + static_cast<size_t>(q) * a.dim;
-            // unrolled: the loads of 8 steps in flight, the sum in d order
-#pragma unroll 8
-            for (uint32_t d = lane; d < a.dim; d += kWave) {
-                const float diff = qq[d] - __half2float(b[d]);
-                acc = fmaf(diff, diff, acc);
-            }
+            acc = lane_chain(a.dim, lane, [&](uint32_t d) { return __half2float(b[d]); },
+                             [&](uint32_t d, float bv) { return qq[d] - bv; });
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off, kWave);

@@ -401,11 +401,14 @@ def test_pq_posting_scan_matches_oracle(gpu_ctx, world):
         assert np.array_equal(as_u32(passes), opass)
 
 
+# dim 72 stays in the per-element tail; 1100 and 4096 run the batched loads
+# (16 elements a lane) and, for 1100, a tail after them.
+@pytest.mark.parametrize("d", [72, 1100, 4096])
 @pytest.mark.parametrize("elem", ["u8", "f32", "f16"])
-def test_exact_rerank_matches_oracle(gpu_ctx, elem):
-    say("rerank", elem)
+def test_exact_rerank_matches_oracle(gpu_ctx, elem, d):
+    say("rerank", elem, "dim", d)
     rng = np.random.default_rng(5)
-    n, d, routes, width, topk = 2000, 72, 40, 100, 10
+    n, routes, width, topk = 2000, 40, 100, 10
     if elem == "u8":
         base = rng.integers(0, 256, (n, d)).astype(np.uint8)
         q = rng.integers(0, 256, (routes, d)).astype(np.uint8)
