@@ -145,6 +145,9 @@ __device__ __forceinline__ float lane_chain(uint32_t dim, int lane, Load load, D
             acc = fmaf(x, x, acc);
         }
     }
+    // the rest (whole rows under kRerankBatch * 64 elements): unrolled so
+    // that 8 steps' loads are in flight
+#pragma unroll 8
     for (; d < dim; d += kWave) {
         const float x = diff(d, load(d));
         acc = fmaf(x, x, acc);
