@@ -307,8 +307,9 @@ __device__ __forceinline__ void load_node(const gofann_graph_view& g,
 // time, one per 32-lane half (l2_w32_partial + w32_tree), which keeps every
 // lane busy, with kExactLongBatch row words per lane in flight: at C3's
 // 16 KB rows 181 ms a step for the graph routes, against 269 with 8 words
-// and 348 for the quads; at C4's 1 KB rows the quads take 140 against 329.
-// Either form gives the same bits for any row length.
+// and 348 for the quads; at C4's 1 KB rows the quads (then two blocks a
+// lane in flight) took 140 against 329 for the halves.  Either form gives
+// the same bits for any row length.
 constexpr size_t kQuadMaxRowBytes = 4096;
 
 #ifndef GOFANN_EXACT_LONG_BATCH
