@@ -1021,7 +1021,10 @@ def stage_times(pipe, scan_name):
     """Stage times (HIP events) of a timed RaBitQ step: the traversal from
     the end of preparation to the last class stream's end, the scan on the
     main stream (it overlaps the traversal), `graph_and_scan` to the join,
-    then rerank and merge."""
+    then rerank and merge.  In the overlapped step each class's rerank runs
+    on its stream and the posting routes' behind the scan, so they fall
+    inside `graph_and_scan` and `rerank` is near zero; the single-stream
+    step (serial_classes) reranks every route after the join."""
     e = pipe.ev
     ends = pipe.ev_class[: pipe.n_class_used]
     trav = max((e[1].elapsed_time(x) for x in ends), default=e[1].elapsed_time(e[2]))
