@@ -124,7 +124,7 @@ struct RerankArgs {
 constexpr int kRerankThreads = 256;
 
 // One lane's chain of the rerank distance: acc = fma(diff, diff, acc) over
-// d = lane, lane + 64, ... in d order, with kRerankBatch rows elements
+// d = lane, lane + 64, ... in d order, with kRerankBatch row elements
 // loaded before the first of them is used (the compiler's unrolling of the
 // plain loop kept the loads in small groups).  load(d): the base element as
 // float; diff(d, b): query minus base, in the element type's form.
